@@ -1,0 +1,137 @@
+"""Pin the CPU oracle to the reference's own torch path (golden vectors).
+
+The fixtures in tests/golden/ were written by tests/golden/make_golden.py
+from the reference (src/refinekv/summary.py, reference.py, attention.py).
+Summaries must match bit for bit; selection statistics within the error of a
+reordered fp32 dot product; masks, anchor unions and access counters
+exactly; attention outputs within the north-star tolerance.
+"""
+
+import json
+import os
+
+import numpy as np
+import pytest
+import torch
+
+import golden_cases as gc
+
+PATHS = gc.fixture_paths()
+IDS = [os.path.basename(p)[:-4] for p in PATHS]
+
+
+@pytest.fixture(scope="module", params=PATHS, ids=IDS)
+def case(request, oracle_lib):
+    g, meta = gc.load(request.param)
+    inp = gc.regenerate(meta)
+    return g, meta, inp
+
+
+def _summary_from_golden(g, inp, block):
+    return dict(counts=g["counts"], key_mean=g["key_mean"], value_mean=g["value_mean"],
+                ellipsoid=g["ellipsoid"], value_norm=g["value_norm"],
+                max_value_norm=g["max_value_norm"], prompt_length=inp["keys"].shape[1],
+                block_size=block)
+
+
+def test_inputs_regenerate_exactly(case):
+    g, meta, inp = case
+    got = gc.digest(inp["query"], inp["keys"], inp["values"], inp["suffix_keys"],
+                    inp["suffix_values"])
+    assert got == meta["input_sha256"]
+
+
+def test_summary_bit_exact(case, oracle_lib):
+    g, meta, inp = case
+    s = oracle_lib.summary(inp["keys"].float().numpy(), inp["values"].float().numpy(),
+                           meta["config"]["block_size"])
+    assert np.array_equal(s["counts"], g["counts"])
+    for key in ("key_mean", "value_mean", "ellipsoid"):
+        assert np.array_equal(s[key], g[key]), key
+    for key in ("value_norm", "max_value_norm"):
+        assert np.array_equal(s[key].view(np.uint32), g[key].view(np.uint32)), key
+
+
+def test_selection_statistics_close(case, oracle_lib):
+    g, meta, inp = case
+    block = meta["config"]["block_size"]
+    summ = _summary_from_golden(g, inp, block)
+    q = inp["query"][:, :, 0].float()
+    st = oracle_lib.select_stats(q.numpy(), summ)
+    # A reordered fp32 dot product of D terms differs by at most ~D*u*sum|terms|.
+    qt = q.to(torch.bfloat16).float()
+    km = torch.from_numpy(oracle_lib.bf16_value(g["key_mean"]))
+    D = q.shape[-1]
+    bound = torch.einsum("hgd,hbd->hgb", qt.abs(), km.abs()) * D ** -0.5 * D * 2.0 ** -23
+    err = np.abs(st["z"] - g["z"])
+    assert (err <= bound.numpy() + 4 * np.spacing(np.abs(g["z"]))).all()
+    for key in ("log_z", "log_c"):
+        scale = np.maximum(np.abs(g[key]), 1.0)
+        assert (np.abs(st[key] - g[key]) <= 1e-4 * scale).all(), key
+
+
+def _near_eps(risk, reduction, eps, rel=1e-6):
+    if reduction == "mean":
+        stat = risk.mean(1)
+        return np.abs(stat - eps) <= rel * eps
+    if reduction == "max":
+        stat = risk.max(1)
+        return np.abs(stat - eps) <= rel * eps
+    return (np.abs(risk - eps) <= rel * eps).any(1)
+
+
+def test_masks_and_counters_exact(case, oracle_lib):
+    g, meta, inp = case
+    cfg = meta["config"]
+    block, eps, red = cfg["block_size"], cfg["eps"], cfg["gqa_reduction"]
+    summ = _summary_from_golden(g, inp, block)
+    q = inp["query"][:, :, 0].float().numpy()
+    mask, z, risk = oracle_lib.select(q, summ, eps, red)
+    near = _near_eps(g["risk"], red, eps)
+    # The north-star exception: only blocks within 1e-6 relative of eps may differ.
+    assert ((mask != g["mask"]) & ~near).sum() == 0
+    anchor = g.get("anchor")
+    kp = gc.padded_pages(inp["keys"], block)
+    vp = gc.padded_pages(inp["values"], block)
+    out, sel = oracle_lib.sparse_attention(
+        q, summ, gc.bf16_bits(kp), gc.bf16_bits(vp), gc.bf16_bits(inp["suffix_keys"]),
+        gc.bf16_bits(inp["suffix_values"]), eps, red, anchor)
+    assert ((sel != g["selected"]) & ~near).sum() == 0
+    assert oracle_lib.access_blocks(sel, g["counts"]) == int(g["accessed_blocks"])
+
+
+def test_attention_output_within_tolerance(case, oracle_lib):
+    g, meta, inp = case
+    cfg = meta["config"]
+    block = cfg["block_size"]
+    summ = _summary_from_golden(g, inp, block)
+    q = inp["query"][:, :, 0].float().numpy()
+    kp = gc.padded_pages(inp["keys"], block)
+    vp = gc.padded_pages(inp["values"], block)
+    out, _ = oracle_lib.sparse_attention(
+        q, summ, gc.bf16_bits(kp), gc.bf16_bits(vp), gc.bf16_bits(inp["suffix_keys"]),
+        gc.bf16_bits(inp["suffix_values"]), cfg["eps"], cfg["gqa_reduction"], g.get("anchor"))
+    ref = g["output"].reshape(out.shape)
+    if inp["query"].dtype == torch.bfloat16:
+        out = torch.from_numpy(out).to(torch.bfloat16).float().numpy()
+    # North-star tolerance for bf16: max-abs 2e-2, mean-rel 1e-3.
+    assert np.abs(out - ref).max() <= 2e-2
+    assert np.abs(out - ref).mean() <= 1e-3 * np.abs(ref).mean()
+
+
+def test_figure2_known_answers(oracle_lib):
+    """Large-delta branch against the reference's published Figure-2 points:
+    risk = 2 p Vmax ((cosh d - 1)/D + tanh(d/2)) with D = C/Z."""
+    path = os.path.join(gc.GOLDEN_DIR, "kat_figure2.json")
+    pts = json.load(open(path))["points"]
+    delta = np.array([p["delta"] for p in pts], np.float32)
+    imp = np.array([p["importance"] for p in pts], np.float64)
+    vmax = np.array([p["vmax"] for p in pts], np.float32)
+    den = np.array([p["denominator"] for p in pts], np.float64)
+    want = np.array([p["risk"] for p in pts], np.float64)
+    # z - log Z = log p and z - log C = log p - log D; pick z = 0.
+    log_z = (-np.log(imp)).astype(np.float32)
+    log_c = (-np.log(imp) + np.log(den)).astype(np.float32)
+    got = oracle_lib.risk(np.zeros_like(delta), delta, log_z, log_c, vmax, vmax)
+    assert np.all(delta > 10)
+    np.testing.assert_allclose(got, want, rtol=2e-5)
