@@ -1,0 +1,339 @@
+#!/usr/bin/env python3
+"""RefineKV decode-attention benchmark on one MI355X.
+
+Workload (the headline): a Llama-3.1-8B-shaped
+attention stack -- 32 layers, 32 query / 8 KV heads, head_dim 128, bf16 --
+at 131072 prompt tokens, block_size 32, eps 0.01, GQA "any", decoding 128
+tokens; like the reference's protocol (speed/README.md:84-91) the timed
+window is the last 125 of the 127 decode intervals, replayed as HIP graphs
+(one graph = one decode step over all layers).  Each layer has its own KV
+cache and summaries (17 GB in all), so the 256 MB Infinity Cache cannot hold
+a step's data.  K/V are synthetic (refinekv.testing recipe drawn on the GPU:
+N(0,1) keys/values, per-block key offsets, 2% of blocks with query-aligned
+spikes); weights play no part in this op.
+
+One JSON line on stdout: value = microseconds per decode step per layer.
+"""
+
+import argparse
+import ctypes
+import json
+import math
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+for _p in (ROOT, os.path.join(ROOT, "refinekv-release_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+import torch  # noqa: E402
+
+METRIC = "decode attn µs/step/layer @128K ctx GQA32/8 d128; HBM GB/s vs peak"
+PEAK_HBM_GBPS = 8000.0
+KERNELS = ("score", "decide", "attend", "merge")
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=125)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=32)
+    ap.add_argument("--context", type=int, default=131072)
+    ap.add_argument("--heads", type=int, default=8)
+    ap.add_argument("--group", type=int, default=4)
+    ap.add_argument("--dim", type=int, default=128)
+    ap.add_argument("--block", type=int, default=32)
+    ap.add_argument("--eps", type=float, default=0.01)
+    ap.add_argument("--reduction", default="any")
+    ap.add_argument("--spikes", type=float, default=0.02)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--no-dense", action="store_true", help="skip the eps=0 dense baseline")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--graph-only", action="store_true",
+                    help="only the graph-replay timing (for profiler runs)")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# HIP events through the runtime's C API (timing on the kernels' own stream)
+# ---------------------------------------------------------------------------
+
+class HipEvents:
+    def __init__(self, n):
+        self.rt = ctypes.CDLL("libamdhip64.so")
+        self.rt.hipEventCreate.argtypes = [ctypes.POINTER(ctypes.c_void_p)]
+        self.rt.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                ctypes.c_void_p]
+        self.rt.hipEventDestroy.argtypes = [ctypes.c_void_p]
+        self.events = (ctypes.c_void_p * n)()
+        for i in range(n):
+            ev = ctypes.c_void_p()
+            assert self.rt.hipEventCreate(ctypes.byref(ev)) == 0
+            self.events[i] = ev
+
+    def ptr(self, offset=0):
+        return ctypes.cast(ctypes.byref(self.events, offset * ctypes.sizeof(ctypes.c_void_p)),
+                           ctypes.c_void_p)
+
+    def elapsed_ms(self, a, b):
+        ms = ctypes.c_float()
+        assert self.rt.hipEventElapsedTime(ctypes.byref(ms), self.events[a], self.events[b]) == 0
+        return ms.value
+
+    def close(self):
+        for ev in self.events:
+            self.rt.hipEventDestroy(ev)
+
+
+# ---------------------------------------------------------------------------
+# Workload
+# ---------------------------------------------------------------------------
+
+def make_layer(gen, a, capacity, device):
+    """refinekv.testing.decode_inputs' recipe, drawn with a device generator."""
+    H, G, D, P, B = a.heads, a.group, a.dim, a.context, a.block
+    q = torch.randn(H, G, 1, D, generator=gen, device=device)
+    keys = torch.randn(H, P + capacity, D, generator=gen, device=device)
+    values = torch.randn(H, P + capacity, D, generator=gen, device=device)
+    n = math.ceil(P / B)
+    offset = torch.randn(H, n, D, generator=gen, device=device) * 0.5
+    n_spikes = round(a.spikes * H * n)
+    picks = torch.randperm(H * n, generator=gen, device=device)[:n_spikes]
+    spike = torch.zeros(H * n, D, device=device)
+    spike[picks] = 4.0 * q[:, :, 0].mean(1)[picks // n]
+    offset += spike.view(H, n, D)
+    keys[:, :P] += offset.repeat_interleave(B, dim=1)[:, :P]
+    return (q.to(torch.bfloat16), keys.to(torch.bfloat16), values.to(torch.bfloat16))
+
+
+def algorithmic_bytes(a, masks, counts, suffix):
+    """Bytes each kernel must move per layer-step, in the reference's formats:
+    score reads k-means and ellipsoids; decide reads value norms and writes
+    the mask; attend reads the value means of unexpanded blocks, the K/V pages
+    of expanded blocks and the suffix; merge writes the output."""
+    H, G, D = a.heads, a.group, a.dim
+    n = counts.numel()
+    sel = masks.float().mean(0)  # (H, N) fraction over layers
+    expanded_tokens = (sel * counts.float()[None]).sum().item()
+    unexpanded = ((1 - sel).sum()).item()
+    q_bytes = H * G * D * 2
+    score = 2 * H * n * D * 2 + q_bytes
+    decide = H * n * 4 + H * n
+    attend = unexpanded * D * 2 + expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
+    merge = H * G * D * 2
+    return dict(score=score, decide=decide, attend=attend, merge=merge)
+
+
+def main():
+    a = parse_args()
+    if a.gpus != 1:
+        print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
+              "(the path would shard by KV head with no exchange; see DESIGN.md)",
+              file=sys.stderr)
+        sys.exit(2)
+    from refinekv import RefineKVConfig, build_summary, sparse_attention, _hip
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _hip.lib()
+    capacity = a.warmup + a.steps + 1
+    cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps,
+                         gqa_reduction=a.reduction)
+    dense_cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=0.0,
+                               gqa_reduction=a.reduction)
+
+    # ---- layers, caches and prefill summaries ---------------------------
+    gen = torch.Generator(device=dev).manual_seed(a.seed)
+    layers = []
+    t_sum = 0.0
+    for i in range(a.layers):
+        q, k, v = make_layer(gen, a, capacity, dev)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        summary = build_summary(k[:, :a.context], v[:, :a.context], cfg)
+        torch.cuda.synchronize()
+        t_sum += time.perf_counter() - t0
+        layers.append(dict(q=q, k=k, v=v, summary=summary, ws={}, dws={}))
+    log(f"[bench] {a.layers} layers ready, summary build {t_sum / a.layers * 1e6:.1f} us/layer "
+        "(wall, includes launch)")
+    suffix_len = torch.zeros((), dtype=torch.int32, device=dev)
+
+    def step(config, key):
+        suffix_len.add_(1)
+        for L in layers:
+            sparse_attention(L["q"], L["summary"], L["k"][:, a.context:], L["v"][:, a.context:],
+                             config, workspace=L[key], suffix_length=suffix_len)
+
+    def timed_graph(config, key, warmup, steps):
+        suffix_len.fill_(0)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            for _ in range(warmup):
+                step(config, key)
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            step(config, key)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        return start.elapsed_time(end), graph
+
+    # ---- headline: graph replays over the timed window ------------------
+    torch.cuda.synchronize()
+    ms, graph = timed_graph(cfg, "ws", a.warmup, a.steps)
+    us_layer = ms * 1e3 / (a.steps * a.layers)
+    log(f"[bench] refinekv graph: {ms / a.steps:.3f} ms/step, {us_layer:.2f} us/layer-step")
+    del graph
+    if a.graph_only:
+        print(json.dumps(dict(metric=METRIC, value=round(us_layer, 3), unit="us/step/layer")))
+        return
+
+    # Masks of the last step (suffix = warmup + steps) for f and bytes.
+    masks = []
+    for L in layers:
+        res = sparse_attention(L["q"], L["summary"], L["k"][:, a.context:], L["v"][:, a.context:],
+                               cfg, workspace=L["ws"], return_selected=True,
+                               suffix_length=suffix_len)
+        masks.append(res.selected.clone())
+    masks = torch.stack(masks)
+    frac = masks.float().mean().item()
+    counts = layers[0]["summary"].counts
+    suffix_now = int(suffix_len.item())
+    nbytes = algorithmic_bytes(a, masks, counts, suffix_now)
+    total_bytes = sum(nbytes.values())
+
+    # ---- per-kernel durations with HIP events (eager, same stream) ------
+    ev = HipEvents(5 * a.layers)
+    kernel_ms = {k: 0.0 for k in KERNELS}
+    reps = 3
+    for _ in range(reps):
+        for i, L in enumerate(layers):
+            lib.rkv_set_profile_events(ev.ptr(5 * i))
+            sparse_attention(L["q"], L["summary"], L["k"][:, a.context:], L["v"][:, a.context:],
+                             cfg, workspace=L["ws"], suffix_length=suffix_len)
+        lib.rkv_set_profile_events(None)
+        torch.cuda.synchronize()
+        for i in range(a.layers):
+            for j, name in enumerate(KERNELS):
+                kernel_ms[name] += ev.elapsed_ms(5 * i + j, 5 * i + j + 1)
+    ev.close()
+    kernel_us = {k: v * 1e3 / (reps * a.layers) for k, v in kernel_ms.items()}
+    dominant = max(kernel_us, key=kernel_us.get)
+    achieved = nbytes[dominant] / (kernel_us[dominant] * 1e-6) / 1e9
+    log(f"[bench] kernels (us, eager): " + ", ".join(f"{k} {v:.2f}" for k, v in kernel_us.items())
+        + f"; expanded {frac:.4f}")
+
+    # ---- dense baseline on the same GPU: every block expanded -----------
+    dense_us = None
+    if not a.no_dense:
+        d_steps = min(a.steps, 20)
+        ms_d, graph = timed_graph(dense_cfg, "dws", 1, d_steps)
+        dense_us = ms_d * 1e3 / (d_steps * a.layers)
+        del graph
+        log(f"[bench] dense (eps=0) graph: {dense_us:.2f} us/layer-step")
+        for L in layers:
+            L["dws"].clear()
+
+    # ---- CPU baseline: the oracle (C restatement), one thread -----------
+    cpu = None
+    if not a.no_cpu:
+        cpu = cpu_baseline(a, layers[0], suffix_now)
+        log(f"[bench] cpu oracle: {cpu['value']:.0f} us/layer-step ({cpu['sample']})")
+
+    result = {
+        "metric": METRIC,
+        "value": round(us_layer, 3),
+        "unit": "us/step/layer",
+        "n_gpus": 1,
+        "steps": a.steps,
+        "warmup": a.warmup,
+        "ms_per_step": round(ms / a.steps, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (refinekv.testing recipe on GPU: N(0,1) K/V, block key offsets, "
+                f"{a.spikes:.0%} query-aligned spike blocks)",
+        "config": {
+            "workload": f"RefineKV decode attention, Llama-3.1-8B attention shape: {a.layers} "
+                        f"layers x {a.heads * a.group}q/{a.heads}kv heads, d{a.dim}, "
+                        f"{a.context} prompt tokens, block {a.block}, eps {a.eps}, "
+                        f"GQA {a.reduction}, suffix {a.warmup + 1}..{suffix_now}, HIP graph "
+                        "per decode step",
+            "context": a.context, "layers": a.layers, "kv_heads": a.heads,
+            "q_heads": a.heads * a.group, "head_dim": a.dim, "block_size": a.block,
+            "eps": a.eps, "gqa_reduction": a.reduction, "parallelism": "single GPU",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "kernel": dominant,
+            "achieved": round(achieved, 1),
+            "peak": PEAK_HBM_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / PEAK_HBM_GBPS, 4),
+            "traffic": None,
+        },
+        "cpu_baseline": cpu,
+        "expanded_fraction": round(frac, 5),
+        "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
+        "algorithmic_bytes": {k: int(v) for k, v in nbytes.items()},
+        "step_GBps": round(total_bytes / (us_layer * 1e-6) / 1e9, 1),
+        "step_frac_of_peak": round(total_bytes / (us_layer * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
+        "dense_us_per_layer_step": None if dense_us is None else round(dense_us, 3),
+        "speedup_vs_dense": None if dense_us is None else round(dense_us / us_layer, 3),
+        "summary_us_per_layer_wall": round(t_sum / a.layers * 1e6, 1),
+        "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
+    }
+    print(json.dumps(result), flush=True)
+
+
+def cpu_baseline(a, layer, suffix):
+    """The oracle's select + mixed attention on one layer's tensors, timed on
+    the host for about --cpu-seconds (single thread)."""
+    import numpy as np
+
+    import oracle
+
+    s = layer["summary"]
+    bits = lambda t: t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+    summ = dict(counts=s.counts.cpu().numpy(), key_mean=bits(s.key_mean),
+                value_mean=bits(s.value_mean), ellipsoid=bits(s.ellipsoid),
+                value_norm=s.value_norm.cpu().numpy(),
+                max_value_norm=s.max_value_norm.cpu().numpy(), prompt_length=s.prompt_length,
+                block_size=s.block_size)
+    kp, vp = bits(s.keys), bits(s.values)
+    ks = bits(layer["k"][:, a.context:a.context + suffix])
+    vs = bits(layer["v"][:, a.context:a.context + suffix])
+    q = layer["q"][:, :, 0].float().cpu().numpy()
+    oracle.sparse_attention(q, summ, kp, vp, ks, vs, a.eps, a.reduction)  # warm
+    n, t0 = 0, time.perf_counter()
+    while True:
+        oracle.sparse_attention(q, summ, kp, vp, ks, vs, a.eps, a.reduction)
+        n += 1
+        el = time.perf_counter() - t0
+        if el >= a.cpu_seconds or n >= 1000:
+            break
+    return {"value": round(el / n * 1e6, 1), "unit": "us/step/layer", "cores": 1,
+            "kind": "port",
+            "sample": f"{n} layer-steps of the same workload on one layer's tensors "
+                      f"({a.context} tokens, suffix {suffix}), oracle C restatement "
+                      f"(oracle/rkv_oracle.c), 1 thread, {os.cpu_count()} host CPUs visible"}
+
+
+if __name__ == "__main__":
+    main()

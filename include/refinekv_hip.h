@@ -1,0 +1,133 @@
+/*
+ * refinekv_hip.h -- C ABI of librefinekv_hip.so, RefineKV's decode-time
+ * attention path on AMD Instinct MI355X (gfx950).
+ *
+ * Conventions for every entry point:
+ *  - Pointers are device pointers unless stated otherwise; strides are in
+ *    elements; head_dim (the innermost axis) is always dense.
+ *  - bfloat16 data is passed as its 16-bit pattern.
+ *  - Work is enqueued on `stream` (a hipStream_t); nothing synchronizes the
+ *    host, nothing allocates device memory, so every call can be captured in
+ *    a HIP graph.  Calls that share a workspace must be ordered on one stream.
+ *  - Return value: 0 on success, else RKV_* error code; rkv_last_error()
+ *    gives a message (thread-local, valid until the next call).
+ */
+#ifndef REFINEKV_HIP_H
+#define REFINEKV_HIP_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct ihipStream_t* rkv_stream_t; /* == hipStream_t */
+
+enum {
+  RKV_OK = 0,
+  RKV_INVALID_ARGUMENT = 1, /* raised as ValueError by the Python binding */
+  RKV_UNSUPPORTED = 2,      /* TypeError */
+  RKV_LAUNCH_FAILED = 3,    /* RuntimeError */
+  RKV_WORKSPACE_TOO_SMALL = 4
+};
+
+/* GQA reduction codes (src/refinekv/kernels/runtime.py:23). */
+enum { RKV_REDUCE_MEAN = 0, RKV_REDUCE_MAX = 1, RKV_REDUCE_ANY = 2 };
+
+/* Key/value dtype codes for rkv_summary. */
+enum { RKV_BF16 = 0, RKV_F16 = 1, RKV_F32 = 2 };
+
+/* Message of the last failed call on this thread ("" after a success). */
+const char* rkv_last_error(void);
+
+/* ABI version (incremented on incompatible changes). */
+int rkv_version(void);
+
+/*
+ * Prompt block summaries.  Replaces build_summary
+ * (src/refinekv/summary.py:46-113; it has no accelerated backend in the
+ * reference, which runs torch ops on the cache's device).
+ *   keys/values: (heads, length, dim) with head/token strides, dtype RKV_*.
+ *   counts: (ceil(length/block_size),) int64.
+ *   key_mean, value_mean, ellipsoid: (heads, n_blocks, dim) bf16.
+ *   value_norm: (heads, n_blocks) fp32; max_value_norm: (heads,) fp32.
+ * dim in 32..256 (multiple of 32); block_size in {16, 32, 64}.
+ */
+int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
+                const void* values, int64_t v_head_stride, int64_t v_token_stride, int dtype,
+                int64_t heads, int64_t length, int64_t dim, int64_t block_size, int64_t* counts,
+                void* key_mean, void* value_mean, void* ellipsoid, float* value_norm,
+                float* max_value_norm, rkv_stream_t stream);
+
+/* Workspace bytes needed by rkv_select / rkv_decode for this shape. */
+size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
+
+/* Byte offsets inside the workspace (for tests): z, delta, lse, tilebits,
+ * attn_m, attn_l, attn_acc, total, n_tiles, workers -> out10[0..9]. */
+int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
+                         int64_t* out10);
+
+/*
+ * Expanded-block mask for one query.  Replaces select_blocks_triton
+ * (src/refinekv/kernels/runtime.py:93-120) behind select_blocks
+ * (src/refinekv/attention.py:62-73); semantics of select_blocks_reference
+ * (src/refinekv/reference.py:37-47) plus an optional anchor union.
+ *   query: (heads, group, dim) bf16, dense.  Summary tensors as above.
+ *   anchor_mask: (heads, n_blocks) bytes 0/1 or NULL.
+ *   mask_out: (heads, n_blocks) bytes 0/1 (a torch.bool tensor).
+ *   risk_out (heads, group, n_blocks) fp32, stats_out (heads, group, 2) fp32
+ *   (log Z, log C) and accessed_blocks (+= sum over blocks of count if
+ *   expanded else 1) are optional (NULL = off).
+ *   workspace: rkv_workspace_bytes() bytes, 256-byte aligned.
+ */
+int rkv_select(const void* query, const void* key_mean, const void* ellipsoid,
+               const float* value_norm, const float* max_value_norm, int64_t heads,
+               int64_t group, int64_t dim, int64_t n_blocks, int64_t block_size,
+               int64_t prompt_length, float eps, int reduction, const uint8_t* anchor_mask,
+               uint8_t* mask_out, float* risk_out, float* stats_out,
+               unsigned long long* accessed_blocks, void* workspace, size_t workspace_bytes,
+               rkv_stream_t stream);
+
+/*
+ * One decode step of RefineKV attention.  Replaces sparse_attention_triton
+ * (src/refinekv/kernels/runtime.py:123-227) behind sparse_attention
+ * (src/refinekv/attention.py:76-134); semantics of
+ * sparse_attention_reference (src/refinekv/reference.py:50-73).
+ *   key_pages/value_pages: (heads, n_blocks, block_size, dim) bf16 pages of
+ *     the prompt cache; only the head stride is free (block and token
+ *     strides are block_size*dim and dim).
+ *   key_suffix/value_suffix: generated tokens, (heads, capacity, dim) with
+ *     head/token strides; suffix_length: device int32 scalar giving the valid
+ *     prefix (clamped to [0, capacity]), or NULL to use all `capacity` tokens.
+ *   mask_out: (heads, n_blocks) bytes 0/1; output: (heads, group, dim) bf16.
+ *   accessed_blocks: optional access counter as in rkv_select.
+ */
+int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
+               const void* value_mean, const float* value_norm, const float* max_value_norm,
+               const void* key_pages, int64_t key_page_head_stride, const void* value_pages,
+               int64_t value_page_head_stride, const void* key_suffix,
+               int64_t key_suffix_head_stride, int64_t key_suffix_token_stride,
+               const void* value_suffix, int64_t value_suffix_head_stride,
+               int64_t value_suffix_token_stride, int64_t suffix_capacity,
+               const int32_t* suffix_length, int64_t heads, int64_t group, int64_t dim,
+               int64_t n_blocks, int64_t block_size, int64_t prompt_length, float eps,
+               int reduction, const uint8_t* anchor_mask, uint8_t* mask_out, void* output,
+               unsigned long long* accessed_blocks, void* workspace, size_t workspace_bytes,
+               rkv_stream_t stream);
+
+/* Profiling hook with no reference counterpart: when `events` points to 5
+ * hipEvent_t, later rkv_select / rkv_decode calls on this thread record
+ * events[0] before the first kernel and events[1..4] after the score,
+ * decide, attend and merge kernels.  NULL turns it off. */
+int rkv_set_profile_events(void* events);
+
+/* Test hook with no reference counterpart: applies the kernels' device
+ * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */
+int rkv_math_probe(int fn, const float* x, float* y, int64_t n, rkv_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* REFINEKV_HIP_H */

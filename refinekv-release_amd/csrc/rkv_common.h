@@ -1,0 +1,116 @@
+// Device-side building blocks shared by the RefineKV kernels (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "rkv_math.h"
+
+namespace rkv {
+
+constexpr int kWave = 64;
+constexpr int kTile = 64;             // blocks per log-sum-exp tile (one per lane)
+constexpr int kMaxGroup = 16;         // query heads per KV head
+constexpr float kDeltaMax = 10.0f;    // reference.py:20 switch between risk branches
+constexpr float kInflate = 1.00390625f;  // 1 + 2^-8 (reference.py:16, summary.py:96)
+constexpr float kLn2 = 0.693147182464599609375f;  // fp32(math.log(2))
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kPosInf = __builtin_inff();
+
+// Reduction codes of runtime.py:23.
+enum Reduction { kMean = 0, kMax = 1, kAny = 2 };
+
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+__device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, kWave); }
+
+// Sum over the 16 lanes of a lane group, xor butterfly with distances 8,4,2,1.
+// Every lane of the group ends with the same value (fp32 add commutes).
+__device__ __forceinline__ float group16_sum(float v) {
+  v = v + shfl_xor(v, 8);
+  v = v + shfl_xor(v, 4);
+  v = v + shfl_xor(v, 2);
+  v = v + shfl_xor(v, 1);
+  return v;
+}
+
+// Sum over the wave, xor butterfly with distances 32..1.
+__device__ __forceinline__ float wave_sum(float v) {
+  v = v + shfl_xor(v, 32);
+  v = v + shfl_xor(v, 16);
+  v = v + shfl_xor(v, 8);
+  v = v + shfl_xor(v, 4);
+  v = v + shfl_xor(v, 2);
+  v = v + shfl_xor(v, 1);
+  return v;
+}
+
+__device__ __forceinline__ float wave_nanmax(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = nanmax(v, shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float wave_nanmin(float v) {
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) v = nanmin(v, shfl_xor(v, o));
+  return v;
+}
+
+__device__ __forceinline__ float finite_or_zero(float m) { return is_finite(m) || is_nan(m) ? m : 0.0f; }
+
+// 16-byte aligned bf16 vector loads.
+template <int N>
+struct Bf16Vec {
+  uint16_t v[N];
+};
+
+template <int N>
+__device__ __forceinline__ void load_bf16(const uint16_t* __restrict__ p, float (&out)[N]) {
+  static_assert(N % 2 == 0, "even element count");
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 8) {
+      uint4 u = *reinterpret_cast<const uint4*>(p + i);
+      uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        out[i + 2 * j] = bits_f32(w[j] << 16);
+        out[i + 2 * j + 1] = bits_f32(w[j] & 0xFFFF0000u);
+      }
+    }
+  } else if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N; i += 4) {
+      uint2 u = *reinterpret_cast<const uint2*>(p + i);
+      out[i] = bits_f32(u.x << 16);
+      out[i + 1] = bits_f32(u.x & 0xFFFF0000u);
+      out[i + 2] = bits_f32(u.y << 16);
+      out[i + 3] = bits_f32(u.y & 0xFFFF0000u);
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N; i += 2) {
+      uint32_t u = *reinterpret_cast<const uint32_t*>(p + i);
+      out[i] = bits_f32(u << 16);
+      out[i + 1] = bits_f32(u & 0xFFFF0000u);
+    }
+  }
+}
+
+// Position of the k-th (0-based) set bit of m; m must have more than k bits.
+__device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
+  int pos = 0;
+#pragma unroll
+  for (int w = 32; w >= 1; w >>= 1) {
+    const uint64_t low = m & ((1ull << w) - 1ull);
+    int c = __popcll(low);
+    if (k >= c) {
+      k -= c;
+      m >>= w;
+      pos += w;
+    }
+  }
+  return pos;
+}
+
+}  // namespace rkv

@@ -1,0 +1,241 @@
+"""ctypes binding of librefinekv_hip.so, the gfx950 kernels behind ``backend="hip"``.
+
+The library's C ABI (declared in include/refinekv_hip.h) takes raw device
+pointers, element strides and the current HIP stream; it allocates nothing
+and never synchronizes, so calls can be captured in a HIP graph.  This module
+owns the per-call plumbing: argument checks the kernels rely on, the
+caller-owned workspace, and mapping C error codes to Python exceptions.
+There is no fallback: if the library is missing, calls raise.
+"""
+
+import ctypes
+import os
+
+import torch
+
+LIB_NAME = "librefinekv_hip.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+REDUCTION_CODES = {"mean": 0, "max": 1, "any": 2}  # src/refinekv/kernels/runtime.py:23
+DTYPE_CODES = {torch.bfloat16: 0, torch.float16: 1, torch.float32: 2}
+SUPPORTED_DIMS = tuple(range(32, 257, 32))
+MAX_GROUP = 16
+
+_lib = None
+_load_error = None
+
+_p = ctypes.c_void_p
+_i64 = ctypes.c_int64
+_f32 = ctypes.c_float
+_int = ctypes.c_int
+_size = ctypes.c_size_t
+
+
+class HipUnavailable(RuntimeError):
+    pass
+
+
+def _bind(lib):
+    lib.rkv_last_error.restype = ctypes.c_char_p
+    lib.rkv_version.restype = _int
+    lib.rkv_summary.argtypes = [_p, _i64, _i64, _p, _i64, _i64, _int, _i64, _i64, _i64, _i64, _p,
+                                _p, _p, _p, _p, _p, _p]
+    lib.rkv_summary.restype = _int
+    lib.rkv_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
+    lib.rkv_workspace_bytes.restype = _size
+    lib.rkv_workspace_layout.argtypes = [_i64, _i64, _i64, _i64, _p]
+    lib.rkv_workspace_layout.restype = _int
+    lib.rkv_select.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int,
+                               _p, _p, _p, _p, _p, _p, _size, _p]
+    lib.rkv_select.restype = _int
+    lib.rkv_decode.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p,
+                               _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
+                               _int, _p, _p, _p, _p, _p, _size, _p]
+    lib.rkv_decode.restype = _int
+    lib.rkv_math_probe.argtypes = [_int, _p, _p, _i64, _p]
+    lib.rkv_math_probe.restype = _int
+    lib.rkv_set_profile_events.argtypes = [_p]
+    lib.rkv_set_profile_events.restype = _int
+    return lib
+
+
+def lib():
+    """The loaded library; raises HipUnavailable if it is not built."""
+    global _lib, _load_error
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise HipUnavailable(
+                f"RefineKV HIP library not built ({LIB_PATH}); run __graft_entry__.build()")
+        try:
+            _lib = _bind(ctypes.CDLL(LIB_PATH))
+        except OSError as error:  # pragma: no cover - depends on the image
+            _load_error = error
+            raise HipUnavailable(f"cannot load {LIB_PATH}: {error}") from error
+    return _lib
+
+
+def is_rocm_device(tensor):
+    return tensor.is_cuda and torch.version.hip is not None
+
+
+def _check(rc, name):
+    if rc:
+        message = lib().rkv_last_error().decode(errors="replace")
+        if rc in (1, 4):
+            raise ValueError(f"{name}: {message}")
+        if rc == 2:
+            raise TypeError(f"{name}: {message}")
+        raise RuntimeError(f"{name}: {message}")
+
+
+def _ptr(t):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else None
+
+
+def _stream(device):
+    return ctypes.c_void_p(torch.cuda.current_stream(device).cuda_stream)
+
+
+# ---------------------------------------------------------------------------
+# Summary
+# ---------------------------------------------------------------------------
+
+def _row_aligned(t, nbytes):
+    """t with dim stride 1, its data pointer and head/token strides multiples
+    of ``nbytes`` (a copy only when the view is not)."""
+    es = t.element_size()
+    ok = (t.stride(-1) == 1 and t.data_ptr() % nbytes == 0
+          and all((t.stride(i) * es) % nbytes == 0 for i in range(t.dim() - 1)))
+    return t if ok else t.clone(memory_format=torch.contiguous_format)
+
+
+def summary_fields(keys, values, block):
+    """Run the summary kernel on (H, L, D) keys/values; returns the tensors of
+    BlockSummary other than the page views."""
+    heads, length, dim = keys.shape
+    need = keys.element_size() * (2 if dim <= 128 else 4)
+    keys, values = _row_aligned(keys, need), _row_aligned(values, need)
+    n_blocks = -(-length // block)
+    dev = keys.device
+    counts = torch.empty(n_blocks, device=dev, dtype=torch.int64)
+    key_mean = torch.empty(heads, n_blocks, dim, device=dev, dtype=torch.bfloat16)
+    value_mean = torch.empty_like(key_mean)
+    ellipsoid = torch.empty_like(key_mean)
+    value_norm = torch.empty(heads, n_blocks, device=dev, dtype=torch.float32)
+    max_value_norm = torch.empty(heads, device=dev, dtype=torch.float32)
+    rc = lib().rkv_summary(
+        _ptr(keys), keys.stride(0), keys.stride(1), _ptr(values), values.stride(0),
+        values.stride(1), DTYPE_CODES[keys.dtype], heads, length, dim, block, _ptr(counts),
+        _ptr(key_mean), _ptr(value_mean), _ptr(ellipsoid), _ptr(value_norm),
+        _ptr(max_value_norm), _stream(dev))
+    _check(rc, "rkv_summary")
+    return counts, key_mean, value_mean, ellipsoid, value_norm, max_value_norm
+
+
+# ---------------------------------------------------------------------------
+# Workspace
+# ---------------------------------------------------------------------------
+
+def workspace_bytes(heads, group, dim, n_blocks):
+    return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
+
+
+def workspace_layout(heads, group, dim, n_blocks):
+    out = (ctypes.c_int64 * 10)()
+    _check(lib().rkv_workspace_layout(heads, group, dim, n_blocks, out), "rkv_workspace_layout")
+    names = ("z", "delta", "lse", "tilebits", "attn_m", "attn_l", "attn_acc", "total",
+             "n_tiles", "workers")
+    return dict(zip(names, list(out)))
+
+
+def _buffer(workspace, name, shape, device, dtype):
+    """Reusable tensor keyed by name (the reference's workspace dict,
+    src/refinekv/kernels/runtime.py:26-37)."""
+    tensor = workspace.get(name) if workspace is not None else None
+    if (tensor is None or tuple(tensor.shape) != tuple(shape) or tensor.device != device
+            or tensor.dtype != dtype):
+        tensor = torch.empty(shape, device=device, dtype=dtype)
+        if workspace is not None:
+            workspace[name] = tensor
+    return tensor
+
+
+def _scratch(workspace, heads, group, dim, n_blocks, device):
+    nbytes = workspace_bytes(heads, group, dim, n_blocks)
+    return _buffer(workspace, "hip_scratch", (nbytes,), device, torch.uint8)
+
+
+# ---------------------------------------------------------------------------
+# Selection and decode
+# ---------------------------------------------------------------------------
+
+def _summary_args(summary):
+    return (_ptr(summary.key_mean), _ptr(summary.ellipsoid), _ptr(summary.value_norm),
+            _ptr(summary.max_value_norm))
+
+
+def select(query, summary, config, workspace=None, risk_out=None, stats_out=None,
+           accessed=None, anchor_mask=None):
+    """Expanded-block mask (H, N) for one query (H, G, 1, D); a fresh tensor."""
+    heads, group, _, dim = query.shape
+    q = query.reshape(heads * group, dim)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    n_blocks = summary.num_blocks
+    scratch = _scratch(workspace, heads, group, dim, n_blocks, query.device)
+    mask = torch.empty(heads, n_blocks, device=query.device, dtype=torch.bool)
+    anchor = anchor_mask.contiguous() if anchor_mask is not None else None
+    rc = lib().rkv_select(
+        _ptr(q), *_summary_args(summary), heads, group, dim, n_blocks, summary.block_size,
+        summary.prompt_length, float(config.eps), REDUCTION_CODES[config.gqa_reduction],
+        _ptr(anchor), _ptr(mask), _ptr(risk_out), _ptr(stats_out), _ptr(accessed),
+        _ptr(scratch), scratch.numel(), _stream(query.device))
+    _check(rc, "rkv_select")
+    return mask
+
+
+def decode(query, summary, key_suffix, value_suffix, config, anchor_mask=None, workspace=None,
+           suffix_length=None, accessed=None):
+    """One decode step: returns (output (H, G, 1, D), mask (H, N) bool).
+
+    Both outputs live in ``workspace`` and are overwritten by the next call
+    that reuses it (the reference's contract, src/refinekv/attention.py:96-98).
+    """
+    heads, group, _, dim = query.shape
+    device = query.device
+    q = query.reshape(heads * group, dim)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    n_blocks = summary.num_blocks
+    scratch = _scratch(workspace, heads, group, dim, n_blocks, device)
+    mask = _buffer(workspace, "hip_mask", (heads, n_blocks), device, torch.bool)
+    output = _buffer(workspace, "hip_output", (heads, group, 1, dim), device, query.dtype)
+    ch_bytes = dim // 16 * 2
+    need = 16 if ch_bytes % 16 == 0 else (8 if ch_bytes % 8 == 0 else 4)
+    key_suffix = _row_aligned(key_suffix, need)
+    value_suffix = _row_aligned(value_suffix, need)
+    anchor = None
+    if anchor_mask is not None:
+        anchor = anchor_mask if anchor_mask.is_contiguous() else anchor_mask.contiguous()
+    kp, vp = summary.keys, summary.values
+    capacity = key_suffix.shape[1]
+    rc = lib().rkv_decode(
+        _ptr(q), _ptr(summary.key_mean), _ptr(summary.ellipsoid), _ptr(summary.value_mean),
+        _ptr(summary.value_norm), _ptr(summary.max_value_norm), _ptr(kp), kp.stride(0), _ptr(vp),
+        vp.stride(0), _ptr(key_suffix) if capacity else None, key_suffix.stride(0),
+        key_suffix.stride(1), _ptr(value_suffix) if capacity else None, value_suffix.stride(0),
+        value_suffix.stride(1), capacity, _ptr(suffix_length), heads, group, dim, n_blocks,
+        summary.block_size, summary.prompt_length, float(config.eps),
+        REDUCTION_CODES[config.gqa_reduction], _ptr(anchor), _ptr(mask), _ptr(output),
+        _ptr(accessed), _ptr(scratch), scratch.numel(), _stream(device))
+    _check(rc, "rkv_decode")
+    return output, mask
+
+
+def math_probe(fn, x):
+    """Device scalar functions for tests: fn in {'exp', 'log', 'bf16', 'sqrt'}."""
+    code = {"exp": 0, "log": 1, "bf16": 2, "sqrt": 3}[fn]
+    x = x.contiguous().float()
+    y = torch.empty_like(x)
+    _check(lib().rkv_math_probe(code, _ptr(x), _ptr(y), x.numel(), _stream(x.device)),
+           "rkv_math_probe")
+    return y

@@ -1,0 +1,139 @@
+"""Single-token decode attention API (mirror of src/refinekv/attention.py:12-134).
+
+``select_blocks`` and ``sparse_attention`` keep the reference's signatures,
+validation and error types.  ``backend="hip"`` runs the gfx950 kernels
+through the C ABI; ``"auto"`` picks them for ROCm tensors whose shapes they
+support (bf16 query, head_dim 32..256 in steps of 32, GQA group <= 16) and
+the torch restatement for CPU tensors.  On a ROCm device "auto" never falls
+back silently when the library is missing: it raises.
+"""
+
+from typing import NamedTuple
+
+import torch
+
+from .config import RefineKVConfig
+from .summary import BlockSummary
+
+
+class AttentionResult(NamedTuple):
+    output: torch.Tensor
+    selected: torch.Tensor | None
+
+
+def _backend(query, config):
+    """Mirror of attention.py:17-40 with the HIP backend in Triton's place."""
+    from . import _hip
+
+    if config.backend == "torch":
+        return "torch"
+    on_rocm = _hip.is_rocm_device(query)
+    if config.backend == "hip" and not on_rocm:
+        raise RuntimeError("the HIP backend requires a ROCm GPU tensor")
+    if not on_rocm:
+        return "torch"
+    if query.dtype != torch.bfloat16:
+        if config.backend == "hip":
+            raise TypeError("the HIP backend requires BF16 queries")
+        return "torch"
+    dim, group = query.shape[-1], query.shape[1]
+    if dim < 32 or dim > 256 or dim % 32 or group > _hip.MAX_GROUP:
+        if config.backend == "hip":
+            raise ValueError("HIP requires head_dim in 32..256 (multiple of 32) and GQA group <= 16")
+        return "torch"
+    _hip.lib()  # raises when the kernels are not built: no silent fallback on a GPU
+    return "hip"
+
+
+def _validate(query, summary, config, anchor_mask=None):
+    """Mirror of attention.py:43-59."""
+    if query.ndim != 4 or query.shape[2] != 1 or min(query.shape) <= 0:
+        raise ValueError("query must have shape (kv_heads, group_size, 1, head_dim)")
+    if query.shape[0] != summary.keys.shape[0] or query.shape[-1] != summary.keys.shape[-1]:
+        raise ValueError("query heads and dimension must match the summary")
+    if query.device != summary.keys.device:
+        raise ValueError("query and summary must be on the same device")
+    if config.block_size != summary.block_size:
+        raise ValueError("config.block_size must match the summary")
+    if anchor_mask is not None:
+        if anchor_mask.dtype != torch.bool or tuple(anchor_mask.shape) != (
+            query.shape[0],
+            summary.num_blocks,
+        ):
+            raise ValueError("anchor_mask must be boolean with shape (kv_heads, blocks)")
+        if anchor_mask.device != query.device:
+            raise ValueError("anchor_mask must be on the query device")
+
+
+def _check_hip_summary(summary):
+    if summary.key_mean.dtype != torch.bfloat16 or summary.keys.dtype != torch.bfloat16:
+        raise TypeError("the HIP decode kernels need bf16 summaries and a bf16 KV cache")
+
+
+@torch.no_grad()
+def select_blocks(query, summary, config=None, *, workspace=None):
+    """Boolean (kv_heads, blocks) mask of expanded blocks for one query."""
+    config = config or RefineKVConfig(block_size=summary.block_size)
+    _validate(query, summary, config)
+    if _backend(query, config) == "hip":
+        from . import _hip
+
+        _check_hip_summary(summary)
+        return _hip.select(query, summary, config, workspace)
+    from .reference import select_blocks as select_torch
+
+    return select_torch(query, summary, config)[0]
+
+
+@torch.no_grad()
+def sparse_attention(
+    query: torch.Tensor,
+    summary: BlockSummary,
+    key_suffix: torch.Tensor,
+    value_suffix: torch.Tensor,
+    config: RefineKVConfig | None = None,
+    *,
+    anchor_mask: torch.Tensor | None = None,
+    workspace: dict | None = None,
+    return_selected: bool = False,
+    suffix_length: torch.Tensor | None = None,
+) -> AttentionResult:
+    """Attend to representatives, expanded prompt blocks and the exact suffix.
+
+    ``query`` is (kv_heads, group_size, 1, head_dim); suffix K/V are
+    (kv_heads, suffix_tokens, head_dim) and hold only visible tokens.
+    ``suffix_length`` (a device int32 scalar) gives the valid prefix of a
+    fixed-capacity suffix buffer, for HIP graph replay.  HIP outputs live in
+    the workspace and are overwritten by the next call that reuses it; clone
+    them to keep them longer.
+    """
+    config = config or RefineKVConfig(block_size=summary.block_size)
+    _validate(query, summary, config, anchor_mask)
+    expected = (query.shape[0], query.shape[-1])
+    if key_suffix.ndim != 3 or key_suffix.shape != value_suffix.shape:
+        raise ValueError("suffix K/V must have matching (kv_heads, tokens, head_dim) shapes")
+    if (key_suffix.shape[0], key_suffix.shape[-1]) != expected:
+        raise ValueError("suffix heads and dimension must match the query")
+    if key_suffix.device != query.device or value_suffix.device != query.device:
+        raise ValueError("suffix K/V must be on the query device")
+    backend = _backend(query, config)
+    if suffix_length is not None:
+        if (suffix_length.shape != () or suffix_length.device != query.device
+                or suffix_length.dtype != torch.int32):
+            raise ValueError("suffix_length must be a scalar int32 tensor on the query device")
+        if backend != "hip":
+            raise ValueError("device-side suffix_length requires the HIP backend")
+    if backend == "hip":
+        from . import _hip
+
+        _check_hip_summary(summary)
+        if key_suffix.dtype != torch.bfloat16 or value_suffix.dtype != torch.bfloat16:
+            raise TypeError("the HIP decode kernels need a bf16 suffix")
+        output, mask = _hip.decode(query, summary, key_suffix, value_suffix, config,
+                                   anchor_mask, workspace, suffix_length)
+        return AttentionResult(output, mask if return_selected else None)
+    from .reference import sparse_attention as attention_torch
+
+    output, selected = attention_torch(query, summary, key_suffix, value_suffix, config,
+                                       anchor_mask)
+    return AttentionResult(output, selected if return_selected else None)

@@ -1,0 +1,66 @@
+"""The C-ABI library loads and exports every entry point of include/refinekv_hip.h.
+
+CPU only: no call here touches a GPU (rkv_workspace_bytes, rkv_workspace_layout,
+rkv_version and rkv_last_error are host functions).
+"""
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "refinekv_hip.h")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(rkv_[a-z_]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    from refinekv import _hip
+
+    if not os.path.exists(_hip.LIB_PATH):
+        pytest.fail("librefinekv_hip.so is not built; run __graft_entry__.build()")
+    return _hip.lib()
+
+
+def test_header_is_valid_c():
+    subprocess.run(["gcc", "-std=c99", "-fsyntax-only", "-Wall", "-Werror", "-x", "c", HEADER],
+                   check=True)
+
+
+def test_every_declared_symbol_is_exported(lib):
+    names = declared_functions()
+    assert {"rkv_summary", "rkv_select", "rkv_decode", "rkv_workspace_bytes",
+            "rkv_last_error"} <= set(names)
+    for name in names:
+        assert hasattr(lib, name), name
+
+
+def test_version_and_error_channel(lib):
+    assert lib.rkv_version() >= 1
+    assert lib.rkv_workspace_layout(0, 0, 0, 0, None) == 1
+    assert b"bad arguments" in lib.rkv_last_error()
+
+
+def test_workspace_size_covers_layout(lib):
+    from refinekv import _hip
+
+    for heads, group, dim, n in ((8, 4, 128, 4096), (4, 7, 128, 1024), (2, 16, 64, 3),
+                                 (1, 1, 256, 1)):
+        layout = _hip.workspace_layout(heads, group, dim, n)
+        assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
+        assert layout["n_tiles"] == -(-n // 64)
+        regions = [layout[k] for k in ("z", "delta", "lse", "tilebits", "attn_m", "attn_l",
+                                       "attn_acc", "total")]
+        assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
+        rows = heads * group
+        assert layout["delta"] - layout["z"] >= rows * n * 4
+        assert layout["total"] - layout["attn_acc"] >= rows * layout["workers"] * dim * 4
+    assert _hip.workspace_bytes(0, 4, 128, 10) == 0

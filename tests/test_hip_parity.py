@@ -1,0 +1,327 @@
+"""HIP kernels vs the CPU oracle and the reference's golden vectors (GPU).
+
+Bar: bit-exact summaries, selection statistics (z, delta, log Z, log C,
+risk) and masks/counters against the oracle, which shares the kernels' fixed
+fp32 evaluation orders; attention outputs within the north-star tolerance
+(max-abs 2e-2, mean-rel 1e-3) of the oracle's softmax, which is exact to fp64
+over the same bf16 inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import golden_cases as gc
+from refinekv import RefineKVConfig, build_summary, select_blocks, sparse_attention, testing
+
+pytestmark = pytest.mark.gpu
+DEV = torch.device("cuda")
+MAX_ABS, MEAN_REL = 2e-2, 1e-3
+
+
+@pytest.fixture(scope="module")
+def hip():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    from refinekv import _hip
+
+    _hip.lib()  # the HIP library must load: no fallback
+    return _hip
+
+
+def bits16(t):
+    return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+
+def bits32(t):
+    a = t.detach().cpu().contiguous().numpy() if torch.is_tensor(t) else np.asarray(t)
+    return np.ascontiguousarray(a, dtype=np.float32).view(np.uint32)
+
+
+def oracle_summary_of(summary):
+    return dict(counts=summary.counts.cpu().numpy(), key_mean=bits16(summary.key_mean),
+                value_mean=bits16(summary.value_mean), ellipsoid=bits16(summary.ellipsoid),
+                value_norm=summary.value_norm.cpu().numpy(),
+                max_value_norm=summary.max_value_norm.cpu().numpy(),
+                prompt_length=summary.prompt_length, block_size=summary.block_size)
+
+
+def assert_summary_equal(summary, ref):
+    assert np.array_equal(summary.counts.cpu().numpy(), ref["counts"])
+    for name in ("key_mean", "value_mean", "ellipsoid"):
+        got = bits16(getattr(summary, name))
+        bad = int((got != ref[name]).sum())
+        assert bad == 0, f"{name}: {bad} of {got.size} bf16 values differ"
+    for name in ("value_norm", "max_value_norm"):
+        got, want = bits32(getattr(summary, name)), bits32(ref[name])
+        assert np.array_equal(got, want), f"{name}: {int((got != want).sum())} differ"
+
+
+def assert_close_output(got, want):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    err = np.abs(got - want)
+    assert err.max() <= MAX_ABS, f"max-abs {err.max():.3e}"
+    assert err.mean() <= MEAN_REL * np.abs(want).mean() + 1e-6, f"mean-abs {err.mean():.3e}"
+
+
+# ---------------------------------------------------------------------------
+# Device scalar math
+# ---------------------------------------------------------------------------
+
+def test_device_math_bitwise_equals_oracle(hip, oracle_lib):
+    rng = np.random.default_rng(0)
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, 88.72283, 88.7229, -103.97,
+                         -104.5, 1e-40, 1e-45, 3.4e38], np.float32)
+    xe = np.concatenate([rng.uniform(-110, 90, 400000), rng.uniform(-1, 1, 200000),
+                         specials]).astype(np.float32)
+    xl = np.concatenate([np.exp(rng.uniform(-103, 88, 400000)), rng.uniform(0.5, 2, 200000),
+                         np.arange(1, 129), specials]).astype(np.float32)
+    for fn, x, want in (("exp", xe, oracle_lib.expf(xe)), ("log", xl, oracle_lib.logf(xl)),
+                        ("bf16", xe, oracle_lib.bf16_value(oracle_lib.bf16_bits(xe))),
+                        ("sqrt", np.abs(xl), np.sqrt(np.abs(xl)))):
+        got = hip.math_probe(fn, torch.from_numpy(x).to(DEV)).cpu().numpy()
+        g, w = got.view(np.uint32), np.asarray(want, np.float32).view(np.uint32)
+        both_nan = np.isnan(got) & np.isnan(want)
+        bad = (g != w) & ~both_nan
+        assert not bad.any(), f"{fn}: {int(bad.sum())} differ, e.g. x={x[bad][:4]}"
+
+
+# ---------------------------------------------------------------------------
+# Summary
+# ---------------------------------------------------------------------------
+
+SUMMARY_CASES = [
+    (torch.bfloat16, 128, 32, 4099), (torch.bfloat16, 128, 16, 1000), (torch.bfloat16, 128, 64, 4096),
+    (torch.bfloat16, 32, 32, 517), (torch.bfloat16, 64, 16, 300), (torch.bfloat16, 96, 64, 1000),
+    (torch.bfloat16, 160, 32, 333), (torch.bfloat16, 192, 16, 250), (torch.bfloat16, 224, 64, 130),
+    (torch.bfloat16, 256, 32, 999), (torch.float16, 128, 32, 777), (torch.float16, 64, 64, 200),
+    (torch.float32, 128, 32, 999), (torch.float32, 32, 16, 517), (torch.float32, 96, 64, 1000),
+    (torch.float32, 256, 16, 400), (torch.bfloat16, 128, 32, 1), (torch.bfloat16, 64, 64, 63),
+]
+
+
+@pytest.mark.parametrize("dtype,dim,block,length", SUMMARY_CASES,
+                         ids=lambda v: str(v).replace("torch.", ""))
+def test_summary_bit_exact(hip, oracle_lib, dtype, dim, block, length):
+    if dtype == torch.float32:
+        _, k, v = testing.wide_inputs(length=length, dim=dim, heads=3)
+    else:
+        _, k, v = testing.small_inputs(length=length, dim=dim, heads=3, dtype=torch.float32)
+        k, v = k * 3, v * 3
+    k, v = k.to(dtype), v.to(dtype)
+    ref = oracle_lib.summary(k.float().numpy(), v.float().numpy(), block)
+    cfg = RefineKVConfig(backend="hip", block_size=block)
+    summary = build_summary(k.to(DEV), v.to(DEV), cfg)
+    torch.cuda.synchronize()
+    assert_summary_equal(summary, ref)
+
+
+def test_summary_of_strided_cache_view(hip, oracle_lib):
+    """A prefix view of a larger (1, H, capacity, D) cache, as the hook passes it."""
+    _, k, v = testing.small_inputs(length=3000, dim=128, heads=4)
+    cache_k = torch.zeros(1, 4, 3100, 128, dtype=torch.bfloat16)
+    cache_v = torch.zeros_like(cache_k)
+    cache_k[0, :, :3000], cache_v[0, :, :3000] = k, v
+    ref = oracle_lib.summary(k.float().numpy(), v.float().numpy(), 32)
+    ck, cv = cache_k.to(DEV), cache_v.to(DEV)
+    summary = build_summary(ck[0, :, :2990], cv[0, :, :2990], RefineKVConfig(backend="hip"))
+    ref = oracle_lib.summary(k[:, :2990].float().numpy(), v[:, :2990].float().numpy(), 32)
+    torch.cuda.synchronize()
+    assert_summary_equal(summary, ref)
+    # 2990 % 32 != 0: the pages are a padded copy; 2976 tokens: a view of the cache.
+    s2 = build_summary(ck[0, :, :2976], cv[0, :, :2976], RefineKVConfig(backend="hip"))
+    assert s2.keys.data_ptr() == ck.data_ptr()
+
+
+# ---------------------------------------------------------------------------
+# Selection statistics and masks
+# ---------------------------------------------------------------------------
+
+SELECT_CASES = [
+    # heads, group, dim, block, prompt, reduction, eps, spikes
+    (8, 4, 128, 32, 4096, "any", 0.01, 0.02),
+    (4, 7, 128, 64, 3000, "max", 0.005, 0.05),
+    (2, 16, 64, 16, 1000, "mean", 0.1, 0.05),
+    (2, 1, 32, 32, 100, "any", 0.01, 0.1),
+    (3, 5, 96, 16, 777, "mean", 0.02, 0.05),
+    (2, 4, 256, 64, 999, "max", 0.01, 0.05),
+    (2, 2, 160, 32, 2050, "any", 0.001, 0.01),
+    (1, 4, 128, 32, 20000, "any", 0.01, 0.01),
+]
+
+
+def _decode_case(heads, group, dim, block, prompt, spikes, suffix=16, seed=11):
+    inp = testing.decode_inputs(heads=heads, group=group, dim=dim, prompt=prompt, suffix=suffix,
+                                block=block, spike_fraction=spikes, anchors=4, seed=seed)
+    return {k: (v.to(torch.bfloat16) if v.is_floating_point() else v) for k, v in inp.items()}
+
+
+@pytest.mark.parametrize("heads,group,dim,block,prompt,reduction,eps,spikes", SELECT_CASES)
+def test_selection_bit_exact(hip, oracle_lib, heads, group, dim, block, prompt, reduction, eps,
+                             spikes):
+    inp = _decode_case(heads, group, dim, block, prompt, spikes)
+    cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps, gqa_reduction=reduction)
+    summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
+    n = summary.num_blocks
+    risk = torch.empty(heads, group, n, device=DEV)
+    stats = torch.empty(heads, group, 2, device=DEV)
+    ws = {}
+    mask = hip.select(inp["query"].to(DEV), summary, cfg, ws, risk_out=risk, stats_out=stats)
+    torch.cuda.synchronize()
+    summ = oracle_summary_of(summary)
+    qn = inp["query"][:, :, 0].float().numpy()
+    st = oracle_lib.select_stats(qn, summ)
+    layout = hip.workspace_layout(heads, group, dim, n)
+    scratch = ws["hip_scratch"].cpu().numpy()
+    z = scratch[layout["z"]:layout["z"] + heads * group * n * 4].view(np.float32)
+    delta = scratch[layout["delta"]:layout["delta"] + heads * group * n * 4].view(np.float32)
+    assert np.array_equal(bits32(z), bits32(st["z"].ravel())), "z"
+    assert np.array_equal(bits32(delta), bits32(st["delta"].ravel())), "delta"
+    sc = stats.cpu().numpy()
+    assert np.array_equal(bits32(sc[..., 0]), bits32(st["log_z"])), "log Z"
+    assert np.array_equal(bits32(sc[..., 1]), bits32(st["log_c"])), "log C"
+    assert np.array_equal(bits32(risk), bits32(st["risk"])), "risk"
+    want, _, _ = oracle_lib.select(qn, summ, eps, reduction)
+    assert np.array_equal(mask.cpu().numpy().astype(np.uint8), want)
+    # the public API returns the same mask
+    api = select_blocks(inp["query"].to(DEV), summary, cfg, workspace={})
+    assert torch.equal(api.cpu(), mask.cpu())
+
+
+# ---------------------------------------------------------------------------
+# Decode step
+# ---------------------------------------------------------------------------
+
+DECODE_CASES = SELECT_CASES + [
+    (8, 4, 128, 32, 4096, "any", 0.0, 0.02),   # every block expanded (dense)
+    (8, 4, 128, 32, 4096, "mean", 1e6, 0.02),  # none expanded
+]
+
+
+def _pages_bits(t, block):
+    return gc.bf16_bits(gc.padded_pages(t, block))
+
+
+@pytest.mark.parametrize("heads,group,dim,block,prompt,reduction,eps,spikes", DECODE_CASES)
+def test_decode_matches_oracle(hip, oracle_lib, heads, group, dim, block, prompt, reduction,
+                               eps, spikes):
+    inp = _decode_case(heads, group, dim, block, prompt, spikes, suffix=16)
+    cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps, gqa_reduction=reduction)
+    k, v = inp["prompt_keys"], inp["prompt_values"]
+    summary = build_summary(k.to(DEV), v.to(DEV), cfg)
+    summ = oracle_summary_of(summary)
+    n = summary.num_blocks
+    anchor = torch.zeros(heads, n, dtype=torch.bool)
+    anchor[:, -1] = True
+    anchor[0, 0] = True
+    ws = {}
+    qn = inp["query"][:, :, 0].float().numpy()
+    kp, vp = _pages_bits(k, block), _pages_bits(v, block)
+    for suffix in (0, 5, 16):
+        for use_anchor in (False, True):
+            a = anchor if use_anchor else None
+            res = sparse_attention(inp["query"].to(DEV), summary,
+                                   inp["suffix_keys"][:, :suffix].to(DEV),
+                                   inp["suffix_values"][:, :suffix].to(DEV), cfg,
+                                   anchor_mask=a.to(DEV) if a is not None else None,
+                                   workspace=ws, return_selected=True)
+            torch.cuda.synchronize()
+            out, mask = oracle_lib.sparse_attention(
+                qn, summ, kp, vp, gc.bf16_bits(inp["suffix_keys"][:, :suffix]),
+                gc.bf16_bits(inp["suffix_values"][:, :suffix]), eps, reduction,
+                None if a is None else a.numpy())
+            assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask), \
+                f"mask suffix={suffix} anchor={use_anchor}"
+            got = res.output.float().cpu().numpy()[:, :, 0]
+            assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+
+
+def test_device_suffix_length_matches_slicing(hip):
+    """tests/test_attention.py:186-204 for the HIP backend: bit-equal outputs."""
+    q, keys, values = testing.small_inputs(length=71, dim=128)
+    cfg = RefineKVConfig(backend="hip", gqa_reduction="mean")
+    summary = build_summary(keys.to(DEV), values.to(DEV), cfg)
+    sk, sv = [t.to(DEV) for t in testing.small_inputs(length=16, dim=128, seed=5)[1:]]
+    visible = torch.zeros((), device=DEV, dtype=torch.int32)
+    for count in (0, 1, 5, 16):
+        visible.fill_(count)
+        actual = sparse_attention(q.to(DEV), summary, sk, sv, cfg, suffix_length=visible,
+                                  workspace={}).output.clone()
+        expected = sparse_attention(q.to(DEV), summary, sk[:, :count], sv[:, :count], cfg,
+                                    workspace={}).output.clone()
+        assert torch.equal(actual, expected), count
+
+
+def test_workspace_reuse_and_access_counter(hip, oracle_lib):
+    inp = _decode_case(4, 4, 128, 32, 5000, 0.05)
+    cfg = RefineKVConfig(backend="hip", eps=0.01)
+    summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
+    ws = {}
+    counter = torch.zeros(1, dtype=torch.int64, device=DEV)
+    outs = []
+    for _ in range(3):
+        out, mask = hip.decode(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                               inp["suffix_values"].to(DEV), cfg, None, ws, None, counter)
+        outs.append(out.clone())
+    torch.cuda.synchronize()
+    assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
+    want = oracle_lib.access_blocks(mask.cpu().numpy(), summary.counts.cpu().numpy())
+    assert int(counter.item()) == 3 * want
+
+
+@pytest.mark.parametrize("path", [p for p in gc.fixture_paths() if "f32" not in p],
+                         ids=lambda p: p.split("/")[-1][:-4])
+def test_reference_golden_end_to_end(hip, path):
+    """bf16 golden cases: HIP summary bit-exact to the reference, selection
+    (with anchors) equal, outputs within tolerance of the reference's."""
+    g, meta = gc.load(path)
+    inp = gc.regenerate(meta)
+    cfg = RefineKVConfig(backend="hip", **meta["config"])
+    summary = build_summary(inp["keys"].to(DEV), inp["values"].to(DEV), cfg)
+    ref = {k: g[k] for k in ("counts", "key_mean", "value_mean", "ellipsoid", "value_norm",
+                             "max_value_norm")}
+    torch.cuda.synchronize()
+    assert_summary_equal(summary, ref)
+    anchor = torch.from_numpy(g["anchor"]).bool().to(DEV) if "anchor" in g else None
+    mask = select_blocks(inp["query"].to(DEV), summary, cfg, workspace={})
+    assert np.array_equal(mask.cpu().numpy().astype(np.uint8), g["mask"])
+    res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                           inp["suffix_values"].to(DEV), cfg, anchor_mask=anchor, workspace={},
+                           return_selected=True)
+    assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), g["selected"])
+    assert_close_output(res.output.float().cpu().numpy(), g["output"])
+
+
+def test_headline_shape_128k(hip, oracle_lib):
+    """BASELINE config 3 shape (H_kv 8, G 4, d 128, 131072 prompt tokens, B 32):
+    masks equal the oracle's at full size, outputs within tolerance, and the
+    all-expanded step equals dense attention."""
+    inp = _decode_case(8, 4, 128, 32, 131072, 0.02, suffix=65, seed=1)
+    cfg = RefineKVConfig(backend="hip", eps=0.01)
+    k, v = inp["prompt_keys"], inp["prompt_values"]
+    kd, vd = k.to(DEV), v.to(DEV)
+    summary = build_summary(kd, vd, cfg)
+    summ = oracle_summary_of(summary)
+    ref = oracle_lib.summary(k.float().numpy(), v.float().numpy(), 32)
+    assert_summary_equal(summary, ref)
+    qn = inp["query"][:, :, 0].float().numpy()
+    res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                           inp["suffix_values"].to(DEV), cfg, workspace={}, return_selected=True)
+    torch.cuda.synchronize()
+    out, mask = oracle_lib.sparse_attention(qn, summ, _pages_bits(k, 32), _pages_bits(v, 32),
+                                            gc.bf16_bits(inp["suffix_keys"]),
+                                            gc.bf16_bits(inp["suffix_values"]), 0.01, "any")
+    assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask)
+    assert 0.005 < mask.mean() < 0.1
+    assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
+                        torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+    dense = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                             inp["suffix_values"].to(DEV), RefineKVConfig(backend="hip", eps=0),
+                             workspace={}, return_selected=True)
+    assert dense.selected.all()
+    kk = torch.cat([kd, inp["suffix_keys"].to(DEV)], 1).float().repeat_interleave(4, 0)
+    vv = torch.cat([vd, inp["suffix_values"].to(DEV)], 1).float().repeat_interleave(4, 0)
+    want = torch.nn.functional.scaled_dot_product_attention(
+        inp["query"].to(DEV).float().reshape(32, 1, 128), kk, vv)
+    assert_close_output(dense.output.float().reshape(32, 1, 128).cpu().numpy(), want.cpu().numpy())
