@@ -32,7 +32,7 @@ import torch  # noqa: E402
 
 METRIC = "decode attn µs/step/layer @128K ctx GQA32/8 d128; HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
-KERNELS = ("score", "decide", "attend", "merge")
+KERNELS = ("score", "decide", "pages", "merge")
 
 
 def log(msg):
@@ -115,21 +115,24 @@ def make_layer(gen, a, capacity, device):
 
 
 def algorithmic_bytes(a, masks, counts, suffix):
-    """Bytes each kernel must move per layer-step, in the reference's formats:
-    score reads k-means and ellipsoids; decide reads value norms and writes
-    the mask; attend reads the value means of unexpanded blocks, the K/V pages
-    of expanded blocks and the suffix; merge writes the output."""
+    """Bytes each kernel must move per layer-step, counted once in the
+    reference's storage formats (the per-step formula of the decode path):
+    score reads key means and ellipsoids of every block and the value means of
+    unexpanded blocks (its representative half); decide reads value norms and
+    writes the mask; pages read the K/V tokens of expanded blocks and the
+    suffix; merge writes the output.  Intermediates (z, delta, partials) are
+    not algorithmic bytes."""
     H, G, D = a.heads, a.group, a.dim
     n = counts.numel()
     sel = masks.float().mean(0)  # (H, N) fraction over layers
     expanded_tokens = (sel * counts.float()[None]).sum().item()
     unexpanded = ((1 - sel).sum()).item()
     q_bytes = H * G * D * 2
-    score = 2 * H * n * D * 2 + q_bytes
+    score = 2 * H * n * D * 2 + unexpanded * D * 2 + q_bytes
     decide = H * n * 4 + H * n
-    attend = unexpanded * D * 2 + expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
+    pages = expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
     merge = H * G * D * 2
-    return dict(score=score, decide=decide, attend=attend, merge=merge)
+    return dict(score=score, decide=decide, pages=pages, merge=merge)
 
 
 def main():

@@ -64,9 +64,10 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
 /* Byte offsets inside the workspace (for tests): z, delta, lse, tilebits,
- * attn_m, attn_l, attn_acc, total, n_tiles, workers -> out10[0..9]. */
+ * rep_l, rep_acc, page_m, page_l, page_acc, total, then n_tiles and the
+ * number of page workers -> out12[0..11]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out10);
+                         int64_t* out12);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton
@@ -119,7 +120,7 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
 /* Profiling hook with no reference counterpart: when `events` points to 5
  * hipEvent_t, later rkv_select / rkv_decode calls on this thread record
  * events[0] before the first kernel and events[1..4] after the score,
- * decide, attend and merge kernels.  NULL turns it off. */
+ * decide, pages and merge kernels.  NULL turns it off. */
 int rkv_set_profile_events(void* events);
 
 /* Test hook with no reference counterpart: applies the kernels' device

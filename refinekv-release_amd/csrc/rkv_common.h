@@ -56,6 +56,32 @@ __device__ __forceinline__ float wave_nanmin(float v) {
   return v;
 }
 
+// DPP row_shr:N -- lane i of each 16-lane row reads lane i-N of the same row
+// (lanes i < N read 0).  A register move fused into the consuming VALU op.
+template <int N>
+__device__ __forceinline__ float row_shr(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x110 + N, 0xF, 0xF, false));
+}
+
+// Sum of each 16-lane row in the xor-butterfly tree (distances 8, 4, 2, 1:
+// P[j] <- P[j] + P[j^o]).  Lane 15 of the row computes exactly the tree the
+// butterfly leaves in lane 0 (operands commuted, which fp32 add ignores);
+// other lanes hold partial sums.
+__device__ __forceinline__ float row16_sum_last(float v) {
+  v = v + row_shr<8>(v);
+  v = v + row_shr<4>(v);
+  v = v + row_shr<2>(v);
+  v = v + row_shr<1>(v);
+  return v;
+}
+
+// Broadcast lane 15 of each 16-lane row to the whole row.
+__device__ __forceinline__ float row_bcast_last(float v) {
+  const int lane = threadIdx.x % kWave;
+  return __shfl(v, (lane & ~15) | 15, kWave);
+}
+
 __device__ __forceinline__ float finite_or_zero(float m) { return is_finite(m) || is_nan(m) ? m : 0.0f; }
 
 // 16-byte aligned bf16 vector loads.

@@ -1,24 +1,35 @@
 // Decode-step selection and mixed attention (src/refinekv/reference.py:10-73,
 // the semantics the reference's Triton kernels in src/refinekv/kernels/ also
-// follow).  Four kernels per step, all on the caller's stream, no host sync,
-// no allocation (the caller passes a workspace):
+// follow).  Four kernels per step on the caller's stream; no host sync, no
+// allocation (the caller passes a workspace):
 //
-//   score   grid (tiles, H): per 64-block tile, s = q.k_mean and the ellipsoid
-//           projection for every query row; z = s + ln(count), delta, and the
-//           tile's log-sum-exp partials of z and z + log cosh(delta).
-//   decide  grid (tiles, H): merges the tile partials into log Z / log C,
-//           evaluates the risk, the GQA reduction, non-finite fail-safes and
-//           the anchor union; writes the mask, a 64-bit ballot per tile and
-//           the access counter.
-//   attend  grid (workers, H, row-blocks): split-K attention.  The head's work
-//           (representatives of unexpanded blocks, pages of expanded blocks,
-//           suffix tokens) is laid out as one list ordered by cost and cut
-//           into equal-cost ranges, so clustered expansions do not serialize
-//           on one workgroup.  Online-softmax state per 16-lane group.
-//   merge   grid (rows): combines the workers' (m, l, acc) partials.
+//   score   grid (tiles, H), one 64-block tile per workgroup.  Streams the
+//           tile's key means, ellipsoids and value means once: s = q.k_mean
+//           and the ellipsoid projection for every query row, z = s + ln n,
+//           delta, the tile's log-sum-exp partials of z and z + log cosh delta,
+//           and the tile's representative-attention accumulator
+//           sum_b exp(z_b - m_tile) v_mean_b over all its blocks (the z
+//           log-sum-exp partial is that attention's (m, l)).
+//   decide  grid (tiles, H).  Merges the tile partials into log Z / log C,
+//           evaluates the risk, the GQA reduction, the non-finite fail-safes
+//           and the anchor union; writes the mask, a 64-bit ballot per tile
+//           and the access counter.  Then removes the expanded blocks from the
+//           tile's representative partial: l is recomputed over the
+//           unexpanded blocks, acc has the expanded blocks' terms subtracted
+//           (its rounding error stays below fp32 eps times the tile's
+//           representative mass, itself at most the exact mass of the step).
+//   pages   grid (workers, row blocks).  Every head's expanded pages and
+//           suffix tokens form one list ordered by head; each worker takes an
+//           equal-cost range of it (a page costs 2*block_size rows, a suffix
+//           token 2), so expansion clustered in a few heads or blocks is
+//           still spread over the whole GPU.  Online softmax per 16-lane group.
+//   merge   grid (rows, head_dim/32).  Combines the live representative and
+//           page partials of each query row in a fixed order.
 //
-// Scores, radii and log-sum-exp follow the fixed fp32 orders documented in
-// rkv_math.h / the oracle header, so masks are reproducible bit for bit.
+// Scores, radii and log-sum-exp follow fixed fp32 orders shared with the CPU
+// oracle (oracle/rkv_oracle.c), so masks and selection statistics are
+// reproducible bit for bit; every summation order is fixed, so outputs are
+// deterministic run to run.
 #include "rkv_common.h"
 #include "rkv_internal.h"
 
@@ -27,61 +38,70 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+constexpr float kLog2e = 1.44269504088896341f;
+constexpr int kMaxHeadTiles = 8192;  // page-kernel LDS prefix capacity (heads * tiles)
 
 // Optional profiling events (rkv_set_profile_events): recorded on the launch
-// stream before score and after score, decide, attend and merge.
+// stream before score and after score, decide, pages and merge.
 thread_local hipEvent_t* g_events = nullptr;
 
 inline void mark(int i, hipStream_t stream) {
   if (g_events) (void)hipEventRecord(g_events[i], stream);
 }
-constexpr float kLog2e = 1.44269504088896341f;
 
 // ---------------------------------------------------------------------------
 // Workspace layout
 // ---------------------------------------------------------------------------
 struct Layout {
-  int64_t n_tiles, workers, row_blocks, rows_per_block;
-  int64_t z, delta, lse, tilebits, attn_m, attn_l, attn_acc, total;
+  int64_t n_tiles, workers, rows_per_block, row_blocks;
+  int64_t z, delta, lse, tilebits, rep_l, rep_acc, page_m, page_l, page_acc, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-inline int64_t rows_per_block(int64_t dim) {
-  int64_t ch = dim / 16;
-  int64_t r = 64 / ch;
-  return r > kMaxGroup ? kMaxGroup : r;
+// Rows of the GQA group one page workgroup carries in registers: the next
+// power of two >= group (at least 4), capped so that rows * head_dim / 16
+// (per-lane accumulators) stays <= 64.
+inline int64_t rows_per_block(int64_t group, int64_t dim) {
+  const int64_t ch = dim / 16;
+  const int64_t cap = 64 / ch;
+  int64_t p = 16;
+  while (p > cap) p >>= 1;
+  int64_t want = 4;
+  while (want < group && want < 16) want <<= 1;
+  return want < p ? want : p;
 }
 
-inline int64_t workers_for(int64_t n_blocks) {
-  int64_t w = (n_blocks + 63) / 64;
+// One page worker per 64 (head, block) pairs, 1..512.
+inline int64_t workers_for(int64_t heads, int64_t n_blocks) {
+  int64_t w = (heads * n_blocks + 63) / 64;
   if (w < 1) w = 1;
-  if (w > 64) w = 64;
+  if (w > 512) w = 512;
   return w;
 }
 
 Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) {
   Layout L{};
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
-  L.workers = workers_for(n_blocks);
-  L.rows_per_block = rows_per_block(dim);
+  L.workers = workers_for(heads, n_blocks);
+  L.rows_per_block = rows_per_block(group, dim);
   L.row_blocks = (group + L.rows_per_block - 1) / L.rows_per_block;
   const int64_t rows = heads * group;
   int64_t off = 0;
-  L.z = off;
-  off = align256(off + rows * n_blocks * 4);
-  L.delta = off;
-  off = align256(off + rows * n_blocks * 4);
-  L.lse = off;
-  off = align256(off + rows * L.n_tiles * 4 * 4);
-  L.tilebits = off;
-  off = align256(off + heads * L.n_tiles * 8);
-  L.attn_m = off;
-  off = align256(off + rows * L.workers * 4);
-  L.attn_l = off;
-  off = align256(off + rows * L.workers * 4);
-  L.attn_acc = off;
-  off = align256(off + rows * L.workers * dim * 4);
+  auto take = [&](int64_t bytes) {
+    const int64_t at = off;
+    off = align256(off + bytes);
+    return at;
+  };
+  L.z = take(rows * n_blocks * 4);
+  L.delta = take(rows * n_blocks * 4);
+  L.lse = take(rows * L.n_tiles * 4 * 4);
+  L.tilebits = take(heads * L.n_tiles * 8);
+  L.rep_l = take(rows * L.n_tiles * 4);
+  L.rep_acc = take(rows * L.n_tiles * dim * 4);
+  L.page_m = take(rows * L.workers * 4);
+  L.page_l = take(rows * L.workers * 4);
+  L.page_acc = take(rows * L.workers * dim * 4);
   L.total = off;
   return L;
 }
@@ -119,33 +139,59 @@ __device__ __forceinline__ float risk_of(float z, float delta, float log_z, floa
   return mass + value;
 }
 
-__device__ __forceinline__ float inf_to_zero(float m) {
+__host__ __device__ __forceinline__ float inf_to_zero(float m) {
   return (m == kPosInf || m == kNegInf) ? 0.0f : m;
 }
 
-// Log-sum-exp partial of one 64-block tile; x is lane j's value (-inf pads).
-__device__ __forceinline__ void tile_lse(float x, float& m, float& l) {
-  m = wave_nanmax(x);
-  const float ms = inf_to_zero(m);
-  l = wave_sum(expf_(x - ms));
+__device__ __forceinline__ int64_t block_count(int64_t b, int64_t n, int64_t block,
+                                               int64_t length) {
+  return b == n - 1 ? length - (n - 1) * block : block;
+}
+
+// Block-wide exclusive scan of one value per thread (integers: exact).
+__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tot,
+                                                         uint32_t& total) {
+  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
+  uint32_t inc = v;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t n = __shfl_up(inc, o, kWave);
+    if (lane >= o) inc += n;
+  }
+  if (lane == kWave - 1) wave_tot[wave] = inc;
+  __syncthreads();
+  uint32_t before = 0;
+  total = 0;
+  for (int w = 0; w < kWaves; ++w) {
+    if (w < wave) before += wave_tot[w];
+    total += wave_tot[w];
+  }
+  __syncthreads();
+  return before + inc - v;
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 1: scores
+// Kernel 1: scores (+ representative accumulators)
 // ---------------------------------------------------------------------------
 struct ScoreArgs {
-  const uint16_t* query;      // (H, G, D) bf16
-  const uint16_t* key_mean;   // (H, N, D) bf16
-  const uint16_t* ellipsoid;  // (H, N, D) bf16
-  float* z;                   // (H, G, N)
-  float* delta;               // (H, G, N)
-  float* lse;                 // (H, G, tiles, 4): zm, zl, cm, cl
+  const uint16_t* query;       // (H, G, D) bf16
+  const uint16_t* key_mean;    // (H, N, D) bf16
+  const uint16_t* ellipsoid;   // (H, N, D) bf16
+  const uint16_t* value_mean;  // (H, N, D) bf16 (representatives only)
+  float* z;                    // (H, G, N)
+  float* delta;                // (H, G, N)
+  float* lse;                  // (H, G, tiles, 4): zm, zl, cm, cl
+  float* rep_acc;              // (H, G, tiles, D)
   int64_t n_blocks, n_tiles, block, length;
   int group;
   float scale;
 };
 
-template <int D>
+inline size_t score_smem(int64_t group, int64_t dim) {
+  return sizeof(float) * (2 * group * dim + 5 * group * kTile + kWaves * dim);
+}
+
+template <int D, bool REPS>
 __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   constexpr int CH = D / 16;
   extern __shared__ float smem[];
@@ -156,6 +202,8 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   float* pdot = sdot + G * kTile;   // [G][64]
   float* zbuf = pdot + G * kTile;   // [G][64]
   float* zcbuf = zbuf + G * kTile;  // [G][64]
+  float* pbuf = zcbuf + G * kTile;  // [G][64] exp(z - m_tile)
+  float* racc = pbuf + G * kTile;   // [waves][D]
 
   const int64_t h = blockIdx.y;
   const int64_t tile = blockIdx.x;
@@ -163,23 +211,27 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   const int grp = lane / 16, c = lane % 16;
   const int64_t N = a.n_blocks;
 
-  for (int i = tid; i < G * D; i += kThreads) {
-    const float q = bf16_to_f32(a.query[h * G * D + i]);
-    qs[i] = q;
-    q2s[i] = round_bf16(q * q);
-  }
-
-  float km[4][CH], el[4][CH];
+  float km[4][CH], el[4][CH], vm[REPS ? 4 : 1][REPS ? CH : 1];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int64_t b = tile * kTile + wave * 16 + it * 4 + grp;
     if (b < N) {
-      load_bf16<CH>(a.key_mean + (h * N + b) * D + c * CH, km[it]);
-      load_bf16<CH>(a.ellipsoid + (h * N + b) * D + c * CH, el[it]);
+      const int64_t o = (h * N + b) * D + c * CH;
+      load_bf16<CH>(a.key_mean + o, km[it]);
+      load_bf16<CH>(a.ellipsoid + o, el[it]);
+      if constexpr (REPS) load_bf16<CH>(a.value_mean + o, vm[it]);
     } else {
 #pragma unroll
-      for (int i = 0; i < CH; ++i) km[it][i] = el[it][i] = 0.0f;
+      for (int i = 0; i < CH; ++i) {
+        km[it][i] = el[it][i] = 0.0f;
+        if constexpr (REPS) vm[it][i] = 0.0f;
+      }
     }
+  }
+  for (int i = tid; i < G * D; i += kThreads) {
+    const float q = bf16_to_f32(a.query[h * G * D + i]);
+    qs[i] = q;
+    q2s[i] = round_bf16(q * q);
   }
   __syncthreads();
 
@@ -192,7 +244,8 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     }
 #pragma unroll
     for (int it = 0; it < 4; ++it) {
-      // DSUM: chunk of CH consecutive elements left to right, then butterfly.
+      // DSUM: this lane's CH consecutive elements left to right, then the
+      // 16-lane butterfly (complete in lane 15 of the row).
       float s = qv[0] * km[it][0];
       float p = q2v[0] * el[it][0];
 #pragma unroll
@@ -200,9 +253,9 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
         s = s + qv[i] * km[it][i];
         p = p + q2v[i] * el[it][i];
       }
-      s = group16_sum(s);
-      p = group16_sum(p);
-      if (c == 0) {
+      s = row16_sum_last(s);
+      p = row16_sum_last(p);
+      if (c == 15) {
         const int bl = wave * 16 + it * 4 + grp;
         sdot[g * kTile + bl] = s;
         pdot[g * kTile + bl] = p;
@@ -218,8 +271,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     if (b < N) {
       const float s = sdot[idx] * a.scale;
       const float dl = (sqrtf(clamp_min(pdot[idx], 0.0f)) * a.scale) * kInflate;
-      const float cnt = (float)(b == N - 1 ? a.length - (N - 1) * a.block : a.block);
-      z = s + logf_(cnt);
+      z = s + logf_((float)block_count(b, N, a.block, a.length));
       zc = z + log_cosh(dl);
       const int64_t o = (h * G + g) * N + b;
       a.z[o] = z;
@@ -231,9 +283,14 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   __syncthreads();
 
   for (int g = wave; g < G; g += kWaves) {
-    float zm, zl, cm, cl;
-    tile_lse(zbuf[g * kTile + lane], zm, zl);
-    tile_lse(zcbuf[g * kTile + lane], cm, cl);
+    const float x = zbuf[g * kTile + lane];
+    const float zm = wave_nanmax(x);
+    const float e = expf_(x - inf_to_zero(zm));
+    const float zl = wave_sum(e);
+    pbuf[g * kTile + lane] = e;
+    const float xc = zcbuf[g * kTile + lane];
+    const float cm = wave_nanmax(xc);
+    const float cl = wave_sum(expf_(xc - inf_to_zero(cm)));
     if (lane == 0) {
       float* o = a.lse + ((h * G + g) * a.n_tiles + tile) * 4;
       o[0] = zm;
@@ -242,10 +299,38 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
       o[3] = cl;
     }
   }
+
+  if constexpr (REPS) {
+    __syncthreads();
+    for (int g = 0; g < G; ++g) {
+      float acc[CH];
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const float p = pbuf[g * kTile + wave * 16 + it * 4 + grp];
+#pragma unroll
+        for (int i = 0; i < CH; ++i) acc[i] = it == 0 ? p * vm[0][i] : acc[i] + p * vm[it][i];
+      }
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        acc[i] = acc[i] + shfl_xor(acc[i], 16);
+        acc[i] = acc[i] + shfl_xor(acc[i], 32);
+      }
+      if (grp == 0) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) racc[wave * D + c * CH + i] = acc[i];
+      }
+      __syncthreads();
+      for (int d = tid; d < D; d += kThreads) {
+        const float sum = ((racc[d] + racc[D + d]) + racc[2 * D + d]) + racc[3 * D + d];
+        a.rep_acc[((h * G + g) * a.n_tiles + tile) * D + d] = sum;
+      }
+      __syncthreads();
+    }
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: decisions
+// Kernel 2: decisions (+ representative corrections)
 // ---------------------------------------------------------------------------
 struct DecideArgs {
   const float* z;
@@ -253,14 +338,17 @@ struct DecideArgs {
   const float* lse;
   const float* value_norm;      // (H, N)
   const float* max_value_norm;  // (H)
+  const uint16_t* value_mean;   // (H, N, D) (representatives only)
   const uint8_t* anchor;        // (H, N) or null
   uint8_t* mask;                // (H, N)
   uint64_t* tilebits;           // (H, tiles)
   float* risk_out;              // (H, G, N) or null
   float* stats_out;             // (H, G, 2) or null: log Z, log C
   unsigned long long* accessed; // or null
+  float* rep_l;                 // (H, G, tiles) or null (select only)
+  float* rep_acc;               // (H, G, tiles, D)
   int64_t n_blocks, n_tiles, block, length;
-  int group, reduction;
+  int group, reduction, dim;
   float eps;
 };
 
@@ -286,6 +374,8 @@ __device__ __forceinline__ float merge_lse(const float* part, int64_t n_tiles, i
 __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   __shared__ float gstat[kMaxGroup][2];
   __shared__ float risk_s[kMaxGroup][kTile];
+  __shared__ float psel[kMaxGroup][kTile];
+  __shared__ uint64_t sel_bits;
   const int64_t h = blockIdx.y;
   const int64_t tile = blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -321,9 +411,10 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   }
   __syncthreads();
 
+  const int64_t nvalid = N - tile * kTile >= kTile ? kTile : N - tile * kTile;
   if (wave == 0) {
     const int64_t b = tile * kTile + lane;
-    const bool valid = b < N;
+    const bool valid = lane < nvalid;
     bool bad_global = false;
     for (int g = 0; g < G; ++g) bad_global |= !is_finite(gstat[g][0]) || !is_finite(gstat[g][1]);
     bool sel = false, bad_local = false;
@@ -347,91 +438,73 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
     sel = sel && valid;
     if (valid) a.mask[h * N + b] = sel ? 1 : 0;
     const uint64_t bits = __ballot(sel);
-    if (lane == 0) a.tilebits[h * a.n_tiles + tile] = bits;
+    if (lane == 0) {
+      a.tilebits[h * a.n_tiles + tile] = bits;
+      sel_bits = bits;
+    }
     if (a.accessed) {
-      const int64_t cnt = b == N - 1 ? a.length - (N - 1) * a.block : a.block;
-      unsigned long long term = valid ? (sel ? (unsigned long long)cnt : 1ull) : 0ull;
+      unsigned long long term =
+          valid ? (sel ? (unsigned long long)block_count(b, N, a.block, a.length) : 1ull) : 0ull;
 #pragma unroll
       for (int o = 32; o >= 1; o >>= 1) term += __shfl_xor(term, o, kWave);
       if (lane == 0) atomicAdd(a.accessed, term);
     }
   }
+  if (!a.rep_l) return;
+  __syncthreads();
+
+  // Representatives of this tile: drop the expanded blocks.
+  const uint64_t bits = sel_bits;
+  const int nsel = __popcll(bits);
+  for (int g = wave; g < G; g += kWaves) {
+    const int64_t row = h * G + g;
+    const float ms = inf_to_zero(a.lse[(row * a.n_tiles + tile) * 4]);
+    const bool valid = lane < nvalid;
+    const bool expanded = (bits >> lane) & 1ull;
+    const float e = valid ? expf_(a.z[row * N + tile * kTile + lane] - ms) : 0.0f;
+    const float l = wave_sum(expanded ? 0.0f : e);
+    psel[g][lane] = expanded ? e : 0.0f;
+    if (lane == 0) a.rep_l[row * a.n_tiles + tile] = nsel == nvalid ? 0.0f : l;
+  }
+  if (nsel == 0 || nsel == nvalid) return;
+  __syncthreads();
+  const int D = a.dim;
+  for (int idx = tid; idx < G * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    float* acc_p = a.rep_acc + ((h * G + g) * a.n_tiles + tile) * D + d;
+    float acc = *acc_p;
+    uint64_t m = bits;
+    while (m) {
+      const int j = __builtin_ctzll(m);
+      m &= m - 1;
+      const float v = bf16_to_f32(a.value_mean[(h * N + tile * kTile + j) * D + d]);
+      acc = acc - psel[g][j] * v;
+    }
+    *acc_p = acc;
+  }
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 3: split-K mixed attention
+// Kernel 3: expanded pages and suffix tokens
 // ---------------------------------------------------------------------------
-struct AttendArgs {
+struct PageArgs {
   const uint16_t* query;       // (H, G, D) bf16
-  const float* z;              // (H, G, N)
-  const uint16_t* value_mean;  // (H, N, D)
-  const uint16_t* key_pages;   // page h at key_pages + h * kp_hs; (N, B, D) rows
+  const uint16_t* key_pages;   // head h at key_pages + h * kp_hs; rows (N*B, D)
   const uint16_t* value_pages;
   const uint16_t* key_suffix;  // token t of head h at h * ks_hs + t * ks_ts
   const uint16_t* value_suffix;
   const uint64_t* tilebits;    // (H, tiles)
   const int32_t* suffix_len_dev;  // or null
-  float* part_m;               // (H*G, W)
-  float* part_l;
-  float* part_acc;             // (H*G, W, D)
+  float* page_m;               // (H*G, W)
+  float* page_l;
+  float* page_acc;             // (H*G, W, D)
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
   int64_t suffix_cap, n_blocks, n_tiles, block, length;
-  int group, workers, rows_per_block;
+  int heads, group, workers, rows_per_block;
   float scale;
 };
 
 constexpr int kListCap = kThreads;  // block indices resolved per chunk
-
-// Index -> block lookups over the per-tile ballots (prefix sums in LDS).
-struct TileIndex {
-  const uint32_t* selpre;    // [tiles + 1] exclusive prefix of expanded blocks
-  const uint32_t* unselpre;  // [tiles + 1] exclusive prefix of unexpanded blocks
-  const uint64_t* bits;      // [tiles]
-  int64_t n_tiles, n_blocks;
-
-  __device__ __forceinline__ int64_t find(const uint32_t* pre, int64_t i) const {
-    int64_t lo = 0, hi = n_tiles - 1;
-    while (lo < hi) {
-      const int64_t mid = (lo + hi + 1) >> 1;
-      if ((int64_t)pre[mid] <= i) lo = mid; else hi = mid - 1;
-    }
-    return lo;
-  }
-  __device__ __forceinline__ uint64_t valid_bits(int64_t t) const {
-    const int64_t n = n_blocks - t * kTile;
-    return n >= 64 ? ~0ull : ((1ull << n) - 1ull);
-  }
-  __device__ __forceinline__ int64_t selected(int64_t j) const {
-    const int64_t t = find(selpre, j);
-    return t * kTile + nth_set_bit(bits[t], (int)(j - selpre[t]));
-  }
-  __device__ __forceinline__ int64_t unselected(int64_t i) const {
-    const int64_t t = find(unselpre, i);
-    return t * kTile + nth_set_bit(~bits[t] & valid_bits(t), (int)(i - unselpre[t]));
-  }
-};
-
-// Block-wide exclusive scan of one value per thread (integers: exact).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tot,
-                                                         uint32_t& total) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t n = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += n;
-  }
-  if (lane == kWave - 1) wave_tot[wave] = inc;
-  __syncthreads();
-  uint32_t before = 0;
-  total = 0;
-  for (int w = 0; w < kWaves; ++w) {
-    if (w < wave) before += wave_tot[w];
-    total += wave_tot[w];
-  }
-  __syncthreads();
-  return before + inc - v;
-}
 
 template <int D, int GBM>
 struct SoftmaxState {
@@ -447,22 +520,21 @@ struct SoftmaxState {
       for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
     }
   }
-  // x: logits in log2 units (one per row); v: this lane's slice of the value row.
+  // x: natural-log logits (one per row); v: this lane's slice of the value row.
   __device__ __forceinline__ void update(const float (&x)[GBM], const float (&v)[CH], int gn) {
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       if (g >= gn) break;
       const float mn = fmaxf(m[g], x[g]);
       if (mn == kNegInf) continue;
-      const float alpha = __builtin_amdgcn_exp2f(m[g] - mn);
-      const float p = __builtin_amdgcn_exp2f(x[g] - mn);
+      const float alpha = __builtin_amdgcn_exp2f((m[g] - mn) * kLog2e);
+      const float p = __builtin_amdgcn_exp2f((x[g] - mn) * kLog2e);
       l[g] = l[g] * alpha + p;
 #pragma unroll
       for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * alpha + p * v[i];
       m[g] = mn;
     }
   }
-  // Merge another state (same lane slice) into this one.
   __device__ __forceinline__ void merge(const float* om, const float* ol, const float (*oacc)[CH],
                                         int gn) {
 #pragma unroll
@@ -470,8 +542,8 @@ struct SoftmaxState {
       if (g >= gn) break;
       const float mn = fmaxf(m[g], om[g]);
       if (mn == kNegInf) continue;
-      const float a = __builtin_amdgcn_exp2f(m[g] - mn);
-      const float b = __builtin_amdgcn_exp2f(om[g] - mn);
+      const float a = __builtin_amdgcn_exp2f((m[g] - mn) * kLog2e);
+      const float b = __builtin_amdgcn_exp2f((om[g] - mn) * kLog2e);
       l[g] = l[g] * a + ol[g] * b;
 #pragma unroll
       for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * a + oacc[g][i] * b;
@@ -480,233 +552,287 @@ struct SoftmaxState {
   }
 };
 
+// Exact logits of one K row for this lane's query slice (DSUM order), natural
+// units, broadcast to the 16-lane group.
 template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) void attend_kernel(AttendArgs a) {
+__device__ __forceinline__ void row_logits(const float (&q)[GBM][D / 16], const float (&k)[D / 16],
+                                           int gn, float scale, float (&x)[GBM]) {
+  constexpr int CH = D / 16;
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+    float s = q[g][0] * k[0];
+#pragma unroll
+    for (int i = 1; i < CH; ++i) s = s + q[g][i] * k[i];
+    s = row_bcast_last(row16_sum_last(s));
+    x[g] = g < gn ? s * scale : kNegInf;
+  }
+}
+
+inline size_t page_smem(int64_t heads, int64_t n_tiles) {
+  return (size_t)align256((heads * n_tiles + 1) * 4) + sizeof(int64_t) * kListCap;
+}
+
+template <int D, int GBM>
+__global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
   constexpr int CH = D / 16;
   extern __shared__ unsigned char smem_raw[];
-  const int64_t T = a.n_tiles;
-  uint32_t* selpre = reinterpret_cast<uint32_t*>(smem_raw);
-  uint32_t* unselpre = selpre + (T + 1);
-  uint64_t* bits = reinterpret_cast<uint64_t*>(smem_raw + align256((T + 1) * 8));
-  int64_t* list = reinterpret_cast<int64_t*>(reinterpret_cast<unsigned char*>(bits) +
-                                             align256(T * 8));
+  const int64_t T = a.n_tiles, H = a.heads, HT = H * T;
+  uint32_t* pre = reinterpret_cast<uint32_t*>(smem_raw);  // [HT + 1] page prefix, head-major
+  int64_t* list = reinterpret_cast<int64_t*>(smem_raw + align256((HT + 1) * 4));
   __shared__ uint32_t wave_tot[kWaves];
   __shared__ float xm[kWaves][GBM], xl[kWaves][GBM];
   __shared__ float xacc[kWaves][GBM][D];
 
-  const int64_t h = blockIdx.y;
   const int w = blockIdx.x;
-  const int g0 = blockIdx.z * a.rows_per_block;
+  const int g0 = blockIdx.y * a.rows_per_block;
   const int gn = min(a.rows_per_block, a.group - g0);
   const int G = a.group;
   const int tid = threadIdx.x, lg = tid >> 4, c = tid & 15, wave = tid / kWave;
-  const int64_t N = a.n_blocks;
+  const int64_t N = a.n_blocks, B = a.block;
 
-  // ---- per-tile prefix sums of expanded / unexpanded blocks -------------
-  const int64_t per = (T + kThreads - 1) / kThreads;
-  const int64_t t_begin = min((int64_t)tid * per, T), t_end = min(t_begin + per, T);
-  uint32_t my_sel = 0, my_valid = 0;
+  // ---- expanded-page prefix over every (head, tile) ----------------------
+  const int64_t per = (HT + kThreads - 1) / kThreads;
+  const int64_t t_begin = min((int64_t)tid * per, HT), t_end = min(t_begin + per, HT);
+  uint32_t mine = 0;
+  for (int64_t t = t_begin; t < t_end; ++t) mine += (uint32_t)__popcll(a.tilebits[t]);
+  uint32_t total;
+  uint32_t run = block_exclusive_scan(mine, wave_tot, total);
   for (int64_t t = t_begin; t < t_end; ++t) {
-    const uint64_t b = a.tilebits[h * T + t];
-    bits[t] = b;
-    my_sel += (uint32_t)__popcll(b);
-    const int64_t nv = N - t * kTile;
-    my_valid += (uint32_t)(nv >= 64 ? 64 : nv);
+    pre[t] = run;
+    run += (uint32_t)__popcll(a.tilebits[t]);
   }
-  uint32_t tot_sel, tot_valid;
-  const uint32_t ex_sel = block_exclusive_scan(my_sel, wave_tot, tot_sel);
-  const uint32_t ex_valid = block_exclusive_scan(my_valid, wave_tot, tot_valid);
-  {
-    uint32_t s = ex_sel, u = ex_valid - ex_sel;
-    for (int64_t t = t_begin; t < t_end; ++t) {
-      selpre[t] = s;
-      unselpre[t] = u;
-      const uint32_t ns = (uint32_t)__popcll(bits[t]);
-      const int64_t nv = N - t * kTile;
-      s += ns;
-      u += (uint32_t)(nv >= 64 ? 64 : nv) - ns;
-    }
-    if (tid == 0) {
-      selpre[T] = tot_sel;
-      unselpre[T] = tot_valid - tot_sel;
-    }
-  }
+  if (tid == 0) pre[HT] = total;
   __syncthreads();
-  const TileIndex index{selpre, unselpre, bits, T, N};
 
-  // ---- this worker's equal-cost share of the head's work ---------------
-  const int64_t n_sel = tot_sel, n_unsel = (int64_t)tot_valid - tot_sel;
   int64_t S = a.suffix_cap;
   if (a.suffix_len_dev) {
     const int64_t s = *a.suffix_len_dev;
     S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
   }
-  const int64_t page_cost = 2 * a.block;
-  const int64_t C = n_unsel + page_cost * n_sel + 2 * S;
+  const int64_t pc = 2 * B;  // cost of one page
+  const int64_t C = pc * (int64_t)total + 2 * S * H;
   const int64_t lo = C * w / a.workers, hi = C * (w + 1) / a.workers;
-  auto clampi = [](int64_t x, int64_t lo_, int64_t hi_) { return x < lo_ ? lo_ : (x > hi_ ? hi_ : x); };
+  auto clampi = [](int64_t x, int64_t l, int64_t h) { return x < l ? l : (x > h ? h : x); };
   auto ceil_div = [](int64_t x, int64_t d) { return x <= 0 ? 0 : (x + d - 1) / d; };
-  const int64_t r0 = clampi(lo, 0, n_unsel), r1 = clampi(hi, 0, n_unsel);
-  const int64_t p0 = clampi(ceil_div(lo - n_unsel, page_cost), 0, n_sel);
-  const int64_t p1 = clampi(ceil_div(hi - n_unsel, page_cost), 0, n_sel);
-  const int64_t sbase = n_unsel + page_cost * n_sel;
-  const int64_t s0 = clampi(ceil_div(lo - sbase, 2), 0, S);
-  const int64_t s1 = clampi(ceil_div(hi - sbase, 2), 0, S);
 
-  // ---- query slice for this lane ---------------------------------------
-  float q[GBM][CH];
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-    if (g < gn) {
-      load_bf16<CH>(a.query + ((h * G + g0 + g) * D + c * CH), q[g]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) q[g][i] = 0.0f;
-    }
-  }
-  const float qscale = a.scale * kLog2e;
-
-  SoftmaxState<D, GBM> st;
-  st.init();
-
-  // ---- representatives: logit z, value k-mean row ----------------------
-  for (int64_t base = r0; base < r1; base += kListCap) {
-    const int64_t n = min((int64_t)kListCap, r1 - base);
-    __syncthreads();
-    if (tid < n) list[tid] = index.unselected(base + tid);
-    __syncthreads();
-    for (int64_t i = lg; i < n; i += 16) {
-      const int64_t b = list[i];
-      float x[GBM], v[CH];
-#pragma unroll
-      for (int g = 0; g < GBM; ++g)
-        x[g] = g < gn ? a.z[(h * G + g0 + g) * N + b] * kLog2e : kNegInf;
-      load_bf16<CH>(a.value_mean + (h * N + b) * D + c * CH, v);
-      st.update(x, v, gn);
-    }
-  }
-
-  // ---- expanded pages: exact tokens ------------------------------------
-  for (int64_t base = p0; base < p1; base += kListCap) {
-    const int64_t n = min((int64_t)kListCap, p1 - base);
-    __syncthreads();
-    if (tid < n) list[tid] = index.selected(base + tid);
-    __syncthreads();
-    const int64_t rows = n * a.block;
-    for (int64_t r = lg; r < rows; r += 16) {
-      const int64_t j = r / a.block, t = r - j * a.block;
-      const int64_t b = list[j];
-      const int64_t cnt = b == N - 1 ? a.length - (N - 1) * a.block : a.block;
-      if (t >= cnt) continue;
-      const int64_t row = b * a.block + t;
-      float kv[CH], v[CH], x[GBM];
-      load_bf16<CH>(a.key_pages + h * a.kp_hs + row * D + c * CH, kv);
-      load_bf16<CH>(a.value_pages + h * a.vp_hs + row * D + c * CH, v);
-#pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        float s = q[g][0] * kv[0];
-#pragma unroll
-        for (int i = 1; i < CH; ++i) s = s + q[g][i] * kv[i];
-        s = group16_sum(s);
-        x[g] = g < gn ? s * qscale : kNegInf;
+  for (int64_t h = 0; h < H; ++h) {
+    const int64_t first = pre[h * T];
+    const int64_t n_h = (int64_t)pre[(h + 1) * T] - first;
+    const int64_t hs = pc * first + 2 * S * h;
+    const int64_t he = hs + pc * n_h + 2 * S;
+    const int64_t slot0 = (h * G + g0) * a.workers + w;
+    if (!(lo < he && hi > hs)) {
+      if (tid < gn) {
+        a.page_m[slot0 + (int64_t)tid * a.workers] = kNegInf;
+        a.page_l[slot0 + (int64_t)tid * a.workers] = 0.0f;
       }
-      st.update(x, v, gn);
+      continue;
     }
-  }
+    const int64_t lo_h = lo - hs, hi_h = hi - hs;
+    const int64_t p0 = clampi(ceil_div(lo_h, pc), 0, n_h), p1 = clampi(ceil_div(hi_h, pc), 0, n_h);
+    const int64_t s0 = clampi(ceil_div(lo_h - pc * n_h, 2), 0, S);
+    const int64_t s1 = clampi(ceil_div(hi_h - pc * n_h, 2), 0, S);
 
-  // ---- generated suffix tokens -----------------------------------------
-  for (int64_t k = s0 + lg; k < s1; k += 16) {
-    float kv[CH], v[CH], x[GBM];
-    load_bf16<CH>(a.key_suffix + h * a.ks_hs + k * a.ks_ts + c * CH, kv);
-    load_bf16<CH>(a.value_suffix + h * a.vs_hs + k * a.vs_ts + c * CH, v);
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      float s = q[g][0] * kv[0];
-#pragma unroll
-      for (int i = 1; i < CH; ++i) s = s + q[g][i] * kv[i];
-      s = group16_sum(s);
-      x[g] = g < gn ? s * qscale : kNegInf;
-    }
-    st.update(x, v, gn);
-  }
-
-  // ---- merge the 16 lane groups ----------------------------------------
-#pragma unroll
-  for (int o = 16; o <= 32; o <<= 1) {
-    float om[GBM], ol[GBM], oacc[GBM][CH];
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      om[g] = shfl_xor(st.m[g], o);
-      ol[g] = shfl_xor(st.l[g], o);
-#pragma unroll
-      for (int i = 0; i < CH; ++i) oacc[g][i] = shfl_xor(st.acc[g][i], o);
-    }
-    st.merge(om, ol, oacc, gn);
-  }
-  if ((tid & 63) < 16) {
+    float q[GBM][CH];
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       if (g < gn) {
-        if (c == 0) {
-          xm[wave][g] = st.m[g];
-          xl[wave][g] = st.l[g];
-        }
+        load_bf16<CH>(a.query + ((h * G + g0 + g) * D + c * CH), q[g]);
+      } else {
 #pragma unroll
-        for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = st.acc[g][i];
+        for (int i = 0; i < CH; ++i) q[g][i] = 0.0f;
       }
     }
-  }
-  __syncthreads();
-  if (tid < 16) {
-    for (int ow = 1; ow < kWaves; ++ow) {
+    SoftmaxState<D, GBM> st;
+    st.init();
+
+    for (int64_t base = p0; base < p1; base += kListCap) {
+      const int64_t n = min((int64_t)kListCap, p1 - base);
+      __syncthreads();
+      if (tid < n) {
+        // page index -> (tile, bit) by binary search over head h's tiles
+        const int64_t j = first + base + tid;
+        int64_t lo_t = h * T, hi_t = h * T + T - 1;
+        while (lo_t < hi_t) {
+          const int64_t mid = (lo_t + hi_t + 1) >> 1;
+          if ((int64_t)pre[mid] <= j) lo_t = mid; else hi_t = mid - 1;
+        }
+        const int64_t t = lo_t - h * T;
+        list[tid] = t * kTile + nth_set_bit(a.tilebits[lo_t], (int)(j - pre[lo_t]));
+      }
+      __syncthreads();
+      const int64_t rows = n * B;
+      for (int64_t r = lg; r < rows; r += 16) {
+        const int64_t jj = r / B, t = r - jj * B;
+        const int64_t b = list[jj];
+        if (t >= block_count(b, N, B, a.length)) continue;
+        const int64_t row = b * B + t;
+        float kv[CH], v[CH], x[GBM];
+        load_bf16<CH>(a.key_pages + h * a.kp_hs + row * D + c * CH, kv);
+        load_bf16<CH>(a.value_pages + h * a.vp_hs + row * D + c * CH, v);
+        row_logits<D, GBM>(q, kv, gn, a.scale, x);
+        st.update(x, v, gn);
+      }
+    }
+    for (int64_t k = s0 + lg; k < s1; k += 16) {
+      float kv[CH], v[CH], x[GBM];
+      load_bf16<CH>(a.key_suffix + h * a.ks_hs + k * a.ks_ts + c * CH, kv);
+      load_bf16<CH>(a.value_suffix + h * a.vs_hs + k * a.vs_ts + c * CH, v);
+      row_logits<D, GBM>(q, kv, gn, a.scale, x);
+      st.update(x, v, gn);
+    }
+
+    // merge the 16 lane groups: within a wave by xor 16/32, then across waves
+#pragma unroll
+    for (int o = 16; o <= 32; o <<= 1) {
       float om[GBM], ol[GBM], oacc[GBM][CH];
 #pragma unroll
       for (int g = 0; g < GBM; ++g) {
-        om[g] = g < gn ? xm[ow][g] : kNegInf;
-        ol[g] = g < gn ? xl[ow][g] : 0.0f;
+        om[g] = shfl_xor(st.m[g], o);
+        ol[g] = shfl_xor(st.l[g], o);
 #pragma unroll
-        for (int i = 0; i < CH; ++i) oacc[g][i] = g < gn ? xacc[ow][g][c * CH + i] : 0.0f;
+        for (int i = 0; i < CH; ++i) oacc[g][i] = shfl_xor(st.acc[g][i], o);
       }
       st.merge(om, ol, oacc, gn);
     }
+    __syncthreads();
+    if ((tid & 63) < 16) {
 #pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      if (g < gn) {
-        const int64_t slot = (h * G + g0 + g) * a.workers + w;
-        if (c == 0) {
-          a.part_m[slot] = st.m[g];
-          a.part_l[slot] = st.l[g];
+      for (int g = 0; g < GBM; ++g) {
+        if (g < gn) {
+          if (c == 0) {
+            xm[wave][g] = st.m[g];
+            xl[wave][g] = st.l[g];
+          }
+#pragma unroll
+          for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = st.acc[g][i];
         }
+      }
+    }
+    __syncthreads();
+    if (tid < 16) {
+      for (int ow = 1; ow < kWaves; ++ow) {
+        float om[GBM], ol[GBM], oacc[GBM][CH];
 #pragma unroll
-        for (int i = 0; i < CH; ++i) a.part_acc[slot * D + c * CH + i] = st.acc[g][i];
+        for (int g = 0; g < GBM; ++g) {
+          om[g] = g < gn ? xm[ow][g] : kNegInf;
+          ol[g] = g < gn ? xl[ow][g] : 0.0f;
+#pragma unroll
+          for (int i = 0; i < CH; ++i) oacc[g][i] = g < gn ? xacc[ow][g][c * CH + i] : 0.0f;
+        }
+        st.merge(om, ol, oacc, gn);
+      }
+#pragma unroll
+      for (int g = 0; g < GBM; ++g) {
+        if (g < gn) {
+          const int64_t slot = slot0 + (int64_t)g * a.workers;
+          if (c == 0) {
+            a.page_m[slot] = st.m[g];
+            a.page_l[slot] = st.l[g];
+          }
+#pragma unroll
+          for (int i = 0; i < CH; ++i) a.page_acc[slot * D + c * CH + i] = st.acc[g][i];
+        }
       }
     }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 4: merge split-K partials -> bf16 output
+// Kernel 4: merge representative and page partials -> bf16 output
 // ---------------------------------------------------------------------------
-__global__ __launch_bounds__(256) void merge_kernel(const float* __restrict__ part_m,
-                                                    const float* __restrict__ part_l,
-                                                    const float* __restrict__ part_acc,
-                                                    uint16_t* __restrict__ out, int workers,
-                                                    int dim) {
+struct MergeArgs {
+  const float* lse;       // rep m = inf_to_zero(zm)
+  const float* rep_l;
+  const float* rep_acc;
+  const float* page_m;
+  const float* page_l;
+  const float* page_acc;
+  uint16_t* out;          // (H*G, D)
+  int64_t n_tiles;
+  int workers, dim;
+};
+
+constexpr int kMergeD = 32;                   // output columns per workgroup
+constexpr int kMergeK = kThreads / kMergeD;   // partial-list stripes
+
+inline size_t merge_smem(int64_t n_tiles, int64_t workers) {
+  const int64_t P = n_tiles + workers;
+  return sizeof(float) * 2 * P + sizeof(int) * P;
+}
+
+__global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
+  extern __shared__ unsigned char smem_raw[];
+  const int64_t T = a.n_tiles, W = a.workers, P = T + W;
+  float* pm = reinterpret_cast<float*>(smem_raw);  // [P] partial max (natural log)
+  float* pl = pm + P;                               // [P] partial l (0 if dead)
+  int* live = reinterpret_cast<int*>(pl + P);       // [P] live partial indices, in order
+  __shared__ float red[kWaves];
+  __shared__ uint32_t wave_tot[kWaves];
+  __shared__ float num_s[kMergeK][kMergeD];
+  __shared__ float den_s[kMergeK];
   const int64_t r = blockIdx.x;
-  const int d = threadIdx.x;
-  float M = kNegInf;
-  for (int w = 0; w < workers; ++w) M = fmaxf(M, part_m[r * workers + w]);
-  const float ms = M == kNegInf ? 0.0f : M;
-  float den = 0.0f, num = 0.0f;
-  for (int w = 0; w < workers; ++w) {
-    const float l = part_l[r * workers + w];
-    if (l > 0.0f) {
-      const float e = __builtin_amdgcn_exp2f(part_m[r * workers + w] - ms);
-      den = den + l * e;
-      if (d < dim) num = num + part_acc[(r * workers + w) * dim + d] * e;
+  const int d0 = blockIdx.y * kMergeD;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int D = a.dim;
+
+  float mx = kNegInf;
+  for (int64_t i = tid; i < P; i += kThreads) {
+    float m, l;
+    if (i < T) {
+      m = inf_to_zero(a.lse[(r * T + i) * 4]);
+      l = a.rep_l[r * T + i];
+    } else {
+      m = a.page_m[r * W + (i - T)];
+      l = a.page_l[r * W + (i - T)];
+    }
+    const bool alive = l > 0.0f;
+    pm[i] = m;
+    pl[i] = alive ? l : 0.0f;
+    if (alive) mx = fmaxf(mx, m);
+  }
+  mx = wave_nanmax(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float Ms = M == kNegInf ? 0.0f : M;
+
+  // live list in index order (chunked block scans)
+  int64_t n_live = 0;
+  for (int64_t base = 0; base < P; base += kThreads) {
+    const int64_t i = base + tid;
+    const bool alive = i < P && pl[i] > 0.0f;
+    uint32_t tot;
+    const uint32_t pos = block_exclusive_scan(alive ? 1u : 0u, wave_tot, tot);
+    if (alive) live[n_live + pos] = (int)i;
+    n_live += tot;
+  }
+  __syncthreads();
+
+  const int dl = tid % kMergeD, k = tid / kMergeD;
+  const int d = d0 + dl;
+  float num = 0.0f, den = 0.0f;
+  for (int64_t q = k; q < n_live; q += kMergeK) {
+    const int i = live[q];
+    const float e = __builtin_amdgcn_exp2f((pm[i] - Ms) * kLog2e);
+    den = den + pl[i] * e;
+    if (d < D) {
+      const float acc = i < T ? a.rep_acc[(r * T + i) * D + d]
+                              : a.page_acc[(r * W + (i - T)) * D + d];
+      num = num + acc * e;
     }
   }
-  if (d < dim) out[r * dim + d] = bf16_rne(num / fmaxf(den, 1e-30f));
+  num_s[k][dl] = num;
+  if (dl == 0) den_s[k] = den;
+  __syncthreads();
+  if (tid < kMergeD && d < D) {
+    float n = num_s[0][tid], dd = den_s[0];
+    for (int kk = 1; kk < kMergeK; ++kk) {
+      n = n + num_s[kk][tid];
+      dd = dd + den_s[kk];
+    }
+    a.out[r * D + d] = bf16_rne(n / fmaxf(dd, 1e-30f));
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -716,6 +842,7 @@ struct SelectParams {
   const void* query;
   const void* key_mean;
   const void* ellipsoid;
+  const void* value_mean;  // non-null: also build representative partials
   const float* value_norm;
   const float* max_value_norm;
   int64_t heads, group, dim, n_blocks, block, length;
@@ -748,35 +875,46 @@ int validate_select(const SelectParams& p, const char* who, Layout& L) {
     return set_error(kInvalidArgument, "%s: n_blocks != ceil(prompt_length / block_size)", who);
   if (p.reduction < 0 || p.reduction > 2)
     return set_error(kInvalidArgument, "%s: reduction code %d", who, p.reduction);
-  if (!aligned(p.query, 16) || !aligned(p.key_mean, 16) || !aligned(p.ellipsoid, 16))
+  if (!aligned(p.query, 16) || !aligned(p.key_mean, 16) || !aligned(p.ellipsoid, 16) ||
+      (p.value_mean && !aligned(p.value_mean, 16)))
     return set_error(kInvalidArgument, "%s: query/summary must be 16-byte aligned", who);
   L = make_layout(p.heads, p.group, p.dim, p.n_blocks);
   if (!p.ws || p.ws_bytes < (size_t)L.total || !aligned(p.ws, 256))
     return set_error(kWorkspaceTooSmall, "%s: workspace needs %lld bytes, 256-byte aligned", who,
                      (long long)L.total);
   if (L.n_tiles > 0x7FFFFFFF) return set_error(kInvalidArgument, "%s: too many blocks", who);
+  if (score_smem(p.group, p.dim) > 64 * 1024)
+    return set_error(kUnsupported, "%s: group x head_dim too large", who);
   return kOk;
 }
 
 int launch_select(const SelectParams& p, const Layout& L) {
+  const bool reps = p.value_mean != nullptr;
   ScoreArgs sa;
   sa.query = static_cast<const uint16_t*>(p.query);
   sa.key_mean = static_cast<const uint16_t*>(p.key_mean);
   sa.ellipsoid = static_cast<const uint16_t*>(p.ellipsoid);
+  sa.value_mean = static_cast<const uint16_t*>(p.value_mean);
   sa.z = at<float>(p.ws, L.z);
   sa.delta = at<float>(p.ws, L.delta);
   sa.lse = at<float>(p.ws, L.lse);
+  sa.rep_acc = at<float>(p.ws, L.rep_acc);
   sa.n_blocks = p.n_blocks;
   sa.n_tiles = L.n_tiles;
   sa.block = p.block;
   sa.length = p.length;
   sa.group = (int)p.group;
   sa.scale = (float)pow((double)p.dim, -0.5);
-  const size_t score_smem = sizeof(float) * (2 * p.group * p.dim + 4 * p.group * kTile);
+  const size_t smem = score_smem(p.group, p.dim);
   dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
   mark(0, p.stream);
-  RKV_DISPATCH_DIM(p.dim, D,
-                   score_kernel<D><<<grid, dim3(kThreads), score_smem, p.stream>>>(sa));
+  if (reps) {
+    RKV_DISPATCH_DIM(p.dim, D,
+                     score_kernel<D, true><<<grid, dim3(kThreads), smem, p.stream>>>(sa));
+  } else {
+    RKV_DISPATCH_DIM(p.dim, D,
+                     score_kernel<D, false><<<grid, dim3(kThreads), smem, p.stream>>>(sa));
+  }
   int rc = check_launch("score_kernel");
   if (rc) return rc;
   mark(1, p.stream);
@@ -787,18 +925,22 @@ int launch_select(const SelectParams& p, const Layout& L) {
   da.lse = sa.lse;
   da.value_norm = p.value_norm;
   da.max_value_norm = p.max_value_norm;
+  da.value_mean = static_cast<const uint16_t*>(p.value_mean);
   da.anchor = p.anchor;
   da.mask = p.mask;
   da.tilebits = at<uint64_t>(p.ws, L.tilebits);
   da.risk_out = p.risk_out;
   da.stats_out = p.stats_out;
   da.accessed = p.accessed;
+  da.rep_l = reps ? at<float>(p.ws, L.rep_l) : nullptr;
+  da.rep_acc = at<float>(p.ws, L.rep_acc);
   da.n_blocks = p.n_blocks;
   da.n_tiles = L.n_tiles;
   da.block = p.block;
   da.length = p.length;
   da.group = (int)p.group;
   da.reduction = p.reduction;
+  da.dim = (int)p.dim;
   da.eps = p.eps;
   decide_kernel<<<grid, dim3(kThreads), 0, p.stream>>>(da);
   rc = check_launch("decide_kernel");
@@ -807,15 +949,23 @@ int launch_select(const SelectParams& p, const Layout& L) {
 }
 
 template <int D>
-int launch_attend(const AttendArgs& aa, const Layout& L, int64_t heads, hipStream_t stream) {
-  constexpr int GBM = (64 / (D / 16)) > kMaxGroup ? kMaxGroup : (64 / (D / 16));
-  const size_t smem = align256((L.n_tiles + 1) * 8) + align256(L.n_tiles * 8) +
-                      sizeof(int64_t) * kListCap;
-  if (smem > 48 * 1024) return set_error(kUnsupported, "attend: %lld tiles exceed LDS",
-                                         (long long)L.n_tiles);
-  dim3 grid((unsigned)L.workers, (unsigned)heads, (unsigned)L.row_blocks);
-  attend_kernel<D, GBM><<<grid, dim3(kThreads), smem, stream>>>(aa);
-  return check_launch("attend_kernel");
+int launch_pages(const PageArgs& pa, const Layout& L, hipStream_t stream) {
+  const size_t smem = page_smem(pa.heads, L.n_tiles);
+  dim3 grid((unsigned)L.workers, (unsigned)L.row_blocks);
+  constexpr int CH = D / 16;
+  constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
+  switch (L.rows_per_block) {
+    case 4:
+      page_kernel<D, 4><<<grid, dim3(kThreads), smem, stream>>>(pa);
+      break;
+    case 8:
+      if constexpr (CAP >= 8) page_kernel<D, 8><<<grid, dim3(kThreads), smem, stream>>>(pa);
+      break;
+    default:
+      if constexpr (CAP >= 16) page_kernel<D, 16><<<grid, dim3(kThreads), smem, stream>>>(pa);
+      break;
+  }
+  return check_launch("page_kernel");
 }
 
 }  // namespace
@@ -830,15 +980,16 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 }
 
 // Byte offsets of the workspace regions, for tests: z, delta, lse, tilebits,
-// attn_m, attn_l, attn_acc, total, n_tiles, workers.
+// rep_l, rep_acc, page_m, page_l, page_acc, total, then n_tiles and workers.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out10) {
-  if (!out10 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+                                    int64_t* out12) {
+  clear_error();
+  if (!out12 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[10] = {L.z, L.delta, L.lse, L.tilebits, L.attn_m,
-                         L.attn_l, L.attn_acc, L.total, L.n_tiles, L.workers};
-  for (int i = 0; i < 10; ++i) out10[i] = v[i];
+  const int64_t v[12] = {L.z,      L.delta,  L.lse,      L.tilebits, L.rep_l,   L.rep_acc,
+                         L.page_m, L.page_l, L.page_acc, L.total,    L.n_tiles, L.workers};
+  for (int i = 0; i < 12; ++i) out12[i] = v[i];
   return kOk;
 }
 
@@ -850,8 +1001,8 @@ extern "C" int rkv_select(const void* query, const void* key_mean, const void* e
                           float* stats_out, unsigned long long* accessed_blocks, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
   clear_error();
-  SelectParams p{query, key_mean, ellipsoid, value_norm, max_value_norm, heads, group, dim,
-                 n_blocks, block_size, prompt_length, eps, reduction, anchor_mask, mask_out,
+  SelectParams p{query, key_mean, ellipsoid, nullptr, value_norm, max_value_norm, heads, group,
+                 dim, n_blocks, block_size, prompt_length, eps, reduction, anchor_mask, mask_out,
                  risk_out, stats_out, accessed_blocks, workspace, workspace_bytes, stream};
   Layout L;
   int rc = validate_select(p, "rkv_select", L);
@@ -874,22 +1025,26 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
                           unsigned long long* accessed_blocks, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
   clear_error();
-  SelectParams p{query, key_mean, ellipsoid, value_norm, max_value_norm, heads, group, dim,
-                 n_blocks, block_size, prompt_length, eps, reduction, anchor_mask, mask_out,
-                 nullptr, nullptr, accessed_blocks, workspace, workspace_bytes, stream};
+  if (!value_mean) return set_error(kInvalidArgument, "rkv_decode: null value_mean");
+  SelectParams p{query, key_mean, ellipsoid, value_mean, value_norm, max_value_norm, heads,
+                 group, dim, n_blocks, block_size, prompt_length, eps, reduction, anchor_mask,
+                 mask_out, nullptr, nullptr, accessed_blocks, workspace, workspace_bytes, stream};
   Layout L;
   int rc = validate_select(p, "rkv_decode", L);
   if (rc) return rc;
-  if (!value_mean || !key_pages || !value_pages || !output)
+  if (!key_pages || !value_pages || !output)
     return set_error(kInvalidArgument, "rkv_decode: null pointer argument");
   if (suffix_capacity < 0)
     return set_error(kInvalidArgument, "rkv_decode: negative suffix capacity");
   if (suffix_capacity > 0 && (!key_suffix || !value_suffix))
     return set_error(kInvalidArgument, "rkv_decode: null suffix with nonzero capacity");
+  if (heads * L.n_tiles > kMaxHeadTiles)
+    return set_error(kUnsupported, "rkv_decode: heads x tiles %lld exceeds %d",
+                     (long long)(heads * L.n_tiles), kMaxHeadTiles);
   const int64_t es = 2;
   const int64_t ch_bytes = dim / 16 * es;
   const uintptr_t need = ch_bytes % 16 == 0 ? 16 : (ch_bytes % 8 == 0 ? 8 : 4);
-  if (!aligned(value_mean, 16) || !aligned(key_pages, need) || !aligned(value_pages, need) ||
+  if (!aligned(key_pages, need) || !aligned(value_pages, need) ||
       (key_page_head_stride * es) % need || (value_page_head_stride * es) % need)
     return set_error(kInvalidArgument, "rkv_decode: pages must be %d-byte aligned", (int)need);
   if (suffix_capacity > 0 &&
@@ -899,44 +1054,56 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
     return set_error(kInvalidArgument, "rkv_decode: suffix rows must be %d-byte aligned",
                      (int)need);
   if (!aligned(output, 4)) return set_error(kInvalidArgument, "rkv_decode: output alignment");
+  const size_t msmem = merge_smem(L.n_tiles, L.workers);
+  if (msmem > 64 * 1024) return set_error(kUnsupported, "rkv_decode: too many partials");
   rc = launch_select(p, L);
   if (rc) return rc;
 
-  AttendArgs aa;
-  aa.query = static_cast<const uint16_t*>(query);
-  aa.z = at<float>(workspace, L.z);
-  aa.value_mean = static_cast<const uint16_t*>(value_mean);
-  aa.key_pages = static_cast<const uint16_t*>(key_pages);
-  aa.value_pages = static_cast<const uint16_t*>(value_pages);
-  aa.key_suffix = static_cast<const uint16_t*>(key_suffix);
-  aa.value_suffix = static_cast<const uint16_t*>(value_suffix);
-  aa.tilebits = at<uint64_t>(workspace, L.tilebits);
-  aa.suffix_len_dev = suffix_length;
-  aa.part_m = at<float>(workspace, L.attn_m);
-  aa.part_l = at<float>(workspace, L.attn_l);
-  aa.part_acc = at<float>(workspace, L.attn_acc);
-  aa.kp_hs = key_page_head_stride;
-  aa.vp_hs = value_page_head_stride;
-  aa.ks_hs = key_suffix_head_stride;
-  aa.ks_ts = key_suffix_token_stride;
-  aa.vs_hs = value_suffix_head_stride;
-  aa.vs_ts = value_suffix_token_stride;
-  aa.suffix_cap = suffix_capacity;
-  aa.n_blocks = n_blocks;
-  aa.n_tiles = L.n_tiles;
-  aa.block = block_size;
-  aa.length = prompt_length;
-  aa.group = (int)group;
-  aa.workers = (int)L.workers;
-  aa.rows_per_block = (int)L.rows_per_block;
-  aa.scale = (float)pow((double)dim, -0.5);
+  PageArgs pa;
+  pa.query = static_cast<const uint16_t*>(query);
+  pa.key_pages = static_cast<const uint16_t*>(key_pages);
+  pa.value_pages = static_cast<const uint16_t*>(value_pages);
+  pa.key_suffix = static_cast<const uint16_t*>(key_suffix);
+  pa.value_suffix = static_cast<const uint16_t*>(value_suffix);
+  pa.tilebits = at<uint64_t>(workspace, L.tilebits);
+  pa.suffix_len_dev = suffix_length;
+  pa.page_m = at<float>(workspace, L.page_m);
+  pa.page_l = at<float>(workspace, L.page_l);
+  pa.page_acc = at<float>(workspace, L.page_acc);
+  pa.kp_hs = key_page_head_stride;
+  pa.vp_hs = value_page_head_stride;
+  pa.ks_hs = key_suffix_head_stride;
+  pa.ks_ts = key_suffix_token_stride;
+  pa.vs_hs = value_suffix_head_stride;
+  pa.vs_ts = value_suffix_token_stride;
+  pa.suffix_cap = suffix_capacity;
+  pa.n_blocks = n_blocks;
+  pa.n_tiles = L.n_tiles;
+  pa.block = block_size;
+  pa.length = prompt_length;
+  pa.heads = (int)heads;
+  pa.group = (int)group;
+  pa.workers = (int)L.workers;
+  pa.rows_per_block = (int)L.rows_per_block;
+  pa.scale = (float)pow((double)dim, -0.5);
   rc = kOk;
-  RKV_DISPATCH_DIM(dim, D, rc = launch_attend<D>(aa, L, heads, stream));
+  RKV_DISPATCH_DIM(dim, D, rc = launch_pages<D>(pa, L, stream));
   if (rc) return rc;
   mark(3, stream);
-  merge_kernel<<<dim3((unsigned)(heads * group)), dim3((unsigned)((dim + 63) / 64 * 64)), 0,
-                 stream>>>(aa.part_m, aa.part_l, aa.part_acc, static_cast<uint16_t*>(output),
-                           (int)L.workers, (int)dim);
+
+  MergeArgs ma;
+  ma.lse = at<float>(workspace, L.lse);
+  ma.rep_l = at<float>(workspace, L.rep_l);
+  ma.rep_acc = at<float>(workspace, L.rep_acc);
+  ma.page_m = pa.page_m;
+  ma.page_l = pa.page_l;
+  ma.page_acc = pa.page_acc;
+  ma.out = static_cast<uint16_t*>(output);
+  ma.n_tiles = L.n_tiles;
+  ma.workers = (int)L.workers;
+  ma.dim = (int)dim;
+  merge_kernel<<<dim3((unsigned)(heads * group), (unsigned)((dim + kMergeD - 1) / kMergeD)),
+                 dim3(kThreads), msmem, stream>>>(ma);
   rc = check_launch("merge_kernel");
   mark(4, stream);
   return rc;
@@ -944,7 +1111,7 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
 
 // Profiling hook: when events is non-null (an array of 5 hipEvent_t), the
 // following rkv_select / rkv_decode calls on this thread record events[0]
-// before the score kernel and events[1..4] after score, decide, attend and
+// before the score kernel and events[1..4] after score, decide, pages and
 // merge.  Pass NULL to stop.
 extern "C" int rkv_set_profile_events(void* events) {
   g_events = static_cast<hipEvent_t*>(events);

@@ -139,12 +139,15 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
+LAYOUT_NAMES = ("z", "delta", "lse", "tilebits", "rep_l", "rep_acc", "page_m", "page_l",
+                "page_acc", "total", "n_tiles", "workers")
+
+
 def workspace_layout(heads, group, dim, n_blocks):
-    out = (ctypes.c_int64 * 10)()
+    """Byte offsets of the workspace regions (rkv_workspace_layout)."""
+    out = (ctypes.c_int64 * len(LAYOUT_NAMES))()
     _check(lib().rkv_workspace_layout(heads, group, dim, n_blocks, out), "rkv_workspace_layout")
-    names = ("z", "delta", "lse", "tilebits", "attn_m", "attn_l", "attn_acc", "total",
-             "n_tiles", "workers")
-    return dict(zip(names, list(out)))
+    return dict(zip(LAYOUT_NAMES, list(out)))
 
 
 def _buffer(workspace, name, shape, device, dtype):
