@@ -123,6 +123,50 @@ __device__ __forceinline__ void load_bf16(const uint16_t* __restrict__ p, float 
   }
 }
 
+// Raw 16-bit payload of N bf16 values, loaded with the widest aligned vector
+// loads and unpacked later: keeping the load and the conversion apart lets
+// every load of a batch be in flight before the first wait.
+template <int N>
+struct RawBf16 {
+  static_assert(N % 2 == 0, "even element count");
+  uint32_t w[N / 2];
+};
+
+template <int N>
+__device__ __forceinline__ RawBf16<N> load_raw(const uint16_t* __restrict__ p) {
+  RawBf16<N> r;
+  if constexpr (N % 8 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 8; ++i) {
+      const uint4 u = *reinterpret_cast<const uint4*>(p + 8 * i);
+      r.w[4 * i] = u.x;
+      r.w[4 * i + 1] = u.y;
+      r.w[4 * i + 2] = u.z;
+      r.w[4 * i + 3] = u.w;
+    }
+  } else if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int i = 0; i < N / 4; ++i) {
+      const uint2 u = *reinterpret_cast<const uint2*>(p + 4 * i);
+      r.w[2 * i] = u.x;
+      r.w[2 * i + 1] = u.y;
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < N / 2; ++i) r.w[i] = *reinterpret_cast<const uint32_t*>(p + 2 * i);
+  }
+  return r;
+}
+
+template <int N>
+__device__ __forceinline__ void unpack(const RawBf16<N>& r, float (&out)[N]) {
+#pragma unroll
+  for (int j = 0; j < N / 2; ++j) {
+    out[2 * j] = bits_f32(r.w[j] << 16);
+    out[2 * j + 1] = bits_f32(r.w[j] & 0xFFFF0000u);
+  }
+}
+
 // Position of the k-th (0-based) set bit of m; m must have more than k bits.
 __device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
   int pos = 0;

@@ -211,29 +211,34 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   const int grp = lane / 16, c = lane % 16;
   const int64_t N = a.n_blocks;
 
-  float km[4][CH], el[4][CH], vm[REPS ? 4 : 1][REPS ? CH : 1];
+  // Issue every load of the tile before the first wait.  Blocks past the end
+  // read block N-1 (their scores are discarded, their weights are 0).
+  RawBf16<CH> kraw[4], eraw[4], vraw[REPS ? 4 : 1];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int64_t b = tile * kTile + wave * 16 + it * 4 + grp;
-    if (b < N) {
-      const int64_t o = (h * N + b) * D + c * CH;
-      load_bf16<CH>(a.key_mean + o, km[it]);
-      load_bf16<CH>(a.ellipsoid + o, el[it]);
-      if constexpr (REPS) load_bf16<CH>(a.value_mean + o, vm[it]);
-    } else {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        km[it][i] = el[it][i] = 0.0f;
-        if constexpr (REPS) vm[it][i] = 0.0f;
-      }
-    }
+    int64_t b = tile * kTile + wave * 16 + it * 4 + grp;
+    b = b < N ? b : N - 1;
+    const int64_t o = (h * N + b) * D + c * CH;
+    kraw[it] = load_raw<CH>(a.key_mean + o);
+    eraw[it] = load_raw<CH>(a.ellipsoid + o);
+    if constexpr (REPS) vraw[it] = load_raw<CH>(a.value_mean + o);
   }
-  for (int i = tid; i < G * D; i += kThreads) {
-    const float q = bf16_to_f32(a.query[h * G * D + i]);
-    qs[i] = q;
-    q2s[i] = round_bf16(q * q);
+  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
+  for (int i = tid; i < G * D / 2; i += kThreads) {
+    const uint32_t u = q32[i];
+    const float q0 = bits_f32(u << 16), q1 = bits_f32(u & 0xFFFF0000u);
+    qs[2 * i] = q0;
+    qs[2 * i + 1] = q1;
+    q2s[2 * i] = round_bf16(q0 * q0);
+    q2s[2 * i + 1] = round_bf16(q1 * q1);
   }
   __syncthreads();
+  float km[4][CH], el[4][CH];
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    unpack(kraw[it], km[it]);
+    unpack(eraw[it], el[it]);
+  }
 
   for (int g = 0; g < G; ++g) {
     float qv[CH], q2v[CH];
@@ -307,8 +312,10 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const float p = pbuf[g * kTile + wave * 16 + it * 4 + grp];
+        float vm[CH];
+        unpack(vraw[it], vm);
 #pragma unroll
-        for (int i = 0; i < CH; ++i) acc[i] = it == 0 ? p * vm[0][i] : acc[i] + p * vm[it][i];
+        for (int i = 0; i < CH; ++i) acc[i] = it == 0 ? p * vm[i] : acc[i] + p * vm[i];
       }
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
@@ -352,24 +359,30 @@ struct DecideArgs {
   float eps;
 };
 
-// Merge the tile partials of one row in the fixed order: max first, then
-// 64 lane accumulators (tile t -> lane t % 64, left to right) and a butterfly.
-__device__ __forceinline__ float merge_lse(const float* part, int64_t n_tiles, int which,
+constexpr int kLseRegs = 4;  // tile partials per lane held in registers (tiles <= 256)
+
+// Merge the tile partials (m, l) of one row in the fixed order: max first,
+// then 64 lane accumulators (tile t -> lane t % 64, left to right) and a
+// butterfly.  m[k], l[k] hold tile lane + 64 k (k < kLseRegs), preloaded.
+__device__ __forceinline__ float merge_lse(const float (&m)[kLseRegs], const float (&l)[kLseRegs],
+                                           const float* part, int which, int64_t n_tiles,
                                            int lane) {
-  float m = kNegInf;
-  for (int64_t t = lane; t < n_tiles; t += kWave) m = nanmax(m, part[t * 4 + 2 * which]);
-  m = wave_nanmax(m);
-  const float ms = inf_to_zero(m);
+  float mx = kNegInf;
+  for (int64_t t = lane, k = 0; t < n_tiles; t += kWave, ++k)
+    mx = nanmax(mx, k < kLseRegs ? m[k] : part[t * 4 + 2 * which]);
+  mx = wave_nanmax(mx);
+  const float ms = inf_to_zero(mx);
   float acc = 0.0f;
-  bool first = true;
-  for (int64_t t = lane; t < n_tiles; t += kWave) {
-    const float term = part[t * 4 + 2 * which + 1] * expf_(part[t * 4 + 2 * which] - ms);
-    acc = first ? term : acc + term;
-    first = false;
+  for (int64_t t = lane, k = 0; t < n_tiles; t += kWave, ++k) {
+    const float mt = k < kLseRegs ? m[k] : part[t * 4 + 2 * which];
+    const float lt = k < kLseRegs ? l[k] : part[t * 4 + 2 * which + 1];
+    const float term = lt * expf_(mt - ms);
+    acc = k == 0 ? term : acc + term;
   }
-  const float L = wave_sum(acc);
-  return logf_(L) + ms;
+  return logf_(wave_sum(acc)) + ms;
 }
+
+constexpr int kRiskPerThread = kMaxGroup * kTile / kThreads;  // (row, block) pairs per thread
 
 __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   __shared__ float gstat[kMaxGroup][2];
@@ -380,12 +393,57 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   const int64_t tile = blockIdx.x;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
-  const int64_t N = a.n_blocks;
+  const int64_t N = a.n_blocks, T = a.n_tiles;
+  const int64_t nvalid = N - tile * kTile >= kTile ? kTile : N - tile * kTile;
 
-  for (int g = wave; g < G; g += kWaves) {
-    const float* part = a.lse + (h * G + g) * a.n_tiles * 4;
-    const float lz = merge_lse(part, a.n_tiles, 0, lane);
-    const float lc = merge_lse(part, a.n_tiles, 1, lane);
+  // ---- every load this tile needs before any wait ---------------------
+  float pz_m[kMaxGroup / kWaves][kLseRegs], pz_l[kMaxGroup / kWaves][kLseRegs];
+  float pc_m[kMaxGroup / kWaves][kLseRegs], pc_l[kMaxGroup / kWaves][kLseRegs];
+#pragma unroll
+  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
+    const int g = wave + gi * kWaves;
+#pragma unroll
+    for (int k = 0; k < kLseRegs; ++k) {
+      const int64_t t = lane + (int64_t)k * kWave;
+      if (g < G && t < T) {
+        const float4 v = *reinterpret_cast<const float4*>(a.lse + ((h * G + g) * T + t) * 4);
+        pz_m[gi][k] = v.x;
+        pz_l[gi][k] = v.y;
+        pc_m[gi][k] = v.z;
+        pc_l[gi][k] = v.w;
+      } else {
+        pz_m[gi][k] = pc_m[gi][k] = kNegInf;
+        pz_l[gi][k] = pc_l[gi][k] = 0.0f;
+      }
+    }
+  }
+  float rz[kRiskPerThread], rd[kRiskPerThread], rv[kRiskPerThread];
+#pragma unroll
+  for (int k = 0; k < kRiskPerThread; ++k) {
+    const int idx = tid + k * kThreads;
+    const int g = idx / kTile, bl = idx % kTile;
+    if (g < G && bl < nvalid) {
+      const int64_t b = tile * kTile + bl;
+      const int64_t o = (h * G + g) * N + b;
+      rz[k] = a.z[o];
+      rd[k] = a.delta[o];
+      rv[k] = a.value_norm[h * N + b];
+    } else {
+      rz[k] = rd[k] = rv[k] = 0.0f;
+    }
+  }
+  const bool anchored =
+      wave == 0 && a.anchor && lane < nvalid && a.anchor[h * N + tile * kTile + lane] != 0;
+  const float vmax = a.max_value_norm[h];
+
+  // ---- global log Z / log C of each row --------------------------------
+#pragma unroll
+  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
+    const int g = wave + gi * kWaves;
+    if (g >= G) break;
+    const float* part = a.lse + (h * G + g) * T * 4;
+    const float lz = merge_lse(pz_m[gi], pz_l[gi], part, 0, T, lane);
+    const float lc = merge_lse(pc_m[gi], pc_l[gi], part, 1, T, lane);
     if (lane == 0) {
       gstat[g][0] = lz;
       gstat[g][1] = lc;
@@ -397,21 +455,20 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   }
   __syncthreads();
 
-  const float vmax = a.max_value_norm[h];
-  for (int idx = tid; idx < G * kTile; idx += kThreads) {
+#pragma unroll
+  for (int k = 0; k < kRiskPerThread; ++k) {
+    const int idx = tid + k * kThreads;
     const int g = idx / kTile, bl = idx % kTile;
-    const int64_t b = tile * kTile + bl;
+    if (g >= G) break;
     float r = 0.0f;
-    if (b < N) {
-      const int64_t o = (h * G + g) * N + b;
-      r = risk_of(a.z[o], a.delta[o], gstat[g][0], gstat[g][1], vmax, a.value_norm[h * N + b]);
-      if (a.risk_out) a.risk_out[o] = r;
+    if (bl < nvalid) {
+      r = risk_of(rz[k], rd[k], gstat[g][0], gstat[g][1], vmax, rv[k]);
+      if (a.risk_out) a.risk_out[(h * G + g) * N + tile * kTile + bl] = r;
     }
     risk_s[g][bl] = r;
   }
   __syncthreads();
 
-  const int64_t nvalid = N - tile * kTile >= kTile ? kTile : N - tile * kTile;
   if (wave == 0) {
     const int64_t b = tile * kTile + lane;
     const bool valid = lane < nvalid;
@@ -433,13 +490,11 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
     }
     if (a.reduction == kMean) sel = (acc / (float)G) > a.eps;
     if (a.reduction == kMax) sel = mx > a.eps;
-    sel = sel || bad_global || bad_local;
-    if (valid && a.anchor) sel = sel || a.anchor[h * N + b] != 0;
-    sel = sel && valid;
+    sel = (sel || bad_global || bad_local || anchored) && valid;
     if (valid) a.mask[h * N + b] = sel ? 1 : 0;
     const uint64_t bits = __ballot(sel);
     if (lane == 0) {
-      a.tilebits[h * a.n_tiles + tile] = bits;
+      a.tilebits[h * T + tile] = bits;
       sel_bits = bits;
     }
     if (a.accessed) {
@@ -453,25 +508,25 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   if (!a.rep_l) return;
   __syncthreads();
 
-  // Representatives of this tile: drop the expanded blocks.
+  // ---- representatives of this tile: drop the expanded blocks ----------
   const uint64_t bits = sel_bits;
   const int nsel = __popcll(bits);
   for (int g = wave; g < G; g += kWaves) {
     const int64_t row = h * G + g;
-    const float ms = inf_to_zero(a.lse[(row * a.n_tiles + tile) * 4]);
+    const float ms = inf_to_zero(a.lse[(row * T + tile) * 4]);
     const bool valid = lane < nvalid;
     const bool expanded = (bits >> lane) & 1ull;
     const float e = valid ? expf_(a.z[row * N + tile * kTile + lane] - ms) : 0.0f;
     const float l = wave_sum(expanded ? 0.0f : e);
     psel[g][lane] = expanded ? e : 0.0f;
-    if (lane == 0) a.rep_l[row * a.n_tiles + tile] = nsel == nvalid ? 0.0f : l;
+    if (lane == 0) a.rep_l[row * T + tile] = nsel == nvalid ? 0.0f : l;
   }
   if (nsel == 0 || nsel == nvalid) return;
   __syncthreads();
   const int D = a.dim;
   for (int idx = tid; idx < G * D; idx += kThreads) {
     const int g = idx / D, d = idx % D;
-    float* acc_p = a.rep_acc + ((h * G + g) * a.n_tiles + tile) * D + d;
+    float* acc_p = a.rep_acc + ((h * G + g) * T + tile) * D + d;
     float acc = *acc_p;
     uint64_t m = bits;
     while (m) {
@@ -505,6 +560,7 @@ struct PageArgs {
 };
 
 constexpr int kListCap = kThreads;  // block indices resolved per chunk
+constexpr int kRowBatch = 4;        // K/V rows per lane group with loads in flight
 
 template <int D, int GBM>
 struct SoftmaxState {
@@ -661,25 +717,55 @@ __global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
         list[tid] = t * kTile + nth_set_bit(a.tilebits[lo_t], (int)(j - pre[lo_t]));
       }
       __syncthreads();
+      // Rows (page tokens) go round-robin to the 16 lane groups, kRowBatch at
+      // a time with all their loads in flight; rows past a short last block
+      // or the list end read row 0 and are skipped.
       const int64_t rows = n * B;
-      for (int64_t r = lg; r < rows; r += 16) {
-        const int64_t jj = r / B, t = r - jj * B;
-        const int64_t b = list[jj];
-        if (t >= block_count(b, N, B, a.length)) continue;
-        const int64_t row = b * B + t;
+      for (int64_t r0 = lg; r0 < rows; r0 += 16 * kRowBatch) {
+        RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
+        bool ok[kRowBatch];
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          const int64_t r = r0 + 16 * u;
+          int64_t row = 0;
+          ok[u] = false;
+          if (r < rows) {
+            const int64_t jj = r / B, t = r - jj * B;
+            const int64_t b = list[jj];
+            ok[u] = t < block_count(b, N, B, a.length);
+            if (ok[u]) row = b * B + t;
+          }
+          kr[u] = load_raw<CH>(a.key_pages + h * a.kp_hs + row * D + c * CH);
+          vr[u] = load_raw<CH>(a.value_pages + h * a.vp_hs + row * D + c * CH);
+        }
+#pragma unroll
+        for (int u = 0; u < kRowBatch; ++u) {
+          if (!ok[u]) continue;
+          float kv[CH], v[CH], x[GBM];
+          unpack(kr[u], kv);
+          unpack(vr[u], v);
+          row_logits<D, GBM>(q, kv, gn, a.scale, x);
+          st.update(x, v, gn);
+        }
+      }
+    }
+    for (int64_t k0 = s0 + lg; k0 < s1; k0 += 16 * kRowBatch) {
+      RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        const int64_t k = k0 + 16 * u < s1 ? k0 + 16 * u : s0;
+        kr[u] = load_raw<CH>(a.key_suffix + h * a.ks_hs + k * a.ks_ts + c * CH);
+        vr[u] = load_raw<CH>(a.value_suffix + h * a.vs_hs + k * a.vs_ts + c * CH);
+      }
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        if (k0 + 16 * u >= s1) break;
         float kv[CH], v[CH], x[GBM];
-        load_bf16<CH>(a.key_pages + h * a.kp_hs + row * D + c * CH, kv);
-        load_bf16<CH>(a.value_pages + h * a.vp_hs + row * D + c * CH, v);
+        unpack(kr[u], kv);
+        unpack(vr[u], v);
         row_logits<D, GBM>(q, kv, gn, a.scale, x);
         st.update(x, v, gn);
       }
-    }
-    for (int64_t k = s0 + lg; k < s1; k += 16) {
-      float kv[CH], v[CH], x[GBM];
-      load_bf16<CH>(a.key_suffix + h * a.ks_hs + k * a.ks_ts + c * CH, kv);
-      load_bf16<CH>(a.value_suffix + h * a.vs_hs + k * a.vs_ts + c * CH, v);
-      row_logits<D, GBM>(q, kv, gn, a.scale, x);
-      st.update(x, v, gn);
     }
 
     // merge the 16 lane groups: within a wave by xor 16/32, then across waves
@@ -811,27 +897,37 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
 
   const int dl = tid % kMergeD, k = tid / kMergeD;
   const int d = d0 + dl;
+  const int dd = d < D ? d : 0;
   float num = 0.0f, den = 0.0f;
-  for (int64_t q = k; q < n_live; q += kMergeK) {
-    const int i = live[q];
-    const float e = __builtin_amdgcn_exp2f((pm[i] - Ms) * kLog2e);
-    den = den + pl[i] * e;
-    if (d < D) {
-      const float acc = i < T ? a.rep_acc[(r * T + i) * D + d]
-                              : a.page_acc[(r * W + (i - T)) * D + d];
-      num = num + acc * e;
+  constexpr int kBatch = 8;
+  for (int64_t q0 = k; q0 < n_live; q0 += kMergeK * kBatch) {
+    int idx[kBatch];
+    float accv[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int64_t q = q0 + (int64_t)u * kMergeK;
+      idx[u] = q < n_live ? live[q] : -1;
+      const int i = idx[u] < 0 ? 0 : idx[u];
+      accv[u] = i < T ? a.rep_acc[(r * T + i) * D + dd] : a.page_acc[(r * W + (i - T)) * D + dd];
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      if (idx[u] < 0) break;
+      const float e = __builtin_amdgcn_exp2f((pm[idx[u]] - Ms) * kLog2e);
+      den = den + pl[idx[u]] * e;
+      num = num + accv[u] * e;
     }
   }
   num_s[k][dl] = num;
   if (dl == 0) den_s[k] = den;
   __syncthreads();
   if (tid < kMergeD && d < D) {
-    float n = num_s[0][tid], dd = den_s[0];
+    float n = num_s[0][tid], den_all = den_s[0];
     for (int kk = 1; kk < kMergeK; ++kk) {
       n = n + num_s[kk][tid];
-      dd = dd + den_s[kk];
+      den_all = den_all + den_s[kk];
     }
-    a.out[r * D + d] = bf16_rne(n / fmaxf(dd, 1e-30f));
+    a.out[r * D + d] = bf16_rne(n / fmaxf(den_all, 1e-30f));
   }
 }
 

@@ -32,36 +32,59 @@ struct InF32 {
   static __device__ __forceinline__ float cvt(float x) { return x; }
 };
 
+// Raw payload of N adjacent elements of the cache dtype, loaded with one
+// vector load and converted later (so a batch of loads is in flight at once).
 template <class In, int N>
-__device__ __forceinline__ void load_cols(const typename In::T* __restrict__ p, float (&x)[N]) {
+struct RawCols {
+  static constexpr int W = N * (int)sizeof(typename In::T) / 4;
+  uint32_t w[W];
+};
+
+template <class In, int N>
+__device__ __forceinline__ RawCols<In, N> load_cols(const typename In::T* __restrict__ p) {
+  RawCols<In, N> r;
+  constexpr int W = RawCols<In, N>::W;
+  if constexpr (W == 1) {
+    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
+  } else if constexpr (W == 2) {
+    const uint2 u = *reinterpret_cast<const uint2*>(p);
+    r.w[0] = u.x;
+    r.w[1] = u.y;
+  } else {
+    const uint4 u = *reinterpret_cast<const uint4*>(p);
+    r.w[0] = u.x;
+    r.w[1] = u.y;
+    r.w[2] = u.z;
+    r.w[3] = u.w;
+  }
+  return r;
+}
+
+template <class In, int N>
+__device__ __forceinline__ void cols_f32(const RawCols<In, N>& r, float (&x)[N]) {
   if constexpr (sizeof(typename In::T) == 2) {
-    if constexpr (N == 2) {
-      uint32_t u = *reinterpret_cast<const uint32_t*>(p);
-      x[0] = In::cvt((uint16_t)(u & 0xFFFFu));
-      x[1] = In::cvt((uint16_t)(u >> 16));
-    } else {
-      uint2 u = *reinterpret_cast<const uint2*>(p);
-      x[0] = In::cvt((uint16_t)(u.x & 0xFFFFu));
-      x[1] = In::cvt((uint16_t)(u.x >> 16));
-      x[2] = In::cvt((uint16_t)(u.y & 0xFFFFu));
-      x[3] = In::cvt((uint16_t)(u.y >> 16));
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      x[2 * j] = In::cvt((uint16_t)(r.w[j] & 0xFFFFu));
+      x[2 * j + 1] = In::cvt((uint16_t)(r.w[j] >> 16));
     }
   } else {
-    if constexpr (N == 2) {
-      float2 u = *reinterpret_cast<const float2*>(p);
-      x[0] = u.x;
-      x[1] = u.y;
-    } else {
-      float4 u = *reinterpret_cast<const float4*>(p);
-      x[0] = u.x;
-      x[1] = u.y;
-      x[2] = u.z;
-      x[3] = u.w;
-    }
+#pragma unroll
+    for (int j = 0; j < N; ++j) x[j] = bits_f32(r.w[j]);
+  }
+}
+
+template <class In>
+__device__ __forceinline__ float elem_f32(const typename In::T* __restrict__ p) {
+  if constexpr (sizeof(typename In::T) == 2) {
+    return In::cvt(*reinterpret_cast<const uint16_t*>(p));
+  } else {
+    return *p;
   }
 }
 
 constexpr int kSummaryWaves = 4;
+constexpr int kTokBatch = 8;  // tokens per batch of pass-1 row loads
 
 template <int D, class In>
 __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
@@ -80,13 +103,14 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
   const int64_t h = blockIdx.y;
   const int64_t b = (int64_t)blockIdx.x * kSummaryWaves + wave;
   const bool valid = b < n_blocks;
+  const int64_t bb = valid ? b : n_blocks - 1;  // in-bounds block for addresses
   const int64_t cnt = !valid ? 0 : (b == n_blocks - 1 ? length - (n_blocks - 1) * block : block);
 
   // ---- pass 1: column sums (TOKSUM order), min, max -------------------
   const bool on1 = valid && lane < LANES1;
-  const int col = lane * CPL;
-  const typename In::T* kb = keys + h * k_hs + (b * block) * k_ts + col;
-  const typename In::T* vb = values + h * v_hs + (b * block) * v_ts + col;
+  const int col = lane < LANES1 ? lane * CPL : 0;
+  const typename In::T* kb = keys + h * k_hs + (bb * block) * k_ts + col;
+  const typename In::T* vb = values + h * v_hs + (bb * block) * v_ts + col;
   float ksum[CPL], vsum[CPL], kmax[CPL], kmin[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -100,24 +124,31 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
 #pragma unroll
     for (int j = 0; j < CPL; ++j) ak[j] = av[j] = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      const int t = c0 + i;
-      float xk[CPL], xv[CPL];
-      const bool live = on1 && t < cnt;
-      if (live) {
-        load_cols<In>(kb + t * k_ts, xk);
-        load_cols<In>(vb + t * v_ts, xv);
-      } else {
+    for (int i0 = 0; i0 < 16; i0 += kTokBatch) {
+      RawCols<In, CPL> rk[kTokBatch], rv[kTokBatch];
 #pragma unroll
-        for (int j = 0; j < CPL; ++j) xk[j] = xv[j] = 0.0f;
+      for (int i = 0; i < kTokBatch; ++i) {
+        const int t = c0 + i0 + i;
+        const int tt = t < cnt ? t : 0;  // rows past the block end read its first row
+        rk[i] = load_cols<In, CPL>(kb + tt * k_ts);
+        rv[i] = load_cols<In, CPL>(vb + tt * v_ts);
       }
 #pragma unroll
-      for (int j = 0; j < CPL; ++j) {
-        ak[j] = ak[j] + xk[j];
-        av[j] = av[j] + xv[j];
-        if (live) {
-          kmax[j] = nanmax(kmax[j], xk[j]);
-          kmin[j] = nanmin(kmin[j], xk[j]);
+      for (int i = 0; i < kTokBatch; ++i) {
+        const int t = c0 + i0 + i;
+        const bool live = on1 && t < cnt;
+        float xk[CPL], xv[CPL];
+        cols_f32<In, CPL>(rk[i], xk);
+        cols_f32<In, CPL>(rv[i], xv);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          // Padded tokens add +0, as the reference's zero-padded pages do.
+          ak[j] = ak[j] + (live ? xk[j] : 0.0f);
+          av[j] = av[j] + (live ? xv[j] : 0.0f);
+          if (live) {
+            kmax[j] = nanmax(kmax[j], xk[j]);
+            kmin[j] = nanmin(kmin[j], xk[j]);
+          }
         }
       }
     }
@@ -154,21 +185,26 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
   for (int t0 = 0; t0 < cnt; t0 += 8) {
     const int t = t0 + g8;
     const bool on = t < cnt;
-    const typename In::T* kr = keys + h * k_hs + (b * block + t) * k_ts;
-    const typename In::T* vr = values + h * v_hs + (b * block + t) * v_ts;
+    const int tt = on ? t : 0;
+    const typename In::T* kr = keys + h * k_hs + (bb * block + tt) * k_ts;
+    const typename In::T* vr = values + h * v_hs + (bb * block + tt) * v_ts;
+    float kx[D / 8], vx[D / 8];
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) {
+      kx[m] = elem_f32<In>(kr + 8 * m + l8);
+      vx[m] = elem_f32<In>(vr + 8 * m + l8);
+    }
     float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f, an = 0.0f;
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
       const int e = 8 * m + l8;
-      const float k = on ? In::cvt(kr[e]) : 0.0f;
-      const float v = on ? In::cvt(vr[e]) : 0.0f;
-      const float c = (k - s_mk[wave][e]) * s_rs[wave][e];
+      const float c = (kx[m] - s_mk[wave][e]) * s_rs[wave][e];
       const float c2 = c * c;
       if ((m & 3) == 0) A0 = A0 + c2;
       if ((m & 3) == 1) A1 = A1 + c2;
       if ((m & 3) == 2) A2 = A2 + c2;
       if ((m & 3) == 3) A3 = A3 + c2;
-      an = __builtin_fmaf(v, v, an);
+      an = __builtin_fmaf(vx[m], vx[m], an);
     }
     const float P = ((A0 + A1) + A2) + A3;
     float tot = 0.0f;
