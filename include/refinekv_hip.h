@@ -64,10 +64,10 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
 /* Byte offsets inside the workspace (for tests): z, delta, lse, tilebits,
- * rep_l, rep_acc, page_m, page_l, page_acc, total, then n_tiles and the
- * number of page workers -> out12[0..11]. */
+ * rep_l, rep_acc, header, page_m, page_l, page_acc, total, then n_tiles and
+ * the number of page workers -> out13[0..12]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out12);
+                         int64_t* out13);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton

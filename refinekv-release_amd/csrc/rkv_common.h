@@ -76,6 +76,31 @@ __device__ __forceinline__ float row16_sum_last(float v) {
   return v;
 }
 
+__device__ __forceinline__ float readlane(float v, int lane) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
+}
+
+// Wave-wide sum in the 64-lane xor-butterfly tree (distances 32..1), returned
+// uniformly: the cross-row levels 32 and 16 move data with permutes, the
+// in-row levels with DPP (complete in lane 15), then lane 15 is read out.
+// Bit-identical to the plain butterfly.
+__device__ __forceinline__ float wave_sum_u(float v) {
+  v = v + __shfl_xor(v, 32, kWave);
+  v = v + __shfl_xor(v, 16, kWave);
+  return readlane(row16_sum_last(v), 15);
+}
+
+// NaN-propagating wave max, returned uniformly.
+__device__ __forceinline__ float wave_nanmax_u(float v) {
+  v = nanmax(v, __shfl_xor(v, 32, kWave));
+  v = nanmax(v, __shfl_xor(v, 16, kWave));
+  v = nanmax(v, row_shr<8>(v));
+  v = nanmax(v, row_shr<4>(v));
+  v = nanmax(v, row_shr<2>(v));
+  v = nanmax(v, row_shr<1>(v));
+  return readlane(v, 15);
+}
+
 // Broadcast lane 15 of each 16-lane row to the whole row.
 __device__ __forceinline__ float row_bcast_last(float v) {
   const int lane = threadIdx.x % kWave;

@@ -54,7 +54,7 @@ inline void mark(int i, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int64_t n_tiles, workers, rows_per_block, row_blocks;
-  int64_t z, delta, lse, tilebits, rep_l, rep_acc, page_m, page_l, page_acc, total;
+  int64_t z, delta, lse, tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -99,6 +99,7 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.tilebits = take(heads * L.n_tiles * 8);
   L.rep_l = take(rows * L.n_tiles * 4);
   L.rep_acc = take(rows * L.n_tiles * dim * 4);
+  L.header = take((heads + 1) * 8);
   L.page_m = take(rows * L.workers * 4);
   L.page_l = take(rows * L.workers * 4);
   L.page_acc = take(rows * L.workers * dim * 4);
@@ -187,8 +188,9 @@ struct ScoreArgs {
   float scale;
 };
 
-inline size_t score_smem(int64_t group, int64_t dim) {
-  return sizeof(float) * (2 * group * dim + 5 * group * kTile + kWaves * dim);
+inline size_t score_smem(int64_t group, int64_t dim, bool reps) {
+  return sizeof(float) * (2 * group * dim + 5 * group * kTile) +
+         (reps ? sizeof(uint16_t) * kTile * dim : 0);
 }
 
 template <int D, bool REPS>
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   float* zbuf = pdot + G * kTile;   // [G][64]
   float* zcbuf = zbuf + G * kTile;  // [G][64]
   float* pbuf = zcbuf + G * kTile;  // [G][64] exp(z - m_tile)
-  float* racc = pbuf + G * kTile;   // [waves][D]
+  uint32_t* vsm = reinterpret_cast<uint32_t*>(pbuf + G * kTile);  // [64][D/2] value means
 
   const int64_t h = blockIdx.y;
   const int64_t tile = blockIdx.x;
@@ -232,12 +234,22 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     q2s[2 * i] = round_bf16(q0 * q0);
     q2s[2 * i + 1] = round_bf16(q1 * q1);
   }
+  // ln(count): every block holds block_size tokens except the last.
+  const float ln_full = logf_((float)a.block);
+  const float ln_last = logf_((float)(a.length - (N - 1) * a.block));
   __syncthreads();
+
   float km[4][CH], el[4][CH];
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     unpack(kraw[it], km[it]);
     unpack(eraw[it], el[it]);
+    if constexpr (REPS) {
+      // stage the value means in LDS for the per-row representative sums
+      const int bl = wave * 16 + it * 4 + grp;
+#pragma unroll
+      for (int j = 0; j < CH / 2; ++j) vsm[bl * (D / 2) + c * (CH / 2) + j] = vraw[it].w[j];
+    }
   }
 
   for (int g = 0; g < G; ++g) {
@@ -276,7 +288,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     if (b < N) {
       const float s = sdot[idx] * a.scale;
       const float dl = (sqrtf(clamp_min(pdot[idx], 0.0f)) * a.scale) * kInflate;
-      z = s + logf_((float)block_count(b, N, a.block, a.length));
+      z = s + (b == N - 1 ? ln_last : ln_full);
       zc = z + log_cosh(dl);
       const int64_t o = (h * G + g) * N + b;
       a.z[o] = z;
@@ -289,33 +301,34 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
 
   for (int g = wave; g < G; g += kWaves) {
     const float x = zbuf[g * kTile + lane];
-    const float zm = wave_nanmax(x);
+    const float zm = wave_nanmax_u(x);
     const float e = expf_(x - inf_to_zero(zm));
-    const float zl = wave_sum(e);
-    pbuf[g * kTile + lane] = e;
+    const float zl = wave_sum_u(e);
     const float xc = zcbuf[g * kTile + lane];
-    const float cm = wave_nanmax(xc);
-    const float cl = wave_sum(expf_(xc - inf_to_zero(cm)));
+    const float cm = wave_nanmax_u(xc);
+    const float cl = wave_sum_u(expf_(xc - inf_to_zero(cm)));
     if (lane == 0) {
-      float* o = a.lse + ((h * G + g) * a.n_tiles + tile) * 4;
-      o[0] = zm;
-      o[1] = zl;
-      o[2] = cm;
-      o[3] = cl;
+      *reinterpret_cast<float4*>(a.lse + ((h * G + g) * a.n_tiles + tile) * 4) =
+          make_float4(zm, zl, cm, cl);
     }
-  }
-
-  if constexpr (REPS) {
-    __syncthreads();
-    for (int g = 0; g < G; ++g) {
+    if constexpr (REPS) {
+      // Representative accumulator of row g: sum_b e_b v_b over the tile.
+      // Lane group grp takes blocks grp, grp+4, ...; the four partial sums
+      // are then added by two cross-row permutes.
+      pbuf[g * kTile + lane] = e;
+      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
       float acc[CH];
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const float p = pbuf[g * kTile + wave * 16 + it * 4 + grp];
-        float vm[CH];
-        unpack(vraw[it], vm);
+      for (int k = 0; k < kTile / 4; ++k) {
+        const int bl = grp + 4 * k;
+        const float w = pbuf[g * kTile + bl];
+        RawBf16<CH> r;
 #pragma unroll
-        for (int i = 0; i < CH; ++i) acc[i] = it == 0 ? p * vm[i] : acc[i] + p * vm[i];
+        for (int j = 0; j < CH / 2; ++j) r.w[j] = vsm[bl * (D / 2) + c * (CH / 2) + j];
+        float v[CH];
+        unpack(r, v);
+#pragma unroll
+        for (int i = 0; i < CH; ++i) acc[i] = k == 0 ? w * v[i] : acc[i] + w * v[i];
       }
 #pragma unroll
       for (int i = 0; i < CH; ++i) {
@@ -323,15 +336,10 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
         acc[i] = acc[i] + shfl_xor(acc[i], 32);
       }
       if (grp == 0) {
+        float* o = a.rep_acc + ((h * G + g) * a.n_tiles + tile) * D + c * CH;
 #pragma unroll
-        for (int i = 0; i < CH; ++i) racc[wave * D + c * CH + i] = acc[i];
+        for (int i = 0; i < CH; ++i) o[i] = acc[i];
       }
-      __syncthreads();
-      for (int d = tid; d < D; d += kThreads) {
-        const float sum = ((racc[d] + racc[D + d]) + racc[2 * D + d]) + racc[3 * D + d];
-        a.rep_acc[((h * G + g) * a.n_tiles + tile) * D + d] = sum;
-      }
-      __syncthreads();
     }
   }
 }
@@ -370,7 +378,7 @@ __device__ __forceinline__ float merge_lse(const float (&m)[kLseRegs], const flo
   float mx = kNegInf;
   for (int64_t t = lane, k = 0; t < n_tiles; t += kWave, ++k)
     mx = nanmax(mx, k < kLseRegs ? m[k] : part[t * 4 + 2 * which]);
-  mx = wave_nanmax(mx);
+  mx = wave_nanmax_u(mx);
   const float ms = inf_to_zero(mx);
   float acc = 0.0f;
   for (int64_t t = lane, k = 0; t < n_tiles; t += kWave, ++k) {
@@ -379,7 +387,7 @@ __device__ __forceinline__ float merge_lse(const float (&m)[kLseRegs], const flo
     const float term = lt * expf_(mt - ms);
     acc = k == 0 ? term : acc + term;
   }
-  return logf_(wave_sum(acc)) + ms;
+  return logf_(wave_sum_u(acc)) + ms;
 }
 
 constexpr int kRiskPerThread = kMaxGroup * kTile / kThreads;  // (row, block) pairs per thread
@@ -435,6 +443,26 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   const bool anchored =
       wave == 0 && a.anchor && lane < nvalid && a.anchor[h * N + tile * kTile + lane] != 0;
   const float vmax = a.max_value_norm[h];
+  // Representative partial of this tile: the z max (m of the partial) for
+  // the rows this wave corrects, and the accumulator slice of this thread.
+  float tile_m[kMaxGroup / kWaves];
+#pragma unroll
+  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
+    const int g = wave + gi * kWaves;
+    tile_m[gi] = (a.rep_l && g < G) ? a.lse[((h * G + g) * T + tile) * 4] : 0.0f;
+  }
+  constexpr int kAccPerThread = kMaxGroup * 256 / kThreads;  // G * D <= 16 * 256
+  float racc[kAccPerThread];
+  const int GD = G * a.dim;
+#pragma unroll
+  for (int k = 0; k < kAccPerThread; ++k) {
+    const int idx = tid + k * kThreads;
+    racc[k] = 0.0f;
+    if (a.rep_l && idx < GD) {
+      const int g = idx / a.dim, d = idx % a.dim;
+      racc[k] = a.rep_acc[((h * G + g) * T + tile) * a.dim + d];
+    }
+  }
 
   // ---- global log Z / log C of each row --------------------------------
 #pragma unroll
@@ -442,7 +470,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
     const int g = wave + gi * kWaves;
     if (g >= G) break;
     const float* part = a.lse + (h * G + g) * T * 4;
-    const float lz = merge_lse(pz_m[gi], pz_l[gi], part, 0, T, lane);
+    const float lz = merge_lse(pz_m[gi], pz_l[gi], part, 0, T, lane);  // log Z
     const float lc = merge_lse(pc_m[gi], pc_l[gi], part, 1, T, lane);
     if (lane == 0) {
       gstat[g][0] = lz;
@@ -509,25 +537,29 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   __syncthreads();
 
   // ---- representatives of this tile: drop the expanded blocks ----------
+  // (thread tid's prefetched z/delta pair k is row wave + 4k, block lane)
   const uint64_t bits = sel_bits;
   const int nsel = __popcll(bits);
-  for (int g = wave; g < G; g += kWaves) {
-    const int64_t row = h * G + g;
-    const float ms = inf_to_zero(a.lse[(row * T + tile) * 4]);
+#pragma unroll
+  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
+    const int g = wave + gi * kWaves;
+    if (g >= G) break;
     const bool valid = lane < nvalid;
     const bool expanded = (bits >> lane) & 1ull;
-    const float e = valid ? expf_(a.z[row * N + tile * kTile + lane] - ms) : 0.0f;
-    const float l = wave_sum(expanded ? 0.0f : e);
+    const float e = valid ? expf_(rz[gi] - inf_to_zero(tile_m[gi])) : 0.0f;
+    const float l = wave_sum_u(expanded ? 0.0f : e);
     psel[g][lane] = expanded ? e : 0.0f;
-    if (lane == 0) a.rep_l[row * T + tile] = nsel == nvalid ? 0.0f : l;
+    if (lane == 0) a.rep_l[(h * G + g) * T + tile] = nsel == nvalid ? 0.0f : l;
   }
   if (nsel == 0 || nsel == nvalid) return;
   __syncthreads();
   const int D = a.dim;
-  for (int idx = tid; idx < G * D; idx += kThreads) {
+#pragma unroll
+  for (int k = 0; k < kAccPerThread; ++k) {
+    const int idx = tid + k * kThreads;
+    if (idx >= GD) break;
     const int g = idx / D, d = idx % D;
-    float* acc_p = a.rep_acc + ((h * G + g) * T + tile) * D + d;
-    float acc = *acc_p;
+    float acc = racc[k];
     uint64_t m = bits;
     while (m) {
       const int j = __builtin_ctzll(m);
@@ -535,7 +567,7 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
       const float v = bf16_to_f32(a.value_mean[(h * N + tile * kTile + j) * D + d]);
       acc = acc - psel[g][j] * v;
     }
-    *acc_p = acc;
+    a.rep_acc[((h * G + g) * T + tile) * D + d] = acc;
   }
 }
 
@@ -550,7 +582,8 @@ struct PageArgs {
   const uint16_t* value_suffix;
   const uint64_t* tilebits;    // (H, tiles)
   const int32_t* suffix_len_dev;  // or null
-  float* page_m;               // (H*G, W)
+  int64_t* header;             // (H + 1): cost start of each head's work, [H] = total
+  float* page_m;               // (H*G, W), written only by workers touching the head
   float* page_l;
   float* page_acc;             // (H*G, W, D)
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
@@ -559,73 +592,27 @@ struct PageArgs {
   float scale;
 };
 
-constexpr int kListCap = kThreads;  // block indices resolved per chunk
-constexpr int kRowBatch = 4;        // K/V rows per lane group with loads in flight
+constexpr int kRowBatch = 4;                  // rows per lane group per chunk
+constexpr int kChunkRows = 16 * kRowBatch;    // rows per chunk (one per lane of a wave)
 
-template <int D, int GBM>
-struct SoftmaxState {
-  static constexpr int CH = D / 16;
-  float m[GBM], l[GBM], acc[GBM][CH];
-
-  __device__ __forceinline__ void init() {
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      m[g] = kNegInf;
-      l[g] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
-    }
-  }
-  // x: natural-log logits (one per row); v: this lane's slice of the value row.
-  __device__ __forceinline__ void update(const float (&x)[GBM], const float (&v)[CH], int gn) {
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      if (g >= gn) break;
-      const float mn = fmaxf(m[g], x[g]);
-      if (mn == kNegInf) continue;
-      const float alpha = __builtin_amdgcn_exp2f((m[g] - mn) * kLog2e);
-      const float p = __builtin_amdgcn_exp2f((x[g] - mn) * kLog2e);
-      l[g] = l[g] * alpha + p;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * alpha + p * v[i];
-      m[g] = mn;
-    }
-  }
-  __device__ __forceinline__ void merge(const float* om, const float* ol, const float (*oacc)[CH],
-                                        int gn) {
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      if (g >= gn) break;
-      const float mn = fmaxf(m[g], om[g]);
-      if (mn == kNegInf) continue;
-      const float a = __builtin_amdgcn_exp2f((m[g] - mn) * kLog2e);
-      const float b = __builtin_amdgcn_exp2f((om[g] - mn) * kLog2e);
-      l[g] = l[g] * a + ol[g] * b;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * a + oacc[g][i] * b;
-      m[g] = mn;
-    }
-  }
-};
-
-// Exact logits of one K row for this lane's query slice (DSUM order), natural
-// units, broadcast to the 16-lane group.
+// Exact logits of one K row for this lane's query slice (DSUM order, natural
+// units), complete in lane 15 of the 16-lane group.
 template <int D, int GBM>
 __device__ __forceinline__ void row_logits(const float (&q)[GBM][D / 16], const float (&k)[D / 16],
-                                           int gn, float scale, float (&x)[GBM]) {
+                                           float (&x)[GBM]) {
   constexpr int CH = D / 16;
 #pragma unroll
   for (int g = 0; g < GBM; ++g) {
     float s = q[g][0] * k[0];
 #pragma unroll
     for (int i = 1; i < CH; ++i) s = s + q[g][i] * k[i];
-    s = row_bcast_last(row16_sum_last(s));
-    x[g] = g < gn ? s * scale : kNegInf;
+    x[g] = row16_sum_last(s);
   }
 }
 
 inline size_t page_smem(int64_t heads, int64_t n_tiles) {
-  return (size_t)align256((heads * n_tiles + 1) * 4) + sizeof(int64_t) * kListCap;
+  return (size_t)(align256((heads * n_tiles + 1) * 4) + align256((heads + 1) * 8) +
+                  sizeof(int64_t) * 8);
 }
 
 template <int D, int GBM>
@@ -634,9 +621,11 @@ __global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
   extern __shared__ unsigned char smem_raw[];
   const int64_t T = a.n_tiles, H = a.heads, HT = H * T;
   uint32_t* pre = reinterpret_cast<uint32_t*>(smem_raw);  // [HT + 1] page prefix, head-major
-  int64_t* list = reinterpret_cast<int64_t*>(smem_raw + align256((HT + 1) * 4));
+  int64_t* hs = reinterpret_cast<int64_t*>(smem_raw + align256((HT + 1) * 4));  // [H + 1]
+  int64_t* list = hs + align256((H + 1) * 8) / 8;                               // [8]
   __shared__ uint32_t wave_tot[kWaves];
-  __shared__ float xm[kWaves][GBM], xl[kWaves][GBM];
+  __shared__ float xlog[GBM][kChunkRows];
+  __shared__ float cmax[GBM], csum[GBM];
   __shared__ float xacc[kWaves][GBM][D];
 
   const int w = blockIdx.x;
@@ -644,6 +633,7 @@ __global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
   const int gn = min(a.rows_per_block, a.group - g0);
   const int G = a.group;
   const int tid = threadIdx.x, lg = tid >> 4, c = tid & 15, wave = tid / kWave;
+  const int lane = tid % kWave, grp = lane >> 4;
   const int64_t N = a.n_blocks, B = a.block;
 
   // ---- expanded-page prefix over every (head, tile) ----------------------
@@ -665,160 +655,170 @@ __global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
     const int64_t s = *a.suffix_len_dev;
     S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
   }
-  const int64_t pc = 2 * B;  // cost of one page
-  const int64_t C = pc * (int64_t)total + 2 * S * H;
+  const int64_t pc = 2 * B;  // cost of one page; a suffix token costs 2
+  for (int64_t h = tid; h <= H; h += kThreads) hs[h] = pc * (int64_t)pre[h * T] + 2 * S * h;
+  __syncthreads();
+  const int64_t C = hs[H];
+  if (w == 0 && blockIdx.y == 0)
+    for (int64_t h = tid; h <= H; h += kThreads) a.header[h] = hs[h];
   const int64_t lo = C * w / a.workers, hi = C * (w + 1) / a.workers;
-  auto clampi = [](int64_t x, int64_t l, int64_t h) { return x < l ? l : (x > h ? h : x); };
+  auto clampi = [](int64_t x, int64_t l, int64_t u) { return x < l ? l : (x > u ? u : x); };
   auto ceil_div = [](int64_t x, int64_t d) { return x <= 0 ? 0 : (x + d - 1) / d; };
 
-  for (int64_t h = 0; h < H; ++h) {
+  // first head whose range may hold lo: the largest h with hs[h] <= lo
+  int64_t hb = 0, ht = H - 1;
+  while (hb < ht) {
+    const int64_t mid = (hb + ht + 1) >> 1;
+    if (hs[mid] <= lo) hb = mid; else ht = mid - 1;
+  }
+  for (int64_t h = hb; h < H && hs[h] < hi; ++h) {
+    const int64_t hs_h = hs[h], he_h = hs[h + 1];
+    if (!(lo < he_h && hi > hs_h)) continue;
     const int64_t first = pre[h * T];
     const int64_t n_h = (int64_t)pre[(h + 1) * T] - first;
-    const int64_t hs = pc * first + 2 * S * h;
-    const int64_t he = hs + pc * n_h + 2 * S;
-    const int64_t slot0 = (h * G + g0) * a.workers + w;
-    if (!(lo < he && hi > hs)) {
-      if (tid < gn) {
-        a.page_m[slot0 + (int64_t)tid * a.workers] = kNegInf;
-        a.page_l[slot0 + (int64_t)tid * a.workers] = 0.0f;
-      }
-      continue;
-    }
-    const int64_t lo_h = lo - hs, hi_h = hi - hs;
+    const int64_t lo_h = lo - hs_h, hi_h = hi - hs_h;
     const int64_t p0 = clampi(ceil_div(lo_h, pc), 0, n_h), p1 = clampi(ceil_div(hi_h, pc), 0, n_h);
     const int64_t s0 = clampi(ceil_div(lo_h - pc * n_h, 2), 0, S);
     const int64_t s1 = clampi(ceil_div(hi_h - pc * n_h, 2), 0, S);
+    const int64_t n_prow = (p1 - p0) * B, n_rows = n_prow + (s1 - s0);
 
     float q[GBM][CH];
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
-      if (g < gn) {
-        load_bf16<CH>(a.query + ((h * G + g0 + g) * D + c * CH), q[g]);
-      } else {
-#pragma unroll
-        for (int i = 0; i < CH; ++i) q[g][i] = 0.0f;
-      }
+      const int gg = g < gn ? g : 0;
+      RawBf16<CH> r = load_raw<CH>(a.query + ((h * G + g0 + gg) * D + c * CH));
+      unpack(r, q[g]);
     }
-    SoftmaxState<D, GBM> st;
-    st.init();
+    float m_run[GBM], l_run[GBM], acc[GBM][CH];
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      m_run[g] = kNegInf;
+      l_run[g] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
+    }
 
-    for (int64_t base = p0; base < p1; base += kListCap) {
-      const int64_t n = min((int64_t)kListCap, p1 - base);
+    // Rows in chunks of 64: pass 1 loads K/V and writes the chunk's logits,
+    // pass 2 weighs the V rows with one shared max (no per-row rescaling).
+    for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
+      // pages touched by this chunk -> block indices
+      const int64_t j_first = c0 < n_prow ? p0 + c0 / B : p1;
+      const int64_t j_last = min(c0 + kChunkRows, n_prow) - 1;
+      const int64_t n_pages = c0 < n_prow ? p0 + j_last / B - j_first + 1 : 0;
       __syncthreads();
-      if (tid < n) {
-        // page index -> (tile, bit) by binary search over head h's tiles
-        const int64_t j = first + base + tid;
+      if (tid < n_pages) {
+        const int64_t j = first + j_first + tid;
         int64_t lo_t = h * T, hi_t = h * T + T - 1;
         while (lo_t < hi_t) {
           const int64_t mid = (lo_t + hi_t + 1) >> 1;
           if ((int64_t)pre[mid] <= j) lo_t = mid; else hi_t = mid - 1;
         }
-        const int64_t t = lo_t - h * T;
-        list[tid] = t * kTile + nth_set_bit(a.tilebits[lo_t], (int)(j - pre[lo_t]));
+        list[tid] = (lo_t - h * T) * kTile + nth_set_bit(a.tilebits[lo_t], (int)(j - pre[lo_t]));
       }
       __syncthreads();
-      // Rows (page tokens) go round-robin to the 16 lane groups, kRowBatch at
-      // a time with all their loads in flight; rows past a short last block
-      // or the list end read row 0 and are skipped.
-      const int64_t rows = n * B;
-      for (int64_t r0 = lg; r0 < rows; r0 += 16 * kRowBatch) {
-        RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
-        bool ok[kRowBatch];
-#pragma unroll
-        for (int u = 0; u < kRowBatch; ++u) {
-          const int64_t r = r0 + 16 * u;
-          int64_t row = 0;
-          ok[u] = false;
-          if (r < rows) {
-            const int64_t jj = r / B, t = r - jj * B;
-            const int64_t b = list[jj];
-            ok[u] = t < block_count(b, N, B, a.length);
-            if (ok[u]) row = b * B + t;
-          }
-          kr[u] = load_raw<CH>(a.key_pages + h * a.kp_hs + row * D + c * CH);
-          vr[u] = load_raw<CH>(a.value_pages + h * a.vp_hs + row * D + c * CH);
-        }
-#pragma unroll
-        for (int u = 0; u < kRowBatch; ++u) {
-          if (!ok[u]) continue;
-          float kv[CH], v[CH], x[GBM];
-          unpack(kr[u], kv);
-          unpack(vr[u], v);
-          row_logits<D, GBM>(q, kv, gn, a.scale, x);
-          st.update(x, v, gn);
-        }
-      }
-    }
-    for (int64_t k0 = s0 + lg; k0 < s1; k0 += 16 * kRowBatch) {
       RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
+      bool ok[kRowBatch];
 #pragma unroll
       for (int u = 0; u < kRowBatch; ++u) {
-        const int64_t k = k0 + 16 * u < s1 ? k0 + 16 * u : s0;
-        kr[u] = load_raw<CH>(a.key_suffix + h * a.ks_hs + k * a.ks_ts + c * CH);
-        vr[u] = load_raw<CH>(a.value_suffix + h * a.vs_hs + k * a.vs_ts + c * CH);
+        const int64_t v = c0 + lg + 16 * u;
+        const uint16_t* kp = a.key_pages + h * a.kp_hs;  // a valid row for idle lanes
+        const uint16_t* vp = a.value_pages + h * a.vp_hs;
+        ok[u] = false;
+        if (v < n_prow) {
+          const int64_t jj = v / B, t = v - jj * B;
+          const int64_t b = list[p0 + jj - j_first];
+          if (t < block_count(b, N, B, a.length)) {
+            ok[u] = true;
+            kp += (b * B + t) * D;
+            vp += (b * B + t) * D;
+          }
+        } else if (v < n_rows) {
+          const int64_t k = s0 + (v - n_prow);
+          ok[u] = true;
+          kp = a.key_suffix + h * a.ks_hs + k * a.ks_ts;
+          vp = a.value_suffix + h * a.vs_hs + k * a.vs_ts;
+        }
+        kr[u] = load_raw<CH>(kp + c * CH);
+        vr[u] = load_raw<CH>(vp + c * CH);
       }
 #pragma unroll
       for (int u = 0; u < kRowBatch; ++u) {
-        if (k0 + 16 * u >= s1) break;
-        float kv[CH], v[CH], x[GBM];
+        float kv[CH], x[GBM];
         unpack(kr[u], kv);
+        row_logits<D, GBM>(q, kv, x);
+        if (c == 15) {
+#pragma unroll
+          for (int g = 0; g < GBM; ++g) xlog[g][lg + 16 * u] = ok[u] ? x[g] * a.scale : kNegInf;
+        }
+      }
+      __syncthreads();
+      // chunk max and sum per query row, one wave per row
+      for (int g = wave; g < gn; g += kWaves) {
+        const float x = xlog[g][lane];
+        const float cm = wave_nanmax_u(x);
+        const float ms = cm == kNegInf ? 0.0f : cm;
+        const float sum = wave_sum_u(__builtin_amdgcn_exp2f((x - ms) * kLog2e));
+        if (lane == 0) {
+          cmax[g] = cm;
+          csum[g] = sum;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int g = 0; g < GBM; ++g) {
+        if (g >= gn) break;
+        const float cm = cmax[g];
+        const float mn = fmaxf(m_run[g], cm);
+        if (mn == kNegInf) continue;
+        const float sa = __builtin_amdgcn_exp2f((m_run[g] - mn) * kLog2e);
+        const float sb = __builtin_amdgcn_exp2f((cm - mn) * kLog2e);
+        l_run[g] = l_run[g] * sa + csum[g] * sb;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * sa;
+        m_run[g] = mn;
+      }
+#pragma unroll
+      for (int u = 0; u < kRowBatch; ++u) {
+        float v[CH];
         unpack(vr[u], v);
-        row_logits<D, GBM>(q, kv, gn, a.scale, x);
-        st.update(x, v, gn);
+#pragma unroll
+        for (int g = 0; g < GBM; ++g) {
+          if (g >= gn) break;
+          const float ms = m_run[g] == kNegInf ? 0.0f : m_run[g];
+          const float p = __builtin_amdgcn_exp2f((xlog[g][lg + 16 * u] - ms) * kLog2e);
+#pragma unroll
+          for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + p * v[i];
+        }
       }
     }
 
-    // merge the 16 lane groups: within a wave by xor 16/32, then across waves
+    // sum the 16 lane groups (one shared max: plain adds) and write
 #pragma unroll
-    for (int o = 16; o <= 32; o <<= 1) {
-      float om[GBM], ol[GBM], oacc[GBM][CH];
+    for (int g = 0; g < GBM; ++g) {
 #pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        om[g] = shfl_xor(st.m[g], o);
-        ol[g] = shfl_xor(st.l[g], o);
-#pragma unroll
-        for (int i = 0; i < CH; ++i) oacc[g][i] = shfl_xor(st.acc[g][i], o);
-      }
-      st.merge(om, ol, oacc, gn);
-    }
-    __syncthreads();
-    if ((tid & 63) < 16) {
-#pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        if (g < gn) {
-          if (c == 0) {
-            xm[wave][g] = st.m[g];
-            xl[wave][g] = st.l[g];
-          }
-#pragma unroll
-          for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = st.acc[g][i];
-        }
+      for (int i = 0; i < CH; ++i) {
+        acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 16);
+        acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 32);
       }
     }
     __syncthreads();
-    if (tid < 16) {
-      for (int ow = 1; ow < kWaves; ++ow) {
-        float om[GBM], ol[GBM], oacc[GBM][CH];
-#pragma unroll
-        for (int g = 0; g < GBM; ++g) {
-          om[g] = g < gn ? xm[ow][g] : kNegInf;
-          ol[g] = g < gn ? xl[ow][g] : 0.0f;
-#pragma unroll
-          for (int i = 0; i < CH; ++i) oacc[g][i] = g < gn ? xacc[ow][g][c * CH + i] : 0.0f;
-        }
-        st.merge(om, ol, oacc, gn);
-      }
+    if (grp == 0) {
 #pragma unroll
       for (int g = 0; g < GBM; ++g) {
-        if (g < gn) {
-          const int64_t slot = slot0 + (int64_t)g * a.workers;
-          if (c == 0) {
-            a.page_m[slot] = st.m[g];
-            a.page_l[slot] = st.l[g];
-          }
+        if (g >= gn) break;
 #pragma unroll
-          for (int i = 0; i < CH; ++i) a.page_acc[slot * D + c * CH + i] = st.acc[g][i];
-        }
+        for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = acc[g][i];
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < gn * D; idx += kThreads) {
+      const int g = idx / D, d = idx % D;
+      const int64_t slot = (h * G + g0 + g) * a.workers + w;
+      const float sum = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
+      a.page_acc[slot * D + d] = sum;
+      if (d == 0) {
+        a.page_m[slot] = m_run[g];
+        a.page_l[slot] = l_run[g];
       }
     }
   }
@@ -831,12 +831,13 @@ struct MergeArgs {
   const float* lse;       // rep m = inf_to_zero(zm)
   const float* rep_l;
   const float* rep_acc;
+  const int64_t* header;  // page-work cost starts per head (page kernel)
   const float* page_m;
   const float* page_l;
   const float* page_acc;
   uint16_t* out;          // (H*G, D)
   int64_t n_tiles;
-  int workers, dim;
+  int heads, group, workers, dim;
 };
 
 constexpr int kMergeD = 32;                   // output columns per workgroup
@@ -849,18 +850,31 @@ inline size_t merge_smem(int64_t n_tiles, int64_t workers) {
 
 __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
   extern __shared__ unsigned char smem_raw[];
-  const int64_t T = a.n_tiles, W = a.workers, P = T + W;
+  const int64_t T = a.n_tiles, W = a.workers;
   float* pm = reinterpret_cast<float*>(smem_raw);  // [P] partial max (natural log)
-  float* pl = pm + P;                               // [P] partial l (0 if dead)
-  int* live = reinterpret_cast<int*>(pl + P);       // [P] live partial indices, in order
-  __shared__ float red[kWaves];
+  float* pl = pm + (T + W);                         // [P] partial l (0 if dead)
+  int* live = reinterpret_cast<int*>(pl + (T + W)); // [P] live partial indices, in order
   __shared__ uint32_t wave_tot[kWaves];
+  __shared__ float red[kWaves];
   __shared__ float num_s[kMergeK][kMergeD];
   __shared__ float den_s[kMergeK];
   const int64_t r = blockIdx.x;
+  const int64_t h = r / a.group;
   const int d0 = blockIdx.y * kMergeD;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int D = a.dim;
+
+  // workers whose cost range meets head h's (the page kernel's own test):
+  // w_first = ceil(W (hs+1) / C) - 1, w_last = ceil(W he / C) - 1
+  const int64_t hs = a.header[h], he = a.header[h + 1], C = a.header[a.heads];
+  int64_t w_first = 0, w_last = -1;
+  if (C > 0 && he > hs) {
+    w_first = (W * (hs + 1) + C - 1) / C - 1;
+    w_last = (W * he + C - 1) / C - 1;
+    if (w_first < 0) w_first = 0;
+    if (w_last > W - 1) w_last = W - 1;
+  }
+  const int64_t P = T + (w_last - w_first + 1);
 
   float mx = kNegInf;
   for (int64_t i = tid; i < P; i += kThreads) {
@@ -869,15 +883,16 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
       m = inf_to_zero(a.lse[(r * T + i) * 4]);
       l = a.rep_l[r * T + i];
     } else {
-      m = a.page_m[r * W + (i - T)];
-      l = a.page_l[r * W + (i - T)];
+      const int64_t w = w_first + (i - T);
+      m = a.page_m[r * W + w];
+      l = a.page_l[r * W + w];
     }
     const bool alive = l > 0.0f;
     pm[i] = m;
     pl[i] = alive ? l : 0.0f;
     if (alive) mx = fmaxf(mx, m);
   }
-  mx = wave_nanmax(mx);
+  mx = wave_nanmax_u(mx);
   if (lane == 0) red[wave] = mx;
   __syncthreads();
   const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
@@ -907,8 +922,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
     for (int u = 0; u < kBatch; ++u) {
       const int64_t q = q0 + (int64_t)u * kMergeK;
       idx[u] = q < n_live ? live[q] : -1;
-      const int i = idx[u] < 0 ? 0 : idx[u];
-      accv[u] = i < T ? a.rep_acc[(r * T + i) * D + dd] : a.page_acc[(r * W + (i - T)) * D + dd];
+      const int64_t i = idx[u] < 0 ? 0 : idx[u];
+      accv[u] = i < T ? a.rep_acc[(r * T + i) * D + dd]
+                      : a.page_acc[(r * W + w_first + (i - T)) * D + dd];
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
@@ -979,7 +995,7 @@ int validate_select(const SelectParams& p, const char* who, Layout& L) {
     return set_error(kWorkspaceTooSmall, "%s: workspace needs %lld bytes, 256-byte aligned", who,
                      (long long)L.total);
   if (L.n_tiles > 0x7FFFFFFF) return set_error(kInvalidArgument, "%s: too many blocks", who);
-  if (score_smem(p.group, p.dim) > 64 * 1024)
+  if (score_smem(p.group, p.dim, true) > 64 * 1024)
     return set_error(kUnsupported, "%s: group x head_dim too large", who);
   return kOk;
 }
@@ -1001,7 +1017,7 @@ int launch_select(const SelectParams& p, const Layout& L) {
   sa.length = p.length;
   sa.group = (int)p.group;
   sa.scale = (float)pow((double)p.dim, -0.5);
-  const size_t smem = score_smem(p.group, p.dim);
+  const size_t smem = score_smem(p.group, p.dim, reps);
   dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
   mark(0, p.stream);
   if (reps) {
@@ -1076,16 +1092,18 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 }
 
 // Byte offsets of the workspace regions, for tests: z, delta, lse, tilebits,
-// rep_l, rep_acc, page_m, page_l, page_acc, total, then n_tiles and workers.
+// rep_l, rep_acc, header, page_m, page_l, page_acc, total, then n_tiles and
+// workers.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out12) {
+                                    int64_t* out13) {
   clear_error();
-  if (!out12 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out13 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[12] = {L.z,      L.delta,  L.lse,      L.tilebits, L.rep_l,   L.rep_acc,
-                         L.page_m, L.page_l, L.page_acc, L.total,    L.n_tiles, L.workers};
-  for (int i = 0; i < 12; ++i) out12[i] = v[i];
+  const int64_t v[13] = {L.z,        L.delta,  L.lse,    L.tilebits, L.rep_l,
+                         L.rep_acc,  L.header, L.page_m, L.page_l,   L.page_acc,
+                         L.total,    L.n_tiles, L.workers};
+  for (int i = 0; i < 13; ++i) out13[i] = v[i];
   return kOk;
 }
 
@@ -1163,6 +1181,7 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
   pa.value_suffix = static_cast<const uint16_t*>(value_suffix);
   pa.tilebits = at<uint64_t>(workspace, L.tilebits);
   pa.suffix_len_dev = suffix_length;
+  pa.header = at<int64_t>(workspace, L.header);
   pa.page_m = at<float>(workspace, L.page_m);
   pa.page_l = at<float>(workspace, L.page_l);
   pa.page_acc = at<float>(workspace, L.page_acc);
@@ -1191,11 +1210,14 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
   ma.lse = at<float>(workspace, L.lse);
   ma.rep_l = at<float>(workspace, L.rep_l);
   ma.rep_acc = at<float>(workspace, L.rep_acc);
+  ma.header = pa.header;
   ma.page_m = pa.page_m;
   ma.page_l = pa.page_l;
   ma.page_acc = pa.page_acc;
   ma.out = static_cast<uint16_t*>(output);
   ma.n_tiles = L.n_tiles;
+  ma.heads = (int)heads;
+  ma.group = (int)group;
   ma.workers = (int)L.workers;
   ma.dim = (int)dim;
   merge_kernel<<<dim3((unsigned)(heads * group), (unsigned)((dim + kMergeD - 1) / kMergeD)),

@@ -139,8 +139,8 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("z", "delta", "lse", "tilebits", "rep_l", "rep_acc", "page_m", "page_l",
-                "page_acc", "total", "n_tiles", "workers")
+LAYOUT_NAMES = ("z", "delta", "lse", "tilebits", "rep_l", "rep_acc", "header", "page_m",
+                "page_l", "page_acc", "total", "n_tiles", "workers")
 
 
 def workspace_layout(heads, group, dim, n_blocks):

@@ -57,11 +57,12 @@ def test_workspace_size_covers_layout(lib):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
-        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:10]]
+        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:11]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
         rows, tiles = heads * group, layout["n_tiles"]
         assert layout["delta"] - layout["z"] >= rows * n * 4
-        assert layout["page_m"] - layout["rep_acc"] >= rows * tiles * dim * 4
+        assert layout["header"] - layout["rep_acc"] >= rows * tiles * dim * 4
+        assert layout["page_m"] - layout["header"] >= (heads + 1) * 8
         assert layout["total"] - layout["page_acc"] >= rows * layout["workers"] * dim * 4
         assert 1 <= layout["workers"] <= 512
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0
