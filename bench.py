@@ -32,7 +32,8 @@ import torch  # noqa: E402
 
 METRIC = "decode attn µs/step/layer @128K ctx GQA32/8 d128; HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
-KERNELS = ("score", "decide", "pages", "merge")
+# Kernels one rkv_decode call launches, per pipeline.
+KERNELS = {"persistent": ("decode",), "split": ("score", "decide", "pages", "merge")}
 
 
 def log(msg):
@@ -57,6 +58,8 @@ def parse_args():
     ap.add_argument("--no-dense", action="store_true", help="skip the eps=0 dense baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pipeline", choices=("persistent", "split"), default="persistent",
+                    help="rkv_decode pipeline: one persistent kernel, or four kernels")
     ap.add_argument("--graph-only", action="store_true",
                     help="only the graph-replay timing (for profiler runs)")
     return ap.parse_args()
@@ -115,13 +118,13 @@ def make_layer(gen, a, capacity, device):
 
 
 def algorithmic_bytes(a, masks, counts, suffix):
-    """Bytes each kernel must move per layer-step, counted once in the
-    reference's storage formats (the per-step formula of the decode path):
-    score reads key means and ellipsoids of every block and the value means of
-    unexpanded blocks (its representative half); decide reads value norms and
-    writes the mask; pages read the K/V tokens of expanded blocks and the
-    suffix; merge writes the output.  Intermediates (z, delta, partials) are
-    not algorithmic bytes."""
+    """Bytes each phase of the decode kernel must move per layer-step, counted
+    once in the reference's storage formats: score reads key means and
+    ellipsoids of every block and the value means of unexpanded blocks (its
+    representative half); decide reads value norms and writes the mask; pages
+    read the K/V tokens of expanded blocks and the suffix; merge writes the
+    output.  "decode" is their sum (one kernel runs all four phases).
+    Intermediates (z, delta, partials) are not algorithmic bytes."""
     H, G, D = a.heads, a.group, a.dim
     n = counts.numel()
     sel = masks.float().mean(0)  # (H, N) fraction over layers
@@ -132,7 +135,8 @@ def algorithmic_bytes(a, masks, counts, suffix):
     decide = H * n * 4 + H * n
     pages = expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
     merge = H * G * D * 2
-    return dict(score=score, decide=decide, pages=pages, merge=merge)
+    phases = dict(score=score, decide=decide, pages=pages, merge=merge)
+    return dict(phases, decode=sum(phases.values()))
 
 
 def main():
@@ -148,6 +152,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = _hip.lib()
+    _hip.set_decode_pipeline(a.pipeline)
+    kernels = KERNELS[a.pipeline]
     capacity = a.warmup + a.steps + 1
     cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps,
                          gqa_reduction=a.reduction)
@@ -218,22 +224,23 @@ def main():
     counts = layers[0]["summary"].counts
     suffix_now = int(suffix_len.item())
     nbytes = algorithmic_bytes(a, masks, counts, suffix_now)
-    total_bytes = sum(nbytes.values())
+    total_bytes = nbytes["decode"]
 
     # ---- per-kernel durations with HIP events (eager, same stream) ------
-    ev = HipEvents(5 * a.layers)
-    kernel_ms = {k: 0.0 for k in KERNELS}
+    n_ev = len(kernels) + 1
+    ev = HipEvents(n_ev * a.layers)
+    kernel_ms = {k: 0.0 for k in kernels}
     reps = 3
     for _ in range(reps):
         for i, L in enumerate(layers):
-            lib.rkv_set_profile_events(ev.ptr(5 * i))
+            lib.rkv_set_profile_events(ev.ptr(n_ev * i))
             sparse_attention(L["q"], L["summary"], L["k"][:, a.context:], L["v"][:, a.context:],
                              cfg, workspace=L["ws"], suffix_length=suffix_len)
         lib.rkv_set_profile_events(None)
         torch.cuda.synchronize()
         for i in range(a.layers):
-            for j, name in enumerate(KERNELS):
-                kernel_ms[name] += ev.elapsed_ms(5 * i + j, 5 * i + j + 1)
+            for j, name in enumerate(kernels):
+                kernel_ms[name] += ev.elapsed_ms(n_ev * i + j, n_ev * i + j + 1)
     ev.close()
     kernel_us = {k: v * 1e3 / (reps * a.layers) for k, v in kernel_ms.items()}
     dominant = max(kernel_us, key=kernel_us.get)
@@ -281,6 +288,7 @@ def main():
             "context": a.context, "layers": a.layers, "kv_heads": a.heads,
             "q_heads": a.heads * a.group, "head_dim": a.dim, "block_size": a.block,
             "eps": a.eps, "gqa_reduction": a.reduction, "parallelism": "single GPU",
+            "pipeline": a.pipeline,
         },
         "roofline": {
             "bound": "hbm",

@@ -60,14 +60,20 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
                 void* key_mean, void* value_mean, void* ellipsoid, float* value_norm,
                 float* max_value_norm, rkv_stream_t stream);
 
-/* Workspace bytes needed by rkv_select / rkv_decode for this shape. */
+/* Workspace bytes needed by rkv_select / rkv_decode for this shape.  A new
+ * workspace must be zero-filled once before its first rkv_decode (its control
+ * words must start at zero; every call leaves them at zero again). */
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
-/* Byte offsets inside the workspace (for tests): z, delta, lse, tilebits,
- * rep_l, rep_acc, header, page_m, page_l, page_acc, total, then n_tiles and
- * the number of page workers -> out13[0..12]. */
+/* Byte offsets inside the workspace (for tests): control, z, delta, lse,
+ * tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc, total, then
+ * n_tiles, the page items per head and row block (persistent kernel) and the
+ * page workers (split pipeline) -> out15[0..14].  The control block (uint32
+ * words: ticket, exits, error, -, per-head counters) is always at offset 0
+ * with a fixed size; word 2 becomes 1 (and stays 1) if a decode kernel's
+ * dependency wait ever timed out. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out13);
+                         int64_t* out15);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton
@@ -118,10 +124,18 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
                rkv_stream_t stream);
 
 /* Profiling hook with no reference counterpart: when `events` points to 5
- * hipEvent_t, later rkv_select / rkv_decode calls on this thread record
- * events[0] before the first kernel and events[1..4] after the score,
- * decide, pages and merge kernels.  NULL turns it off. */
+ * hipEvent_t handles, later rkv_select / rkv_decode calls on this thread
+ * record events[0] before their first kernel and events[k] after their k-th
+ * (rkv_select: score, decide; rkv_decode: the persistent kernel, or score,
+ * decide, pages, merge on the split pipeline).  NULL turns it off. */
 int rkv_set_profile_events(void* events);
+
+/* Test and benchmark hook with no reference counterpart: which rkv_decode
+ * pipeline runs on this thread.  0 automatic (the persistent kernel where
+ * its resource rules hold: head_dim <= 128, LDS <= 64 KiB per workgroup, no
+ * private-memory traffic; else the split pipeline), 1 persistent kernel only
+ * (RKV_UNSUPPORTED where it cannot run), 2 split pipeline. */
+int rkv_set_decode_pipeline(int mode);
 
 /* Test hook with no reference counterpart: applies the kernels' device
  * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */

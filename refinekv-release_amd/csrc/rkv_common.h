@@ -20,6 +20,15 @@ constexpr float kPosInf = __builtin_inff();
 // Reduction codes of runtime.py:23.
 enum Reduction { kMean = 0, kMax = 1, kAny = 2 };
 
+// threadIdx.x as a value the compiler cannot hoist out of an enclosing loop:
+// in a persistent kernel each work item recomputes its per-thread index math
+// instead of keeping every item kind's hoisted copies live across the loop.
+__device__ __forceinline__ int item_tid() {
+  int t = threadIdx.x;
+  asm volatile("" : "+v"(t));
+  return t;
+}
+
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 __device__ __forceinline__ float shfl(float v, int src) { return __shfl(v, src, kWave); }
 

@@ -1,30 +1,45 @@
 // Decode-step selection and mixed attention (src/refinekv/reference.py:10-73,
 // the semantics the reference's Triton kernels in src/refinekv/kernels/ also
-// follow).  Four kernels per step on the caller's stream; no host sync, no
-// allocation (the caller passes a workspace):
+// follow).  No host sync, no allocation: the caller passes a workspace.
 //
-//   score   grid (tiles, H), one 64-block tile per workgroup.  Streams the
-//           tile's key means, ellipsoids and value means once: s = q.k_mean
-//           and the ellipsoid projection for every query row, z = s + ln n,
-//           delta, the tile's log-sum-exp partials of z and z + log cosh delta,
-//           and the tile's representative-attention accumulator
-//           sum_b exp(z_b - m_tile) v_mean_b over all its blocks (the z
-//           log-sum-exp partial is that attention's (m, l)).
-//   decide  grid (tiles, H).  Merges the tile partials into log Z / log C,
-//           evaluates the risk, the GQA reduction, the non-finite fail-safes
-//           and the anchor union; writes the mask, a 64-bit ballot per tile
-//           and the access counter.  Then removes the expanded blocks from the
-//           tile's representative partial: l is recomputed over the
-//           unexpanded blocks, acc has the expanded blocks' terms subtracted
-//           (its rounding error stays below fp32 eps times the tile's
-//           representative mass, itself at most the exact mass of the step).
-//   pages   grid (workers, row blocks).  Every head's expanded pages and
-//           suffix tokens form one list ordered by head; each worker takes an
-//           equal-cost range of it (a page costs 2*block_size rows, a suffix
-//           token 2), so expansion clustered in a few heads or blocks is
-//           still spread over the whole GPU.  Online softmax per 16-lane group.
-//   merge   grid (rows, head_dim/32).  Combines the live representative and
-//           page partials of each query row in a fixed order.
+// rkv_decode runs ONE persistent kernel per step.  Its workgroups take work
+// items from a ticket counter in the order below; an item waits only for
+// items with smaller tickets (per-head completion counters), so the earliest
+// unfinished item always belongs to a running workgroup and the grid drains
+// whatever the residency.  Per KV head h:
+//
+//   score  (h, tile)   one 64-block tile: streams the tile's key means,
+//                      ellipsoids and value means once; s = q.k_mean and the
+//                      ellipsoid projection for every query row, z = s + ln n,
+//                      delta, the tile's log-sum-exp partials of z and
+//                      z + log cosh delta, and the representative accumulator
+//                      sum_b exp(z_b - m_tile) v_mean_b over all its blocks
+//                      (the z partial is that attention's (m, l)).
+//   decide (h, tile)   after every score item of h: log Z / log C of each
+//                      row from the tile partials, the risk, the GQA
+//                      reduction, the non-finite fail-safes and the anchor
+//                      union; the mask, a 64-bit ballot per tile and the
+//                      access counter; then the tile's representative
+//                      partial without its expanded blocks (l recomputed over
+//                      the unexpanded blocks, acc minus the expanded blocks'
+//                      terms: rounding error below fp32 eps times the tile's
+//                      representative mass).
+//   pages  (h, rows, k) after every decide item of h: the head's expanded
+//                      pages and suffix tokens split into equal-cost ranges (a
+//                      page costs 2 * block_size, a suffix token 2); item k
+//                      also absorbs the representative partials of a 1/P
+//                      share of the head's tiles.  Exact softmax over 64-row
+//                      chunks with one shared max per chunk.
+//   merge  (h, g, cols) after every page item of h: the P partials of row g
+//                      -> bf16 output columns.
+//
+// The last workgroup to leave returns the counters to zero, so a workspace
+// that was zero-filled once stays ready for the next call.  The persistent
+// kernel runs where its resource rules hold (head_dim <= 128, LDS per
+// workgroup <= 64 KiB, no private-memory traffic); other shapes run the split
+// pipeline: score and decide as two kernels, then a page kernel over global
+// equal-cost ranges of every head's expanded pages and a merge kernel.
+// rkv_select runs the score and decide kernels only.
 //
 // Scores, radii and log-sum-exp follow fixed fp32 orders shared with the CPU
 // oracle (oracle/rkv_oracle.c), so masks and selection statistics are
@@ -39,28 +54,42 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr int kMaxHeadTiles = 8192;  // page-kernel LDS prefix capacity (heads * tiles)
+constexpr int64_t kMaxTiles = 2048;    // tiles per head in the decode kernel (LDS page index)
+constexpr int64_t kMaxHeads = 4096;    // KV heads in the decode kernel (control block)
+constexpr int64_t kMaxPageItems = 64;  // page items per (head, row block)
+constexpr int64_t kMaxHeadTiles = 8192;  // split page kernel: heads * tiles in LDS
+constexpr int64_t kMaxFusedDim = 128;    // widest head_dim the persistent kernel runs
+constexpr size_t kMaxFusedLds = 64 * 1024;  // its LDS per workgroup (static + dynamic)
+constexpr size_t kMaxFusedPrivate = 64;     // its private bytes per lane (no spill traffic)
+constexpr int64_t kControlWords = 4 + 3 * kMaxHeads;  // ticket, exits, error, -, 3 x H counters
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a dependency wait gives up (~1 s)
 
-// Optional profiling events (rkv_set_profile_events): recorded on the launch
-// stream before score and after score, decide, pages and merge.
+// Optional profiling events (rkv_set_profile_events): events[0] is recorded
+// before the first kernel of a call and events[k] after its k-th kernel.
 thread_local hipEvent_t* g_events = nullptr;
 
 inline void mark(int i, hipStream_t stream) {
   if (g_events) (void)hipEventRecord(g_events[i], stream);
 }
 
+// Decode pipeline choice (rkv_set_decode_pipeline): 0 automatic, 1 the
+// persistent kernel, 2 the four-kernel split pipeline.
+thread_local int g_pipeline = 0;
+
 // ---------------------------------------------------------------------------
-// Workspace layout
+// Workspace layout.  The control block comes first and has a fixed size, so
+// its words are at the same place for every shape that shares a workspace.
 // ---------------------------------------------------------------------------
 struct Layout {
-  int64_t n_tiles, workers, rows_per_block, row_blocks;
-  int64_t z, delta, lse, tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc, total;
+  int64_t n_tiles, page_items, workers, rows_per_block, row_blocks;
+  int64_t control, z, delta, lse, tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc,
+      total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-// Rows of the GQA group one page workgroup carries in registers: the next
-// power of two >= group (at least 4), capped so that rows * head_dim / 16
+// Rows of the GQA group one page item carries in registers: the next power
+// of two >= group (at least 4), capped so that rows * head_dim / 16
 // (per-lane accumulators) stays <= 64.
 inline int64_t rows_per_block(int64_t group, int64_t dim) {
   const int64_t ch = dim / 16;
@@ -72,7 +101,7 @@ inline int64_t rows_per_block(int64_t group, int64_t dim) {
   return want < p ? want : p;
 }
 
-// One page worker per 64 (head, block) pairs, 1..512.
+// Split pipeline: one page worker per 64 (head, block) pairs, 1..512.
 inline int64_t workers_for(int64_t heads, int64_t n_blocks) {
   int64_t w = (heads * n_blocks + 63) / 64;
   if (w < 1) w = 1;
@@ -80,19 +109,33 @@ inline int64_t workers_for(int64_t heads, int64_t n_blocks) {
   return w;
 }
 
+// Page items per (head, row block): about 512 in all, at most one per tile
+// and at most kMaxPageItems.
+inline int64_t page_items_for(int64_t heads, int64_t row_blocks, int64_t n_tiles) {
+  int64_t p = (512 + heads * row_blocks - 1) / (heads * row_blocks);
+  if (p > n_tiles) p = n_tiles;
+  if (p > kMaxPageItems) p = kMaxPageItems;
+  return p < 1 ? 1 : p;
+}
+
 Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) {
   Layout L{};
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
-  L.workers = workers_for(heads, n_blocks);
   L.rows_per_block = rows_per_block(group, dim);
   L.row_blocks = (group + L.rows_per_block - 1) / L.rows_per_block;
+  L.page_items = page_items_for(heads, L.row_blocks, L.n_tiles);
+  L.workers = workers_for(heads, n_blocks);
   const int64_t rows = heads * group;
+  // page partials: (rows, page_items) for the persistent kernel, (rows,
+  // workers) for the split pipeline
+  const int64_t slots = L.page_items > L.workers ? L.page_items : L.workers;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = off;
     off = align256(off + bytes);
     return at;
   };
+  L.control = take(kControlWords * 4);
   L.z = take(rows * n_blocks * 4);
   L.delta = take(rows * n_blocks * 4);
   L.lse = take(rows * L.n_tiles * 4 * 4);
@@ -100,9 +143,9 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.rep_l = take(rows * L.n_tiles * 4);
   L.rep_acc = take(rows * L.n_tiles * dim * 4);
   L.header = take((heads + 1) * 8);
-  L.page_m = take(rows * L.workers * 4);
-  L.page_l = take(rows * L.workers * 4);
-  L.page_acc = take(rows * L.workers * dim * 4);
+  L.page_m = take(rows * slots * 4);
+  L.page_l = take(rows * slots * 4);
+  L.page_acc = take(rows * slots * dim * 4);
   L.total = off;
   return L;
 }
@@ -172,7 +215,7 @@ __device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* w
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 1: scores (+ representative accumulators)
+// Phase 1: scores (+ representative accumulators) of one (head, tile)
 // ---------------------------------------------------------------------------
 struct ScoreArgs {
   const uint16_t* query;       // (H, G, D) bf16
@@ -194,9 +237,10 @@ inline size_t score_smem(int64_t group, int64_t dim, bool reps) {
 }
 
 template <int D, bool REPS>
-__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
+__device__ __forceinline__ void score_tile(const ScoreArgs& a, int64_t h, int64_t tile,
+                                          unsigned char* dyn) {
   constexpr int CH = D / 16;
-  extern __shared__ float smem[];
+  float* smem = reinterpret_cast<float*>(dyn);
   const int G = a.group;
   float* qs = smem;                 // [G][D] bf16(q)
   float* q2s = qs + G * D;          // [G][D] bf16(q^2)
@@ -207,9 +251,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   float* pbuf = zcbuf + G * kTile;  // [G][64] exp(z - m_tile)
   uint32_t* vsm = reinterpret_cast<uint32_t*>(pbuf + G * kTile);  // [64][D/2] value means
 
-  const int64_t h = blockIdx.y;
-  const int64_t tile = blockIdx.x;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = item_tid(), wave = tid / kWave, lane = tid % kWave;
   const int grp = lane / 16, c = lane % 16;
   const int64_t N = a.n_blocks;
 
@@ -345,7 +387,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 2: decisions (+ representative corrections)
+// Phase 2: decisions (+ representative corrections) of one (head, tile)
 // ---------------------------------------------------------------------------
 struct DecideArgs {
   const float* z;
@@ -375,31 +417,38 @@ constexpr int kLseRegs = 4;  // tile partials per lane held in registers (tiles 
 __device__ __forceinline__ float merge_lse(const float (&m)[kLseRegs], const float (&l)[kLseRegs],
                                            const float* part, int which, int64_t n_tiles,
                                            int lane) {
+  // (register part unrolled, then the rest from memory: same order as one
+  // loop over t, without indexing the register arrays at run time)
+  constexpr int64_t kRegTiles = (int64_t)kLseRegs * kWave;
   float mx = kNegInf;
-  for (int64_t t = lane, k = 0; t < n_tiles; t += kWave, ++k)
-    mx = nanmax(mx, k < kLseRegs ? m[k] : part[t * 4 + 2 * which]);
+#pragma unroll
+  for (int k = 0; k < kLseRegs; ++k)
+    if (lane + (int64_t)k * kWave < n_tiles) mx = nanmax(mx, m[k]);
+  for (int64_t t = lane + kRegTiles; t < n_tiles; t += kWave)
+    mx = nanmax(mx, part[t * 4 + 2 * which]);
   mx = wave_nanmax_u(mx);
   const float ms = inf_to_zero(mx);
   float acc = 0.0f;
-  for (int64_t t = lane, k = 0; t < n_tiles; t += kWave, ++k) {
-    const float mt = k < kLseRegs ? m[k] : part[t * 4 + 2 * which];
-    const float lt = k < kLseRegs ? l[k] : part[t * 4 + 2 * which + 1];
-    const float term = lt * expf_(mt - ms);
-    acc = k == 0 ? term : acc + term;
+#pragma unroll
+  for (int k = 0; k < kLseRegs; ++k) {
+    if (lane + (int64_t)k * kWave < n_tiles) {
+      const float term = l[k] * expf_(m[k] - ms);
+      acc = k == 0 ? term : acc + term;
+    }
   }
+  for (int64_t t = lane + kRegTiles; t < n_tiles; t += kWave)
+    acc = acc + part[t * 4 + 2 * which + 1] * expf_(part[t * 4 + 2 * which] - ms);
   return logf_(wave_sum_u(acc)) + ms;
 }
 
 constexpr int kRiskPerThread = kMaxGroup * kTile / kThreads;  // (row, block) pairs per thread
 
-__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
+__device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int64_t tile) {
   __shared__ float gstat[kMaxGroup][2];
   __shared__ float risk_s[kMaxGroup][kTile];
   __shared__ float psel[kMaxGroup][kTile];
   __shared__ uint64_t sel_bits;
-  const int64_t h = blockIdx.y;
-  const int64_t tile = blockIdx.x;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = item_tid(), wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
   const int64_t nvalid = N - tile * kTile >= kTile ? kTile : N - tile * kTile;
@@ -571,8 +620,18 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
   }
 }
 
+template <int D, bool REPS>
+__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
+  extern __shared__ unsigned char score_dyn[];
+  score_tile<D, REPS>(a, blockIdx.y, blockIdx.x, score_dyn);
+}
+
+__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
+  decide_tile(a, blockIdx.y, blockIdx.x);
+}
+
 // ---------------------------------------------------------------------------
-// Kernel 3: expanded pages and suffix tokens
+// Phase 3: expanded pages, suffix tokens and representative partials
 // ---------------------------------------------------------------------------
 struct PageArgs {
   const uint16_t* query;       // (H, G, D) bf16
@@ -582,13 +641,15 @@ struct PageArgs {
   const uint16_t* value_suffix;
   const uint64_t* tilebits;    // (H, tiles)
   const int32_t* suffix_len_dev;  // or null
-  int64_t* header;             // (H + 1): cost start of each head's work, [H] = total
-  float* page_m;               // (H*G, W), written only by workers touching the head
+  const float* lse;            // (H, G, tiles, 4): representative m = inf_to_zero(zm)
+  const float* rep_l;          // (H, G, tiles)
+  const float* rep_acc;        // (H, G, tiles, D)
+  float* page_m;               // (H, G, P)
   float* page_l;
-  float* page_acc;             // (H*G, W, D)
+  float* page_acc;             // (H, G, P, D)
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
   int64_t suffix_cap, n_blocks, n_tiles, block, length;
-  int heads, group, workers, rows_per_block;
+  int group, page_items;
   float scale;
 };
 
@@ -610,13 +671,359 @@ __device__ __forceinline__ void row_logits(const float (&q)[GBM][D / 16], const 
   }
 }
 
-inline size_t page_smem(int64_t heads, int64_t n_tiles) {
+// CH consecutive floats (CH even; 16-byte aligned when CH % 4 == 0, else 8).
+template <int CH>
+__device__ __forceinline__ void load_f32(const float* p, float (&out)[CH]) {
+  if constexpr (CH % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < CH / 4; ++j) {
+      const float4 v = reinterpret_cast<const float4*>(p)[j];
+      out[4 * j] = v.x;
+      out[4 * j + 1] = v.y;
+      out[4 * j + 2] = v.z;
+      out[4 * j + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < CH / 2; ++j) {
+      const float2 v = reinterpret_cast<const float2*>(p)[j];
+      out[2 * j] = v.x;
+      out[2 * j + 1] = v.y;
+    }
+  }
+}
+
+// LDS of a page item: the head's tile ballots, their prefix and a page list.
+inline int64_t page_smem(int64_t n_tiles) {
+  return align256(n_tiles * 8) + align256((n_tiles + 1) * 4) + 8 * 8;
+}
+
+template <int D, int GBM>
+__device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, int k,
+                                          unsigned char* dyn) {
+  constexpr int CH = D / 16;
+  const int64_t T = a.n_tiles;
+  uint64_t* bits_s = reinterpret_cast<uint64_t*>(dyn);                    // [T]
+  uint32_t* pre = reinterpret_cast<uint32_t*>(dyn + align256(T * 8));     // [T + 1]
+  int64_t* list = reinterpret_cast<int64_t*>(dyn + align256(T * 8) + align256((T + 1) * 4));
+  __shared__ uint32_t wave_tot[kWaves];
+  __shared__ float xlog[GBM][kChunkRows];
+  __shared__ float cmax[GBM], csum[GBM];
+  __shared__ float xacc[kWaves][GBM][D];
+
+  const int G = a.group, P = a.page_items;
+  const int g0 = rb * GBM;
+  const int gn = min(GBM, G - g0);
+  const int tid = item_tid(), lg = tid >> 4, c = tid & 15, wave = tid / kWave;
+  const int lane = tid % kWave, grp = lane >> 4;
+  const int64_t N = a.n_blocks, B = a.block;
+
+  // ---- the head's expanded pages: ballots and their prefix --------------
+  const int64_t per = (T + kThreads - 1) / kThreads;
+  const int64_t t_begin = min((int64_t)tid * per, T), t_end = min(t_begin + per, T);
+  uint32_t mine = 0;
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    const uint64_t b = a.tilebits[h * T + t];
+    bits_s[t] = b;
+    mine += (uint32_t)__popcll(b);
+  }
+  uint32_t n_h;
+  uint32_t run = block_exclusive_scan(mine, wave_tot, n_h);
+  for (int64_t t = t_begin; t < t_end; ++t) {
+    pre[t] = run;
+    run += (uint32_t)__popcll(bits_s[t]);
+  }
+  if (tid == 0) pre[T] = n_h;
+
+  // ---- this item's equal-cost range of pages and suffix tokens ----------
+  int64_t S = a.suffix_cap;
+  if (a.suffix_len_dev) {
+    const int64_t s = *a.suffix_len_dev;
+    S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
+  }
+  const int64_t pc = 2 * B;  // cost of one page; a suffix token costs 2
+  const int64_t C = pc * (int64_t)n_h + 2 * S;
+  const int64_t lo = C * k / P, hi = C * (k + 1) / P;
+  auto clampi = [](int64_t x, int64_t l, int64_t u) { return x < l ? l : (x > u ? u : x); };
+  auto ceil_div = [](int64_t x, int64_t d) { return x <= 0 ? 0 : (x + d - 1) / d; };
+  const int64_t p0 = clampi(ceil_div(lo, pc), 0, n_h), p1 = clampi(ceil_div(hi, pc), 0, n_h);
+  const int64_t s0 = clampi(ceil_div(lo - pc * n_h, 2), 0, S);
+  const int64_t s1 = clampi(ceil_div(hi - pc * n_h, 2), 0, S);
+  const int64_t n_prow = (p1 - p0) * B, n_rows = n_prow + (s1 - s0);
+
+  float q[GBM][CH];
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+    const int gg = g < gn ? g : 0;
+    RawBf16<CH> r = load_raw<CH>(a.query + ((h * G + g0 + gg) * D + c * CH));
+    unpack(r, q[g]);
+  }
+
+  // ---- start from the representative partials of tiles [r0, r1) ---------
+  // (m, l, acc) of each live tile, rescaled to their common max; lane group 0
+  // holds the accumulator, the other groups start at zero.
+  const int64_t r0 = T * k / P, r1 = T * (k + 1) / P;
+  float m_run[GBM], l_run[GBM], acc[GBM][CH];
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+    m_run[g] = kNegInf;
+    l_run[g] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
+    if (g >= gn) continue;
+    const int64_t row = h * G + g0 + g;
+    float mr = kNegInf;
+    for (int64_t t = r0; t < r1; ++t) {
+      const float lt = a.rep_l[row * T + t];
+      const float mt = inf_to_zero(a.lse[(row * T + t) * 4]);
+      if (lt > 0.0f) mr = fmaxf(mr, mt);
+    }
+    if (mr == kNegInf) continue;
+    float l = 0.0f;
+    for (int64_t t = r0; t < r1; ++t) {
+      const float lt = a.rep_l[row * T + t];
+      const float mt = inf_to_zero(a.lse[(row * T + t) * 4]);
+      float at[CH];
+      load_f32<CH>(a.rep_acc + (row * T + t) * D + c * CH, at);
+      if (lt > 0.0f) {
+        const float e = __builtin_amdgcn_exp2f((mt - mr) * kLog2e);
+        l = l + lt * e;
+        if (lg == 0) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + at[i] * e;
+        }
+      }
+    }
+    m_run[g] = mr;
+    l_run[g] = l;
+  }
+
+  // Rows in chunks of 64: pass 1 loads K/V and writes the chunk's logits,
+  // pass 2 weighs the V rows with one shared max (no per-row rescaling).
+  for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
+    // pages touched by this chunk -> block indices (block_size divides 64)
+    const int64_t j_first = c0 < n_prow ? p0 + c0 / B : p1;
+    const int64_t j_last = min(c0 + kChunkRows, n_prow) - 1;
+    const int64_t n_pages = c0 < n_prow ? p0 + j_last / B - j_first + 1 : 0;
+    __syncthreads();
+    if (tid < n_pages) {
+      const int64_t j = j_first + tid;
+      int64_t lo_t = 0, hi_t = T - 1;
+      while (lo_t < hi_t) {
+        const int64_t mid = (lo_t + hi_t + 1) >> 1;
+        if ((int64_t)pre[mid] <= j) lo_t = mid; else hi_t = mid - 1;
+      }
+      list[tid] = lo_t * kTile + nth_set_bit(bits_s[lo_t], (int)(j - pre[lo_t]));
+    }
+    __syncthreads();
+    RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
+    bool ok[kRowBatch];
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      const int64_t v = c0 + lg + 16 * u;
+      const uint16_t* kp = a.key_pages + h * a.kp_hs;  // a valid row for idle lanes
+      const uint16_t* vp = a.value_pages + h * a.vp_hs;
+      ok[u] = false;
+      if (v < n_prow) {
+        const int64_t jj = v / B, t = v - jj * B;
+        const int64_t b = list[p0 + jj - j_first];
+        if (t < block_count(b, N, B, a.length)) {
+          ok[u] = true;
+          kp += (b * B + t) * D;
+          vp += (b * B + t) * D;
+        }
+      } else if (v < n_rows) {
+        const int64_t kk = s0 + (v - n_prow);
+        ok[u] = true;
+        kp = a.key_suffix + h * a.ks_hs + kk * a.ks_ts;
+        vp = a.value_suffix + h * a.vs_hs + kk * a.vs_ts;
+      }
+      kr[u] = load_raw<CH>(kp + c * CH);
+      vr[u] = load_raw<CH>(vp + c * CH);
+    }
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      float kv[CH], x[GBM];
+      unpack(kr[u], kv);
+      row_logits<D, GBM>(q, kv, x);
+      if (c == 15) {
+#pragma unroll
+        for (int g = 0; g < GBM; ++g) xlog[g][lg + 16 * u] = ok[u] ? x[g] * a.scale : kNegInf;
+      }
+    }
+    __syncthreads();
+    // chunk max and sum per query row, one wave per row
+    for (int g = wave; g < gn; g += kWaves) {
+      const float x = xlog[g][lane];
+      const float cm = wave_nanmax_u(x);
+      const float ms = cm == kNegInf ? 0.0f : cm;
+      const float sum = wave_sum_u(__builtin_amdgcn_exp2f((x - ms) * kLog2e));
+      if (lane == 0) {
+        cmax[g] = cm;
+        csum[g] = sum;
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      if (g >= gn) break;
+      const float cm = cmax[g];
+      const float mn = fmaxf(m_run[g], cm);
+      if (mn == kNegInf) continue;
+      const float sa = __builtin_amdgcn_exp2f((m_run[g] - mn) * kLog2e);
+      const float sb = __builtin_amdgcn_exp2f((cm - mn) * kLog2e);
+      l_run[g] = l_run[g] * sa + csum[g] * sb;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * sa;
+      m_run[g] = mn;
+    }
+#pragma unroll
+    for (int u = 0; u < kRowBatch; ++u) {
+      float v[CH];
+      unpack(vr[u], v);
+#pragma unroll
+      for (int g = 0; g < GBM; ++g) {
+        if (g >= gn) break;
+        const float ms = m_run[g] == kNegInf ? 0.0f : m_run[g];
+        const float p = __builtin_amdgcn_exp2f((xlog[g][lg + 16 * u] - ms) * kLog2e);
+#pragma unroll
+        for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + p * v[i];
+      }
+    }
+  }
+
+  // sum the 16 lane groups (one shared max: plain adds) and write
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+#pragma unroll
+    for (int i = 0; i < CH; ++i) {
+      acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 16);
+      acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 32);
+    }
+  }
+  __syncthreads();
+  if (grp == 0) {
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      if (g >= gn) break;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = acc[g][i];
+    }
+  }
+  __syncthreads();
+  for (int idx = tid; idx < gn * D; idx += kThreads) {
+    const int g = idx / D, d = idx % D;
+    const int64_t slot = (h * G + g0 + g) * P + k;
+    const float sum = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
+    a.page_acc[slot * D + d] = sum;
+    if (d == 0) {
+      a.page_m[slot] = m_run[g];
+      a.page_l[slot] = l_run[g];
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Phase 4: merge a row's page-item partials -> bf16 output columns
+// ---------------------------------------------------------------------------
+struct MergeArgs {
+  const float* page_m;    // (H, G, P)
+  const float* page_l;
+  const float* page_acc;  // (H, G, P, D)
+  uint16_t* out;          // (H*G, D)
+  int group, page_items, dim;
+};
+
+constexpr int kMergeD = 32;                   // output columns per item
+constexpr int kMergeK = kThreads / kMergeD;   // partial stripes
+constexpr int kMergeBatch = 8;                // partials per stripe per batch
+
+__device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g, int dc) {
+  __shared__ float red[kWaves];
+  __shared__ float num_s[kMergeK][kMergeD];
+  __shared__ float den_s[kMergeK];
+  const int P = a.page_items, D = a.dim;
+  const int64_t r = h * a.group + g;
+  const int tid = item_tid(), lane = tid % kWave, wave = tid / kWave;
+
+  float mx = kNegInf;
+  for (int i = tid; i < P; i += kThreads) {
+    const float l = a.page_l[r * P + i];
+    const float m = a.page_m[r * P + i];
+    if (l > 0.0f) mx = fmaxf(mx, m);
+  }
+  mx = wave_nanmax_u(mx);
+  if (lane == 0) red[wave] = mx;
+  __syncthreads();
+  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float Ms = M == kNegInf ? 0.0f : M;
+
+  const int dl = tid % kMergeD, kk = tid / kMergeD;
+  const int d = dc * kMergeD + dl;
+  const int dd = d < D ? d : 0;
+  float num = 0.0f, den = 0.0f;
+  for (int i0 = kk; i0 < P; i0 += kMergeK * kMergeBatch) {
+    float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      const int i = i0 + u * kMergeK;
+      const int ii = i < P ? i : 0;
+      mv[u] = a.page_m[r * P + ii];
+      lv[u] = a.page_l[r * P + ii];
+      av[u] = a.page_acc[(r * P + ii) * D + dd];
+    }
+#pragma unroll
+    for (int u = 0; u < kMergeBatch; ++u) {
+      if (i0 + u * kMergeK < P && lv[u] > 0.0f) {
+        const float e = __builtin_amdgcn_exp2f((mv[u] - Ms) * kLog2e);
+        den = den + lv[u] * e;
+        num = num + av[u] * e;
+      }
+    }
+  }
+  num_s[kk][dl] = num;
+  if (dl == 0) den_s[kk] = den;
+  __syncthreads();
+  if (tid < kMergeD && d < D) {
+    float n = num_s[0][tid], den_all = den_s[0];
+    for (int j = 1; j < kMergeK; ++j) {
+      n = n + num_s[j][tid];
+      den_all = den_all + den_s[j];
+    }
+    a.out[r * D + d] = bf16_rne(n / fmaxf(den_all, 1e-30f));
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Split pipeline, kernel 3: expanded pages and suffix tokens
+// ---------------------------------------------------------------------------
+struct SplitPageArgs {
+  const uint16_t* query;       // (H, G, D) bf16
+  const uint16_t* key_pages;   // head h at key_pages + h * kp_hs; rows (N*B, D)
+  const uint16_t* value_pages;
+  const uint16_t* key_suffix;  // token t of head h at h * ks_hs + t * ks_ts
+  const uint16_t* value_suffix;
+  const uint64_t* tilebits;    // (H, tiles)
+  const int32_t* suffix_len_dev;  // or null
+  int64_t* header;             // (H + 1): cost start of each head's work, [H] = total
+  float* page_m;               // (H*G, W), written only by workers touching the head
+  float* page_l;
+  float* page_acc;             // (H*G, W, D)
+  int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
+  int64_t suffix_cap, n_blocks, n_tiles, block, length;
+  int heads, group, workers, rows_per_block;
+  float scale;
+};
+
+
+
+inline size_t split_page_smem(int64_t heads, int64_t n_tiles) {
   return (size_t)(align256((heads * n_tiles + 1) * 4) + align256((heads + 1) * 8) +
                   sizeof(int64_t) * 8);
 }
 
 template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
+__global__ __launch_bounds__(kThreads) void split_page_kernel(SplitPageArgs a) {
   constexpr int CH = D / 16;
   extern __shared__ unsigned char smem_raw[];
   const int64_t T = a.n_tiles, H = a.heads, HT = H * T;
@@ -632,7 +1039,7 @@ __global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
   const int g0 = blockIdx.y * a.rows_per_block;
   const int gn = min(a.rows_per_block, a.group - g0);
   const int G = a.group;
-  const int tid = threadIdx.x, lg = tid >> 4, c = tid & 15, wave = tid / kWave;
+  const int tid = item_tid(), lg = tid >> 4, c = tid & 15, wave = tid / kWave;
   const int lane = tid % kWave, grp = lane >> 4;
   const int64_t N = a.n_blocks, B = a.block;
 
@@ -825,9 +1232,9 @@ __global__ __launch_bounds__(kThreads) void page_kernel(PageArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// Kernel 4: merge representative and page partials -> bf16 output
+// Split pipeline, kernel 4: merge representative and page partials -> bf16 output
 // ---------------------------------------------------------------------------
-struct MergeArgs {
+struct SplitMergeArgs {
   const float* lse;       // rep m = inf_to_zero(zm)
   const float* rep_l;
   const float* rep_acc;
@@ -840,15 +1247,13 @@ struct MergeArgs {
   int heads, group, workers, dim;
 };
 
-constexpr int kMergeD = 32;                   // output columns per workgroup
-constexpr int kMergeK = kThreads / kMergeD;   // partial-list stripes
 
-inline size_t merge_smem(int64_t n_tiles, int64_t workers) {
+inline size_t split_merge_smem(int64_t n_tiles, int64_t workers) {
   const int64_t P = n_tiles + workers;
   return sizeof(float) * 2 * P + sizeof(int) * P;
 }
 
-__global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
+__global__ __launch_bounds__(kThreads) void split_merge_kernel(SplitMergeArgs a) {
   extern __shared__ unsigned char smem_raw[];
   const int64_t T = a.n_tiles, W = a.workers;
   float* pm = reinterpret_cast<float*>(smem_raw);  // [P] partial max (natural log)
@@ -861,7 +1266,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
   const int64_t r = blockIdx.x;
   const int64_t h = r / a.group;
   const int d0 = blockIdx.y * kMergeD;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int tid = item_tid(), lane = tid % kWave, wave = tid / kWave;
   const int D = a.dim;
 
   // workers whose cost range meets head h's (the page kernel's own test):
@@ -947,6 +1352,131 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
   }
 }
 
+
+// ---------------------------------------------------------------------------
+// The persistent decode kernel
+// ---------------------------------------------------------------------------
+struct DecodeArgs {
+  ScoreArgs score;
+  DecideArgs decide;
+  PageArgs page;
+  MergeArgs merge;
+  uint32_t* control;  // [0] ticket, [1] exits, [2] error (sticky), then 3 x kMaxHeads counters
+  uint32_t n_score, n_decide, n_page, n_merge;
+  int heads, row_blocks, merge_cols;
+};
+
+// Thread 0 polls a completion counter until it reaches target (bounded: on
+// timeout the sticky error word is set and the item goes on), then the
+// workgroup acquires what the counted items wrote.
+__device__ __forceinline__ void wait_count(const uint32_t* cnt, uint32_t target, uint32_t* err) {
+  if (threadIdx.x == 0) {
+    uint32_t spins = 0;
+    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+      if (++spins > kSpinLimit) {
+        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        break;
+      }
+      __builtin_amdgcn_s_sleep(4);
+    }
+  }
+  __syncthreads();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+}
+
+// Every thread releases its writes, then thread 0 counts the item done.
+__device__ __forceinline__ void signal_done(uint32_t* cnt) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// The kernel's arguments re-read from the kernarg segment for each item:
+// the item kinds' fields are not kept live (in SGPRs) across the item loop.
+typedef __attribute__((address_space(4))) const DecodeArgs KernelArgs;
+__device__ __forceinline__ const DecodeArgs* item_args() {
+  KernelArgs* p = (KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+  asm volatile("" : "+s"(p));
+  return (const DecodeArgs*)p;
+}
+
+// Two workgroups per CU (<= 256 registers per lane): every phase fits in
+// registers without spilling.
+template <int D, int GBM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void decode_kernel(DecodeArgs a) {
+  extern __shared__ unsigned char decode_dyn[];
+  __shared__ uint32_t s_item;
+  __shared__ uint32_t s_last;
+  uint32_t* ctl = a.control;
+  uint32_t* score_done = ctl + 4;
+  uint32_t* decide_done = score_done + kMaxHeads;
+  uint32_t* page_done = decide_done + kMaxHeads;
+  const uint32_t T = (uint32_t)a.score.n_tiles;
+  const uint32_t e_score = a.n_score, e_decide = e_score + a.n_decide;
+  const uint32_t e_page = e_decide + a.n_page, e_all = e_page + a.n_merge;
+  const uint32_t P = (uint32_t)a.page.page_items;
+  const uint32_t page_per_head = (uint32_t)a.row_blocks * P;
+  const uint32_t merge_per_head = (uint32_t)a.merge.group * (uint32_t)a.merge_cols;
+  const int tid = threadIdx.x;
+
+  if (tid == 0) s_item = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  uint32_t item = s_item;
+  while (item < e_all) {
+    // claim the next item now; its ticket is larger than this one's
+    uint32_t next = 0;
+    if (tid == 0) next = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (item < e_score) {
+      const uint32_t h = item / T, t = item % T;
+      const ScoreArgs sa = item_args()->score;
+      score_tile<D, true>(sa, h, t, decode_dyn);
+      signal_done(score_done + h);
+    } else if (item < e_decide) {
+      const uint32_t i = item - e_score, h = i / T, t = i % T;
+      wait_count(score_done + h, T, ctl + 2);
+      const DecideArgs da = item_args()->decide;
+      decide_tile(da, h, t);
+      signal_done(decide_done + h);
+    } else if (item < e_page) {
+      const uint32_t i = item - e_decide, h = i / page_per_head, r = i % page_per_head;
+      wait_count(decide_done + h, T, ctl + 2);
+      const PageArgs pa = item_args()->page;
+      page_item<D, GBM>(pa, h, (int)(r / P), (int)(r % P), decode_dyn);
+      signal_done(page_done + h);
+    } else {
+      const uint32_t i = item - e_page, h = i / merge_per_head, r = i % merge_per_head;
+      wait_count(page_done + h, page_per_head, ctl + 2);
+      const MergeArgs ma = item_args()->merge;
+      merge_item(ma, h, (int)(r / a.merge_cols), (int)(r % a.merge_cols));
+    }
+    __syncthreads();
+    if (tid == 0) s_item = next;
+    __syncthreads();
+    item = s_item;
+  }
+
+  // The last workgroup out returns the ticket, exit and head counters to 0
+  // (every other workgroup has made its last access to them by then).
+  if (tid == 0) {
+    const uint32_t out =
+        __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = out == gridDim.x - 1 ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s_last) {
+    for (int i = tid; i < a.heads; i += kThreads) {
+      __hip_atomic_store(score_done + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(decide_done + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(page_done + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (tid == 0) {
+      __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
@@ -1000,8 +1530,7 @@ int validate_select(const SelectParams& p, const char* who, Layout& L) {
   return kOk;
 }
 
-int launch_select(const SelectParams& p, const Layout& L) {
-  const bool reps = p.value_mean != nullptr;
+ScoreArgs score_args(const SelectParams& p, const Layout& L) {
   ScoreArgs sa;
   sa.query = static_cast<const uint16_t*>(p.query);
   sa.key_mean = static_cast<const uint16_t*>(p.key_mean);
@@ -1017,24 +1546,15 @@ int launch_select(const SelectParams& p, const Layout& L) {
   sa.length = p.length;
   sa.group = (int)p.group;
   sa.scale = (float)pow((double)p.dim, -0.5);
-  const size_t smem = score_smem(p.group, p.dim, reps);
-  dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
-  mark(0, p.stream);
-  if (reps) {
-    RKV_DISPATCH_DIM(p.dim, D,
-                     score_kernel<D, true><<<grid, dim3(kThreads), smem, p.stream>>>(sa));
-  } else {
-    RKV_DISPATCH_DIM(p.dim, D,
-                     score_kernel<D, false><<<grid, dim3(kThreads), smem, p.stream>>>(sa));
-  }
-  int rc = check_launch("score_kernel");
-  if (rc) return rc;
-  mark(1, p.stream);
+  return sa;
+}
 
+DecideArgs decide_args(const SelectParams& p, const Layout& L) {
+  const bool reps = p.value_mean != nullptr;
   DecideArgs da;
-  da.z = sa.z;
-  da.delta = sa.delta;
-  da.lse = sa.lse;
+  da.z = at<float>(p.ws, L.z);
+  da.delta = at<float>(p.ws, L.delta);
+  da.lse = at<float>(p.ws, L.lse);
   da.value_norm = p.value_norm;
   da.max_value_norm = p.max_value_norm;
   da.value_mean = static_cast<const uint16_t*>(p.value_mean);
@@ -1054,30 +1574,266 @@ int launch_select(const SelectParams& p, const Layout& L) {
   da.reduction = p.reduction;
   da.dim = (int)p.dim;
   da.eps = p.eps;
+  return da;
+}
+
+// Selection only (rkv_select): score and decide as two kernels.
+int launch_select(const SelectParams& p, const Layout& L) {
+  const ScoreArgs sa = score_args(p, L);
+  const DecideArgs da = decide_args(p, L);
+  const size_t smem = score_smem(p.group, p.dim, false);
+  dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
+  mark(0, p.stream);
+  RKV_DISPATCH_DIM(p.dim, D,
+                   score_kernel<D, false><<<grid, dim3(kThreads), smem, p.stream>>>(sa));
+  int rc = check_launch("score_kernel");
+  if (rc) return rc;
+  mark(1, p.stream);
   decide_kernel<<<grid, dim3(kThreads), 0, p.stream>>>(da);
   rc = check_launch("decide_kernel");
   mark(2, p.stream);
   return rc;
 }
 
+// Grid of the persistent kernel: as many workgroups as the device holds at
+// once (more would only wait for a slot), never more than there are items.
+struct GridCache {
+  const void* fn;
+  int device;
+  size_t dyn;
+  int per_cu, cus;
+  size_t static_lds, private_bytes;
+};
+
+constexpr int kNotEligible = -1;  // internal: use the split pipeline
+
+// Launches the persistent kernel, or returns kNotEligible when this build of
+// it does not meet the persistent kernel's resource rules (LDS per
+// workgroup, no private memory traffic): its workgroups wait on each other,
+// so each must run with everything it needs from its first instruction.
+template <int D, int GBM>
+int launch_decode(const DecodeArgs& da, size_t dyn, uint32_t items, hipStream_t stream) {
+  const void* fn = reinterpret_cast<const void*>(&decode_kernel<D, GBM>);
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess)
+    return set_error(kLaunchFailed, "rkv_decode: no current device");
+  thread_local GridCache cache[16] = {};
+  thread_local int cache_next = 0;
+  GridCache* hit = nullptr;
+  for (GridCache& e : cache)
+    if (e.fn == fn && e.device == device && e.dyn == dyn) hit = &e;
+  if (!hit) {
+    GridCache e{fn, device, dyn, 0, 0, 0, 0};
+    hipFuncAttributes attr;
+    if (hipFuncGetAttributes(&attr, fn) != hipSuccess ||
+        hipDeviceGetAttribute(&e.cus, hipDeviceAttributeMultiprocessorCount, device) !=
+            hipSuccess)
+      return set_error(kLaunchFailed, "rkv_decode: cannot query the device");
+    e.static_lds = attr.sharedSizeBytes;
+    e.private_bytes = attr.localSizeBytes;
+    if (e.static_lds + dyn <= kMaxFusedLds &&
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&e.per_cu, decode_kernel<D, GBM>, kThreads,
+                                                     dyn) != hipSuccess)
+      return set_error(kLaunchFailed, "rkv_decode: occupancy query failed");
+    hit = &cache[cache_next];
+    cache_next = (cache_next + 1) % 16;
+    *hit = e;
+  }
+  if (hit->static_lds + dyn > kMaxFusedLds || hit->private_bytes > kMaxFusedPrivate ||
+      hit->per_cu < 1)
+    return kNotEligible;
+  const int64_t slots = (int64_t)hit->per_cu * hit->cus;
+  const unsigned grid = (unsigned)(slots < (int64_t)items ? slots : (int64_t)items);
+  decode_kernel<D, GBM><<<dim3(grid), dim3(kThreads), dyn, stream>>>(da);
+  return check_launch("decode_kernel");
+}
+
 template <int D>
-int launch_pages(const PageArgs& pa, const Layout& L, hipStream_t stream) {
-  const size_t smem = page_smem(pa.heads, L.n_tiles);
+int launch_decode_rows(const DecodeArgs& da, int64_t rows_per_block, size_t dyn, uint32_t items,
+                       hipStream_t stream) {
+  if constexpr (D > kMaxFusedDim) {
+    return kNotEligible;
+  } else {
+    constexpr int CH = D / 16;
+    constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
+    switch (rows_per_block) {
+      case 4:
+        return launch_decode<D, 4>(da, dyn, items, stream);
+      case 8:
+        if constexpr (CAP >= 8) return launch_decode<D, 8>(da, dyn, items, stream);
+        break;
+      default:
+        if constexpr (CAP >= 16) return launch_decode<D, 16>(da, dyn, items, stream);
+        break;
+    }
+    return kNotEligible;
+  }
+}
+
+template <int D>
+int launch_split_pages(const SplitPageArgs& pa, const Layout& L, hipStream_t stream) {
+  const size_t smem = split_page_smem(pa.heads, L.n_tiles);
   dim3 grid((unsigned)L.workers, (unsigned)L.row_blocks);
   constexpr int CH = D / 16;
   constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
   switch (L.rows_per_block) {
     case 4:
-      page_kernel<D, 4><<<grid, dim3(kThreads), smem, stream>>>(pa);
+      split_page_kernel<D, 4><<<grid, dim3(kThreads), smem, stream>>>(pa);
       break;
     case 8:
-      if constexpr (CAP >= 8) page_kernel<D, 8><<<grid, dim3(kThreads), smem, stream>>>(pa);
+      if constexpr (CAP >= 8) split_page_kernel<D, 8><<<grid, dim3(kThreads), smem, stream>>>(pa);
       break;
     default:
-      if constexpr (CAP >= 16) page_kernel<D, 16><<<grid, dim3(kThreads), smem, stream>>>(pa);
+      if constexpr (CAP >= 16)
+        split_page_kernel<D, 16><<<grid, dim3(kThreads), smem, stream>>>(pa);
       break;
   }
-  return check_launch("page_kernel");
+  return check_launch("split_page_kernel");
+}
+
+struct DecodeBuffers {
+  const void* key_pages;
+  int64_t kp_hs;
+  const void* value_pages;
+  int64_t vp_hs;
+  const void* key_suffix;
+  int64_t ks_hs, ks_ts;
+  const void* value_suffix;
+  int64_t vs_hs, vs_ts;
+  int64_t suffix_cap;
+  const int32_t* suffix_len;
+  void* output;
+};
+
+// The split pipeline: score and decide kernels, then the page kernel (global
+// equal-cost ranges over every head's expanded pages) and the merge kernel.
+int launch_split(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  const ScoreArgs sa = score_args(p, L);
+  const DecideArgs da = decide_args(p, L);
+  dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
+  mark(0, p.stream);
+  RKV_DISPATCH_DIM(p.dim, D,
+                   score_kernel<D, true><<<grid, dim3(kThreads), score_smem(p.group, p.dim, true),
+                                           p.stream>>>(sa));
+  int rc = check_launch("score_kernel");
+  if (rc) return rc;
+  mark(1, p.stream);
+  decide_kernel<<<grid, dim3(kThreads), 0, p.stream>>>(da);
+  rc = check_launch("decide_kernel");
+  if (rc) return rc;
+  mark(2, p.stream);
+
+  SplitPageArgs pa;
+  pa.query = static_cast<const uint16_t*>(p.query);
+  pa.key_pages = static_cast<const uint16_t*>(b.key_pages);
+  pa.value_pages = static_cast<const uint16_t*>(b.value_pages);
+  pa.key_suffix = static_cast<const uint16_t*>(b.key_suffix);
+  pa.value_suffix = static_cast<const uint16_t*>(b.value_suffix);
+  pa.tilebits = at<uint64_t>(p.ws, L.tilebits);
+  pa.suffix_len_dev = b.suffix_len;
+  pa.header = at<int64_t>(p.ws, L.header);
+  pa.page_m = at<float>(p.ws, L.page_m);
+  pa.page_l = at<float>(p.ws, L.page_l);
+  pa.page_acc = at<float>(p.ws, L.page_acc);
+  pa.kp_hs = b.kp_hs;
+  pa.vp_hs = b.vp_hs;
+  pa.ks_hs = b.ks_hs;
+  pa.ks_ts = b.ks_ts;
+  pa.vs_hs = b.vs_hs;
+  pa.vs_ts = b.vs_ts;
+  pa.suffix_cap = b.suffix_cap;
+  pa.n_blocks = p.n_blocks;
+  pa.n_tiles = L.n_tiles;
+  pa.block = p.block;
+  pa.length = p.length;
+  pa.heads = (int)p.heads;
+  pa.group = (int)p.group;
+  pa.workers = (int)L.workers;
+  pa.rows_per_block = (int)L.rows_per_block;
+  pa.scale = (float)pow((double)p.dim, -0.5);
+  rc = kOk;
+  RKV_DISPATCH_DIM(p.dim, D, rc = launch_split_pages<D>(pa, L, p.stream));
+  if (rc) return rc;
+  mark(3, p.stream);
+
+  SplitMergeArgs ma;
+  ma.lse = at<float>(p.ws, L.lse);
+  ma.rep_l = at<float>(p.ws, L.rep_l);
+  ma.rep_acc = at<float>(p.ws, L.rep_acc);
+  ma.header = pa.header;
+  ma.page_m = pa.page_m;
+  ma.page_l = pa.page_l;
+  ma.page_acc = pa.page_acc;
+  ma.out = static_cast<uint16_t*>(b.output);
+  ma.n_tiles = L.n_tiles;
+  ma.heads = (int)p.heads;
+  ma.group = (int)p.group;
+  ma.workers = (int)L.workers;
+  ma.dim = (int)p.dim;
+  split_merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
+                       dim3(kThreads), split_merge_smem(L.n_tiles, L.workers), p.stream>>>(ma);
+  rc = check_launch("split_merge_kernel");
+  mark(4, p.stream);
+  return rc;
+}
+
+// The persistent kernel, or kNotEligible.
+int launch_fused(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  if (p.dim > kMaxFusedDim || p.heads > kMaxHeads || L.n_tiles > kMaxTiles) return kNotEligible;
+  DecodeArgs da;
+  da.score = score_args(p, L);
+  da.decide = decide_args(p, L);
+  PageArgs& pa = da.page;
+  pa.query = static_cast<const uint16_t*>(p.query);
+  pa.key_pages = static_cast<const uint16_t*>(b.key_pages);
+  pa.value_pages = static_cast<const uint16_t*>(b.value_pages);
+  pa.key_suffix = static_cast<const uint16_t*>(b.key_suffix);
+  pa.value_suffix = static_cast<const uint16_t*>(b.value_suffix);
+  pa.tilebits = at<uint64_t>(p.ws, L.tilebits);
+  pa.suffix_len_dev = b.suffix_len;
+  pa.lse = at<float>(p.ws, L.lse);
+  pa.rep_l = at<float>(p.ws, L.rep_l);
+  pa.rep_acc = at<float>(p.ws, L.rep_acc);
+  pa.page_m = at<float>(p.ws, L.page_m);
+  pa.page_l = at<float>(p.ws, L.page_l);
+  pa.page_acc = at<float>(p.ws, L.page_acc);
+  pa.kp_hs = b.kp_hs;
+  pa.vp_hs = b.vp_hs;
+  pa.ks_hs = b.ks_hs;
+  pa.ks_ts = b.ks_ts;
+  pa.vs_hs = b.vs_hs;
+  pa.vs_ts = b.vs_ts;
+  pa.suffix_cap = b.suffix_cap;
+  pa.n_blocks = p.n_blocks;
+  pa.n_tiles = L.n_tiles;
+  pa.block = p.block;
+  pa.length = p.length;
+  pa.group = (int)p.group;
+  pa.page_items = (int)L.page_items;
+  pa.scale = (float)pow((double)p.dim, -0.5);
+  MergeArgs& ma = da.merge;
+  ma.page_m = pa.page_m;
+  ma.page_l = pa.page_l;
+  ma.page_acc = pa.page_acc;
+  ma.out = static_cast<uint16_t*>(b.output);
+  ma.group = (int)p.group;
+  ma.page_items = (int)L.page_items;
+  ma.dim = (int)p.dim;
+  da.control = at<uint32_t>(p.ws, L.control);
+  da.heads = (int)p.heads;
+  da.row_blocks = (int)L.row_blocks;
+  da.merge_cols = (int)((p.dim + kMergeD - 1) / kMergeD);
+  da.n_score = (uint32_t)(p.heads * L.n_tiles);
+  da.n_decide = da.n_score;
+  da.n_page = (uint32_t)(p.heads * L.row_blocks * L.page_items);
+  da.n_merge = (uint32_t)(p.heads * p.group * da.merge_cols);
+  const uint32_t items = da.n_score + da.n_decide + da.n_page + da.n_merge;
+  const int64_t dyn_score = (int64_t)score_smem(p.group, p.dim, true);
+  const int64_t dyn_page = page_smem(L.n_tiles);
+  const size_t dyn = (size_t)(dyn_score > dyn_page ? dyn_score : dyn_page);
+  int rc = kNotEligible;
+  RKV_DISPATCH_DIM(p.dim, D, rc = launch_decode_rows<D>(da, L.rows_per_block, dyn, items, p.stream));
+  return rc;
 }
 
 }  // namespace
@@ -1091,19 +1847,20 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
   return (size_t)make_layout(heads, group, dim, n_blocks).total;
 }
 
-// Byte offsets of the workspace regions, for tests: z, delta, lse, tilebits,
-// rep_l, rep_acc, header, page_m, page_l, page_acc, total, then n_tiles and
-// workers.
+// Byte offsets of the workspace regions, for tests: control, z, delta, lse,
+// tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc, total, then
+// n_tiles, the page items per head and row block (persistent kernel) and the
+// page workers (split pipeline).
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out13) {
+                                    int64_t* out15) {
   clear_error();
-  if (!out13 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out15 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[13] = {L.z,        L.delta,  L.lse,    L.tilebits, L.rep_l,
-                         L.rep_acc,  L.header, L.page_m, L.page_l,   L.page_acc,
-                         L.total,    L.n_tiles, L.workers};
-  for (int i = 0; i < 13; ++i) out13[i] = v[i];
+  const int64_t v[15] = {L.control, L.z,       L.delta,   L.lse,       L.tilebits,
+                         L.rep_l,   L.rep_acc, L.header,  L.page_m,    L.page_l,
+                         L.page_acc, L.total,  L.n_tiles, L.page_items, L.workers};
+  for (int i = 0; i < 15; ++i) out15[i] = v[i];
   return kOk;
 }
 
@@ -1152,9 +1909,6 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
     return set_error(kInvalidArgument, "rkv_decode: negative suffix capacity");
   if (suffix_capacity > 0 && (!key_suffix || !value_suffix))
     return set_error(kInvalidArgument, "rkv_decode: null suffix with nonzero capacity");
-  if (heads * L.n_tiles > kMaxHeadTiles)
-    return set_error(kUnsupported, "rkv_decode: heads x tiles %lld exceeds %d",
-                     (long long)(heads * L.n_tiles), kMaxHeadTiles);
   const int64_t es = 2;
   const int64_t ch_bytes = dim / 16 * es;
   const uintptr_t need = ch_bytes % 16 == 0 ? 16 : (ch_bytes % 8 == 0 ? 8 : 4);
@@ -1168,70 +1922,45 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
     return set_error(kInvalidArgument, "rkv_decode: suffix rows must be %d-byte aligned",
                      (int)need);
   if (!aligned(output, 4)) return set_error(kInvalidArgument, "rkv_decode: output alignment");
-  const size_t msmem = merge_smem(L.n_tiles, L.workers);
-  if (msmem > 64 * 1024) return set_error(kUnsupported, "rkv_decode: too many partials");
-  rc = launch_select(p, L);
-  if (rc) return rc;
 
-  PageArgs pa;
-  pa.query = static_cast<const uint16_t*>(query);
-  pa.key_pages = static_cast<const uint16_t*>(key_pages);
-  pa.value_pages = static_cast<const uint16_t*>(value_pages);
-  pa.key_suffix = static_cast<const uint16_t*>(key_suffix);
-  pa.value_suffix = static_cast<const uint16_t*>(value_suffix);
-  pa.tilebits = at<uint64_t>(workspace, L.tilebits);
-  pa.suffix_len_dev = suffix_length;
-  pa.header = at<int64_t>(workspace, L.header);
-  pa.page_m = at<float>(workspace, L.page_m);
-  pa.page_l = at<float>(workspace, L.page_l);
-  pa.page_acc = at<float>(workspace, L.page_acc);
-  pa.kp_hs = key_page_head_stride;
-  pa.vp_hs = value_page_head_stride;
-  pa.ks_hs = key_suffix_head_stride;
-  pa.ks_ts = key_suffix_token_stride;
-  pa.vs_hs = value_suffix_head_stride;
-  pa.vs_ts = value_suffix_token_stride;
-  pa.suffix_cap = suffix_capacity;
-  pa.n_blocks = n_blocks;
-  pa.n_tiles = L.n_tiles;
-  pa.block = block_size;
-  pa.length = prompt_length;
-  pa.heads = (int)heads;
-  pa.group = (int)group;
-  pa.workers = (int)L.workers;
-  pa.rows_per_block = (int)L.rows_per_block;
-  pa.scale = (float)pow((double)dim, -0.5);
-  rc = kOk;
-  RKV_DISPATCH_DIM(dim, D, rc = launch_pages<D>(pa, L, stream));
-  if (rc) return rc;
-  mark(3, stream);
-
-  MergeArgs ma;
-  ma.lse = at<float>(workspace, L.lse);
-  ma.rep_l = at<float>(workspace, L.rep_l);
-  ma.rep_acc = at<float>(workspace, L.rep_acc);
-  ma.header = pa.header;
-  ma.page_m = pa.page_m;
-  ma.page_l = pa.page_l;
-  ma.page_acc = pa.page_acc;
-  ma.out = static_cast<uint16_t*>(output);
-  ma.n_tiles = L.n_tiles;
-  ma.heads = (int)heads;
-  ma.group = (int)group;
-  ma.workers = (int)L.workers;
-  ma.dim = (int)dim;
-  merge_kernel<<<dim3((unsigned)(heads * group), (unsigned)((dim + kMergeD - 1) / kMergeD)),
-                 dim3(kThreads), msmem, stream>>>(ma);
-  rc = check_launch("merge_kernel");
-  mark(4, stream);
-  return rc;
+  const DecodeBuffers b{key_pages,     key_page_head_stride,   value_pages,
+                        value_page_head_stride,  key_suffix,   key_suffix_head_stride,
+                        key_suffix_token_stride, value_suffix, value_suffix_head_stride,
+                        value_suffix_token_stride, suffix_capacity, suffix_length, output};
+  if (g_pipeline != 2) {
+    mark(0, stream);
+    rc = launch_fused(p, L, b);
+    if (rc != kNotEligible) {
+      if (rc == kOk) mark(1, stream);
+      return rc;
+    }
+    if (g_pipeline == 1)
+      return set_error(kUnsupported, "rkv_decode: the persistent kernel does not run this shape");
+  }
+  if (heads * L.n_tiles > kMaxHeadTiles)
+    return set_error(kUnsupported, "rkv_decode: heads x tiles %lld exceeds %lld",
+                     (long long)(heads * L.n_tiles), (long long)kMaxHeadTiles);
+  if (split_merge_smem(L.n_tiles, L.workers) > 64 * 1024)
+    return set_error(kUnsupported, "rkv_decode: too many partials");
+  return launch_split(p, L, b);
 }
 
-// Profiling hook: when events is non-null (an array of 5 hipEvent_t), the
-// following rkv_select / rkv_decode calls on this thread record events[0]
-// before the score kernel and events[1..4] after score, decide, pages and
-// merge.  Pass NULL to stop.
+// Profiling hook: when events is non-null, the following rkv_select /
+// rkv_decode calls on this thread record events[0] before their first kernel
+// and events[k] after their k-th (rkv_select: score, decide; rkv_decode: the
+// persistent kernel, or score, decide, pages, merge on the split pipeline).
+// Pass NULL to stop.
 extern "C" int rkv_set_profile_events(void* events) {
   g_events = static_cast<hipEvent_t*>(events);
+  return kOk;
+}
+
+// Test and benchmark hook: 0 automatic (the persistent kernel where its
+// resource rules hold, else the split pipeline), 1 persistent kernel only
+// (RKV_UNSUPPORTED where it cannot run), 2 split pipeline.  Per thread.
+extern "C" int rkv_set_decode_pipeline(int mode) {
+  clear_error();
+  if (mode < 0 || mode > 2) return set_error(kInvalidArgument, "rkv_set_decode_pipeline: mode");
+  g_pipeline = mode;
   return kOk;
 }

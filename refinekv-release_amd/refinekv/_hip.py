@@ -55,6 +55,8 @@ def _bind(lib):
     lib.rkv_math_probe.restype = _int
     lib.rkv_set_profile_events.argtypes = [_p]
     lib.rkv_set_profile_events.restype = _int
+    lib.rkv_set_decode_pipeline.argtypes = [_int]
+    lib.rkv_set_decode_pipeline.restype = _int
     return lib
 
 
@@ -139,8 +141,9 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("z", "delta", "lse", "tilebits", "rep_l", "rep_acc", "header", "page_m",
-                "page_l", "page_acc", "total", "n_tiles", "workers")
+LAYOUT_NAMES = ("control", "z", "delta", "lse", "tilebits", "rep_l", "rep_acc", "header",
+                "page_m", "page_l", "page_acc", "total", "n_tiles", "page_items", "workers")
+CONTROL_ERROR_WORD = 2  # sticky flag: a decode kernel's dependency wait timed out
 
 
 def workspace_layout(heads, group, dim, n_blocks):
@@ -150,21 +153,24 @@ def workspace_layout(heads, group, dim, n_blocks):
     return dict(zip(LAYOUT_NAMES, list(out)))
 
 
-def _buffer(workspace, name, shape, device, dtype):
+def _buffer(workspace, name, shape, device, dtype, zero=False):
     """Reusable tensor keyed by name (the reference's workspace dict,
-    src/refinekv/kernels/runtime.py:26-37)."""
+    src/refinekv/kernels/runtime.py:26-37); zero-filled when first made if
+    `zero`."""
     tensor = workspace.get(name) if workspace is not None else None
     if (tensor is None or tuple(tensor.shape) != tuple(shape) or tensor.device != device
             or tensor.dtype != dtype):
-        tensor = torch.empty(shape, device=device, dtype=dtype)
+        tensor = (torch.zeros if zero else torch.empty)(shape, device=device, dtype=dtype)
         if workspace is not None:
             workspace[name] = tensor
     return tensor
 
 
 def _scratch(workspace, heads, group, dim, n_blocks, device):
+    """The kernels' workspace.  Zero-filled once when made: rkv_decode's
+    control words start at zero and every call leaves them at zero."""
     nbytes = workspace_bytes(heads, group, dim, n_blocks)
-    return _buffer(workspace, "hip_scratch", (nbytes,), device, torch.uint8)
+    return _buffer(workspace, "hip_scratch", (nbytes,), device, torch.uint8, zero=True)
 
 
 # ---------------------------------------------------------------------------
@@ -242,3 +248,12 @@ def math_probe(fn, x):
     _check(lib().rkv_math_probe(code, _ptr(x), _ptr(y), x.numel(), _stream(x.device)),
            "rkv_math_probe")
     return y
+
+
+PIPELINES = {"auto": 0, "persistent": 1, "split": 2}
+
+
+def set_decode_pipeline(name):
+    """Which rkv_decode pipeline runs on this thread ("auto", "persistent",
+    "split"); a test and benchmark hook."""
+    _check(lib().rkv_set_decode_pipeline(PIPELINES[name]), "rkv_set_decode_pipeline")

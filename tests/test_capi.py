@@ -47,11 +47,14 @@ def test_version_and_error_channel(lib):
     assert lib.rkv_version() >= 1
     assert lib.rkv_workspace_layout(0, 0, 0, 0, None) == 1
     assert b"bad arguments" in lib.rkv_last_error()
+    assert lib.rkv_set_decode_pipeline(3) == 1
+    assert lib.rkv_set_decode_pipeline(0) == 0 and lib.rkv_last_error() == b""
 
 
 def test_workspace_size_covers_layout(lib):
     from refinekv import _hip
 
+    controls = _hip.workspace_layout(1, 1, 32, 1)["z"]
     for heads, group, dim, n in ((8, 4, 128, 4096), (4, 7, 128, 1024), (2, 16, 64, 3),
                                  (1, 1, 256, 1)):
         layout = _hip.workspace_layout(heads, group, dim, n)
@@ -60,9 +63,14 @@ def test_workspace_size_covers_layout(lib):
         regions = [layout[k] for k in _hip.LAYOUT_NAMES[:11]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
         rows, tiles = heads * group, layout["n_tiles"]
+        # fixed-size control block first, so every shape finds it at offset 0
+        assert layout["control"] == 0 and layout["z"] == controls
         assert layout["delta"] - layout["z"] >= rows * n * 4
         assert layout["header"] - layout["rep_acc"] >= rows * tiles * dim * 4
         assert layout["page_m"] - layout["header"] >= (heads + 1) * 8
-        assert layout["total"] - layout["page_acc"] >= rows * layout["workers"] * dim * 4
+        slots = max(layout["page_items"], layout["workers"])
+        assert layout["page_l"] - layout["page_m"] >= rows * slots * 4
+        assert layout["total"] - layout["page_acc"] >= rows * slots * dim * 4
+        assert 1 <= layout["page_items"] <= min(64, tiles)
         assert 1 <= layout["workers"] <= 512
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0
