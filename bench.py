@@ -58,8 +58,9 @@ def parse_args():
     ap.add_argument("--no-dense", action="store_true", help="skip the eps=0 dense baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--pipeline", choices=("persistent", "split"), default="persistent",
-                    help="rkv_decode pipeline: one persistent kernel, or four kernels")
+    ap.add_argument("--pipeline", choices=("persistent", "split"), default="split",
+                    help="rkv_decode pipeline: four kernels (the default), or one persistent "
+                         "kernel")
     ap.add_argument("--graph-only", action="store_true",
                     help="only the graph-replay timing (for profiler runs)")
     return ap.parse_args()

@@ -131,10 +131,11 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
 int rkv_set_profile_events(void* events);
 
 /* Test and benchmark hook with no reference counterpart: which rkv_decode
- * pipeline runs on this thread.  0 automatic (the persistent kernel where
- * its resource rules hold: head_dim <= 128, LDS <= 64 KiB per workgroup, no
- * private-memory traffic; else the split pipeline), 1 persistent kernel only
- * (RKV_UNSUPPORTED where it cannot run), 2 split pipeline. */
+ * pipeline runs on this thread.  0 automatic (= 2), 1 the persistent kernel
+ * (one launch; head_dim <= 128, LDS <= 64 KiB per workgroup, no
+ * private-memory traffic, else RKV_UNSUPPORTED), 2 the split pipeline
+ * (score, decide, pages, merge kernels), 3 the persistent kernel where it
+ * runs, else the split pipeline. */
 int rkv_set_decode_pipeline(int mode);
 
 /* Test hook with no reference counterpart: applies the kernels' device

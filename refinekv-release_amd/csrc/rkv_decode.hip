@@ -34,12 +34,17 @@
 //                      -> bf16 output columns.
 //
 // The last workgroup to leave returns the counters to zero, so a workspace
-// that was zero-filled once stays ready for the next call.  The persistent
-// kernel runs where its resource rules hold (head_dim <= 128, LDS per
-// workgroup <= 64 KiB, no private-memory traffic); other shapes run the split
-// pipeline: score and decide as two kernels, then a page kernel over global
-// equal-cost ranges of every head's expanded pages and a merge kernel.
-// rkv_select runs the score and decide kernels only.
+// that was zero-filled once stays ready for the next call.  It runs on
+// request (rkv_set_decode_pipeline) where its resource rules hold (head_dim
+// <= 128, LDS per workgroup <= 64 KiB, no private-memory traffic): on a
+// multi-XCD device every cross-workgroup hand-off pays a device-scope L2
+// write-back and a same-address ticket atomic, which makes it slower than
+// kernel boundaries for this workload today.
+//
+// The default is the split pipeline: the score and decide phases as two
+// kernels, then a page kernel over global equal-cost ranges of every head's
+// expanded pages and a merge kernel.  rkv_select runs the score and decide
+// kernels only.
 //
 // Scores, radii and log-sum-exp follow fixed fp32 orders shared with the CPU
 // oracle (oracle/rkv_oracle.c), so masks and selection statistics are
@@ -72,8 +77,9 @@ inline void mark(int i, hipStream_t stream) {
   if (g_events) (void)hipEventRecord(g_events[i], stream);
 }
 
-// Decode pipeline choice (rkv_set_decode_pipeline): 0 automatic, 1 the
-// persistent kernel, 2 the four-kernel split pipeline.
+// Decode pipeline choice (rkv_set_decode_pipeline): 0 automatic (the split
+// pipeline), 1 the persistent kernel, 2 the split pipeline, 3 the persistent
+// kernel where it runs, else the split pipeline.
 thread_local int g_pipeline = 0;
 
 // ---------------------------------------------------------------------------
@@ -1927,7 +1933,7 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
                         value_page_head_stride,  key_suffix,   key_suffix_head_stride,
                         key_suffix_token_stride, value_suffix, value_suffix_head_stride,
                         value_suffix_token_stride, suffix_capacity, suffix_length, output};
-  if (g_pipeline != 2) {
+  if (g_pipeline == 1 || g_pipeline == 3) {
     mark(0, stream);
     rc = launch_fused(p, L, b);
     if (rc != kNotEligible) {
@@ -1955,12 +1961,12 @@ extern "C" int rkv_set_profile_events(void* events) {
   return kOk;
 }
 
-// Test and benchmark hook: 0 automatic (the persistent kernel where its
-// resource rules hold, else the split pipeline), 1 persistent kernel only
-// (RKV_UNSUPPORTED where it cannot run), 2 split pipeline.  Per thread.
+// Test and benchmark hook: 0 automatic (the split pipeline), 1 persistent
+// kernel (RKV_UNSUPPORTED where it cannot run), 2 split pipeline, 3 the
+// persistent kernel where it runs, else the split pipeline.  Per thread.
 extern "C" int rkv_set_decode_pipeline(int mode) {
   clear_error();
-  if (mode < 0 || mode > 2) return set_error(kInvalidArgument, "rkv_set_decode_pipeline: mode");
+  if (mode < 0 || mode > 3) return set_error(kInvalidArgument, "rkv_set_decode_pipeline: mode");
   g_pipeline = mode;
   return kOk;
 }

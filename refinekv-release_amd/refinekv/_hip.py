@@ -250,10 +250,11 @@ def math_probe(fn, x):
     return y
 
 
-PIPELINES = {"auto": 0, "persistent": 1, "split": 2}
+PIPELINES = {"auto": 0, "persistent": 1, "split": 2, "prefer_persistent": 3}
 
 
 def set_decode_pipeline(name):
-    """Which rkv_decode pipeline runs on this thread ("auto", "persistent",
-    "split"); a test and benchmark hook."""
+    """Which rkv_decode pipeline runs on this thread: "auto" (the split
+    pipeline), "persistent", "split", or "prefer_persistent" (the persistent
+    kernel where it runs, else split); a test and benchmark hook."""
     _check(lib().rkv_set_decode_pipeline(PIPELINES[name]), "rkv_set_decode_pipeline")

@@ -47,7 +47,7 @@ def test_version_and_error_channel(lib):
     assert lib.rkv_version() >= 1
     assert lib.rkv_workspace_layout(0, 0, 0, 0, None) == 1
     assert b"bad arguments" in lib.rkv_last_error()
-    assert lib.rkv_set_decode_pipeline(3) == 1
+    assert lib.rkv_set_decode_pipeline(4) == 1
     assert lib.rkv_set_decode_pipeline(0) == 0 and lib.rkv_last_error() == b""
 
 

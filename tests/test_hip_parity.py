@@ -210,10 +210,10 @@ DECODE_CASES = [
 ]
 
 
-@pytest.fixture(params=["auto", "split"])
+@pytest.fixture(params=["split", "prefer_persistent"])
 def pipeline(request, hip):
-    """Each decode test on the automatic pipeline (the persistent kernel
-    where it runs) and on the split pipeline."""
+    """Each decode test on the split pipeline (the default) and on the
+    persistent kernel where it runs (else the split pipeline again)."""
     hip.set_decode_pipeline(request.param)
     yield request.param
     hip.set_decode_pipeline("auto")
