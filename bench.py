@@ -61,6 +61,9 @@ def parse_args():
     ap.add_argument("--pipeline", choices=("persistent", "split"), default="split",
                     help="rkv_decode pipeline: four kernels (the default), or one persistent "
                          "kernel")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="only copy a 64 MiB buffer 5 times (scales rocprofv3 FETCH_SIZE / "
+                         "WRITE_SIZE readings to bytes)")
     ap.add_argument("--graph-only", action="store_true",
                     help="only the graph-replay timing (for profiler runs)")
     return ap.parse_args()
@@ -147,6 +150,9 @@ def main():
               "(the path would shard by KV head with no exchange; see DESIGN.md)",
               file=sys.stderr)
         sys.exit(2)
+    if a.copy_calibration:
+        copy_calibration()
+        return
     from refinekv import RefineKVConfig, build_summary, sparse_attention, _hip
 
     assert torch.cuda.is_available(), "bench.py needs a GPU"
@@ -312,6 +318,18 @@ def main():
         "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
     }
     print(json.dumps(result), flush=True)
+
+
+def copy_calibration():
+    """A plain device copy of known size: its FETCH_SIZE / WRITE_SIZE counter
+    readings per byte convert the decode kernels' readings to bytes."""
+    n = 64 << 20
+    src = torch.ones(n, dtype=torch.uint8, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "copies": 5}))
 
 
 def cpu_baseline(a, layer, suffix):

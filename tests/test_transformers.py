@@ -1,0 +1,250 @@
+"""The Transformers adapter (reference tests/test_transformers.py, restated).
+
+CPU tests use tiny random-init Llama / Qwen2 models and the torch backend;
+the GPU tests (marked gpu) run the same models in bf16 with backend="hip":
+dynamic and static caches give the same tokens, and graph-replayed decode
+gives the eager tokens.
+"""
+
+import pytest
+import torch
+
+transformers = pytest.importorskip("transformers")
+from refinekv import RefineKV, RefineKVConfig, make_visible_static_cache  # noqa: E402
+
+
+def tiny_model(family="llama", device="cpu"):
+    torch.manual_seed(9)
+    config_cls, model_cls = {
+        "llama": (transformers.LlamaConfig, transformers.LlamaForCausalLM),
+        "qwen2": (transformers.Qwen2Config, transformers.Qwen2ForCausalLM),
+    }[family]
+    config = config_cls(vocab_size=64, hidden_size=128, intermediate_size=256,
+                        num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                        pad_token_id=0, eos_token_id=None)
+    model = model_cls(config).eval().to(device)
+    return model.to(torch.bfloat16) if device == "cuda" else model
+
+
+def generate(model, length=39, static=False, **extra):
+    ids = torch.arange(length, device=model.device)[None] % 61 + 3
+    options = {"cache_implementation": "static"} if static else {}
+    options.update(extra)
+    return model.generate(input_ids=ids, attention_mask=torch.ones_like(ids), max_new_tokens=4,
+                          do_sample=False, **options)
+
+
+def assert_released(model, session, implementation, hooks):
+    assert model.config._attn_implementation == implementation
+    assert hooks == (len(model._forward_pre_hooks), len(model._forward_hooks))
+    assert not session._layers
+    assert not hasattr(model, "_refinekv_session")
+    assert all(not hasattr(m.self_attn, "_refinekv_session") for m in model.model.layers)
+    assert "generate" not in model.__dict__
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen2"])
+@pytest.mark.parametrize("static", [False, True])
+def test_generation_with_anchors_and_request_reset(family, static):
+    model = tiny_model(family)
+    implementation = model.config._attn_implementation
+    hooks = len(model._forward_pre_hooks), len(model._forward_hooks)
+    config = RefineKVConfig(backend="torch", anchor_tokens=3, eps=1e6, collect_stats=True)
+    with RefineKV(model, config) as session:
+        out = generate(model, static=static)
+        assert out.shape == (1, 43)
+        if static:
+            assert type(session._cache.layers[0]).__name__ == "_VisibleStaticLayer"
+        stats = session.stats
+        assert 0 < stats["equivalent_access_ratio"] <= 1
+        assert stats["decode_attention_calls"] == 6  # 3 decode forwards x 2 layers
+        assert all(s.anchor_mask is not None for s in session._layers.values())
+        # a new generation in the same context rebuilds every layer's prompt state
+        shorter = generate(model, length=17, static=static)
+        assert shorter.shape == (1, 21)
+        assert session.stats["decode_attention_calls"] == 6
+        assert all(s.prompt_length == 17 for s in session._layers.values())
+    assert_released(model, session, implementation, hooks)
+
+
+def test_access_counter_closed_form():
+    """accessed = sum over decode calls of G * (sum_b sel_b * count_b + #unselected)
+    + H_q * suffix; dense = H_q * visible (transformers.py:590-594)."""
+    model = tiny_model()
+    with RefineKV(model, RefineKVConfig(backend="torch", eps=1e6, collect_stats=True)) as s:
+        generate(model, length=39)
+        stats = s.stats
+    # eps 1e6 expands nothing: per head 2 representatives (39 tokens, block 32)
+    q_heads, groups, layers = 4, 2, 2
+    accessed = dense = 0
+    for step in range(1, 4):  # 3 decode forwards; suffix holds `step` tokens
+        visible = 39 + step
+        accessed += layers * (2 * 2 * groups + q_heads * step)
+        dense += layers * q_heads * visible
+    assert stats["accessed"] == accessed and stats["dense"] == dense
+
+
+def test_generation_config_static_uses_visible_cache():
+    model = tiny_model()
+    model.generation_config.cache_implementation = "static"
+    with RefineKV(model, RefineKVConfig(backend="torch")) as session:
+        assert generate(model).shape == (1, 43)
+        assert type(session._cache.layers[0]).__name__ == "_VisibleStaticLayer"
+
+
+def test_visible_cache_exposes_written_prefix():
+    model = tiny_model()
+    cache = make_visible_static_cache(model, 8)
+    layer = cache.layers[0]
+    k = torch.randn(1, 2, 3, 32)
+    keys, values = layer.update(k, k + 1)
+    assert keys.shape[2] == 3 and layer.get_seq_length() == 3
+    assert layer.get_mask_sizes(1) == (4, 0)
+    keys, _ = layer.update(k[:, :, :1], k[:, :, :1])
+    assert keys.shape[2] == 4 and torch.equal(keys[:, :, :3], k)
+    with pytest.raises(ValueError, match="capacity"):
+        layer.update(torch.randn(1, 2, 5, 32), torch.randn(1, 2, 5, 32))
+    with pytest.raises(ValueError, match="positive"):
+        make_visible_static_cache(model, 0)
+
+
+def test_stock_static_cache_is_rejected():
+    model = tiny_model()
+    ids = torch.arange(39)[None] % 61 + 3
+    cache = transformers.StaticCache(config=model.config, max_cache_len=43)
+    with RefineKV(model):
+        with pytest.raises(ValueError, match="stock StaticCache is unsupported"):
+            model.generate(input_ids=ids, max_new_tokens=4, past_key_values=cache)
+
+
+def test_dense_layers_match_native_generation_and_leave_other_models_alone():
+    model, other = tiny_model(), tiny_model()
+    with torch.inference_mode():
+        expected = generate(model)
+    other_implementation = other.config._attn_implementation
+    with RefineKV(model, RefineKVConfig(full_attention_layers=2, collect_stats=True)) as s:
+        actual = generate(model)
+        assert other.config._attn_implementation == other_implementation
+    assert torch.equal(actual, expected)
+    assert s.stats["equivalent_access_ratio"] == 1
+
+
+def test_errors_restore_the_model():
+    model = tiny_model()
+    implementation = model.config._attn_implementation
+    with pytest.raises(ValueError, match="unpadded"):
+        with RefineKV(model):
+            with pytest.raises(RuntimeError, match="active"):
+                with RefineKV(model):
+                    pass
+            model.generate(input_ids=torch.tensor([[0, 3, 4]]),
+                           attention_mask=torch.tensor([[0, 1, 1]]), max_new_tokens=2)
+    assert model.config._attn_implementation == implementation
+    assert not hasattr(model, "_refinekv_session")
+    with pytest.raises(ValueError, match="inference-only"):
+        with RefineKV(model.train()):
+            pass
+    model.eval()
+    with pytest.raises(RuntimeError, match="RefineKV context"):
+        from refinekv.integrations.transformers import _refinekv_attention
+
+        _refinekv_attention(model.model.layers[0].self_attn, None, None, None, None)
+
+
+@pytest.mark.parametrize("family", ["llama", "qwen2"])
+def test_anchor_queries_come_from_the_tail_projection(family, monkeypatch):
+    """A projection of the whole prompt that rounds differently must not
+    change the anchors (transformers.py:505-507)."""
+    model = tiny_model(family)
+    for layer in model.model.layers:
+        proj = layer.self_attn.q_proj
+        with torch.no_grad():
+            proj.weight.zero_()
+            if proj.bias is not None:
+                proj.bias.zero_()
+        original = proj.forward
+
+        def perturbed(hidden, original=original):
+            out = original(hidden)
+            return out + 1 if hidden.shape[1] > 2 else out
+
+        monkeypatch.setattr(proj, "forward", perturbed)
+    with RefineKV(model, RefineKVConfig(backend="torch", eps=0, anchor_tokens=2)) as s:
+        generate(model)
+        assert all(not st.anchor_mask.any() for st in s._layers.values())
+
+
+def test_graph_mode_preconditions_on_cpu():
+    model = tiny_model()
+    ids = torch.tensor([[3, 4, 5]])
+    with RefineKV(model, RefineKVConfig(backend="torch"), cuda_graph=True):
+        with pytest.raises(ValueError, match="fixed output"):
+            model.generate(input_ids=ids, max_new_tokens=4)
+        with pytest.raises(ValueError, match="GPU BF16 model"):
+            model.generate(input_ids=ids, max_new_tokens=4, min_new_tokens=4, eos_token_id=None)
+        with pytest.raises(ValueError, match="does not support"):
+            model.generate(input_ids=ids, max_new_tokens=4, min_new_tokens=4, eos_token_id=None,
+                           top_k=3)
+
+
+# ---------------------------------------------------------------------------
+# GPU: backend="hip"
+# ---------------------------------------------------------------------------
+
+def _gpu_or_skip():
+    if not torch.cuda.is_available():
+        pytest.skip("no GPU in this environment")
+    from refinekv import _hip
+
+    _hip.lib()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("family", ["llama", "qwen2"])
+def test_hip_generation_dynamic_equals_static(family):
+    _gpu_or_skip()
+    model = tiny_model(family, "cuda")
+    config = RefineKVConfig(backend="hip", eps=1e6, anchor_tokens=2)
+    with RefineKV(model, config):
+        dynamic = generate(model)
+    with RefineKV(model, config):
+        static = generate(model, static=True)
+    assert torch.equal(dynamic, static)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("family", ["llama", "qwen2"])
+@pytest.mark.parametrize("reduction,anchors", [("mean", 0), ("any", 2)])
+def test_hip_graph_decode_matches_eager(family, reduction, anchors):
+    _gpu_or_skip()
+    model = tiny_model(family, "cuda")
+    if family == "qwen2":
+        model.generation_config.repetition_penalty = 1.05
+    config = RefineKVConfig(backend="hip", eps=0.01, gqa_reduction=reduction,
+                            anchor_tokens=anchors)
+    requests = []
+    for length in (39, 17):
+        ids = torch.arange(length, device="cuda")[None] % 61 + 3
+        options = dict(input_ids=ids, attention_mask=torch.ones_like(ids), max_new_tokens=8,
+                       min_new_tokens=8, eos_token_id=None, forced_eos_token_id=None,
+                       do_sample=False)
+        with RefineKV(model, config):
+            eager = model.generate(**options)
+        requests.append((options, eager))
+    with RefineKV(model, config, cuda_graph=True):
+        for options, eager in requests:
+            assert torch.equal(model.generate(**options), eager)
+
+
+@pytest.mark.gpu
+def test_hip_stats_and_dense_layers():
+    _gpu_or_skip()
+    model = tiny_model("llama", "cuda")
+    with RefineKV(model, RefineKVConfig(backend="hip", eps=1e6, collect_stats=True)) as s:
+        generate(model)
+        stats = s.stats
+    assert stats["decode_attention_calls"] == 6 and 0 < stats["equivalent_access_ratio"] < 1
+    with RefineKV(model, RefineKVConfig(backend="hip", full_attention_layers=2,
+                                        collect_stats=True)) as s:
+        generate(model)
+        assert s.stats["equivalent_access_ratio"] == 1
