@@ -252,6 +252,7 @@ def main():
     kernel_us = {k: v * 1e3 / (reps * a.layers) for k, v in kernel_ms.items()}
     dominant = max(kernel_us, key=kernel_us.get)
     achieved = nbytes[dominant] / (kernel_us[dominant] * 1e-6) / 1e9
+    traffic = measured_traffic(dominant)
     log(f"[bench] kernels (us, eager): " + ", ".join(f"{k} {v:.2f}" for k, v in kernel_us.items())
         + f"; expanded {frac:.4f}")
 
@@ -304,7 +305,7 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic,
         },
         "cpu_baseline": cpu,
         "expanded_fraction": round(frac, 5),
@@ -318,6 +319,19 @@ def main():
         "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
     }
     print(json.dumps(result), flush=True)
+
+
+def measured_traffic(kernel):
+    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
+    summary (FETCH_SIZE and WRITE_SIZE runs scaled by a plain copy's
+    readings), or None when it has none."""
+    path = os.path.join(ROOT, "profiles", "traffic.json")
+    try:
+        with open(path) as f:
+            entry = json.load(f)["kernels"].get(kernel)
+    except (OSError, ValueError, KeyError):
+        return None
+    return None if entry is None else entry["traffic_bytes"]
 
 
 def copy_calibration():
