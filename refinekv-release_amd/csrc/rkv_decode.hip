@@ -60,13 +60,19 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr int64_t kMaxTiles = 2048;    // tiles per head in the decode kernel (LDS page index)
-constexpr int64_t kMaxHeads = 4096;    // KV heads in the decode kernel (control block)
+constexpr int64_t kMaxHeads = 1024;    // KV heads in the persistent kernel (control block)
 constexpr int64_t kMaxPageItems = 64;  // page items per (head, row block)
 constexpr int64_t kMaxHeadTiles = 8192;  // split page kernel: heads * tiles in LDS
 constexpr int64_t kMaxFusedDim = 128;    // widest head_dim the persistent kernel runs
 constexpr size_t kMaxFusedLds = 64 * 1024;  // its LDS per workgroup (static + dynamic)
 constexpr size_t kMaxFusedPrivate = 64;     // its private bytes per lane (no spill traffic)
-constexpr int64_t kControlWords = 4 + 3 * kMaxHeads;  // ticket, exits, error, -, 3 x H counters
+// Control block of the persistent kernel (uint32 words; see decode_kernel).
+constexpr int kMaxQueues = 16;               // one work queue per XCD (XCC_ID is 4 bits)
+constexpr int64_t kCtlHeadTicket = 0, kCtlExits = 1, kCtlError = 2, kCtlEpoch = 3;
+constexpr int64_t kCtlQueues = 16;           // per queue: claim, ready, ticket, -
+constexpr int64_t kCtlSlots = kCtlQueues + 4 * kMaxQueues;  // per queue: kMaxHeads u64 slots
+constexpr int64_t kCtlCounters = kCtlSlots + 2 * kMaxQueues * kMaxHeads;  // 3 x kMaxHeads
+constexpr int64_t kControlWords = kCtlCounters + 3 * kMaxHeads;
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a dependency wait gives up (~1 s)
 
 // Optional profiling events (rkv_set_profile_events): events[0] is recorded
@@ -88,6 +94,9 @@ thread_local int g_pipeline = 0;
 // ---------------------------------------------------------------------------
 struct Layout {
   int64_t n_tiles, page_items, workers, rows_per_block, row_blocks;
+  // Padded row strides: every head's slice of an intermediate array covers
+  // whole 256-byte lines, so no cache line holds two heads' data.
+  int64_t z_stride, tile_stride, part_stride;
   int64_t control, z, delta, lse, tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc,
       total;
 };
@@ -134,7 +143,11 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   const int64_t rows = heads * group;
   // page partials: (rows, page_items) for the persistent kernel, (rows,
   // workers) for the split pipeline
-  const int64_t slots = L.page_items > L.workers ? L.page_items : L.workers;
+  auto round64 = [](int64_t x) { return (x + 63) / 64 * 64; };
+  L.z_stride = L.n_tiles * kTile;
+  L.tile_stride = round64(L.n_tiles);
+  L.part_stride = round64(L.page_items);
+  const int64_t slots = L.part_stride > L.workers ? L.part_stride : L.workers;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = off;
@@ -142,12 +155,12 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
     return at;
   };
   L.control = take(kControlWords * 4);
-  L.z = take(rows * n_blocks * 4);
-  L.delta = take(rows * n_blocks * 4);
-  L.lse = take(rows * L.n_tiles * 4 * 4);
-  L.tilebits = take(heads * L.n_tiles * 8);
-  L.rep_l = take(rows * L.n_tiles * 4);
-  L.rep_acc = take(rows * L.n_tiles * dim * 4);
+  L.z = take(rows * L.z_stride * 4);
+  L.delta = take(rows * L.z_stride * 4);
+  L.lse = take(rows * L.tile_stride * 4 * 4);
+  L.tilebits = take(heads * L.tile_stride * 8);
+  L.rep_l = take(rows * L.tile_stride * 4);
+  L.rep_acc = take(rows * L.tile_stride * dim * 4);
   L.header = take((heads + 1) * 8);
   L.page_m = take(rows * slots * 4);
   L.page_l = take(rows * slots * 4);
@@ -233,6 +246,8 @@ struct ScoreArgs {
   float* lse;                  // (H, G, tiles, 4): zm, zl, cm, cl
   float* rep_acc;              // (H, G, tiles, D)
   int64_t n_blocks, n_tiles, block, length;
+  int64_t z_stride;            // row stride of z / delta (blocks padded to whole tiles)
+  int64_t tile_stride;         // row stride of the per-tile arrays (tiles padded to 64)
   int group;
   float scale;
 };
@@ -338,7 +353,7 @@ __device__ __forceinline__ void score_tile(const ScoreArgs& a, int64_t h, int64_
       const float dl = (sqrtf(clamp_min(pdot[idx], 0.0f)) * a.scale) * kInflate;
       z = s + (b == N - 1 ? ln_last : ln_full);
       zc = z + log_cosh(dl);
-      const int64_t o = (h * G + g) * N + b;
+      const int64_t o = (h * G + g) * a.z_stride + b;
       a.z[o] = z;
       a.delta[o] = dl;
     }
@@ -356,7 +371,7 @@ __device__ __forceinline__ void score_tile(const ScoreArgs& a, int64_t h, int64_
     const float cm = wave_nanmax_u(xc);
     const float cl = wave_sum_u(expf_(xc - inf_to_zero(cm)));
     if (lane == 0) {
-      *reinterpret_cast<float4*>(a.lse + ((h * G + g) * a.n_tiles + tile) * 4) =
+      *reinterpret_cast<float4*>(a.lse + ((h * G + g) * a.tile_stride + tile) * 4) =
           make_float4(zm, zl, cm, cl);
     }
     if constexpr (REPS) {
@@ -384,7 +399,7 @@ __device__ __forceinline__ void score_tile(const ScoreArgs& a, int64_t h, int64_
         acc[i] = acc[i] + shfl_xor(acc[i], 32);
       }
       if (grp == 0) {
-        float* o = a.rep_acc + ((h * G + g) * a.n_tiles + tile) * D + c * CH;
+        float* o = a.rep_acc + ((h * G + g) * a.tile_stride + tile) * D + c * CH;
 #pragma unroll
         for (int i = 0; i < CH; ++i) o[i] = acc[i];
       }
@@ -411,6 +426,7 @@ struct DecideArgs {
   float* rep_l;                 // (H, G, tiles) or null (select only)
   float* rep_acc;               // (H, G, tiles, D)
   int64_t n_blocks, n_tiles, block, length;
+  int64_t z_stride, tile_stride;  // padded row strides (see ScoreArgs)
   int group, reduction, dim;
   float eps;
 };
@@ -469,7 +485,8 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     for (int k = 0; k < kLseRegs; ++k) {
       const int64_t t = lane + (int64_t)k * kWave;
       if (g < G && t < T) {
-        const float4 v = *reinterpret_cast<const float4*>(a.lse + ((h * G + g) * T + t) * 4);
+        const float4 v =
+            *reinterpret_cast<const float4*>(a.lse + ((h * G + g) * a.tile_stride + t) * 4);
         pz_m[gi][k] = v.x;
         pz_l[gi][k] = v.y;
         pc_m[gi][k] = v.z;
@@ -487,7 +504,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     const int g = idx / kTile, bl = idx % kTile;
     if (g < G && bl < nvalid) {
       const int64_t b = tile * kTile + bl;
-      const int64_t o = (h * G + g) * N + b;
+      const int64_t o = (h * G + g) * a.z_stride + b;
       rz[k] = a.z[o];
       rd[k] = a.delta[o];
       rv[k] = a.value_norm[h * N + b];
@@ -504,7 +521,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
 #pragma unroll
   for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
     const int g = wave + gi * kWaves;
-    tile_m[gi] = (a.rep_l && g < G) ? a.lse[((h * G + g) * T + tile) * 4] : 0.0f;
+    tile_m[gi] = (a.rep_l && g < G) ? a.lse[((h * G + g) * a.tile_stride + tile) * 4] : 0.0f;
   }
   constexpr int kAccPerThread = kMaxGroup * 256 / kThreads;  // G * D <= 16 * 256
   float racc[kAccPerThread];
@@ -515,7 +532,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     racc[k] = 0.0f;
     if (a.rep_l && idx < GD) {
       const int g = idx / a.dim, d = idx % a.dim;
-      racc[k] = a.rep_acc[((h * G + g) * T + tile) * a.dim + d];
+      racc[k] = a.rep_acc[((h * G + g) * a.tile_stride + tile) * a.dim + d];
     }
   }
 
@@ -524,7 +541,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
   for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
     const int g = wave + gi * kWaves;
     if (g >= G) break;
-    const float* part = a.lse + (h * G + g) * T * 4;
+    const float* part = a.lse + (h * G + g) * a.tile_stride * 4;
     const float lz = merge_lse(pz_m[gi], pz_l[gi], part, 0, T, lane);  // log Z
     const float lc = merge_lse(pc_m[gi], pc_l[gi], part, 1, T, lane);
     if (lane == 0) {
@@ -577,7 +594,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     if (valid) a.mask[h * N + b] = sel ? 1 : 0;
     const uint64_t bits = __ballot(sel);
     if (lane == 0) {
-      a.tilebits[h * T + tile] = bits;
+      a.tilebits[h * a.tile_stride + tile] = bits;
       sel_bits = bits;
     }
     if (a.accessed) {
@@ -604,7 +621,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     const float e = valid ? expf_(rz[gi] - inf_to_zero(tile_m[gi])) : 0.0f;
     const float l = wave_sum_u(expanded ? 0.0f : e);
     psel[g][lane] = expanded ? e : 0.0f;
-    if (lane == 0) a.rep_l[(h * G + g) * T + tile] = nsel == nvalid ? 0.0f : l;
+    if (lane == 0) a.rep_l[(h * G + g) * a.tile_stride + tile] = nsel == nvalid ? 0.0f : l;
   }
   if (nsel == 0 || nsel == nvalid) return;
   __syncthreads();
@@ -622,7 +639,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
       const float v = bf16_to_f32(a.value_mean[(h * N + tile * kTile + j) * D + d]);
       acc = acc - psel[g][j] * v;
     }
-    a.rep_acc[((h * G + g) * T + tile) * D + d] = acc;
+    a.rep_acc[((h * G + g) * a.tile_stride + tile) * D + d] = acc;
   }
 }
 
@@ -655,6 +672,8 @@ struct PageArgs {
   float* page_acc;             // (H, G, P, D)
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
   int64_t suffix_cap, n_blocks, n_tiles, block, length;
+  int64_t tile_stride;         // row stride of the per-tile arrays
+  int64_t part_stride;         // row stride of the page partials (items padded to 64)
   int group, page_items;
   float scale;
 };
@@ -729,7 +748,7 @@ __device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, 
   const int64_t t_begin = min((int64_t)tid * per, T), t_end = min(t_begin + per, T);
   uint32_t mine = 0;
   for (int64_t t = t_begin; t < t_end; ++t) {
-    const uint64_t b = a.tilebits[h * T + t];
+    const uint64_t b = a.tilebits[h * a.tile_stride + t];
     bits_s[t] = b;
     mine += (uint32_t)__popcll(b);
   }
@@ -780,17 +799,17 @@ __device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, 
     const int64_t row = h * G + g0 + g;
     float mr = kNegInf;
     for (int64_t t = r0; t < r1; ++t) {
-      const float lt = a.rep_l[row * T + t];
-      const float mt = inf_to_zero(a.lse[(row * T + t) * 4]);
+      const float lt = a.rep_l[row * a.tile_stride + t];
+      const float mt = inf_to_zero(a.lse[(row * a.tile_stride + t) * 4]);
       if (lt > 0.0f) mr = fmaxf(mr, mt);
     }
     if (mr == kNegInf) continue;
     float l = 0.0f;
     for (int64_t t = r0; t < r1; ++t) {
-      const float lt = a.rep_l[row * T + t];
-      const float mt = inf_to_zero(a.lse[(row * T + t) * 4]);
+      const float lt = a.rep_l[row * a.tile_stride + t];
+      const float mt = inf_to_zero(a.lse[(row * a.tile_stride + t) * 4]);
       float at[CH];
-      load_f32<CH>(a.rep_acc + (row * T + t) * D + c * CH, at);
+      load_f32<CH>(a.rep_acc + (row * a.tile_stride + t) * D + c * CH, at);
       if (lt > 0.0f) {
         const float e = __builtin_amdgcn_exp2f((mt - mr) * kLog2e);
         l = l + lt * e;
@@ -919,7 +938,7 @@ __device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, 
   __syncthreads();
   for (int idx = tid; idx < gn * D; idx += kThreads) {
     const int g = idx / D, d = idx % D;
-    const int64_t slot = (h * G + g0 + g) * P + k;
+    const int64_t slot = (h * G + g0 + g) * a.part_stride + k;
     const float sum = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
     a.page_acc[slot * D + d] = sum;
     if (d == 0) {
@@ -937,6 +956,7 @@ struct MergeArgs {
   const float* page_l;
   const float* page_acc;  // (H, G, P, D)
   uint16_t* out;          // (H*G, D)
+  int64_t part_stride;    // row stride of the page partials
   int group, page_items, dim;
 };
 
@@ -954,8 +974,8 @@ __device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g,
 
   float mx = kNegInf;
   for (int i = tid; i < P; i += kThreads) {
-    const float l = a.page_l[r * P + i];
-    const float m = a.page_m[r * P + i];
+    const float l = a.page_l[r * a.part_stride + i];
+    const float m = a.page_m[r * a.part_stride + i];
     if (l > 0.0f) mx = fmaxf(mx, m);
   }
   mx = wave_nanmax_u(mx);
@@ -974,9 +994,9 @@ __device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g,
     for (int u = 0; u < kMergeBatch; ++u) {
       const int i = i0 + u * kMergeK;
       const int ii = i < P ? i : 0;
-      mv[u] = a.page_m[r * P + ii];
-      lv[u] = a.page_l[r * P + ii];
-      av[u] = a.page_acc[(r * P + ii) * D + dd];
+      mv[u] = a.page_m[r * a.part_stride + ii];
+      lv[u] = a.page_l[r * a.part_stride + ii];
+      av[u] = a.page_acc[(r * a.part_stride + ii) * D + dd];
     }
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
@@ -1017,11 +1037,16 @@ struct SplitPageArgs {
   float* page_acc;             // (H*G, W, D)
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
   int64_t suffix_cap, n_blocks, n_tiles, block, length;
+  int64_t tile_stride;         // head stride of tilebits (tiles padded to 64)
   int heads, group, workers, rows_per_block;
   float scale;
 };
 
-
+// Ballot of dense (head, tile) index ht (ht = h * tiles + t).
+__device__ __forceinline__ uint64_t head_tile_bits(const SplitPageArgs& a, int64_t ht) {
+  const int64_t h = ht / a.n_tiles;
+  return a.tilebits[h * a.tile_stride + (ht - h * a.n_tiles)];
+}
 
 inline size_t split_page_smem(int64_t heads, int64_t n_tiles) {
   return (size_t)(align256((heads * n_tiles + 1) * 4) + align256((heads + 1) * 8) +
@@ -1053,12 +1078,12 @@ __global__ __launch_bounds__(kThreads) void split_page_kernel(SplitPageArgs a) {
   const int64_t per = (HT + kThreads - 1) / kThreads;
   const int64_t t_begin = min((int64_t)tid * per, HT), t_end = min(t_begin + per, HT);
   uint32_t mine = 0;
-  for (int64_t t = t_begin; t < t_end; ++t) mine += (uint32_t)__popcll(a.tilebits[t]);
+  for (int64_t t = t_begin; t < t_end; ++t) mine += (uint32_t)__popcll(head_tile_bits(a, t));
   uint32_t total;
   uint32_t run = block_exclusive_scan(mine, wave_tot, total);
   for (int64_t t = t_begin; t < t_end; ++t) {
     pre[t] = run;
-    run += (uint32_t)__popcll(a.tilebits[t]);
+    run += (uint32_t)__popcll(head_tile_bits(a, t));
   }
   if (tid == 0) pre[HT] = total;
   __syncthreads();
@@ -1126,7 +1151,8 @@ __global__ __launch_bounds__(kThreads) void split_page_kernel(SplitPageArgs a) {
           const int64_t mid = (lo_t + hi_t + 1) >> 1;
           if ((int64_t)pre[mid] <= j) lo_t = mid; else hi_t = mid - 1;
         }
-        list[tid] = (lo_t - h * T) * kTile + nth_set_bit(a.tilebits[lo_t], (int)(j - pre[lo_t]));
+        list[tid] = (lo_t - h * T) * kTile +
+                    nth_set_bit(head_tile_bits(a, lo_t), (int)(j - pre[lo_t]));
       }
       __syncthreads();
       RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
@@ -1250,6 +1276,7 @@ struct SplitMergeArgs {
   const float* page_acc;
   uint16_t* out;          // (H*G, D)
   int64_t n_tiles;
+  int64_t tile_stride;    // row stride of the per-tile arrays
   int heads, group, workers, dim;
 };
 
@@ -1291,8 +1318,8 @@ __global__ __launch_bounds__(kThreads) void split_merge_kernel(SplitMergeArgs a)
   for (int64_t i = tid; i < P; i += kThreads) {
     float m, l;
     if (i < T) {
-      m = inf_to_zero(a.lse[(r * T + i) * 4]);
-      l = a.rep_l[r * T + i];
+      m = inf_to_zero(a.lse[(r * a.tile_stride + i) * 4]);
+      l = a.rep_l[r * a.tile_stride + i];
     } else {
       const int64_t w = w_first + (i - T);
       m = a.page_m[r * W + w];
@@ -1334,7 +1361,7 @@ __global__ __launch_bounds__(kThreads) void split_merge_kernel(SplitMergeArgs a)
       const int64_t q = q0 + (int64_t)u * kMergeK;
       idx[u] = q < n_live ? live[q] : -1;
       const int64_t i = idx[u] < 0 ? 0 : idx[u];
-      accv[u] = i < T ? a.rep_acc[(r * T + i) * D + dd]
+      accv[u] = i < T ? a.rep_acc[(r * a.tile_stride + i) * D + dd]
                       : a.page_acc[(r * W + w_first + (i - T)) * D + dd];
     }
 #pragma unroll
@@ -1367,34 +1394,45 @@ struct DecodeArgs {
   DecideArgs decide;
   PageArgs page;
   MergeArgs merge;
-  uint32_t* control;  // [0] ticket, [1] exits, [2] error (sticky), then 3 x kMaxHeads counters
-  uint32_t n_score, n_decide, n_page, n_merge;
+  uint32_t* control;  // kControlWords words, zero when the workspace is new
   int heads, row_blocks, merge_cols;
 };
 
-// Thread 0 polls a completion counter until it reaches target (bounded: on
-// timeout the sticky error word is set and the item goes on), then the
-// workgroup acquires what the counted items wrote.
-__device__ __forceinline__ void wait_count(const uint32_t* cnt, uint32_t target, uint32_t* err) {
-  if (threadIdx.x == 0) {
-    uint32_t spins = 0;
-    while (__hip_atomic_load(cnt, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
-      if (++spins > kSpinLimit) {
-        __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        break;
-      }
-      __builtin_amdgcn_s_sleep(4);
-    }
-  }
-  __syncthreads();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent");
+// This workgroup's XCD (HW_REG_XCC_ID bits [3:0]).
+__device__ __forceinline__ uint32_t xcc_id() {
+  return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (kMaxQueues - 1);
 }
 
-// Every thread releases its writes, then thread 0 counts the item done.
-__device__ __forceinline__ void signal_done(uint32_t* cnt) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+__device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Thread 0: polls until *p >= target (bounded: on timeout it sets the sticky
+// error word and returns).
+__device__ __forceinline__ void poll_at_least(const uint32_t* p, uint32_t target, uint32_t* err) {
+  for (uint32_t spins = 0; load_dev(p) < target; ++spins) {
+    if (spins > kSpinLimit) {
+      __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return;
+    }
+    __builtin_amdgcn_s_sleep(2);
+  }
+}
+
+// Waits until a head's completion counter reaches target.  The counted items
+// ran on this XCD, whose L2 holds what they wrote, and this workgroup has not
+// read those lines before: no cache maintenance is needed.
+__device__ __forceinline__ void wait_count(const uint32_t* cnt, uint32_t target, uint32_t* err) {
+  if (threadIdx.x == 0) poll_at_least(cnt, target, err);
   __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELEASE, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Every thread waits until its stores have reached the XCD's L2, then thread
+// 0 counts the item done.
+__device__ __forceinline__ void signal_done(uint32_t* cnt) {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // The kernel's arguments re-read from the kernarg segment for each item:
@@ -1408,77 +1446,136 @@ __device__ __forceinline__ const DecodeArgs* item_args() {
 
 // Two workgroups per CU (<= 256 registers per lane): every phase fits in
 // registers without spilling.
+//
+// Work distribution.  Every XCD has its own queue; its workgroups draw queue
+// tickets, and a queue takes whole KV heads from a device-wide head counter,
+// so all items of a head run on one XCD and hand data to each other through
+// that XCD's L2.  A head is K consecutive tickets of its queue (its score,
+// decide, page and merge items, in that order); the workgroup that draws the
+// first ticket of a head's slot claims the head and publishes it in the slot
+// (epoch-tagged, so slots need no reset).  An item waits only for items with
+// smaller tickets of its own queue (the slot's first ticket, or its head's
+// earlier phases), so the smallest unfinished ticket of every queue is held
+// by a running workgroup: the grid drains whatever the residency.  Queue
+// state is reset by the queue's first workgroup of each launch (epoch), the
+// device-wide counters by the last workgroup out.
 template <int D, int GBM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(DecodeArgs a) {
   extern __shared__ unsigned char decode_dyn[];
-  __shared__ uint32_t s_item;
-  __shared__ uint32_t s_last;
+  __shared__ uint32_t s_ticket, s_head, s_tag, s_last;
   uint32_t* ctl = a.control;
-  uint32_t* score_done = ctl + 4;
+  uint32_t* err = ctl + kCtlError;
+  uint32_t* score_done = ctl + kCtlCounters;
   uint32_t* decide_done = score_done + kMaxHeads;
   uint32_t* page_done = decide_done + kMaxHeads;
+  const uint32_t q = xcc_id();
+  uint32_t* queue = ctl + kCtlQueues + 4 * q;  // [0] claim, [1] ready, [2] ticket
+  uint64_t* slots = reinterpret_cast<uint64_t*>(ctl + kCtlSlots) + (int64_t)q * kMaxHeads;
   const uint32_t T = (uint32_t)a.score.n_tiles;
-  const uint32_t e_score = a.n_score, e_decide = e_score + a.n_decide;
-  const uint32_t e_page = e_decide + a.n_page, e_all = e_page + a.n_merge;
   const uint32_t P = (uint32_t)a.page.page_items;
   const uint32_t page_per_head = (uint32_t)a.row_blocks * P;
   const uint32_t merge_per_head = (uint32_t)a.merge.group * (uint32_t)a.merge_cols;
+  const uint32_t e_score = T, e_decide = 2 * T, e_page = e_decide + page_per_head;
+  const uint32_t K = e_page + merge_per_head;  // tickets per head
   const int tid = threadIdx.x;
 
-  if (tid == 0) s_item = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) {
+    // this launch's tag; the queue's first workgroup of the launch resets it
+    const uint32_t tag = load_dev(ctl + kCtlEpoch) + 1;
+    if (__hip_atomic_fetch_max(queue, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < tag) {
+      __hip_atomic_store(queue + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __builtin_amdgcn_s_waitcnt(0);
+      __hip_atomic_store(queue + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    } else {
+      poll_at_least(queue + 1, tag, err);
+    }
+    s_tag = tag;
+    s_ticket = __hip_atomic_fetch_add(queue + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  }
   __syncthreads();
-  uint32_t item = s_item;
-  while (item < e_all) {
-    // claim the next item now; its ticket is larger than this one's
+  const uint32_t tag = s_tag;
+  uint32_t ticket = s_ticket;
+  for (;;) {
+    const uint32_t slot = ticket / K, i = ticket % K;
+    if (tid == 0) {
+      uint32_t h = 0xFFFFFFFFu;
+      if (slot < (uint32_t)kMaxHeads) {
+        uint64_t* entry = slots + slot;
+        if (i == 0) {
+          // claim the next head for this queue (or none left) and publish it
+          h = __hip_atomic_fetch_add(ctl + kCtlHeadTicket, 1u, __ATOMIC_RELAXED,
+                                     __HIP_MEMORY_SCOPE_AGENT);
+          if (h < (uint32_t)a.heads) {
+            __hip_atomic_store(score_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(decide_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(page_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __builtin_amdgcn_s_waitcnt(0);
+          } else {
+            h = 0xFFFFFFFFu;
+          }
+          __hip_atomic_store(entry, ((uint64_t)tag << 32) | h, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+        } else {
+          uint64_t v = 0;
+          for (uint32_t spins = 0;; ++spins) {
+            v = __hip_atomic_load(entry, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            if ((uint32_t)(v >> 32) == tag) break;
+            if (spins > kSpinLimit) {
+              __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+              v = 0xFFFFFFFFull;
+              break;
+            }
+            __builtin_amdgcn_s_sleep(2);
+          }
+          h = (uint32_t)v;
+        }
+      }
+      s_head = h;
+    }
+    __syncthreads();
+    const uint32_t h = s_head;
+    if (h >= (uint32_t)a.heads) break;
+    // claim the next ticket now; it is larger than this one
     uint32_t next = 0;
-    if (tid == 0) next = __hip_atomic_fetch_add(ctl, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (item < e_score) {
-      const uint32_t h = item / T, t = item % T;
+    if (tid == 0)
+      next = __hip_atomic_fetch_add(queue + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (i < e_score) {
       const ScoreArgs sa = item_args()->score;
-      score_tile<D, true>(sa, h, t, decode_dyn);
+      score_tile<D, true>(sa, h, i, decode_dyn);
       signal_done(score_done + h);
-    } else if (item < e_decide) {
-      const uint32_t i = item - e_score, h = i / T, t = i % T;
-      wait_count(score_done + h, T, ctl + 2);
+    } else if (i < e_decide) {
+      wait_count(score_done + h, T, err);
       const DecideArgs da = item_args()->decide;
-      decide_tile(da, h, t);
+      decide_tile(da, h, i - e_score);
       signal_done(decide_done + h);
-    } else if (item < e_page) {
-      const uint32_t i = item - e_decide, h = i / page_per_head, r = i % page_per_head;
-      wait_count(decide_done + h, T, ctl + 2);
+    } else if (i < e_page) {
+      const uint32_t r = i - e_decide;
+      wait_count(decide_done + h, T, err);
       const PageArgs pa = item_args()->page;
       page_item<D, GBM>(pa, h, (int)(r / P), (int)(r % P), decode_dyn);
       signal_done(page_done + h);
     } else {
-      const uint32_t i = item - e_page, h = i / merge_per_head, r = i % merge_per_head;
-      wait_count(page_done + h, page_per_head, ctl + 2);
+      const uint32_t r = i - e_page;
+      wait_count(page_done + h, page_per_head, err);
       const MergeArgs ma = item_args()->merge;
       merge_item(ma, h, (int)(r / a.merge_cols), (int)(r % a.merge_cols));
     }
     __syncthreads();
-    if (tid == 0) s_item = next;
+    if (tid == 0) s_ticket = next;
     __syncthreads();
-    item = s_item;
+    ticket = s_ticket;
   }
 
-  // The last workgroup out returns the ticket, exit and head counters to 0
-  // (every other workgroup has made its last access to them by then).
+  // The last workgroup out resets the device-wide counters and advances the
+  // epoch (every other workgroup has made its last access to them).
   if (tid == 0) {
     const uint32_t out =
-        __hip_atomic_fetch_add(ctl + 1, 1u, __ATOMIC_ACQ_REL, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = out == gridDim.x - 1 ? 1u : 0u;
-  }
-  __syncthreads();
-  if (s_last) {
-    for (int i = tid; i < a.heads; i += kThreads) {
-      __hip_atomic_store(score_done + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(decide_done + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(page_done + i, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
-    if (tid == 0) {
-      __hip_atomic_store(ctl, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctl + 1, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        __hip_atomic_fetch_add(ctl + kCtlExits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (out == gridDim.x - 1) {
+      __hip_atomic_store(ctl + kCtlHeadTicket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_store(ctl + kCtlExits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      __hip_atomic_fetch_add(ctl + kCtlEpoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     }
   }
 }
@@ -1548,6 +1645,8 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
   sa.rep_acc = at<float>(p.ws, L.rep_acc);
   sa.n_blocks = p.n_blocks;
   sa.n_tiles = L.n_tiles;
+  sa.z_stride = L.z_stride;
+  sa.tile_stride = L.tile_stride;
   sa.block = p.block;
   sa.length = p.length;
   sa.group = (int)p.group;
@@ -1574,6 +1673,8 @@ DecideArgs decide_args(const SelectParams& p, const Layout& L) {
   da.rep_acc = at<float>(p.ws, L.rep_acc);
   da.n_blocks = p.n_blocks;
   da.n_tiles = L.n_tiles;
+  da.z_stride = L.z_stride;
+  da.tile_stride = L.tile_stride;
   da.block = p.block;
   da.length = p.length;
   da.group = (int)p.group;
@@ -1750,6 +1851,7 @@ int launch_split(const SelectParams& p, const Layout& L, const DecodeBuffers& b)
   pa.suffix_cap = b.suffix_cap;
   pa.n_blocks = p.n_blocks;
   pa.n_tiles = L.n_tiles;
+  pa.tile_stride = L.tile_stride;
   pa.block = p.block;
   pa.length = p.length;
   pa.heads = (int)p.heads;
@@ -1772,6 +1874,7 @@ int launch_split(const SelectParams& p, const Layout& L, const DecodeBuffers& b)
   ma.page_acc = pa.page_acc;
   ma.out = static_cast<uint16_t*>(b.output);
   ma.n_tiles = L.n_tiles;
+  ma.tile_stride = L.tile_stride;
   ma.heads = (int)p.heads;
   ma.group = (int)p.group;
   ma.workers = (int)L.workers;
@@ -1812,6 +1915,8 @@ int launch_fused(const SelectParams& p, const Layout& L, const DecodeBuffers& b)
   pa.suffix_cap = b.suffix_cap;
   pa.n_blocks = p.n_blocks;
   pa.n_tiles = L.n_tiles;
+  pa.tile_stride = L.tile_stride;
+  pa.part_stride = L.part_stride;
   pa.block = p.block;
   pa.length = p.length;
   pa.group = (int)p.group;
@@ -1822,6 +1927,7 @@ int launch_fused(const SelectParams& p, const Layout& L, const DecodeBuffers& b)
   ma.page_l = pa.page_l;
   ma.page_acc = pa.page_acc;
   ma.out = static_cast<uint16_t*>(b.output);
+  ma.part_stride = L.part_stride;
   ma.group = (int)p.group;
   ma.page_items = (int)L.page_items;
   ma.dim = (int)p.dim;
@@ -1829,11 +1935,8 @@ int launch_fused(const SelectParams& p, const Layout& L, const DecodeBuffers& b)
   da.heads = (int)p.heads;
   da.row_blocks = (int)L.row_blocks;
   da.merge_cols = (int)((p.dim + kMergeD - 1) / kMergeD);
-  da.n_score = (uint32_t)(p.heads * L.n_tiles);
-  da.n_decide = da.n_score;
-  da.n_page = (uint32_t)(p.heads * L.row_blocks * L.page_items);
-  da.n_merge = (uint32_t)(p.heads * p.group * da.merge_cols);
-  const uint32_t items = da.n_score + da.n_decide + da.n_page + da.n_merge;
+  const uint32_t items = (uint32_t)(p.heads * (2 * L.n_tiles + L.row_blocks * L.page_items +
+                                                p.group * da.merge_cols));
   const int64_t dyn_score = (int64_t)score_smem(p.group, p.dim, true);
   const int64_t dyn_page = page_smem(L.n_tiles);
   const size_t dyn = (size_t)(dyn_score > dyn_page ? dyn_score : dyn_page);

@@ -65,8 +65,10 @@ def test_workspace_size_covers_layout(lib):
         rows, tiles = heads * group, layout["n_tiles"]
         # fixed-size control block first, so every shape finds it at offset 0
         assert layout["control"] == 0 and layout["z"] == controls
-        assert layout["delta"] - layout["z"] >= rows * n * 4
+        assert layout["delta"] - layout["z"] >= rows * tiles * 64 * 4
         assert layout["header"] - layout["rep_acc"] >= rows * tiles * dim * 4
+        # per-head slices of the intermediates are whole 256-byte lines
+        assert (layout["delta"] - layout["z"]) % (256 * heads) == 0 or heads == 1
         assert layout["page_m"] - layout["header"] >= (heads + 1) * 8
         slots = max(layout["page_items"], layout["workers"])
         assert layout["page_l"] - layout["page_m"] >= rows * slots * 4
