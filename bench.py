@@ -33,7 +33,7 @@ import torch  # noqa: E402
 METRIC = "decode attn µs/step/layer @128K ctx GQA32/8 d128; HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
 # Kernels one rkv_decode call launches, per pipeline.
-KERNELS = {"persistent": ("decode",), "split": ("score", "decide", "pages", "merge")}
+KERNELS = {"persistent": ("decode",), "split": ("score", "attend", "merge")}
 
 
 def log(msg):
@@ -122,12 +122,12 @@ def make_layer(gen, a, capacity, device):
 
 
 def algorithmic_bytes(a, masks, counts, suffix):
-    """Bytes each phase of the decode kernel must move per layer-step, counted
+    """Bytes each phase of the decode step must move per layer-step, counted
     once in the reference's storage formats: score reads key means and
     ellipsoids of every block and the value means of unexpanded blocks (its
-    representative half); decide reads value norms and writes the mask; pages
-    read the K/V tokens of expanded blocks and the suffix; merge writes the
-    output.  "decode" is their sum (one kernel runs all four phases).
+    representative half); attend reads value norms, writes the mask and reads
+    the K/V tokens of expanded blocks and the suffix; merge writes the output.
+    "decode" is their sum (the persistent kernel runs every phase).
     Intermediates (z, delta, partials) are not algorithmic bytes."""
     H, G, D = a.heads, a.group, a.dim
     n = counts.numel()
@@ -136,10 +136,9 @@ def algorithmic_bytes(a, masks, counts, suffix):
     unexpanded = ((1 - sel).sum()).item()
     q_bytes = H * G * D * 2
     score = 2 * H * n * D * 2 + unexpanded * D * 2 + q_bytes
-    decide = H * n * 4 + H * n
-    pages = expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
+    attend = H * n * 4 + H * n + expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
     merge = H * G * D * 2
-    phases = dict(score=score, decide=decide, pages=pages, merge=merge)
+    phases = dict(score=score, attend=attend, merge=merge)
     return dict(phases, decode=sum(phases.values()))
 
 

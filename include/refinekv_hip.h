@@ -66,14 +66,14 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
 /* Byte offsets inside the workspace (for tests): control, z, delta, lse,
- * tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc, total, then
- * n_tiles, the page items per head and row block (persistent kernel) and the
- * page workers (split pipeline) -> out15[0..14].  The control block (uint32
- * words: ticket, exits, error, -, per-head counters) is always at offset 0
- * with a fixed size; word 2 becomes 1 (and stays 1) if a decode kernel's
- * dependency wait ever timed out. */
+ * tilebits, rep_acc, part_m, part_l, part_acc, total, then n_tiles and the
+ * padded row strides (elements) of z / delta, of the per-tile arrays and of
+ * the partials -> out14[0..13].  The control block (uint32 words: head
+ * ticket, exit count, error, epoch, per-XCD queues, slots, per-head counters)
+ * is always at offset 0 with a fixed size; word 2 becomes 1 (and stays 1) if a
+ * persistent kernel's dependency wait ever timed out. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out15);
+                         int64_t* out14);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton
@@ -123,18 +123,18 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
                unsigned long long* accessed_blocks, void* workspace, size_t workspace_bytes,
                rkv_stream_t stream);
 
-/* Profiling hook with no reference counterpart: when `events` points to 5
+/* Profiling hook with no reference counterpart: when `events` points to 4
  * hipEvent_t handles, later rkv_select / rkv_decode calls on this thread
  * record events[0] before their first kernel and events[k] after their k-th
  * (rkv_select: score, decide; rkv_decode: the persistent kernel, or score,
- * decide, pages, merge on the split pipeline).  NULL turns it off. */
+ * attend, merge on the split pipeline).  NULL turns it off. */
 int rkv_set_profile_events(void* events);
 
 /* Test and benchmark hook with no reference counterpart: which rkv_decode
  * pipeline runs on this thread.  0 automatic (= 2), 1 the persistent kernel
  * (one launch; head_dim <= 128, LDS <= 64 KiB per workgroup, no
  * private-memory traffic, else RKV_UNSUPPORTED), 2 the split pipeline
- * (score, decide, pages, merge kernels), 3 the persistent kernel where it
+ * (score, decide+attend, merge kernels), 3 the persistent kernel where it
  * runs, else the split pipeline. */
 int rkv_set_decode_pipeline(int mode);
 

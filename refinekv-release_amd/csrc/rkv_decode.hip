@@ -2,11 +2,7 @@
 // the semantics the reference's Triton kernels in src/refinekv/kernels/ also
 // follow).  No host sync, no allocation: the caller passes a workspace.
 //
-// rkv_decode runs ONE persistent kernel per step.  Its workgroups take work
-// items from a ticket counter in the order below; an item waits only for
-// items with smaller tickets (per-head completion counters), so the earliest
-// unfinished item always belongs to a running workgroup and the grid drains
-// whatever the residency.  Per KV head h:
+// Per KV head h the step has three phases:
 //
 //   score  (h, tile)   one 64-block tile: streams the tile's key means,
 //                      ellipsoids and value means once; s = q.k_mean and the
@@ -15,36 +11,27 @@
 //                      z + log cosh delta, and the representative accumulator
 //                      sum_b exp(z_b - m_tile) v_mean_b over all its blocks
 //                      (the z partial is that attention's (m, l)).
-//   decide (h, tile)   after every score item of h: log Z / log C of each
-//                      row from the tile partials, the risk, the GQA
-//                      reduction, the non-finite fail-safes and the anchor
-//                      union; the mask, a 64-bit ballot per tile and the
-//                      access counter; then the tile's representative
-//                      partial without its expanded blocks (l recomputed over
-//                      the unexpanded blocks, acc minus the expanded blocks'
-//                      terms: rounding error below fp32 eps times the tile's
-//                      representative mass).
-//   pages  (h, rows, k) after every decide item of h: the head's expanded
-//                      pages and suffix tokens split into equal-cost ranges (a
-//                      page costs 2 * block_size, a suffix token 2); item k
-//                      also absorbs the representative partials of a 1/P
-//                      share of the head's tiles.  Exact softmax over 64-row
-//                      chunks with one shared max per chunk.
-//   merge  (h, g, cols) after every page item of h: the P partials of row g
-//                      -> bf16 output columns.
+//   attend (h, tile)   after every score item of h: log Z / log C of each row
+//                      from the tile partials, the risk, the GQA reduction,
+//                      the non-finite fail-safes and the anchor union; the
+//                      mask and the access counter; the tile's
+//                      representative partial without its expanded blocks
+//                      (l over the unexpanded blocks, acc minus the expanded
+//                      blocks' terms: rounding error below fp32 eps times the
+//                      tile's representative mass); then, from that partial,
+//                      exact attention over the tile's expanded blocks token
+//                      by token (64-row chunks, one shared max per chunk).
+//                      One (m, l, acc) partial per query row and tile.
+//   suffix (h)         exact attention over the generated tokens (a device
+//                      length clamps them), independent of the decisions.
+//   merge  (h, g, cols) the tiles' and the suffix's partials of row g ->
+//                      bf16 output columns.
 //
-// The last workgroup to leave returns the counters to zero, so a workspace
-// that was zero-filled once stays ready for the next call.  It runs on
-// request (rkv_set_decode_pipeline) where its resource rules hold (head_dim
-// <= 128, LDS per workgroup <= 64 KiB, no private-memory traffic): on a
-// multi-XCD device every cross-workgroup hand-off pays a device-scope L2
-// write-back and a same-address ticket atomic, which makes it slower than
-// kernel boundaries for this workload today.
-//
-// The default is the split pipeline: the score and decide phases as two
-// kernels, then a page kernel over global equal-cost ranges of every head's
-// expanded pages and a merge kernel.  rkv_select runs the score and decide
-// kernels only.
+// Two ways to run them.  The split pipeline (default) launches three kernels:
+// score; attend with the suffix as one more column of its grid; merge.  The
+// persistent kernel (rkv_set_decode_pipeline) runs all phases in one launch:
+// each XCD has a work queue that takes whole heads, so a head's items hand
+// data to each other through that XCD's L2 (see decode_kernel).
 //
 // Scores, radii and log-sum-exp follow fixed fp32 orders shared with the CPU
 // oracle (oracle/rkv_oracle.c), so masks and selection statistics are
@@ -59,20 +46,17 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr int64_t kMaxTiles = 2048;    // tiles per head in the decode kernel (LDS page index)
 constexpr int64_t kMaxHeads = 1024;    // KV heads in the persistent kernel (control block)
-constexpr int64_t kMaxPageItems = 64;  // page items per (head, row block)
-constexpr int64_t kMaxHeadTiles = 8192;  // split page kernel: heads * tiles in LDS
 constexpr int64_t kMaxFusedDim = 128;    // widest head_dim the persistent kernel runs
 constexpr size_t kMaxFusedLds = 64 * 1024;  // its LDS per workgroup (static + dynamic)
 constexpr size_t kMaxFusedPrivate = 64;     // its private bytes per lane (no spill traffic)
 // Control block of the persistent kernel (uint32 words; see decode_kernel).
 constexpr int kMaxQueues = 16;               // one work queue per XCD (XCC_ID is 4 bits)
 constexpr int64_t kCtlHeadTicket = 0, kCtlExits = 1, kCtlError = 2, kCtlEpoch = 3;
-constexpr int64_t kCtlQueues = 16;           // per queue: claim, ready, ticket, -
+constexpr int64_t kCtlQueues = 16;           // per queue: -, -, ticket, -
 constexpr int64_t kCtlSlots = kCtlQueues + 4 * kMaxQueues;  // per queue: kMaxHeads u64 slots
-constexpr int64_t kCtlCounters = kCtlSlots + 2 * kMaxQueues * kMaxHeads;  // 3 x kMaxHeads
-constexpr int64_t kControlWords = kCtlCounters + 3 * kMaxHeads;
+constexpr int64_t kCtlCounters = kCtlSlots + 2 * kMaxQueues * kMaxHeads;  // 2 x kMaxHeads
+constexpr int64_t kControlWords = kCtlCounters + 2 * kMaxHeads;
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a dependency wait gives up (~1 s)
 
 // Optional profiling events (rkv_set_profile_events): events[0] is recorded
@@ -93,18 +77,17 @@ thread_local int g_pipeline = 0;
 // its words are at the same place for every shape that shares a workspace.
 // ---------------------------------------------------------------------------
 struct Layout {
-  int64_t n_tiles, page_items, workers, rows_per_block, row_blocks;
+  int64_t n_tiles, rows_per_block, row_blocks;
   // Padded row strides: every head's slice of an intermediate array covers
   // whole 256-byte lines, so no cache line holds two heads' data.
   int64_t z_stride, tile_stride, part_stride;
-  int64_t control, z, delta, lse, tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc,
-      total;
+  int64_t control, z, delta, lse, tilebits, rep_acc, part_m, part_l, part_acc, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-// Rows of the GQA group one page item carries in registers: the next power
-// of two >= group (at least 4), capped so that rows * head_dim / 16
+// Rows of the GQA group one attention pass carries in registers: the next
+// power of two >= group (at least 4), capped so that rows * head_dim / 16
 // (per-lane accumulators) stays <= 64.
 inline int64_t rows_per_block(int64_t group, int64_t dim) {
   const int64_t ch = dim / 16;
@@ -116,38 +99,16 @@ inline int64_t rows_per_block(int64_t group, int64_t dim) {
   return want < p ? want : p;
 }
 
-// Split pipeline: one page worker per 64 (head, block) pairs, 1..512.
-inline int64_t workers_for(int64_t heads, int64_t n_blocks) {
-  int64_t w = (heads * n_blocks + 63) / 64;
-  if (w < 1) w = 1;
-  if (w > 512) w = 512;
-  return w;
-}
-
-// Page items per (head, row block): about 512 in all, at most one per tile
-// and at most kMaxPageItems.
-inline int64_t page_items_for(int64_t heads, int64_t row_blocks, int64_t n_tiles) {
-  int64_t p = (512 + heads * row_blocks - 1) / (heads * row_blocks);
-  if (p > n_tiles) p = n_tiles;
-  if (p > kMaxPageItems) p = kMaxPageItems;
-  return p < 1 ? 1 : p;
-}
-
 Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) {
   Layout L{};
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
   L.rows_per_block = rows_per_block(group, dim);
   L.row_blocks = (group + L.rows_per_block - 1) / L.rows_per_block;
-  L.page_items = page_items_for(heads, L.row_blocks, L.n_tiles);
-  L.workers = workers_for(heads, n_blocks);
-  const int64_t rows = heads * group;
-  // page partials: (rows, page_items) for the persistent kernel, (rows,
-  // workers) for the split pipeline
   auto round64 = [](int64_t x) { return (x + 63) / 64 * 64; };
   L.z_stride = L.n_tiles * kTile;
   L.tile_stride = round64(L.n_tiles);
-  L.part_stride = round64(L.page_items);
-  const int64_t slots = L.part_stride > L.workers ? L.part_stride : L.workers;
+  L.part_stride = round64(L.n_tiles + 1);  // one partial per tile + the suffix's
+  const int64_t rows = heads * group;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
     const int64_t at = off;
@@ -159,12 +120,10 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.delta = take(rows * L.z_stride * 4);
   L.lse = take(rows * L.tile_stride * 4 * 4);
   L.tilebits = take(heads * L.tile_stride * 8);
-  L.rep_l = take(rows * L.tile_stride * 4);
   L.rep_acc = take(rows * L.tile_stride * dim * 4);
-  L.header = take((heads + 1) * 8);
-  L.page_m = take(rows * slots * 4);
-  L.page_l = take(rows * slots * 4);
-  L.page_acc = take(rows * slots * dim * 4);
+  L.part_m = take(rows * L.part_stride * 4);
+  L.part_l = take(rows * L.part_stride * 4);
+  L.part_acc = take(rows * L.part_stride * dim * 4);
   L.total = off;
   return L;
 }
@@ -423,8 +382,7 @@ struct DecideArgs {
   float* risk_out;              // (H, G, N) or null
   float* stats_out;             // (H, G, 2) or null: log Z, log C
   unsigned long long* accessed; // or null
-  float* rep_l;                 // (H, G, tiles) or null (select only)
-  float* rep_acc;               // (H, G, tiles, D)
+  const float* rep_acc;         // (H, G, tiles, D) from the score pass (decode only)
   int64_t n_blocks, n_tiles, block, length;
   int64_t z_stride, tile_stride;  // padded row strides (see ScoreArgs)
   int group, reduction, dim;
@@ -465,7 +423,17 @@ __device__ __forceinline__ float merge_lse(const float (&m)[kLseRegs], const flo
 
 constexpr int kRiskPerThread = kMaxGroup * kTile / kThreads;  // (row, block) pairs per thread
 
-__device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int64_t tile) {
+// The tile's representative partial after its expanded blocks are removed,
+// left in LDS for the attention that follows in the same workgroup.
+struct RepShared {
+  float* acc;      // [G][D]
+  float* l;        // [G] (0: no live representative)
+  float* m;        // [G] the partial's max, inf_to_zero(tile max of z)
+  uint64_t* bits;  // the tile's expanded-block ballot
+};
+
+__device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int64_t tile,
+                                            const RepShared* rep) {
   __shared__ float gstat[kMaxGroup][2];
   __shared__ float risk_s[kMaxGroup][kTile];
   __shared__ float psel[kMaxGroup][kTile];
@@ -521,7 +489,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
 #pragma unroll
   for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
     const int g = wave + gi * kWaves;
-    tile_m[gi] = (a.rep_l && g < G) ? a.lse[((h * G + g) * a.tile_stride + tile) * 4] : 0.0f;
+    tile_m[gi] = (rep && g < G) ? a.lse[((h * G + g) * a.tile_stride + tile) * 4] : 0.0f;
   }
   constexpr int kAccPerThread = kMaxGroup * 256 / kThreads;  // G * D <= 16 * 256
   float racc[kAccPerThread];
@@ -530,7 +498,7 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
   for (int k = 0; k < kAccPerThread; ++k) {
     const int idx = tid + k * kThreads;
     racc[k] = 0.0f;
-    if (a.rep_l && idx < GD) {
+    if (rep && idx < GD) {
       const int g = idx / a.dim, d = idx % a.dim;
       racc[k] = a.rep_acc[((h * G + g) * a.tile_stride + tile) * a.dim + d];
     }
@@ -605,41 +573,46 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
       if (lane == 0) atomicAdd(a.accessed, term);
     }
   }
-  if (!a.rep_l) return;
+  if (!rep) return;
   __syncthreads();
 
   // ---- representatives of this tile: drop the expanded blocks ----------
   // (thread tid's prefetched z/delta pair k is row wave + 4k, block lane)
   const uint64_t bits = sel_bits;
   const int nsel = __popcll(bits);
+  if (tid == 0) *rep->bits = bits;
 #pragma unroll
   for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
     const int g = wave + gi * kWaves;
     if (g >= G) break;
     const bool valid = lane < nvalid;
     const bool expanded = (bits >> lane) & 1ull;
-    const float e = valid ? expf_(rz[gi] - inf_to_zero(tile_m[gi])) : 0.0f;
+    const float mt = inf_to_zero(tile_m[gi]);
+    const float e = valid ? expf_(rz[gi] - mt) : 0.0f;
     const float l = wave_sum_u(expanded ? 0.0f : e);
     psel[g][lane] = expanded ? e : 0.0f;
-    if (lane == 0) a.rep_l[(h * G + g) * a.tile_stride + tile] = nsel == nvalid ? 0.0f : l;
+    if (lane == 0) {
+      rep->l[g] = nsel == nvalid ? 0.0f : l;
+      rep->m[g] = mt;
+    }
   }
-  if (nsel == 0 || nsel == nvalid) return;
   __syncthreads();
   const int D = a.dim;
+  const bool correct = nsel > 0 && nsel < nvalid;
 #pragma unroll
   for (int k = 0; k < kAccPerThread; ++k) {
     const int idx = tid + k * kThreads;
     if (idx >= GD) break;
     const int g = idx / D, d = idx % D;
     float acc = racc[k];
-    uint64_t m = bits;
+    uint64_t m = correct ? bits : 0ull;
     while (m) {
       const int j = __builtin_ctzll(m);
       m &= m - 1;
       const float v = bf16_to_f32(a.value_mean[(h * N + tile * kTile + j) * D + d]);
       acc = acc - psel[g][j] * v;
     }
-    a.rep_acc[((h * G + g) * a.tile_stride + tile) * D + d] = acc;
+    rep->acc[idx] = acc;
   }
 }
 
@@ -650,31 +623,31 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
 }
 
 __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
-  decide_tile(a, blockIdx.y, blockIdx.x);
+  decide_tile(a, blockIdx.y, blockIdx.x, nullptr);
 }
 
 // ---------------------------------------------------------------------------
-// Phase 3: expanded pages, suffix tokens and representative partials
+// Phase 3: exact attention over a tile's expanded blocks, and over the suffix
 // ---------------------------------------------------------------------------
-struct PageArgs {
+// After deciding a tile, the same workgroup attends to the tile's expanded
+// blocks token by token, starting from the tile's representative partial, and
+// writes one (m, l, acc) partial per query row: slot `tile` of the row.  The
+// generated suffix is one more item per head (slot n_tiles), independent of
+// the decisions.  The merge then combines n_tiles + 1 partials per row.
+struct AttendArgs {
+  DecideArgs decide;
   const uint16_t* query;       // (H, G, D) bf16
   const uint16_t* key_pages;   // head h at key_pages + h * kp_hs; rows (N*B, D)
   const uint16_t* value_pages;
   const uint16_t* key_suffix;  // token t of head h at h * ks_hs + t * ks_ts
   const uint16_t* value_suffix;
-  const uint64_t* tilebits;    // (H, tiles)
   const int32_t* suffix_len_dev;  // or null
-  const float* lse;            // (H, G, tiles, 4): representative m = inf_to_zero(zm)
-  const float* rep_l;          // (H, G, tiles)
-  const float* rep_acc;        // (H, G, tiles, D)
-  float* page_m;               // (H, G, P)
-  float* page_l;
-  float* page_acc;             // (H, G, P, D)
+  float* part_m;               // (H, G, part_stride)
+  float* part_l;
+  float* part_acc;             // (H, G, part_stride, D)
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
-  int64_t suffix_cap, n_blocks, n_tiles, block, length;
-  int64_t tile_stride;         // row stride of the per-tile arrays
-  int64_t part_stride;         // row stride of the page partials (items padded to 64)
-  int group, page_items;
+  int64_t suffix_cap, part_stride;
+  int row_blocks;
   float scale;
 };
 
@@ -718,151 +691,38 @@ __device__ __forceinline__ void load_f32(const float* p, float (&out)[CH]) {
   }
 }
 
-// LDS of a page item: the head's tile ballots, their prefix and a page list.
-inline int64_t page_smem(int64_t n_tiles) {
-  return align256(n_tiles * 8) + align256((n_tiles + 1) * 4) + 8 * 8;
-}
+template <int GBM>
+struct AttendShared {
+  float xlog[GBM][kChunkRows];
+  float cmax[GBM], csum[GBM];
+};
 
-template <int D, int GBM>
-__device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, int k,
-                                          unsigned char* dyn) {
+// Folds n_rows K/V rows into the state, 64 rows per chunk: pass 1 loads the
+// chunk's K and V and writes its logits, pass 2 weighs the V rows with one
+// shared max per chunk.  row(v, kp, vp) points kp / vp at row v and returns
+// false for a masked row (kp / vp must then stay valid addresses).
+// The online-softmax state of GBM query rows is (m, l), uniform over the
+// workgroup, and acc, per 16-lane group (this lane's D/16 columns; the groups
+// are summed at the end).
+template <int D, int GBM, typename RowFn>
+__device__ __forceinline__ void attend_rows(const float (&q)[GBM][D / 16], float (&m_run)[GBM],
+                                            float (&l_run)[GBM], float (&acc)[GBM][D / 16],
+                                            int64_t n_rows, int gn, float scale, RowFn row,
+                                            const uint16_t* kdef, const uint16_t* vdef,
+                                            AttendShared<GBM>& sh) {
   constexpr int CH = D / 16;
-  const int64_t T = a.n_tiles;
-  uint64_t* bits_s = reinterpret_cast<uint64_t*>(dyn);                    // [T]
-  uint32_t* pre = reinterpret_cast<uint32_t*>(dyn + align256(T * 8));     // [T + 1]
-  int64_t* list = reinterpret_cast<int64_t*>(dyn + align256(T * 8) + align256((T + 1) * 4));
-  __shared__ uint32_t wave_tot[kWaves];
-  __shared__ float xlog[GBM][kChunkRows];
-  __shared__ float cmax[GBM], csum[GBM];
-  __shared__ float xacc[kWaves][GBM][D];
-
-  const int G = a.group, P = a.page_items;
-  const int g0 = rb * GBM;
-  const int gn = min(GBM, G - g0);
   const int tid = item_tid(), lg = tid >> 4, c = tid & 15, wave = tid / kWave;
-  const int lane = tid % kWave, grp = lane >> 4;
-  const int64_t N = a.n_blocks, B = a.block;
-
-  // ---- the head's expanded pages: ballots and their prefix --------------
-  const int64_t per = (T + kThreads - 1) / kThreads;
-  const int64_t t_begin = min((int64_t)tid * per, T), t_end = min(t_begin + per, T);
-  uint32_t mine = 0;
-  for (int64_t t = t_begin; t < t_end; ++t) {
-    const uint64_t b = a.tilebits[h * a.tile_stride + t];
-    bits_s[t] = b;
-    mine += (uint32_t)__popcll(b);
-  }
-  uint32_t n_h;
-  uint32_t run = block_exclusive_scan(mine, wave_tot, n_h);
-  for (int64_t t = t_begin; t < t_end; ++t) {
-    pre[t] = run;
-    run += (uint32_t)__popcll(bits_s[t]);
-  }
-  if (tid == 0) pre[T] = n_h;
-
-  // ---- this item's equal-cost range of pages and suffix tokens ----------
-  int64_t S = a.suffix_cap;
-  if (a.suffix_len_dev) {
-    const int64_t s = *a.suffix_len_dev;
-    S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
-  }
-  const int64_t pc = 2 * B;  // cost of one page; a suffix token costs 2
-  const int64_t C = pc * (int64_t)n_h + 2 * S;
-  const int64_t lo = C * k / P, hi = C * (k + 1) / P;
-  auto clampi = [](int64_t x, int64_t l, int64_t u) { return x < l ? l : (x > u ? u : x); };
-  auto ceil_div = [](int64_t x, int64_t d) { return x <= 0 ? 0 : (x + d - 1) / d; };
-  const int64_t p0 = clampi(ceil_div(lo, pc), 0, n_h), p1 = clampi(ceil_div(hi, pc), 0, n_h);
-  const int64_t s0 = clampi(ceil_div(lo - pc * n_h, 2), 0, S);
-  const int64_t s1 = clampi(ceil_div(hi - pc * n_h, 2), 0, S);
-  const int64_t n_prow = (p1 - p0) * B, n_rows = n_prow + (s1 - s0);
-
-  float q[GBM][CH];
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-    const int gg = g < gn ? g : 0;
-    RawBf16<CH> r = load_raw<CH>(a.query + ((h * G + g0 + gg) * D + c * CH));
-    unpack(r, q[g]);
-  }
-
-  // ---- start from the representative partials of tiles [r0, r1) ---------
-  // (m, l, acc) of each live tile, rescaled to their common max; lane group 0
-  // holds the accumulator, the other groups start at zero.
-  const int64_t r0 = T * k / P, r1 = T * (k + 1) / P;
-  float m_run[GBM], l_run[GBM], acc[GBM][CH];
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-    m_run[g] = kNegInf;
-    l_run[g] = 0.0f;
-#pragma unroll
-    for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
-    if (g >= gn) continue;
-    const int64_t row = h * G + g0 + g;
-    float mr = kNegInf;
-    for (int64_t t = r0; t < r1; ++t) {
-      const float lt = a.rep_l[row * a.tile_stride + t];
-      const float mt = inf_to_zero(a.lse[(row * a.tile_stride + t) * 4]);
-      if (lt > 0.0f) mr = fmaxf(mr, mt);
-    }
-    if (mr == kNegInf) continue;
-    float l = 0.0f;
-    for (int64_t t = r0; t < r1; ++t) {
-      const float lt = a.rep_l[row * a.tile_stride + t];
-      const float mt = inf_to_zero(a.lse[(row * a.tile_stride + t) * 4]);
-      float at[CH];
-      load_f32<CH>(a.rep_acc + (row * a.tile_stride + t) * D + c * CH, at);
-      if (lt > 0.0f) {
-        const float e = __builtin_amdgcn_exp2f((mt - mr) * kLog2e);
-        l = l + lt * e;
-        if (lg == 0) {
-#pragma unroll
-          for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + at[i] * e;
-        }
-      }
-    }
-    m_run[g] = mr;
-    l_run[g] = l;
-  }
-
-  // Rows in chunks of 64: pass 1 loads K/V and writes the chunk's logits,
-  // pass 2 weighs the V rows with one shared max (no per-row rescaling).
+  const int lane = tid % kWave;
   for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
-    // pages touched by this chunk -> block indices (block_size divides 64)
-    const int64_t j_first = c0 < n_prow ? p0 + c0 / B : p1;
-    const int64_t j_last = min(c0 + kChunkRows, n_prow) - 1;
-    const int64_t n_pages = c0 < n_prow ? p0 + j_last / B - j_first + 1 : 0;
-    __syncthreads();
-    if (tid < n_pages) {
-      const int64_t j = j_first + tid;
-      int64_t lo_t = 0, hi_t = T - 1;
-      while (lo_t < hi_t) {
-        const int64_t mid = (lo_t + hi_t + 1) >> 1;
-        if ((int64_t)pre[mid] <= j) lo_t = mid; else hi_t = mid - 1;
-      }
-      list[tid] = lo_t * kTile + nth_set_bit(bits_s[lo_t], (int)(j - pre[lo_t]));
-    }
-    __syncthreads();
+    __syncthreads();  // the previous chunk's logits are consumed
     RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
-    bool ok[kRowBatch];
+    uint32_t okm = 0;
 #pragma unroll
     for (int u = 0; u < kRowBatch; ++u) {
       const int64_t v = c0 + lg + 16 * u;
-      const uint16_t* kp = a.key_pages + h * a.kp_hs;  // a valid row for idle lanes
-      const uint16_t* vp = a.value_pages + h * a.vp_hs;
-      ok[u] = false;
-      if (v < n_prow) {
-        const int64_t jj = v / B, t = v - jj * B;
-        const int64_t b = list[p0 + jj - j_first];
-        if (t < block_count(b, N, B, a.length)) {
-          ok[u] = true;
-          kp += (b * B + t) * D;
-          vp += (b * B + t) * D;
-        }
-      } else if (v < n_rows) {
-        const int64_t kk = s0 + (v - n_prow);
-        ok[u] = true;
-        kp = a.key_suffix + h * a.ks_hs + kk * a.ks_ts;
-        vp = a.value_suffix + h * a.vs_hs + kk * a.vs_ts;
-      }
+      const uint16_t* kp = kdef;
+      const uint16_t* vp = vdef;
+      if (v < n_rows && row(v, kp, vp)) okm |= 1u << u;
       kr[u] = load_raw<CH>(kp + c * CH);
       vr[u] = load_raw<CH>(vp + c * CH);
     }
@@ -873,31 +733,32 @@ __device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, 
       row_logits<D, GBM>(q, kv, x);
       if (c == 15) {
 #pragma unroll
-        for (int g = 0; g < GBM; ++g) xlog[g][lg + 16 * u] = ok[u] ? x[g] * a.scale : kNegInf;
+        for (int g = 0; g < GBM; ++g)
+          sh.xlog[g][lg + 16 * u] = ((okm >> u) & 1u) ? x[g] * scale : kNegInf;
       }
     }
     __syncthreads();
     // chunk max and sum per query row, one wave per row
     for (int g = wave; g < gn; g += kWaves) {
-      const float x = xlog[g][lane];
+      const float x = sh.xlog[g][lane];
       const float cm = wave_nanmax_u(x);
       const float ms = cm == kNegInf ? 0.0f : cm;
       const float sum = wave_sum_u(__builtin_amdgcn_exp2f((x - ms) * kLog2e));
       if (lane == 0) {
-        cmax[g] = cm;
-        csum[g] = sum;
+        sh.cmax[g] = cm;
+        sh.csum[g] = sum;
       }
     }
     __syncthreads();
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       if (g >= gn) break;
-      const float cm = cmax[g];
+      const float cm = sh.cmax[g];
       const float mn = fmaxf(m_run[g], cm);
       if (mn == kNegInf) continue;
       const float sa = __builtin_amdgcn_exp2f((m_run[g] - mn) * kLog2e);
       const float sb = __builtin_amdgcn_exp2f((cm - mn) * kLog2e);
-      l_run[g] = l_run[g] * sa + csum[g] * sb;
+      l_run[g] = l_run[g] * sa + sh.csum[g] * sb;
 #pragma unroll
       for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * sa;
       m_run[g] = mn;
@@ -910,14 +771,23 @@ __device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, 
       for (int g = 0; g < GBM; ++g) {
         if (g >= gn) break;
         const float ms = m_run[g] == kNegInf ? 0.0f : m_run[g];
-        const float p = __builtin_amdgcn_exp2f((xlog[g][lg + 16 * u] - ms) * kLog2e);
+        const float p = __builtin_amdgcn_exp2f((sh.xlog[g][lg + 16 * u] - ms) * kLog2e);
 #pragma unroll
         for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + p * v[i];
       }
     }
   }
+}
 
-  // sum the 16 lane groups (one shared max: plain adds) and write
+// Sums the 16 lane groups (one shared max: plain adds) and writes rows
+// row0 .. row0+gn-1 of the partial arrays at `slot`.
+template <int D, int GBM>
+__device__ __forceinline__ void write_partial(const float (&m_run)[GBM], const float (&l_run)[GBM],
+                                              float (&acc)[GBM][D / 16], int gn,
+                                              const AttendArgs& a, int64_t row0, int64_t slot,
+                                              float (&xacc)[kWaves][GBM][D]) {
+  constexpr int CH = D / 16;
+  const int tid = item_tid(), c = tid & 15, wave = tid / kWave, grp = (tid % kWave) >> 4;
 #pragma unroll
   for (int g = 0; g < GBM; ++g) {
 #pragma unroll
@@ -938,26 +808,147 @@ __device__ __forceinline__ void page_item(const PageArgs& a, int64_t h, int rb, 
   __syncthreads();
   for (int idx = tid; idx < gn * D; idx += kThreads) {
     const int g = idx / D, d = idx % D;
-    const int64_t slot = (h * G + g0 + g) * a.part_stride + k;
-    const float sum = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
-    a.page_acc[slot * D + d] = sum;
+    const int64_t at = (row0 + g) * a.part_stride + slot;
+    a.part_acc[at * D + d] = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
     if (d == 0) {
-      a.page_m[slot] = m_run[g];
-      a.page_l[slot] = l_run[g];
+      a.part_m[at] = m_run[g];
+      a.part_l[at] = l_run[g];
     }
   }
 }
 
+template <int D, int GBM>
+__device__ __forceinline__ void load_query(const AttendArgs& a, int64_t h, int g0, int gn,
+                                           float (&q)[GBM][D / 16]) {
+  constexpr int CH = D / 16;
+  const int c = item_tid() & 15;
+  const int G = a.decide.group;
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+    const int gg = g < gn ? g : 0;
+    RawBf16<CH> r = load_raw<CH>(a.query + ((h * G + g0 + gg) * D + c * CH));
+    unpack(r, q[g]);
+  }
+}
+
+// Decide tile `tile` of head h (RepShared in `dyn`), then attend to its
+// expanded blocks from its representative partial.
+template <int D, int GBM>
+__device__ __forceinline__ void decide_attend_tile(const AttendArgs& a, int64_t h, int64_t tile,
+                                                   unsigned char* dyn) {
+  constexpr int CH = D / 16;
+  __shared__ AttendShared<GBM> sh;
+  __shared__ float xacc[kWaves][GBM][D];
+  __shared__ int32_t blocks[kTile];
+  __shared__ uint64_t tile_bits;
+  const DecideArgs& da = a.decide;
+  const int G = da.group;
+  float* rep_acc = reinterpret_cast<float*>(dyn);
+  RepShared rep{rep_acc, rep_acc + G * D, rep_acc + G * D + G, &tile_bits};
+  decide_tile(da, h, tile, &rep);
+  __syncthreads();
+
+  const int tid = item_tid(), lg = tid >> 4, c = tid & 15;
+  const uint64_t bits = tile_bits;
+  const int nsel = __popcll(bits);
+  if (tid < nsel) blocks[tid] = (int32_t)(tile * kTile + nth_set_bit(bits, tid));
+  __syncthreads();
+  const int64_t N = da.n_blocks, B = da.block, L = da.length;
+  const uint16_t* kbase = a.key_pages + h * a.kp_hs;
+  const uint16_t* vbase = a.value_pages + h * a.vp_hs;
+  const int32_t* blk = blocks;
+  auto row = [=](int64_t v, const uint16_t*& kp, const uint16_t*& vp) {
+    const int64_t j = v / B, t = v - j * B;
+    const int64_t b = blk[j];
+    if (t >= block_count(b, N, B, L)) return false;
+    kp = kbase + (b * B + t) * D;
+    vp = vbase + (b * B + t) * D;
+    return true;
+  };
+  for (int rb = 0; rb < a.row_blocks; ++rb) {
+    const int g0 = rb * GBM, gn = min(GBM, G - g0);
+    float q[GBM][CH];
+    load_query<D, GBM>(a, h, g0, gn, q);
+    float m_run[GBM], l_run[GBM], acc[GBM][CH];
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      const int gg = g < gn ? g0 + g : 0;
+      const bool live = g < gn && rep.l[gg] > 0.0f;
+      m_run[g] = live ? rep.m[gg] : kNegInf;
+      l_run[g] = live ? rep.l[gg] : 0.0f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i)
+        acc[g][i] = (live && lg == 0) ? rep.acc[gg * D + c * CH + i] : 0.0f;
+    }
+    attend_rows<D, GBM>(q, m_run, l_run, acc, (int64_t)nsel * B, gn, a.scale, row, kbase, vbase,
+                        sh);
+    write_partial<D, GBM>(m_run, l_run, acc, gn, a, h * G + g0, tile, xacc);
+  }
+}
+
+// Attention of head h's query rows over the generated suffix (slot n_tiles).
+template <int D, int GBM>
+__device__ __forceinline__ void suffix_item(const AttendArgs& a, int64_t h) {
+  constexpr int CH = D / 16;
+  __shared__ AttendShared<GBM> sh;
+  __shared__ float xacc[kWaves][GBM][D];
+  const int G = a.decide.group;
+  int64_t S = a.suffix_cap;
+  if (a.suffix_len_dev) {
+    const int64_t s = *a.suffix_len_dev;
+    S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
+  }
+  const uint16_t* kbase = a.key_pages + h * a.kp_hs;  // valid rows for masked lanes
+  const uint16_t* vbase = a.value_pages + h * a.vp_hs;
+  const uint16_t* ks = a.key_suffix + h * a.ks_hs;
+  const uint16_t* vs = a.value_suffix + h * a.vs_hs;
+  const int64_t kts = a.ks_ts, vts = a.vs_ts;
+  auto row = [=](int64_t v, const uint16_t*& kp, const uint16_t*& vp) {
+    kp = ks + v * kts;
+    vp = vs + v * vts;
+    return true;
+  };
+  for (int rb = 0; rb < a.row_blocks; ++rb) {
+    const int g0 = rb * GBM, gn = min(GBM, G - g0);
+    float q[GBM][CH];
+    load_query<D, GBM>(a, h, g0, gn, q);
+    float m_run[GBM], l_run[GBM], acc[GBM][CH];
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      m_run[g] = kNegInf;
+      l_run[g] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
+    }
+    attend_rows<D, GBM>(q, m_run, l_run, acc, S, gn, a.scale, row, kbase, vbase, sh);
+    write_partial<D, GBM>(m_run, l_run, acc, gn, a, h * G + g0, a.decide.n_tiles, xacc);
+  }
+}
+
+inline size_t attend_smem(int64_t group, int64_t dim) {
+  return sizeof(float) * (group * dim + 2 * group);
+}
+
+// Split pipeline, kernel 2: grid (tiles + 1, H); the last column is the suffix.
+template <int D, int GBM>
+__global__ __launch_bounds__(kThreads) void attend_kernel(AttendArgs a) {
+  extern __shared__ unsigned char attend_dyn[];
+  if ((int64_t)blockIdx.x == a.decide.n_tiles)
+    suffix_item<D, GBM>(a, blockIdx.y);
+  else
+    decide_attend_tile<D, GBM>(a, blockIdx.y, blockIdx.x, attend_dyn);
+}
+
 // ---------------------------------------------------------------------------
-// Phase 4: merge a row's page-item partials -> bf16 output columns
+// Phase 4: merge a row's partials -> bf16 output columns
 // ---------------------------------------------------------------------------
 struct MergeArgs {
-  const float* page_m;    // (H, G, P)
-  const float* page_l;
-  const float* page_acc;  // (H, G, P, D)
+  const float* part_m;    // (H, G, part_stride)
+  const float* part_l;
+  const float* part_acc;  // (H, G, part_stride, D)
   uint16_t* out;          // (H*G, D)
-  int64_t part_stride;    // row stride of the page partials
-  int group, page_items, dim;
+  int64_t part_stride;    // row stride of the partials
+  int group, parts, dim;  // parts = n_tiles + 1
 };
 
 constexpr int kMergeD = 32;                   // output columns per item
@@ -968,14 +959,14 @@ __device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g,
   __shared__ float red[kWaves];
   __shared__ float num_s[kMergeK][kMergeD];
   __shared__ float den_s[kMergeK];
-  const int P = a.page_items, D = a.dim;
+  const int P = a.parts, D = a.dim;
   const int64_t r = h * a.group + g;
   const int tid = item_tid(), lane = tid % kWave, wave = tid / kWave;
 
   float mx = kNegInf;
   for (int i = tid; i < P; i += kThreads) {
-    const float l = a.page_l[r * a.part_stride + i];
-    const float m = a.page_m[r * a.part_stride + i];
+    const float l = a.part_l[r * a.part_stride + i];
+    const float m = a.part_m[r * a.part_stride + i];
     if (l > 0.0f) mx = fmaxf(mx, m);
   }
   mx = wave_nanmax_u(mx);
@@ -994,9 +985,9 @@ __device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g,
     for (int u = 0; u < kMergeBatch; ++u) {
       const int i = i0 + u * kMergeK;
       const int ii = i < P ? i : 0;
-      mv[u] = a.page_m[r * a.part_stride + ii];
-      lv[u] = a.page_l[r * a.part_stride + ii];
-      av[u] = a.page_acc[(r * a.part_stride + ii) * D + dd];
+      mv[u] = a.part_m[r * a.part_stride + ii];
+      lv[u] = a.part_l[r * a.part_stride + ii];
+      av[u] = a.part_acc[(r * a.part_stride + ii) * D + dd];
     }
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
@@ -1020,382 +1011,20 @@ __device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g,
   }
 }
 
-// ---------------------------------------------------------------------------
-// Split pipeline, kernel 3: expanded pages and suffix tokens
-// ---------------------------------------------------------------------------
-struct SplitPageArgs {
-  const uint16_t* query;       // (H, G, D) bf16
-  const uint16_t* key_pages;   // head h at key_pages + h * kp_hs; rows (N*B, D)
-  const uint16_t* value_pages;
-  const uint16_t* key_suffix;  // token t of head h at h * ks_hs + t * ks_ts
-  const uint16_t* value_suffix;
-  const uint64_t* tilebits;    // (H, tiles)
-  const int32_t* suffix_len_dev;  // or null
-  int64_t* header;             // (H + 1): cost start of each head's work, [H] = total
-  float* page_m;               // (H*G, W), written only by workers touching the head
-  float* page_l;
-  float* page_acc;             // (H*G, W, D)
-  int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
-  int64_t suffix_cap, n_blocks, n_tiles, block, length;
-  int64_t tile_stride;         // head stride of tilebits (tiles padded to 64)
-  int heads, group, workers, rows_per_block;
-  float scale;
-};
-
-// Ballot of dense (head, tile) index ht (ht = h * tiles + t).
-__device__ __forceinline__ uint64_t head_tile_bits(const SplitPageArgs& a, int64_t ht) {
-  const int64_t h = ht / a.n_tiles;
-  return a.tilebits[h * a.tile_stride + (ht - h * a.n_tiles)];
+// Split pipeline, kernel 3: grid (H * G, ceil(D / 32)).
+__global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
+  merge_item(a, blockIdx.x / a.group, blockIdx.x % a.group, blockIdx.y);
 }
-
-inline size_t split_page_smem(int64_t heads, int64_t n_tiles) {
-  return (size_t)(align256((heads * n_tiles + 1) * 4) + align256((heads + 1) * 8) +
-                  sizeof(int64_t) * 8);
-}
-
-template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) void split_page_kernel(SplitPageArgs a) {
-  constexpr int CH = D / 16;
-  extern __shared__ unsigned char smem_raw[];
-  const int64_t T = a.n_tiles, H = a.heads, HT = H * T;
-  uint32_t* pre = reinterpret_cast<uint32_t*>(smem_raw);  // [HT + 1] page prefix, head-major
-  int64_t* hs = reinterpret_cast<int64_t*>(smem_raw + align256((HT + 1) * 4));  // [H + 1]
-  int64_t* list = hs + align256((H + 1) * 8) / 8;                               // [8]
-  __shared__ uint32_t wave_tot[kWaves];
-  __shared__ float xlog[GBM][kChunkRows];
-  __shared__ float cmax[GBM], csum[GBM];
-  __shared__ float xacc[kWaves][GBM][D];
-
-  const int w = blockIdx.x;
-  const int g0 = blockIdx.y * a.rows_per_block;
-  const int gn = min(a.rows_per_block, a.group - g0);
-  const int G = a.group;
-  const int tid = item_tid(), lg = tid >> 4, c = tid & 15, wave = tid / kWave;
-  const int lane = tid % kWave, grp = lane >> 4;
-  const int64_t N = a.n_blocks, B = a.block;
-
-  // ---- expanded-page prefix over every (head, tile) ----------------------
-  const int64_t per = (HT + kThreads - 1) / kThreads;
-  const int64_t t_begin = min((int64_t)tid * per, HT), t_end = min(t_begin + per, HT);
-  uint32_t mine = 0;
-  for (int64_t t = t_begin; t < t_end; ++t) mine += (uint32_t)__popcll(head_tile_bits(a, t));
-  uint32_t total;
-  uint32_t run = block_exclusive_scan(mine, wave_tot, total);
-  for (int64_t t = t_begin; t < t_end; ++t) {
-    pre[t] = run;
-    run += (uint32_t)__popcll(head_tile_bits(a, t));
-  }
-  if (tid == 0) pre[HT] = total;
-  __syncthreads();
-
-  int64_t S = a.suffix_cap;
-  if (a.suffix_len_dev) {
-    const int64_t s = *a.suffix_len_dev;
-    S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
-  }
-  const int64_t pc = 2 * B;  // cost of one page; a suffix token costs 2
-  for (int64_t h = tid; h <= H; h += kThreads) hs[h] = pc * (int64_t)pre[h * T] + 2 * S * h;
-  __syncthreads();
-  const int64_t C = hs[H];
-  if (w == 0 && blockIdx.y == 0)
-    for (int64_t h = tid; h <= H; h += kThreads) a.header[h] = hs[h];
-  const int64_t lo = C * w / a.workers, hi = C * (w + 1) / a.workers;
-  auto clampi = [](int64_t x, int64_t l, int64_t u) { return x < l ? l : (x > u ? u : x); };
-  auto ceil_div = [](int64_t x, int64_t d) { return x <= 0 ? 0 : (x + d - 1) / d; };
-
-  // first head whose range may hold lo: the largest h with hs[h] <= lo
-  int64_t hb = 0, ht = H - 1;
-  while (hb < ht) {
-    const int64_t mid = (hb + ht + 1) >> 1;
-    if (hs[mid] <= lo) hb = mid; else ht = mid - 1;
-  }
-  for (int64_t h = hb; h < H && hs[h] < hi; ++h) {
-    const int64_t hs_h = hs[h], he_h = hs[h + 1];
-    if (!(lo < he_h && hi > hs_h)) continue;
-    const int64_t first = pre[h * T];
-    const int64_t n_h = (int64_t)pre[(h + 1) * T] - first;
-    const int64_t lo_h = lo - hs_h, hi_h = hi - hs_h;
-    const int64_t p0 = clampi(ceil_div(lo_h, pc), 0, n_h), p1 = clampi(ceil_div(hi_h, pc), 0, n_h);
-    const int64_t s0 = clampi(ceil_div(lo_h - pc * n_h, 2), 0, S);
-    const int64_t s1 = clampi(ceil_div(hi_h - pc * n_h, 2), 0, S);
-    const int64_t n_prow = (p1 - p0) * B, n_rows = n_prow + (s1 - s0);
-
-    float q[GBM][CH];
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      const int gg = g < gn ? g : 0;
-      RawBf16<CH> r = load_raw<CH>(a.query + ((h * G + g0 + gg) * D + c * CH));
-      unpack(r, q[g]);
-    }
-    float m_run[GBM], l_run[GBM], acc[GBM][CH];
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      m_run[g] = kNegInf;
-      l_run[g] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
-    }
-
-    // Rows in chunks of 64: pass 1 loads K/V and writes the chunk's logits,
-    // pass 2 weighs the V rows with one shared max (no per-row rescaling).
-    for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
-      // pages touched by this chunk -> block indices
-      const int64_t j_first = c0 < n_prow ? p0 + c0 / B : p1;
-      const int64_t j_last = min(c0 + kChunkRows, n_prow) - 1;
-      const int64_t n_pages = c0 < n_prow ? p0 + j_last / B - j_first + 1 : 0;
-      __syncthreads();
-      if (tid < n_pages) {
-        const int64_t j = first + j_first + tid;
-        int64_t lo_t = h * T, hi_t = h * T + T - 1;
-        while (lo_t < hi_t) {
-          const int64_t mid = (lo_t + hi_t + 1) >> 1;
-          if ((int64_t)pre[mid] <= j) lo_t = mid; else hi_t = mid - 1;
-        }
-        list[tid] = (lo_t - h * T) * kTile +
-                    nth_set_bit(head_tile_bits(a, lo_t), (int)(j - pre[lo_t]));
-      }
-      __syncthreads();
-      RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
-      bool ok[kRowBatch];
-#pragma unroll
-      for (int u = 0; u < kRowBatch; ++u) {
-        const int64_t v = c0 + lg + 16 * u;
-        const uint16_t* kp = a.key_pages + h * a.kp_hs;  // a valid row for idle lanes
-        const uint16_t* vp = a.value_pages + h * a.vp_hs;
-        ok[u] = false;
-        if (v < n_prow) {
-          const int64_t jj = v / B, t = v - jj * B;
-          const int64_t b = list[p0 + jj - j_first];
-          if (t < block_count(b, N, B, a.length)) {
-            ok[u] = true;
-            kp += (b * B + t) * D;
-            vp += (b * B + t) * D;
-          }
-        } else if (v < n_rows) {
-          const int64_t k = s0 + (v - n_prow);
-          ok[u] = true;
-          kp = a.key_suffix + h * a.ks_hs + k * a.ks_ts;
-          vp = a.value_suffix + h * a.vs_hs + k * a.vs_ts;
-        }
-        kr[u] = load_raw<CH>(kp + c * CH);
-        vr[u] = load_raw<CH>(vp + c * CH);
-      }
-#pragma unroll
-      for (int u = 0; u < kRowBatch; ++u) {
-        float kv[CH], x[GBM];
-        unpack(kr[u], kv);
-        row_logits<D, GBM>(q, kv, x);
-        if (c == 15) {
-#pragma unroll
-          for (int g = 0; g < GBM; ++g) xlog[g][lg + 16 * u] = ok[u] ? x[g] * a.scale : kNegInf;
-        }
-      }
-      __syncthreads();
-      // chunk max and sum per query row, one wave per row
-      for (int g = wave; g < gn; g += kWaves) {
-        const float x = xlog[g][lane];
-        const float cm = wave_nanmax_u(x);
-        const float ms = cm == kNegInf ? 0.0f : cm;
-        const float sum = wave_sum_u(__builtin_amdgcn_exp2f((x - ms) * kLog2e));
-        if (lane == 0) {
-          cmax[g] = cm;
-          csum[g] = sum;
-        }
-      }
-      __syncthreads();
-#pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        if (g >= gn) break;
-        const float cm = cmax[g];
-        const float mn = fmaxf(m_run[g], cm);
-        if (mn == kNegInf) continue;
-        const float sa = __builtin_amdgcn_exp2f((m_run[g] - mn) * kLog2e);
-        const float sb = __builtin_amdgcn_exp2f((cm - mn) * kLog2e);
-        l_run[g] = l_run[g] * sa + csum[g] * sb;
-#pragma unroll
-        for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * sa;
-        m_run[g] = mn;
-      }
-#pragma unroll
-      for (int u = 0; u < kRowBatch; ++u) {
-        float v[CH];
-        unpack(vr[u], v);
-#pragma unroll
-        for (int g = 0; g < GBM; ++g) {
-          if (g >= gn) break;
-          const float ms = m_run[g] == kNegInf ? 0.0f : m_run[g];
-          const float p = __builtin_amdgcn_exp2f((xlog[g][lg + 16 * u] - ms) * kLog2e);
-#pragma unroll
-          for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + p * v[i];
-        }
-      }
-    }
-
-    // sum the 16 lane groups (one shared max: plain adds) and write
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 16);
-        acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 32);
-      }
-    }
-    __syncthreads();
-    if (grp == 0) {
-#pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        if (g >= gn) break;
-#pragma unroll
-        for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = acc[g][i];
-      }
-    }
-    __syncthreads();
-    for (int idx = tid; idx < gn * D; idx += kThreads) {
-      const int g = idx / D, d = idx % D;
-      const int64_t slot = (h * G + g0 + g) * a.workers + w;
-      const float sum = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
-      a.page_acc[slot * D + d] = sum;
-      if (d == 0) {
-        a.page_m[slot] = m_run[g];
-        a.page_l[slot] = l_run[g];
-      }
-    }
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Split pipeline, kernel 4: merge representative and page partials -> bf16 output
-// ---------------------------------------------------------------------------
-struct SplitMergeArgs {
-  const float* lse;       // rep m = inf_to_zero(zm)
-  const float* rep_l;
-  const float* rep_acc;
-  const int64_t* header;  // page-work cost starts per head (page kernel)
-  const float* page_m;
-  const float* page_l;
-  const float* page_acc;
-  uint16_t* out;          // (H*G, D)
-  int64_t n_tiles;
-  int64_t tile_stride;    // row stride of the per-tile arrays
-  int heads, group, workers, dim;
-};
-
-
-inline size_t split_merge_smem(int64_t n_tiles, int64_t workers) {
-  const int64_t P = n_tiles + workers;
-  return sizeof(float) * 2 * P + sizeof(int) * P;
-}
-
-__global__ __launch_bounds__(kThreads) void split_merge_kernel(SplitMergeArgs a) {
-  extern __shared__ unsigned char smem_raw[];
-  const int64_t T = a.n_tiles, W = a.workers;
-  float* pm = reinterpret_cast<float*>(smem_raw);  // [P] partial max (natural log)
-  float* pl = pm + (T + W);                         // [P] partial l (0 if dead)
-  int* live = reinterpret_cast<int*>(pl + (T + W)); // [P] live partial indices, in order
-  __shared__ uint32_t wave_tot[kWaves];
-  __shared__ float red[kWaves];
-  __shared__ float num_s[kMergeK][kMergeD];
-  __shared__ float den_s[kMergeK];
-  const int64_t r = blockIdx.x;
-  const int64_t h = r / a.group;
-  const int d0 = blockIdx.y * kMergeD;
-  const int tid = item_tid(), lane = tid % kWave, wave = tid / kWave;
-  const int D = a.dim;
-
-  // workers whose cost range meets head h's (the page kernel's own test):
-  // w_first = ceil(W (hs+1) / C) - 1, w_last = ceil(W he / C) - 1
-  const int64_t hs = a.header[h], he = a.header[h + 1], C = a.header[a.heads];
-  int64_t w_first = 0, w_last = -1;
-  if (C > 0 && he > hs) {
-    w_first = (W * (hs + 1) + C - 1) / C - 1;
-    w_last = (W * he + C - 1) / C - 1;
-    if (w_first < 0) w_first = 0;
-    if (w_last > W - 1) w_last = W - 1;
-  }
-  const int64_t P = T + (w_last - w_first + 1);
-
-  float mx = kNegInf;
-  for (int64_t i = tid; i < P; i += kThreads) {
-    float m, l;
-    if (i < T) {
-      m = inf_to_zero(a.lse[(r * a.tile_stride + i) * 4]);
-      l = a.rep_l[r * a.tile_stride + i];
-    } else {
-      const int64_t w = w_first + (i - T);
-      m = a.page_m[r * W + w];
-      l = a.page_l[r * W + w];
-    }
-    const bool alive = l > 0.0f;
-    pm[i] = m;
-    pl[i] = alive ? l : 0.0f;
-    if (alive) mx = fmaxf(mx, m);
-  }
-  mx = wave_nanmax_u(mx);
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float Ms = M == kNegInf ? 0.0f : M;
-
-  // live list in index order (chunked block scans)
-  int64_t n_live = 0;
-  for (int64_t base = 0; base < P; base += kThreads) {
-    const int64_t i = base + tid;
-    const bool alive = i < P && pl[i] > 0.0f;
-    uint32_t tot;
-    const uint32_t pos = block_exclusive_scan(alive ? 1u : 0u, wave_tot, tot);
-    if (alive) live[n_live + pos] = (int)i;
-    n_live += tot;
-  }
-  __syncthreads();
-
-  const int dl = tid % kMergeD, k = tid / kMergeD;
-  const int d = d0 + dl;
-  const int dd = d < D ? d : 0;
-  float num = 0.0f, den = 0.0f;
-  constexpr int kBatch = 8;
-  for (int64_t q0 = k; q0 < n_live; q0 += kMergeK * kBatch) {
-    int idx[kBatch];
-    float accv[kBatch];
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int64_t q = q0 + (int64_t)u * kMergeK;
-      idx[u] = q < n_live ? live[q] : -1;
-      const int64_t i = idx[u] < 0 ? 0 : idx[u];
-      accv[u] = i < T ? a.rep_acc[(r * a.tile_stride + i) * D + dd]
-                      : a.page_acc[(r * W + w_first + (i - T)) * D + dd];
-    }
-#pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      if (idx[u] < 0) break;
-      const float e = __builtin_amdgcn_exp2f((pm[idx[u]] - Ms) * kLog2e);
-      den = den + pl[idx[u]] * e;
-      num = num + accv[u] * e;
-    }
-  }
-  num_s[k][dl] = num;
-  if (dl == 0) den_s[k] = den;
-  __syncthreads();
-  if (tid < kMergeD && d < D) {
-    float n = num_s[0][tid], den_all = den_s[0];
-    for (int kk = 1; kk < kMergeK; ++kk) {
-      n = n + num_s[kk][tid];
-      den_all = den_all + den_s[kk];
-    }
-    a.out[r * D + d] = bf16_rne(n / fmaxf(den_all, 1e-30f));
-  }
-}
-
 
 // ---------------------------------------------------------------------------
 // The persistent decode kernel
 // ---------------------------------------------------------------------------
 struct DecodeArgs {
   ScoreArgs score;
-  DecideArgs decide;
-  PageArgs page;
+  AttendArgs attend;
   MergeArgs merge;
   uint32_t* control;  // kControlWords words, zero when the workspace is new
-  int heads, row_blocks, merge_cols;
+  int heads, merge_cols;
 };
 
 // This workgroup's XCD (HW_REG_XCC_ID bits [3:0]).
@@ -1450,15 +1079,15 @@ __device__ __forceinline__ const DecodeArgs* item_args() {
 // Work distribution.  Every XCD has its own queue; its workgroups draw queue
 // tickets, and a queue takes whole KV heads from a device-wide head counter,
 // so all items of a head run on one XCD and hand data to each other through
-// that XCD's L2.  A head is K consecutive tickets of its queue (its score,
-// decide, page and merge items, in that order); the workgroup that draws the
-// first ticket of a head's slot claims the head and publishes it in the slot
-// (epoch-tagged, so slots need no reset).  An item waits only for items with
-// smaller tickets of its own queue (the slot's first ticket, or its head's
-// earlier phases), so the smallest unfinished ticket of every queue is held
-// by a running workgroup: the grid drains whatever the residency.  Queue
-// state is reset by the queue's first workgroup of each launch (epoch), the
-// device-wide counters by the last workgroup out.
+// that XCD's L2.  A head is K consecutive tickets of its queue (its score
+// items, its decide+attend items and suffix item, its merge items, in that
+// order); the workgroup that draws the first ticket of a head's slot claims
+// the head and publishes it in the slot (tagged with the launch's epoch, so
+// slots need no reset).  An item waits only for items with smaller tickets of
+// its own queue (the slot's first ticket, or its head's earlier phase), so the
+// smallest unfinished ticket of every queue is held by a running workgroup:
+// the grid drains whatever the residency.  The last workgroup out resets the
+// tickets and counters and advances the epoch.
 template <int D, int GBM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void decode_kernel(DecodeArgs a) {
@@ -1467,30 +1096,21 @@ void decode_kernel(DecodeArgs a) {
   uint32_t* ctl = a.control;
   uint32_t* err = ctl + kCtlError;
   uint32_t* score_done = ctl + kCtlCounters;
-  uint32_t* decide_done = score_done + kMaxHeads;
-  uint32_t* page_done = decide_done + kMaxHeads;
+  uint32_t* attend_done = score_done + kMaxHeads;
   const uint32_t q = xcc_id();
   uint32_t* queue = ctl + kCtlQueues + 4 * q;  // [0] claim, [1] ready, [2] ticket
   uint64_t* slots = reinterpret_cast<uint64_t*>(ctl + kCtlSlots) + (int64_t)q * kMaxHeads;
   const uint32_t T = (uint32_t)a.score.n_tiles;
-  const uint32_t P = (uint32_t)a.page.page_items;
-  const uint32_t page_per_head = (uint32_t)a.row_blocks * P;
   const uint32_t merge_per_head = (uint32_t)a.merge.group * (uint32_t)a.merge_cols;
-  const uint32_t e_score = T, e_decide = 2 * T, e_page = e_decide + page_per_head;
-  const uint32_t K = e_page + merge_per_head;  // tickets per head
+  // per head: T score items, T decide+attend items, the suffix item, merges
+  const uint32_t e_score = T, e_attend = 2 * T, e_suffix = e_attend + 1;
+  const uint32_t K = e_suffix + merge_per_head;  // tickets per head
   const int tid = threadIdx.x;
 
   if (tid == 0) {
-    // this launch's tag; the queue's first workgroup of the launch resets it
-    const uint32_t tag = load_dev(ctl + kCtlEpoch) + 1;
-    if (__hip_atomic_fetch_max(queue, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < tag) {
-      __hip_atomic_store(queue + 2, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __builtin_amdgcn_s_waitcnt(0);
-      __hip_atomic_store(queue + 1, tag, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    } else {
-      poll_at_least(queue + 1, tag, err);
-    }
-    s_tag = tag;
+    // this launch's slot tag, and a first ticket (queue tickets start at 0:
+    // the previous launch's last workgroup reset them)
+    s_tag = load_dev(ctl + kCtlEpoch) + 1;
     s_ticket = __hip_atomic_fetch_add(queue + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
   __syncthreads();
@@ -1508,8 +1128,7 @@ void decode_kernel(DecodeArgs a) {
                                      __HIP_MEMORY_SCOPE_AGENT);
           if (h < (uint32_t)a.heads) {
             __hip_atomic_store(score_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(decide_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(page_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(attend_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             __builtin_amdgcn_s_waitcnt(0);
           } else {
             h = 0xFFFFFFFFu;
@@ -1544,20 +1163,18 @@ void decode_kernel(DecodeArgs a) {
       const ScoreArgs sa = item_args()->score;
       score_tile<D, true>(sa, h, i, decode_dyn);
       signal_done(score_done + h);
-    } else if (i < e_decide) {
+    } else if (i < e_attend) {
       wait_count(score_done + h, T, err);
-      const DecideArgs da = item_args()->decide;
-      decide_tile(da, h, i - e_score);
-      signal_done(decide_done + h);
-    } else if (i < e_page) {
-      const uint32_t r = i - e_decide;
-      wait_count(decide_done + h, T, err);
-      const PageArgs pa = item_args()->page;
-      page_item<D, GBM>(pa, h, (int)(r / P), (int)(r % P), decode_dyn);
-      signal_done(page_done + h);
+      const AttendArgs aa = item_args()->attend;
+      decide_attend_tile<D, GBM>(aa, h, i - e_score, decode_dyn);
+      signal_done(attend_done + h);
+    } else if (i < e_suffix) {
+      const AttendArgs aa = item_args()->attend;
+      suffix_item<D, GBM>(aa, h);
+      signal_done(attend_done + h);
     } else {
-      const uint32_t r = i - e_page;
-      wait_count(page_done + h, page_per_head, err);
+      const uint32_t r = i - e_suffix;
+      wait_count(attend_done + h, T + 1, err);
       const MergeArgs ma = item_args()->merge;
       merge_item(ma, h, (int)(r / a.merge_cols), (int)(r % a.merge_cols));
     }
@@ -1567,12 +1184,20 @@ void decode_kernel(DecodeArgs a) {
     ticket = s_ticket;
   }
 
-  // The last workgroup out resets the device-wide counters and advances the
-  // epoch (every other workgroup has made its last access to them).
+  // The last workgroup out resets the head ticket, the exit count and every
+  // queue's ticket, and advances the epoch (every other workgroup has made its
+  // last access to them; slots stay, tagged with the old epoch).
   if (tid == 0) {
     const uint32_t out =
         __hip_atomic_fetch_add(ctl + kCtlExits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (out == gridDim.x - 1) {
+    s_last = out == gridDim.x - 1 ? 1u : 0u;
+  }
+  __syncthreads();
+  if (s_last) {
+    if (tid < kMaxQueues)
+      __hip_atomic_store(ctl + kCtlQueues + 4 * tid + 2, 0u, __ATOMIC_RELAXED,
+                         __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) {
       __hip_atomic_store(ctl + kCtlHeadTicket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_store(ctl + kCtlExits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       __hip_atomic_fetch_add(ctl + kCtlEpoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -1655,7 +1280,6 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
 }
 
 DecideArgs decide_args(const SelectParams& p, const Layout& L) {
-  const bool reps = p.value_mean != nullptr;
   DecideArgs da;
   da.z = at<float>(p.ws, L.z);
   da.delta = at<float>(p.ws, L.delta);
@@ -1669,7 +1293,6 @@ DecideArgs decide_args(const SelectParams& p, const Layout& L) {
   da.risk_out = p.risk_out;
   da.stats_out = p.stats_out;
   da.accessed = p.accessed;
-  da.rep_l = reps ? at<float>(p.ws, L.rep_l) : nullptr;
   da.rep_acc = at<float>(p.ws, L.rep_acc);
   da.n_blocks = p.n_blocks;
   da.n_tiles = L.n_tiles;
@@ -1777,27 +1400,6 @@ int launch_decode_rows(const DecodeArgs& da, int64_t rows_per_block, size_t dyn,
   }
 }
 
-template <int D>
-int launch_split_pages(const SplitPageArgs& pa, const Layout& L, hipStream_t stream) {
-  const size_t smem = split_page_smem(pa.heads, L.n_tiles);
-  dim3 grid((unsigned)L.workers, (unsigned)L.row_blocks);
-  constexpr int CH = D / 16;
-  constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
-  switch (L.rows_per_block) {
-    case 4:
-      split_page_kernel<D, 4><<<grid, dim3(kThreads), smem, stream>>>(pa);
-      break;
-    case 8:
-      if constexpr (CAP >= 8) split_page_kernel<D, 8><<<grid, dim3(kThreads), smem, stream>>>(pa);
-      break;
-    default:
-      if constexpr (CAP >= 16)
-        split_page_kernel<D, 16><<<grid, dim3(kThreads), smem, stream>>>(pa);
-      break;
-  }
-  return check_launch("split_page_kernel");
-}
-
 struct DecodeBuffers {
   const void* key_pages;
   int64_t kp_hs;
@@ -1812,134 +1414,107 @@ struct DecodeBuffers {
   void* output;
 };
 
-// The split pipeline: score and decide kernels, then the page kernel (global
-// equal-cost ranges over every head's expanded pages) and the merge kernel.
+AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  AttendArgs aa;
+  aa.decide = decide_args(p, L);
+  aa.query = static_cast<const uint16_t*>(p.query);
+  aa.key_pages = static_cast<const uint16_t*>(b.key_pages);
+  aa.value_pages = static_cast<const uint16_t*>(b.value_pages);
+  aa.key_suffix = static_cast<const uint16_t*>(b.key_suffix);
+  aa.value_suffix = static_cast<const uint16_t*>(b.value_suffix);
+  aa.suffix_len_dev = b.suffix_len;
+  aa.part_m = at<float>(p.ws, L.part_m);
+  aa.part_l = at<float>(p.ws, L.part_l);
+  aa.part_acc = at<float>(p.ws, L.part_acc);
+  aa.kp_hs = b.kp_hs;
+  aa.vp_hs = b.vp_hs;
+  aa.ks_hs = b.ks_hs;
+  aa.ks_ts = b.ks_ts;
+  aa.vs_hs = b.vs_hs;
+  aa.vs_ts = b.vs_ts;
+  aa.suffix_cap = b.suffix_cap;
+  aa.part_stride = L.part_stride;
+  aa.row_blocks = (int)L.row_blocks;
+  aa.scale = (float)pow((double)p.dim, -0.5);
+  return aa;
+}
+
+MergeArgs merge_args(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  MergeArgs ma;
+  ma.part_m = at<float>(p.ws, L.part_m);
+  ma.part_l = at<float>(p.ws, L.part_l);
+  ma.part_acc = at<float>(p.ws, L.part_acc);
+  ma.out = static_cast<uint16_t*>(b.output);
+  ma.part_stride = L.part_stride;
+  ma.group = (int)p.group;
+  ma.parts = (int)(L.n_tiles + 1);
+  ma.dim = (int)p.dim;
+  return ma;
+}
+
+// The split pipeline: score kernel, then decide+attend (and the suffix), then
+// merge.
 int launch_split(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const ScoreArgs sa = score_args(p, L);
-  const DecideArgs da = decide_args(p, L);
-  dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
+  const AttendArgs aa = attend_args(p, L, b);
+  const MergeArgs ma = merge_args(p, L, b);
+  const dim3 score_grid((unsigned)L.n_tiles, (unsigned)p.heads);
+  const dim3 attend_grid((unsigned)(L.n_tiles + 1), (unsigned)p.heads);
+  const size_t attend_lds = attend_smem(p.group, p.dim);
   mark(0, p.stream);
   RKV_DISPATCH_DIM(p.dim, D,
-                   score_kernel<D, true><<<grid, dim3(kThreads), score_smem(p.group, p.dim, true),
-                                           p.stream>>>(sa));
+                   score_kernel<D, true><<<score_grid, dim3(kThreads),
+                                           score_smem(p.group, p.dim, true), p.stream>>>(sa));
   int rc = check_launch("score_kernel");
   if (rc) return rc;
   mark(1, p.stream);
-  decide_kernel<<<grid, dim3(kThreads), 0, p.stream>>>(da);
-  rc = check_launch("decide_kernel");
+  rc = kUnsupported;
+  RKV_DISPATCH_DIM(p.dim, D, {
+    constexpr int CH = D / 16;
+    constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
+    switch (L.rows_per_block) {
+      case 4:
+        attend_kernel<D, 4><<<attend_grid, dim3(kThreads), attend_lds, p.stream>>>(aa);
+        rc = check_launch("attend_kernel");
+        break;
+      case 8:
+        if constexpr (CAP >= 8) {
+          attend_kernel<D, 8><<<attend_grid, dim3(kThreads), attend_lds, p.stream>>>(aa);
+          rc = check_launch("attend_kernel");
+        }
+        break;
+      default:
+        if constexpr (CAP >= 16) {
+          attend_kernel<D, 16><<<attend_grid, dim3(kThreads), attend_lds, p.stream>>>(aa);
+          rc = check_launch("attend_kernel");
+        }
+        break;
+    }
+  });
   if (rc) return rc;
   mark(2, p.stream);
-
-  SplitPageArgs pa;
-  pa.query = static_cast<const uint16_t*>(p.query);
-  pa.key_pages = static_cast<const uint16_t*>(b.key_pages);
-  pa.value_pages = static_cast<const uint16_t*>(b.value_pages);
-  pa.key_suffix = static_cast<const uint16_t*>(b.key_suffix);
-  pa.value_suffix = static_cast<const uint16_t*>(b.value_suffix);
-  pa.tilebits = at<uint64_t>(p.ws, L.tilebits);
-  pa.suffix_len_dev = b.suffix_len;
-  pa.header = at<int64_t>(p.ws, L.header);
-  pa.page_m = at<float>(p.ws, L.page_m);
-  pa.page_l = at<float>(p.ws, L.page_l);
-  pa.page_acc = at<float>(p.ws, L.page_acc);
-  pa.kp_hs = b.kp_hs;
-  pa.vp_hs = b.vp_hs;
-  pa.ks_hs = b.ks_hs;
-  pa.ks_ts = b.ks_ts;
-  pa.vs_hs = b.vs_hs;
-  pa.vs_ts = b.vs_ts;
-  pa.suffix_cap = b.suffix_cap;
-  pa.n_blocks = p.n_blocks;
-  pa.n_tiles = L.n_tiles;
-  pa.tile_stride = L.tile_stride;
-  pa.block = p.block;
-  pa.length = p.length;
-  pa.heads = (int)p.heads;
-  pa.group = (int)p.group;
-  pa.workers = (int)L.workers;
-  pa.rows_per_block = (int)L.rows_per_block;
-  pa.scale = (float)pow((double)p.dim, -0.5);
-  rc = kOk;
-  RKV_DISPATCH_DIM(p.dim, D, rc = launch_split_pages<D>(pa, L, p.stream));
-  if (rc) return rc;
+  merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
+                 dim3(kThreads), 0, p.stream>>>(ma);
+  rc = check_launch("merge_kernel");
   mark(3, p.stream);
-
-  SplitMergeArgs ma;
-  ma.lse = at<float>(p.ws, L.lse);
-  ma.rep_l = at<float>(p.ws, L.rep_l);
-  ma.rep_acc = at<float>(p.ws, L.rep_acc);
-  ma.header = pa.header;
-  ma.page_m = pa.page_m;
-  ma.page_l = pa.page_l;
-  ma.page_acc = pa.page_acc;
-  ma.out = static_cast<uint16_t*>(b.output);
-  ma.n_tiles = L.n_tiles;
-  ma.tile_stride = L.tile_stride;
-  ma.heads = (int)p.heads;
-  ma.group = (int)p.group;
-  ma.workers = (int)L.workers;
-  ma.dim = (int)p.dim;
-  split_merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
-                       dim3(kThreads), split_merge_smem(L.n_tiles, L.workers), p.stream>>>(ma);
-  rc = check_launch("split_merge_kernel");
-  mark(4, p.stream);
   return rc;
 }
 
 // The persistent kernel, or kNotEligible.
 int launch_fused(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
-  if (p.dim > kMaxFusedDim || p.heads > kMaxHeads || L.n_tiles > kMaxTiles) return kNotEligible;
+  if (p.dim > kMaxFusedDim || p.heads > kMaxHeads) return kNotEligible;
   DecodeArgs da;
   da.score = score_args(p, L);
-  da.decide = decide_args(p, L);
-  PageArgs& pa = da.page;
-  pa.query = static_cast<const uint16_t*>(p.query);
-  pa.key_pages = static_cast<const uint16_t*>(b.key_pages);
-  pa.value_pages = static_cast<const uint16_t*>(b.value_pages);
-  pa.key_suffix = static_cast<const uint16_t*>(b.key_suffix);
-  pa.value_suffix = static_cast<const uint16_t*>(b.value_suffix);
-  pa.tilebits = at<uint64_t>(p.ws, L.tilebits);
-  pa.suffix_len_dev = b.suffix_len;
-  pa.lse = at<float>(p.ws, L.lse);
-  pa.rep_l = at<float>(p.ws, L.rep_l);
-  pa.rep_acc = at<float>(p.ws, L.rep_acc);
-  pa.page_m = at<float>(p.ws, L.page_m);
-  pa.page_l = at<float>(p.ws, L.page_l);
-  pa.page_acc = at<float>(p.ws, L.page_acc);
-  pa.kp_hs = b.kp_hs;
-  pa.vp_hs = b.vp_hs;
-  pa.ks_hs = b.ks_hs;
-  pa.ks_ts = b.ks_ts;
-  pa.vs_hs = b.vs_hs;
-  pa.vs_ts = b.vs_ts;
-  pa.suffix_cap = b.suffix_cap;
-  pa.n_blocks = p.n_blocks;
-  pa.n_tiles = L.n_tiles;
-  pa.tile_stride = L.tile_stride;
-  pa.part_stride = L.part_stride;
-  pa.block = p.block;
-  pa.length = p.length;
-  pa.group = (int)p.group;
-  pa.page_items = (int)L.page_items;
-  pa.scale = (float)pow((double)p.dim, -0.5);
-  MergeArgs& ma = da.merge;
-  ma.page_m = pa.page_m;
-  ma.page_l = pa.page_l;
-  ma.page_acc = pa.page_acc;
-  ma.out = static_cast<uint16_t*>(b.output);
-  ma.part_stride = L.part_stride;
-  ma.group = (int)p.group;
-  ma.page_items = (int)L.page_items;
-  ma.dim = (int)p.dim;
+  da.attend = attend_args(p, L, b);
+  da.merge = merge_args(p, L, b);
   da.control = at<uint32_t>(p.ws, L.control);
   da.heads = (int)p.heads;
-  da.row_blocks = (int)L.row_blocks;
   da.merge_cols = (int)((p.dim + kMergeD - 1) / kMergeD);
-  const uint32_t items = (uint32_t)(p.heads * (2 * L.n_tiles + L.row_blocks * L.page_items +
-                                                p.group * da.merge_cols));
+  const uint32_t items =
+      (uint32_t)(p.heads * (2 * L.n_tiles + 1 + p.group * da.merge_cols));
   const int64_t dyn_score = (int64_t)score_smem(p.group, p.dim, true);
-  const int64_t dyn_page = page_smem(L.n_tiles);
-  const size_t dyn = (size_t)(dyn_score > dyn_page ? dyn_score : dyn_page);
+  const int64_t dyn_attend = (int64_t)attend_smem(p.group, p.dim);
+  const size_t dyn = (size_t)(dyn_score > dyn_attend ? dyn_score : dyn_attend);
   int rc = kNotEligible;
   RKV_DISPATCH_DIM(p.dim, D, rc = launch_decode_rows<D>(da, L.rows_per_block, dyn, items, p.stream));
   return rc;
@@ -1957,19 +1532,18 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 }
 
 // Byte offsets of the workspace regions, for tests: control, z, delta, lse,
-// tilebits, rep_l, rep_acc, header, page_m, page_l, page_acc, total, then
-// n_tiles, the page items per head and row block (persistent kernel) and the
-// page workers (split pipeline).
+// tilebits, rep_acc, part_m, part_l, part_acc, total, then n_tiles, the row
+// stride of z / delta, of the per-tile arrays and of the partials.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out15) {
+                                    int64_t* out14) {
   clear_error();
-  if (!out15 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out14 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[15] = {L.control, L.z,       L.delta,   L.lse,       L.tilebits,
-                         L.rep_l,   L.rep_acc, L.header,  L.page_m,    L.page_l,
-                         L.page_acc, L.total,  L.n_tiles, L.page_items, L.workers};
-  for (int i = 0; i < 15; ++i) out15[i] = v[i];
+  const int64_t v[14] = {L.control, L.z,        L.delta,    L.lse,         L.tilebits,
+                         L.rep_acc, L.part_m,   L.part_l,   L.part_acc,    L.total,
+                         L.n_tiles, L.z_stride, L.tile_stride, L.part_stride};
+  for (int i = 0; i < 14; ++i) out14[i] = v[i];
   return kOk;
 }
 
@@ -2046,11 +1620,6 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
     if (g_pipeline == 1)
       return set_error(kUnsupported, "rkv_decode: the persistent kernel does not run this shape");
   }
-  if (heads * L.n_tiles > kMaxHeadTiles)
-    return set_error(kUnsupported, "rkv_decode: heads x tiles %lld exceeds %lld",
-                     (long long)(heads * L.n_tiles), (long long)kMaxHeadTiles);
-  if (split_merge_smem(L.n_tiles, L.workers) > 64 * 1024)
-    return set_error(kUnsupported, "rkv_decode: too many partials");
   return launch_split(p, L, b);
 }
 

@@ -141,8 +141,8 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("control", "z", "delta", "lse", "tilebits", "rep_l", "rep_acc", "header",
-                "page_m", "page_l", "page_acc", "total", "n_tiles", "page_items", "workers")
+LAYOUT_NAMES = ("control", "z", "delta", "lse", "tilebits", "rep_acc", "part_m", "part_l",
+                "part_acc", "total", "n_tiles", "z_stride", "tile_stride", "part_stride")
 CONTROL_ERROR_WORD = 2  # sticky flag: a decode kernel's dependency wait timed out
 
 

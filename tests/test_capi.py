@@ -60,19 +60,15 @@ def test_workspace_size_covers_layout(lib):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
-        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:11]]
+        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:10]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
         rows, tiles = heads * group, layout["n_tiles"]
         # fixed-size control block first, so every shape finds it at offset 0
         assert layout["control"] == 0 and layout["z"] == controls
-        assert layout["delta"] - layout["z"] >= rows * tiles * 64 * 4
-        assert layout["header"] - layout["rep_acc"] >= rows * tiles * dim * 4
-        # per-head slices of the intermediates are whole 256-byte lines
-        assert (layout["delta"] - layout["z"]) % (256 * heads) == 0 or heads == 1
-        assert layout["page_m"] - layout["header"] >= (heads + 1) * 8
-        slots = max(layout["page_items"], layout["workers"])
-        assert layout["page_l"] - layout["page_m"] >= rows * slots * 4
-        assert layout["total"] - layout["page_acc"] >= rows * slots * dim * 4
-        assert 1 <= layout["page_items"] <= min(64, tiles)
-        assert 1 <= layout["workers"] <= 512
+        # padded strides: every head's slice covers whole 256-byte lines
+        assert layout["z_stride"] == tiles * 64 and layout["tile_stride"] % 64 == 0
+        assert layout["part_stride"] % 64 == 0 and layout["part_stride"] >= tiles + 1
+        assert layout["delta"] - layout["z"] >= rows * layout["z_stride"] * 4
+        assert layout["part_m"] - layout["rep_acc"] >= rows * layout["tile_stride"] * dim * 4
+        assert layout["total"] - layout["part_acc"] >= rows * layout["part_stride"] * dim * 4
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0
