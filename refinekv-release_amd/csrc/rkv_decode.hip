@@ -607,10 +607,20 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     float acc = racc[k];
     uint64_t m = correct ? bits : 0ull;
     while (m) {
-      const int j = __builtin_ctzll(m);
-      m &= m - 1;
-      const float v = bf16_to_f32(a.value_mean[(h * N + tile * kTile + j) * D + d]);
-      acc = acc - psel[g][j] * v;
+      // up to 8 expanded blocks at a time: their loads in flight together
+      constexpr int kBatch = 8;
+      int js[kBatch];
+      uint16_t raw[kBatch];
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        js[u] = m ? __builtin_ctzll(m) : -1;
+        if (m) m &= m - 1;
+        const int jj = js[u] < 0 ? 0 : js[u];
+        raw[u] = a.value_mean[(h * N + tile * kTile + jj) * D + d];
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u)
+        if (js[u] >= 0) acc = acc - psel[g][js[u]] * bf16_to_f32(raw[u]);
     }
     rep->acc[idx] = acc;
   }
@@ -711,11 +721,12 @@ __device__ __forceinline__ void attend_rows(const float (&q)[GBM][D / 16], float
                                             const uint16_t* kdef, const uint16_t* vdef,
                                             AttendShared<GBM>& sh) {
   constexpr int CH = D / 16;
+  // Double-buffer the K/V rows (the next chunk's loads in flight while this
+  // chunk is computed) when the registers allow it.
+  constexpr bool kPrefetch = GBM * CH <= 32;
   const int tid = item_tid(), lg = tid >> 4, c = tid & 15, wave = tid / kWave;
   const int lane = tid % kWave;
-  for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
-    __syncthreads();  // the previous chunk's logits are consumed
-    RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
+  auto issue = [&](int64_t c0, RawBf16<CH> (&kr)[kRowBatch], RawBf16<CH> (&vr)[kRowBatch]) {
     uint32_t okm = 0;
 #pragma unroll
     for (int u = 0; u < kRowBatch; ++u) {
@@ -726,6 +737,10 @@ __device__ __forceinline__ void attend_rows(const float (&q)[GBM][D / 16], float
       kr[u] = load_raw<CH>(kp + c * CH);
       vr[u] = load_raw<CH>(vp + c * CH);
     }
+    return okm;
+  };
+  auto consume = [&](const RawBf16<CH> (&kr)[kRowBatch], const RawBf16<CH> (&vr)[kRowBatch],
+                     uint32_t okm) {
 #pragma unroll
     for (int u = 0; u < kRowBatch; ++u) {
       float kv[CH], x[GBM];
@@ -775,6 +790,28 @@ __device__ __forceinline__ void attend_rows(const float (&q)[GBM][D / 16], float
 #pragma unroll
         for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + p * v[i];
       }
+    }
+    __syncthreads();  // this chunk's logits are consumed
+  };
+  if (n_rows <= 0) return;
+  if constexpr (kPrefetch) {
+    RawBf16<CH> ka[kRowBatch], va[kRowBatch], kb[kRowBatch], vb[kRowBatch];
+    uint32_t oka = issue(0, ka, va), okb = 0;
+    for (int64_t c0 = 0;;) {
+      if (c0 + kChunkRows < n_rows) okb = issue(c0 + kChunkRows, kb, vb);
+      consume(ka, va, oka);
+      c0 += kChunkRows;
+      if (c0 >= n_rows) break;
+      if (c0 + kChunkRows < n_rows) oka = issue(c0 + kChunkRows, ka, va);
+      consume(kb, vb, okb);
+      c0 += kChunkRows;
+      if (c0 >= n_rows) break;
+    }
+  } else {
+    for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
+      RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
+      const uint32_t okm = issue(c0, kr, vr);
+      consume(kr, vr, okm);
     }
   }
 }
@@ -1079,8 +1116,8 @@ __device__ __forceinline__ const DecodeArgs* item_args() {
 // Work distribution.  Every XCD has its own queue; its workgroups draw queue
 // tickets, and a queue takes whole KV heads from a device-wide head counter,
 // so all items of a head run on one XCD and hand data to each other through
-// that XCD's L2.  A head is K consecutive tickets of its queue (its score
-// items, its decide+attend items and suffix item, its merge items, in that
+// that XCD's L2.  A head is K consecutive tickets of its queue (its suffix
+// item, its score items, its decide+attend items, its merge items, in that
 // order); the workgroup that draws the first ticket of a head's slot claims
 // the head and publishes it in the slot (tagged with the launch's epoch, so
 // slots need no reset).  An item waits only for items with smaller tickets of
@@ -1102,9 +1139,10 @@ void decode_kernel(DecodeArgs a) {
   uint64_t* slots = reinterpret_cast<uint64_t*>(ctl + kCtlSlots) + (int64_t)q * kMaxHeads;
   const uint32_t T = (uint32_t)a.score.n_tiles;
   const uint32_t merge_per_head = (uint32_t)a.merge.group * (uint32_t)a.merge_cols;
-  // per head: T score items, T decide+attend items, the suffix item, merges
-  const uint32_t e_score = T, e_attend = 2 * T, e_suffix = e_attend + 1;
-  const uint32_t K = e_suffix + merge_per_head;  // tickets per head
+  // per head: the suffix item (no dependency: first, so it overlaps the
+  // scores), T score items, T decide+attend items, the merge items
+  const uint32_t e_suffix = 1, e_score = 1 + T, e_attend = 1 + 2 * T;
+  const uint32_t K = e_attend + merge_per_head;  // tickets per head
   const int tid = threadIdx.x;
 
   if (tid == 0) {
@@ -1159,21 +1197,21 @@ void decode_kernel(DecodeArgs a) {
     uint32_t next = 0;
     if (tid == 0)
       next = __hip_atomic_fetch_add(queue + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (i < e_score) {
+    if (i < e_suffix) {
+      const AttendArgs aa = item_args()->attend;
+      suffix_item<D, GBM>(aa, h);
+      signal_done(attend_done + h);
+    } else if (i < e_score) {
       const ScoreArgs sa = item_args()->score;
-      score_tile<D, true>(sa, h, i, decode_dyn);
+      score_tile<D, true>(sa, h, i - e_suffix, decode_dyn);
       signal_done(score_done + h);
     } else if (i < e_attend) {
       wait_count(score_done + h, T, err);
       const AttendArgs aa = item_args()->attend;
       decide_attend_tile<D, GBM>(aa, h, i - e_score, decode_dyn);
       signal_done(attend_done + h);
-    } else if (i < e_suffix) {
-      const AttendArgs aa = item_args()->attend;
-      suffix_item<D, GBM>(aa, h);
-      signal_done(attend_done + h);
     } else {
-      const uint32_t r = i - e_suffix;
+      const uint32_t r = i - e_attend;
       wait_count(attend_done + h, T + 1, err);
       const MergeArgs ma = item_args()->merge;
       merge_item(ma, h, (int)(r / a.merge_cols), (int)(r % a.merge_cols));
