@@ -32,8 +32,8 @@ import torch  # noqa: E402
 
 METRIC = "decode attn µs/step/layer @128K ctx GQA32/8 d128; HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
-# Kernels one rkv_decode call launches, per pipeline.
-KERNELS = {"persistent": ("decode",), "split": ("score", "attend", "merge")}
+# Kernels one rkv_decode call launches, in order.
+KERNELS = ("score", "attend", "merge")
 
 
 def log(msg):
@@ -58,9 +58,6 @@ def parse_args():
     ap.add_argument("--no-dense", action="store_true", help="skip the eps=0 dense baseline")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
-    ap.add_argument("--pipeline", choices=("persistent", "split"), default="split",
-                    help="rkv_decode pipeline: four kernels (the default), or one persistent "
-                         "kernel")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 64 MiB buffer 5 times (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings to bytes)")
@@ -122,21 +119,22 @@ def make_layer(gen, a, capacity, device):
 
 
 def algorithmic_bytes(a, masks, counts, suffix):
-    """Bytes each phase of the decode step must move per layer-step, counted
-    once in the reference's storage formats: score reads key means and
-    ellipsoids of every block and the value means of unexpanded blocks (its
-    representative half); attend reads value norms, writes the mask and reads
-    the K/V tokens of expanded blocks and the suffix; merge writes the output.
-    "decode" is their sum (the persistent kernel runs every phase).
-    Intermediates (z, delta, partials) are not algorithmic bytes."""
+    """Bytes each kernel of the decode step must move per layer-step, counted
+    once in the reference's storage formats: score reads the key means and
+    ellipsoids of every block; attend reads the value means of unexpanded
+    blocks (the representatives), the value norms, the K/V tokens of expanded
+    blocks and of the suffix, and writes the mask; merge writes the output.
+    "decode" is their sum.  Intermediates (z, delta, partials) are not
+    algorithmic bytes."""
     H, G, D = a.heads, a.group, a.dim
     n = counts.numel()
     sel = masks.float().mean(0)  # (H, N) fraction over layers
     expanded_tokens = (sel * counts.float()[None]).sum().item()
     unexpanded = ((1 - sel).sum()).item()
     q_bytes = H * G * D * 2
-    score = 2 * H * n * D * 2 + unexpanded * D * 2 + q_bytes
-    attend = H * n * 4 + H * n + expanded_tokens * D * 2 * 2 + H * suffix * D * 2 * 2 + q_bytes
+    score = 2 * H * n * D * 2 + q_bytes
+    attend = (unexpanded * D * 2 + H * n * 4 + H * n + expanded_tokens * D * 2 * 2
+              + H * suffix * D * 2 * 2 + q_bytes)
     merge = H * G * D * 2
     phases = dict(score=score, attend=attend, merge=merge)
     return dict(phases, decode=sum(phases.values()))
@@ -158,8 +156,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = _hip.lib()
-    _hip.set_decode_pipeline(a.pipeline)
-    kernels = KERNELS[a.pipeline]
+    kernels = KERNELS
     capacity = a.warmup + a.steps + 1
     cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps,
                          gqa_reduction=a.reduction)
@@ -295,7 +292,6 @@ def main():
             "context": a.context, "layers": a.layers, "kv_heads": a.heads,
             "q_heads": a.heads * a.group, "head_dim": a.dim, "block_size": a.block,
             "eps": a.eps, "gqa_reduction": a.reduction, "parallelism": "single GPU",
-            "pipeline": a.pipeline,
         },
         "roofline": {
             "bound": "hbm",

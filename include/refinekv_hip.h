@@ -60,20 +60,18 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
                 void* key_mean, void* value_mean, void* ellipsoid, float* value_norm,
                 float* max_value_norm, rkv_stream_t stream);
 
-/* Workspace bytes needed by rkv_select / rkv_decode for this shape.  A new
- * workspace must be zero-filled once before its first rkv_decode (its control
- * words must start at zero; every call leaves them at zero again). */
+/* Workspace bytes needed by rkv_select / rkv_decode for this shape (device
+ * memory the caller owns; its contents need no initialisation). */
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
-/* Byte offsets inside the workspace (for tests): control, z, delta, lse,
- * tilebits, rep_acc, part_m, part_l, part_acc, total, then n_tiles and the
- * padded row strides (elements) of z / delta, of the per-tile arrays and of
- * the partials -> out14[0..13].  The control block (uint32 words: head
- * ticket, exit count, error, epoch, per-XCD queues, slots, per-head counters)
- * is always at offset 0 with a fixed size; word 2 becomes 1 (and stays 1) if a
- * persistent kernel's dependency wait ever timed out. */
+/* Byte offsets inside the workspace (for tests): control (reserved), zf
+ * (float4 z, delta, A, th per query row and block: the selection statistics
+ * and the delta-only factors of the risk), lse (per-tile log-sum-exp
+ * partials), part_m, part_l, part_acc (per-tile attention partials), counts
+ * (per-tile access counts), total, then n_tiles and the padded row strides
+ * (elements) of zf and of the per-tile arrays -> out11[0..10]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out14);
+                         int64_t* out11);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton
@@ -126,17 +124,9 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
 /* Profiling hook with no reference counterpart: when `events` points to 4
  * hipEvent_t handles, later rkv_select / rkv_decode calls on this thread
  * record events[0] before their first kernel and events[k] after their k-th
- * (rkv_select: score, decide; rkv_decode: the persistent kernel, or score,
- * attend, merge on the split pipeline).  NULL turns it off. */
+ * (rkv_select: score, decide; rkv_decode: score, attend, merge).  NULL turns
+ * it off. */
 int rkv_set_profile_events(void* events);
-
-/* Test and benchmark hook with no reference counterpart: which rkv_decode
- * pipeline runs on this thread.  0 automatic (= 2), 1 the persistent kernel
- * (one launch; head_dim <= 128, LDS <= 64 KiB per workgroup, no
- * private-memory traffic, else RKV_UNSUPPORTED), 2 the split pipeline
- * (score, decide+attend, merge kernels), 3 the persistent kernel where it
- * runs, else the split pipeline. */
-int rkv_set_decode_pipeline(int mode);
 
 /* Test hook with no reference counterpart: applies the kernels' device
  * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */

@@ -30,10 +30,12 @@
  *           A[l] = fma(x[8m+l], x[8m+l], A[l]) over m (from +0), result
  *           ((A[0] + A[1]) + ...) + A[7]: torch's CPU vector_norm (its
  *           2-norm kernel runs 8-wide with fused multiply-adds).
- *   DSUM    head_dim dot products in selection and attention (torch uses
- *           MKL there, whose order is not reproducible): 16 chunks of D/16
- *           consecutive elements, each summed left to right from its first
- *           element, then an xor butterfly with distances 8, 4, 2, 1
+ *   DSUM    head_dim dot products x.y in selection and attention (torch
+ *           uses MKL there, whose order is not reproducible): W = 8 lanes for
+ *           D <= 128, else 16; lane j takes the D/W consecutive elements
+ *           j*D/W ..., starting from the rounded first product x0*y0 and
+ *           adding the rest with fmaf left to right; then an xor butterfly
+ *           over the W lanes with distances W/2, ..., 1
  *           (P[j] <- P[j] + P[j^o]); the result is P[0].
  *   LSE     log-sum-exp over blocks: tiles of 64 consecutive blocks; per tile
  *           m = max, l = butterfly sum (distances 32..1) of exp(x - m);
@@ -146,17 +148,18 @@ float orc_logf(float x) {
          ((hfsq - (s * (hfsq + R) + dk * 1.42860682030941723e-06f)) - f);
 }
 
-/* DSUM order over x[0..D-1], D a multiple of 16. */
-static float dsum(const float *x, int64_t D) {
+/* DSUM order of x.y over D elements, D a multiple of 16. */
+static float dsum(const float *x, const float *y, int64_t D) {
   float P[16], Q[16];
-  int64_t c = D / 16;
-  for (int j = 0; j < 16; ++j) {
-    float a = x[j * c];
-    for (int64_t i = 1; i < c; ++i) a = a + x[j * c + i];
+  int W = D <= 128 ? 8 : 16;
+  int64_t c = D / W;
+  for (int j = 0; j < W; ++j) {
+    float a = x[j * c] * y[j * c];
+    for (int64_t i = 1; i < c; ++i) a = fmaf(x[j * c + i], y[j * c + i], a);
     P[j] = a;
   }
-  for (int o = 8; o >= 1; o >>= 1) {
-    for (int j = 0; j < 16; ++j) Q[j] = P[j] + P[j ^ o];
+  for (int o = W / 2; o >= 1; o >>= 1) {
+    for (int j = 0; j < W; ++j) Q[j] = P[j] + P[j ^ o];
     memcpy(P, Q, sizeof(P));
   }
   return P[0];
@@ -365,10 +368,10 @@ int orc_select_stats(const float *q, const uint16_t *key_mean, const uint16_t *e
       for (int64_t b = 0; b < N; ++b) {
         const uint16_t *km = key_mean + (h * N + b) * D;
         const uint16_t *el = ellipsoid + (h * N + b) * D;
-        for (int64_t d = 0; d < D; ++d) prod[d] = qt[d] * bf16f(km[d]);
-        float s = dsum(prod, D) * scale;
-        for (int64_t d = 0; d < D; ++d) prod[d] = q2[d] * bf16f(el[d]);
-        float p = dsum(prod, D);
+        for (int64_t d = 0; d < D; ++d) prod[d] = bf16f(km[d]);
+        float s = dsum(qt, prod, D) * scale;
+        for (int64_t d = 0; d < D; ++d) prod[d] = bf16f(el[d]);
+        float p = dsum(q2, prod, D);
         float dl = (sqrtf(cmin(p, 0.0f)) * scale) * ORC_INFLATE;
         float cnt = (float)block_count(b, N, B, L);
         zr[b] = s + orc_logf(cnt);
@@ -474,15 +477,15 @@ int orc_sparse_attention(const float *q, const uint16_t *key_mean, const uint16_
         int64_t cnt = block_count(b, N, B, L);
         for (int64_t t = 0; t < cnt; ++t) {
           const uint16_t *k = key_pages + ((h * N + b) * B + t) * D;
-          for (int64_t d = 0; d < D; ++d) prod[d] = qt[d] * bf16f(k[d]);
-          logit[n] = dsum(prod, D) * scale;
+          for (int64_t d = 0; d < D; ++d) prod[d] = bf16f(k[d]);
+          logit[n] = dsum(qt, prod, D) * scale;
           vrow[n++] = value_pages + ((h * N + b) * B + t) * D;
         }
       }
       for (int64_t t = 0; t < S; ++t) {
         const uint16_t *k = key_suffix + (h * S + t) * D;
-        for (int64_t d = 0; d < D; ++d) prod[d] = qt[d] * bf16f(k[d]);
-        logit[n] = dsum(prod, D) * scale;
+        for (int64_t d = 0; d < D; ++d) prod[d] = bf16f(k[d]);
+        logit[n] = dsum(qt, prod, D) * scale;
         vrow[n++] = value_suffix + (h * S + t) * D;
       }
       /* softmax(-1) @ values in fp32; sums accumulated in fp64 here so the

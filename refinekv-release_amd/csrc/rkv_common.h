@@ -89,20 +89,63 @@ __device__ __forceinline__ float readlane(float v, int lane) {
   return __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, v), lane));
 }
 
-// Wave-wide sum in the 64-lane xor-butterfly tree (distances 32..1), returned
-// uniformly: the cross-row levels 32 and 16 move data with permutes, the
-// in-row levels with DPP (complete in lane 15), then lane 15 is read out.
-// Bit-identical to the plain butterfly.
+// Cross-row butterfly steps without LDS (gfx950 v_permlane32_swap /
+// v_permlane16_swap, which exchange lanes 32-63 of the first register with
+// lanes 0-31 of the second, or the odd 16-lane rows of the first with the
+// even rows of the second).  Swapping a value with a copy of itself leaves
+// {x_l, x_(l^32)} (or {x_l, x_(l^16)}) in the two registers of every lane l,
+// so op(a, b) is the xor-butterfly step in every lane (for a commutative op,
+// bit-identical in both lanes of each pair).  Inline asm: both registers are
+// results of the swap (the compiler builtin returns the first one twice).
+// The s_nop covers the VALU-write -> permlane-read hazard.
+__device__ __forceinline__ void xor32_pair(float v, float& a, float& b) {
+  a = v;
+  b = v;
+  asm volatile("s_nop 1\n\tv_permlane32_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+__device__ __forceinline__ void xor16_pair(float v, float& a, float& b) {
+  a = v;
+  b = v;
+  asm volatile("s_nop 1\n\tv_permlane16_swap_b32 %0, %1" : "+v"(a), "+v"(b));
+}
+
+// DPP row_ror:N -- lane i of each 16-lane row reads lane (i + N) mod 16.
+template <int N>
+__device__ __forceinline__ float row_ror(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), 0x120 + N, 0xF, 0xF, false));
+}
+
+// Sum of each 16-lane row in the xor-butterfly tree (distances 8, 4, 2, 1),
+// in every lane of the row: rotating a vector of period 2k by k pairs lane i
+// with lane i^k.
+__device__ __forceinline__ float row16_sum_all(float v) {
+  v = v + row_ror<8>(v);
+  v = v + row_ror<4>(v);
+  v = v + row_ror<2>(v);
+  v = v + row_ror<1>(v);
+  return v;
+}
+
+// Wave-wide sum in the 64-lane xor-butterfly tree (distances 32..1),
+// returned uniformly.  Bit-identical to the plain butterfly.
 __device__ __forceinline__ float wave_sum_u(float v) {
-  v = v + __shfl_xor(v, 32, kWave);
-  v = v + __shfl_xor(v, 16, kWave);
+  float a, b;
+  xor32_pair(v, a, b);
+  v = a + b;
+  xor16_pair(v, a, b);
+  v = a + b;
   return readlane(row16_sum_last(v), 15);
 }
 
 // NaN-propagating wave max, returned uniformly.
 __device__ __forceinline__ float wave_nanmax_u(float v) {
-  v = nanmax(v, __shfl_xor(v, 32, kWave));
-  v = nanmax(v, __shfl_xor(v, 16, kWave));
+  float a, b;
+  xor32_pair(v, a, b);
+  v = nanmax(a, b);
+  xor16_pair(v, a, b);
+  v = nanmax(a, b);
   v = nanmax(v, row_shr<8>(v));
   v = nanmax(v, row_shr<4>(v));
   v = nanmax(v, row_shr<2>(v));

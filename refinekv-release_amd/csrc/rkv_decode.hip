@@ -1,42 +1,34 @@
-// Decode-step selection and mixed attention (src/refinekv/reference.py:10-73,
-// the semantics the reference's Triton kernels in src/refinekv/kernels/ also
-// follow).  No host sync, no allocation: the caller passes a workspace.
+// Decode-step selection and mixed attention (src/refinekv/reference.py:10-73;
+// the reference's Triton kernels in src/refinekv/kernels/ follow the same
+// semantics).  No host sync, no allocation: the caller passes a workspace.
 //
-// Per KV head h the step has three phases:
+// One decode step is three kernels, each over every (tile, KV head) pair or
+// every query row:
 //
-//   score  (h, tile)   one 64-block tile: streams the tile's key means,
-//                      ellipsoids and value means once; s = q.k_mean and the
-//                      ellipsoid projection for every query row, z = s + ln n,
-//                      delta, the tile's log-sum-exp partials of z and
-//                      z + log cosh delta, and the representative accumulator
-//                      sum_b exp(z_b - m_tile) v_mean_b over all its blocks
-//                      (the z partial is that attention's (m, l)).
-//   attend (h, tile)   after every score item of h: log Z / log C of each row
-//                      from the tile partials, the risk, the GQA reduction,
-//                      the non-finite fail-safes and the anchor union; the
-//                      mask and the access counter; the tile's
-//                      representative partial without its expanded blocks
-//                      (l over the unexpanded blocks, acc minus the expanded
-//                      blocks' terms: rounding error below fp32 eps times the
-//                      tile's representative mass); then, from that partial,
-//                      exact attention over the tile's expanded blocks token
-//                      by token (64-row chunks, one shared max per chunk).
-//                      One (m, l, acc) partial per query row and tile.
-//   suffix (h)         exact attention over the generated tokens (a device
-//                      length clamps them), independent of the decisions.
-//   merge  (h, g, cols) the tiles' and the suffix's partials of row g ->
-//                      bf16 output columns.
+//   score  (tile, h)    one 64-block tile of head h: for every query row the
+//                       selection dot products s = q.k_mean and
+//                       p = q^2.ellipsoid (FMA chains over 8 or 16 lanes per
+//                       block, then an xor butterfly), z = s*scale + ln n,
+//                       delta, and the tile's log-sum-exp partials of z and
+//                       of z + log cosh delta.  Reads the two summary arrays
+//                       once; nothing else.
+//   attend (tile, h)    log Z / log C of each row from the tile partials, the
+//                       risk, the GQA reduction, the non-finite fail-safes and
+//                       the anchor union -> mask and access count; then one
+//                       online softmax per row over the tile's
+//                       representatives (the value means of its unexpanded
+//                       blocks, logit z), the tokens of its expanded blocks
+//                       and a 1/T slice of the generated suffix -> one
+//                       (m, l, acc) partial per row and tile.
+//   merge  (row, cols)  the row's tile partials -> bf16 output columns, and
+//                       the access counter.
 //
-// Two ways to run them.  The split pipeline (default) launches three kernels:
-// score; attend with the suffix as one more column of its grid; merge.  The
-// persistent kernel (rkv_set_decode_pipeline) runs all phases in one launch:
-// each XCD has a work queue that takes whole heads, so a head's items hand
-// data to each other through that XCD's L2 (see decode_kernel).
-//
-// Scores, radii and log-sum-exp follow fixed fp32 orders shared with the CPU
-// oracle (oracle/rkv_oracle.c), so masks and selection statistics are
-// reproducible bit for bit; every summation order is fixed, so outputs are
-// deterministic run to run.
+// Selection statistics (z, delta, log Z, log C, risk) follow fixed fp32
+// orders shared with the CPU oracle (oracle/rkv_oracle.c), so masks are
+// reproducible bit for bit; the attention's orders are fixed too, so outputs
+// are deterministic run to run.
+#include <math.h>
+
 #include "rkv_common.h"
 #include "rkv_internal.h"
 
@@ -45,19 +37,9 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
+constexpr int kRowsPerWave = kMaxGroup / kWaves;  // query rows a wave owns in a tile
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr int64_t kMaxHeads = 1024;    // KV heads in the persistent kernel (control block)
-constexpr int64_t kMaxFusedDim = 128;    // widest head_dim the persistent kernel runs
-constexpr size_t kMaxFusedLds = 64 * 1024;  // its LDS per workgroup (static + dynamic)
-constexpr size_t kMaxFusedPrivate = 64;     // its private bytes per lane (no spill traffic)
-// Control block of the persistent kernel (uint32 words; see decode_kernel).
-constexpr int kMaxQueues = 16;               // one work queue per XCD (XCC_ID is 4 bits)
-constexpr int64_t kCtlHeadTicket = 0, kCtlExits = 1, kCtlError = 2, kCtlEpoch = 3;
-constexpr int64_t kCtlQueues = 16;           // per queue: -, -, ticket, -
-constexpr int64_t kCtlSlots = kCtlQueues + 4 * kMaxQueues;  // per queue: kMaxHeads u64 slots
-constexpr int64_t kCtlCounters = kCtlSlots + 2 * kMaxQueues * kMaxHeads;  // 2 x kMaxHeads
-constexpr int64_t kControlWords = kCtlCounters + 2 * kMaxHeads;
-constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a dependency wait gives up (~1 s)
+constexpr int64_t kControlWords = 64;  // reserved, zero-filled
 
 // Optional profiling events (rkv_set_profile_events): events[0] is recorded
 // before the first kernel of a call and events[k] after its k-th kernel.
@@ -67,47 +49,22 @@ inline void mark(int i, hipStream_t stream) {
   if (g_events) (void)hipEventRecord(g_events[i], stream);
 }
 
-// Decode pipeline choice (rkv_set_decode_pipeline): 0 automatic (the split
-// pipeline), 1 the persistent kernel, 2 the split pipeline, 3 the persistent
-// kernel where it runs, else the split pipeline.
-thread_local int g_pipeline = 0;
-
 // ---------------------------------------------------------------------------
-// Workspace layout.  The control block comes first and has a fixed size, so
-// its words are at the same place for every shape that shares a workspace.
+// Workspace layout.  Every per-row region starts on a 256-byte boundary and
+// per-row strides cover whole tiles.
 // ---------------------------------------------------------------------------
 struct Layout {
-  int64_t n_tiles, rows_per_block, row_blocks;
-  // Padded row strides: every head's slice of an intermediate array covers
-  // whole 256-byte lines, so no cache line holds two heads' data.
-  int64_t z_stride, tile_stride, part_stride;
-  int64_t control, z, delta, lse, tilebits, rep_acc, part_m, part_l, part_acc, total;
+  int64_t n_tiles, z_stride, tile_stride;
+  int64_t control, zf, lse, part_m, part_l, part_acc, counts, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
 
-// Rows of the GQA group one attention pass carries in registers: the next
-// power of two >= group (at least 4), capped so that rows * head_dim / 16
-// (per-lane accumulators) stays <= 64.
-inline int64_t rows_per_block(int64_t group, int64_t dim) {
-  const int64_t ch = dim / 16;
-  const int64_t cap = 64 / ch;
-  int64_t p = 16;
-  while (p > cap) p >>= 1;
-  int64_t want = 4;
-  while (want < group && want < 16) want <<= 1;
-  return want < p ? want : p;
-}
-
 Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) {
   Layout L{};
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
-  L.rows_per_block = rows_per_block(group, dim);
-  L.row_blocks = (group + L.rows_per_block - 1) / L.rows_per_block;
-  auto round64 = [](int64_t x) { return (x + 63) / 64 * 64; };
   L.z_stride = L.n_tiles * kTile;
-  L.tile_stride = round64(L.n_tiles);
-  L.part_stride = round64(L.n_tiles + 1);  // one partial per tile + the suffix's
+  L.tile_stride = (L.n_tiles + 63) / 64 * 64;
   const int64_t rows = heads * group;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -116,14 +73,12 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
     return at;
   };
   L.control = take(kControlWords * 4);
-  L.z = take(rows * L.z_stride * 4);
-  L.delta = take(rows * L.z_stride * 4);
+  L.zf = take(rows * L.z_stride * 16);
   L.lse = take(rows * L.tile_stride * 4 * 4);
-  L.tilebits = take(heads * L.tile_stride * 8);
-  L.rep_acc = take(rows * L.tile_stride * dim * 4);
-  L.part_m = take(rows * L.part_stride * 4);
-  L.part_l = take(rows * L.part_stride * 4);
-  L.part_acc = take(rows * L.part_stride * dim * 4);
+  L.part_m = take(rows * L.tile_stride * 4);
+  L.part_l = take(rows * L.tile_stride * 4);
+  L.part_acc = take(rows * L.tile_stride * dim * 4);
+  L.counts = take(heads * L.tile_stride * 4);
   L.total = off;
   return L;
 }
@@ -133,30 +88,48 @@ T* at(void* ws, int64_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
 }
 
+// Query rows one attention pass carries in registers: the next power of two
+// >= group (at least 4), capped so that rows * head_dim / 16 (per-lane
+// accumulators) stays <= 64.
+inline int64_t rows_per_pass(int64_t group, int64_t dim) {
+  const int64_t cap = 64 / (dim / 16);
+  int64_t p = 16;
+  while (p > cap) p >>= 1;
+  int64_t want = 4;
+  while (want < group && want < 16) want <<= 1;
+  return want < p ? want : p;
+}
+
 // ---------------------------------------------------------------------------
 // Shared scalar math (reference.py:16-34), identical to the CPU oracle.
 // ---------------------------------------------------------------------------
-__device__ __forceinline__ float log_cosh(float delta) {
+// The delta-only terms of a (row, block) pair, computed once by the score
+// kernel: log cosh delta (reference.py:19-22) and the two factors the risk
+// (reference.py:24-34) multiplies in -- A = cosh(delta) - 1 written as
+// 0.5 (t + 1/t) - 1 with t = e^delta (delta <= 10), or log(cosh(delta) - 1)
+// in its large-delta form; th = tanh(delta / 2) in the matching form.
+__device__ __forceinline__ void delta_terms(float delta, float& log_cosh, float& A, float& th) {
   const float c = clamp_max(delta, kDeltaMax);
-  if (delta <= kDeltaMax) return logf_((expf_(c) + expf_(-c)) * 0.5f);
-  return delta + logf_((1.0f + expf_(-2.0f * delta)) * 0.5f);
-}
-
-__device__ __forceinline__ float risk_of(float z, float delta, float log_z, float log_c,
-                                         float vmax, float vnorm) {
-  const float clipped = clamp_max(delta, kDeltaMax);
-  const float t = expf_(clipped);
-  const float exp_neg = expf_(-delta);
-  float mass, th;
+  const float t = expf_(c);
   if (delta <= kDeltaMax) {
-    const float direct = (2.0f * vmax) * expf_(z - log_c);
-    mass = direct * ((0.5f * (t + 1.0f / t)) - 1.0f);
+    log_cosh = logf_((t + expf_(-c)) * 0.5f);
+    A = (0.5f * (t + 1.0f / t)) - 1.0f;
     th = (t - 1.0f) / (t + 1.0f);
   } else {
-    const float lcm1 = (delta + 2.0f * logf_(clamp_min(1.0f - exp_neg, 1e-30f))) - kLn2;
-    mass = (2.0f * vmax) * expf_((z - log_c) + lcm1);
+    log_cosh = delta + logf_((1.0f + expf_(-2.0f * delta)) * 0.5f);
+    const float exp_neg = expf_(-delta);
+    A = (delta + 2.0f * logf_(clamp_min(1.0f - exp_neg, 1e-30f))) - kLn2;
     th = (1.0f - exp_neg) / (1.0f + exp_neg);
   }
+}
+
+// risk (reference.py:24-34) from z, delta and the delta terms: the same
+// operations in the same order as computing everything here.
+__device__ __forceinline__ float risk_from(float z, float delta, float A, float th, float log_z,
+                                           float log_c, float vmax, float vnorm) {
+  float mass;
+  if (delta <= kDeltaMax) mass = ((2.0f * vmax) * expf_(z - log_c)) * A;
+  else mass = (2.0f * vmax) * expf_((z - log_c) + A);
   const float value = ((2.0f * vnorm) * expf_(z - log_z)) * th;
   return mass + value;
 }
@@ -170,382 +143,293 @@ __device__ __forceinline__ int64_t block_count(int64_t b, int64_t n, int64_t blo
   return b == n - 1 ? length - (n - 1) * block : block;
 }
 
-// Block-wide exclusive scan of one value per thread (integers: exact).
-__device__ __forceinline__ uint32_t block_exclusive_scan(uint32_t v, uint32_t* wave_tot,
-                                                         uint32_t& total) {
-  const int lane = threadIdx.x % kWave, wave = threadIdx.x / kWave;
-  uint32_t inc = v;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t n = __shfl_up(inc, o, kWave);
-    if (lane >= o) inc += n;
-  }
-  if (lane == kWave - 1) wave_tot[wave] = inc;
-  __syncthreads();
-  uint32_t before = 0;
-  total = 0;
-  for (int w = 0; w < kWaves; ++w) {
-    if (w < wave) before += wave_tot[w];
-    total += wave_tot[w];
-  }
-  __syncthreads();
-  return before + inc - v;
+// Sum over each 8-lane group (lanes 0-7 and 8-15 of every 16-lane row) in
+// the xor-butterfly tree (distances 4, 2, 1: P[j] <- P[j] + P[j^o]).  The
+// group's last lane computes exactly the tree the butterfly leaves in its
+// first lane (operands commuted, which fp32 add ignores); its dependency
+// chain stays inside the group.
+__device__ __forceinline__ float group8_sum_last(float v) {
+  v = v + row_shr<4>(v);
+  v = v + row_shr<2>(v);
+  v = v + row_shr<1>(v);
+  return v;
 }
 
+template <int L>
+__device__ __forceinline__ float lanes_sum_last(float v) {
+  if constexpr (L == 8) return group8_sum_last(v);
+  else return row16_sum_last(v);
+}
+
+// The selection dot products of one block are split over kLanes lanes, each
+// holding kCh consecutive elements: 8 lanes up to head_dim 128, else 16.
+template <int D>
+struct Dots {
+  static constexpr int kLanes = D <= 128 ? 8 : 16;
+  static constexpr int kCh = D / kLanes;
+  static constexpr int kPerPass = kThreads / kLanes;  // blocks per pass of the workgroup
+  static constexpr int kPasses = kTile / kPerPass;
+};
+
 // ---------------------------------------------------------------------------
-// Phase 1: scores (+ representative accumulators) of one (head, tile)
+// Kernel 1: scores of one (tile, head)
 // ---------------------------------------------------------------------------
 struct ScoreArgs {
-  const uint16_t* query;       // (H, G, D) bf16
-  const uint16_t* key_mean;    // (H, N, D) bf16
-  const uint16_t* ellipsoid;   // (H, N, D) bf16
-  const uint16_t* value_mean;  // (H, N, D) bf16 (representatives only)
-  float* z;                    // (H, G, N)
-  float* delta;                // (H, G, N)
-  float* lse;                  // (H, G, tiles, 4): zm, zl, cm, cl
-  float* rep_acc;              // (H, G, tiles, D)
-  int64_t n_blocks, n_tiles, block, length;
-  int64_t z_stride;            // row stride of z / delta (blocks padded to whole tiles)
-  int64_t tile_stride;         // row stride of the per-tile arrays (tiles padded to 64)
+  const uint16_t* query;      // (H, G, D) bf16
+  const uint16_t* key_mean;   // (H, N, D) bf16
+  const uint16_t* ellipsoid;  // (H, N, D) bf16
+  float4* zf;                 // (H*G, z_stride): z, delta, A, th
+  float* lse;                 // (H*G, tile_stride, 4): zm, zl, cm, cl
+  int64_t n_blocks, block, length;
+  int64_t z_stride, tile_stride;
   int group;
   float scale;
 };
 
-inline size_t score_smem(int64_t group, int64_t dim, bool reps) {
-  return sizeof(float) * (2 * group * dim + 5 * group * kTile) +
-         (reps ? sizeof(uint16_t) * kTile * dim : 0);
+// q and bf16(q^2) are staged in LDS as fp32, each row as kLanes slices of
+// kCh values padded by 4 (so the slices the lanes of a block read start on
+// distinct banks).  When G * D <= kOwnQ each wave stages its own copy, so no
+// barrier (and no wait for the summary loads in flight) precedes the dot
+// products; larger groups share one copy.
+constexpr int kOwnQ = 1024;
+constexpr int kQPad = 4;
+
+inline size_t score_smem(int64_t group, int64_t dim) {
+  const int64_t copies = group * dim <= kOwnQ ? kWaves : 1;
+  const int64_t lanes = dim <= 128 ? 8 : 16;
+  const int64_t row = dim + lanes * kQPad;
+  return sizeof(float) * (2 * group * kTile + copies * 2 * group * row);
 }
 
-template <int D, bool REPS>
-__device__ __forceinline__ void score_tile(const ScoreArgs& a, int64_t h, int64_t tile,
-                                          unsigned char* dyn) {
-  constexpr int CH = D / 16;
-  float* smem = reinterpret_cast<float*>(dyn);
-  const int G = a.group;
-  float* qs = smem;                 // [G][D] bf16(q)
-  float* q2s = qs + G * D;          // [G][D] bf16(q^2)
-  float* sdot = q2s + G * D;        // [G][64]
-  float* pdot = sdot + G * kTile;   // [G][64]
-  float* zbuf = pdot + G * kTile;   // [G][64]
-  float* zcbuf = zbuf + G * kTile;  // [G][64]
-  float* pbuf = zcbuf + G * kTile;  // [G][64] exp(z - m_tile)
-  uint32_t* vsm = reinterpret_cast<uint32_t*>(pbuf + G * kTile);  // [64][D/2] value means
-
-  const int tid = item_tid(), wave = tid / kWave, lane = tid % kWave;
-  const int grp = lane / 16, c = lane % 16;
-  const int64_t N = a.n_blocks;
-
-  // Issue every load of the tile before the first wait.  Blocks past the end
-  // read block N-1 (their scores are discarded, their weights are 0).
-  RawBf16<CH> kraw[4], eraw[4], vraw[REPS ? 4 : 1];
+// N consecutive floats from LDS (16-byte loads when aligned, else 8-byte).
+template <int N>
+__device__ __forceinline__ void lds_read(const float* p, float (&out)[N]) {
+  if constexpr (N % 4 == 0) {
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    int64_t b = tile * kTile + wave * 16 + it * 4 + grp;
+    for (int j = 0; j < N / 4; ++j) {
+      const float4 v = reinterpret_cast<const float4*>(p)[j];
+      out[4 * j] = v.x;
+      out[4 * j + 1] = v.y;
+      out[4 * j + 2] = v.z;
+      out[4 * j + 3] = v.w;
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N / 2; ++j) {
+      const float2 v = reinterpret_cast<const float2*>(p)[j];
+      out[2 * j] = v.x;
+      out[2 * j + 1] = v.y;
+    }
+  }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
+  using S = Dots<D>;
+  constexpr int CH = S::kCh;
+  extern __shared__ float score_lds[];
+  const int G = a.group;
+  float* sdot = score_lds;          // [G][64]
+  float* pdot = sdot + G * kTile;   // [G][64]
+  const int64_t h = blockIdx.y, tile = blockIdx.x, N = a.n_blocks;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int c = tid % S::kLanes, sub = tid / S::kLanes;
+  const bool own_q = G * D <= kOwnQ;
+
+  // Every load of the tile first.  Blocks past the end read block N-1 (their
+  // results are discarded).
+  RawBf16<CH> kraw[S::kPasses], eraw[S::kPasses];
+#pragma unroll
+  for (int ps = 0; ps < S::kPasses; ++ps) {
+    int64_t b = tile * kTile + ps * S::kPerPass + sub;
     b = b < N ? b : N - 1;
     const int64_t o = (h * N + b) * D + c * CH;
-    kraw[it] = load_raw<CH>(a.key_mean + o);
-    eraw[it] = load_raw<CH>(a.ellipsoid + o);
-    if constexpr (REPS) vraw[it] = load_raw<CH>(a.value_mean + o);
+    kraw[ps] = load_raw<CH>(a.key_mean + o);
+    eraw[ps] = load_raw<CH>(a.ellipsoid + o);
   }
+  constexpr int QW = CH + kQPad;          // padded slice
+  constexpr int QS = S::kLanes * QW;      // padded row
+  float* qs = pdot + G * kTile + (own_q ? wave * 2 * G * QS : 0);  // [G][QS] bf16(q)
+  float* q2s = qs + G * QS;                                         // [G][QS] bf16(q^2)
   const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
-  for (int i = tid; i < G * D / 2; i += kThreads) {
+  const int first = own_q ? lane : tid, step = own_q ? kWave : kThreads;
+  for (int i = first; i < G * D / 2; i += step) {
     const uint32_t u = q32[i];
     const float q0 = bits_f32(u << 16), q1 = bits_f32(u & 0xFFFF0000u);
-    qs[2 * i] = q0;
-    qs[2 * i + 1] = q1;
-    q2s[2 * i] = round_bf16(q0 * q0);
-    q2s[2 * i + 1] = round_bf16(q1 * q1);
+    const int g = 2 * i / D, e = 2 * i % D;  // element pair e, e + 1 of row g
+    const int at = g * QS + (e / CH) * QW + e % CH;
+    qs[at] = q0;
+    qs[at + 1] = q1;
+    q2s[at] = round_bf16(q0 * q0);
+    q2s[at + 1] = round_bf16(q1 * q1);
   }
+  // A wave's LDS operations complete in order, so its own copy is ready for
+  // its own reads; the shared copy needs the workgroup.
+  if (!own_q) __syncthreads();
   // ln(count): every block holds block_size tokens except the last.
   const float ln_full = logf_((float)a.block);
   const float ln_last = logf_((float)(a.length - (N - 1) * a.block));
-  __syncthreads();
 
-  float km[4][CH], el[4][CH];
+  for (int g0 = 0; g0 < G; g0 += 4) {
+    // this lane's slice of q and q^2 for rows g0 .. g0+3 (clamped)
+    float qv[4][CH], q2v[4][CH];
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    unpack(kraw[it], km[it]);
-    unpack(eraw[it], el[it]);
-    if constexpr (REPS) {
-      // stage the value means in LDS for the per-row representative sums
-      const int bl = wave * 16 + it * 4 + grp;
+    for (int j = 0; j < 4; ++j) {
+      const int g = g0 + j < G ? g0 + j : G - 1;
+      lds_read<CH>(qs + g * QS + c * QW, qv[j]);
+      lds_read<CH>(q2s + g * QS + c * QW, q2v[j]);
+    }
 #pragma unroll
-      for (int j = 0; j < CH / 2; ++j) vsm[bl * (D / 2) + c * (CH / 2) + j] = vraw[it].w[j];
+    for (int ps = 0; ps < S::kPasses; ++ps) {
+      float km[CH], el[CH];
+      unpack(kraw[ps], km);
+      unpack(eraw[ps], el);
+      float sv[4], pv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        // DSUM: this lane's CH elements as an FMA chain from the first
+        // product, then the butterfly over the block's lanes.
+        float s = qv[j][0] * km[0];
+        float p = q2v[j][0] * el[0];
+#pragma unroll
+        for (int i = 1; i < CH; ++i) {
+          s = __builtin_fmaf(qv[j][i], km[i], s);
+          p = __builtin_fmaf(q2v[j][i], el[i], p);
+        }
+        sv[j] = lanes_sum_last<S::kLanes>(s);
+        pv[j] = lanes_sum_last<S::kLanes>(p);
+      }
+      if (c == S::kLanes - 1) {
+        const int bl = ps * S::kPerPass + sub;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (g0 + j < G) {
+            sdot[(g0 + j) * kTile + bl] = sv[j];
+            pdot[(g0 + j) * kTile + bl] = pv[j];
+          }
+        }
+      }
     }
   }
-
-  for (int g = 0; g < G; ++g) {
-    float qv[CH], q2v[CH];
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      qv[i] = qs[g * D + c * CH + i];
-      q2v[i] = q2s[g * D + c * CH + i];
-    }
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      // DSUM: this lane's CH consecutive elements left to right, then the
-      // 16-lane butterfly (complete in lane 15 of the row).
-      float s = qv[0] * km[it][0];
-      float p = q2v[0] * el[it][0];
-#pragma unroll
-      for (int i = 1; i < CH; ++i) {
-        s = s + qv[i] * km[it][i];
-        p = p + q2v[i] * el[it][i];
-      }
-      s = row16_sum_last(s);
-      p = row16_sum_last(p);
-      if (c == 15) {
-        const int bl = wave * 16 + it * 4 + grp;
-        sdot[g * kTile + bl] = s;
-        pdot[g * kTile + bl] = p;
-      }
-    }
-  }
   __syncthreads();
 
-  for (int idx = tid; idx < G * kTile; idx += kThreads) {
-    const int g = idx / kTile, bl = idx % kTile;
-    const int64_t b = tile * kTile + bl;
+  // z, delta and the LSE partials: wave w owns rows w, w + 4, ...; lane =
+  // block of the tile.
+  for (int g = wave; g < G; g += kWaves) {
+    const int64_t b = tile * kTile + lane;
     float z = kNegInf, zc = kNegInf;
     if (b < N) {
-      const float s = sdot[idx] * a.scale;
-      const float dl = (sqrtf(clamp_min(pdot[idx], 0.0f)) * a.scale) * kInflate;
+      const float s = sdot[g * kTile + lane] * a.scale;
+      const float dl = (sqrtf(clamp_min(pdot[g * kTile + lane], 0.0f)) * a.scale) * kInflate;
       z = s + (b == N - 1 ? ln_last : ln_full);
-      zc = z + log_cosh(dl);
-      const int64_t o = (h * G + g) * a.z_stride + b;
-      a.z[o] = z;
-      a.delta[o] = dl;
+      float lcosh, ra, rth;
+      delta_terms(dl, lcosh, ra, rth);
+      zc = z + lcosh;
+      a.zf[(h * G + g) * a.z_stride + b] = make_float4(z, dl, ra, rth);
     }
-    zbuf[idx] = z;
-    zcbuf[idx] = zc;
-  }
-  __syncthreads();
-
-  for (int g = wave; g < G; g += kWaves) {
-    const float x = zbuf[g * kTile + lane];
-    const float zm = wave_nanmax_u(x);
-    const float e = expf_(x - inf_to_zero(zm));
-    const float zl = wave_sum_u(e);
-    const float xc = zcbuf[g * kTile + lane];
-    const float cm = wave_nanmax_u(xc);
-    const float cl = wave_sum_u(expf_(xc - inf_to_zero(cm)));
-    if (lane == 0) {
+    const float zm = wave_nanmax_u(z);
+    const float zl = wave_sum_u(expf_(z - inf_to_zero(zm)));
+    const float cm = wave_nanmax_u(zc);
+    const float cl = wave_sum_u(expf_(zc - inf_to_zero(cm)));
+    if (lane == 0)
       *reinterpret_cast<float4*>(a.lse + ((h * G + g) * a.tile_stride + tile) * 4) =
           make_float4(zm, zl, cm, cl);
-    }
-    if constexpr (REPS) {
-      // Representative accumulator of row g: sum_b e_b v_b over the tile.
-      // Lane group grp takes blocks grp, grp+4, ...; the four partial sums
-      // are then added by two cross-row permutes.
-      pbuf[g * kTile + lane] = e;
-      __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
-      float acc[CH];
-#pragma unroll
-      for (int k = 0; k < kTile / 4; ++k) {
-        const int bl = grp + 4 * k;
-        const float w = pbuf[g * kTile + bl];
-        RawBf16<CH> r;
-#pragma unroll
-        for (int j = 0; j < CH / 2; ++j) r.w[j] = vsm[bl * (D / 2) + c * (CH / 2) + j];
-        float v[CH];
-        unpack(r, v);
-#pragma unroll
-        for (int i = 0; i < CH; ++i) acc[i] = k == 0 ? w * v[i] : acc[i] + w * v[i];
-      }
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        acc[i] = acc[i] + shfl_xor(acc[i], 16);
-        acc[i] = acc[i] + shfl_xor(acc[i], 32);
-      }
-      if (grp == 0) {
-        float* o = a.rep_acc + ((h * G + g) * a.tile_stride + tile) * D + c * CH;
-#pragma unroll
-        for (int i = 0; i < CH; ++i) o[i] = acc[i];
-      }
-    }
   }
 }
 
 // ---------------------------------------------------------------------------
-// Phase 2: decisions (+ representative corrections) of one (head, tile)
+// Decisions of one (tile, head)
 // ---------------------------------------------------------------------------
 struct DecideArgs {
-  const float* z;
-  const float* delta;
+  const float4* zf;             // (H*G, z_stride): z, delta, A, th
   const float* lse;
   const float* value_norm;      // (H, N)
   const float* max_value_norm;  // (H)
-  const uint16_t* value_mean;   // (H, N, D) (representatives only)
   const uint8_t* anchor;        // (H, N) or null
   uint8_t* mask;                // (H, N)
-  uint64_t* tilebits;           // (H, tiles)
   float* risk_out;              // (H, G, N) or null
   float* stats_out;             // (H, G, 2) or null: log Z, log C
-  unsigned long long* accessed; // or null
-  const float* rep_acc;         // (H, G, tiles, D) from the score pass (decode only)
   int64_t n_blocks, n_tiles, block, length;
-  int64_t z_stride, tile_stride;  // padded row strides (see ScoreArgs)
-  int group, reduction, dim;
+  int64_t z_stride, tile_stride;
+  int group, reduction;
   float eps;
 };
 
-constexpr int kLseRegs = 4;  // tile partials per lane held in registers (tiles <= 256)
+struct DecideShared {
+  float gstat[kMaxGroup][2];
+  float risk[kMaxGroup][kTile];
+  int32_t list[kTile];  // tile-relative indices of the expanded blocks, ascending
+  uint64_t bits;        // expanded-block ballot
+  uint32_t accessed;    // access count of the tile
+};
 
-// Merge the tile partials (m, l) of one row in the fixed order: max first,
-// then 64 lane accumulators (tile t -> lane t % 64, left to right) and a
-// butterfly.  m[k], l[k] hold tile lane + 64 k (k < kLseRegs), preloaded.
-__device__ __forceinline__ float merge_lse(const float (&m)[kLseRegs], const float (&l)[kLseRegs],
-                                           const float* part, int which, int64_t n_tiles,
-                                           int lane) {
-  // (register part unrolled, then the rest from memory: same order as one
-  // loop over t, without indexing the register arrays at run time)
-  constexpr int64_t kRegTiles = (int64_t)kLseRegs * kWave;
-  float mx = kNegInf;
-#pragma unroll
-  for (int k = 0; k < kLseRegs; ++k)
-    if (lane + (int64_t)k * kWave < n_tiles) mx = nanmax(mx, m[k]);
-  for (int64_t t = lane + kRegTiles; t < n_tiles; t += kWave)
+// LSE of one row from the tile partials in the fixed order: the max first,
+// then 64 lane accumulators (tile t -> lane t % 64, left to right) and the
+// 64-wide butterfly.  (m0, l0) is this lane's partial of tile `lane`.
+__device__ __forceinline__ float merge_lse(float m0, float l0, const float* part, int which,
+                                           int64_t n_tiles, int lane) {
+  float mx = lane < n_tiles ? m0 : kNegInf;
+  for (int64_t t = lane + kWave; t < n_tiles; t += kWave)
     mx = nanmax(mx, part[t * 4 + 2 * which]);
   mx = wave_nanmax_u(mx);
   const float ms = inf_to_zero(mx);
-  float acc = 0.0f;
-#pragma unroll
-  for (int k = 0; k < kLseRegs; ++k) {
-    if (lane + (int64_t)k * kWave < n_tiles) {
-      const float term = l[k] * expf_(m[k] - ms);
-      acc = k == 0 ? term : acc + term;
-    }
-  }
-  for (int64_t t = lane + kRegTiles; t < n_tiles; t += kWave)
+  float acc = lane < n_tiles ? l0 * expf_(m0 - ms) : 0.0f;
+  for (int64_t t = lane + kWave; t < n_tiles; t += kWave)
     acc = acc + part[t * 4 + 2 * which + 1] * expf_(part[t * 4 + 2 * which] - ms);
   return logf_(wave_sum_u(acc)) + ms;
 }
 
-constexpr int kRiskPerThread = kMaxGroup * kTile / kThreads;  // (row, block) pairs per thread
-
-// The tile's representative partial after its expanded blocks are removed,
-// left in LDS for the attention that follows in the same workgroup.
-struct RepShared {
-  float* acc;      // [G][D]
-  float* l;        // [G] (0: no live representative)
-  float* m;        // [G] the partial's max, inf_to_zero(tile max of z)
-  uint64_t* bits;  // the tile's expanded-block ballot
-};
-
+// Decides tile `tile` of head h: stores the mask (and risk / stats when
+// asked); leaves the tile's ballot, expanded-block list and access count in
+// `sh`, and z of every (row, block) of the tile in zsh when it is not null
+// (-inf for blocks past the end).  Ends with a barrier.
 __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int64_t tile,
-                                            const RepShared* rep) {
-  __shared__ float gstat[kMaxGroup][2];
-  __shared__ float risk_s[kMaxGroup][kTile];
-  __shared__ float psel[kMaxGroup][kTile];
-  __shared__ uint64_t sel_bits;
-  const int tid = item_tid(), wave = tid / kWave, lane = tid % kWave;
+                                            DecideShared& sh, float (*zsh)[kTile]) {
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
-  const int64_t nvalid = N - tile * kTile >= kTile ? kTile : N - tile * kTile;
-
-  // ---- every load this tile needs before any wait ---------------------
-  float pz_m[kMaxGroup / kWaves][kLseRegs], pz_l[kMaxGroup / kWaves][kLseRegs];
-  float pc_m[kMaxGroup / kWaves][kLseRegs], pc_l[kMaxGroup / kWaves][kLseRegs];
-#pragma unroll
-  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
-    const int g = wave + gi * kWaves;
-#pragma unroll
-    for (int k = 0; k < kLseRegs; ++k) {
-      const int64_t t = lane + (int64_t)k * kWave;
-      if (g < G && t < T) {
-        const float4 v =
-            *reinterpret_cast<const float4*>(a.lse + ((h * G + g) * a.tile_stride + t) * 4);
-        pz_m[gi][k] = v.x;
-        pz_l[gi][k] = v.y;
-        pc_m[gi][k] = v.z;
-        pc_l[gi][k] = v.w;
-      } else {
-        pz_m[gi][k] = pc_m[gi][k] = kNegInf;
-        pz_l[gi][k] = pc_l[gi][k] = 0.0f;
-      }
-    }
-  }
-  float rz[kRiskPerThread], rd[kRiskPerThread], rv[kRiskPerThread];
-#pragma unroll
-  for (int k = 0; k < kRiskPerThread; ++k) {
-    const int idx = tid + k * kThreads;
-    const int g = idx / kTile, bl = idx % kTile;
-    if (g < G && bl < nvalid) {
-      const int64_t b = tile * kTile + bl;
-      const int64_t o = (h * G + g) * a.z_stride + b;
-      rz[k] = a.z[o];
-      rd[k] = a.delta[o];
-      rv[k] = a.value_norm[h * N + b];
-    } else {
-      rz[k] = rd[k] = rv[k] = 0.0f;
-    }
-  }
-  const bool anchored =
-      wave == 0 && a.anchor && lane < nvalid && a.anchor[h * N + tile * kTile + lane] != 0;
+  const int64_t b = tile * kTile + lane;
+  const bool valid = b < N;
+  const float vnorm = valid ? a.value_norm[h * N + b] : 0.0f;
+  const bool anchored = valid && a.anchor && a.anchor[h * N + b] != 0;
   const float vmax = a.max_value_norm[h];
-  // Representative partial of this tile: the z max (m of the partial) for
-  // the rows this wave corrects, and the accumulator slice of this thread.
-  float tile_m[kMaxGroup / kWaves];
-#pragma unroll
-  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
-    const int g = wave + gi * kWaves;
-    tile_m[gi] = (rep && g < G) ? a.lse[((h * G + g) * a.tile_stride + tile) * 4] : 0.0f;
-  }
-  constexpr int kAccPerThread = kMaxGroup * 256 / kThreads;  // G * D <= 16 * 256
-  float racc[kAccPerThread];
-  const int GD = G * a.dim;
-#pragma unroll
-  for (int k = 0; k < kAccPerThread; ++k) {
-    const int idx = tid + k * kThreads;
-    racc[k] = 0.0f;
-    if (rep && idx < GD) {
-      const int g = idx / a.dim, d = idx % a.dim;
-      racc[k] = a.rep_acc[((h * G + g) * a.tile_stride + tile) * a.dim + d];
-    }
-  }
 
-  // ---- global log Z / log C of each row --------------------------------
-#pragma unroll
-  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
-    const int g = wave + gi * kWaves;
-    if (g >= G) break;
-    const float* part = a.lse + (h * G + g) * a.tile_stride * 4;
-    const float lz = merge_lse(pz_m[gi], pz_l[gi], part, 0, T, lane);  // log Z
-    const float lc = merge_lse(pc_m[gi], pc_l[gi], part, 1, T, lane);
+  // ---- log Z, log C of each row this wave owns, then its risks ----------
+#pragma unroll 1
+  for (int g = wave; g < G; g += kWaves) {
+    const float* prow = a.lse + (h * G + g) * a.tile_stride * 4;
+    float4 part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
+    if (lane < T) part = *reinterpret_cast<const float4*>(prow + lane * 4);
+    float4 zf = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    if (valid) zf = a.zf[(h * G + g) * a.z_stride + b];
+    const float lz = merge_lse(part.x, part.y, prow, 0, T, lane);
+    const float lc = merge_lse(part.z, part.w, prow, 1, T, lane);
     if (lane == 0) {
-      gstat[g][0] = lz;
-      gstat[g][1] = lc;
+      sh.gstat[g][0] = lz;
+      sh.gstat[g][1] = lc;
       if (a.stats_out && tile == 0) {
         a.stats_out[(h * G + g) * 2] = lz;
         a.stats_out[(h * G + g) * 2 + 1] = lc;
       }
     }
-  }
-  __syncthreads();
-
-#pragma unroll
-  for (int k = 0; k < kRiskPerThread; ++k) {
-    const int idx = tid + k * kThreads;
-    const int g = idx / kTile, bl = idx % kTile;
-    if (g >= G) break;
     float r = 0.0f;
-    if (bl < nvalid) {
-      r = risk_of(rz[k], rd[k], gstat[g][0], gstat[g][1], vmax, rv[k]);
-      if (a.risk_out) a.risk_out[(h * G + g) * N + tile * kTile + bl] = r;
+    if (valid) {
+      r = risk_from(zf.x, zf.y, zf.z, zf.w, lz, lc, vmax, vnorm);
+      if (a.risk_out) a.risk_out[(h * G + g) * N + b] = r;
     }
-    risk_s[g][bl] = r;
+    sh.risk[g][lane] = r;
+    if (zsh) zsh[g][lane] = valid ? zf.x : kNegInf;
   }
   __syncthreads();
 
+  // ---- GQA reduction, fail-safes, anchors (select_blocks_reference) ------
   if (wave == 0) {
-    const int64_t b = tile * kTile + lane;
-    const bool valid = lane < nvalid;
     bool bad_global = false;
-    for (int g = 0; g < G; ++g) bad_global |= !is_finite(gstat[g][0]) || !is_finite(gstat[g][1]);
+    for (int g = 0; g < G; ++g) bad_global |= !is_finite(sh.gstat[g][0]) || !is_finite(sh.gstat[g][1]);
     bool sel = false, bad_local = false;
     float acc = 0.0f, mx = 0.0f;
     for (int g = 0; g < G; ++g) {
-      const float r = risk_s[g][lane];
+      const float r = sh.risk[g][lane];
       bad_local |= !is_finite(r);
       if (g == 0) {
         acc = r;
@@ -561,685 +445,445 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     sel = (sel || bad_global || bad_local || anchored) && valid;
     if (valid) a.mask[h * N + b] = sel ? 1 : 0;
     const uint64_t bits = __ballot(sel);
-    if (lane == 0) {
-      a.tilebits[h * a.tile_stride + tile] = bits;
-      sel_bits = bits;
+    if (sel) {
+      const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+          (uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
+      sh.list[below] = lane;
     }
-    if (a.accessed) {
-      unsigned long long term =
-          valid ? (sel ? (unsigned long long)block_count(b, N, a.block, a.length) : 1ull) : 0ull;
-#pragma unroll
-      for (int o = 32; o >= 1; o >>= 1) term += __shfl_xor(term, o, kWave);
-      if (lane == 0) atomicAdd(a.accessed, term);
-    }
-  }
-  if (!rep) return;
-  __syncthreads();
-
-  // ---- representatives of this tile: drop the expanded blocks ----------
-  // (thread tid's prefetched z/delta pair k is row wave + 4k, block lane)
-  const uint64_t bits = sel_bits;
-  const int nsel = __popcll(bits);
-  if (tid == 0) *rep->bits = bits;
-#pragma unroll
-  for (int gi = 0; gi < kMaxGroup / kWaves; ++gi) {
-    const int g = wave + gi * kWaves;
-    if (g >= G) break;
-    const bool valid = lane < nvalid;
-    const bool expanded = (bits >> lane) & 1ull;
-    const float mt = inf_to_zero(tile_m[gi]);
-    const float e = valid ? expf_(rz[gi] - mt) : 0.0f;
-    const float l = wave_sum_u(expanded ? 0.0f : e);
-    psel[g][lane] = expanded ? e : 0.0f;
     if (lane == 0) {
-      rep->l[g] = nsel == nvalid ? 0.0f : l;
-      rep->m[g] = mt;
+      // access count (transformers.py:590-594): count of an expanded block,
+      // 1 for a representative; only the prompt's last block can be short
+      const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
+      const int64_t nsel = __popcll(bits);
+      int64_t count = (nvalid - nsel) + nsel * a.block;
+      if (tile == T - 1 && ((bits >> (N - 1 - tile * kTile)) & 1ull))
+        count -= a.block - (a.length - (N - 1) * a.block);
+      sh.bits = bits;
+      sh.accessed = (uint32_t)count;
     }
   }
   __syncthreads();
-  const int D = a.dim;
-  const bool correct = nsel > 0 && nsel < nvalid;
-#pragma unroll
-  for (int k = 0; k < kAccPerThread; ++k) {
-    const int idx = tid + k * kThreads;
-    if (idx >= GD) break;
-    const int g = idx / D, d = idx % D;
-    float acc = racc[k];
-    uint64_t m = correct ? bits : 0ull;
-    while (m) {
-      // up to 8 expanded blocks at a time: their loads in flight together
-      constexpr int kBatch = 8;
-      int js[kBatch];
-      uint16_t raw[kBatch];
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u) {
-        js[u] = m ? __builtin_ctzll(m) : -1;
-        if (m) m &= m - 1;
-        const int jj = js[u] < 0 ? 0 : js[u];
-        raw[u] = a.value_mean[(h * N + tile * kTile + jj) * D + d];
-      }
-#pragma unroll
-      for (int u = 0; u < kBatch; ++u)
-        if (js[u] >= 0) acc = acc - psel[g][js[u]] * bf16_to_f32(raw[u]);
-    }
-    rep->acc[idx] = acc;
-  }
 }
 
-template <int D, bool REPS>
-__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
-  extern __shared__ unsigned char score_dyn[];
-  score_tile<D, REPS>(a, blockIdx.y, blockIdx.x, score_dyn);
-}
-
-__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a) {
-  decide_tile(a, blockIdx.y, blockIdx.x, nullptr);
+// rkv_select's second kernel: decisions only.
+__global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a,
+                                                          unsigned long long* accessed) {
+  __shared__ DecideShared sh;
+  decide_tile(a, blockIdx.y, blockIdx.x, sh, nullptr);
+  if (accessed && threadIdx.x == 0) atomicAdd(accessed, (unsigned long long)sh.accessed);
 }
 
 // ---------------------------------------------------------------------------
-// Phase 3: exact attention over a tile's expanded blocks, and over the suffix
+// Kernel 2: decisions + mixed attention of one (tile, head)
 // ---------------------------------------------------------------------------
-// After deciding a tile, the same workgroup attends to the tile's expanded
-// blocks token by token, starting from the tile's representative partial, and
-// writes one (m, l, acc) partial per query row: slot `tile` of the row.  The
-// generated suffix is one more item per head (slot n_tiles), independent of
-// the decisions.  The merge then combines n_tiles + 1 partials per row.
 struct AttendArgs {
   DecideArgs decide;
-  const uint16_t* query;       // (H, G, D) bf16
-  const uint16_t* key_pages;   // head h at key_pages + h * kp_hs; rows (N*B, D)
+  const uint16_t* query;        // (H, G, D) bf16
+  const uint16_t* value_mean;   // (H, N, D) bf16
+  const uint16_t* key_pages;    // head h at key_pages + h * kp_hs; rows (N*B, D)
   const uint16_t* value_pages;
-  const uint16_t* key_suffix;  // token t of head h at h * ks_hs + t * ks_ts
+  const uint16_t* key_suffix;   // token t of head h at h * ks_hs + t * ks_ts
   const uint16_t* value_suffix;
   const int32_t* suffix_len_dev;  // or null
-  float* part_m;               // (H, G, part_stride)
+  float* part_m;                // (H*G, tile_stride)
   float* part_l;
-  float* part_acc;             // (H, G, part_stride, D)
+  float* part_acc;              // (H*G, tile_stride, D)
+  uint32_t* tile_counts;        // (H, tile_stride) or null
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
-  int64_t suffix_cap, part_stride;
-  int row_blocks;
+  int64_t suffix_cap;
+  int row_passes;
+  int log2_block;  // block_size is 16, 32 or 64
   float scale;
 };
 
-constexpr int kRowBatch = 4;                  // rows per lane group per chunk
-constexpr int kChunkRows = 16 * kRowBatch;    // rows per chunk (one per lane of a wave)
+constexpr int kRowBatch = 2;  // token rows per lane group per batch
 
-// Exact logits of one K row for this lane's query slice (DSUM order, natural
-// units), complete in lane 15 of the 16-lane group.
+// Online-softmax state of GBM query rows held by one 16-lane group: m and l
+// (uniform over the group) and acc, this lane's D/16 columns.
 template <int D, int GBM>
-__device__ __forceinline__ void row_logits(const float (&q)[GBM][D / 16], const float (&k)[D / 16],
-                                           float (&x)[GBM]) {
-  constexpr int CH = D / 16;
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-    float s = q[g][0] * k[0];
-#pragma unroll
-    for (int i = 1; i < CH; ++i) s = s + q[g][i] * k[i];
-    x[g] = row16_sum_last(s);
-  }
-}
-
-// CH consecutive floats (CH even; 16-byte aligned when CH % 4 == 0, else 8).
-template <int CH>
-__device__ __forceinline__ void load_f32(const float* p, float (&out)[CH]) {
-  if constexpr (CH % 4 == 0) {
-#pragma unroll
-    for (int j = 0; j < CH / 4; ++j) {
-      const float4 v = reinterpret_cast<const float4*>(p)[j];
-      out[4 * j] = v.x;
-      out[4 * j + 1] = v.y;
-      out[4 * j + 2] = v.z;
-      out[4 * j + 3] = v.w;
-    }
-  } else {
-#pragma unroll
-    for (int j = 0; j < CH / 2; ++j) {
-      const float2 v = reinterpret_cast<const float2*>(p)[j];
-      out[2 * j] = v.x;
-      out[2 * j + 1] = v.y;
-    }
-  }
-}
-
-template <int GBM>
-struct AttendShared {
-  float xlog[GBM][kChunkRows];
-  float cmax[GBM], csum[GBM];
+struct GroupState {
+  float m[GBM], l[GBM], acc[GBM][D / 16];
 };
 
-// Folds n_rows K/V rows into the state, 64 rows per chunk: pass 1 loads the
-// chunk's K and V and writes its logits, pass 2 weighs the V rows with one
-// shared max per chunk.  row(v, kp, vp) points kp / vp at row v and returns
-// false for a masked row (kp / vp must then stay valid addresses).
-// The online-softmax state of GBM query rows is (m, l), uniform over the
-// workgroup, and acc, per 16-lane group (this lane's D/16 columns; the groups
-// are summed at the end).
-template <int D, int GBM, typename RowFn>
-__device__ __forceinline__ void attend_rows(const float (&q)[GBM][D / 16], float (&m_run)[GBM],
-                                            float (&l_run)[GBM], float (&acc)[GBM][D / 16],
-                                            int64_t n_rows, int gn, float scale, RowFn row,
-                                            const uint16_t* kdef, const uint16_t* vdef,
-                                            AttendShared<GBM>& sh) {
+// Folds R rows (logits x[g][u], values v[u]) into the group's state with one
+// rescale per row of the query.  Rows with x = -inf contribute nothing.
+template <int D, int GBM, int R>
+__device__ __forceinline__ void fold(GroupState<D, GBM>& st, const float (&x)[GBM][R],
+                                     const float (&v)[R][D / 16], int gn) {
   constexpr int CH = D / 16;
-  // Double-buffer the K/V rows (the next chunk's loads in flight while this
-  // chunk is computed) when the registers allow it.
-  constexpr bool kPrefetch = GBM * CH <= 32;
-  const int tid = item_tid(), lg = tid >> 4, c = tid & 15, wave = tid / kWave;
-  const int lane = tid % kWave;
-  auto issue = [&](int64_t c0, RawBf16<CH> (&kr)[kRowBatch], RawBf16<CH> (&vr)[kRowBatch]) {
-    uint32_t okm = 0;
 #pragma unroll
-    for (int u = 0; u < kRowBatch; ++u) {
-      const int64_t v = c0 + lg + 16 * u;
-      const uint16_t* kp = kdef;
-      const uint16_t* vp = vdef;
-      if (v < n_rows && row(v, kp, vp)) okm |= 1u << u;
-      kr[u] = load_raw<CH>(kp + c * CH);
-      vr[u] = load_raw<CH>(vp + c * CH);
-    }
-    return okm;
-  };
-  auto consume = [&](const RawBf16<CH> (&kr)[kRowBatch], const RawBf16<CH> (&vr)[kRowBatch],
-                     uint32_t okm) {
+  for (int g = 0; g < GBM; ++g) {
+    if (g >= gn) break;
+    float mx = x[g][0];
 #pragma unroll
-    for (int u = 0; u < kRowBatch; ++u) {
-      float kv[CH], x[GBM];
-      unpack(kr[u], kv);
-      row_logits<D, GBM>(q, kv, x);
-      if (c == 15) {
+    for (int u = 1; u < R; ++u) mx = fmaxf(mx, x[g][u]);
+    const float mn = fmaxf(st.m[g], mx);
+    if (mn == kNegInf) continue;
+    const float sc = __builtin_amdgcn_exp2f((st.m[g] - mn) * kLog2e);
+    st.l[g] = st.l[g] * sc;
 #pragma unroll
-        for (int g = 0; g < GBM; ++g)
-          sh.xlog[g][lg + 16 * u] = ((okm >> u) & 1u) ? x[g] * scale : kNegInf;
-      }
+    for (int i = 0; i < CH; ++i) st.acc[g][i] = st.acc[g][i] * sc;
+    st.m[g] = mn;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const float p = __builtin_amdgcn_exp2f((x[g][u] - mn) * kLog2e);
+      st.l[g] = st.l[g] + p;
+#pragma unroll
+      for (int i = 0; i < CH; ++i) st.acc[g][i] = __builtin_fmaf(p, v[u][i], st.acc[g][i]);
     }
-    __syncthreads();
-    // chunk max and sum per query row, one wave per row
-    for (int g = wave; g < gn; g += kWaves) {
-      const float x = sh.xlog[g][lane];
-      const float cm = wave_nanmax_u(x);
-      const float ms = cm == kNegInf ? 0.0f : cm;
-      const float sum = wave_sum_u(__builtin_amdgcn_exp2f((x - ms) * kLog2e));
-      if (lane == 0) {
-        sh.cmax[g] = cm;
-        sh.csum[g] = sum;
-      }
+  }
+}
+
+// Logits of R token rows (K raw, this lane's slice) for GBM query rows, then
+// the fold.  Row u is live when bit u of ok is set.
+template <int D, int GBM>
+__device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st, const float (&q)[GBM][D / 16],
+                                            const RawBf16<D / 16> (&kr)[kRowBatch],
+                                            const RawBf16<D / 16> (&vr)[kRowBatch], uint32_t ok,
+                                            float scale, int gn) {
+  constexpr int CH = D / 16;
+  float x[GBM][kRowBatch], v[kRowBatch][CH];
+#pragma unroll
+  for (int u = 0; u < kRowBatch; ++u) {
+    const bool live = (ok >> u) & 1u;
+    float k[CH];
+    unpack(kr[u], k);
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      float s = q[g][0] * k[0];
+#pragma unroll
+      for (int i = 1; i < CH; ++i) s = __builtin_fmaf(q[g][i], k[i], s);
+      s = row16_sum_all(s);
+      x[g][u] = live ? s * scale : kNegInf;
     }
-    __syncthreads();
+    unpack(vr[u], v[u]);
+#pragma unroll
+    for (int i = 0; i < CH; ++i) v[u][i] = live ? v[u][i] : 0.0f;
+  }
+  fold<D, GBM, kRowBatch>(st, x, v, gn);
+}
+
+// (m, l, acc) of two states -> their union (symmetric in the two).
+__device__ __forceinline__ void merge_pair(float ma, float la, float mb, float lb, float& m,
+                                           float& ea, float& eb, float& l) {
+  m = fmaxf(ma, mb);
+  ea = ma == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((ma - m) * kLog2e);
+  eb = mb == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mb - m) * kLog2e);
+  l = la * ea + lb * eb;
+}
+
+// Combines the four lane groups of this wave (xor 32 then xor 16 partners):
+// afterwards every group holds the wave's state.
+template <int D, int GBM>
+__device__ __forceinline__ void combine_wave(GroupState<D, GBM>& st, int gn) {
+  constexpr int CH = D / 16;
+#pragma unroll
+  for (int step = 0; step < 2; ++step) {
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       if (g >= gn) break;
-      const float cm = sh.cmax[g];
-      const float mn = fmaxf(m_run[g], cm);
-      if (mn == kNegInf) continue;
-      const float sa = __builtin_amdgcn_exp2f((m_run[g] - mn) * kLog2e);
-      const float sb = __builtin_amdgcn_exp2f((cm - mn) * kLog2e);
-      l_run[g] = l_run[g] * sa + sh.csum[g] * sb;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] * sa;
-      m_run[g] = mn;
-    }
-#pragma unroll
-    for (int u = 0; u < kRowBatch; ++u) {
-      float v[CH];
-      unpack(vr[u], v);
-#pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        if (g >= gn) break;
-        const float ms = m_run[g] == kNegInf ? 0.0f : m_run[g];
-        const float p = __builtin_amdgcn_exp2f((sh.xlog[g][lg + 16 * u] - ms) * kLog2e);
-#pragma unroll
-        for (int i = 0; i < CH; ++i) acc[g][i] = acc[g][i] + p * v[i];
+      float ma, mb, la, lb, m, ea, eb, l;
+      if (step == 0) {
+        xor32_pair(st.m[g], ma, mb);
+        xor32_pair(st.l[g], la, lb);
+      } else {
+        xor16_pair(st.m[g], ma, mb);
+        xor16_pair(st.l[g], la, lb);
       }
-    }
-    __syncthreads();  // this chunk's logits are consumed
-  };
-  if (n_rows <= 0) return;
-  if constexpr (kPrefetch) {
-    RawBf16<CH> ka[kRowBatch], va[kRowBatch], kb[kRowBatch], vb[kRowBatch];
-    uint32_t oka = issue(0, ka, va), okb = 0;
-    for (int64_t c0 = 0;;) {
-      if (c0 + kChunkRows < n_rows) okb = issue(c0 + kChunkRows, kb, vb);
-      consume(ka, va, oka);
-      c0 += kChunkRows;
-      if (c0 >= n_rows) break;
-      if (c0 + kChunkRows < n_rows) oka = issue(c0 + kChunkRows, ka, va);
-      consume(kb, vb, okb);
-      c0 += kChunkRows;
-      if (c0 >= n_rows) break;
-    }
-  } else {
-    for (int64_t c0 = 0; c0 < n_rows; c0 += kChunkRows) {
-      RawBf16<CH> kr[kRowBatch], vr[kRowBatch];
-      const uint32_t okm = issue(c0, kr, vr);
-      consume(kr, vr, okm);
+      merge_pair(ma, la, mb, lb, m, ea, eb, l);
+#pragma unroll
+      for (int i = 0; i < CH; ++i) {
+        float aa, ab;
+        if (step == 0) xor32_pair(st.acc[g][i], aa, ab);
+        else xor16_pair(st.acc[g][i], aa, ab);
+        st.acc[g][i] = aa * ea + ab * eb;
+      }
+      st.m[g] = m;
+      st.l[g] = l;
     }
   }
 }
 
-// Sums the 16 lane groups (one shared max: plain adds) and writes rows
-// row0 .. row0+gn-1 of the partial arrays at `slot`.
+// Two workgroups per CU (<= 256 registers per lane), so a 512-tile step runs
+// in one round on 256 CUs.
 template <int D, int GBM>
-__device__ __forceinline__ void write_partial(const float (&m_run)[GBM], const float (&l_run)[GBM],
-                                              float (&acc)[GBM][D / 16], int gn,
-                                              const AttendArgs& a, int64_t row0, int64_t slot,
-                                              float (&xacc)[kWaves][GBM][D]) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void attend_kernel(AttendArgs a) {
   constexpr int CH = D / 16;
-  const int tid = item_tid(), c = tid & 15, wave = tid / kWave, grp = (tid % kWave) >> 4;
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-#pragma unroll
-    for (int i = 0; i < CH; ++i) {
-      acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 16);
-      acc[g][i] = acc[g][i] + shfl_xor(acc[g][i], 32);
-    }
-  }
-  __syncthreads();
-  if (grp == 0) {
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      if (g >= gn) break;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) xacc[wave][g][c * CH + i] = acc[g][i];
-    }
-  }
-  __syncthreads();
-  for (int idx = tid; idx < gn * D; idx += kThreads) {
-    const int g = idx / D, d = idx % D;
-    const int64_t at = (row0 + g) * a.part_stride + slot;
-    a.part_acc[at * D + d] = ((xacc[0][g][d] + xacc[1][g][d]) + xacc[2][g][d]) + xacc[3][g][d];
-    if (d == 0) {
-      a.part_m[at] = m_run[g];
-      a.part_l[at] = l_run[g];
-    }
-  }
-}
-
-template <int D, int GBM>
-__device__ __forceinline__ void load_query(const AttendArgs& a, int64_t h, int g0, int gn,
-                                           float (&q)[GBM][D / 16]) {
-  constexpr int CH = D / 16;
-  const int c = item_tid() & 15;
-  const int G = a.decide.group;
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-    const int gg = g < gn ? g : 0;
-    RawBf16<CH> r = load_raw<CH>(a.query + ((h * G + g0 + gg) * D + c * CH));
-    unpack(r, q[g]);
-  }
-}
-
-// Decide tile `tile` of head h (RepShared in `dyn`), then attend to its
-// expanded blocks from its representative partial.
-template <int D, int GBM>
-__device__ __forceinline__ void decide_attend_tile(const AttendArgs& a, int64_t h, int64_t tile,
-                                                   unsigned char* dyn) {
-  constexpr int CH = D / 16;
-  __shared__ AttendShared<GBM> sh;
-  __shared__ float xacc[kWaves][GBM][D];
-  __shared__ int32_t blocks[kTile];
-  __shared__ uint64_t tile_bits;
+  constexpr int R = kRowBatch;
+  __shared__ DecideShared dsh;
+  __shared__ float zsh[kMaxGroup][kTile];
+  __shared__ float comb[kWaves][GBM][D + 2];
   const DecideArgs& da = a.decide;
+  const int64_t h = blockIdx.y, tile = blockIdx.x;
   const int G = da.group;
-  float* rep_acc = reinterpret_cast<float*>(dyn);
-  RepShared rep{rep_acc, rep_acc + G * D, rep_acc + G * D + G, &tile_bits};
-  decide_tile(da, h, tile, &rep);
-  __syncthreads();
+  const int64_t N = da.n_blocks, T = da.n_tiles, B = da.block, L = da.length;
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int lg = tid >> 4, c = tid & 15;
 
-  const int tid = item_tid(), lg = tid >> 4, c = tid & 15;
-  const uint64_t bits = tile_bits;
-  const int nsel = __popcll(bits);
-  if (tid < nsel) blocks[tid] = (int32_t)(tile * kTile + nth_set_bit(bits, tid));
-  __syncthreads();
-  const int64_t N = da.n_blocks, B = da.block, L = da.length;
-  const uint16_t* kbase = a.key_pages + h * a.kp_hs;
-  const uint16_t* vbase = a.value_pages + h * a.vp_hs;
-  const int32_t* blk = blocks;
-  auto row = [=](int64_t v, const uint16_t*& kp, const uint16_t*& vp) {
-    const int64_t j = v / B, t = v - j * B;
-    const int64_t b = blk[j];
-    if (t >= block_count(b, N, B, L)) return false;
-    kp = kbase + (b * B + t) * D;
-    vp = vbase + (b * B + t) * D;
-    return true;
-  };
-  for (int rb = 0; rb < a.row_blocks; ++rb) {
-    const int g0 = rb * GBM, gn = min(GBM, G - g0);
-    float q[GBM][CH];
-    load_query<D, GBM>(a, h, g0, gn, q);
-    float m_run[GBM], l_run[GBM], acc[GBM][CH];
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      const int gg = g < gn ? g0 + g : 0;
-      const bool live = g < gn && rep.l[gg] > 0.0f;
-      m_run[g] = live ? rep.m[gg] : kNegInf;
-      l_run[g] = live ? rep.l[gg] : 0.0f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i)
-        acc[g][i] = (live && lg == 0) ? rep.acc[gg * D + c * CH + i] : 0.0f;
-    }
-    attend_rows<D, GBM>(q, m_run, l_run, acc, (int64_t)nsel * B, gn, a.scale, row, kbase, vbase,
-                        sh);
-    write_partial<D, GBM>(m_run, l_run, acc, gn, a, h * G + g0, tile, xacc);
-  }
-}
-
-// Attention of head h's query rows over the generated suffix (slot n_tiles).
-template <int D, int GBM>
-__device__ __forceinline__ void suffix_item(const AttendArgs& a, int64_t h) {
-  constexpr int CH = D / 16;
-  __shared__ AttendShared<GBM> sh;
-  __shared__ float xacc[kWaves][GBM][D];
-  const int G = a.decide.group;
+  // This tile's slice of the suffix: tokens tile, tile + T, ... (< S).
   int64_t S = a.suffix_cap;
   if (a.suffix_len_dev) {
-    const int64_t s = *a.suffix_len_dev;
-    S = s < 0 ? 0 : (s > a.suffix_cap ? a.suffix_cap : s);
+    const int64_t sl = *a.suffix_len_dev;
+    S = sl < 0 ? 0 : (sl > a.suffix_cap ? a.suffix_cap : sl);
   }
-  const uint16_t* kbase = a.key_pages + h * a.kp_hs;  // valid rows for masked lanes
+  const int64_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0;
+  const uint16_t* kbase = a.key_pages + h * a.kp_hs;
   const uint16_t* vbase = a.value_pages + h * a.vp_hs;
   const uint16_t* ks = a.key_suffix + h * a.ks_hs;
   const uint16_t* vs = a.value_suffix + h * a.vs_hs;
-  const int64_t kts = a.ks_ts, vts = a.vs_ts;
-  auto row = [=](int64_t v, const uint16_t*& kp, const uint16_t*& vp) {
-    kp = ks + v * kts;
-    vp = vs + v * vts;
-    return true;
+
+  // ---- loads independent of the decision, in flight during it ----------
+  // value means of this lane group's blocks lg, lg + 16, lg + 32, lg + 48
+  RawBf16<CH> vraw[kTile / 16];
+#pragma unroll
+  for (int i = 0; i < kTile / 16; ++i) {
+    int64_t b = tile * kTile + lg + 16 * i;
+    b = b < N ? b : N - 1;
+    vraw[i] = load_raw<CH>(a.value_mean + (h * N + b) * D + c * CH);
+  }
+  // the query rows of the first pass
+  RawBf16<CH> qraw[GBM];
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+    const int gg = g < G ? g : G - 1;
+    qraw[g] = load_raw<CH>(a.query + (h * G + gg) * D + c * CH);
+  }
+  // batch 0's suffix rows (rows lg + 16u)
+  RawBf16<CH> ka[R], va[R], kb[R], vb[R];
+#pragma unroll
+  for (int u = 0; u < R; ++u) {
+    const int64_t v = lg + 16 * u;
+    const int64_t t = v < n_suffix ? tile + v * T : 0;
+    const uint16_t* kp = v < n_suffix ? ks + t * a.ks_ts : kbase;
+    const uint16_t* vp = v < n_suffix ? vs + t * a.vs_ts : vbase;
+    ka[u] = load_raw<CH>(kp + c * CH);
+    va[u] = load_raw<CH>(vp + c * CH);
+  }
+
+  decide_tile(da, h, tile, dsh, zsh);
+  const uint64_t bits = dsh.bits;
+  const int64_t n_rows = n_suffix + (int64_t)__popcll(bits) * B;
+  const int32_t* list = dsh.list;
+
+  // Token row v: the suffix slice first, then the expanded blocks' tokens in
+  // block order.  Points kp / vp at the row (a valid row when it is masked)
+  // and returns whether it is live.
+  auto row = [&](int64_t v, const uint16_t*& kp, const uint16_t*& vp) -> bool {
+    kp = kbase;
+    vp = vbase;
+    if (v >= n_rows) return false;
+    if (v < n_suffix) {
+      const int64_t t = tile + v * T;
+      kp = ks + t * a.ks_ts;
+      vp = vs + t * a.vs_ts;
+      return true;
+    }
+    const int64_t w = v - n_suffix;
+    const int64_t j = w >> a.log2_block, t = w & (B - 1);
+    const int64_t bb = tile * kTile + list[j];
+    kp = kbase + ((bb << a.log2_block) + t) * D;
+    vp = vbase + ((bb << a.log2_block) + t) * D;
+    return t < block_count(bb, N, B, L);
   };
-  for (int rb = 0; rb < a.row_blocks; ++rb) {
-    const int g0 = rb * GBM, gn = min(GBM, G - g0);
+  auto issue = [&](int64_t batch, RawBf16<CH> (&kr)[R], RawBf16<CH> (&vr)[R]) {
+    uint32_t ok = 0;
+#pragma unroll
+    for (int u = 0; u < R; ++u) {
+      const uint16_t *kp, *vp;
+      if (row(batch * 16 * R + lg + 16 * u, kp, vp)) ok |= 1u << u;
+      kr[u] = load_raw<CH>(kp + c * CH);
+      vr[u] = load_raw<CH>(vp + c * CH);
+    }
+    return ok;
+  };
+
+  for (int rp = 0; rp < a.row_passes; ++rp) {
+    const int g0 = rp * GBM, gn = min(GBM, G - g0);
+    uint32_t oka = 0, okb = 0;
+    if (rp == 0) {
+      // batch 0: the suffix rows are in flight already; add its page rows
+#pragma unroll
+      for (int u = 0; u < R; ++u) {
+        const int64_t v = lg + 16 * u;
+        if (v < n_suffix) {
+          oka |= 1u << u;
+        } else if (v < n_rows) {
+          const uint16_t *kp, *vp;
+          if (row(v, kp, vp)) oka |= 1u << u;
+          ka[u] = load_raw<CH>(kp + c * CH);
+          va[u] = load_raw<CH>(vp + c * CH);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int g = 0; g < GBM; ++g) {
+        const int gg = g0 + g < G ? g0 + g : G - 1;
+        qraw[g] = load_raw<CH>(a.query + (h * G + gg) * D + c * CH);
+      }
+      oka = issue(0, ka, va);
+    }
+    if (16 * R < n_rows) okb = issue(1, kb, vb);
     float q[GBM][CH];
-    load_query<D, GBM>(a, h, g0, gn, q);
-    float m_run[GBM], l_run[GBM], acc[GBM][CH];
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) unpack(qraw[g], q[g]);
+
+    GroupState<D, GBM> st;
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
-      m_run[g] = kNegInf;
-      l_run[g] = 0.0f;
+      st.m[g] = kNegInf;
+      st.l[g] = 0.0f;
 #pragma unroll
-      for (int i = 0; i < CH; ++i) acc[g][i] = 0.0f;
+      for (int i = 0; i < CH; ++i) st.acc[g][i] = 0.0f;
     }
-    attend_rows<D, GBM>(q, m_run, l_run, acc, S, gn, a.scale, row, kbase, vbase, sh);
-    write_partial<D, GBM>(m_run, l_run, acc, gn, a, h * G + g0, a.decide.n_tiles, xacc);
+    // representatives: this lane group's unexpanded blocks, logit z
+    {
+      float x[GBM][kTile / 16], v[kTile / 16][CH];
+#pragma unroll
+      for (int i = 0; i < kTile / 16; ++i) {
+        const int bl = lg + 16 * i;
+        const bool rep = !((bits >> bl) & 1ull) && tile * kTile + bl < N;
+        unpack(vraw[i], v[i]);
+#pragma unroll
+        for (int e = 0; e < CH; ++e) v[i][e] = rep ? v[i][e] : 0.0f;
+#pragma unroll
+        for (int g = 0; g < GBM; ++g) {
+          const int gg = g0 + g < G ? g0 + g : G - 1;
+          x[g][i] = rep ? zsh[gg][bl] : kNegInf;
+        }
+      }
+      fold<D, GBM, kTile / 16>(st, x, v, gn);
+    }
+    // token rows, two batches in flight
+#pragma unroll 1
+    for (int64_t k = 0; k * 16 * R < n_rows; k += 2) {
+      fold_tokens<D, GBM>(st, q, ka, va, oka, a.scale, gn);
+      if ((k + 2) * 16 * R < n_rows) oka = issue(k + 2, ka, va);
+      if ((k + 1) * 16 * R >= n_rows) break;
+      fold_tokens<D, GBM>(st, q, kb, vb, okb, a.scale, gn);
+      if ((k + 3) * 16 * R < n_rows) okb = issue(k + 3, kb, vb);
+    }
+
+    // the 16 lane groups -> one partial per query row
+    combine_wave<D, GBM>(st, gn);
+    if (lane < 16) {
+#pragma unroll
+      for (int g = 0; g < GBM; ++g) {
+        if (g >= gn) break;
+#pragma unroll
+        for (int i = 0; i < CH; ++i) comb[wave][g][c * CH + i] = st.acc[g][i];
+        if (c == 0) {
+          comb[wave][g][D] = st.m[g];
+          comb[wave][g][D + 1] = st.l[g];
+        }
+      }
+    }
+    __syncthreads();
+    for (int idx = tid; idx < gn * D; idx += kThreads) {
+      const int g = idx / D, d = idx % D;
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][g][D]);
+      float acc = 0.0f, l = 0.0f;
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        const float mw = comb[w][g][D];
+        const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
+        acc = __builtin_fmaf(comb[w][g][d], e, acc);
+        l = __builtin_fmaf(comb[w][g][D + 1], e, l);
+      }
+      const int64_t at = (h * G + g0 + g) * da.tile_stride + tile;
+      a.part_acc[at * D + d] = acc;
+      if (d == 0) {
+        a.part_m[at] = M;
+        a.part_l[at] = l;
+      }
+    }
+    __syncthreads();  // comb is reused by the next pass
   }
-}
-
-inline size_t attend_smem(int64_t group, int64_t dim) {
-  return sizeof(float) * (group * dim + 2 * group);
-}
-
-// Split pipeline, kernel 2: grid (tiles + 1, H); the last column is the suffix.
-template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) void attend_kernel(AttendArgs a) {
-  extern __shared__ unsigned char attend_dyn[];
-  if ((int64_t)blockIdx.x == a.decide.n_tiles)
-    suffix_item<D, GBM>(a, blockIdx.y);
-  else
-    decide_attend_tile<D, GBM>(a, blockIdx.y, blockIdx.x, attend_dyn);
+  if (a.tile_counts && tid == 0) a.tile_counts[h * da.tile_stride + tile] = dsh.accessed;
 }
 
 // ---------------------------------------------------------------------------
-// Phase 4: merge a row's partials -> bf16 output columns
+// Kernel 3: merge a row's tile partials -> bf16 output columns
 // ---------------------------------------------------------------------------
 struct MergeArgs {
-  const float* part_m;    // (H, G, part_stride)
+  const float* part_m;    // (H*G, tile_stride)
   const float* part_l;
-  const float* part_acc;  // (H, G, part_stride, D)
+  const float* part_acc;  // (H*G, tile_stride, D)
   uint16_t* out;          // (H*G, D)
-  int64_t part_stride;    // row stride of the partials
-  int group, parts, dim;  // parts = n_tiles + 1
+  const uint32_t* tile_counts;     // (H, tile_stride) or null
+  unsigned long long* accessed;    // or null
+  int64_t tile_stride;
+  int parts, dim, heads;
 };
 
-constexpr int kMergeD = 32;                   // output columns per item
-constexpr int kMergeK = kThreads / kMergeD;   // partial stripes
-constexpr int kMergeBatch = 8;                // partials per stripe per batch
+constexpr int kMergeD = 32;                  // output columns per workgroup
+constexpr int kMergeK = kThreads / kMergeD;  // partial stripes
+constexpr int kMergeBatch = 8;               // partials per stripe per batch
 
-__device__ __forceinline__ void merge_item(const MergeArgs& a, int64_t h, int g, int dc) {
-  __shared__ float red[kWaves];
-  __shared__ float num_s[kMergeK][kMergeD];
-  __shared__ float den_s[kMergeK];
-  const int P = a.parts, D = a.dim;
-  const int64_t r = h * a.group + g;
-  const int tid = item_tid(), lane = tid % kWave, wave = tid / kWave;
-
-  float mx = kNegInf;
-  for (int i = tid; i < P; i += kThreads) {
-    const float l = a.part_l[r * a.part_stride + i];
-    const float m = a.part_m[r * a.part_stride + i];
-    if (l > 0.0f) mx = fmaxf(mx, m);
+// Online merge of one partial into (mx, num, den); skips empty partials.
+__device__ __forceinline__ void merge_one(float m, float l, float acc, float& mx, float& num,
+                                          float& den) {
+  if (!(l > 0.0f)) return;
+  if (m > mx) {
+    const float s = mx == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mx - m) * kLog2e);
+    num = num * s + acc;
+    den = den * s + l;
+    mx = m;
+  } else {
+    const float e = __builtin_amdgcn_exp2f((m - mx) * kLog2e);
+    num = __builtin_fmaf(acc, e, num);
+    den = __builtin_fmaf(l, e, den);
   }
-  mx = wave_nanmax_u(mx);
-  if (lane == 0) red[wave] = mx;
-  __syncthreads();
-  const float M = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float Ms = M == kNegInf ? 0.0f : M;
+}
 
-  const int dl = tid % kMergeD, kk = tid / kMergeD;
-  const int d = dc * kMergeD + dl;
+__global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
+  __shared__ float sm[kMergeK], sd[kMergeK], sn[kMergeK][kMergeD];
+  __shared__ unsigned long long wsum[kWaves];
+  const int64_t r = blockIdx.x;
+  const int P = a.parts, D = a.dim;
+  const int tid = threadIdx.x, dl = tid % kMergeD, kk = tid / kMergeD;
+  const int d = blockIdx.y * kMergeD + dl;
   const int dd = d < D ? d : 0;
-  float num = 0.0f, den = 0.0f;
+  const float* pm = a.part_m + r * a.tile_stride;
+  const float* pl = a.part_l + r * a.tile_stride;
+  const float* pa = a.part_acc + r * a.tile_stride * D + dd;
+  float mx = kNegInf, num = 0.0f, den = 0.0f;
   for (int i0 = kk; i0 < P; i0 += kMergeK * kMergeBatch) {
     float mv[kMergeBatch], lv[kMergeBatch], av[kMergeBatch];
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) {
       const int i = i0 + u * kMergeK;
       const int ii = i < P ? i : 0;
-      mv[u] = a.part_m[r * a.part_stride + ii];
-      lv[u] = a.part_l[r * a.part_stride + ii];
-      av[u] = a.part_acc[(r * a.part_stride + ii) * D + dd];
+      mv[u] = pm[ii];
+      lv[u] = i < P ? pl[ii] : 0.0f;
+      av[u] = pa[(int64_t)ii * D];
     }
 #pragma unroll
-    for (int u = 0; u < kMergeBatch; ++u) {
-      if (i0 + u * kMergeK < P && lv[u] > 0.0f) {
-        const float e = __builtin_amdgcn_exp2f((mv[u] - Ms) * kLog2e);
-        den = den + lv[u] * e;
-        num = num + av[u] * e;
-      }
-    }
+    for (int u = 0; u < kMergeBatch; ++u) merge_one(mv[u], lv[u], av[u], mx, num, den);
   }
-  num_s[kk][dl] = num;
-  if (dl == 0) den_s[kk] = den;
+  sn[kk][dl] = num;
+  if (dl == 0) {
+    sm[kk] = mx;
+    sd[kk] = den;
+  }
   __syncthreads();
   if (tid < kMergeD && d < D) {
-    float n = num_s[0][tid], den_all = den_s[0];
-    for (int j = 1; j < kMergeK; ++j) {
-      n = n + num_s[j][tid];
-      den_all = den_all + den_s[j];
-    }
-    a.out[r * D + d] = bf16_rne(n / fmaxf(den_all, 1e-30f));
+    float m2 = kNegInf, n2 = 0.0f, d2 = 0.0f;
+    for (int j = 0; j < kMergeK; ++j) merge_one(sm[j], sd[j], sn[j][tid], m2, n2, d2);
+    a.out[r * D + d] = bf16_rne(n2 / fmaxf(d2, 1e-30f));
   }
-}
-
-// Split pipeline, kernel 3: grid (H * G, ceil(D / 32)).
-__global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
-  merge_item(a, blockIdx.x / a.group, blockIdx.x % a.group, blockIdx.y);
-}
-
-// ---------------------------------------------------------------------------
-// The persistent decode kernel
-// ---------------------------------------------------------------------------
-struct DecodeArgs {
-  ScoreArgs score;
-  AttendArgs attend;
-  MergeArgs merge;
-  uint32_t* control;  // kControlWords words, zero when the workspace is new
-  int heads, merge_cols;
-};
-
-// This workgroup's XCD (HW_REG_XCC_ID bits [3:0]).
-__device__ __forceinline__ uint32_t xcc_id() {
-  return __builtin_amdgcn_s_getreg((3 << 11) | (0 << 6) | 20) & (kMaxQueues - 1);
-}
-
-__device__ __forceinline__ uint32_t load_dev(const uint32_t* p) {
-  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// Thread 0: polls until *p >= target (bounded: on timeout it sets the sticky
-// error word and returns).
-__device__ __forceinline__ void poll_at_least(const uint32_t* p, uint32_t target, uint32_t* err) {
-  for (uint32_t spins = 0; load_dev(p) < target; ++spins) {
-    if (spins > kSpinLimit) {
-      __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    __builtin_amdgcn_s_sleep(2);
-  }
-}
-
-// Waits until a head's completion counter reaches target.  The counted items
-// ran on this XCD, whose L2 holds what they wrote, and this workgroup has not
-// read those lines before: no cache maintenance is needed.
-__device__ __forceinline__ void wait_count(const uint32_t* cnt, uint32_t target, uint32_t* err) {
-  if (threadIdx.x == 0) poll_at_least(cnt, target, err);
-  __syncthreads();
-}
-
-// Every thread waits until its stores have reached the XCD's L2, then thread
-// 0 counts the item done.
-__device__ __forceinline__ void signal_done(uint32_t* cnt) {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
-  if (threadIdx.x == 0) __hip_atomic_fetch_add(cnt, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-}
-
-// The kernel's arguments re-read from the kernarg segment for each item:
-// the item kinds' fields are not kept live (in SGPRs) across the item loop.
-typedef __attribute__((address_space(4))) const DecodeArgs KernelArgs;
-__device__ __forceinline__ const DecodeArgs* item_args() {
-  KernelArgs* p = (KernelArgs*)__builtin_amdgcn_kernarg_segment_ptr();
-  asm volatile("" : "+s"(p));
-  return (const DecodeArgs*)p;
-}
-
-// Two workgroups per CU (<= 256 registers per lane): every phase fits in
-// registers without spilling.
-//
-// Work distribution.  Every XCD has its own queue; its workgroups draw queue
-// tickets, and a queue takes whole KV heads from a device-wide head counter,
-// so all items of a head run on one XCD and hand data to each other through
-// that XCD's L2.  A head is K consecutive tickets of its queue (its suffix
-// item, its score items, its decide+attend items, its merge items, in that
-// order); the workgroup that draws the first ticket of a head's slot claims
-// the head and publishes it in the slot (tagged with the launch's epoch, so
-// slots need no reset).  An item waits only for items with smaller tickets of
-// its own queue (the slot's first ticket, or its head's earlier phase), so the
-// smallest unfinished ticket of every queue is held by a running workgroup:
-// the grid drains whatever the residency.  The last workgroup out resets the
-// tickets and counters and advances the epoch.
-template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void decode_kernel(DecodeArgs a) {
-  extern __shared__ unsigned char decode_dyn[];
-  __shared__ uint32_t s_ticket, s_head, s_tag, s_last;
-  uint32_t* ctl = a.control;
-  uint32_t* err = ctl + kCtlError;
-  uint32_t* score_done = ctl + kCtlCounters;
-  uint32_t* attend_done = score_done + kMaxHeads;
-  const uint32_t q = xcc_id();
-  uint32_t* queue = ctl + kCtlQueues + 4 * q;  // [0] claim, [1] ready, [2] ticket
-  uint64_t* slots = reinterpret_cast<uint64_t*>(ctl + kCtlSlots) + (int64_t)q * kMaxHeads;
-  const uint32_t T = (uint32_t)a.score.n_tiles;
-  const uint32_t merge_per_head = (uint32_t)a.merge.group * (uint32_t)a.merge_cols;
-  // per head: the suffix item (no dependency: first, so it overlaps the
-  // scores), T score items, T decide+attend items, the merge items
-  const uint32_t e_suffix = 1, e_score = 1 + T, e_attend = 1 + 2 * T;
-  const uint32_t K = e_attend + merge_per_head;  // tickets per head
-  const int tid = threadIdx.x;
-
-  if (tid == 0) {
-    // this launch's slot tag, and a first ticket (queue tickets start at 0:
-    // the previous launch's last workgroup reset them)
-    s_tag = load_dev(ctl + kCtlEpoch) + 1;
-    s_ticket = __hip_atomic_fetch_add(queue + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  }
-  __syncthreads();
-  const uint32_t tag = s_tag;
-  uint32_t ticket = s_ticket;
-  for (;;) {
-    const uint32_t slot = ticket / K, i = ticket % K;
-    if (tid == 0) {
-      uint32_t h = 0xFFFFFFFFu;
-      if (slot < (uint32_t)kMaxHeads) {
-        uint64_t* entry = slots + slot;
-        if (i == 0) {
-          // claim the next head for this queue (or none left) and publish it
-          h = __hip_atomic_fetch_add(ctl + kCtlHeadTicket, 1u, __ATOMIC_RELAXED,
-                                     __HIP_MEMORY_SCOPE_AGENT);
-          if (h < (uint32_t)a.heads) {
-            __hip_atomic_store(score_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __hip_atomic_store(attend_done + h, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            __builtin_amdgcn_s_waitcnt(0);
-          } else {
-            h = 0xFFFFFFFFu;
-          }
-          __hip_atomic_store(entry, ((uint64_t)tag << 32) | h, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-        } else {
-          uint64_t v = 0;
-          for (uint32_t spins = 0;; ++spins) {
-            v = __hip_atomic_load(entry, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-            if ((uint32_t)(v >> 32) == tag) break;
-            if (spins > kSpinLimit) {
-              __hip_atomic_store(err, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-              v = 0xFFFFFFFFull;
-              break;
-            }
-            __builtin_amdgcn_s_sleep(2);
-          }
-          h = (uint32_t)v;
-        }
-      }
-      s_head = h;
-    }
+  // the step's access count: sum of the tile counts, added once
+  if (a.accessed && blockIdx.x == 0 && blockIdx.y == 0) {
+    unsigned long long s = 0;
+    for (int64_t i = tid; i < (int64_t)a.heads * a.tile_stride; i += kThreads)
+      s += a.tile_counts[i];
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
+    if (tid % kWave == 0) wsum[tid / kWave] = s;
     __syncthreads();
-    const uint32_t h = s_head;
-    if (h >= (uint32_t)a.heads) break;
-    // claim the next ticket now; it is larger than this one
-    uint32_t next = 0;
-    if (tid == 0)
-      next = __hip_atomic_fetch_add(queue + 2, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    if (i < e_suffix) {
-      const AttendArgs aa = item_args()->attend;
-      suffix_item<D, GBM>(aa, h);
-      signal_done(attend_done + h);
-    } else if (i < e_score) {
-      const ScoreArgs sa = item_args()->score;
-      score_tile<D, true>(sa, h, i - e_suffix, decode_dyn);
-      signal_done(score_done + h);
-    } else if (i < e_attend) {
-      wait_count(score_done + h, T, err);
-      const AttendArgs aa = item_args()->attend;
-      decide_attend_tile<D, GBM>(aa, h, i - e_score, decode_dyn);
-      signal_done(attend_done + h);
-    } else {
-      const uint32_t r = i - e_attend;
-      wait_count(attend_done + h, T + 1, err);
-      const MergeArgs ma = item_args()->merge;
-      merge_item(ma, h, (int)(r / a.merge_cols), (int)(r % a.merge_cols));
-    }
-    __syncthreads();
-    if (tid == 0) s_ticket = next;
-    __syncthreads();
-    ticket = s_ticket;
-  }
-
-  // The last workgroup out resets the head ticket, the exit count and every
-  // queue's ticket, and advances the epoch (every other workgroup has made its
-  // last access to them; slots stay, tagged with the old epoch).
-  if (tid == 0) {
-    const uint32_t out =
-        __hip_atomic_fetch_add(ctl + kCtlExits, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = out == gridDim.x - 1 ? 1u : 0u;
-  }
-  __syncthreads();
-  if (s_last) {
-    if (tid < kMaxQueues)
-      __hip_atomic_store(ctl + kCtlQueues + 4 * tid + 2, 0u, __ATOMIC_RELAXED,
-                         __HIP_MEMORY_SCOPE_AGENT);
-    if (tid == 0) {
-      __hip_atomic_store(ctl + kCtlHeadTicket, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_store(ctl + kCtlExits, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      __hip_atomic_fetch_add(ctl + kCtlEpoch, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    }
+    if (tid == 0) atomicAdd(a.accessed, ((wsum[0] + wsum[1]) + wsum[2]) + wsum[3]);
   }
 }
 
@@ -1250,7 +894,6 @@ struct SelectParams {
   const void* query;
   const void* key_mean;
   const void* ellipsoid;
-  const void* value_mean;  // non-null: also build representative partials
   const float* value_norm;
   const float* max_value_norm;
   int64_t heads, group, dim, n_blocks, block, length;
@@ -1283,15 +926,14 @@ int validate_select(const SelectParams& p, const char* who, Layout& L) {
     return set_error(kInvalidArgument, "%s: n_blocks != ceil(prompt_length / block_size)", who);
   if (p.reduction < 0 || p.reduction > 2)
     return set_error(kInvalidArgument, "%s: reduction code %d", who, p.reduction);
-  if (!aligned(p.query, 16) || !aligned(p.key_mean, 16) || !aligned(p.ellipsoid, 16) ||
-      (p.value_mean && !aligned(p.value_mean, 16)))
+  if (!aligned(p.query, 16) || !aligned(p.key_mean, 16) || !aligned(p.ellipsoid, 16))
     return set_error(kInvalidArgument, "%s: query/summary must be 16-byte aligned", who);
   L = make_layout(p.heads, p.group, p.dim, p.n_blocks);
   if (!p.ws || p.ws_bytes < (size_t)L.total || !aligned(p.ws, 256))
     return set_error(kWorkspaceTooSmall, "%s: workspace needs %lld bytes, 256-byte aligned", who,
                      (long long)L.total);
   if (L.n_tiles > 0x7FFFFFFF) return set_error(kInvalidArgument, "%s: too many blocks", who);
-  if (score_smem(p.group, p.dim, true) > 64 * 1024)
+  if (score_smem(p.group, p.dim) > 64 * 1024)
     return set_error(kUnsupported, "%s: group x head_dim too large", who);
   return kOk;
 }
@@ -1301,17 +943,13 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
   sa.query = static_cast<const uint16_t*>(p.query);
   sa.key_mean = static_cast<const uint16_t*>(p.key_mean);
   sa.ellipsoid = static_cast<const uint16_t*>(p.ellipsoid);
-  sa.value_mean = static_cast<const uint16_t*>(p.value_mean);
-  sa.z = at<float>(p.ws, L.z);
-  sa.delta = at<float>(p.ws, L.delta);
+  sa.zf = at<float4>(p.ws, L.zf);
   sa.lse = at<float>(p.ws, L.lse);
-  sa.rep_acc = at<float>(p.ws, L.rep_acc);
   sa.n_blocks = p.n_blocks;
-  sa.n_tiles = L.n_tiles;
-  sa.z_stride = L.z_stride;
-  sa.tile_stride = L.tile_stride;
   sa.block = p.block;
   sa.length = p.length;
+  sa.z_stride = L.z_stride;
+  sa.tile_stride = L.tile_stride;
   sa.group = (int)p.group;
   sa.scale = (float)pow((double)p.dim, -0.5);
   return sa;
@@ -1319,126 +957,51 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
 
 DecideArgs decide_args(const SelectParams& p, const Layout& L) {
   DecideArgs da;
-  da.z = at<float>(p.ws, L.z);
-  da.delta = at<float>(p.ws, L.delta);
+  da.zf = at<float4>(p.ws, L.zf);
   da.lse = at<float>(p.ws, L.lse);
   da.value_norm = p.value_norm;
   da.max_value_norm = p.max_value_norm;
-  da.value_mean = static_cast<const uint16_t*>(p.value_mean);
   da.anchor = p.anchor;
   da.mask = p.mask;
-  da.tilebits = at<uint64_t>(p.ws, L.tilebits);
   da.risk_out = p.risk_out;
   da.stats_out = p.stats_out;
-  da.accessed = p.accessed;
-  da.rep_acc = at<float>(p.ws, L.rep_acc);
   da.n_blocks = p.n_blocks;
   da.n_tiles = L.n_tiles;
-  da.z_stride = L.z_stride;
-  da.tile_stride = L.tile_stride;
   da.block = p.block;
   da.length = p.length;
+  da.z_stride = L.z_stride;
+  da.tile_stride = L.tile_stride;
   da.group = (int)p.group;
   da.reduction = p.reduction;
-  da.dim = (int)p.dim;
   da.eps = p.eps;
   return da;
 }
 
-// Selection only (rkv_select): score and decide as two kernels.
-int launch_select(const SelectParams& p, const Layout& L) {
+int launch_score(const SelectParams& p, const Layout& L) {
   const ScoreArgs sa = score_args(p, L);
-  const DecideArgs da = decide_args(p, L);
-  const size_t smem = score_smem(p.group, p.dim, false);
-  dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
-  mark(0, p.stream);
+  const dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
   RKV_DISPATCH_DIM(p.dim, D,
-                   score_kernel<D, false><<<grid, dim3(kThreads), smem, p.stream>>>(sa));
-  int rc = check_launch("score_kernel");
+                   score_kernel<D><<<grid, dim3(kThreads), score_smem(p.group, p.dim),
+                                     p.stream>>>(sa));
+  return check_launch("score_kernel");
+}
+
+// Selection only (rkv_select): score and decide kernels.
+int launch_select(const SelectParams& p, const Layout& L) {
+  mark(0, p.stream);
+  int rc = launch_score(p, L);
   if (rc) return rc;
   mark(1, p.stream);
-  decide_kernel<<<grid, dim3(kThreads), 0, p.stream>>>(da);
+  const DecideArgs da = decide_args(p, L);
+  decide_kernel<<<dim3((unsigned)L.n_tiles, (unsigned)p.heads), dim3(kThreads), 0, p.stream>>>(
+      da, p.accessed);
   rc = check_launch("decide_kernel");
   mark(2, p.stream);
   return rc;
 }
 
-// Grid of the persistent kernel: as many workgroups as the device holds at
-// once (more would only wait for a slot), never more than there are items.
-struct GridCache {
-  const void* fn;
-  int device;
-  size_t dyn;
-  int per_cu, cus;
-  size_t static_lds, private_bytes;
-};
-
-constexpr int kNotEligible = -1;  // internal: use the split pipeline
-
-// Launches the persistent kernel, or returns kNotEligible when this build of
-// it does not meet the persistent kernel's resource rules (LDS per
-// workgroup, no private memory traffic): its workgroups wait on each other,
-// so each must run with everything it needs from its first instruction.
-template <int D, int GBM>
-int launch_decode(const DecodeArgs& da, size_t dyn, uint32_t items, hipStream_t stream) {
-  const void* fn = reinterpret_cast<const void*>(&decode_kernel<D, GBM>);
-  int device = 0;
-  if (hipGetDevice(&device) != hipSuccess)
-    return set_error(kLaunchFailed, "rkv_decode: no current device");
-  thread_local GridCache cache[16] = {};
-  thread_local int cache_next = 0;
-  GridCache* hit = nullptr;
-  for (GridCache& e : cache)
-    if (e.fn == fn && e.device == device && e.dyn == dyn) hit = &e;
-  if (!hit) {
-    GridCache e{fn, device, dyn, 0, 0, 0, 0};
-    hipFuncAttributes attr;
-    if (hipFuncGetAttributes(&attr, fn) != hipSuccess ||
-        hipDeviceGetAttribute(&e.cus, hipDeviceAttributeMultiprocessorCount, device) !=
-            hipSuccess)
-      return set_error(kLaunchFailed, "rkv_decode: cannot query the device");
-    e.static_lds = attr.sharedSizeBytes;
-    e.private_bytes = attr.localSizeBytes;
-    if (e.static_lds + dyn <= kMaxFusedLds &&
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&e.per_cu, decode_kernel<D, GBM>, kThreads,
-                                                     dyn) != hipSuccess)
-      return set_error(kLaunchFailed, "rkv_decode: occupancy query failed");
-    hit = &cache[cache_next];
-    cache_next = (cache_next + 1) % 16;
-    *hit = e;
-  }
-  if (hit->static_lds + dyn > kMaxFusedLds || hit->private_bytes > kMaxFusedPrivate ||
-      hit->per_cu < 1)
-    return kNotEligible;
-  const int64_t slots = (int64_t)hit->per_cu * hit->cus;
-  const unsigned grid = (unsigned)(slots < (int64_t)items ? slots : (int64_t)items);
-  decode_kernel<D, GBM><<<dim3(grid), dim3(kThreads), dyn, stream>>>(da);
-  return check_launch("decode_kernel");
-}
-
-template <int D>
-int launch_decode_rows(const DecodeArgs& da, int64_t rows_per_block, size_t dyn, uint32_t items,
-                       hipStream_t stream) {
-  if constexpr (D > kMaxFusedDim) {
-    return kNotEligible;
-  } else {
-    constexpr int CH = D / 16;
-    constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
-    switch (rows_per_block) {
-      case 4:
-        return launch_decode<D, 4>(da, dyn, items, stream);
-      case 8:
-        if constexpr (CAP >= 8) return launch_decode<D, 8>(da, dyn, items, stream);
-        break;
-      default:
-        if constexpr (CAP >= 16) return launch_decode<D, 16>(da, dyn, items, stream);
-        break;
-    }
-    return kNotEligible;
-  }
-}
-
 struct DecodeBuffers {
+  const void* value_mean;
   const void* key_pages;
   int64_t kp_hs;
   const void* value_pages;
@@ -1456,14 +1019,17 @@ AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffe
   AttendArgs aa;
   aa.decide = decide_args(p, L);
   aa.query = static_cast<const uint16_t*>(p.query);
+  aa.value_mean = static_cast<const uint16_t*>(b.value_mean);
   aa.key_pages = static_cast<const uint16_t*>(b.key_pages);
   aa.value_pages = static_cast<const uint16_t*>(b.value_pages);
-  aa.key_suffix = static_cast<const uint16_t*>(b.key_suffix);
-  aa.value_suffix = static_cast<const uint16_t*>(b.value_suffix);
+  // with no suffix the pages stand in (never read: no suffix rows)
+  aa.key_suffix = static_cast<const uint16_t*>(b.suffix_cap ? b.key_suffix : b.key_pages);
+  aa.value_suffix = static_cast<const uint16_t*>(b.suffix_cap ? b.value_suffix : b.value_pages);
   aa.suffix_len_dev = b.suffix_len;
   aa.part_m = at<float>(p.ws, L.part_m);
   aa.part_l = at<float>(p.ws, L.part_l);
   aa.part_acc = at<float>(p.ws, L.part_acc);
+  aa.tile_counts = p.accessed ? at<uint32_t>(p.ws, L.counts) : nullptr;
   aa.kp_hs = b.kp_hs;
   aa.vp_hs = b.vp_hs;
   aa.ks_hs = b.ks_hs;
@@ -1471,8 +1037,9 @@ AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffe
   aa.vs_hs = b.vs_hs;
   aa.vs_ts = b.vs_ts;
   aa.suffix_cap = b.suffix_cap;
-  aa.part_stride = L.part_stride;
-  aa.row_blocks = (int)L.row_blocks;
+  const int64_t rows = rows_per_pass(p.group, p.dim);
+  aa.row_passes = (int)((p.group + rows - 1) / rows);
+  aa.log2_block = p.block == 16 ? 4 : (p.block == 32 ? 5 : 6);
   aa.scale = (float)pow((double)p.dim, -0.5);
   return aa;
 }
@@ -1483,78 +1050,57 @@ MergeArgs merge_args(const SelectParams& p, const Layout& L, const DecodeBuffers
   ma.part_l = at<float>(p.ws, L.part_l);
   ma.part_acc = at<float>(p.ws, L.part_acc);
   ma.out = static_cast<uint16_t*>(b.output);
-  ma.part_stride = L.part_stride;
-  ma.group = (int)p.group;
-  ma.parts = (int)(L.n_tiles + 1);
+  ma.tile_counts = at<uint32_t>(p.ws, L.counts);
+  ma.accessed = p.accessed;
+  ma.tile_stride = L.tile_stride;
+  ma.parts = (int)L.n_tiles;
   ma.dim = (int)p.dim;
+  ma.heads = (int)p.heads;
   return ma;
 }
 
-// The split pipeline: score kernel, then decide+attend (and the suffix), then
-// merge.
-int launch_split(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
-  const ScoreArgs sa = score_args(p, L);
+template <int D>
+int launch_attend(const AttendArgs& aa, int64_t rows, dim3 grid, hipStream_t stream) {
+  constexpr int CH = D / 16;
+  constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
+  switch (rows) {
+    case 4:
+      attend_kernel<D, 4><<<grid, dim3(kThreads), 0, stream>>>(aa);
+      return check_launch("attend_kernel");
+    case 8:
+      if constexpr (CAP >= 8) {
+        attend_kernel<D, 8><<<grid, dim3(kThreads), 0, stream>>>(aa);
+        return check_launch("attend_kernel");
+      }
+      break;
+    default:
+      if constexpr (CAP >= 16) {
+        attend_kernel<D, 16><<<grid, dim3(kThreads), 0, stream>>>(aa);
+        return check_launch("attend_kernel");
+      }
+      break;
+  }
+  return set_error(kUnsupported, "rkv_decode: no attention kernel for this group");
+}
+
+// One decode step: score, decide + attend, merge.
+int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const AttendArgs aa = attend_args(p, L, b);
   const MergeArgs ma = merge_args(p, L, b);
-  const dim3 score_grid((unsigned)L.n_tiles, (unsigned)p.heads);
-  const dim3 attend_grid((unsigned)(L.n_tiles + 1), (unsigned)p.heads);
-  const size_t attend_lds = attend_smem(p.group, p.dim);
+  const dim3 tiles((unsigned)L.n_tiles, (unsigned)p.heads);
   mark(0, p.stream);
-  RKV_DISPATCH_DIM(p.dim, D,
-                   score_kernel<D, true><<<score_grid, dim3(kThreads),
-                                           score_smem(p.group, p.dim, true), p.stream>>>(sa));
-  int rc = check_launch("score_kernel");
+  int rc = launch_score(p, L);
   if (rc) return rc;
   mark(1, p.stream);
   rc = kUnsupported;
-  RKV_DISPATCH_DIM(p.dim, D, {
-    constexpr int CH = D / 16;
-    constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
-    switch (L.rows_per_block) {
-      case 4:
-        attend_kernel<D, 4><<<attend_grid, dim3(kThreads), attend_lds, p.stream>>>(aa);
-        rc = check_launch("attend_kernel");
-        break;
-      case 8:
-        if constexpr (CAP >= 8) {
-          attend_kernel<D, 8><<<attend_grid, dim3(kThreads), attend_lds, p.stream>>>(aa);
-          rc = check_launch("attend_kernel");
-        }
-        break;
-      default:
-        if constexpr (CAP >= 16) {
-          attend_kernel<D, 16><<<attend_grid, dim3(kThreads), attend_lds, p.stream>>>(aa);
-          rc = check_launch("attend_kernel");
-        }
-        break;
-    }
-  });
+  const int64_t rows = rows_per_pass(p.group, p.dim);
+  RKV_DISPATCH_DIM(p.dim, D, rc = launch_attend<D>(aa, rows, tiles, p.stream));
   if (rc) return rc;
   mark(2, p.stream);
   merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
                  dim3(kThreads), 0, p.stream>>>(ma);
   rc = check_launch("merge_kernel");
   mark(3, p.stream);
-  return rc;
-}
-
-// The persistent kernel, or kNotEligible.
-int launch_fused(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
-  if (p.dim > kMaxFusedDim || p.heads > kMaxHeads) return kNotEligible;
-  DecodeArgs da;
-  da.score = score_args(p, L);
-  da.attend = attend_args(p, L, b);
-  da.merge = merge_args(p, L, b);
-  da.control = at<uint32_t>(p.ws, L.control);
-  da.heads = (int)p.heads;
-  da.merge_cols = (int)((p.dim + kMergeD - 1) / kMergeD);
-  const uint32_t items =
-      (uint32_t)(p.heads * (2 * L.n_tiles + 1 + p.group * da.merge_cols));
-  const int64_t dyn_score = (int64_t)score_smem(p.group, p.dim, true);
-  const int64_t dyn_attend = (int64_t)attend_smem(p.group, p.dim);
-  const size_t dyn = (size_t)(dyn_score > dyn_attend ? dyn_score : dyn_attend);
-  int rc = kNotEligible;
-  RKV_DISPATCH_DIM(p.dim, D, rc = launch_decode_rows<D>(da, L.rows_per_block, dyn, items, p.stream));
   return rc;
 }
 
@@ -1569,19 +1115,18 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
   return (size_t)make_layout(heads, group, dim, n_blocks).total;
 }
 
-// Byte offsets of the workspace regions, for tests: control, z, delta, lse,
-// tilebits, rep_acc, part_m, part_l, part_acc, total, then n_tiles, the row
-// stride of z / delta, of the per-tile arrays and of the partials.
+// Byte offsets of the workspace regions, for tests: control, zf (z, delta,
+// A, th per row and block), lse, part_m, part_l, part_acc, counts, total,
+// then n_tiles, the row stride (blocks) of zf and of the per-tile arrays.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out14) {
+                                    int64_t* out11) {
   clear_error();
-  if (!out14 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out11 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[14] = {L.control, L.z,        L.delta,    L.lse,         L.tilebits,
-                         L.rep_acc, L.part_m,   L.part_l,   L.part_acc,    L.total,
-                         L.n_tiles, L.z_stride, L.tile_stride, L.part_stride};
-  for (int i = 0; i < 14; ++i) out14[i] = v[i];
+  const int64_t v[11] = {L.control, L.zf,    L.lse,     L.part_m,   L.part_l,     L.part_acc,
+                         L.counts,  L.total, L.n_tiles, L.z_stride, L.tile_stride};
+  for (int i = 0; i < 11; ++i) out11[i] = v[i];
   return kOk;
 }
 
@@ -1593,8 +1138,8 @@ extern "C" int rkv_select(const void* query, const void* key_mean, const void* e
                           float* stats_out, unsigned long long* accessed_blocks, void* workspace,
                           size_t workspace_bytes, hipStream_t stream) {
   clear_error();
-  SelectParams p{query, key_mean, ellipsoid, nullptr, value_norm, max_value_norm, heads, group,
-                 dim, n_blocks, block_size, prompt_length, eps, reduction, anchor_mask, mask_out,
+  SelectParams p{query, key_mean, ellipsoid, value_norm, max_value_norm, heads, group, dim,
+                 n_blocks, block_size, prompt_length, eps, reduction, anchor_mask, mask_out,
                  risk_out, stats_out, accessed_blocks, workspace, workspace_bytes, stream};
   Layout L;
   int rc = validate_select(p, "rkv_select", L);
@@ -1618,9 +1163,9 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
                           size_t workspace_bytes, hipStream_t stream) {
   clear_error();
   if (!value_mean) return set_error(kInvalidArgument, "rkv_decode: null value_mean");
-  SelectParams p{query, key_mean, ellipsoid, value_mean, value_norm, max_value_norm, heads,
-                 group, dim, n_blocks, block_size, prompt_length, eps, reduction, anchor_mask,
-                 mask_out, nullptr, nullptr, accessed_blocks, workspace, workspace_bytes, stream};
+  SelectParams p{query, key_mean, ellipsoid, value_norm, max_value_norm, heads, group, dim,
+                 n_blocks, block_size, prompt_length, eps, reduction, anchor_mask, mask_out,
+                 nullptr, nullptr, accessed_blocks, workspace, workspace_bytes, stream};
   Layout L;
   int rc = validate_select(p, "rkv_decode", L);
   if (rc) return rc;
@@ -1633,6 +1178,9 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
   const int64_t es = 2;
   const int64_t ch_bytes = dim / 16 * es;
   const uintptr_t need = ch_bytes % 16 == 0 ? 16 : (ch_bytes % 8 == 0 ? 8 : 4);
+  if (!aligned(value_mean, need))
+    return set_error(kInvalidArgument, "rkv_decode: value_mean must be %d-byte aligned",
+                     (int)need);
   if (!aligned(key_pages, need) || !aligned(value_pages, need) ||
       (key_page_head_stride * es) % need || (value_page_head_stride * es) % need)
     return set_error(kInvalidArgument, "rkv_decode: pages must be %d-byte aligned", (int)need);
@@ -1644,39 +1192,18 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
                      (int)need);
   if (!aligned(output, 4)) return set_error(kInvalidArgument, "rkv_decode: output alignment");
 
-  const DecodeBuffers b{key_pages,     key_page_head_stride,   value_pages,
-                        value_page_head_stride,  key_suffix,   key_suffix_head_stride,
+  const DecodeBuffers b{value_mean, key_pages, key_page_head_stride, value_pages,
+                        value_page_head_stride, key_suffix, key_suffix_head_stride,
                         key_suffix_token_stride, value_suffix, value_suffix_head_stride,
                         value_suffix_token_stride, suffix_capacity, suffix_length, output};
-  if (g_pipeline == 1 || g_pipeline == 3) {
-    mark(0, stream);
-    rc = launch_fused(p, L, b);
-    if (rc != kNotEligible) {
-      if (rc == kOk) mark(1, stream);
-      return rc;
-    }
-    if (g_pipeline == 1)
-      return set_error(kUnsupported, "rkv_decode: the persistent kernel does not run this shape");
-  }
-  return launch_split(p, L, b);
+  return launch_decode(p, L, b);
 }
 
 // Profiling hook: when events is non-null, the following rkv_select /
 // rkv_decode calls on this thread record events[0] before their first kernel
-// and events[k] after their k-th (rkv_select: score, decide; rkv_decode: the
-// persistent kernel, or score, decide, pages, merge on the split pipeline).
-// Pass NULL to stop.
+// and events[k] after their k-th (rkv_select: score, decide; rkv_decode:
+// score, attend, merge).  Pass NULL to stop.
 extern "C" int rkv_set_profile_events(void* events) {
   g_events = static_cast<hipEvent_t*>(events);
-  return kOk;
-}
-
-// Test and benchmark hook: 0 automatic (the split pipeline), 1 persistent
-// kernel (RKV_UNSUPPORTED where it cannot run), 2 split pipeline, 3 the
-// persistent kernel where it runs, else the split pipeline.  Per thread.
-extern "C" int rkv_set_decode_pipeline(int mode) {
-  clear_error();
-  if (mode < 0 || mode > 3) return set_error(kInvalidArgument, "rkv_set_decode_pipeline: mode");
-  g_pipeline = mode;
   return kOk;
 }

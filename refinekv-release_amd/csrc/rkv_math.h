@@ -110,7 +110,13 @@ RKV_HD float expf_(float x) {
   p = __builtin_fmaf(p, r, 0.5f);
   p = __builtin_fmaf(p, r, 1.0f);
   p = __builtin_fmaf(p, r, 1.0f);
+#if defined(__HIP_DEVICE_COMPILE__)
+  // v_ldexp_f32 rounds once, exactly as scale_pow2's exact-then-rounded
+  // multiplies do.
+  return __builtin_amdgcn_ldexpf(p, (int)k);
+#else
   return scale_pow2(p, (int)k);
+#endif
 }
 
 // log(x): the reduction of fdlibm's e_log.c (Sun Microsystems, 1993):

@@ -55,8 +55,6 @@ def _bind(lib):
     lib.rkv_math_probe.restype = _int
     lib.rkv_set_profile_events.argtypes = [_p]
     lib.rkv_set_profile_events.restype = _int
-    lib.rkv_set_decode_pipeline.argtypes = [_int]
-    lib.rkv_set_decode_pipeline.restype = _int
     return lib
 
 
@@ -141,9 +139,8 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("control", "z", "delta", "lse", "tilebits", "rep_acc", "part_m", "part_l",
-                "part_acc", "total", "n_tiles", "z_stride", "tile_stride", "part_stride")
-CONTROL_ERROR_WORD = 2  # sticky flag: a decode kernel's dependency wait timed out
+LAYOUT_NAMES = ("control", "zf", "lse", "part_m", "part_l", "part_acc", "counts", "total",
+                "n_tiles", "z_stride", "tile_stride")
 
 
 def workspace_layout(heads, group, dim, n_blocks):
@@ -167,8 +164,7 @@ def _buffer(workspace, name, shape, device, dtype, zero=False):
 
 
 def _scratch(workspace, heads, group, dim, n_blocks, device):
-    """The kernels' workspace.  Zero-filled once when made: rkv_decode's
-    control words start at zero and every call leaves them at zero."""
+    """The kernels' workspace (zero-filled once when made)."""
     nbytes = workspace_bytes(heads, group, dim, n_blocks)
     return _buffer(workspace, "hip_scratch", (nbytes,), device, torch.uint8, zero=True)
 
@@ -248,13 +244,3 @@ def math_probe(fn, x):
     _check(lib().rkv_math_probe(code, _ptr(x), _ptr(y), x.numel(), _stream(x.device)),
            "rkv_math_probe")
     return y
-
-
-PIPELINES = {"auto": 0, "persistent": 1, "split": 2, "prefer_persistent": 3}
-
-
-def set_decode_pipeline(name):
-    """Which rkv_decode pipeline runs on this thread: "auto" (the split
-    pipeline), "persistent", "split", or "prefer_persistent" (the persistent
-    kernel where it runs, else split); a test and benchmark hook."""
-    _check(lib().rkv_set_decode_pipeline(PIPELINES[name]), "rkv_set_decode_pipeline")

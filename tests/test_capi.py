@@ -47,28 +47,28 @@ def test_version_and_error_channel(lib):
     assert lib.rkv_version() >= 1
     assert lib.rkv_workspace_layout(0, 0, 0, 0, None) == 1
     assert b"bad arguments" in lib.rkv_last_error()
-    assert lib.rkv_set_decode_pipeline(4) == 1
-    assert lib.rkv_set_decode_pipeline(0) == 0 and lib.rkv_last_error() == b""
 
 
 def test_workspace_size_covers_layout(lib):
     from refinekv import _hip
 
-    controls = _hip.workspace_layout(1, 1, 32, 1)["z"]
+    controls = _hip.workspace_layout(1, 1, 32, 1)["zf"]
     for heads, group, dim, n in ((8, 4, 128, 4096), (4, 7, 128, 1024), (2, 16, 64, 3),
                                  (1, 1, 256, 1)):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
-        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:10]]
+        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:8]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
-        rows, tiles = heads * group, layout["n_tiles"]
+        rows, tiles, ts = heads * group, layout["n_tiles"], layout["tile_stride"]
         # fixed-size control block first, so every shape finds it at offset 0
-        assert layout["control"] == 0 and layout["z"] == controls
-        # padded strides: every head's slice covers whole 256-byte lines
-        assert layout["z_stride"] == tiles * 64 and layout["tile_stride"] % 64 == 0
-        assert layout["part_stride"] % 64 == 0 and layout["part_stride"] >= tiles + 1
-        assert layout["delta"] - layout["z"] >= rows * layout["z_stride"] * 4
-        assert layout["part_m"] - layout["rep_acc"] >= rows * layout["tile_stride"] * dim * 4
-        assert layout["total"] - layout["part_acc"] >= rows * layout["part_stride"] * dim * 4
+        assert layout["control"] == 0 and layout["zf"] == controls
+        # padded strides: zf rows cover whole tiles, per-tile rows 64 tiles
+        assert layout["z_stride"] == tiles * 64 and ts % 64 == 0 and ts >= tiles
+        assert layout["lse"] - layout["zf"] >= rows * layout["z_stride"] * 16
+        assert layout["part_m"] - layout["lse"] >= rows * ts * 16
+        assert layout["part_l"] - layout["part_m"] >= rows * ts * 4
+        assert layout["part_acc"] - layout["part_l"] >= rows * ts * 4
+        assert layout["counts"] - layout["part_acc"] >= rows * ts * dim * 4
+        assert layout["total"] - layout["counts"] >= heads * ts * 4
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0

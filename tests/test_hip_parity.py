@@ -174,10 +174,10 @@ def test_selection_bit_exact(hip, oracle_lib, heads, group, dim, block, prompt, 
     st = oracle_lib.select_stats(qn, summ)
     layout = hip.workspace_layout(heads, group, dim, n)
     scratch = ws["hip_scratch"].cpu().numpy()
-    rows, stride = heads * group, layout["n_tiles"] * 64  # blocks padded to whole tiles
-    z = scratch[layout["z"]:layout["z"] + rows * stride * 4].view(np.float32)
-    delta = scratch[layout["delta"]:layout["delta"] + rows * stride * 4].view(np.float32)
-    z, delta = z.reshape(rows, stride)[:, :n], delta.reshape(rows, stride)[:, :n]
+    rows, stride = heads * group, layout["z_stride"]  # blocks padded to whole tiles
+    zf = scratch[layout["zf"]:layout["zf"] + rows * stride * 16].view(np.float32)
+    zf = zf.reshape(rows, stride, 4)[:, :n]
+    z, delta = np.ascontiguousarray(zf[..., 0]), np.ascontiguousarray(zf[..., 1])
     assert np.array_equal(bits32(z), bits32(st["z"].reshape(rows, n))), "z"
     assert np.array_equal(bits32(delta), bits32(st["delta"].reshape(rows, n))), "delta"
     sc = stats.cpu().numpy()
@@ -195,50 +195,30 @@ def test_selection_bit_exact(hip, oracle_lib, heads, group, dim, block, prompt, 
 # Decode step
 # ---------------------------------------------------------------------------
 
-# The persistent decode kernel once faulted the GPU on this shape (head_dim
-# 256, its first launch at that width); the cause is not yet shown, so the
-# case stays off the GPU (on every pipeline) until it is.  head_dim > 128 now
-# runs the split pipeline.
+# This shape faulted the GPU on the first launch of a since-removed persistent
+# decode kernel's head_dim-256 build; the cause was never shown, so the case
+# stays off the GPU.  Other head_dim-256 decode shapes run below.
 FAULTED = (2, 4, 256, 64, 999, "max", 0.01, 0.05)
 
 DECODE_CASES = [
-    pytest.param(*c, marks=pytest.mark.skip(reason="faulted the GPU with the persistent "
-                                            "decode kernel; cause not yet shown"))
+    pytest.param(*c, marks=pytest.mark.skip(reason="faulted the GPU with a since-removed "
+                                            "persistent decode kernel; cause not shown"))
     if c == FAULTED else c
     for c in SELECT_CASES + [
         (8, 4, 128, 32, 4096, "any", 0.0, 0.02),   # every block expanded (dense)
         (8, 4, 128, 32, 4096, "mean", 1e6, 0.02),  # none expanded
+        (2, 2, 256, 32, 1500, "any", 0.01, 0.05),
+        (2, 4, 224, 16, 700, "max", 0.01, 0.05),
     ]
 ]
-
-
-@pytest.fixture(params=["split", "prefer_persistent"])
-def pipeline(request, hip):
-    """Each decode test on the split pipeline (the default) and on the
-    persistent kernel where it runs (else the split pipeline again)."""
-    hip.set_decode_pipeline(request.param)
-    yield request.param
-    hip.set_decode_pipeline("auto")
 
 
 def _pages_bits(t, block):
     return gc.bf16_bits(gc.padded_pages(t, block))
 
 
-def assert_control_clean(ws):
-    """After a decode the persistent kernel's device-wide counters are back at
-    zero (head ticket, exit count) and no dependency wait timed out (the
-    queue words and slots are epoch-tagged and keep their values)."""
-    from refinekv import _hip
-
-    torch.cuda.synchronize()
-    words = ws["hip_scratch"][:64].view(torch.int32).cpu().numpy()
-    assert words[_hip.CONTROL_ERROR_WORD] == 0, "a dependency wait timed out"
-    assert words[0] == 0 and words[1] == 0, words[:4]
-
-
 @pytest.mark.parametrize("heads,group,dim,block,prompt,reduction,eps,spikes", DECODE_CASES)
-def test_decode_matches_oracle(hip, oracle_lib, pipeline, heads, group, dim, block, prompt,
+def test_decode_matches_oracle(hip, oracle_lib, heads, group, dim, block, prompt,
                                reduction, eps, spikes):
     inp = _decode_case(heads, group, dim, block, prompt, spikes, suffix=16)
     cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps, gqa_reduction=reduction)
@@ -269,7 +249,6 @@ def test_decode_matches_oracle(hip, oracle_lib, pipeline, heads, group, dim, blo
                 f"mask suffix={suffix} anchor={use_anchor}"
             got = res.output.float().cpu().numpy()[:, :, 0]
             assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
-            assert_control_clean(ws)
 
 
 def test_device_suffix_length_matches_slicing(hip):
@@ -288,7 +267,7 @@ def test_device_suffix_length_matches_slicing(hip):
         assert torch.equal(actual, expected), count
 
 
-def test_workspace_reuse_and_access_counter(hip, oracle_lib, pipeline):
+def test_workspace_reuse_and_access_counter(hip, oracle_lib):
     inp = _decode_case(4, 4, 128, 32, 5000, 0.05)
     cfg = RefineKVConfig(backend="hip", eps=0.01)
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
@@ -303,14 +282,12 @@ def test_workspace_reuse_and_access_counter(hip, oracle_lib, pipeline):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
     want = oracle_lib.access_blocks(mask.cpu().numpy(), summary.counts.cpu().numpy())
     assert int(counter.item()) == 3 * want
-    assert_control_clean(ws)
 
 
 def test_graph_replays_match_eager(hip):
     """A captured decode step replayed several times (suffix length advanced
     on the device between replays, eager work and syncs in between) gives the
-    eager result every time: the kernel's counters start from zero on every
-    replay."""
+    eager result every time."""
     inp = _decode_case(8, 4, 128, 32, 8192, 0.05, suffix=16, seed=3)
     cfg = RefineKVConfig(backend="hip", eps=0.01)
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
@@ -331,7 +308,6 @@ def test_graph_replays_match_eager(hip):
                                 workspace={}).output
         torch.cuda.synchronize()
         assert torch.equal(got, want), count
-        assert_control_clean(ws)
 
 
 @pytest.mark.parametrize("path", [p for p in gc.fixture_paths() if "f32" not in p],
@@ -357,16 +333,11 @@ def test_reference_golden_end_to_end(hip, path):
     assert_close_output(res.output.float().cpu().numpy(), g["output"])
 
 
-@pytest.mark.parametrize("mode", ["persistent", "split"])
-def test_headline_shape_128k(hip, oracle_lib, mode):
+def test_headline_shape_128k(hip, oracle_lib):
     """BASELINE config 3 shape (H_kv 8, G 4, d 128, 131072 prompt tokens, B 32):
     masks equal the oracle's at full size, outputs within tolerance, and the
     all-expanded step equals dense attention."""
-    hip.set_decode_pipeline(mode)
-    try:
-        _headline_shape_128k(hip, oracle_lib)
-    finally:
-        hip.set_decode_pipeline("auto")
+    _headline_shape_128k(hip, oracle_lib)
 
 
 def _headline_shape_128k(hip, oracle_lib):
