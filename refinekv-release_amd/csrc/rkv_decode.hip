@@ -356,11 +356,10 @@ struct DecideArgs {
 };
 
 struct DecideShared {
-  float gstat[kMaxGroup][2];
-  float risk[kMaxGroup][kTile];
-  int32_t list[kTile];  // tile-relative indices of the expanded blocks, ascending
-  uint64_t bits;        // expanded-block ballot
-  uint32_t accessed;    // access count of the tile
+  float risk[kMaxGroup][kTile];  // the mean reduction reads every row's risks
+  uint64_t wsel[kWaves];         // per wave: OR over its rows of (risk > eps or not finite)
+  uint32_t wbad[kWaves];         // per wave: a row's log Z or log C is not finite
+  int32_t list[kWaves][kTile];   // per wave: the expanded blocks (tile-relative), ascending
 };
 
 // LSE of one row from the tile partials in the fixed order: the max first,
@@ -379,12 +378,20 @@ __device__ __forceinline__ float merge_lse(float m0, float l0, const float* part
   return logf_(wave_sum_u(acc)) + ms;
 }
 
-// Decides tile `tile` of head h: stores the mask (and risk / stats when
-// asked); leaves the tile's ballot, expanded-block list and access count in
-// `sh`, and z of every (row, block) of the tile in zsh when it is not null
-// (-inf for blocks past the end).  Ends with a barrier.
-__device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int64_t tile,
-                                            DecideShared& sh, float (*zsh)[kTile]) {
+// Decides tile `tile` of head h (select_blocks_reference plus the anchor
+// union): stores the mask (and risk / stats when asked) and returns the
+// tile's expanded-block ballot, uniform over the workgroup; list (this
+// wave's copy in sh) holds the expanded blocks in ascending order.  zsh, when
+// not null, receives z of every (row, block) of the tile (-inf past the end).
+// count (thread 0) receives the tile's access count.  One barrier.
+//
+// After the fail-safes the max reduction selects exactly the blocks "any"
+// selects: a NaN risk makes the max NaN (not > eps) but is non-finite, which
+// selects the block anyway.  So both are the OR over rows of
+// (risk > eps or risk not finite); mean sums the rows in order.
+__device__ __forceinline__ uint64_t decide_tile(const DecideArgs& a, int64_t h, int64_t tile,
+                                                DecideShared& sh, float (*zsh)[kTile],
+                                                const int32_t*& list, uint32_t& count) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
@@ -395,6 +402,8 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
   const float vmax = a.max_value_norm[h];
 
   // ---- log Z, log C of each row this wave owns, then its risks ----------
+  uint64_t wsel = 0;
+  bool wbad = false;
 #pragma unroll 1
   for (int g = wave; g < G; g += kWaves) {
     const float* prow = a.lse + (h * G + g) * a.tile_stride * 4;
@@ -404,73 +413,71 @@ __device__ __forceinline__ void decide_tile(const DecideArgs& a, int64_t h, int6
     if (valid) zf = a.zf[(h * G + g) * a.z_stride + b];
     const float lz = merge_lse(part.x, part.y, prow, 0, T, lane);
     const float lc = merge_lse(part.z, part.w, prow, 1, T, lane);
-    if (lane == 0) {
-      sh.gstat[g][0] = lz;
-      sh.gstat[g][1] = lc;
-      if (a.stats_out && tile == 0) {
-        a.stats_out[(h * G + g) * 2] = lz;
-        a.stats_out[(h * G + g) * 2 + 1] = lc;
-      }
+    if (a.stats_out && tile == 0 && lane == 0) {
+      a.stats_out[(h * G + g) * 2] = lz;
+      a.stats_out[(h * G + g) * 2 + 1] = lc;
     }
+    wbad |= !is_finite(lz) || !is_finite(lc);
     float r = 0.0f;
     if (valid) {
       r = risk_from(zf.x, zf.y, zf.z, zf.w, lz, lc, vmax, vnorm);
       if (a.risk_out) a.risk_out[(h * G + g) * N + b] = r;
     }
+    wsel |= __ballot(valid && (r > a.eps || !is_finite(r)));
     sh.risk[g][lane] = r;
     if (zsh) zsh[g][lane] = valid ? zf.x : kNegInf;
   }
-  __syncthreads();
-
-  // ---- GQA reduction, fail-safes, anchors (select_blocks_reference) ------
-  if (wave == 0) {
-    bool bad_global = false;
-    for (int g = 0; g < G; ++g) bad_global |= !is_finite(sh.gstat[g][0]) || !is_finite(sh.gstat[g][1]);
-    bool sel = false, bad_local = false;
-    float acc = 0.0f, mx = 0.0f;
-    for (int g = 0; g < G; ++g) {
-      const float r = sh.risk[g][lane];
-      bad_local |= !is_finite(r);
-      if (g == 0) {
-        acc = r;
-        mx = r;
-      } else {
-        acc = acc + r;
-        mx = nanmax(mx, r);
-      }
-      if (a.reduction == kAny) sel |= r > a.eps;
-    }
-    if (a.reduction == kMean) sel = (acc / (float)G) > a.eps;
-    if (a.reduction == kMax) sel = mx > a.eps;
-    sel = (sel || bad_global || bad_local || anchored) && valid;
-    if (valid) a.mask[h * N + b] = sel ? 1 : 0;
-    const uint64_t bits = __ballot(sel);
-    if (sel) {
-      const uint32_t below = __builtin_amdgcn_mbcnt_hi(
-          (uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
-      sh.list[below] = lane;
-    }
-    if (lane == 0) {
-      // access count (transformers.py:590-594): count of an expanded block,
-      // 1 for a representative; only the prompt's last block can be short
-      const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
-      const int64_t nsel = __popcll(bits);
-      int64_t count = (nvalid - nsel) + nsel * a.block;
-      if (tile == T - 1 && ((bits >> (N - 1 - tile * kTile)) & 1ull))
-        count -= a.block - (a.length - (N - 1) * a.block);
-      sh.bits = bits;
-      sh.accessed = (uint32_t)count;
-    }
+  if (lane == 0) {
+    sh.wsel[wave] = wsel;
+    sh.wbad[wave] = wbad ? 1u : 0u;
   }
   __syncthreads();
+
+  // ---- GQA reduction, fail-safes, anchors: every wave computes the same ---
+  bool sel;
+  if (a.reduction == kMean) {
+    float acc = sh.risk[0][lane];
+    bool bad_local = !is_finite(acc);
+    for (int g = 1; g < G; ++g) {
+      const float r = sh.risk[g][lane];
+      acc = acc + r;
+      bad_local |= !is_finite(r);
+    }
+    sel = (acc / (float)G) > a.eps || bad_local;
+  } else {
+    sel = (((sh.wsel[0] | sh.wsel[1]) | (sh.wsel[2] | sh.wsel[3])) >> lane) & 1ull;
+  }
+  const bool bad_global = (sh.wbad[0] | sh.wbad[1] | sh.wbad[2] | sh.wbad[3]) != 0;
+  sel = (sel || bad_global || anchored) && valid;
+  const uint64_t bits = __ballot(sel);
+  if (sel) {
+    const uint32_t below = __builtin_amdgcn_mbcnt_hi(
+        (uint32_t)(bits >> 32), __builtin_amdgcn_mbcnt_lo((uint32_t)bits, 0u));
+    sh.list[wave][below] = lane;  // this wave's copy: its LDS writes precede its reads
+  }
+  list = sh.list[wave];
+  if (wave == 0) {
+    if (valid) a.mask[h * N + b] = sel ? 1 : 0;
+    // access count (transformers.py:590-594): count of an expanded block,
+    // 1 for a representative; only the prompt's last block can be short
+    const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
+    const int64_t nsel = __popcll(bits);
+    int64_t c = (nvalid - nsel) + nsel * a.block;
+    if (tile == T - 1 && ((bits >> (N - 1 - tile * kTile)) & 1ull))
+      c -= a.block - (a.length - (N - 1) * a.block);
+    count = (uint32_t)c;
+  }
+  return bits;
 }
 
 // rkv_select's second kernel: decisions only.
 __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a,
                                                           unsigned long long* accessed) {
   __shared__ DecideShared sh;
-  decide_tile(a, blockIdx.y, blockIdx.x, sh, nullptr);
-  if (accessed && threadIdx.x == 0) atomicAdd(accessed, (unsigned long long)sh.accessed);
+  const int32_t* list;
+  uint32_t count = 0;
+  decide_tile(a, blockIdx.y, blockIdx.x, sh, nullptr, list, count);
+  if (accessed && threadIdx.x == 0) atomicAdd(accessed, (unsigned long long)count);
 }
 
 // ---------------------------------------------------------------------------
@@ -563,46 +570,14 @@ __device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st, const float 
   fold<D, GBM, kRowBatch>(st, x, v, gn);
 }
 
-// (m, l, acc) of two states -> their union (symmetric in the two).
-__device__ __forceinline__ void merge_pair(float ma, float la, float mb, float lb, float& m,
-                                           float& ea, float& eb, float& l) {
-  m = fmaxf(ma, mb);
-  ea = ma == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((ma - m) * kLog2e);
-  eb = mb == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mb - m) * kLog2e);
-  l = la * ea + lb * eb;
-}
-
-// Combines the four lane groups of this wave (xor 32 then xor 16 partners):
-// afterwards every group holds the wave's state.
+// Lane-group states are combined through LDS in chunks of rows small enough
+// that 16 groups' accumulators fit in 32 KiB.
 template <int D, int GBM>
-__device__ __forceinline__ void combine_wave(GroupState<D, GBM>& st, int gn) {
-  constexpr int CH = D / 16;
-#pragma unroll
-  for (int step = 0; step < 2; ++step) {
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      if (g >= gn) break;
-      float ma, mb, la, lb, m, ea, eb, l;
-      if (step == 0) {
-        xor32_pair(st.m[g], ma, mb);
-        xor32_pair(st.l[g], la, lb);
-      } else {
-        xor16_pair(st.m[g], ma, mb);
-        xor16_pair(st.l[g], la, lb);
-      }
-      merge_pair(ma, la, mb, lb, m, ea, eb, l);
-#pragma unroll
-      for (int i = 0; i < CH; ++i) {
-        float aa, ab;
-        if (step == 0) xor32_pair(st.acc[g][i], aa, ab);
-        else xor16_pair(st.acc[g][i], aa, ab);
-        st.acc[g][i] = aa * ea + ab * eb;
-      }
-      st.m[g] = m;
-      st.l[g] = l;
-    }
-  }
-}
+struct CombineShared {
+  static constexpr int kRows = (512 / D) < GBM ? (512 / D) : GBM;
+  float acc[16][kRows][D];
+  float ml[16][kRows][2];
+};
 
 // Two workgroups per CU (<= 256 registers per lane), so a 512-tile step runs
 // in one round on 256 CUs.
@@ -611,82 +586,87 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void attend_kernel(AttendArgs a) {
   constexpr int CH = D / 16;
   constexpr int R = kRowBatch;
+  using Comb = CombineShared<D, GBM>;
   __shared__ DecideShared dsh;
   __shared__ float zsh[kMaxGroup][kTile];
-  __shared__ float comb[kWaves][GBM][D + 2];
+  __shared__ Comb cmb;
   const DecideArgs& da = a.decide;
-  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  const int64_t h = blockIdx.y;
+  const uint32_t tile = blockIdx.x;
   const int G = da.group;
-  const int64_t N = da.n_blocks, T = da.n_tiles, B = da.block, L = da.length;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
+  const uint32_t L = (uint32_t)da.length, lb = (uint32_t)a.log2_block, B = 1u << lb;
+  const int tid = threadIdx.x;
   const int lg = tid >> 4, c = tid & 15;
 
   // This tile's slice of the suffix: tokens tile, tile + T, ... (< S).
-  int64_t S = a.suffix_cap;
+  uint32_t S = (uint32_t)a.suffix_cap;
   if (a.suffix_len_dev) {
-    const int64_t sl = *a.suffix_len_dev;
-    S = sl < 0 ? 0 : (sl > a.suffix_cap ? a.suffix_cap : sl);
+    const int32_t sl = *a.suffix_len_dev;
+    S = sl < 0 ? 0u : ((uint32_t)sl > S ? S : (uint32_t)sl);
   }
-  const int64_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0;
+  const uint32_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0u;
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
   const uint16_t* vbase = a.value_pages + h * a.vp_hs;
   const uint16_t* ks = a.key_suffix + h * a.ks_hs;
   const uint16_t* vs = a.value_suffix + h * a.vs_hs;
+  const uint32_t kts = (uint32_t)a.ks_ts, vts = (uint32_t)a.vs_ts;
 
   // ---- loads independent of the decision, in flight during it ----------
   // value means of this lane group's blocks lg, lg + 16, lg + 32, lg + 48
   RawBf16<CH> vraw[kTile / 16];
+  const uint16_t* vm = a.value_mean + (h * N) * D + c * CH;
 #pragma unroll
   for (int i = 0; i < kTile / 16; ++i) {
-    int64_t b = tile * kTile + lg + 16 * i;
+    uint32_t b = tile * kTile + lg + 16 * i;
     b = b < N ? b : N - 1;
-    vraw[i] = load_raw<CH>(a.value_mean + (h * N + b) * D + c * CH);
+    vraw[i] = load_raw<CH>(vm + b * D);
   }
   // the query rows of the first pass
   RawBf16<CH> qraw[GBM];
+  const uint16_t* qh = a.query + (h * G) * D + c * CH;
 #pragma unroll
-  for (int g = 0; g < GBM; ++g) {
-    const int gg = g < G ? g : G - 1;
-    qraw[g] = load_raw<CH>(a.query + (h * G + gg) * D + c * CH);
-  }
+  for (int g = 0; g < GBM; ++g) qraw[g] = load_raw<CH>(qh + (g < G ? g : G - 1) * D);
   // batch 0's suffix rows (rows lg + 16u)
   RawBf16<CH> ka[R], va[R], kb[R], vb[R];
 #pragma unroll
   for (int u = 0; u < R; ++u) {
-    const int64_t v = lg + 16 * u;
-    const int64_t t = v < n_suffix ? tile + v * T : 0;
-    const uint16_t* kp = v < n_suffix ? ks + t * a.ks_ts : kbase;
-    const uint16_t* vp = v < n_suffix ? vs + t * a.vs_ts : vbase;
+    const uint32_t v = lg + 16 * u;
+    const uint32_t t = v < n_suffix ? tile + v * T : 0u;
+    const uint16_t* kp = v < n_suffix ? ks + (uint64_t)t * kts : kbase;
+    const uint16_t* vp = v < n_suffix ? vs + (uint64_t)t * vts : vbase;
     ka[u] = load_raw<CH>(kp + c * CH);
     va[u] = load_raw<CH>(vp + c * CH);
   }
 
-  decide_tile(da, h, tile, dsh, zsh);
-  const uint64_t bits = dsh.bits;
-  const int64_t n_rows = n_suffix + (int64_t)__popcll(bits) * B;
-  const int32_t* list = dsh.list;
+  const int32_t* list;
+  uint32_t count = 0;
+  const uint64_t bits = decide_tile(da, h, tile, dsh, zsh, list, count);
+  const uint32_t n_rows = n_suffix + (uint32_t)__popcll(bits) * B;
+  const uint32_t last = N - 1, last_count = L - last * B;
 
   // Token row v: the suffix slice first, then the expanded blocks' tokens in
   // block order.  Points kp / vp at the row (a valid row when it is masked)
   // and returns whether it is live.
-  auto row = [&](int64_t v, const uint16_t*& kp, const uint16_t*& vp) -> bool {
+  auto row = [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) -> bool {
     kp = kbase;
     vp = vbase;
     if (v >= n_rows) return false;
     if (v < n_suffix) {
-      const int64_t t = tile + v * T;
-      kp = ks + t * a.ks_ts;
-      vp = vs + t * a.vs_ts;
+      const uint32_t t = tile + v * T;
+      kp = ks + (uint64_t)t * kts;
+      vp = vs + (uint64_t)t * vts;
       return true;
     }
-    const int64_t w = v - n_suffix;
-    const int64_t j = w >> a.log2_block, t = w & (B - 1);
-    const int64_t bb = tile * kTile + list[j];
-    kp = kbase + ((bb << a.log2_block) + t) * D;
-    vp = vbase + ((bb << a.log2_block) + t) * D;
-    return t < block_count(bb, N, B, L);
+    const uint32_t w = v - n_suffix;
+    const uint32_t t = w & (B - 1);
+    const uint32_t bb = tile * kTile + (uint32_t)list[w >> lb];
+    const uint32_t off = ((bb << lb) + t) * (uint32_t)D;
+    kp = kbase + off;
+    vp = vbase + off;
+    return bb != last || t < last_count;
   };
-  auto issue = [&](int64_t batch, RawBf16<CH> (&kr)[R], RawBf16<CH> (&vr)[R]) {
+  auto issue = [&](uint32_t batch, RawBf16<CH> (&kr)[R], RawBf16<CH> (&vr)[R]) {
     uint32_t ok = 0;
 #pragma unroll
     for (int u = 0; u < R; ++u) {
@@ -705,7 +685,7 @@ void attend_kernel(AttendArgs a) {
       // batch 0: the suffix rows are in flight already; add its page rows
 #pragma unroll
       for (int u = 0; u < R; ++u) {
-        const int64_t v = lg + 16 * u;
+        const uint32_t v = lg + 16 * u;
         if (v < n_suffix) {
           oka |= 1u << u;
         } else if (v < n_rows) {
@@ -717,10 +697,8 @@ void attend_kernel(AttendArgs a) {
       }
     } else {
 #pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        const int gg = g0 + g < G ? g0 + g : G - 1;
-        qraw[g] = load_raw<CH>(a.query + (h * G + gg) * D + c * CH);
-      }
+      for (int g = 0; g < GBM; ++g)
+        qraw[g] = load_raw<CH>(qh + (g0 + g < G ? g0 + g : G - 1) * D);
       oka = issue(0, ka, va);
     }
     if (16 * R < n_rows) okb = issue(1, kb, vb);
@@ -756,7 +734,7 @@ void attend_kernel(AttendArgs a) {
     }
     // token rows, two batches in flight
 #pragma unroll 1
-    for (int64_t k = 0; k * 16 * R < n_rows; k += 2) {
+    for (uint32_t k = 0; k * 16 * R < n_rows; k += 2) {
       fold_tokens<D, GBM>(st, q, ka, va, oka, a.scale, gn);
       if ((k + 2) * 16 * R < n_rows) oka = issue(k + 2, ka, va);
       if ((k + 1) * 16 * R >= n_rows) break;
@@ -764,44 +742,50 @@ void attend_kernel(AttendArgs a) {
       if ((k + 3) * 16 * R < n_rows) okb = issue(k + 3, kb, vb);
     }
 
-    // the 16 lane groups -> one partial per query row
-    combine_wave<D, GBM>(st, gn);
-    if (lane < 16) {
+    // the 16 lane groups -> one partial per query row, through LDS (fully
+    // unrolled: the state arrays are indexed by constants only)
 #pragma unroll
-      for (int g = 0; g < GBM; ++g) {
-        if (g >= gn) break;
+    for (int gc = 0; gc < GBM; gc += Comb::kRows) {
+      if (gc > 0) __syncthreads();  // the previous chunk's reads are done
 #pragma unroll
-        for (int i = 0; i < CH; ++i) comb[wave][g][c * CH + i] = st.acc[g][i];
-        if (c == 0) {
-          comb[wave][g][D] = st.m[g];
-          comb[wave][g][D + 1] = st.l[g];
+      for (int j = 0; j < Comb::kRows; ++j) {
+        if (gc + j < gn) {
+#pragma unroll
+          for (int i = 0; i < CH; ++i) cmb.acc[lg][j][c * CH + i] = st.acc[gc + j][i];
+          if (c == 0) {
+            cmb.ml[lg][j][0] = st.m[gc + j];
+            cmb.ml[lg][j][1] = st.l[gc + j];
+          }
+        }
+      }
+      __syncthreads();
+      const int rows = gn - gc < Comb::kRows ? gn - gc : Comb::kRows;
+      for (int idx = 2 * tid; idx < rows * D; idx += 2 * kThreads) {
+        const int j = idx / D, d = idx % D;
+        float M = kNegInf;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) M = fmaxf(M, cmb.ml[w][j][0]);
+        float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+#pragma unroll
+        for (int w = 0; w < 16; ++w) {
+          const float mw = cmb.ml[w][j][0];
+          const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
+          const float2 av = *reinterpret_cast<const float2*>(&cmb.acc[w][j][d]);
+          a0 = __builtin_fmaf(av.x, e, a0);
+          a1 = __builtin_fmaf(av.y, e, a1);
+          l = __builtin_fmaf(cmb.ml[w][j][1], e, l);
+        }
+        const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + tile;
+        *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
+        if (d == 0) {
+          a.part_m[at] = M;
+          a.part_l[at] = l;
         }
       }
     }
-    __syncthreads();
-    for (int idx = tid; idx < gn * D; idx += kThreads) {
-      const int g = idx / D, d = idx % D;
-      float M = kNegInf;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, comb[w][g][D]);
-      float acc = 0.0f, l = 0.0f;
-#pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float mw = comb[w][g][D];
-        const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
-        acc = __builtin_fmaf(comb[w][g][d], e, acc);
-        l = __builtin_fmaf(comb[w][g][D + 1], e, l);
-      }
-      const int64_t at = (h * G + g0 + g) * da.tile_stride + tile;
-      a.part_acc[at * D + d] = acc;
-      if (d == 0) {
-        a.part_m[at] = M;
-        a.part_l[at] = l;
-      }
-    }
-    __syncthreads();  // comb is reused by the next pass
+    __syncthreads();  // cmb is reused by the next pass
   }
-  if (a.tile_counts && tid == 0) a.tile_counts[h * da.tile_stride + tile] = dsh.accessed;
+  if (a.tile_counts && tid == 0) a.tile_counts[h * da.tile_stride + tile] = count;
 }
 
 // ---------------------------------------------------------------------------
@@ -1171,6 +1155,9 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
   if (rc) return rc;
   if (!key_pages || !value_pages || !output)
     return set_error(kInvalidArgument, "rkv_decode: null pointer argument");
+  // the attention kernel addresses a head's pages with 32-bit element offsets
+  if (n_blocks * block_size * dim >= (int64_t(1) << 31))
+    return set_error(kUnsupported, "rkv_decode: more than 2^31 page elements per head");
   if (suffix_capacity < 0)
     return set_error(kInvalidArgument, "rkv_decode: negative suffix capacity");
   if (suffix_capacity > 0 && (!key_suffix || !value_suffix))
