@@ -236,8 +236,22 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   const int c = tid % S::kLanes, sub = tid / S::kLanes;
   const bool own_q = G * D <= kOwnQ;
 
-  // Every load of the tile first.  Blocks past the end read block N-1 (their
-  // results are discarded).
+  constexpr int QW = CH + kQPad;          // padded slice
+  constexpr int QS = S::kLanes * QW;      // padded row
+  float* qs = pdot + G * kTile + (own_q ? wave * 2 * G * QS : 0);  // [G][QS] bf16(q)
+  float* q2s = qs + G * QS;                                         // [G][QS] bf16(q^2)
+  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
+  const int first = own_q ? lane : tid, step = own_q ? kWave : kThreads;
+  // The query words first (the staging below waits only for them: loads
+  // complete in order), then every load of the tile.  Blocks past the end
+  // read block N-1 (their results are discarded).
+  constexpr int kQWords = kOwnQ / 2 / kWave;  // words per lane of a wave's own copy
+  uint32_t qw[kQWords];
+#pragma unroll
+  for (int k = 0; k < kQWords; ++k) {
+    const int i = first + k * step;
+    qw[k] = q32[i < G * D / 2 ? i : 0];
+  }
   RawBf16<CH> kraw[S::kPasses], eraw[S::kPasses];
 #pragma unroll
   for (int ps = 0; ps < S::kPasses; ++ps) {
@@ -247,14 +261,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     kraw[ps] = load_raw<CH>(a.key_mean + o);
     eraw[ps] = load_raw<CH>(a.ellipsoid + o);
   }
-  constexpr int QW = CH + kQPad;          // padded slice
-  constexpr int QS = S::kLanes * QW;      // padded row
-  float* qs = pdot + G * kTile + (own_q ? wave * 2 * G * QS : 0);  // [G][QS] bf16(q)
-  float* q2s = qs + G * QS;                                         // [G][QS] bf16(q^2)
-  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
-  const int first = own_q ? lane : tid, step = own_q ? kWave : kThreads;
-  for (int i = first; i < G * D / 2; i += step) {
-    const uint32_t u = q32[i];
+  auto stage = [&](int i, uint32_t u) {
     const float q0 = bits_f32(u << 16), q1 = bits_f32(u & 0xFFFF0000u);
     const int g = 2 * i / D, e = 2 * i % D;  // element pair e, e + 1 of row g
     const int at = g * QS + (e / CH) * QW + e % CH;
@@ -262,7 +269,13 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     qs[at + 1] = q1;
     q2s[at] = round_bf16(q0 * q0);
     q2s[at + 1] = round_bf16(q1 * q1);
+  };
+#pragma unroll
+  for (int k = 0; k < kQWords; ++k) {
+    const int i = first + k * step;
+    if (i < G * D / 2) stage(i, qw[k]);
   }
+  for (int i = first + kQWords * step; i < G * D / 2; i += step) stage(i, q32[i]);
   // A wave's LDS operations complete in order, so its own copy is ready for
   // its own reads; the shared copy needs the workgroup.
   if (!own_q) __syncthreads();
@@ -379,41 +392,72 @@ __device__ __forceinline__ float merge_lse(float m0, float l0, const float* part
 }
 
 // Decides tile `tile` of head h (select_blocks_reference plus the anchor
-// union): stores the mask (and risk / stats when asked) and returns the
-// tile's expanded-block ballot, uniform over the workgroup; list (this
-// wave's copy in sh) holds the expanded blocks in ascending order.  zsh, when
-// not null, receives z of every (row, block) of the tile (-inf past the end).
-// count (thread 0) receives the tile's access count.  One barrier.
+// union), from the loads decide_issue made: stores the mask (and risk /
+// stats when asked) and returns the tile's expanded-block ballot, uniform
+// over the workgroup; list (this wave's copy in sh) holds the expanded blocks
+// in ascending order.  zsh, when not null, receives z of every (row, block)
+// of the tile (-inf past the end).  count (thread 0) receives the tile's
+// access count.  One barrier.  The next row's loads are issued before this
+// row's arithmetic.
 //
 // After the fail-safes the max reduction selects exactly the blocks "any"
 // selects: a NaN risk makes the max NaN (not > eps) but is non-finite, which
 // selects the block anyway.  So both are the OR over rows of
 // (risk > eps or risk not finite); mean sums the rows in order.
-__device__ __forceinline__ uint64_t decide_tile(const DecideArgs& a, int64_t h, int64_t tile,
-                                                DecideShared& sh, float (*zsh)[kTile],
-                                                const int32_t*& list, uint32_t& count) {
+// The decision's inputs for this thread (block lane of the tile, this wave's
+// first row), loaded before anything else is computed.  Every load is
+// unconditional (clamped addresses and rows, a stand-in anchor pointer;
+// results are selected only after all are issued), so no load waits for
+// another at a branch join.
+struct DecideLoads {
+  float vnorm;
+  uint8_t anc;
+  float4 part, zf;
+};
+
+__device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t h,
+                                                    int64_t tile) {
+  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int G = a.group;
+  const int64_t N = a.n_blocks, T = a.n_tiles;
+  const int64_t b = tile * kTile + lane;
+  const int64_t bc = b < N ? b : N - 1;
+  const int tl = lane < T ? lane : 0;
+  const int gl = wave < G ? wave : G - 1;
+  const uint8_t* anc = a.anchor ? a.anchor : a.mask;
+  DecideLoads d;
+  d.vnorm = a.value_norm[h * N + bc];
+  d.anc = anc[h * N + bc];
+  d.part = *reinterpret_cast<const float4*>(a.lse + ((h * G + gl) * a.tile_stride + tl) * 4);
+  d.zf = a.zf[(h * G + gl) * a.z_stride + bc];
+  return d;
+}
+
+__device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
+                                                  const DecideLoads& in, DecideShared& sh,
+                                                  float (*zsh)[kTile], const int32_t*& list,
+                                                  uint32_t& count) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
   const int64_t b = tile * kTile + lane;
   const bool valid = b < N;
-  const float vnorm = valid ? a.value_norm[h * N + b] : 0.0f;
-  const bool anchored = valid && a.anchor && a.anchor[h * N + b] != 0;
+  const bool owner = blockIdx.z == 0;  // row passes beyond the first repeat the decision
+  const int64_t bc = valid ? b : N - 1;
+  const int tl = lane < T ? lane : 0;
   const float vmax = a.max_value_norm[h];
+  const float vnorm = valid ? in.vnorm : 0.0f;
+  const bool anchored = valid && a.anchor != nullptr && in.anc != 0;
 
   // ---- log Z, log C of each row this wave owns, then its risks ----------
   uint64_t wsel = 0;
   bool wbad = false;
-#pragma unroll 1
-  for (int g = wave; g < G; g += kWaves) {
+  auto row_stats = [&](int g, float4 part, float4 zf) {
     const float* prow = a.lse + (h * G + g) * a.tile_stride * 4;
-    float4 part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
-    if (lane < T) part = *reinterpret_cast<const float4*>(prow + lane * 4);
-    float4 zf = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    if (valid) zf = a.zf[(h * G + g) * a.z_stride + b];
+    if (lane >= T) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
     const float lz = merge_lse(part.x, part.y, prow, 0, T, lane);
     const float lc = merge_lse(part.z, part.w, prow, 1, T, lane);
-    if (a.stats_out && tile == 0 && lane == 0) {
+    if (a.stats_out && owner && tile == 0 && lane == 0) {
       a.stats_out[(h * G + g) * 2] = lz;
       a.stats_out[(h * G + g) * 2 + 1] = lc;
     }
@@ -421,11 +465,20 @@ __device__ __forceinline__ uint64_t decide_tile(const DecideArgs& a, int64_t h, 
     float r = 0.0f;
     if (valid) {
       r = risk_from(zf.x, zf.y, zf.z, zf.w, lz, lc, vmax, vnorm);
-      if (a.risk_out) a.risk_out[(h * G + g) * N + b] = r;
+      if (a.risk_out && owner) a.risk_out[(h * G + g) * N + b] = r;
     }
     wsel |= __ballot(valid && (r > a.eps || !is_finite(r)));
     sh.risk[g][lane] = r;
     if (zsh) zsh[g][lane] = valid ? zf.x : kNegInf;
+  };
+  // the first row from the loads already made, further rows (groups above
+  // four) with their own loads
+  if (wave < G) row_stats(wave, in.part, in.zf);
+#pragma unroll 1
+  for (int g = wave + kWaves; g < G; g += kWaves) {
+    const float4 part =
+        *reinterpret_cast<const float4*>(a.lse + ((h * G + g) * a.tile_stride + tl) * 4);
+    row_stats(g, part, a.zf[(h * G + g) * a.z_stride + bc]);
   }
   if (lane == 0) {
     sh.wsel[wave] = wsel;
@@ -457,7 +510,7 @@ __device__ __forceinline__ uint64_t decide_tile(const DecideArgs& a, int64_t h, 
   }
   list = sh.list[wave];
   if (wave == 0) {
-    if (valid) a.mask[h * N + b] = sel ? 1 : 0;
+    if (valid && owner) a.mask[h * N + b] = sel ? 1 : 0;
     // access count (transformers.py:590-594): count of an expanded block,
     // 1 for a representative; only the prompt's last block can be short
     const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
@@ -476,7 +529,8 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a,
   __shared__ DecideShared sh;
   const int32_t* list;
   uint32_t count = 0;
-  decide_tile(a, blockIdx.y, blockIdx.x, sh, nullptr, list, count);
+  const DecideLoads in = decide_issue(a, blockIdx.y, blockIdx.x);
+  decide_finish(a, blockIdx.y, blockIdx.x, in, sh, nullptr, list, count);
   if (accessed && threadIdx.x == 0) atomicAdd(accessed, (unsigned long long)count);
 }
 
@@ -498,7 +552,6 @@ struct AttendArgs {
   uint32_t* tile_counts;        // (H, tile_stride) or null
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
   int64_t suffix_cap;
-  int row_passes;
   int log2_block;  // block_size is 16, 32 or 64
   float scale;
 };
@@ -571,24 +624,35 @@ __device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st, const float 
 }
 
 // Lane-group states are combined through LDS in chunks of rows small enough
-// that 16 groups' accumulators fit in 32 KiB.
+// that 16 groups' accumulators fit in 32 KiB.  A lane's D/16 columns sit in
+// a slice padded by 4 floats, so the 16-byte stores of a group's lanes fall
+// on distinct banks.
 template <int D, int GBM>
 struct CombineShared {
   static constexpr int kRows = (512 / D) < GBM ? (512 / D) : GBM;
-  float acc[16][kRows][D];
+  static constexpr int kSlice = D / 16 + 4;
+  float acc[16][kRows][16 * kSlice];
   float ml[16][kRows][2];
 };
 
 // Two workgroups per CU (<= 256 registers per lane), so a 512-tile step runs
 // in one round on 256 CUs.
+//
+// Order of work: every load that does not depend on the decision is issued
+// first (the decision's inputs, the value means, z and the tile max of this
+// lane group's representatives, one suffix row per lane group); the full
+// representative sum over the tile is folded while the decision's inputs
+// are in flight; after the decision the
+// expanded blocks' representative terms are taken out again and the
+// expanded blocks' tokens and the suffix rows are attended.
 template <int D, int GBM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void attend_kernel(AttendArgs a) {
   constexpr int CH = D / 16;
   constexpr int R = kRowBatch;
+  constexpr int NB = kTile / 16;  // representatives per lane group
   using Comb = CombineShared<D, GBM>;
   __shared__ DecideShared dsh;
-  __shared__ float zsh[kMaxGroup][kTile];
   __shared__ Comb cmb;
   const DecideArgs& da = a.decide;
   const int64_t h = blockIdx.y;
@@ -598,67 +662,141 @@ void attend_kernel(AttendArgs a) {
   const uint32_t L = (uint32_t)da.length, lb = (uint32_t)a.log2_block, B = 1u << lb;
   const int tid = threadIdx.x;
   const int lg = tid >> 4, c = tid & 15;
+  const int g0 = blockIdx.z * GBM, gn = min(GBM, G - g0);  // this pass's query rows
 
-  // This tile's slice of the suffix: tokens tile, tile + T, ... (< S).
+  // ---- loads independent of the decision ---------------------------------
+  const DecideLoads din = decide_issue(da, h, tile);
+  // The suffix length does not change during a launch: a scalar load from
+  // the constant address space, outside the vector loads' in-order count.
   uint32_t S = (uint32_t)a.suffix_cap;
   if (a.suffix_len_dev) {
-    const int32_t sl = *a.suffix_len_dev;
+    typedef __attribute__((address_space(4))) const int32_t ConstI32;
+    const int32_t sl = *(ConstI32*)(uintptr_t)a.suffix_len_dev;
     S = sl < 0 ? 0u : ((uint32_t)sl > S ? S : (uint32_t)sl);
   }
+  // value means, z and row maxima of this lane group's blocks lg + 16 i
+  RawBf16<CH> vraw[NB];
+  float zr[GBM][NB], mt[GBM];
+  const uint16_t* vm = a.value_mean + (h * N) * D + c * CH;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    uint32_t b = tile * kTile + lg + 16 * i;
+    b = b < N ? b : N - 1;
+    vraw[i] = load_raw<CH>(vm + b * D);
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      const int gg = g0 + g < G ? g0 + g : G - 1;
+      zr[g][i] = da.zf[(h * G + gg) * da.z_stride + b].x;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) {
+    const int gg = g0 + g < G ? g0 + g : G - 1;
+    mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
+  }
+  RawBf16<CH> qraw[GBM];
+  const uint16_t* qh = a.query + (h * G) * D + c * CH;
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) qraw[g] = load_raw<CH>(qh + (g0 + g < G ? g0 + g : G - 1) * D);
+  // This tile's slice of the suffix: tokens tile, tile + T, ... (< S); the
+  // first 16 of them, one per lane group, are prefetched here.
   const uint32_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0u;
+  const uint32_t n_pre = n_suffix < 16u ? n_suffix : 16u;
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
   const uint16_t* vbase = a.value_pages + h * a.vp_hs;
   const uint16_t* ks = a.key_suffix + h * a.ks_hs;
   const uint16_t* vs = a.value_suffix + h * a.vs_hs;
   const uint32_t kts = (uint32_t)a.ks_ts, vts = (uint32_t)a.vs_ts;
-
-  // ---- loads independent of the decision, in flight during it ----------
-  // value means of this lane group's blocks lg, lg + 16, lg + 32, lg + 48
-  RawBf16<CH> vraw[kTile / 16];
-  const uint16_t* vm = a.value_mean + (h * N) * D + c * CH;
-#pragma unroll
-  for (int i = 0; i < kTile / 16; ++i) {
-    uint32_t b = tile * kTile + lg + 16 * i;
-    b = b < N ? b : N - 1;
-    vraw[i] = load_raw<CH>(vm + b * D);
-  }
-  // the query rows of the first pass
-  RawBf16<CH> qraw[GBM];
-  const uint16_t* qh = a.query + (h * G) * D + c * CH;
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) qraw[g] = load_raw<CH>(qh + (g < G ? g : G - 1) * D);
-  // batch 0's suffix rows (rows lg + 16u)
-  RawBf16<CH> ka[R], va[R], kb[R], vb[R];
-#pragma unroll
-  for (int u = 0; u < R; ++u) {
-    const uint32_t v = lg + 16 * u;
-    const uint32_t t = v < n_suffix ? tile + v * T : 0u;
-    const uint16_t* kp = v < n_suffix ? ks + (uint64_t)t * kts : kbase;
-    const uint16_t* vp = v < n_suffix ? vs + (uint64_t)t * vts : vbase;
-    ka[u] = load_raw<CH>(kp + c * CH);
-    va[u] = load_raw<CH>(vp + c * CH);
+  RawBf16<CH> ksr[1], vsr[1];
+  {
+    const bool has = (uint32_t)lg < n_pre;
+    const uint64_t t = has ? tile + (uint32_t)lg * T : 0u;
+    ksr[0] = load_raw<CH>((has ? ks + t * kts : kbase) + c * CH);
+    vsr[0] = load_raw<CH>((has ? vs + t * vts : vbase) + c * CH);
   }
 
+  float q[GBM][CH];
+#pragma unroll
+  for (int g = 0; g < GBM; ++g) unpack(qraw[g], q[g]);
+
+  // ---- every representative of this lane group, expanded or not ----------
+  GroupState<D, GBM> st;
+  float pw[GBM][NB];
+  {
+    float v[NB][CH];
+#pragma unroll
+    for (int i = 0; i < NB; ++i) unpack(vraw[i], v[i]);
+#pragma unroll
+    for (int g = 0; g < GBM; ++g) {
+      const float m = inf_to_zero(mt[g]);
+      st.m[g] = m;
+      st.l[g] = 0.0f;
+#pragma unroll
+      for (int e = 0; e < CH; ++e) st.acc[g][e] = 0.0f;
+#pragma unroll
+      for (int i = 0; i < NB; ++i) {
+        const bool valid = tile * kTile + lg + 16 * i < N;
+        pw[g][i] = valid ? __builtin_amdgcn_exp2f((zr[g][i] - m) * kLog2e) : 0.0f;
+        st.l[g] = st.l[g] + pw[g][i];
+#pragma unroll
+        for (int e = 0; e < CH; ++e) st.acc[g][e] = __builtin_fmaf(pw[g][i], v[i][e], st.acc[g][e]);
+      }
+    }
+  }
+  // ---- the decision -------------------------------------------------------
   const int32_t* list;
   uint32_t count = 0;
-  const uint64_t bits = decide_tile(da, h, tile, dsh, zsh, list, count);
-  const uint32_t n_rows = n_suffix + (uint32_t)__popcll(bits) * B;
-  const uint32_t last = N - 1, last_count = L - last * B;
+  const uint64_t bits = decide_finish(da, h, tile, din, dsh, nullptr, list, count);
 
-  // Token row v: the suffix slice first, then the expanded blocks' tokens in
-  // block order.  Points kp / vp at the row (a valid row when it is masked)
-  // and returns whether it is live.
+  // take the expanded blocks' representatives out again
+  if ((bits >> lg) & 0x0001000100010001ull) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      if ((bits >> (lg + 16 * i)) & 1ull) {
+        float v[CH];
+        unpack(vraw[i], v);
+#pragma unroll
+        for (int g = 0; g < GBM; ++g) {
+          st.l[g] = st.l[g] - pw[g][i];
+#pragma unroll
+          for (int e = 0; e < CH; ++e) st.acc[g][e] = __builtin_fmaf(-pw[g][i], v[e], st.acc[g][e]);
+        }
+      }
+    }
+  }
+
+  // ---- the prefetched suffix rows (after the subtraction, which assumes
+  // the representatives' scale) ---------------------------------------------
+  {
+    RawBf16<CH> kr[R], vr[R];
+    kr[0] = ksr[0];
+    vr[0] = vsr[0];
+#pragma unroll
+    for (int u = 1; u < R; ++u) {
+      kr[u] = ksr[0];
+      vr[u] = vsr[0];
+    }
+    fold_tokens<D, GBM>(st, q, kr, vr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
+  }
+
+  // ---- token rows after the prefetched ones ------------------------------
+  // Row v: the rest of the suffix slice first, then the expanded blocks'
+  // tokens in block order.  Points kp / vp at the row (a valid row when it
+  // is masked) and returns whether it is live.
+  const uint32_t n_rest = n_suffix - n_pre;
+  const uint32_t n_rows = n_rest + (uint32_t)__popcll(bits) * B;
+  const uint32_t last = N - 1, last_count = L - last * B;
   auto row = [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) -> bool {
     kp = kbase;
     vp = vbase;
     if (v >= n_rows) return false;
-    if (v < n_suffix) {
-      const uint32_t t = tile + v * T;
-      kp = ks + (uint64_t)t * kts;
-      vp = vs + (uint64_t)t * vts;
+    if (v < n_rest) {
+      const uint64_t t = tile + (n_pre + v) * T;
+      kp = ks + t * kts;
+      vp = vs + t * vts;
       return true;
     }
-    const uint32_t w = v - n_suffix;
+    const uint32_t w = v - n_rest;
     const uint32_t t = w & (B - 1);
     const uint32_t bb = tile * kTile + (uint32_t)list[w >> lb];
     const uint32_t off = ((bb << lb) + t) * (uint32_t)D;
@@ -677,115 +815,64 @@ void attend_kernel(AttendArgs a) {
     }
     return ok;
   };
-
-  for (int rp = 0; rp < a.row_passes; ++rp) {
-    const int g0 = rp * GBM, gn = min(GBM, G - g0);
-    uint32_t oka = 0, okb = 0;
-    if (rp == 0) {
-      // batch 0: the suffix rows are in flight already; add its page rows
-#pragma unroll
-      for (int u = 0; u < R; ++u) {
-        const uint32_t v = lg + 16 * u;
-        if (v < n_suffix) {
-          oka |= 1u << u;
-        } else if (v < n_rows) {
-          const uint16_t *kp, *vp;
-          if (row(v, kp, vp)) oka |= 1u << u;
-          ka[u] = load_raw<CH>(kp + c * CH);
-          va[u] = load_raw<CH>(vp + c * CH);
-        }
-      }
-    } else {
-#pragma unroll
-      for (int g = 0; g < GBM; ++g)
-        qraw[g] = load_raw<CH>(qh + (g0 + g < G ? g0 + g : G - 1) * D);
-      oka = issue(0, ka, va);
-    }
-    if (16 * R < n_rows) okb = issue(1, kb, vb);
-    float q[GBM][CH];
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) unpack(qraw[g], q[g]);
-
-    GroupState<D, GBM> st;
-#pragma unroll
-    for (int g = 0; g < GBM; ++g) {
-      st.m[g] = kNegInf;
-      st.l[g] = 0.0f;
-#pragma unroll
-      for (int i = 0; i < CH; ++i) st.acc[g][i] = 0.0f;
-    }
-    // representatives: this lane group's unexpanded blocks, logit z
-    {
-      float x[GBM][kTile / 16], v[kTile / 16][CH];
-#pragma unroll
-      for (int i = 0; i < kTile / 16; ++i) {
-        const int bl = lg + 16 * i;
-        const bool rep = !((bits >> bl) & 1ull) && tile * kTile + bl < N;
-        unpack(vraw[i], v[i]);
-#pragma unroll
-        for (int e = 0; e < CH; ++e) v[i][e] = rep ? v[i][e] : 0.0f;
-#pragma unroll
-        for (int g = 0; g < GBM; ++g) {
-          const int gg = g0 + g < G ? g0 + g : G - 1;
-          x[g][i] = rep ? zsh[gg][bl] : kNegInf;
-        }
-      }
-      fold<D, GBM, kTile / 16>(st, x, v, gn);
-    }
-    // token rows, two batches in flight
+  if (n_rows > 0) {
+    RawBf16<CH> ka[R], va[R], kb[R], vb[R];
+    uint32_t oka = issue(0, ka, va);
+    uint32_t okb = issue(1, kb, vb);
 #pragma unroll 1
     for (uint32_t k = 0; k * 16 * R < n_rows; k += 2) {
       fold_tokens<D, GBM>(st, q, ka, va, oka, a.scale, gn);
-      if ((k + 2) * 16 * R < n_rows) oka = issue(k + 2, ka, va);
+      oka = issue(k + 2, ka, va);
       if ((k + 1) * 16 * R >= n_rows) break;
       fold_tokens<D, GBM>(st, q, kb, vb, okb, a.scale, gn);
-      if ((k + 3) * 16 * R < n_rows) okb = issue(k + 3, kb, vb);
+      okb = issue(k + 3, kb, vb);
     }
-
-    // the 16 lane groups -> one partial per query row, through LDS (fully
-    // unrolled: the state arrays are indexed by constants only)
-#pragma unroll
-    for (int gc = 0; gc < GBM; gc += Comb::kRows) {
-      if (gc > 0) __syncthreads();  // the previous chunk's reads are done
-#pragma unroll
-      for (int j = 0; j < Comb::kRows; ++j) {
-        if (gc + j < gn) {
-#pragma unroll
-          for (int i = 0; i < CH; ++i) cmb.acc[lg][j][c * CH + i] = st.acc[gc + j][i];
-          if (c == 0) {
-            cmb.ml[lg][j][0] = st.m[gc + j];
-            cmb.ml[lg][j][1] = st.l[gc + j];
-          }
-        }
-      }
-      __syncthreads();
-      const int rows = gn - gc < Comb::kRows ? gn - gc : Comb::kRows;
-      for (int idx = 2 * tid; idx < rows * D; idx += 2 * kThreads) {
-        const int j = idx / D, d = idx % D;
-        float M = kNegInf;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) M = fmaxf(M, cmb.ml[w][j][0]);
-        float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
-#pragma unroll
-        for (int w = 0; w < 16; ++w) {
-          const float mw = cmb.ml[w][j][0];
-          const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
-          const float2 av = *reinterpret_cast<const float2*>(&cmb.acc[w][j][d]);
-          a0 = __builtin_fmaf(av.x, e, a0);
-          a1 = __builtin_fmaf(av.y, e, a1);
-          l = __builtin_fmaf(cmb.ml[w][j][1], e, l);
-        }
-        const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + tile;
-        *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
-        if (d == 0) {
-          a.part_m[at] = M;
-          a.part_l[at] = l;
-        }
-      }
-    }
-    __syncthreads();  // cmb is reused by the next pass
   }
-  if (a.tile_counts && tid == 0) a.tile_counts[h * da.tile_stride + tile] = count;
+
+  // ---- the 16 lane groups -> one partial per query row, through LDS ------
+  // (fully unrolled: the state arrays are indexed by constants only)
+#pragma unroll
+  for (int gc = 0; gc < GBM; gc += Comb::kRows) {
+    if (gc > 0) __syncthreads();  // the previous chunk's reads are done
+#pragma unroll
+    for (int j = 0; j < Comb::kRows; ++j) {
+      if (gc + j < gn) {
+#pragma unroll
+        for (int i = 0; i < CH; ++i) cmb.acc[lg][j][c * Comb::kSlice + i] = st.acc[gc + j][i];
+        if (c == 0) {
+          cmb.ml[lg][j][0] = st.m[gc + j];
+          cmb.ml[lg][j][1] = st.l[gc + j];
+        }
+      }
+    }
+    __syncthreads();
+    const int rows = gn - gc < Comb::kRows ? gn - gc : Comb::kRows;
+    for (int idx = 2 * tid; idx < rows * D; idx += 2 * kThreads) {
+      const int j = idx / D, d = idx % D;
+      const int at_d = (d / CH) * Comb::kSlice + d % CH;  // CH is even: d, d+1 in one slice
+      float M = kNegInf;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) M = fmaxf(M, cmb.ml[w][j][0]);
+      float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+#pragma unroll
+      for (int w = 0; w < 16; ++w) {
+        const float mw = cmb.ml[w][j][0];
+        const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
+        const float2 av = *reinterpret_cast<const float2*>(&cmb.acc[w][j][at_d]);
+        a0 = __builtin_fmaf(av.x, e, a0);
+        a1 = __builtin_fmaf(av.y, e, a1);
+        l = __builtin_fmaf(cmb.ml[w][j][1], e, l);
+      }
+      const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + tile;
+      *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
+      if (d == 0) {
+        a.part_m[at] = M;
+        a.part_l[at] = l;
+      }
+    }
+  }
+  if (a.tile_counts && tid == 0 && blockIdx.z == 0)
+    a.tile_counts[h * da.tile_stride + tile] = count;
 }
 
 // ---------------------------------------------------------------------------
@@ -841,8 +928,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
       const int i = i0 + u * kMergeK;
       const int ii = i < P ? i : 0;
       mv[u] = pm[ii];
-      lv[u] = i < P ? pl[ii] : 0.0f;
+      lv[u] = pl[ii];
       av[u] = pa[(int64_t)ii * D];
+      if (i >= P) lv[u] = 0.0f;
     }
 #pragma unroll
     for (int u = 0; u < kMergeBatch; ++u) merge_one(mv[u], lv[u], av[u], mx, num, den);
@@ -1021,8 +1109,6 @@ AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffe
   aa.vs_hs = b.vs_hs;
   aa.vs_ts = b.vs_ts;
   aa.suffix_cap = b.suffix_cap;
-  const int64_t rows = rows_per_pass(p.group, p.dim);
-  aa.row_passes = (int)((p.group + rows - 1) / rows);
   aa.log2_block = p.block == 16 ? 4 : (p.block == 32 ? 5 : 6);
   aa.scale = (float)pow((double)p.dim, -0.5);
   return aa;
@@ -1071,13 +1157,13 @@ int launch_attend(const AttendArgs& aa, int64_t rows, dim3 grid, hipStream_t str
 int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const AttendArgs aa = attend_args(p, L, b);
   const MergeArgs ma = merge_args(p, L, b);
-  const dim3 tiles((unsigned)L.n_tiles, (unsigned)p.heads);
+  const int64_t rows = rows_per_pass(p.group, p.dim);
+  const dim3 tiles((unsigned)L.n_tiles, (unsigned)p.heads, (unsigned)((p.group + rows - 1) / rows));
   mark(0, p.stream);
   int rc = launch_score(p, L);
   if (rc) return rc;
   mark(1, p.stream);
   rc = kUnsupported;
-  const int64_t rows = rows_per_pass(p.group, p.dim);
   RKV_DISPATCH_DIM(p.dim, D, rc = launch_attend<D>(aa, rows, tiles, p.stream));
   if (rc) return rc;
   mark(2, p.stream);
