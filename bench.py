@@ -32,8 +32,8 @@ import torch  # noqa: E402
 
 METRIC = "decode attn µs/step/layer @128K ctx GQA32/8 d128; HBM GB/s vs peak"
 PEAK_HBM_GBPS = 8000.0
-# Kernels one rkv_decode call launches, in order.
-KERNELS = ("score", "attend", "merge")
+# Kernels one rkv_decode call launches, in order, per decode path.
+KERNELS = {"step": ("step",), "split": ("score", "attend", "merge")}
 
 
 def log(msg):
@@ -61,6 +61,8 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 64 MiB buffer 5 times (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings to bytes)")
+    ap.add_argument("--path", choices=("step", "split"), default="step",
+                    help="rkv_decode path: one launch per step (default) or three kernels")
     ap.add_argument("--graph-only", action="store_true",
                     help="only the graph-replay timing (for profiler runs)")
     return ap.parse_args()
@@ -124,7 +126,7 @@ def algorithmic_bytes(a, masks, counts, suffix):
     ellipsoids of every block; attend reads the value means of unexpanded
     blocks (the representatives), the value norms, the K/V tokens of expanded
     blocks and of the suffix, and writes the mask; merge writes the output.
-    "decode" is their sum.  Intermediates (z, delta, partials) are not
+    "step" (the one-launch kernel) and "decode" are their sum.  Intermediates (z, delta, partials) are not
     algorithmic bytes."""
     H, G, D = a.heads, a.group, a.dim
     n = counts.numel()
@@ -137,7 +139,8 @@ def algorithmic_bytes(a, masks, counts, suffix):
               + H * suffix * D * 2 * 2 + q_bytes)
     merge = H * G * D * 2
     phases = dict(score=score, attend=attend, merge=merge)
-    return dict(phases, decode=sum(phases.values()))
+    total = sum(phases.values())
+    return dict(phases, step=total, decode=total)
 
 
 def main():
@@ -156,7 +159,8 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = _hip.lib()
-    kernels = KERNELS
+    _hip.set_decode_path(a.path)
+    kernels = KERNELS[a.path]
     capacity = a.warmup + a.steps + 1
     cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps,
                          gqa_reduction=a.reduction)

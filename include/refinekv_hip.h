@@ -61,17 +61,23 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
                 float* max_value_norm, rkv_stream_t stream);
 
 /* Workspace bytes needed by rkv_select / rkv_decode for this shape (device
- * memory the caller owns; its contents need no initialisation). */
+ * memory the caller owns).  Zero-fill it when it is created: its first region
+ * holds rkv_decode's hand-off counters, which count this shape's tiles (each
+ * call adds the same amount), so zero-fill it again before using it for
+ * another shape. */
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
-/* Byte offsets inside the workspace (for tests): control (reserved), zf
- * (float4 z, delta, A, th per query row and block: the selection statistics
- * and the delta-only factors of the risk), lse (per-tile log-sum-exp
- * partials), part_m, part_l, part_acc (per-tile attention partials), counts
+/* Byte offsets inside the workspace (for tests): control (hand-off
+ * counters: one 64-byte line per KV head -- u64 tiles arrived and tiles
+ * merged, summed over calls -- then a line starting with a sticky u32 error
+ * word, bit 0 set if a hand-off wait gave up), zf (float4 z,
+ * delta, A, th per query row and block: the selection statistics and the
+ * delta-only factors of the risk), lse (per-tile log-sum-exp partials),
+ * part_ml, part_acc (per-tile attention partials: (m, l) and acc), counts
  * (per-tile access counts), total, then n_tiles and the padded row strides
- * (elements) of zf and of the per-tile arrays -> out11[0..10]. */
+ * (elements) of zf and of the per-tile arrays -> out10[0..9]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out11);
+                         int64_t* out10);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton
@@ -124,9 +130,17 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
 /* Profiling hook with no reference counterpart: when `events` points to 4
  * hipEvent_t handles, later rkv_select / rkv_decode calls on this thread
  * record events[0] before their first kernel and events[k] after their k-th
- * (rkv_select: score, decide; rkv_decode: score, attend, merge).  NULL turns
- * it off. */
+ * (rkv_select: score, decide; rkv_decode: the one-launch step, or score,
+ * attend, merge).  NULL turns it off. */
 int rkv_set_profile_events(void* events);
+
+/* Test hook with no reference counterpart: 0 (default) lets rkv_decode run
+ * one launch per step (score, decision, attention and merge in one kernel,
+ * heads handed off through the workspace's counters) where the shape allows
+ * it -- every query row in one attention pass and at most 256 tiles of 64
+ * blocks per head -- and three kernels otherwise; 1 always uses the three
+ * kernels.  Per thread. */
+int rkv_set_decode_path(int path);
 
 /* Test hook with no reference counterpart: applies the kernels' device
  * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */

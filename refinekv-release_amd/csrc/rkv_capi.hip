@@ -45,7 +45,7 @@ using namespace rkv;
 
 extern "C" const char* rkv_last_error(void) { return g_error; }
 
-extern "C" int rkv_version(void) { return 1; }
+extern "C" int rkv_version(void) { return 2; }
 
 // Applies a device scalar function elementwise: fn 0 = exp, 1 = log,
 // 2 = bfloat16 round trip, 3 = sqrt.  x and y are device arrays of n floats.

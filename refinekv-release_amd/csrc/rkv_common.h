@@ -244,6 +244,69 @@ __device__ __forceinline__ void unpack(const RawBf16<N>& r, float (&out)[N]) {
   }
 }
 
+// Data handed from one workgroup to another inside a launch.  The two may
+// run on different XCDs, each with its own L2, so a plain store can sit in
+// the writer's L2 while the reader's L2 holds a stale line.  These accesses
+// carry the sc1 cache-policy bit: stores write through to the device's point
+// of coherence and loads read from it.  A writer makes its stores visible by
+// waiting for them (s_waitcnt) before it bumps a counter; a reader that has
+// seen the counter reach its target then loads with these accesses.  No L2
+// write-back or invalidate is needed (an agent-scope fence costs both).
+// Offsets are bytes from `base`; accesses past `bytes` read 0 and are dropped.
+constexpr int kCoherentPolicy = 16;  // sc1
+
+struct Coherent {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ Coherent(const void* base, uint32_t bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes,
+                                            0x00020000)) {}
+  __device__ float4 load4(uint32_t off) const {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, kCoherentPolicy);
+    return make_float4(bits_f32(v[0]), bits_f32(v[1]), bits_f32(v[2]), bits_f32(v[3]));
+  }
+  __device__ float2 load2(uint32_t off) const {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kCoherentPolicy);
+    return make_float2(bits_f32(v[0]), bits_f32(v[1]));
+  }
+  __device__ uint32_t load_u32(uint32_t off) const {
+    return __builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, kCoherentPolicy);
+  }
+  __device__ void store4(uint32_t off, float4 x) const {
+    typedef unsigned int U4 __attribute__((ext_vector_type(4)));
+    const U4 v = {f32_bits(x.x), f32_bits(x.y), f32_bits(x.z), f32_bits(x.w)};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, (int)off, 0, kCoherentPolicy);
+  }
+  __device__ void store2(uint32_t off, float2 x) const {
+    typedef unsigned int U2 __attribute__((ext_vector_type(2)));
+    const U2 v = {f32_bits(x.x), f32_bits(x.y)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, kCoherentPolicy);
+  }
+  __device__ void store_u32(uint32_t off, uint32_t x) const {
+    __builtin_amdgcn_raw_buffer_store_b32(x, r, (int)off, 0, kCoherentPolicy);
+  }
+};
+
+// Waits until every earlier memory access of this wave has completed (a
+// writer's coherent stores before it signals a counter).
+__device__ __forceinline__ void wait_memory() { __builtin_amdgcn_s_waitcnt(0); }
+
+// Polls a device-scope counter until it reaches `target`; after `limit`
+// polls it gives up, sets bit 0 of *error and returns false (so a launch
+// whose hand-off never completes still ends, with its error recorded).
+template <typename U>
+__device__ __forceinline__ bool wait_counter(const U* counter, U target, uint32_t limit,
+                                             uint32_t* error) {
+  uint32_t n = 0;
+  while (__hip_atomic_load(counter, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < target) {
+    if (++n >= limit) {
+      __hip_atomic_fetch_or(error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      return false;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return true;
+}
+
 // Position of the k-th (0-based) set bit of m; m must have more than k bits.
 __device__ __forceinline__ int nth_set_bit(uint64_t m, int k) {
   int pos = 0;

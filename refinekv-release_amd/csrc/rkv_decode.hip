@@ -39,7 +39,13 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsPerWave = kMaxGroup / kWaves;  // query rows a wave owns in a tile
 constexpr float kLog2e = 1.44269504088896341f;
-constexpr int64_t kControlWords = 64;  // reserved, zero-filled
+constexpr int kLine = 8;  // u64 counters per 64-byte hand-off line
+
+// Bytes of the one-launch step's hand-off counters: one line per KV head
+// and one for the launch.
+__host__ __device__ constexpr int64_t control_bytes(int64_t heads) {
+  return (heads + 1) * kLine * 8;
+}
 
 // Optional profiling events (rkv_set_profile_events): events[0] is recorded
 // before the first kernel of a call and events[k] after its k-th kernel.
@@ -55,7 +61,7 @@ inline void mark(int i, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
-  int64_t control, zf, lse, part_m, part_l, part_acc, counts, total;
+  int64_t control, zf, lse, part_ml, part_acc, counts, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -72,11 +78,10 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
     off = align256(off + bytes);
     return at;
   };
-  L.control = take(kControlWords * 4);
+  L.control = take(control_bytes(heads));
   L.zf = take(rows * L.z_stride * 16);
   L.lse = take(rows * L.tile_stride * 4 * 4);
-  L.part_m = take(rows * L.tile_stride * 4);
-  L.part_l = take(rows * L.tile_stride * 4);
+  L.part_ml = take(rows * L.tile_stride * 8);
   L.part_acc = take(rows * L.tile_stride * dim * 4);
   L.counts = take(heads * L.tile_stride * 4);
   L.total = off;
@@ -194,11 +199,21 @@ struct ScoreArgs {
 constexpr int kOwnQ = 1024;
 constexpr int kQPad = 4;
 
+// Floats of LDS that stage q and bf16(q^2) for `group` rows.
+__host__ __device__ constexpr int64_t score_q_floats(int64_t group, int64_t dim) {
+  return (group * dim <= kOwnQ ? kWaves : 1) * 2 * group *
+         (dim + (dim <= 128 ? 8 : 16) * kQPad);
+}
+
+// The most score_q_floats needs for any group up to `group`.
+__host__ __device__ constexpr int64_t score_q_floats_max(int64_t group, int64_t dim) {
+  int64_t m = 0;
+  for (int64_t g = 1; g <= group; ++g) m = score_q_floats(g, dim) > m ? score_q_floats(g, dim) : m;
+  return m;
+}
+
 inline size_t score_smem(int64_t group, int64_t dim) {
-  const int64_t copies = group * dim <= kOwnQ ? kWaves : 1;
-  const int64_t lanes = dim <= 128 ? 8 : 16;
-  const int64_t row = dim + lanes * kQPad;
-  return sizeof(float) * (2 * group * kTile + copies * 2 * group * row);
+  return sizeof(float) * (2 * group * kTile + score_q_floats(group, dim));
 }
 
 // N consecutive floats from LDS (16-byte loads when aligned, else 8-byte).
@@ -223,22 +238,24 @@ __device__ __forceinline__ void lds_read(const float* p, float (&out)[N]) {
   }
 }
 
+// The selection dot products of tile `tile` of head h for every query row:
+// sdot[g][b] = q_g . k_mean_b and pdot[g][b] = bf16(q_g^2) . ellipsoid_b
+// (DSUM), b tile-relative; ends with a barrier.  qstage holds
+// score_q_floats(G, D) floats of LDS.
 template <int D>
-__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
+__device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_t tile,
+                                           float* sdot, float* pdot, float* qstage) {
   using S = Dots<D>;
   constexpr int CH = S::kCh;
-  extern __shared__ float score_lds[];
   const int G = a.group;
-  float* sdot = score_lds;          // [G][64]
-  float* pdot = sdot + G * kTile;   // [G][64]
-  const int64_t h = blockIdx.y, tile = blockIdx.x, N = a.n_blocks;
+  const int64_t N = a.n_blocks;
   const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
   const int c = tid % S::kLanes, sub = tid / S::kLanes;
   const bool own_q = G * D <= kOwnQ;
 
   constexpr int QW = CH + kQPad;          // padded slice
   constexpr int QS = S::kLanes * QW;      // padded row
-  float* qs = pdot + G * kTile + (own_q ? wave * 2 * G * QS : 0);  // [G][QS] bf16(q)
+  float* qs = qstage + (own_q ? wave * 2 * G * QS : 0);  // [G][QS] bf16(q)
   float* q2s = qs + G * QS;                                         // [G][QS] bf16(q^2)
   const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
   const int first = own_q ? lane : tid, step = own_q ? kWave : kThreads;
@@ -252,6 +269,7 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     const int i = first + k * step;
     qw[k] = q32[i < G * D / 2 ? i : 0];
   }
+
   RawBf16<CH> kraw[S::kPasses], eraw[S::kPasses];
 #pragma unroll
   for (int ps = 0; ps < S::kPasses; ++ps) {
@@ -261,6 +279,11 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     kraw[ps] = load_raw<CH>(a.key_mean + o);
     eraw[ps] = load_raw<CH>(a.ellipsoid + o);
   }
+  // The query words are used here, after the summary loads are issued: a
+  // query load sunk into the staging branch below would be issued after
+  // them and wait for all of them.
+#pragma unroll
+  for (int k = 0; k < kQWords; ++k) asm volatile("" : "+v"(qw[k]));
   auto stage = [&](int i, uint32_t u) {
     const float q0 = bits_f32(u << 16), q1 = bits_f32(u & 0xFFFF0000u);
     const int g = 2 * i / D, e = 2 * i % D;  // element pair e, e + 1 of row g
@@ -279,9 +302,6 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
   // A wave's LDS operations complete in order, so its own copy is ready for
   // its own reads; the shared copy needs the workgroup.
   if (!own_q) __syncthreads();
-  // ln(count): every block holds block_size tokens except the last.
-  const float ln_full = logf_((float)a.block);
-  const float ln_last = logf_((float)(a.length - (N - 1) * a.block));
 
   for (int g0 = 0; g0 < G; g0 += 4) {
     // this lane's slice of q and q^2 for rows g0 .. g0+3 (clamped)
@@ -325,29 +345,61 @@ __global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
     }
   }
   __syncthreads();
+}
 
-  // z, delta and the LSE partials: wave w owns rows w, w + 4, ...; lane =
-  // block of the tile.
+// z, delta, the risk's delta-only factors and the tile's LSE partials from
+// the dot products: wave w owns rows w, w + 4, ...; lane = block of the
+// tile.  put_z(g, valid, (z, delta, A, th)) is called by every lane (valid:
+// the block exists); put_lse(g, (zm, zl, cm, cl)) by lane 0.
+template <typename PutZ, typename PutLse>
+__device__ __forceinline__ void score_stats(const ScoreArgs& a, int64_t tile, const float* sdot,
+                                            const float* pdot, PutZ put_z, PutLse put_lse) {
+  const int G = a.group;
+  const int64_t N = a.n_blocks;
+  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  // ln(count): every block holds block_size tokens except the last.
+  const float ln_full = logf_((float)a.block);
+  const float ln_last = logf_((float)(a.length - (N - 1) * a.block));
   for (int g = wave; g < G; g += kWaves) {
     const int64_t b = tile * kTile + lane;
+    const bool valid = b < N;
     float z = kNegInf, zc = kNegInf;
-    if (b < N) {
+    float4 zf = make_float4(kNegInf, 0.0f, 0.0f, 0.0f);
+    if (valid) {
       const float s = sdot[g * kTile + lane] * a.scale;
       const float dl = (sqrtf(clamp_min(pdot[g * kTile + lane], 0.0f)) * a.scale) * kInflate;
       z = s + (b == N - 1 ? ln_last : ln_full);
       float lcosh, ra, rth;
       delta_terms(dl, lcosh, ra, rth);
       zc = z + lcosh;
-      a.zf[(h * G + g) * a.z_stride + b] = make_float4(z, dl, ra, rth);
+      zf = make_float4(z, dl, ra, rth);
     }
+    put_z(g, valid, zf);
     const float zm = wave_nanmax_u(z);
     const float zl = wave_sum_u(expf_(z - inf_to_zero(zm)));
     const float cm = wave_nanmax_u(zc);
     const float cl = wave_sum_u(expf_(zc - inf_to_zero(cm)));
-    if (lane == 0)
-      *reinterpret_cast<float4*>(a.lse + ((h * G + g) * a.tile_stride + tile) * 4) =
-          make_float4(zm, zl, cm, cl);
+    if (lane == 0) put_lse(g, make_float4(zm, zl, cm, cl));
   }
+}
+
+template <int D>
+__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
+  extern __shared__ float score_lds[];
+  const int G = a.group;
+  float* sdot = score_lds;          // [G][64]
+  float* pdot = sdot + G * kTile;   // [G][64]
+  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  const int lane = threadIdx.x % kWave;
+  score_dots<D>(a, h, tile, sdot, pdot, pdot + G * kTile);
+  score_stats(
+      a, tile, sdot, pdot,
+      [&](int g, bool valid, float4 zf) {
+        if (valid) a.zf[(h * G + g) * a.z_stride + tile * kTile + lane] = zf;
+      },
+      [&](int g, float4 part) {
+        *reinterpret_cast<float4*>(a.lse + ((h * G + g) * a.tile_stride + tile) * 4) = part;
+      });
 }
 
 // ---------------------------------------------------------------------------
@@ -377,17 +429,20 @@ struct DecideShared {
 
 // LSE of one row from the tile partials in the fixed order: the max first,
 // then 64 lane accumulators (tile t -> lane t % 64, left to right) and the
-// 64-wide butterfly.  (m0, l0) is this lane's partial of tile `lane`.
-__device__ __forceinline__ float merge_lse(float m0, float l0, const float* part, int which,
-                                           int64_t n_tiles, int lane) {
+// 64-wide butterfly.  (m0, l0) is this lane's partial of tile `lane`;
+// part(t) gives tile t's (m, l) for tiles beyond the first 64.
+template <typename Part>
+__device__ __forceinline__ float merge_lse(float m0, float l0, Part part, int64_t n_tiles,
+                                           int lane) {
   float mx = lane < n_tiles ? m0 : kNegInf;
-  for (int64_t t = lane + kWave; t < n_tiles; t += kWave)
-    mx = nanmax(mx, part[t * 4 + 2 * which]);
+  for (int64_t t = lane + kWave; t < n_tiles; t += kWave) mx = nanmax(mx, part(t).x);
   mx = wave_nanmax_u(mx);
   const float ms = inf_to_zero(mx);
   float acc = lane < n_tiles ? l0 * expf_(m0 - ms) : 0.0f;
-  for (int64_t t = lane + kWave; t < n_tiles; t += kWave)
-    acc = acc + part[t * 4 + 2 * which + 1] * expf_(part[t * 4 + 2 * which] - ms);
+  for (int64_t t = lane + kWave; t < n_tiles; t += kWave) {
+    const float2 p = part(t);
+    acc = acc + p.y * expf_(p.x - ms);
+  }
   return logf_(wave_sum_u(acc)) + ms;
 }
 
@@ -415,6 +470,9 @@ struct DecideLoads {
   float4 part, zf;
 };
 
+// kStats = false leaves part and zf to the caller (the one-launch step has
+// them only after its hand-off).
+template <bool kStats = true>
 __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t h,
                                                     int64_t tile) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
@@ -428,15 +486,27 @@ __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t
   DecideLoads d;
   d.vnorm = a.value_norm[h * N + bc];
   d.anc = anc[h * N + bc];
-  d.part = *reinterpret_cast<const float4*>(a.lse + ((h * G + gl) * a.tile_stride + tl) * 4);
-  d.zf = a.zf[(h * G + gl) * a.z_stride + bc];
+  if constexpr (kStats) {
+    d.part = *reinterpret_cast<const float4*>(a.lse + ((h * G + gl) * a.tile_stride + tl) * 4);
+    d.zf = a.zf[(h * G + gl) * a.z_stride + bc];
+  }
   return d;
 }
 
+// Where the one-launch step keeps what the separate kernels pass through
+// the workspace: the tile's (z, delta, A, th) in LDS and the LSE partials
+// behind coherent accesses.
+struct StepStats {
+  const float4 (*zs)[kTile];  // [row][block of the tile]
+  Coherent lse;               // the workspace's lse region
+};
+
+template <bool kFused = false>
 __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
                                                   const DecideLoads& in, DecideShared& sh,
                                                   float (*zsh)[kTile], const int32_t*& list,
-                                                  uint32_t& count) {
+                                                  uint32_t& count,
+                                                  const StepStats* ss = nullptr) {
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
@@ -453,10 +523,18 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   uint64_t wsel = 0;
   bool wbad = false;
   auto row_stats = [&](int g, float4 part, float4 zf) {
-    const float* prow = a.lse + (h * G + g) * a.tile_stride * 4;
+    const int64_t row = (h * G + g) * a.tile_stride;
+    auto tile_part = [&](int64_t t, int which) -> float2 {
+      if constexpr (kFused) {
+        return ss->lse.load2((uint32_t)(((row + t) * 4 + 2 * which) * 4));
+      } else {
+        const float* p = a.lse + (row + t) * 4 + 2 * which;
+        return make_float2(p[0], p[1]);
+      }
+    };
     if (lane >= T) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
-    const float lz = merge_lse(part.x, part.y, prow, 0, T, lane);
-    const float lc = merge_lse(part.z, part.w, prow, 1, T, lane);
+    const float lz = merge_lse(part.x, part.y, [&](int64_t t) { return tile_part(t, 0); }, T, lane);
+    const float lc = merge_lse(part.z, part.w, [&](int64_t t) { return tile_part(t, 1); }, T, lane);
     if (a.stats_out && owner && tile == 0 && lane == 0) {
       a.stats_out[(h * G + g) * 2] = lz;
       a.stats_out[(h * G + g) * 2 + 1] = lc;
@@ -476,9 +554,13 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   if (wave < G) row_stats(wave, in.part, in.zf);
 #pragma unroll 1
   for (int g = wave + kWaves; g < G; g += kWaves) {
-    const float4 part =
-        *reinterpret_cast<const float4*>(a.lse + ((h * G + g) * a.tile_stride + tl) * 4);
-    row_stats(g, part, a.zf[(h * G + g) * a.z_stride + bc]);
+    const int64_t at = (h * G + g) * a.tile_stride + tl;
+    if constexpr (kFused) {
+      row_stats(g, ss->lse.load4((uint32_t)(at * 16)), ss->zs[g][lane]);
+    } else {
+      row_stats(g, *reinterpret_cast<const float4*>(a.lse + at * 4),
+                a.zf[(h * G + g) * a.z_stride + bc]);
+    }
   }
   if (lane == 0) {
     sh.wsel[wave] = wsel;
@@ -546,8 +628,7 @@ struct AttendArgs {
   const uint16_t* key_suffix;   // token t of head h at h * ks_hs + t * ks_ts
   const uint16_t* value_suffix;
   const int32_t* suffix_len_dev;  // or null
-  float* part_m;                // (H*G, tile_stride)
-  float* part_l;
+  float2* part_ml;              // (H*G, tile_stride): m, l
   float* part_acc;              // (H*G, tile_stride, D)
   uint32_t* tile_counts;        // (H, tile_stride) or null
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
@@ -635,6 +716,137 @@ struct CombineShared {
   float ml[16][kRows][2];
 };
 
+// ---------------------------------------------------------------------------
+// One-launch step: hand-off counters and the merge of a head by its last tile
+// ---------------------------------------------------------------------------
+// Counters (u64 at the start of the workspace): head h owns the 64-byte line
+// at counter kLine * h -- [0] tiles that have published their LSE partials,
+// [1] tiles that have published their attention partials; after the heads'
+// lines, a sticky u32 error word (bit 0: a wait gave up after kSpinLimit
+// polls).  The counters are never reset: every launch adds exactly n_tiles
+// to each, so a tile's own arrival (old value / n_tiles) tells it the
+// launch's epoch e and the counts it waits for, (e + 1) n_tiles.  This
+// needs the workspace zero-filled once when created and used for one shape
+// (one n_tiles) thereafter.
+//
+// Progress: a tile waits only for the tiles of its own head, and waits only
+// after publishing its own partials.  Workgroups are dispatched in
+// blockIdx order (x fastest, so a head's tiles are consecutive); with at
+// least n_tiles workgroups resident at once (the host allows this path only
+// for n_tiles <= kStepMaxTiles, one workgroup per CU), the lowest head
+// still waiting has all of its tiles dispatched, so its wait ends.  A wait
+// that does not end within kSpinLimit polls records an error instead of
+// hanging.
+constexpr uint32_t kSpinLimit = 1u << 20;
+constexpr int64_t kStepMaxTiles = 256;
+
+struct StepCtx {
+  StepStats stats;
+  const float* mts;               // [row] the tile's max z (LDS)
+  Coherent ml, acc, counts;       // partial (m, l), partial acc, tile counts
+  uint64_t* control;
+  uint16_t* out;                  // (H, G, D) bf16
+  unsigned long long* accessed;   // or null
+  uint32_t* flag;                 // one LDS word
+  unsigned long long* wsum;       // kWaves LDS words
+  uint64_t* base;                 // LDS: epoch * n_tiles (thread 0's copy)
+  int heads;
+  __device__ uint32_t* error() const {
+    return reinterpret_cast<uint32_t*>(control + (int64_t)heads * kLine);
+  }
+};
+
+constexpr int kMergeBatch = 8;  // partials per lane per batch of loads
+
+// Folds state (m2, d2, n2) into (mx, num, den); empty states (den 0) are
+// skipped.
+__device__ __forceinline__ void merge_state4(float m2, float d2, const float4& n2, float& mx,
+                                             float4& num, float& den) {
+  if (!(d2 > 0.0f)) return;
+  if (!(den > 0.0f)) {
+    mx = m2;
+    den = d2;
+    num = n2;
+    return;
+  }
+  const float M = fmaxf(mx, m2);
+  const float ea = __builtin_amdgcn_exp2f((mx - M) * kLog2e);
+  const float eb = __builtin_amdgcn_exp2f((m2 - M) * kLog2e);
+  den = __builtin_fmaf(d2, eb, den * ea);
+  num.x = __builtin_fmaf(n2.x, eb, num.x * ea);
+  num.y = __builtin_fmaf(n2.y, eb, num.y * ea);
+  num.z = __builtin_fmaf(n2.z, eb, num.z * ea);
+  num.w = __builtin_fmaf(n2.w, eb, num.w * ea);
+  mx = M;
+}
+
+// The head's last kMergers tiles (by ticket) merge it, each a slice of the
+// columns, once every tile of the head has published.  Slice m: head h's
+// rows, column quads [m Q / K, (m + 1) Q / K), from every tile's partial ->
+// bf16 output; slice 0 also adds the head's access count.  Each (row, 4
+// columns) unit is merged by S adjacent lanes (S a power of two; tiles s,
+// s + S, ... each), then an xor tree over the S lanes: a fixed order, so
+// outputs repeat bit for bit.
+constexpr int kMergers = 8;
+
+template <int D>
+__device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, int m, int K) {
+  const DecideArgs& da = a.decide;
+  const int G = da.group, T = (int)da.n_tiles;
+  const int64_t ts = da.tile_stride;
+  const int tid = threadIdx.x;
+  constexpr int Q = D / 4;
+  const int q0 = m * Q / K, nq = (m + 1) * Q / K - q0;
+  const int units = G * nq;
+  int S = 1;
+  while (S * 2 * units <= kThreads) S *= 2;
+  for (int u0 = 0; u0 < units; u0 += kThreads / S) {
+    const int u = u0 + tid / S, sl = tid % S;
+    const int uc = u < units ? u : units - 1;
+    const int g = uc / nq, q = q0 + uc % nq;
+    const int64_t row = (h * G + g) * ts;
+    float mx = kNegInf, den = 0.0f;
+    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+    for (int t0 = sl; t0 < T; t0 += S * kMergeBatch) {
+      float2 ml[kMergeBatch];
+      float4 av[kMergeBatch];
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) {
+        const int t = t0 + k * S;
+        const int tc = t < T ? t : 0;
+        ml[k] = sx.ml.load2((uint32_t)((row + tc) * 8));
+        av[k] = sx.acc.load4((uint32_t)(((row + tc) * D + 4 * q) * 4));
+        if (t >= T) ml[k].y = 0.0f;
+      }
+#pragma unroll
+      for (int k = 0; k < kMergeBatch; ++k) merge_state4(ml[k].x, ml[k].y, av[k], mx, num, den);
+    }
+    for (int o = 1; o < S; o <<= 1) {
+      const float m2 = shfl_xor(mx, o), d2 = shfl_xor(den, o);
+      const float4 n2 = make_float4(shfl_xor(num.x, o), shfl_xor(num.y, o), shfl_xor(num.z, o),
+                                    shfl_xor(num.w, o));
+      merge_state4(m2, d2, n2, mx, num, den);
+    }
+    if (sl == 0 && u < units) {
+      const float dn = fmaxf(den, 1e-30f);
+      const uint32_t lo = (uint32_t)bf16_rne(num.x / dn) | ((uint32_t)bf16_rne(num.y / dn) << 16);
+      const uint32_t hi = (uint32_t)bf16_rne(num.z / dn) | ((uint32_t)bf16_rne(num.w / dn) << 16);
+      *reinterpret_cast<uint2*>(sx.out + (h * G + g) * D + 4 * q) = make_uint2(lo, hi);
+    }
+  }
+  // the step's access count: this head's tile counts, added once
+  if (sx.accessed && m == 0) {
+    unsigned long long c = 0;
+    for (int t = tid; t < T; t += kThreads) c += sx.counts.load_u32((uint32_t)((h * ts + t) * 4));
+#pragma unroll
+    for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, kWave);
+    if (tid % kWave == 0) sx.wsum[tid / kWave] = c;
+    __syncthreads();
+    if (tid == 0)
+      atomicAdd(sx.accessed, ((sx.wsum[0] + sx.wsum[1]) + sx.wsum[2]) + sx.wsum[3]);
+  }
+}
+
 // Two workgroups per CU (<= 256 registers per lane), so a 512-tile step runs
 // in one round on 256 CUs.
 //
@@ -645,15 +857,18 @@ struct CombineShared {
 // are in flight; after the decision the
 // expanded blocks' representative terms are taken out again and the
 // expanded blocks' tokens and the suffix rows are attended.
-template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
-void attend_kernel(AttendArgs a) {
+//
+// kFused: the one-launch step (sx set): the tile's statistics come from
+// LDS, the decision waits until every tile of the head has published its
+// LSE partials, the partials are published with coherent stores and the
+// head's last tile merges them.
+template <int D, int GBM, bool kFused>
+__device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& dsh,
+                                            CombineShared<D, GBM>& cmb, const StepCtx* sx) {
   constexpr int CH = D / 16;
   constexpr int R = kRowBatch;
   constexpr int NB = kTile / 16;  // representatives per lane group
   using Comb = CombineShared<D, GBM>;
-  __shared__ DecideShared dsh;
-  __shared__ Comb cmb;
   const DecideArgs& da = a.decide;
   const int64_t h = blockIdx.y;
   const uint32_t tile = blockIdx.x;
@@ -665,7 +880,7 @@ void attend_kernel(AttendArgs a) {
   const int g0 = blockIdx.z * GBM, gn = min(GBM, G - g0);  // this pass's query rows
 
   // ---- loads independent of the decision ---------------------------------
-  const DecideLoads din = decide_issue(da, h, tile);
+  DecideLoads din = decide_issue<!kFused>(da, h, tile);
   // The suffix length does not change during a launch: a scalar load from
   // the constant address space, outside the vector loads' in-order count.
   uint32_t S = (uint32_t)a.suffix_cap;
@@ -686,13 +901,15 @@ void attend_kernel(AttendArgs a) {
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       const int gg = g0 + g < G ? g0 + g : G - 1;
-      zr[g][i] = da.zf[(h * G + gg) * da.z_stride + b].x;
+      if constexpr (kFused) zr[g][i] = sx->stats.zs[gg][lg + 16 * i].x;
+      else zr[g][i] = da.zf[(h * G + gg) * da.z_stride + b].x;
     }
   }
 #pragma unroll
   for (int g = 0; g < GBM; ++g) {
     const int gg = g0 + g < G ? g0 + g : G - 1;
-    mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
+    if constexpr (kFused) mt[g] = sx->mts[gg];
+    else mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
   }
   RawBf16<CH> qraw[GBM];
   const uint16_t* qh = a.query + (h * G) * D + c * CH;
@@ -744,9 +961,21 @@ void attend_kernel(AttendArgs a) {
     }
   }
   // ---- the decision -------------------------------------------------------
+  if constexpr (kFused) {
+    // every tile of the head has published its LSE partials
+    if (tid == 0)
+      wait_counter<uint64_t>(sx->control + h * kLine, *sx->base + T, kSpinLimit, sx->error());
+    __syncthreads();
+    const int wave = tid / kWave, lane = tid % kWave;
+    const int gl = wave < G ? wave : G - 1;
+    const uint32_t tl = (uint32_t)lane < T ? (uint32_t)lane : 0u;
+    din.part = sx->stats.lse.load4((uint32_t)(((h * G + gl) * da.tile_stride + tl) * 16));
+    din.zf = sx->stats.zs[gl][lane];
+  }
   const int32_t* list;
   uint32_t count = 0;
-  const uint64_t bits = decide_finish(da, h, tile, din, dsh, nullptr, list, count);
+  const uint64_t bits = decide_finish<kFused>(da, h, tile, din, dsh, nullptr, list, count,
+                                              kFused ? &sx->stats : nullptr);
 
   // take the expanded blocks' representatives out again
   if ((bits >> lg) & 0x0001000100010001ull) {
@@ -864,23 +1093,132 @@ void attend_kernel(AttendArgs a) {
         l = __builtin_fmaf(cmb.ml[w][j][1], e, l);
       }
       const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + tile;
-      *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
-      if (d == 0) {
-        a.part_m[at] = M;
-        a.part_l[at] = l;
+      if constexpr (kFused) {
+        sx->acc.store2((uint32_t)((at * D + d) * 4), make_float2(a0, a1));
+        if (d == 0) sx->ml.store2((uint32_t)(at * 8), make_float2(M, l));
+      } else {
+        *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
+        if (d == 0) a.part_ml[at] = make_float2(M, l);
       }
     }
   }
-  if (a.tile_counts && tid == 0 && blockIdx.z == 0)
-    a.tile_counts[h * da.tile_stride + tile] = count;
+  if (a.tile_counts && tid == 0 && blockIdx.z == 0) {
+    if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + tile) * 4), count);
+    else a.tile_counts[h * da.tile_stride + tile] = count;
+  }
+  if constexpr (kFused) {
+    // publish and take a ticket; the head's last K tiles wait for the rest
+    // and merge a column slice each
+    wait_memory();
+    __syncthreads();
+    uint64_t* merged = sx->control + h * kLine + 1;
+    if (tid == 0) {
+      const uint64_t old = __hip_atomic_fetch_add(merged, 1ull, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      *sx->flag = (uint32_t)(old - *sx->base);
+    }
+    __syncthreads();
+    const uint32_t ticket = *sx->flag;
+    const uint32_t K = T < (uint32_t)kMergers ? T : (uint32_t)kMergers;
+    if (ticket >= T - K) {
+      if (tid == 0) wait_counter<uint64_t>(merged, *sx->base + T, kSpinLimit, sx->error());
+      __syncthreads();
+      merge_slice<D>(a, *sx, h, (int)(ticket - (T - K)), (int)K);
+    }
+  }
+}
+
+template <int D, int GBM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void attend_kernel(AttendArgs a) {
+  __shared__ alignas(16) DecideShared dsh;
+  __shared__ alignas(16) CombineShared<D, GBM> cmb;
+  attend_tile<D, GBM, false>(a, dsh, cmb, nullptr);
+}
+
+
+// ---------------------------------------------------------------------------
+// The one-launch step: score, decision, attention and merge of every tile
+// ---------------------------------------------------------------------------
+struct StepArgs {
+  ScoreArgs score;
+  AttendArgs attend;
+  uint64_t* control;              // hand-off counters
+  uint32_t* counts;               // (H, tile_stride) tile access counts
+  uint16_t* out;                  // (H, G, D) bf16
+  unsigned long long* accessed;   // or null
+  uint32_t lse_bytes, ml_bytes, acc_bytes, counts_bytes;
+  int heads;
+};
+
+// Every region starts on a 16-byte boundary: the q staging and the combine
+// buffer are read with 16-byte LDS accesses.
+template <int D, int GBM>
+struct StepShared {
+  alignas(16) float4 zs[GBM][kTile];  // z, delta, A, th of the tile's (row, block) pairs
+  alignas(16) float mts[GBM];         // the tile's max z per row
+  alignas(16) unsigned long long wsum[kWaves];
+  uint64_t base;
+  alignas(16) DecideShared dec;
+  alignas(16) union {
+    struct {
+      alignas(16) float sdot[GBM * kTile];
+      alignas(16) float pdot[GBM * kTile];
+      alignas(16) float q[score_q_floats_max(GBM, D)];
+    } score;
+    alignas(16) CombineShared<D, GBM> cmb;
+  } u;
+  uint32_t flag;
+};
+
+// Workgroup (tile, h): the tile's scores (z, delta and the risk's delta
+// factors stay in LDS; the LSE partials are published and the head's
+// arrival counter bumped), then attend_tile's decision (after the head's
+// tiles have all arrived), attention and, for the head's last tile, the
+// merge.
+template <int D, int GBM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
+void step_kernel(StepArgs s) {
+  __shared__ StepShared<D, GBM> sh;
+  const ScoreArgs& sa = s.score;
+  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  const int G = sa.group, tid = threadIdx.x, lane = tid % kWave;
+  const StepCtx sx{StepStats{sh.zs, Coherent(sa.lse, s.lse_bytes)},
+                   sh.mts,
+                   Coherent(s.attend.part_ml, s.ml_bytes),
+                   Coherent(s.attend.part_acc, s.acc_bytes),
+                   Coherent(s.counts, s.counts_bytes),
+                   s.control,
+                   s.out,
+                   s.accessed,
+                   &sh.flag,
+                   sh.wsum,
+                   &sh.base,
+                   s.heads};
+  score_dots<D>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+  score_stats(
+      sa, tile, sh.u.score.sdot, sh.u.score.pdot,
+      [&](int g, bool, float4 zf) { sh.zs[g][lane] = zf; },
+      [&](int g, float4 part) {
+        sh.mts[g] = part.x;
+        sx.stats.lse.store4((uint32_t)(((h * G + g) * sa.tile_stride + tile) * 16), part);
+      });
+  wait_memory();
+  __syncthreads();
+  if (tid == 0) {
+    const uint64_t T = (uint64_t)s.attend.decide.n_tiles;
+    const uint64_t old = __hip_atomic_fetch_add(s.control + h * kLine, 1ull, __ATOMIC_RELAXED,
+                                                __HIP_MEMORY_SCOPE_AGENT);
+    sh.base = old - old % T;  // this launch's epoch * n_tiles
+  }
+  attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx);
 }
 
 // ---------------------------------------------------------------------------
 // Kernel 3: merge a row's tile partials -> bf16 output columns
 // ---------------------------------------------------------------------------
 struct MergeArgs {
-  const float* part_m;    // (H*G, tile_stride)
-  const float* part_l;
+  const float2* part_ml;  // (H*G, tile_stride): m, l
   const float* part_acc;  // (H*G, tile_stride, D)
   uint16_t* out;          // (H*G, D)
   const uint32_t* tile_counts;     // (H, tile_stride) or null
@@ -891,7 +1229,6 @@ struct MergeArgs {
 
 constexpr int kMergeD = 32;                  // output columns per workgroup
 constexpr int kMergeK = kThreads / kMergeD;  // partial stripes
-constexpr int kMergeBatch = 8;               // partials per stripe per batch
 
 // Online merge of one partial into (mx, num, den); skips empty partials.
 __device__ __forceinline__ void merge_one(float m, float l, float acc, float& mx, float& num,
@@ -917,8 +1254,7 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
   const int tid = threadIdx.x, dl = tid % kMergeD, kk = tid / kMergeD;
   const int d = blockIdx.y * kMergeD + dl;
   const int dd = d < D ? d : 0;
-  const float* pm = a.part_m + r * a.tile_stride;
-  const float* pl = a.part_l + r * a.tile_stride;
+  const float2* pml = a.part_ml + r * a.tile_stride;
   const float* pa = a.part_acc + r * a.tile_stride * D + dd;
   float mx = kNegInf, num = 0.0f, den = 0.0f;
   for (int i0 = kk; i0 < P; i0 += kMergeK * kMergeBatch) {
@@ -927,8 +1263,9 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
     for (int u = 0; u < kMergeBatch; ++u) {
       const int i = i0 + u * kMergeK;
       const int ii = i < P ? i : 0;
-      mv[u] = pm[ii];
-      lv[u] = pl[ii];
+      const float2 ml = pml[ii];
+      mv[u] = ml.x;
+      lv[u] = ml.y;
       av[u] = pa[(int64_t)ii * D];
       if (i >= P) lv[u] = 0.0f;
     }
@@ -1098,8 +1435,7 @@ AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffe
   aa.key_suffix = static_cast<const uint16_t*>(b.suffix_cap ? b.key_suffix : b.key_pages);
   aa.value_suffix = static_cast<const uint16_t*>(b.suffix_cap ? b.value_suffix : b.value_pages);
   aa.suffix_len_dev = b.suffix_len;
-  aa.part_m = at<float>(p.ws, L.part_m);
-  aa.part_l = at<float>(p.ws, L.part_l);
+  aa.part_ml = at<float2>(p.ws, L.part_ml);
   aa.part_acc = at<float>(p.ws, L.part_acc);
   aa.tile_counts = p.accessed ? at<uint32_t>(p.ws, L.counts) : nullptr;
   aa.kp_hs = b.kp_hs;
@@ -1116,8 +1452,7 @@ AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffe
 
 MergeArgs merge_args(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   MergeArgs ma;
-  ma.part_m = at<float>(p.ws, L.part_m);
-  ma.part_l = at<float>(p.ws, L.part_l);
+  ma.part_ml = at<float2>(p.ws, L.part_ml);
   ma.part_acc = at<float>(p.ws, L.part_acc);
   ma.out = static_cast<uint16_t*>(b.output);
   ma.tile_counts = at<uint32_t>(p.ws, L.counts);
@@ -1153,8 +1488,75 @@ int launch_attend(const AttendArgs& aa, int64_t rows, dim3 grid, hipStream_t str
   return set_error(kUnsupported, "rkv_decode: no attention kernel for this group");
 }
 
-// One decode step: score, decide + attend, merge.
+template <int D>
+int launch_step_d(const StepArgs& sa, int64_t rows, dim3 grid, hipStream_t stream) {
+  constexpr int CH = D / 16;
+  constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
+  switch (rows) {
+    case 4:
+      step_kernel<D, 4><<<grid, dim3(kThreads), 0, stream>>>(sa);
+      return check_launch("step_kernel");
+    case 8:
+      if constexpr (CAP >= 8) {
+        step_kernel<D, 8><<<grid, dim3(kThreads), 0, stream>>>(sa);
+        return check_launch("step_kernel");
+      }
+      break;
+    default:
+      if constexpr (CAP >= 16) {
+        step_kernel<D, 16><<<grid, dim3(kThreads), 0, stream>>>(sa);
+        return check_launch("step_kernel");
+      }
+      break;
+  }
+  return set_error(kUnsupported, "rkv_decode: no step kernel for this group");
+}
+
+// Which path rkv_decode takes (rkv_set_decode_path, per thread): 0 = the
+// one-launch step where the shape allows it, else three kernels; 1 = always
+// the three kernels.
+thread_local int g_decode_path = 0;
+
+// The one-launch step needs every query row in one attention pass, at most
+// kStepMaxTiles tiles per head (so that a head's tiles can all be resident),
+// its coherent regions addressable with 31-bit byte offsets and an 8-byte
+// aligned output (it stores 4 columns at a time).
+bool step_fits(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  const int64_t rows = rows_per_pass(p.group, p.dim);
+  const int64_t hg = p.heads * p.group, ts = L.tile_stride;
+  const int64_t limit = int64_t(1) << 31;
+  return p.group <= rows && L.n_tiles <= kStepMaxTiles && hg * ts * 16 < limit &&
+         hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8);
+}
+
+int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  StepArgs s;
+  s.score = score_args(p, L);
+  s.attend = attend_args(p, L, b);
+  s.control = at<uint64_t>(p.ws, L.control);
+  s.counts = at<uint32_t>(p.ws, L.counts);
+  s.attend.tile_counts = p.accessed ? s.counts : nullptr;
+  s.out = static_cast<uint16_t*>(b.output);
+  s.accessed = p.accessed;
+  const int64_t hg = p.heads * p.group, ts = L.tile_stride;
+  s.lse_bytes = (uint32_t)(hg * ts * 16);
+  s.ml_bytes = (uint32_t)(hg * ts * 8);
+  s.acc_bytes = (uint32_t)(hg * ts * p.dim * 4);
+  s.counts_bytes = (uint32_t)(p.heads * ts * 4);
+  s.heads = (int)p.heads;
+  const int64_t rows = rows_per_pass(p.group, p.dim);
+  mark(0, p.stream);
+  int rc = kUnsupported;
+  RKV_DISPATCH_DIM(p.dim, D,
+                   rc = launch_step_d<D>(s, rows, dim3((unsigned)L.n_tiles, (unsigned)p.heads),
+                                         p.stream));
+  mark(1, p.stream);
+  return rc;
+}
+
+// One decode step: the one-launch step, or score, decide + attend, merge.
 int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+  if (g_decode_path == 0 && step_fits(p, L, b)) return launch_step(p, L, b);
   const AttendArgs aa = attend_args(p, L, b);
   const MergeArgs ma = merge_args(p, L, b);
   const int64_t rows = rows_per_pass(p.group, p.dim);
@@ -1185,18 +1587,19 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
   return (size_t)make_layout(heads, group, dim, n_blocks).total;
 }
 
-// Byte offsets of the workspace regions, for tests: control, zf (z, delta,
-// A, th per row and block), lse, part_m, part_l, part_acc, counts, total,
-// then n_tiles, the row stride (blocks) of zf and of the per-tile arrays.
+// Byte offsets of the workspace regions, for tests: control (hand-off
+// counters), zf (z, delta, A, th per row and block), lse, part_ml, part_acc,
+// counts, total, then n_tiles, the row stride (blocks) of zf and of the
+// per-tile arrays.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out11) {
+                                    int64_t* out10) {
   clear_error();
-  if (!out11 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out10 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[11] = {L.control, L.zf,    L.lse,     L.part_m,   L.part_l,     L.part_acc,
+  const int64_t v[10] = {L.control, L.zf,    L.lse,     L.part_ml, L.part_acc,
                          L.counts,  L.total, L.n_tiles, L.z_stride, L.tile_stride};
-  for (int i = 0; i < 11; ++i) out11[i] = v[i];
+  for (int i = 0; i < 10; ++i) out10[i] = v[i];
   return kOk;
 }
 
@@ -1275,8 +1678,17 @@ extern "C" int rkv_decode(const void* query, const void* key_mean, const void* e
 // Profiling hook: when events is non-null, the following rkv_select /
 // rkv_decode calls on this thread record events[0] before their first kernel
 // and events[k] after their k-th (rkv_select: score, decide; rkv_decode:
-// score, attend, merge).  Pass NULL to stop.
+// step, or score, attend, merge).  Pass NULL to stop.
 extern "C" int rkv_set_profile_events(void* events) {
   g_events = static_cast<hipEvent_t*>(events);
+  return kOk;
+}
+
+// Test hook: 0 = rkv_decode uses the one-launch step where it fits (the
+// default), 1 = always the three kernels.  Per thread.
+extern "C" int rkv_set_decode_path(int path) {
+  clear_error();
+  if (path < 0 || path > 1) return set_error(kInvalidArgument, "rkv_set_decode_path: %d", path);
+  g_decode_path = path;
   return kOk;
 }

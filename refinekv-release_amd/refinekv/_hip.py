@@ -55,6 +55,8 @@ def _bind(lib):
     lib.rkv_math_probe.restype = _int
     lib.rkv_set_profile_events.argtypes = [_p]
     lib.rkv_set_profile_events.restype = _int
+    lib.rkv_set_decode_path.argtypes = [_int]
+    lib.rkv_set_decode_path.restype = _int
     return lib
 
 
@@ -139,8 +141,11 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("control", "zf", "lse", "part_m", "part_l", "part_acc", "counts", "total",
-                "n_tiles", "z_stride", "tile_stride")
+LAYOUT_NAMES = ("control", "zf", "lse", "part_ml", "part_acc", "counts", "total", "n_tiles",
+                "z_stride", "tile_stride")
+# rkv_set_decode_path codes: the one-launch step where it fits, or always the
+# three kernels (score, attend, merge).
+DECODE_PATHS = {"step": 0, "split": 1}
 
 
 def workspace_layout(heads, group, dim, n_blocks):
@@ -164,9 +169,19 @@ def _buffer(workspace, name, shape, device, dtype, zero=False):
 
 
 def _scratch(workspace, heads, group, dim, n_blocks, device):
-    """The kernels' workspace (zero-filled once when made)."""
-    nbytes = workspace_bytes(heads, group, dim, n_blocks)
-    return _buffer(workspace, "hip_scratch", (nbytes,), device, torch.uint8, zero=True)
+    """The kernels' workspace, zero-filled when made for a shape: its first
+    region holds the one-launch step's hand-off counters, which count that
+    shape's tiles (a new shape gets a new buffer)."""
+    shape = (heads, group, dim, n_blocks)
+    nbytes = workspace_bytes(*shape)
+    tensor = workspace.get("hip_scratch") if workspace is not None else None
+    if (tensor is None or workspace.get("hip_scratch_shape") != shape
+            or tensor.device != device or tensor.numel() != nbytes):
+        tensor = torch.zeros(nbytes, device=device, dtype=torch.uint8)
+        if workspace is not None:
+            workspace["hip_scratch"] = tensor
+            workspace["hip_scratch_shape"] = shape
+    return tensor
 
 
 # ---------------------------------------------------------------------------
@@ -234,6 +249,12 @@ def decode(query, summary, key_suffix, value_suffix, config, anchor_mask=None, w
         _ptr(accessed), _ptr(scratch), scratch.numel(), _stream(device))
     _check(rc, "rkv_decode")
     return output, mask
+
+
+def set_decode_path(name):
+    """Test hook: "step" (default) or "split" for later decode calls on this
+    thread."""
+    _check(lib().rkv_set_decode_path(DECODE_PATHS[name]), "rkv_set_decode_path")
 
 
 def math_probe(fn, x):

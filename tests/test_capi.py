@@ -44,7 +44,7 @@ def test_every_declared_symbol_is_exported(lib):
 
 
 def test_version_and_error_channel(lib):
-    assert lib.rkv_version() >= 1
+    assert lib.rkv_version() == 2
     assert lib.rkv_workspace_layout(0, 0, 0, 0, None) == 1
     assert b"bad arguments" in lib.rkv_last_error()
 
@@ -52,23 +52,21 @@ def test_version_and_error_channel(lib):
 def test_workspace_size_covers_layout(lib):
     from refinekv import _hip
 
-    controls = _hip.workspace_layout(1, 1, 32, 1)["zf"]
     for heads, group, dim, n in ((8, 4, 128, 4096), (4, 7, 128, 1024), (2, 16, 64, 3),
                                  (1, 1, 256, 1)):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
-        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:8]]
+        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:7]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
         rows, tiles, ts = heads * group, layout["n_tiles"], layout["tile_stride"]
-        # fixed-size control block first, so every shape finds it at offset 0
-        assert layout["control"] == 0 and layout["zf"] == controls
+        # hand-off counters first: one 64-byte line per KV head and one more
+        assert layout["control"] == 0 and layout["zf"] >= (heads + 1) * 64
         # padded strides: zf rows cover whole tiles, per-tile rows 64 tiles
         assert layout["z_stride"] == tiles * 64 and ts % 64 == 0 and ts >= tiles
         assert layout["lse"] - layout["zf"] >= rows * layout["z_stride"] * 16
-        assert layout["part_m"] - layout["lse"] >= rows * ts * 16
-        assert layout["part_l"] - layout["part_m"] >= rows * ts * 4
-        assert layout["part_acc"] - layout["part_l"] >= rows * ts * 4
+        assert layout["part_ml"] - layout["lse"] >= rows * ts * 16
+        assert layout["part_acc"] - layout["part_ml"] >= rows * ts * 8
         assert layout["counts"] - layout["part_acc"] >= rows * ts * dim * 4
         assert layout["total"] - layout["counts"] >= heads * ts * 4
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0

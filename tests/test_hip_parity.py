@@ -29,6 +29,30 @@ def hip():
     return _hip
 
 
+@pytest.fixture(params=["step", "split"])
+def decode_path(hip, request):
+    """rkv_decode's two paths: the one-launch step (where the shape allows
+    it) and the three kernels."""
+    hip.set_decode_path(request.param)
+    yield request.param
+    hip.set_decode_path("step")
+
+
+def assert_control_clean(hip, ws):
+    """After every launch each head's two hand-off counters (tiles arrived,
+    tiles merged) are equal multiples of n_tiles -- a whole number of
+    launches -- and no hand-off wait gave up.  Returns the launch count."""
+    heads, group, dim, n = ws["hip_scratch_shape"]
+    tiles = hip.workspace_layout(heads, group, dim, n)["n_tiles"]
+    lines = ws["hip_scratch"][:(heads + 1) * 64].view(torch.int64).cpu().numpy()
+    lines = lines.reshape(heads + 1, 8)
+    assert lines[heads, 0] & 0xFFFFFFFF == 0, "a hand-off wait gave up"
+    arrived, merged = lines[:heads, 0], lines[:heads, 1]
+    assert np.array_equal(arrived, merged) and not (arrived % tiles).any(), (arrived, merged)
+    assert np.all(arrived == arrived[0]), arrived
+    return int(arrived[0]) // tiles
+
+
 def bits16(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
@@ -218,7 +242,7 @@ def _pages_bits(t, block):
 
 
 @pytest.mark.parametrize("heads,group,dim,block,prompt,reduction,eps,spikes", DECODE_CASES)
-def test_decode_matches_oracle(hip, oracle_lib, heads, group, dim, block, prompt,
+def test_decode_matches_oracle(hip, oracle_lib, decode_path, heads, group, dim, block, prompt,
                                reduction, eps, spikes):
     inp = _decode_case(heads, group, dim, block, prompt, spikes, suffix=16)
     cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps, gqa_reduction=reduction)
@@ -249,9 +273,10 @@ def test_decode_matches_oracle(hip, oracle_lib, heads, group, dim, block, prompt
                 f"mask suffix={suffix} anchor={use_anchor}"
             got = res.output.float().cpu().numpy()[:, :, 0]
             assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+    assert_control_clean(hip, ws)
 
 
-def test_device_suffix_length_matches_slicing(hip):
+def test_device_suffix_length_matches_slicing(hip, decode_path):
     """tests/test_attention.py:186-204 for the HIP backend: bit-equal outputs."""
     q, keys, values = testing.small_inputs(length=71, dim=128)
     cfg = RefineKVConfig(backend="hip", gqa_reduction="mean")
@@ -267,7 +292,7 @@ def test_device_suffix_length_matches_slicing(hip):
         assert torch.equal(actual, expected), count
 
 
-def test_workspace_reuse_and_access_counter(hip, oracle_lib):
+def test_workspace_reuse_and_access_counter(hip, oracle_lib, decode_path):
     inp = _decode_case(4, 4, 128, 32, 5000, 0.05)
     cfg = RefineKVConfig(backend="hip", eps=0.01)
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
@@ -282,9 +307,10 @@ def test_workspace_reuse_and_access_counter(hip, oracle_lib):
     assert torch.equal(outs[0], outs[1]) and torch.equal(outs[1], outs[2])
     want = oracle_lib.access_blocks(mask.cpu().numpy(), summary.counts.cpu().numpy())
     assert int(counter.item()) == 3 * want
+    assert assert_control_clean(hip, ws) == (3 if decode_path == "step" else 0)
 
 
-def test_graph_replays_match_eager(hip):
+def test_graph_replays_match_eager(hip, decode_path):
     """A captured decode step replayed several times (suffix length advanced
     on the device between replays, eager work and syncs in between) gives the
     eager result every time."""
@@ -308,6 +334,7 @@ def test_graph_replays_match_eager(hip):
                                 workspace={}).output
         torch.cuda.synchronize()
         assert torch.equal(got, want), count
+    assert_control_clean(hip, ws)
 
 
 @pytest.mark.parametrize("path", [p for p in gc.fixture_paths() if "f32" not in p],
@@ -335,8 +362,8 @@ def test_reference_golden_end_to_end(hip, path):
 
 def test_headline_shape_128k(hip, oracle_lib):
     """BASELINE config 3 shape (H_kv 8, G 4, d 128, 131072 prompt tokens, B 32):
-    masks equal the oracle's at full size, outputs within tolerance, and the
-    all-expanded step equals dense attention."""
+    masks equal the oracle's at full size, outputs within tolerance (both
+    decode paths), and the all-expanded step equals dense attention."""
     _headline_shape_128k(hip, oracle_lib)
 
 
@@ -350,16 +377,24 @@ def _headline_shape_128k(hip, oracle_lib):
     ref = oracle_lib.summary(k.float().numpy(), v.float().numpy(), 32)
     assert_summary_equal(summary, ref)
     qn = inp["query"][:, :, 0].float().numpy()
-    res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
-                           inp["suffix_values"].to(DEV), cfg, workspace={}, return_selected=True)
-    torch.cuda.synchronize()
     out, mask = oracle_lib.sparse_attention(qn, summ, _pages_bits(k, 32), _pages_bits(v, 32),
                                             gc.bf16_bits(inp["suffix_keys"]),
                                             gc.bf16_bits(inp["suffix_values"]), 0.01, "any")
-    assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask)
     assert 0.005 < mask.mean() < 0.1
-    assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
-                        torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+    for path in ("step", "split"):
+        hip.set_decode_path(path)
+        ws = {}
+        try:
+            res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                                   inp["suffix_values"].to(DEV), cfg, workspace=ws,
+                                   return_selected=True)
+            torch.cuda.synchronize()
+        finally:
+            hip.set_decode_path("step")
+        assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask), path
+        assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
+                            torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+        assert assert_control_clean(hip, ws) == (1 if path == "step" else 0)
     dense = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
                              inp["suffix_values"].to(DEV), RefineKVConfig(backend="hip", eps=0),
                              workspace={}, return_selected=True)
