@@ -284,6 +284,15 @@ struct Coherent {
   __device__ void store_u32(uint32_t off, uint32_t x) const {
     __builtin_amdgcn_raw_buffer_store_b32(x, r, (int)off, 0, kCoherentPolicy);
   }
+  __device__ uint64_t load_u64(uint32_t off) const {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kCoherentPolicy);
+    return (uint64_t)v[0] | ((uint64_t)v[1] << 32);
+  }
+  __device__ void store_u64(uint32_t off, uint64_t x) const {
+    typedef unsigned int U2 __attribute__((ext_vector_type(2)));
+    const U2 v = {(uint32_t)x, (uint32_t)(x >> 32)};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, (int)off, 0, kCoherentPolicy);
+  }
 };
 
 // Waits until every earlier memory access of this wave has completed (a

@@ -61,7 +61,7 @@ inline void mark(int i, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
-  int64_t control, zf, lse, part_ml, part_acc, counts, total;
+  int64_t control, zf, lse, part_ml, part_acc, counts, xbits, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -84,6 +84,7 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.part_ml = take(rows * L.tile_stride * 8);
   L.part_acc = take(rows * L.tile_stride * dim * 4);
   L.counts = take(heads * L.tile_stride * 4);
+  L.xbits = take(heads * L.tile_stride * 8);
   L.total = off;
   return L;
 }
@@ -191,18 +192,16 @@ struct ScoreArgs {
   float scale;
 };
 
-// q and bf16(q^2) are staged in LDS as fp32, each row as kLanes slices of
-// kCh values padded by 4 (so the slices the lanes of a block read start on
-// distinct banks).  When G * D <= kOwnQ each wave stages its own copy, so no
-// barrier (and no wait for the summary loads in flight) precedes the dot
-// products; larger groups share one copy.
-constexpr int kOwnQ = 1024;
+// q and bf16(q^2) are staged once per workgroup in LDS as fp32, each row as
+// kLanes slices of kCh values padded by 4 (so the slices the lanes of a block
+// read start on distinct banks).  The workgroup's threads each stage one or
+// more query word pairs, then a barrier.
 constexpr int kQPad = 4;
+constexpr int kQWords = 4;  // query words a thread loads ahead (G * D <= 2048 * 4)
 
 // Floats of LDS that stage q and bf16(q^2) for `group` rows.
 __host__ __device__ constexpr int64_t score_q_floats(int64_t group, int64_t dim) {
-  return (group * dim <= kOwnQ ? kWaves : 1) * 2 * group *
-         (dim + (dim <= 128 ? 8 : 16) * kQPad);
+  return 2 * group * (dim + (dim <= 128 ? 8 : 16) * kQPad);
 }
 
 // The most score_q_floats needs for any group up to `group`.
@@ -249,20 +248,18 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
   constexpr int CH = S::kCh;
   const int G = a.group;
   const int64_t N = a.n_blocks;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
+  const int tid = threadIdx.x;
   const int c = tid % S::kLanes, sub = tid / S::kLanes;
-  const bool own_q = G * D <= kOwnQ;
 
   constexpr int QW = CH + kQPad;          // padded slice
   constexpr int QS = S::kLanes * QW;      // padded row
-  float* qs = qstage + (own_q ? wave * 2 * G * QS : 0);  // [G][QS] bf16(q)
-  float* q2s = qs + G * QS;                                         // [G][QS] bf16(q^2)
+  float* qs = qstage;                     // [G][QS] bf16(q)
+  float* q2s = qs + G * QS;               // [G][QS] bf16(q^2)
   const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
-  const int first = own_q ? lane : tid, step = own_q ? kWave : kThreads;
+  const int first = tid, step = kThreads;
   // The query words first (the staging below waits only for them: loads
   // complete in order), then every load of the tile.  Blocks past the end
   // read block N-1 (their results are discarded).
-  constexpr int kQWords = kOwnQ / 2 / kWave;  // words per lane of a wave's own copy
   uint32_t qw[kQWords];
 #pragma unroll
   for (int k = 0; k < kQWords; ++k) {
@@ -299,11 +296,11 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
     if (i < G * D / 2) stage(i, qw[k]);
   }
   for (int i = first + kQWords * step; i < G * D / 2; i += step) stage(i, q32[i]);
-  // A wave's LDS operations complete in order, so its own copy is ready for
-  // its own reads; the shared copy needs the workgroup.
-  if (!own_q) __syncthreads();
+  __syncthreads();
 
-  for (int g0 = 0; g0 < G; g0 += 4) {
+  // Rows g0 .. g0+3: a lambda so that the common case (G <= 4, one call)
+  // waits for each pass's loads just before it, not for both passes first.
+  auto four_rows = [&](int g0) {
     // this lane's slice of q and q^2 for rows g0 .. g0+3 (clamped)
     float qv[4][CH], q2v[4][CH];
 #pragma unroll
@@ -343,6 +340,11 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
         }
       }
     }
+  };
+  if (G <= 4) {
+    four_rows(0);
+  } else {
+    for (int g0 = 0; g0 < G; g0 += 4) four_rows(g0);
   }
   __syncthreads();
 }
@@ -721,9 +723,9 @@ struct CombineShared {
 // ---------------------------------------------------------------------------
 // Counters (u64 at the start of the workspace): head h owns the 64-byte line
 // at counter kLine * h -- [0] tiles that have published their LSE partials,
-// [1] tiles that have published their attention partials; after the heads'
-// lines, a sticky u32 error word (bit 0: a wait gave up after kSpinLimit
-// polls).  The counters are never reset: every launch adds exactly n_tiles
+// [1] tiles that have published their attention partials, [2] tiles that
+// have published their expanded-block masks; after the heads' lines, a
+// sticky u32 error word (bit 0: a wait gave up after kSpinLimit polls).  The counters are never reset: every launch adds exactly n_tiles
 // to each, so a tile's own arrival (old value / n_tiles) tells it the
 // launch's epoch e and the counts it waits for, (e + 1) n_tiles.  This
 // needs the workspace zero-filled once when created and used for one shape
@@ -750,11 +752,72 @@ struct StepCtx {
   uint32_t* flag;                 // one LDS word
   unsigned long long* wsum;       // kWaves LDS words
   uint64_t* base;                 // LDS: epoch * n_tiles (thread 0's copy)
+  Coherent xbits;                 // (H, tile_stride) expanded-block masks
+  int32_t* xl;                    // LDS: blocks of this tile's expanded-row share
+  uint32_t* xr;                   // LDS: the share's first row and row count
   int heads;
   __device__ uint32_t* error() const {
     return reinterpret_cast<uint32_t*>(control + (int64_t)heads * kLine);
   }
 };
+
+// Inclusive prefix sum over the wave.
+__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
+  const int lane = threadIdx.x % kWave;
+#pragma unroll
+  for (int o = 1; o < kWave; o <<= 1) {
+    const uint32_t u = __shfl_up(v, o, kWave);
+    if (lane >= o) v += u;
+  }
+  return v;
+}
+
+// Wave 0 of a step workgroup: this tile's share of its head's expanded token
+// rows.  The head's expanded blocks, in (tile, block) order, give B rows each
+// (R rows in all); tile w attends rows [w R / T, (w + 1) R / T), so every
+// tile of the head gets the same number of rows (+-1) wherever the expanded
+// blocks sit.  From the T published masks: xl[i] = the block (index in the
+// head) of ordinal e0 + i for the ordinals the share touches, xr = (first
+// row, row count).  Integer arithmetic only: every tile sees the same split.
+__device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
+                               uint32_t tile, int lb) {
+  constexpr int kChunks = (int)(kStepMaxTiles / kWave);
+  const int lane = threadIdx.x % kWave;
+  uint64_t bm[kChunks];
+  uint32_t cnt[kChunks], first[kChunks];
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const uint32_t t = k * kWave + lane;
+    const uint32_t tc = t < T ? t : 0u;
+    const uint64_t m = k * kWave < (int)T ? sx.xbits.load_u64((uint32_t)((h * ts + tc) * 8)) : 0ull;
+    bm[k] = t < T ? m : 0ull;
+    cnt[k] = (uint32_t)__popcll(bm[k]);
+  }
+  uint32_t total = 0;
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const uint32_t incl = wave_inclusive_sum(cnt[k]);
+    first[k] = total + incl - cnt[k];
+    total += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
+  }
+  const uint64_t R = (uint64_t)total << lb;
+  const uint64_t r0 = (uint64_t)tile * R / T, r1 = ((uint64_t)tile + 1) * R / T;
+  const uint32_t e0 = (uint32_t)(r0 >> lb);
+  const uint32_t e1 = (uint32_t)((r1 + (1u << lb) - 1) >> lb);
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    const uint32_t lo = first[k] > e0 ? first[k] : e0;
+    const uint32_t end = first[k] + cnt[k];
+    const uint32_t hi = end < e1 ? end : e1;
+    const uint32_t t = k * kWave + lane;
+    for (uint32_t e = lo; e < hi; ++e)
+      sx.xl[e - e0] = (int32_t)(t * kTile + (uint32_t)nth_set_bit(bm[k], (int)(e - first[k])));
+  }
+  if (lane == 0) {
+    sx.xr[0] = (uint32_t)r0;
+    sx.xr[1] = (uint32_t)(r1 - r0);
+  }
+}
 
 constexpr int kMergeBatch = 8;  // partials per lane per batch of loads
 
@@ -784,9 +847,10 @@ __device__ __forceinline__ void merge_state4(float m2, float d2, const float4& n
 // columns, once every tile of the head has published.  Slice m: head h's
 // rows, column quads [m Q / K, (m + 1) Q / K), from every tile's partial ->
 // bf16 output; slice 0 also adds the head's access count.  Each (row, 4
-// columns) unit is merged by S adjacent lanes (S a power of two; tiles s,
-// s + S, ... each), then an xor tree over the S lanes: a fixed order, so
-// outputs repeat bit for bit.
+// columns) unit is merged by S adjacent lanes (S a power of two <= 16, so a
+// unit sits inside a 16-lane row; tiles s, s + S, ... each), then a tree
+// over the S lanes into the unit's last lane (DPP row shifts): a fixed
+// order, so outputs repeat bit for bit.
 constexpr int kMergers = 8;
 
 template <int D>
@@ -799,7 +863,7 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
   const int q0 = m * Q / K, nq = (m + 1) * Q / K - q0;
   const int units = G * nq;
   int S = 1;
-  while (S * 2 * units <= kThreads) S *= 2;
+  while (S * 2 * units <= kThreads && S < 16) S *= 2;
   for (int u0 = 0; u0 < units; u0 += kThreads / S) {
     const int u = u0 + tid / S, sl = tid % S;
     const int uc = u < units ? u : units - 1;
@@ -821,13 +885,16 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
 #pragma unroll
       for (int k = 0; k < kMergeBatch; ++k) merge_state4(ml[k].x, ml[k].y, av[k], mx, num, den);
     }
-    for (int o = 1; o < S; o <<= 1) {
-      const float m2 = shfl_xor(mx, o), d2 = shfl_xor(den, o);
-      const float4 n2 = make_float4(shfl_xor(num.x, o), shfl_xor(num.y, o), shfl_xor(num.z, o),
-                                    shfl_xor(num.w, o));
+    auto fold_from = [&](auto shift) {
+      const float m2 = shift(mx), d2 = shift(den);
+      const float4 n2 = make_float4(shift(num.x), shift(num.y), shift(num.z), shift(num.w));
       merge_state4(m2, d2, n2, mx, num, den);
-    }
-    if (sl == 0 && u < units) {
+    };
+    if (S > 8) fold_from([](float v) { return row_shr<8>(v); });
+    if (S > 4) fold_from([](float v) { return row_shr<4>(v); });
+    if (S > 2) fold_from([](float v) { return row_shr<2>(v); });
+    if (S > 1) fold_from([](float v) { return row_shr<1>(v); });
+    if (sl == S - 1 && u < units) {
       const float dn = fmaxf(den, 1e-30f);
       const uint32_t lo = (uint32_t)bf16_rne(num.x / dn) | ((uint32_t)bf16_rne(num.y / dn) << 16);
       const uint32_t hi = (uint32_t)bf16_rne(num.z / dn) | ((uint32_t)bf16_rne(num.w / dn) << 16);
@@ -976,6 +1043,15 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   uint32_t count = 0;
   const uint64_t bits = decide_finish<kFused>(da, h, tile, din, dsh, nullptr, list, count,
                                               kFused ? &sx->stats : nullptr);
+  if constexpr (kFused) {
+    // publish the expanded blocks for the head's even split of token rows
+    if (tid == 0) {
+      sx->xbits.store_u64((uint32_t)((h * da.tile_stride + tile) * 8), bits);
+      wait_memory();
+      __hip_atomic_fetch_add(sx->control + h * kLine + 2, 1ull, __ATOMIC_RELAXED,
+                             __HIP_MEMORY_SCOPE_AGENT);
+    }
+  }
 
   // take the expanded blocks' representatives out again
   if ((bits >> lg) & 0x0001000100010001ull) {
@@ -1008,13 +1084,33 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     fold_tokens<D, GBM>(st, q, kr, vr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
   }
 
+  // ---- expanded token rows this workgroup attends ------------------------
+  // Three kernels: its own tile's.  One-launch step: an even share of the
+  // head's (once every tile of the head has published its mask).  Rows x_first
+  // .. x_first + x_rows of the expanded rows in block order; xl lists the
+  // blocks (offset by blk_base) of the block ordinals from x_first / B on.
+  const int32_t* xl = list;
+  uint32_t blk_base = tile * kTile, x_first = 0, x_rows = (uint32_t)__popcll(bits) * B;
+  if constexpr (kFused) {
+    if (tid == 0)
+      wait_counter<uint64_t>(sx->control + h * kLine + 2, *sx->base + T, kSpinLimit, sx->error());
+    __syncthreads();
+    if (tid < kWave) expanded_share(*sx, h, da.tile_stride, T, tile, (int)lb);
+    __syncthreads();
+    xl = sx->xl;
+    blk_base = 0;
+    x_first = sx->xr[0];
+    x_rows = sx->xr[1];
+  }
+
   // ---- token rows after the prefetched ones ------------------------------
-  // Row v: the rest of the suffix slice first, then the expanded blocks'
-  // tokens in block order.  Points kp / vp at the row (a valid row when it
-  // is masked) and returns whether it is live.
+  // Row v: the rest of the suffix slice first, then the expanded rows.
+  // Points kp / vp at the row (a valid row when it is masked) and returns
+  // whether it is live.
   const uint32_t n_rest = n_suffix - n_pre;
-  const uint32_t n_rows = n_rest + (uint32_t)__popcll(bits) * B;
+  const uint32_t n_rows = n_rest + x_rows;
   const uint32_t last = N - 1, last_count = L - last * B;
+  const uint32_t e_first = x_first >> lb;
   auto row = [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) -> bool {
     kp = kbase;
     vp = vbase;
@@ -1025,9 +1121,9 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       vp = vs + t * vts;
       return true;
     }
-    const uint32_t w = v - n_rest;
-    const uint32_t t = w & (B - 1);
-    const uint32_t bb = tile * kTile + (uint32_t)list[w >> lb];
+    const uint32_t r = x_first + (v - n_rest);
+    const uint32_t t = r & (B - 1);
+    const uint32_t bb = blk_base + (uint32_t)xl[(r >> lb) - e_first];
     const uint32_t off = ((bb << lb) + t) * (uint32_t)D;
     kp = kbase + off;
     vp = vbase + off;
@@ -1147,7 +1243,8 @@ struct StepArgs {
   uint32_t* counts;               // (H, tile_stride) tile access counts
   uint16_t* out;                  // (H, G, D) bf16
   unsigned long long* accessed;   // or null
-  uint32_t lse_bytes, ml_bytes, acc_bytes, counts_bytes;
+  uint64_t* xbits;                // (H, tile_stride) expanded-block masks
+  uint32_t lse_bytes, ml_bytes, acc_bytes, counts_bytes, xbits_bytes;
   int heads;
 };
 
@@ -1158,6 +1255,8 @@ struct StepShared {
   alignas(16) float4 zs[GBM][kTile];  // z, delta, A, th of the tile's (row, block) pairs
   alignas(16) float mts[GBM];         // the tile's max z per row
   alignas(16) unsigned long long wsum[kWaves];
+  alignas(16) int32_t xl[kTile + 4];
+  uint32_t xr[2];
   uint64_t base;
   alignas(16) DecideShared dec;
   alignas(16) union {
@@ -1194,6 +1293,9 @@ void step_kernel(StepArgs s) {
                    &sh.flag,
                    sh.wsum,
                    &sh.base,
+                   Coherent(s.xbits, s.xbits_bytes),
+                   sh.xl,
+                   sh.xr,
                    s.heads};
   score_dots<D>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
   score_stats(
@@ -1543,6 +1645,8 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) 
   s.ml_bytes = (uint32_t)(hg * ts * 8);
   s.acc_bytes = (uint32_t)(hg * ts * p.dim * 4);
   s.counts_bytes = (uint32_t)(p.heads * ts * 4);
+  s.xbits = at<uint64_t>(p.ws, L.xbits);
+  s.xbits_bytes = (uint32_t)(p.heads * ts * 8);
   s.heads = (int)p.heads;
   const int64_t rows = rows_per_pass(p.group, p.dim);
   mark(0, p.stream);
@@ -1589,17 +1693,17 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 
 // Byte offsets of the workspace regions, for tests: control (hand-off
 // counters), zf (z, delta, A, th per row and block), lse, part_ml, part_acc,
-// counts, total, then n_tiles, the row stride (blocks) of zf and of the
-// per-tile arrays.
+// counts, xbits (per-tile expanded-block masks), total, then n_tiles, the row
+// stride (blocks) of zf and of the per-tile arrays.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out10) {
+                                    int64_t* out11) {
   clear_error();
-  if (!out10 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out11 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[10] = {L.control, L.zf,    L.lse,     L.part_ml, L.part_acc,
-                         L.counts,  L.total, L.n_tiles, L.z_stride, L.tile_stride};
-  for (int i = 0; i < 10; ++i) out10[i] = v[i];
+  const int64_t v[11] = {L.control, L.zf,    L.lse,     L.part_ml, L.part_acc,   L.counts,
+                         L.xbits,   L.total, L.n_tiles, L.z_stride, L.tile_stride};
+  for (int i = 0; i < 11; ++i) out11[i] = v[i];
   return kOk;
 }
 

@@ -57,7 +57,7 @@ def test_workspace_size_covers_layout(lib):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
-        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:7]]
+        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:8]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
         rows, tiles, ts = heads * group, layout["n_tiles"], layout["tile_stride"]
         # hand-off counters first: one 64-byte line per KV head and one more
@@ -68,5 +68,6 @@ def test_workspace_size_covers_layout(lib):
         assert layout["part_ml"] - layout["lse"] >= rows * ts * 16
         assert layout["part_acc"] - layout["part_ml"] >= rows * ts * 8
         assert layout["counts"] - layout["part_acc"] >= rows * ts * dim * 4
-        assert layout["total"] - layout["counts"] >= heads * ts * 4
+        assert layout["xbits"] - layout["counts"] >= heads * ts * 4
+        assert layout["total"] - layout["xbits"] >= heads * ts * 8
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0

@@ -39,16 +39,17 @@ def decode_path(hip, request):
 
 
 def assert_control_clean(hip, ws):
-    """After every launch each head's two hand-off counters (tiles arrived,
-    tiles merged) are equal multiples of n_tiles -- a whole number of
+    """After every launch each head's hand-off counters (tiles arrived,
+    merged, decided) are equal multiples of n_tiles -- a whole number of
     launches -- and no hand-off wait gave up.  Returns the launch count."""
     heads, group, dim, n = ws["hip_scratch_shape"]
     tiles = hip.workspace_layout(heads, group, dim, n)["n_tiles"]
     lines = ws["hip_scratch"][:(heads + 1) * 64].view(torch.int64).cpu().numpy()
     lines = lines.reshape(heads + 1, 8)
     assert lines[heads, 0] & 0xFFFFFFFF == 0, "a hand-off wait gave up"
-    arrived, merged = lines[:heads, 0], lines[:heads, 1]
-    assert np.array_equal(arrived, merged) and not (arrived % tiles).any(), (arrived, merged)
+    arrived, merged, decided = lines[:heads, 0], lines[:heads, 1], lines[:heads, 2]
+    assert np.array_equal(arrived, merged) and np.array_equal(arrived, decided), lines[:heads]
+    assert not (arrived % tiles).any(), arrived
     assert np.all(arrived == arrived[0]), arrived
     return int(arrived[0]) // tiles
 
@@ -233,6 +234,9 @@ DECODE_CASES = [
         (8, 4, 128, 32, 4096, "mean", 1e6, 0.02),  # none expanded
         (2, 2, 256, 32, 1500, "any", 0.01, 0.05),
         (2, 4, 224, 16, 700, "max", 0.01, 0.05),
+        # few (row, column) units per merge slice: 1-2 query rows, short rows
+        (2, 1, 64, 16, 9000, "any", 0.01, 0.05),
+        (1, 2, 32, 16, 8200, "max", 0.01, 0.05),
     ]
 ]
 
