@@ -68,18 +68,18 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
 /* Byte offsets inside the workspace (for tests): control (hand-off
- * counters: one 64-byte line per KV head -- u64 tiles arrived, tiles
- * merged and tiles decided, summed over calls -- then a line starting with a
- * sticky u32 error
- * word, bit 0 set if a hand-off wait gave up), zf (float4 z,
- * delta, A, th per query row and block: the selection statistics and the
- * delta-only factors of the risk), lse (per-tile log-sum-exp partials),
- * part_ml, part_acc (per-tile attention partials: (m, l) and acc), counts
- * (per-tile access counts), xbits (per-tile expanded-block masks), total,
- * then n_tiles and the padded row strides (elements) of zf and of the
- * per-tile arrays -> out11[0..10]. */
+ * counters: one 64-byte line per KV head -- u64 tiles merged, summed over
+ * calls -- then a line starting with a sticky u32 error word, bit 0 set if a
+ * hand-off wait gave up, then a u64 call count per tile), zf (float4 z, delta, A, th
+ * per query row and block: the selection statistics and the delta-only
+ * factors of the risk), lse (per-tile log-sum-exp partials), lse_slots (the
+ * same as tagged 16-byte slots for the one-launch step), part_ml, part_acc
+ * (per-tile attention partials: (m, l) and acc), counts (per-tile access
+ * counts), xbits (per-tile expanded-block masks, tagged slots), total, then
+ * n_tiles and the padded row strides (elements) of zf and of the per-tile
+ * arrays -> out12[0..11]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out11);
+                         int64_t* out12);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton

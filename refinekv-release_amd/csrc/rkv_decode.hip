@@ -40,11 +40,13 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsPerWave = kMaxGroup / kWaves;  // query rows a wave owns in a tile
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr int kLine = 8;  // u64 counters per 64-byte hand-off line
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a hand-off wait gives up
+constexpr int64_t kStepMaxTiles = 256;     // tiles per head the one-launch step takes
 
-// Bytes of the one-launch step's hand-off counters: one line per KV head
-// and one for the launch.
-__host__ __device__ constexpr int64_t control_bytes(int64_t heads) {
-  return (heads + 1) * kLine * 8;
+// Bytes of the one-launch step's hand-off counters: one line per KV head,
+// one for the launch, then one launch counter per tile.
+__host__ __device__ constexpr int64_t control_bytes(int64_t heads, int64_t tile_stride) {
+  return (heads + 1) * kLine * 8 + heads * tile_stride * 8;
 }
 
 // Optional profiling events (rkv_set_profile_events): events[0] is recorded
@@ -61,7 +63,7 @@ inline void mark(int i, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
-  int64_t control, zf, lse, part_ml, part_acc, counts, xbits, total;
+  int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, xbits, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -78,13 +80,14 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
     off = align256(off + bytes);
     return at;
   };
-  L.control = take(control_bytes(heads));
+  L.control = take(control_bytes(heads, L.tile_stride));
   L.zf = take(rows * L.z_stride * 16);
   L.lse = take(rows * L.tile_stride * 4 * 4);
+  L.lse_slots = take(rows * L.tile_stride * 2 * 16);
   L.part_ml = take(rows * L.tile_stride * 8);
   L.part_acc = take(rows * L.tile_stride * dim * 4);
   L.counts = take(heads * L.tile_stride * 4);
-  L.xbits = take(heads * L.tile_stride * 8);
+  L.xbits = take(heads * L.tile_stride * 16);
   L.total = off;
   return L;
 }
@@ -495,13 +498,98 @@ __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t
   return d;
 }
 
+// Self-validating hand-off slots of the one-launch step: 16 bytes {a, b,
+// tag, check(a, b, tag)} written with one coherent store, tag = the launch's
+// epoch + 1 (a zero-filled slot is never valid).  A reader accepts a slot
+// only when it carries this launch's tag and a matching check, so it needs
+// no counter to know that the data has landed, and a stale or torn read is
+// simply read again.
+__host__ __device__ inline uint32_t slot_check(uint32_t a, uint32_t b, uint32_t tag) {
+  uint32_t x = (a * 0x9E3779B1u) ^ ((b + 0x7F4A7C15u) * 0x85EBCA77u) ^ (tag * 0xC2B2AE3Du);
+  x ^= x >> 15;
+  x *= 0x2C1B3C6Du;
+  x ^= x >> 12;
+  x *= 0x297A2D39u;
+  x ^= x >> 15;
+  return x;
+}
+
+__device__ __forceinline__ float4 make_slot(uint32_t a, uint32_t b, uint32_t tag) {
+  return make_float4(bits_f32(a), bits_f32(b), bits_f32(tag), bits_f32(slot_check(a, b, tag)));
+}
+
+__device__ __forceinline__ bool slot_ok(float4 s, uint32_t tag) {
+  const uint32_t t = f32_bits(s.z);
+  return t == tag && f32_bits(s.w) == slot_check(f32_bits(s.x), f32_bits(s.y), t);
+}
+
+constexpr int kChunks = (int)(kStepMaxTiles / kWave);  // tiles per lane, at most
+
 // Where the one-launch step keeps what the separate kernels pass through
-// the workspace: the tile's (z, delta, A, th) in LDS and the LSE partials
-// behind coherent accesses.
+// the workspace: the tile's (z, delta, A, th) in LDS and the LSE partials in
+// tagged slots (two per row and tile: (zm, zl) and (cm, cl)).
 struct StepStats {
   const float4 (*zs)[kTile];  // [row][block of the tile]
-  Coherent lse;               // the workspace's lse region
+  Coherent slots;             // (H*G, tile_stride, 2) tagged slots
+  const uint32_t* tag;        // LDS: this launch's tag
+  uint32_t* error;
 };
+
+// One row's LSE partials of the head's T tiles (lane t holds tiles t + 64 k)
+// from the tagged slots, read until every slot carries this launch's tag
+// (at most kSpinLimit rounds, then the error word is set).
+struct RowLse {
+  float zm[kChunks], zl[kChunks], cm[kChunks], cl[kChunks];
+};
+
+__device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, uint32_t T,
+                                             int lane) {
+  RowLse r;
+  const uint32_t tag = *ss.tag;
+  for (uint32_t n = 0;; ++n) {
+    bool ok = true;
+#pragma unroll
+    for (int k = 0; k < kChunks; ++k) {
+      const uint32_t t = k * kWave + lane;
+      const bool live = t < T;
+      float4 a = make_float4(kNegInf, 0.0f, 0.0f, 0.0f), b = a;
+      if (k * kWave < (int)T) {
+        const uint32_t at = (uint32_t)((row + (live ? t : 0u)) * 2);
+        a = ss.slots.load4(at * 16);
+        b = ss.slots.load4(at * 16 + 16);
+        ok = ok && (!live || (slot_ok(a, tag) && slot_ok(b, tag)));
+      }
+      r.zm[k] = live ? a.x : kNegInf;
+      r.zl[k] = live ? a.y : 0.0f;
+      r.cm[k] = live ? b.x : kNegInf;
+      r.cl[k] = live ? b.y : 0.0f;
+    }
+    if (__ballot(!ok) == 0) break;
+    if (n + 1 >= kSpinLimit) {
+      if (lane == 0) __hip_atomic_fetch_or(ss.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+  return r;
+}
+
+// merge_lse over partials held per lane (tiles lane + 64 k; tiles past T
+// hold m = -inf, l = 0): the same fixed order.
+__device__ __forceinline__ float merge_lse_chunks(const float (&m)[kChunks],
+                                                  const float (&l)[kChunks], uint32_t T,
+                                                  int lane) {
+  float mx = m[0];
+#pragma unroll
+  for (int k = 1; k < kChunks; ++k) mx = nanmax(mx, m[k]);
+  mx = wave_nanmax_u(mx);
+  const float ms = inf_to_zero(mx);
+  float acc = (uint32_t)lane < T ? l[0] * expf_(m[0] - ms) : 0.0f;
+#pragma unroll
+  for (int k = 1; k < kChunks; ++k)
+    if ((uint32_t)(k * kWave + lane) < T) acc = acc + l[k] * expf_(m[k] - ms);
+  return logf_(wave_sum_u(acc)) + ms;
+}
 
 template <bool kFused = false>
 __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
@@ -524,19 +612,7 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   // ---- log Z, log C of each row this wave owns, then its risks ----------
   uint64_t wsel = 0;
   bool wbad = false;
-  auto row_stats = [&](int g, float4 part, float4 zf) {
-    const int64_t row = (h * G + g) * a.tile_stride;
-    auto tile_part = [&](int64_t t, int which) -> float2 {
-      if constexpr (kFused) {
-        return ss->lse.load2((uint32_t)(((row + t) * 4 + 2 * which) * 4));
-      } else {
-        const float* p = a.lse + (row + t) * 4 + 2 * which;
-        return make_float2(p[0], p[1]);
-      }
-    };
-    if (lane >= T) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
-    const float lz = merge_lse(part.x, part.y, [&](int64_t t) { return tile_part(t, 0); }, T, lane);
-    const float lc = merge_lse(part.z, part.w, [&](int64_t t) { return tile_part(t, 1); }, T, lane);
+  auto row_tail = [&](int g, float lz, float lc, float4 zf) {
     if (a.stats_out && owner && tile == 0 && lane == 0) {
       a.stats_out[(h * G + g) * 2] = lz;
       a.stats_out[(h * G + g) * 2 + 1] = lc;
@@ -551,15 +627,29 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
     sh.risk[g][lane] = r;
     if (zsh) zsh[g][lane] = valid ? zf.x : kNegInf;
   };
-  // the first row from the loads already made, further rows (groups above
-  // four) with their own loads
-  if (wave < G) row_stats(wave, in.part, in.zf);
+  if constexpr (kFused) {
+    // every row from the head's tagged slots (read until all have landed)
 #pragma unroll 1
-  for (int g = wave + kWaves; g < G; g += kWaves) {
-    const int64_t at = (h * G + g) * a.tile_stride + tl;
-    if constexpr (kFused) {
-      row_stats(g, ss->lse.load4((uint32_t)(at * 16)), ss->zs[g][lane]);
-    } else {
+    for (int g = wave; g < G; g += kWaves) {
+      const RowLse rl = gather_lse(*ss, (h * G + g) * a.tile_stride, (uint32_t)T, lane);
+      row_tail(g, merge_lse_chunks(rl.zm, rl.zl, (uint32_t)T, lane),
+               merge_lse_chunks(rl.cm, rl.cl, (uint32_t)T, lane), ss->zs[g][lane]);
+    }
+  } else {
+    auto row_stats = [&](int g, float4 part, float4 zf) {
+      const float* prow = a.lse + (h * G + g) * a.tile_stride * 4;
+      if (lane >= T) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
+      auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
+      auto pc = [&](int64_t t) { return make_float2(prow[t * 4 + 2], prow[t * 4 + 3]); };
+      row_tail(g, merge_lse(part.x, part.y, pz, T, lane), merge_lse(part.z, part.w, pc, T, lane),
+               zf);
+    };
+    // the first row from the loads already made, further rows (groups above
+    // four) with their own loads
+    if (wave < G) row_stats(wave, in.part, in.zf);
+#pragma unroll 1
+    for (int g = wave + kWaves; g < G; g += kWaves) {
+      const int64_t at = (h * G + g) * a.tile_stride + tl;
       row_stats(g, *reinterpret_cast<const float4*>(a.lse + at * 4),
                 a.zf[(h * G + g) * a.z_stride + bc]);
     }
@@ -721,26 +811,25 @@ struct CombineShared {
 // ---------------------------------------------------------------------------
 // One-launch step: hand-off counters and the merge of a head by its last tile
 // ---------------------------------------------------------------------------
-// Counters (u64 at the start of the workspace): head h owns the 64-byte line
-// at counter kLine * h -- [0] tiles that have published their LSE partials,
-// [1] tiles that have published their attention partials, [2] tiles that
-// have published their expanded-block masks; after the heads' lines, a
-// sticky u32 error word (bit 0: a wait gave up after kSpinLimit polls).  The counters are never reset: every launch adds exactly n_tiles
-// to each, so a tile's own arrival (old value / n_tiles) tells it the
-// launch's epoch e and the counts it waits for, (e + 1) n_tiles.  This
-// needs the workspace zero-filled once when created and used for one shape
-// (one n_tiles) thereafter.
+// Hand-offs between the tiles of a head.  Counters (u64 at the start of
+// the workspace): head h owns the 64-byte line at counter kLine * h, whose
+// [1] counts tiles that have published their attention partials; after the
+// heads' lines, a sticky u32 error word (bit 0: a wait gave up after
+// kSpinLimit polls); then one launch counter per tile.  Nothing is reset:
+// each launch adds one to every tile's counter and n_tiles to each head's,
+// so a tile's own counter (old value) is the launch's epoch e, e + 1 tags
+// the slots it publishes (LSE partials, expanded-block masks: readers poll
+// the slots themselves) and (e + 1) n_tiles is the merge count it waits
+// for.  This needs the workspace zero-filled once when created and used for
+// one shape thereafter.
 //
-// Progress: a tile waits only for the tiles of its own head, and waits only
-// after publishing its own partials.  Workgroups are dispatched in
+// Progress: a tile waits only for the tiles of its own head, and only after
+// publishing what they wait for from it.  Workgroups are dispatched in
 // blockIdx order (x fastest, so a head's tiles are consecutive); with at
 // least n_tiles workgroups resident at once (the host allows this path only
-// for n_tiles <= kStepMaxTiles, one workgroup per CU), the lowest head
-// still waiting has all of its tiles dispatched, so its wait ends.  A wait
-// that does not end within kSpinLimit polls records an error instead of
-// hanging.
-constexpr uint32_t kSpinLimit = 1u << 20;
-constexpr int64_t kStepMaxTiles = 256;
+// for n_tiles <= kStepMaxTiles, one workgroup per CU), the lowest head still
+// waiting has all of its tiles dispatched, so its wait ends.  A wait that
+// does not end within kSpinLimit polls records an error instead of hanging.
 
 struct StepCtx {
   StepStats stats;
@@ -772,27 +861,45 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
   return v;
 }
 
-// Wave 0 of a step workgroup: this tile's share of its head's expanded token
-// rows.  The head's expanded blocks, in (tile, block) order, give B rows each
-// (R rows in all); tile w attends rows [w R / T, (w + 1) R / T), so every
-// tile of the head gets the same number of rows (+-1) wherever the expanded
-// blocks sit.  From the T published masks: xl[i] = the block (index in the
-// head) of ordinal e0 + i for the ordinals the share touches, xr = (first
-// row, row count).  Integer arithmetic only: every tile sees the same split.
+// Wave 0 of a step workgroup: this tile's share of its head's expanded
+// token rows.  The head's expanded blocks, in (tile, block) order, give B
+// rows each (R rows in all) and tile w attends rows [w R / T, (w + 1) R / T),
+// so every tile of the head gets the same number of rows (+-1) wherever the
+// expanded blocks sit.  From the T published masks: xl[i] = the block (index
+// in the head) of ordinal e0 + i for the ordinals the share touches, xr =
+// (first row, row count).  Integer arithmetic only: every tile sees the same
+// split.
 __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
                                uint32_t tile, int lb) {
-  constexpr int kChunks = (int)(kStepMaxTiles / kWave);
   const int lane = threadIdx.x % kWave;
+  const uint32_t tag = *sx.stats.tag;
   uint64_t bm[kChunks];
   uint32_t cnt[kChunks], first[kChunks];
+  // the head's tagged masks, read until every one has landed
+  for (uint32_t n = 0;; ++n) {
+    bool ok = true;
 #pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
-    const uint32_t t = k * kWave + lane;
-    const uint32_t tc = t < T ? t : 0u;
-    const uint64_t m = k * kWave < (int)T ? sx.xbits.load_u64((uint32_t)((h * ts + tc) * 8)) : 0ull;
-    bm[k] = t < T ? m : 0ull;
-    cnt[k] = (uint32_t)__popcll(bm[k]);
+    for (int k = 0; k < kChunks; ++k) {
+      const uint32_t t = k * kWave + lane;
+      bm[k] = 0ull;
+      if (k * kWave < (int)T) {
+        const float4 v = sx.xbits.load4((uint32_t)((h * ts + (t < T ? t : 0u)) * 16));
+        if (t < T) {
+          ok = ok && slot_ok(v, tag);
+          bm[k] = (uint64_t)f32_bits(v.x) | ((uint64_t)f32_bits(v.y) << 32);
+        }
+      }
+    }
+    if (__ballot(!ok) == 0) break;
+    if (n + 1 >= kSpinLimit) {
+      if (lane == 0)
+        __hip_atomic_fetch_or(sx.stats.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
   }
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) cnt[k] = (uint32_t)__popcll(bm[k]);
   uint32_t total = 0;
 #pragma unroll
   for (int k = 0; k < kChunks; ++k) {
@@ -811,7 +918,8 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
     const uint32_t hi = end < e1 ? end : e1;
     const uint32_t t = k * kWave + lane;
     for (uint32_t e = lo; e < hi; ++e)
-      sx.xl[e - e0] = (int32_t)(t * kTile + (uint32_t)nth_set_bit(bm[k], (int)(e - first[k])));
+      sx.xl[e - e0] =
+          (int32_t)(t * kTile + (uint32_t)nth_set_bit(bm[k], (int)(e - first[k])));
   }
   if (lane == 0) {
     sx.xr[0] = (uint32_t)r0;
@@ -1027,30 +1135,17 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       }
     }
   }
-  // ---- the decision -------------------------------------------------------
-  if constexpr (kFused) {
-    // every tile of the head has published its LSE partials
-    if (tid == 0)
-      wait_counter<uint64_t>(sx->control + h * kLine, *sx->base + T, kSpinLimit, sx->error());
-    __syncthreads();
-    const int wave = tid / kWave, lane = tid % kWave;
-    const int gl = wave < G ? wave : G - 1;
-    const uint32_t tl = (uint32_t)lane < T ? (uint32_t)lane : 0u;
-    din.part = sx->stats.lse.load4((uint32_t)(((h * G + gl) * da.tile_stride + tl) * 16));
-    din.zf = sx->stats.zs[gl][lane];
-  }
+  // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
   const int32_t* list;
   uint32_t count = 0;
   const uint64_t bits = decide_finish<kFused>(da, h, tile, din, dsh, nullptr, list, count,
                                               kFused ? &sx->stats : nullptr);
   if constexpr (kFused) {
-    // publish the expanded blocks for the head's even split of token rows
-    if (tid == 0) {
-      sx->xbits.store_u64((uint32_t)((h * da.tile_stride + tile) * 8), bits);
-      wait_memory();
-      __hip_atomic_fetch_add(sx->control + h * kLine + 2, 1ull, __ATOMIC_RELAXED,
-                             __HIP_MEMORY_SCOPE_AGENT);
-    }
+    // publish the expanded blocks (a tagged slot) for the head's even split
+    // of pooled token rows
+    if (tid == 0)
+      sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
+                       make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
   }
 
   // take the expanded blocks' representatives out again
@@ -1084,63 +1179,24 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     fold_tokens<D, GBM>(st, q, kr, vr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
   }
 
-  // ---- expanded token rows this workgroup attends ------------------------
-  // Three kernels: its own tile's.  One-launch step: an even share of the
-  // head's (once every tile of the head has published its mask).  Rows x_first
-  // .. x_first + x_rows of the expanded rows in block order; xl lists the
-  // blocks (offset by blk_base) of the block ordinals from x_first / B on.
-  const int32_t* xl = list;
-  uint32_t blk_base = tile * kTile, x_first = 0, x_rows = (uint32_t)__popcll(bits) * B;
-  if constexpr (kFused) {
-    if (tid == 0)
-      wait_counter<uint64_t>(sx->control + h * kLine + 2, *sx->base + T, kSpinLimit, sx->error());
-    __syncthreads();
-    if (tid < kWave) expanded_share(*sx, h, da.tile_stride, T, tile, (int)lb);
-    __syncthreads();
-    xl = sx->xl;
-    blk_base = 0;
-    x_first = sx->xr[0];
-    x_rows = sx->xr[1];
-  }
-
-  // ---- token rows after the prefetched ones ------------------------------
-  // Row v: the rest of the suffix slice first, then the expanded rows.
-  // Points kp / vp at the row (a valid row when it is masked) and returns
-  // whether it is live.
-  const uint32_t n_rest = n_suffix - n_pre;
-  const uint32_t n_rows = n_rest + x_rows;
-  const uint32_t last = N - 1, last_count = L - last * B;
-  const uint32_t e_first = x_first >> lb;
-  auto row = [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) -> bool {
-    kp = kbase;
-    vp = vbase;
-    if (v >= n_rows) return false;
-    if (v < n_rest) {
-      const uint64_t t = tile + (n_pre + v) * T;
-      kp = ks + t * kts;
-      vp = vs + t * vts;
-      return true;
-    }
-    const uint32_t r = x_first + (v - n_rest);
-    const uint32_t t = r & (B - 1);
-    const uint32_t bb = blk_base + (uint32_t)xl[(r >> lb) - e_first];
-    const uint32_t off = ((bb << lb) + t) * (uint32_t)D;
-    kp = kbase + off;
-    vp = vbase + off;
-    return bb != last || t < last_count;
-  };
-  auto issue = [&](uint32_t batch, RawBf16<CH> (&kr)[R], RawBf16<CH> (&vr)[R]) {
-    uint32_t ok = 0;
+  // ---- token rows ---------------------------------------------------------
+  // Runs n_rows rows through the online softmax, 16 R rows per batch, two
+  // batches in flight; row(v, kp, vp) points kp / vp at row v (a valid row
+  // when it is masked) and returns whether it is live.
+  auto run_rows = [&](uint32_t n_rows, auto row) {
+    if (n_rows == 0) return;
+    auto issue = [&](uint32_t batch, RawBf16<CH> (&kr)[R], RawBf16<CH> (&vr)[R]) {
+      uint32_t ok = 0;
 #pragma unroll
-    for (int u = 0; u < R; ++u) {
-      const uint16_t *kp, *vp;
-      if (row(batch * 16 * R + lg + 16 * u, kp, vp)) ok |= 1u << u;
-      kr[u] = load_raw<CH>(kp + c * CH);
-      vr[u] = load_raw<CH>(vp + c * CH);
-    }
-    return ok;
-  };
-  if (n_rows > 0) {
+      for (int u = 0; u < R; ++u) {
+        const uint16_t *kp = kbase, *vp = vbase;
+        const uint32_t v = batch * 16 * R + lg + 16 * u;
+        if (v < n_rows && row(v, kp, vp)) ok |= 1u << u;
+        kr[u] = load_raw<CH>(kp + c * CH);
+        vr[u] = load_raw<CH>(vp + c * CH);
+      }
+      return ok;
+    };
     RawBf16<CH> ka[R], va[R], kb[R], vb[R];
     uint32_t oka = issue(0, ka, va);
     uint32_t okb = issue(1, kb, vb);
@@ -1152,6 +1208,43 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       fold_tokens<D, GBM>(st, q, kb, vb, okb, a.scale, gn);
       okb = issue(k + 3, kb, vb);
     }
+  };
+  const uint32_t last = N - 1, last_count = L - last * B;
+  // the row of token t of block bb of the head's pages
+  auto page_row = [&](uint32_t bb, uint32_t t, const uint16_t*& kp, const uint16_t*& vp) {
+    const uint32_t off = ((bb << lb) + t) * (uint32_t)D;
+    kp = kbase + off;
+    vp = vbase + off;
+    return bb != last || t < last_count;
+  };
+
+  // ---- first: the rest of the suffix slice and, with three kernels, this
+  // tile's own expanded blocks (the one-launch step splits the head's
+  // expanded rows evenly over its tiles instead, below).
+  const uint32_t n_rest = n_suffix - n_pre;
+  const uint32_t own_rows = kFused ? 0u : (uint32_t)__popcll(bits) * B;
+  run_rows(n_rest + own_rows, [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) {
+    if (v < n_rest) {
+      const uint64_t t = tile + (n_pre + v) * T;
+      kp = ks + t * kts;
+      vp = vs + t * vts;
+      return true;
+    }
+    const uint32_t w = v - n_rest;
+    return page_row(tile * kTile + (uint32_t)list[w >> lb], w & (B - 1), kp, vp);
+  });
+
+  // ---- then (one-launch step): this tile's share of the head's expanded
+  // rows, once every tile of the head has published its mask ---------------
+  if constexpr (kFused) {
+    if (tid < kWave) expanded_share(*sx, h, da.tile_stride, T, tile, (int)lb);
+    __syncthreads();
+    const int32_t* xl = sx->xl;
+    const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
+    run_rows(sx->xr[1], [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) {
+      const uint32_t r = x_first + v;
+      return page_row((uint32_t)xl[(r >> lb) - e_first], r & (B - 1), kp, vp);
+    });
   }
 
   // ---- the 16 lane groups -> one partial per query row, through LDS ------
@@ -1243,8 +1336,9 @@ struct StepArgs {
   uint32_t* counts;               // (H, tile_stride) tile access counts
   uint16_t* out;                  // (H, G, D) bf16
   unsigned long long* accessed;   // or null
-  uint64_t* xbits;                // (H, tile_stride) expanded-block masks
-  uint32_t lse_bytes, ml_bytes, acc_bytes, counts_bytes, xbits_bytes;
+  float4* lse_slots;              // (H*G, tile_stride, 2) tagged LSE slots
+  float4* xbits;                  // (H, tile_stride) tagged expanded-block masks
+  uint32_t slots_bytes, ml_bytes, acc_bytes, counts_bytes, xbits_bytes;
   int heads;
 };
 
@@ -1258,6 +1352,7 @@ struct StepShared {
   alignas(16) int32_t xl[kTile + 4];
   uint32_t xr[2];
   uint64_t base;
+  uint32_t tag;
   alignas(16) DecideShared dec;
   alignas(16) union {
     struct {
@@ -1282,7 +1377,8 @@ void step_kernel(StepArgs s) {
   const ScoreArgs& sa = s.score;
   const int64_t h = blockIdx.y, tile = blockIdx.x;
   const int G = sa.group, tid = threadIdx.x, lane = tid % kWave;
-  const StepCtx sx{StepStats{sh.zs, Coherent(sa.lse, s.lse_bytes)},
+  const StepCtx sx{StepStats{sh.zs, Coherent(s.lse_slots, s.slots_bytes), &sh.tag,
+                             reinterpret_cast<uint32_t*>(s.control + (int64_t)s.heads * kLine)},
                    sh.mts,
                    Coherent(s.attend.part_ml, s.ml_bytes),
                    Coherent(s.attend.part_acc, s.acc_bytes),
@@ -1297,22 +1393,29 @@ void step_kernel(StepArgs s) {
                    sh.xl,
                    sh.xr,
                    s.heads};
+  // this launch's epoch, from the tile's own launch counter: its tag marks
+  // the slots the launch publishes
+  uint64_t epoch = 0;
+  if (tid == 0)
+    epoch = __hip_atomic_fetch_add(
+        s.control + ((int64_t)s.heads + 1) * kLine + h * sa.tile_stride + tile, 1ull,
+        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   score_dots<D>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+  if (tid == 0) {
+    sh.base = epoch * (uint64_t)s.attend.decide.n_tiles;
+    sh.tag = (uint32_t)epoch + 1u;
+  }
+  __syncthreads();
   score_stats(
       sa, tile, sh.u.score.sdot, sh.u.score.pdot,
       [&](int g, bool, float4 zf) { sh.zs[g][lane] = zf; },
       [&](int g, float4 part) {
         sh.mts[g] = part.x;
-        sx.stats.lse.store4((uint32_t)(((h * G + g) * sa.tile_stride + tile) * 16), part);
+        const uint32_t at = (uint32_t)(((h * G + g) * sa.tile_stride + tile) * 2 * 16);
+        sx.stats.slots.store4(at, make_slot(f32_bits(part.x), f32_bits(part.y), sh.tag));
+        sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
       });
-  wait_memory();
   __syncthreads();
-  if (tid == 0) {
-    const uint64_t T = (uint64_t)s.attend.decide.n_tiles;
-    const uint64_t old = __hip_atomic_fetch_add(s.control + h * kLine, 1ull, __ATOMIC_RELAXED,
-                                                __HIP_MEMORY_SCOPE_AGENT);
-    sh.base = old - old % T;  // this launch's epoch * n_tiles
-  }
   attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx);
 }
 
@@ -1627,7 +1730,7 @@ bool step_fits(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const int64_t rows = rows_per_pass(p.group, p.dim);
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
   const int64_t limit = int64_t(1) << 31;
-  return p.group <= rows && L.n_tiles <= kStepMaxTiles && hg * ts * 16 < limit &&
+  return p.group <= rows && L.n_tiles <= kStepMaxTiles && hg * ts * 32 < limit &&
          hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8);
 }
 
@@ -1641,12 +1744,13 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) 
   s.out = static_cast<uint16_t*>(b.output);
   s.accessed = p.accessed;
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
-  s.lse_bytes = (uint32_t)(hg * ts * 16);
+  s.lse_slots = at<float4>(p.ws, L.lse_slots);
+  s.slots_bytes = (uint32_t)(hg * ts * 32);
   s.ml_bytes = (uint32_t)(hg * ts * 8);
   s.acc_bytes = (uint32_t)(hg * ts * p.dim * 4);
   s.counts_bytes = (uint32_t)(p.heads * ts * 4);
-  s.xbits = at<uint64_t>(p.ws, L.xbits);
-  s.xbits_bytes = (uint32_t)(p.heads * ts * 8);
+  s.xbits = at<float4>(p.ws, L.xbits);
+  s.xbits_bytes = (uint32_t)(p.heads * ts * 16);
   s.heads = (int)p.heads;
   const int64_t rows = rows_per_pass(p.group, p.dim);
   mark(0, p.stream);
@@ -1692,18 +1796,19 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 }
 
 // Byte offsets of the workspace regions, for tests: control (hand-off
-// counters), zf (z, delta, A, th per row and block), lse, part_ml, part_acc,
-// counts, xbits (per-tile expanded-block masks), total, then n_tiles, the row
-// stride (blocks) of zf and of the per-tile arrays.
+// counters), zf (z, delta, A, th per row and block), lse, lse_slots (the
+// step's tagged LSE partials), part_ml, part_acc, counts, xbits (the step's
+// tagged expanded-block masks), total, then n_tiles, the row stride (blocks)
+// of zf and of the per-tile arrays.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out11) {
+                                    int64_t* out12) {
   clear_error();
-  if (!out11 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out12 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[11] = {L.control, L.zf,    L.lse,     L.part_ml, L.part_acc,   L.counts,
-                         L.xbits,   L.total, L.n_tiles, L.z_stride, L.tile_stride};
-  for (int i = 0; i < 11; ++i) out11[i] = v[i];
+  const int64_t v[12] = {L.control, L.zf,     L.lse,   L.lse_slots, L.part_ml,  L.part_acc,
+                         L.counts,  L.xbits,  L.total, L.n_tiles,   L.z_stride, L.tile_stride};
+  for (int i = 0; i < 12; ++i) out12[i] = v[i];
   return kOk;
 }
 

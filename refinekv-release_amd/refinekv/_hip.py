@@ -141,8 +141,8 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("control", "zf", "lse", "part_ml", "part_acc", "counts", "xbits", "total",
-                "n_tiles", "z_stride", "tile_stride")
+LAYOUT_NAMES = ("control", "zf", "lse", "lse_slots", "part_ml", "part_acc", "counts", "xbits",
+                "total", "n_tiles", "z_stride", "tile_stride")
 # rkv_set_decode_path codes: the one-launch step where it fits, or always the
 # three kernels (score, attend, merge).
 DECODE_PATHS = {"step": 0, "split": 1}

@@ -57,17 +57,20 @@ def test_workspace_size_covers_layout(lib):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
-        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:8]]
+        regions = [layout[k] for k in _hip.LAYOUT_NAMES[:9]]
         assert regions == sorted(regions) and all(r % 256 == 0 for r in regions)
         rows, tiles, ts = heads * group, layout["n_tiles"], layout["tile_stride"]
-        # hand-off counters first: one 64-byte line per KV head and one more
-        assert layout["control"] == 0 and layout["zf"] >= (heads + 1) * 64
+        # hand-off counters first: a 64-byte line per KV head, one more, and
+        # a launch counter per tile
+        assert layout["control"] == 0
+        assert layout["zf"] >= (heads + 1) * 64 + heads * layout["tile_stride"] * 8
         # padded strides: zf rows cover whole tiles, per-tile rows 64 tiles
         assert layout["z_stride"] == tiles * 64 and ts % 64 == 0 and ts >= tiles
         assert layout["lse"] - layout["zf"] >= rows * layout["z_stride"] * 16
-        assert layout["part_ml"] - layout["lse"] >= rows * ts * 16
+        assert layout["lse_slots"] - layout["lse"] >= rows * ts * 16
+        assert layout["part_ml"] - layout["lse_slots"] >= rows * ts * 32
         assert layout["part_acc"] - layout["part_ml"] >= rows * ts * 8
         assert layout["counts"] - layout["part_acc"] >= rows * ts * dim * 4
         assert layout["xbits"] - layout["counts"] >= heads * ts * 4
-        assert layout["total"] - layout["xbits"] >= heads * ts * 8
+        assert layout["total"] - layout["xbits"] >= heads * ts * 16
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0

@@ -39,19 +39,19 @@ def decode_path(hip, request):
 
 
 def assert_control_clean(hip, ws):
-    """After every launch each head's hand-off counters (tiles arrived,
-    merged, decided) are equal multiples of n_tiles -- a whole number of
-    launches -- and no hand-off wait gave up.  Returns the launch count."""
+    """After every launch each head's merge counter is n_tiles times the
+    launch count that every tile's own counter holds, and no hand-off wait
+    gave up.  Returns the launch count."""
     heads, group, dim, n = ws["hip_scratch_shape"]
-    tiles = hip.workspace_layout(heads, group, dim, n)["n_tiles"]
-    lines = ws["hip_scratch"][:(heads + 1) * 64].view(torch.int64).cpu().numpy()
-    lines = lines.reshape(heads + 1, 8)
+    layout = hip.workspace_layout(heads, group, dim, n)
+    tiles, ts = layout["n_tiles"], layout["tile_stride"]
+    words = ws["hip_scratch"][:layout["zf"]].view(torch.int64).cpu().numpy()
+    lines = words[:(heads + 1) * 8].reshape(heads + 1, 8)
     assert lines[heads, 0] & 0xFFFFFFFF == 0, "a hand-off wait gave up"
-    arrived, merged, decided = lines[:heads, 0], lines[:heads, 1], lines[:heads, 2]
-    assert np.array_equal(arrived, merged) and np.array_equal(arrived, decided), lines[:heads]
-    assert not (arrived % tiles).any(), arrived
-    assert np.all(arrived == arrived[0]), arrived
-    return int(arrived[0]) // tiles
+    launches = words[(heads + 1) * 8:(heads + 1) * 8 + heads * ts].reshape(heads, ts)[:, :tiles]
+    assert np.all(launches == launches[0, 0]), launches
+    assert np.all(lines[:heads, 1] == launches[0, 0] * tiles), lines[:heads, 1]
+    return int(launches[0, 0])
 
 
 def bits16(t):
