@@ -103,6 +103,26 @@ int rkv_select(const void* query, const void* key_mean, const void* ellipsoid,
                rkv_stream_t stream);
 
 /*
+ * Prompt-anchor mask: the union of the expanded-block masks of `anchors`
+ * queries.  Replaces the per-anchor loop of select_blocks calls in the
+ * reference's Transformers hook (src/refinekv/integrations/
+ * transformers.py:539-552) with one scoring launch over every (query, head,
+ * tile) and one launch that ORs the decisions.
+ *   queries: (anchors, heads, group, dim) bf16, dense.  Summary and eps /
+ *   reduction as for rkv_select (each query is reduced over its own group).
+ *   mask_out: (heads, n_blocks) bytes 0/1.
+ *   workspace: rkv_workspace_bytes(heads * anchors, group, dim, n_blocks)
+ *   bytes, 256-byte aligned, contents need no initialisation (not the
+ *   rkv_decode workspace: its counters must not be overwritten).
+ */
+int rkv_select_anchors(const void* queries, const void* key_mean, const void* ellipsoid,
+                       const float* value_norm, const float* max_value_norm, int64_t heads,
+                       int64_t group, int64_t dim, int64_t n_blocks, int64_t block_size,
+                       int64_t prompt_length, float eps, int reduction, int64_t anchors,
+                       uint8_t* mask_out, void* workspace, size_t workspace_bytes,
+                       rkv_stream_t stream);
+
+/*
  * One decode step of RefineKV attention.  Replaces sparse_attention_triton
  * (src/refinekv/kernels/runtime.py:123-227) behind sparse_attention
  * (src/refinekv/attention.py:76-134); semantics of

@@ -192,6 +192,7 @@ struct ScoreArgs {
   int64_t n_blocks, block, length;
   int64_t z_stride, tile_stride;
   int group;
+  int summary_heads;          // query head h reads the summaries of head h % summary_heads
   float scale;
 };
 
@@ -259,6 +260,7 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
   float* qs = qstage;                     // [G][QS] bf16(q)
   float* q2s = qs + G * QS;               // [G][QS] bf16(q^2)
   const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
+  const int64_t hs = h % a.summary_heads;  // the summaries' head
   const int first = tid, step = kThreads;
   // The query words first (the staging below waits only for them: loads
   // complete in order), then every load of the tile.  Blocks past the end
@@ -275,7 +277,7 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
   for (int ps = 0; ps < S::kPasses; ++ps) {
     int64_t b = tile * kTile + ps * S::kPerPass + sub;
     b = b < N ? b : N - 1;
-    const int64_t o = (h * N + b) * D + c * CH;
+    const int64_t o = (hs * N + b) * D + c * CH;
     kraw[ps] = load_raw<CH>(a.key_mean + o);
     eraw[ps] = load_raw<CH>(a.ellipsoid + o);
   }
@@ -417,6 +419,7 @@ struct DecideArgs {
   const float* max_value_norm;  // (H)
   const uint8_t* anchor;        // (H, N) or null
   uint8_t* mask;                // (H, N)
+  bool write_mask;              // false: mask only stands in for a null anchor
   float* risk_out;              // (H, G, N) or null
   float* stats_out;             // (H, G, 2) or null: log Z, log C
   int64_t n_blocks, n_tiles, block, length;
@@ -477,9 +480,12 @@ struct DecideLoads {
 
 // kStats = false leaves part and zf to the caller (the one-launch step has
 // them only after its hand-off).
+// rh: the head index of the statistics rows (lse, zf) -- h except for the
+// batched anchor selection, whose query q of head h has rows of head q H + h.
 template <bool kStats = true>
 __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t h,
-                                                    int64_t tile) {
+                                                    int64_t tile, int64_t rh = -1) {
+  if (rh < 0) rh = h;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
@@ -492,8 +498,8 @@ __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t
   d.vnorm = a.value_norm[h * N + bc];
   d.anc = anc[h * N + bc];
   if constexpr (kStats) {
-    d.part = *reinterpret_cast<const float4*>(a.lse + ((h * G + gl) * a.tile_stride + tl) * 4);
-    d.zf = a.zf[(h * G + gl) * a.z_stride + bc];
+    d.part = *reinterpret_cast<const float4*>(a.lse + ((rh * G + gl) * a.tile_stride + tl) * 4);
+    d.zf = a.zf[(rh * G + gl) * a.z_stride + bc];
   }
   return d;
 }
@@ -596,7 +602,9 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
                                                   const DecideLoads& in, DecideShared& sh,
                                                   float (*zsh)[kTile], const int32_t*& list,
                                                   uint32_t& count,
-                                                  const StepStats* ss = nullptr) {
+                                                  const StepStats* ss = nullptr,
+                                                  int64_t rh = -1) {
+  if (rh < 0) rh = h;
   const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
@@ -614,14 +622,14 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   bool wbad = false;
   auto row_tail = [&](int g, float lz, float lc, float4 zf) {
     if (a.stats_out && owner && tile == 0 && lane == 0) {
-      a.stats_out[(h * G + g) * 2] = lz;
-      a.stats_out[(h * G + g) * 2 + 1] = lc;
+      a.stats_out[(rh * G + g) * 2] = lz;
+      a.stats_out[(rh * G + g) * 2 + 1] = lc;
     }
     wbad |= !is_finite(lz) || !is_finite(lc);
     float r = 0.0f;
     if (valid) {
       r = risk_from(zf.x, zf.y, zf.z, zf.w, lz, lc, vmax, vnorm);
-      if (a.risk_out && owner) a.risk_out[(h * G + g) * N + b] = r;
+      if (a.risk_out && owner) a.risk_out[(rh * G + g) * N + b] = r;
     }
     wsel |= __ballot(valid && (r > a.eps || !is_finite(r)));
     sh.risk[g][lane] = r;
@@ -637,7 +645,7 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
     }
   } else {
     auto row_stats = [&](int g, float4 part, float4 zf) {
-      const float* prow = a.lse + (h * G + g) * a.tile_stride * 4;
+      const float* prow = a.lse + (rh * G + g) * a.tile_stride * 4;
       if (lane >= T) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
       auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
       auto pc = [&](int64_t t) { return make_float2(prow[t * 4 + 2], prow[t * 4 + 3]); };
@@ -649,9 +657,9 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
     if (wave < G) row_stats(wave, in.part, in.zf);
 #pragma unroll 1
     for (int g = wave + kWaves; g < G; g += kWaves) {
-      const int64_t at = (h * G + g) * a.tile_stride + tl;
+      const int64_t at = (rh * G + g) * a.tile_stride + tl;
       row_stats(g, *reinterpret_cast<const float4*>(a.lse + at * 4),
-                a.zf[(h * G + g) * a.z_stride + bc]);
+                a.zf[(rh * G + g) * a.z_stride + bc]);
     }
   }
   if (lane == 0) {
@@ -684,7 +692,7 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   }
   list = sh.list[wave];
   if (wave == 0) {
-    if (valid && owner) a.mask[h * N + b] = sel ? 1 : 0;
+    if (valid && owner && a.write_mask) a.mask[h * N + b] = sel ? 1 : 0;
     // access count (transformers.py:590-594): count of an expanded block,
     // 1 for a representative; only the prompt's last block can be short
     const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
@@ -706,6 +714,27 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a,
   const DecideLoads in = decide_issue(a, blockIdx.y, blockIdx.x);
   decide_finish(a, blockIdx.y, blockIdx.x, in, sh, nullptr, list, count);
   if (accessed && threadIdx.x == 0) atomicAdd(accessed, (unsigned long long)count);
+}
+
+// Batched anchor selection: the union over `anchors` queries of their
+// decisions, for tile (blockIdx.x) of head h (blockIdx.y); query q's rows are
+// those of head q H + h.  The OR of the tiles' ballots is stored once.
+__global__ __launch_bounds__(kThreads) void anchor_decide_kernel(DecideArgs a, int anchors,
+                                                                 int heads, uint8_t* mask_out) {
+  __shared__ DecideShared sh;
+  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  uint64_t any = 0;
+  for (int q = 0; q < anchors; ++q) {
+    const int64_t rh = (int64_t)q * heads + h;
+    const DecideLoads in = decide_issue(a, h, tile, rh);
+    const int32_t* list;
+    uint32_t count = 0;
+    any |= decide_finish(a, h, tile, in, sh, nullptr, list, count, nullptr, rh);
+    __syncthreads();  // the next query reuses sh
+  }
+  const int lane = threadIdx.x % kWave;
+  const int64_t b = tile * kTile + lane;
+  if (threadIdx.x < kWave && b < a.n_blocks) mask_out[h * a.n_blocks + b] = (any >> lane) & 1u;
 }
 
 // ---------------------------------------------------------------------------
@@ -1565,6 +1594,7 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
   sa.z_stride = L.z_stride;
   sa.tile_stride = L.tile_stride;
   sa.group = (int)p.group;
+  sa.summary_heads = (int)p.heads;
   sa.scale = (float)pow((double)p.dim, -0.5);
   return sa;
 }
@@ -1577,6 +1607,7 @@ DecideArgs decide_args(const SelectParams& p, const Layout& L) {
   da.max_value_norm = p.max_value_norm;
   da.anchor = p.anchor;
   da.mask = p.mask;
+  da.write_mask = true;
   da.risk_out = p.risk_out;
   da.stats_out = p.stats_out;
   da.n_blocks = p.n_blocks;
@@ -1591,9 +1622,9 @@ DecideArgs decide_args(const SelectParams& p, const Layout& L) {
   return da;
 }
 
-int launch_score(const SelectParams& p, const Layout& L) {
+int launch_score(const SelectParams& p, const Layout& L, int64_t queries = 1) {
   const ScoreArgs sa = score_args(p, L);
-  const dim3 grid((unsigned)L.n_tiles, (unsigned)p.heads);
+  const dim3 grid((unsigned)L.n_tiles, (unsigned)(p.heads * queries));
   RKV_DISPATCH_DIM(p.dim, D,
                    score_kernel<D><<<grid, dim3(kThreads), score_smem(p.group, p.dim),
                                      p.stream>>>(sa));
@@ -1612,6 +1643,20 @@ int launch_select(const SelectParams& p, const Layout& L) {
   rc = check_launch("decide_kernel");
   mark(2, p.stream);
   return rc;
+}
+
+// Batched anchor selection: score every (query, head, tile), then one
+// workgroup per (tile, head) ORs the queries' decisions.  The layout is the
+// one of heads * anchors heads.
+int launch_select_anchors(const SelectParams& p, int64_t anchors) {
+  const Layout L = make_layout(p.heads * anchors, p.group, p.dim, p.n_blocks);
+  int rc = launch_score(p, L, anchors);
+  if (rc) return rc;
+  DecideArgs da = decide_args(p, L);
+  da.write_mask = false;  // the mask only stands in for the (absent) anchor input
+  anchor_decide_kernel<<<dim3((unsigned)L.n_tiles, (unsigned)p.heads), dim3(kThreads), 0,
+                         p.stream>>>(da, (int)anchors, (int)p.heads, p.mask);
+  return check_launch("anchor_decide_kernel");
 }
 
 struct DecodeBuffers {
@@ -1827,6 +1872,32 @@ extern "C" int rkv_select(const void* query, const void* key_mean, const void* e
   int rc = validate_select(p, "rkv_select", L);
   if (rc) return rc;
   return launch_select(p, L);
+}
+
+extern "C" int rkv_select_anchors(const void* queries, const void* key_mean,
+                                  const void* ellipsoid, const float* value_norm,
+                                  const float* max_value_norm, int64_t heads, int64_t group,
+                                  int64_t dim, int64_t n_blocks, int64_t block_size,
+                                  int64_t prompt_length, float eps, int reduction,
+                                  int64_t anchors, uint8_t* mask_out, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  if (anchors <= 0 || anchors > 65535)
+    return set_error(kInvalidArgument, "rkv_select_anchors: anchors must be in 1..65535");
+  if (heads > 0 && heads * anchors > 65535)
+    return set_error(kUnsupported, "rkv_select_anchors: heads x anchors exceeds 65535");
+  SelectParams p{queries, key_mean, ellipsoid, value_norm, max_value_norm, heads, group, dim,
+                 n_blocks, block_size, prompt_length, eps, reduction, nullptr, mask_out,
+                 nullptr, nullptr, nullptr, workspace, workspace_bytes, stream};
+  Layout L;
+  int rc = validate_select(p, "rkv_select_anchors", L);
+  if (rc) return rc;
+  const Layout LA = make_layout(heads * anchors, group, dim, n_blocks);
+  if (workspace_bytes < (size_t)LA.total)
+    return set_error(kWorkspaceTooSmall,
+                     "rkv_select_anchors: workspace needs %lld bytes (rkv_workspace_bytes of "
+                     "heads x anchors heads)", (long long)LA.total);
+  return launch_select_anchors(p, anchors);
 }
 
 extern "C" int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,

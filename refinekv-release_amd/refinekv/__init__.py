@@ -4,7 +4,7 @@ Same public API as the reference package (src/refinekv/__init__.py:3-25);
 ``RefineKVConfig(backend="hip")`` selects the gfx950 kernels.
 """
 
-from .attention import AttentionResult, select_blocks, sparse_attention
+from .attention import AttentionResult, select_blocks, select_blocks_union, sparse_attention
 from .config import RefineKVConfig
 from .summary import BlockSummary, build_summary
 
@@ -15,6 +15,7 @@ __all__ = [
     "RefineKVConfig",
     "build_summary",
     "select_blocks",
+    "select_blocks_union",
     "sparse_attention",
     "RefineKV",
     "make_visible_static_cache",

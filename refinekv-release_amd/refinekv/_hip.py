@@ -47,6 +47,9 @@ def _bind(lib):
     lib.rkv_select.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32, _int,
                                _p, _p, _p, _p, _p, _p, _size, _p]
     lib.rkv_select.restype = _int
+    lib.rkv_select_anchors.argtypes = [_p, _p, _p, _p, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                       _f32, _int, _i64, _p, _p, _size, _p]
+    lib.rkv_select_anchors.restype = _int
     lib.rkv_decode.argtypes = [_p, _p, _p, _p, _p, _p, _p, _i64, _p, _i64, _p, _i64, _i64, _p,
                                _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _f32,
                                _int, _p, _p, _p, _p, _p, _size, _p]
@@ -210,6 +213,30 @@ def select(query, summary, config, workspace=None, risk_out=None, stats_out=None
         _ptr(anchor), _ptr(mask), _ptr(risk_out), _ptr(stats_out), _ptr(accessed),
         _ptr(scratch), scratch.numel(), _stream(query.device))
     _check(rc, "rkv_select")
+    return mask
+
+
+def select_anchors(queries, summary, config, workspace=None):
+    """Union of the expanded-block masks of queries (H, G, A, D): one launch
+    scores every (query, head, tile), one ORs the decisions.  The scratch is
+    its own workspace entry (sized for H * A heads), apart from the decode
+    step's."""
+    heads, group, count, dim = queries.shape
+    q = queries.permute(2, 0, 1, 3).contiguous()  # (A, H, G, D)
+    n_blocks = summary.num_blocks
+    shape = (heads * count, group, dim, n_blocks)
+    nbytes = workspace_bytes(*shape)
+    scratch = workspace.get("hip_anchor_scratch") if workspace is not None else None
+    if scratch is None or scratch.numel() < nbytes or scratch.device != queries.device:
+        scratch = torch.empty(nbytes, device=queries.device, dtype=torch.uint8)
+        if workspace is not None:
+            workspace["hip_anchor_scratch"] = scratch
+    mask = torch.empty(heads, n_blocks, device=queries.device, dtype=torch.bool)
+    rc = lib().rkv_select_anchors(
+        _ptr(q), *_summary_args(summary), heads, group, dim, n_blocks, summary.block_size,
+        summary.prompt_length, float(config.eps), REDUCTION_CODES[config.gqa_reduction], count,
+        _ptr(mask), _ptr(scratch), scratch.numel(), _stream(queries.device))
+    _check(rc, "rkv_select_anchors")
     return mask
 
 

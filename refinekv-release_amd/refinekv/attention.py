@@ -86,6 +86,31 @@ def select_blocks(query, summary, config=None, *, workspace=None):
 
 
 @torch.no_grad()
+def select_blocks_union(queries, summary, config=None, *, workspace=None):
+    """Union of the (kv_heads, blocks) masks of several queries, (kv_heads,
+    group_size, count, head_dim) -- the prompt-anchor mask.  The reference
+    builds it with one select_blocks call per anchor query
+    (integrations/transformers.py:539-552); the HIP backend scores all of them
+    in one launch and ORs the decisions on the device."""
+    config = config or RefineKVConfig(block_size=summary.block_size)
+    if queries.ndim != 4 or min(queries.shape) <= 0:
+        raise ValueError("queries must have shape (kv_heads, group_size, count, head_dim)")
+    _validate(queries[:, :, :1], summary, config)
+    if _backend(queries[:, :, :1], config) == "hip":
+        from . import _hip
+
+        _check_hip_summary(summary)
+        return _hip.select_anchors(queries, summary, config, workspace)
+    from .reference import select_blocks as select_torch
+
+    union = None
+    for position in range(queries.shape[2]):
+        selected = select_torch(queries[:, :, position:position + 1], summary, config)[0]
+        union = selected if union is None else union | selected
+    return union
+
+
+@torch.no_grad()
 def sparse_attention(
     query: torch.Tensor,
     summary: BlockSummary,

@@ -27,7 +27,7 @@ try:
 except ImportError as error:  # the reference raises the same way (transformers.py:9-16)
     raise ImportError("the RefineKV Transformers adapter needs the 'transformers' package") from error
 
-from ..attention import select_blocks, sparse_attention
+from ..attention import select_blocks_union, sparse_attention
 from ..config import RefineKVConfig
 from ..summary import BlockSummary, build_summary
 
@@ -582,14 +582,14 @@ class RefineKV:
         queries = self._anchor_queries.pop(index, None)
         if count and queries is None:
             raise RuntimeError(f"missing prompt anchor queries in layer {index}")
+        if not count:
+            return None
         heads, dim = key.shape[1], query.shape[-1]
         groups = query.shape[1] // heads
-        union = None
-        for position in range(count):
-            q = queries[:, position:position + 1].reshape(heads, groups, 1, dim)
-            selected = select_blocks(q, state.summary, self.config, workspace=state.workspace)
-            union = selected if union is None else union | selected
-        return union
+        # one batched selection over the anchor queries (the reference calls
+        # select_blocks once per anchor query and ORs the masks)
+        q = queries[:, :count].reshape(heads, groups, count, dim)
+        return select_blocks_union(q, state.summary, self.config, workspace=state.workspace)
 
     def _dense_decode(self, module, query, key, value, mask, scaling, kwargs, visible):
         """Dense layers and the dense baseline: SDPA with an explicit additive

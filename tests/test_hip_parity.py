@@ -12,7 +12,8 @@ import pytest
 import torch
 
 import golden_cases as gc
-from refinekv import RefineKVConfig, build_summary, select_blocks, sparse_attention, testing
+from refinekv import (RefineKVConfig, build_summary, select_blocks, select_blocks_union,
+                      sparse_attention, testing)
 
 pytestmark = pytest.mark.gpu
 DEV = torch.device("cuda")
@@ -214,6 +215,38 @@ def test_selection_bit_exact(hip, oracle_lib, heads, group, dim, block, prompt, 
     # the public API returns the same mask
     api = select_blocks(inp["query"].to(DEV), summary, cfg, workspace={})
     assert torch.equal(api.cpu(), mask.cpu())
+
+
+@pytest.mark.parametrize("heads,group,dim,block,prompt,reduction,eps,spikes", SELECT_CASES)
+def test_anchor_union_matches_per_query_selection(hip, oracle_lib, heads, group, dim, block,
+                                                  prompt, reduction, eps, spikes):
+    """The batched anchor selection (one scoring launch over all queries)
+    equals the OR of the oracle's per-query masks and of per-query HIP
+    selections, for every reduction."""
+    inp = _decode_case(heads, group, dim, block, prompt, spikes)
+    cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps, gqa_reduction=reduction)
+    summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
+    count = 5
+    gen = torch.Generator().manual_seed(7)
+    # perturbed copies of the spike-aligned decode query
+    queries = inp["query"].float() + 0.3 * torch.randn(heads, group, count, dim, generator=gen)
+    queries[:, :, 0] = inp["query"][:, :, 0].float()
+    queries = queries.to(torch.bfloat16)
+    ws = {}
+    got = select_blocks_union(queries.to(DEV), summary, cfg, workspace=ws).cpu().numpy()
+    summ = oracle_summary_of(summary)
+    want = np.zeros((heads, summary.num_blocks), np.uint8)
+    hip_union = torch.zeros(heads, summary.num_blocks, dtype=torch.bool)
+    for a in range(count):
+        qa = queries[:, :, a]
+        mask, _, _ = oracle_lib.select(qa.float().numpy(), summ, eps, reduction)
+        want |= mask
+        hip_union |= select_blocks(qa[:, :, None].to(DEV), summary, cfg, workspace={}).cpu()
+    assert np.array_equal(got.astype(np.uint8), want)
+    assert np.array_equal(got, hip_union.numpy())
+    # a second call with the same workspace (its scratch reused) agrees
+    again = select_blocks_union(queries.to(DEV), summary, cfg, workspace=ws).cpu().numpy()
+    assert np.array_equal(again, got)
 
 
 # ---------------------------------------------------------------------------
