@@ -95,12 +95,22 @@ RKV_HD float scale_pow2(float p, int k) {
 // fma so k*ln2_hi is exact), then the degree-7 Taylor polynomial of e^r on
 // |r| <= ln2/2 (truncation 5e-9 relative), then an exact scale by 2^k.
 // exp(0) == 1 exactly; exp(-inf) == 0; exp(+inf) == +inf.
+//
+// The device build takes the main path in every lane (on an argument
+// clamped to [-104, 88.8], which leaves every input of the main path
+// unchanged) and selects the special cases after, so no lane branches; the
+// results equal the host build's early returns bit for bit.
 RKV_HD float expf_(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float xs = __builtin_fminf(__builtin_fmaxf(x, -104.0f), 88.8f);
+#else
   if (is_nan(x)) return x + x;
   if (x > 88.8f) return bits_f32(0x7F800000u);
   if (x < -104.0f) return 0.0f;
-  float k = __builtin_rintf(x * 1.44269504088896341f);
-  float r = __builtin_fmaf(k, -0.693145751953125f, x);
+  const float xs = x;
+#endif
+  float k = __builtin_rintf(xs * 1.44269504088896341f);
+  float r = __builtin_fmaf(k, -0.693145751953125f, xs);
   r = __builtin_fmaf(k, -1.42860682030941723e-06f, r);
   float p = 1.98412698412698413e-04f;         // 1/7!
   p = __builtin_fmaf(p, r, 1.38888888888888889e-03f);  // 1/6!
@@ -113,7 +123,10 @@ RKV_HD float expf_(float x) {
 #if defined(__HIP_DEVICE_COMPILE__)
   // v_ldexp_f32 rounds once, exactly as scale_pow2's exact-then-rounded
   // multiplies do.
-  return __builtin_amdgcn_ldexpf(p, (int)k);
+  float y = __builtin_amdgcn_ldexpf(p, (int)k);
+  y = x > 88.8f ? bits_f32(0x7F800000u) : y;
+  y = x < -104.0f ? 0.0f : y;
+  return is_nan(x) ? x + x : y;
 #else
   return scale_pow2(p, (int)k);
 #endif
@@ -124,7 +137,25 @@ RKV_HD float expf_(float x) {
 // log(1 + f) = f - (hfsq - s*(hfsq + R(s^2))) with hfsq = f^2/2 and R the
 // Taylor series of 2*atanh(s)/s - 2 - ... truncated after s^8 (2/3, 2/5,
 // 2/7, 2/9).  log(1) == +0 exactly; log(0) == -inf; log(x<0) == NaN.
+//
+// The device build, as for expf_, runs the main path in every lane (on 1.0
+// in place of the special inputs) and selects the special results after.
 RKV_HD float logf_(float x) {
+#if defined(__HIP_DEVICE_COMPILE__)
+  const bool special = !(x > 0.0f) || x == bits_f32(0x7F800000u);  // NaN, <= 0, +inf
+  const float xin = x;
+  x = special ? 1.0f : x;
+  uint32_t u = f32_bits(x);
+  const bool sub = u < 0x00800000u;  // subnormal
+  x = sub ? x * 8388608.0f : x;
+  u = f32_bits(x);
+  int e = sub ? -23 : 0;
+  e += (int)(u >> 23) - 127;
+  float m = bits_f32((u & 0x007FFFFFu) | 0x3F800000u);
+  const bool hi = m > 1.41421356237309505f;
+  m = hi ? m * 0.5f : m;
+  e += hi ? 1 : 0;
+#else
   if (is_nan(x)) return x + x;
   if (x < 0.0f) return bits_f32(0x7FC00000u);
   if (x == 0.0f) return bits_f32(0xFF800000u);
@@ -142,6 +173,7 @@ RKV_HD float logf_(float x) {
     m = m * 0.5f;
     e += 1;
   }
+#endif
   float f = m - 1.0f;
   float s = f / (2.0f + f);
   float s2 = s * s;
@@ -152,8 +184,17 @@ RKV_HD float logf_(float x) {
   R = R * s2;
   float hfsq = 0.5f * f * f;
   float dk = (float)e;
-  return dk * 0.693145751953125f -
-         ((hfsq - (s * (hfsq + R) + dk * 1.42860682030941723e-06f)) - f);
+  const float y = dk * 0.693145751953125f -
+                  ((hfsq - (s * (hfsq + R) + dk * 1.42860682030941723e-06f)) - f);
+#if defined(__HIP_DEVICE_COMPILE__)
+  // the host build's early returns, lowest priority first
+  float r = xin == bits_f32(0x7F800000u) ? xin : y;
+  r = xin == 0.0f ? bits_f32(0xFF800000u) : r;
+  r = xin < 0.0f ? bits_f32(0x7FC00000u) : r;
+  return is_nan(xin) ? xin + xin : r;
+#else
+  return y;
+#endif
 }
 
 }  // namespace rkv

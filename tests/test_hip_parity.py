@@ -98,7 +98,9 @@ def assert_close_output(got, want):
 def test_device_math_bitwise_equals_oracle(hip, oracle_lib):
     rng = np.random.default_rng(0)
     specials = np.array([0.0, -0.0, np.inf, -np.inf, np.nan, 1.0, 88.72283, 88.7229, -103.97,
-                         -104.5, 1e-40, 1e-45, 3.4e38], np.float32)
+                         -104.5, 1e-40, 1e-45, 3.4e38, 88.8, 88.80001, 89.0, -104.0, -104.00001,
+                         -1.0, -3.5, -1e-40, 1.17549435e-38, 1.1754942e-38, 1.41421356,
+                         1.4142137, 0.70710677, -np.nan], np.float32)
     xe = np.concatenate([rng.uniform(-110, 90, 400000), rng.uniform(-1, 1, 200000),
                          specials]).astype(np.float32)
     xl = np.concatenate([np.exp(rng.uniform(-103, 88, 400000)), rng.uniform(0.5, 2, 200000),
