@@ -797,9 +797,19 @@ __device__ __forceinline__ void fold(GroupState<D, GBM>& st, const float (&x)[GB
 }
 
 // Logits of R token rows (K raw, this lane's slice) for GBM query rows, then
-// the fold.  Row u is live when bit u of ok is set.
+// the fold.  Row u is live when bit u of ok is set.  The dot products take
+// the bf16 pairs as they are, with v_dot2_f32_bf16: this is the
+// tolerance-checked attention, not the selection.
+typedef __bf16 Bf16x2 __attribute__((ext_vector_type(2)));
+
+__device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
+  return __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(Bf16x2, a),
+                                         __builtin_bit_cast(Bf16x2, b), c, false);
+}
+
 template <int D, int GBM>
-__device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st, const float (&q)[GBM][D / 16],
+__device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st,
+                                            const RawBf16<D / 16> (&q)[GBM],
                                             const RawBf16<D / 16> (&kr)[kRowBatch],
                                             const RawBf16<D / 16> (&vr)[kRowBatch], uint32_t ok,
                                             float scale, int gn) {
@@ -808,13 +818,11 @@ __device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st, const float 
 #pragma unroll
   for (int u = 0; u < kRowBatch; ++u) {
     const bool live = (ok >> u) & 1u;
-    float k[CH];
-    unpack(kr[u], k);
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
-      float s = q[g][0] * k[0];
+      float s = dot2_bf16(q[g].w[0], kr[u].w[0], 0.0f);
 #pragma unroll
-      for (int i = 1; i < CH; ++i) s = __builtin_fmaf(q[g][i], k[i], s);
+      for (int i = 1; i < CH / 2; ++i) s = dot2_bf16(q[g].w[i], kr[u].w[i], s);
       s = row16_sum_all(s);
       x[g][u] = live ? s * scale : kNegInf;
     }
@@ -1136,9 +1144,6 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     vsr[0] = load_raw<CH>((has ? vs + t * vts : vbase) + c * CH);
   }
 
-  float q[GBM][CH];
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) unpack(qraw[g], q[g]);
 
   // ---- every representative of this lane group, expanded or not ----------
   GroupState<D, GBM> st;
@@ -1205,7 +1210,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       kr[u] = ksr[0];
       vr[u] = vsr[0];
     }
-    fold_tokens<D, GBM>(st, q, kr, vr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
+    fold_tokens<D, GBM>(st, qraw, kr, vr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
   }
 
   // ---- token rows ---------------------------------------------------------
@@ -1231,10 +1236,10 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     uint32_t okb = issue(1, kb, vb);
 #pragma unroll 1
     for (uint32_t k = 0; k * 16 * R < n_rows; k += 2) {
-      fold_tokens<D, GBM>(st, q, ka, va, oka, a.scale, gn);
+      fold_tokens<D, GBM>(st, qraw, ka, va, oka, a.scale, gn);
       oka = issue(k + 2, ka, va);
       if ((k + 1) * 16 * R >= n_rows) break;
-      fold_tokens<D, GBM>(st, q, kb, vb, okb, a.scale, gn);
+      fold_tokens<D, GBM>(st, qraw, kb, vb, okb, a.scale, gn);
       okb = issue(k + 3, kb, vb);
     }
   };
