@@ -55,6 +55,20 @@ def assert_control_clean(hip, ws):
     return int(launches[0, 0])
 
 
+def step_fits(group, dim, n_blocks):
+    """Whether rkv_decode takes the one-launch step for this shape: every
+    query row in one attention pass (4, 8 or 16 rows as head_dim allows) and
+    at most 256 tiles of 64 blocks."""
+    cap = 64 // (dim // 16)
+    rows = 16
+    while rows > cap:
+        rows //= 2
+    want = 4
+    while want < group and want < 16:
+        want *= 2
+    return group <= min(want, rows) and -(-n_blocks // 64) <= 256
+
+
 def bits16(t):
     return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
 
@@ -272,6 +286,10 @@ DECODE_CASES = [
         # few (row, column) units per merge slice: 1-2 query rows, short rows
         (2, 1, 64, 16, 9000, "any", 0.01, 0.05),
         (1, 2, 32, 16, 8200, "max", 0.01, 0.05),
+        # more than 64 tiles per head (several tiles per lane in the step's
+        # hand-offs), and more than the step takes (the three kernels run)
+        (1, 4, 128, 16, 140000, "max", 0.01, 0.02),
+        (1, 2, 64, 16, 310000, "any", 0.01, 0.01),
     ]
 ]
 
@@ -312,7 +330,8 @@ def test_decode_matches_oracle(hip, oracle_lib, decode_path, heads, group, dim, 
                 f"mask suffix={suffix} anchor={use_anchor}"
             got = res.output.float().cpu().numpy()[:, :, 0]
             assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
-    assert_control_clean(hip, ws)
+    launches = assert_control_clean(hip, ws)
+    assert launches == (6 if decode_path == "step" and step_fits(group, dim, n) else 0)
 
 
 def test_device_suffix_length_matches_slicing(hip, decode_path):
