@@ -60,6 +60,23 @@ int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
                 void* key_mean, void* value_mean, void* ellipsoid, float* value_norm,
                 float* max_value_norm, rkv_stream_t stream);
 
+/*
+ * Prompt summaries built while the prompt's keys and values are written to
+ * the KV cache: rkv_summary's outputs, plus every token of keys / values
+ * copied to cache_keys / cache_values (same dtype, (heads, length, dim) with
+ * head/token strides, head_dim dense), from the same loads.  Replaces the
+ * prefill sequence of a cache write and build_summary
+ * (src/refinekv/integrations/transformers.py:529-536 over
+ * src/refinekv/summary.py:46-113), which reads the prompt's K/V again.
+ */
+int rkv_summary_store(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
+                      const void* values, int64_t v_head_stride, int64_t v_token_stride,
+                      int dtype, int64_t heads, int64_t length, int64_t dim, int64_t block_size,
+                      void* cache_keys, int64_t ck_head_stride, int64_t ck_token_stride,
+                      void* cache_values, int64_t cv_head_stride, int64_t cv_token_stride,
+                      int64_t* counts, void* key_mean, void* value_mean, void* ellipsoid,
+                      float* value_norm, float* max_value_norm, rkv_stream_t stream);
+
 /* Workspace bytes needed by rkv_select / rkv_decode for this shape (device
  * memory the caller owns).  Zero-fill it when it is created: its first region
  * holds rkv_decode's hand-off counters, which count this shape's tiles (each

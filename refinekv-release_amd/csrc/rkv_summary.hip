@@ -61,6 +61,18 @@ __device__ __forceinline__ RawCols<In, N> load_cols(const typename In::T* __rest
 }
 
 template <class In, int N>
+__device__ __forceinline__ void store_cols(typename In::T* __restrict__ p, const RawCols<In, N>& r) {
+  constexpr int W = RawCols<In, N>::W;
+  if constexpr (W == 1) {
+    *reinterpret_cast<uint32_t*>(p) = r.w[0];
+  } else if constexpr (W == 2) {
+    *reinterpret_cast<uint2*>(p) = make_uint2(r.w[0], r.w[1]);
+  } else {
+    *reinterpret_cast<uint4*>(p) = make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]);
+  }
+}
+
+template <class In, int N>
 __device__ __forceinline__ void cols_f32(const RawCols<In, N>& r, float (&x)[N]) {
   if constexpr (sizeof(typename In::T) == 2) {
 #pragma unroll
@@ -86,13 +98,24 @@ __device__ __forceinline__ float elem_f32(const typename In::T* __restrict__ p) 
 constexpr int kSummaryWaves = 4;
 constexpr int kTokBatch = 8;  // tokens per batch of pass-1 row loads
 
-template <int D, class In>
+// Where the keys and values also go when the summary is built while the
+// prompt is written to the cache (kStore): the same element strides as the
+// sources' meaning (head, token), head_dim dense.
+template <class In>
+struct CacheOut {
+  typename In::T* keys;
+  int64_t k_hs, k_ts;
+  typename In::T* values;
+  int64_t v_hs, v_ts;
+};
+
+template <int D, class In, bool kStore>
 __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
     const typename In::T* __restrict__ values, int64_t v_hs, int64_t v_ts, int64_t length,
     int block, int64_t n_blocks, int64_t* __restrict__ counts, uint16_t* __restrict__ key_mean,
     uint16_t* __restrict__ value_mean, uint16_t* __restrict__ ellipsoid,
-    float* __restrict__ value_norm) {
+    float* __restrict__ value_norm, CacheOut<In> out) {
   constexpr int CPL = D <= 128 ? 2 : 4;  // columns per lane in pass 1
   constexpr int LANES1 = D / CPL;
   __shared__ float s_mk[kSummaryWaves][D];
@@ -137,6 +160,13 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
       for (int i = 0; i < kTokBatch; ++i) {
         const int t = c0 + i0 + i;
         const bool live = on1 && t < cnt;
+        if constexpr (kStore) {
+          if (live) {
+            store_cols<In, CPL>(out.keys + h * out.k_hs + (bb * block + t) * out.k_ts + col, rk[i]);
+            store_cols<In, CPL>(out.values + h * out.v_hs + (bb * block + t) * out.v_ts + col,
+                                rv[i]);
+          }
+        }
         float xk[CPL], xv[CPL];
         cols_f32<In, CPL>(rk[i], xk);
         cols_f32<In, CPL>(rv[i], xv);
@@ -256,17 +286,27 @@ template <class In>
 int launch_summary(const void* keys, int64_t k_hs, int64_t k_ts, const void* values, int64_t v_hs,
                    int64_t v_ts, int64_t heads, int64_t length, int64_t dim, int64_t block,
                    int64_t* counts, void* key_mean, void* value_mean, void* ellipsoid,
-                   float* value_norm, float* max_value_norm, hipStream_t stream) {
+                   float* value_norm, float* max_value_norm, const CacheOut<In>& out,
+                   hipStream_t stream) {
   const int64_t n_blocks = (length + block - 1) / block;
   dim3 grid((unsigned)((n_blocks + kSummaryWaves - 1) / kSummaryWaves), (unsigned)heads);
   dim3 threads(kWave * kSummaryWaves);
-  RKV_DISPATCH_DIM(dim, D,
-                   summary_kernel<D, In><<<grid, threads, 0, stream>>>(
-                       static_cast<const typename In::T*>(keys), k_hs, k_ts,
-                       static_cast<const typename In::T*>(values), v_hs, v_ts, length, (int)block,
-                       n_blocks, counts, static_cast<uint16_t*>(key_mean),
-                       static_cast<uint16_t*>(value_mean), static_cast<uint16_t*>(ellipsoid),
-                       value_norm));
+  const auto* k = static_cast<const typename In::T*>(keys);
+  const auto* v = static_cast<const typename In::T*>(values);
+  auto* km = static_cast<uint16_t*>(key_mean);
+  auto* vm = static_cast<uint16_t*>(value_mean);
+  auto* el = static_cast<uint16_t*>(ellipsoid);
+  if (out.keys) {
+    RKV_DISPATCH_DIM(dim, D,
+                     summary_kernel<D, In, true><<<grid, threads, 0, stream>>>(
+                         k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, km,
+                         vm, el, value_norm, out));
+  } else {
+    RKV_DISPATCH_DIM(dim, D,
+                     summary_kernel<D, In, false><<<grid, threads, 0, stream>>>(
+                         k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, km,
+                         vm, el, value_norm, out));
+  }
   int rc = check_launch("summary_kernel");
   if (rc) return rc;
   max_norm_kernel<<<dim3((unsigned)heads), dim3(256), 0, stream>>>(value_norm, n_blocks,
@@ -279,6 +319,86 @@ int launch_summary(const void* keys, int64_t k_hs, int64_t k_ts, const void* val
 
 using namespace rkv;
 
+namespace {
+
+int summary_impl(const char* who, const void* keys, int64_t k_head_stride,
+                 int64_t k_token_stride, const void* values, int64_t v_head_stride,
+                 int64_t v_token_stride, int dtype, int64_t heads, int64_t length, int64_t dim,
+                 int64_t block_size, void* cache_keys, int64_t ck_head_stride,
+                 int64_t ck_token_stride, void* cache_values, int64_t cv_head_stride,
+                 int64_t cv_token_stride, int64_t* counts, void* key_mean, void* value_mean,
+                 void* ellipsoid, float* value_norm, float* max_value_norm, hipStream_t stream) {
+  if (!keys || !values || !counts || !key_mean || !value_mean || !ellipsoid || !value_norm ||
+      !max_value_norm)
+    return set_error(kInvalidArgument, "%s: null pointer argument", who);
+  if (heads <= 0 || length <= 0 || heads > 65535)
+    return set_error(kInvalidArgument, "%s: heads=%lld length=%lld out of range", who,
+                     (long long)heads, (long long)length);
+  if (!supported_dim(dim))
+    return set_error(kUnsupported, "%s: head_dim %lld not in 32..256 step 32", who,
+                     (long long)dim);
+  if (!supported_block(block_size))
+    return set_error(kInvalidArgument, "%s: block_size must be 16, 32 or 64", who);
+  if (dtype < 0 || dtype > 2) return set_error(kUnsupported, "%s: dtype code %d", who, dtype);
+  const int64_t elem = dtype == 2 ? 4 : 2;
+  const int64_t cpl = dim <= 128 ? 2 : 4;
+  // Pass-1 row loads (and the cache stores) move CPL adjacent elements; they
+  // need that alignment.
+  const uintptr_t need = (uintptr_t)(elem * cpl);
+  if (!aligned(keys, need) || !aligned(values, need) || (k_head_stride * elem) % need ||
+      (k_token_stride * elem) % need || (v_head_stride * elem) % need ||
+      (v_token_stride * elem) % need)
+    return set_error(kInvalidArgument, "%s: K/V rows must be %d-byte aligned", who, (int)need);
+  if (k_token_stride < dim || v_token_stride < dim)
+    return set_error(kInvalidArgument, "%s: token stride smaller than head_dim", who);
+  const bool store = cache_keys != nullptr || cache_values != nullptr;
+  if (store) {
+    if (!cache_keys || !cache_values)
+      return set_error(kInvalidArgument, "%s: null cache pointer", who);
+    if (!aligned(cache_keys, need) || !aligned(cache_values, need) ||
+        (ck_head_stride * elem) % need || (ck_token_stride * elem) % need ||
+        (cv_head_stride * elem) % need || (cv_token_stride * elem) % need)
+      return set_error(kInvalidArgument, "%s: cache rows must be %d-byte aligned", who,
+                       (int)need);
+    if (ck_token_stride < dim || cv_token_stride < dim)
+      return set_error(kInvalidArgument, "%s: cache token stride smaller than head_dim", who);
+  }
+  const int64_t n_blocks = (length + block_size - 1) / block_size;
+  if ((n_blocks + kSummaryWaves - 1) / kSummaryWaves > 0x7FFFFFFF)
+    return set_error(kInvalidArgument, "%s: too many blocks", who);
+  switch (dtype) {
+    case 0: {
+      const CacheOut<InBf16> out{static_cast<uint16_t*>(cache_keys), ck_head_stride,
+                                 ck_token_stride, static_cast<uint16_t*>(cache_values),
+                                 cv_head_stride, cv_token_stride};
+      return launch_summary<InBf16>(keys, k_head_stride, k_token_stride, values, v_head_stride,
+                                    v_token_stride, heads, length, dim, block_size, counts,
+                                    key_mean, value_mean, ellipsoid, value_norm, max_value_norm,
+                                    out, stream);
+    }
+    case 1: {
+      const CacheOut<InF16> out{static_cast<uint16_t*>(cache_keys), ck_head_stride,
+                                ck_token_stride, static_cast<uint16_t*>(cache_values),
+                                cv_head_stride, cv_token_stride};
+      return launch_summary<InF16>(keys, k_head_stride, k_token_stride, values, v_head_stride,
+                                   v_token_stride, heads, length, dim, block_size, counts,
+                                   key_mean, value_mean, ellipsoid, value_norm, max_value_norm,
+                                   out, stream);
+    }
+    default: {
+      const CacheOut<InF32> out{static_cast<float*>(cache_keys), ck_head_stride, ck_token_stride,
+                                static_cast<float*>(cache_values), cv_head_stride,
+                                cv_token_stride};
+      return launch_summary<InF32>(keys, k_head_stride, k_token_stride, values, v_head_stride,
+                                   v_token_stride, heads, length, dim, block_size, counts,
+                                   key_mean, value_mean, ellipsoid, value_norm, max_value_norm,
+                                   out, stream);
+    }
+  }
+}
+
+}  // namespace
+
 extern "C" int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_token_stride,
                            const void* values, int64_t v_head_stride, int64_t v_token_stride,
                            int dtype, int64_t heads, int64_t length, int64_t dim,
@@ -286,47 +406,28 @@ extern "C" int rkv_summary(const void* keys, int64_t k_head_stride, int64_t k_to
                            void* ellipsoid, float* value_norm, float* max_value_norm,
                            hipStream_t stream) {
   clear_error();
-  if (!keys || !values || !counts || !key_mean || !value_mean || !ellipsoid || !value_norm ||
-      !max_value_norm)
-    return set_error(kInvalidArgument, "rkv_summary: null pointer argument");
-  if (heads <= 0 || length <= 0 || heads > 65535)
-    return set_error(kInvalidArgument, "rkv_summary: heads=%lld length=%lld out of range",
-                     (long long)heads, (long long)length);
-  if (!supported_dim(dim))
-    return set_error(kUnsupported, "rkv_summary: head_dim %lld not in 32..256 step 32",
-                     (long long)dim);
-  if (!supported_block(block_size))
-    return set_error(kInvalidArgument, "rkv_summary: block_size must be 16, 32 or 64");
-  if (dtype < 0 || dtype > 2) return set_error(kUnsupported, "rkv_summary: dtype code %d", dtype);
-  const int64_t elem = dtype == 2 ? 4 : 2;
-  const int64_t cpl = dim <= 128 ? 2 : 4;
-  // Pass-1 row loads read CPL adjacent elements; they need that alignment.
-  const uintptr_t need = (uintptr_t)(elem * cpl);
-  if (!aligned(keys, need) || !aligned(values, need) || (k_head_stride * elem) % need ||
-      (k_token_stride * elem) % need || (v_head_stride * elem) % need ||
-      (v_token_stride * elem) % need)
-    return set_error(kInvalidArgument, "rkv_summary: K/V rows must be %d-byte aligned",
-                     (int)need);
-  if (k_token_stride < dim || v_token_stride < dim)
-    return set_error(kInvalidArgument, "rkv_summary: token stride smaller than head_dim");
-  const int64_t n_blocks = (length + block_size - 1) / block_size;
-  if ((n_blocks + kSummaryWaves - 1) / kSummaryWaves > 0x7FFFFFFF)
-    return set_error(kInvalidArgument, "rkv_summary: too many blocks");
-  switch (dtype) {
-    case 0:
-      return launch_summary<InBf16>(keys, k_head_stride, k_token_stride, values, v_head_stride,
-                                    v_token_stride, heads, length, dim, block_size, counts,
-                                    key_mean, value_mean, ellipsoid, value_norm, max_value_norm,
-                                    stream);
-    case 1:
-      return launch_summary<InF16>(keys, k_head_stride, k_token_stride, values, v_head_stride,
-                                   v_token_stride, heads, length, dim, block_size, counts,
-                                   key_mean, value_mean, ellipsoid, value_norm, max_value_norm,
-                                   stream);
-    default:
-      return launch_summary<InF32>(keys, k_head_stride, k_token_stride, values, v_head_stride,
-                                   v_token_stride, heads, length, dim, block_size, counts,
-                                   key_mean, value_mean, ellipsoid, value_norm, max_value_norm,
-                                   stream);
-  }
+  return summary_impl("rkv_summary", keys, k_head_stride, k_token_stride, values, v_head_stride,
+                      v_token_stride, dtype, heads, length, dim, block_size, nullptr, 0, 0,
+                      nullptr, 0, 0, counts, key_mean, value_mean, ellipsoid, value_norm,
+                      max_value_norm, stream);
+}
+
+extern "C" int rkv_summary_store(const void* keys, int64_t k_head_stride,
+                                 int64_t k_token_stride, const void* values,
+                                 int64_t v_head_stride, int64_t v_token_stride, int dtype,
+                                 int64_t heads, int64_t length, int64_t dim, int64_t block_size,
+                                 void* cache_keys, int64_t ck_head_stride,
+                                 int64_t ck_token_stride, void* cache_values,
+                                 int64_t cv_head_stride, int64_t cv_token_stride,
+                                 int64_t* counts, void* key_mean, void* value_mean,
+                                 void* ellipsoid, float* value_norm, float* max_value_norm,
+                                 hipStream_t stream) {
+  clear_error();
+  if (!cache_keys || !cache_values)
+    return set_error(kInvalidArgument, "rkv_summary_store: null cache pointer");
+  return summary_impl("rkv_summary_store", keys, k_head_stride, k_token_stride, values,
+                      v_head_stride, v_token_stride, dtype, heads, length, dim, block_size,
+                      cache_keys, ck_head_stride, ck_token_stride, cache_values, cv_head_stride,
+                      cv_token_stride, counts, key_mean, value_mean, ellipsoid, value_norm,
+                      max_value_norm, stream);
 }

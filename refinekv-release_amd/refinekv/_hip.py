@@ -40,6 +40,10 @@ def _bind(lib):
     lib.rkv_summary.argtypes = [_p, _i64, _i64, _p, _i64, _i64, _int, _i64, _i64, _i64, _i64, _p,
                                 _p, _p, _p, _p, _p, _p]
     lib.rkv_summary.restype = _int
+    lib.rkv_summary_store.argtypes = [_p, _i64, _i64, _p, _i64, _i64, _int, _i64, _i64, _i64,
+                                      _i64, _p, _i64, _i64, _p, _i64, _i64, _p, _p, _p, _p, _p,
+                                      _p, _p]
+    lib.rkv_summary_store.restype = _int
     lib.rkv_workspace_bytes.argtypes = [_i64, _i64, _i64, _i64]
     lib.rkv_workspace_bytes.restype = _size
     lib.rkv_workspace_layout.argtypes = [_i64, _i64, _i64, _i64, _p]
@@ -113,9 +117,11 @@ def _row_aligned(t, nbytes):
     return t if ok else t.clone(memory_format=torch.contiguous_format)
 
 
-def summary_fields(keys, values, block):
+def summary_fields(keys, values, block, cache_keys=None, cache_values=None):
     """Run the summary kernel on (H, L, D) keys/values; returns the tensors of
-    BlockSummary other than the page views."""
+    BlockSummary other than the page views.  With cache_keys / cache_values
+    ((H, L, D) views of the KV cache, head_dim dense) the same kernel also
+    writes every token there (rkv_summary_store)."""
     heads, length, dim = keys.shape
     need = keys.element_size() * (2 if dim <= 128 else 4)
     keys, values = _row_aligned(keys, need), _row_aligned(values, need)
@@ -127,12 +133,21 @@ def summary_fields(keys, values, block):
     ellipsoid = torch.empty_like(key_mean)
     value_norm = torch.empty(heads, n_blocks, device=dev, dtype=torch.float32)
     max_value_norm = torch.empty(heads, device=dev, dtype=torch.float32)
-    rc = lib().rkv_summary(
-        _ptr(keys), keys.stride(0), keys.stride(1), _ptr(values), values.stride(0),
-        values.stride(1), DTYPE_CODES[keys.dtype], heads, length, dim, block, _ptr(counts),
-        _ptr(key_mean), _ptr(value_mean), _ptr(ellipsoid), _ptr(value_norm),
-        _ptr(max_value_norm), _stream(dev))
-    _check(rc, "rkv_summary")
+    outputs = (_ptr(counts), _ptr(key_mean), _ptr(value_mean), _ptr(ellipsoid),
+               _ptr(value_norm), _ptr(max_value_norm), _stream(dev))
+    sources = (_ptr(keys), keys.stride(0), keys.stride(1), _ptr(values), values.stride(0),
+               values.stride(1), DTYPE_CODES[keys.dtype], heads, length, dim, block)
+    if cache_keys is None:
+        _check(lib().rkv_summary(*sources, *outputs), "rkv_summary")
+    else:
+        for cache in (cache_keys, cache_values):
+            if (cache.shape != keys.shape or cache.dtype != keys.dtype or cache.stride(-1) != 1
+                    or cache.device != dev):
+                raise ValueError("cache views must match keys/values with a dense head_dim")
+        rc = lib().rkv_summary_store(
+            *sources, _ptr(cache_keys), cache_keys.stride(0), cache_keys.stride(1),
+            _ptr(cache_values), cache_values.stride(0), cache_values.stride(1), *outputs)
+        _check(rc, "rkv_summary_store")
     return counts, key_mean, value_mean, ellipsoid, value_norm, max_value_norm
 
 

@@ -29,7 +29,7 @@ except ImportError as error:  # the reference raises the same way (transformers.
 
 from ..attention import select_blocks_union, sparse_attention
 from ..config import RefineKVConfig
-from ..summary import BlockSummary, build_summary
+from ..summary import BlockSummary, build_summary, store_and_build_summary
 
 _NO_ATTRIBUTE = object()
 SUPPORTED_MODEL_TYPES = ("llama", "qwen2")
@@ -51,6 +51,11 @@ class _VisibleStaticLayer(StaticLayer):
     def __init__(self, max_cache_len):
         super().__init__(max_cache_len)
         self.visible = 0
+        # Set by the RefineKV session for its sparse layers: the prompt write
+        # then also builds the layer's block summary (prefill_summary) from
+        # the same read of the prompt's keys and values.
+        self.summary_config = None
+        self.prefill_summary = None
 
     def lazy_initialization(self, key_states, value_states):
         self.dtype, self.device = key_states.dtype, key_states.device
@@ -71,8 +76,13 @@ class _VisibleStaticLayer(StaticLayer):
         end = start + key_states.shape[-2]
         if end > self.max_cache_len:
             raise ValueError("visible KV cache capacity exceeded")
-        self.keys[:, :, start:end].copy_(key_states)
-        self.values[:, :, start:end].copy_(value_states)
+        if start == 0 and self.summary_config is not None and key_states.shape[0] == 1:
+            self.prefill_summary = store_and_build_summary(
+                key_states[0], value_states[0], self.keys[0, :, :end], self.values[0, :, :end],
+                self.summary_config)
+        else:
+            self.keys[:, :, start:end].copy_(key_states)
+            self.values[:, :, start:end].copy_(value_states)
         self.visible = end
         return self.keys[:, :, :end], self.values[:, :, :end]
 
@@ -291,6 +301,13 @@ class RefineKV:
         self._anchor_queries.clear()
         self._totals = self._zero_totals()
         self._cache = cache
+        # the visible caches build the sparse layers' summaries as they take
+        # the prompt
+        for index, layer in enumerate(getattr(cache, "layers", ())):
+            if isinstance(layer, _VisibleStaticLayer):
+                sparse = index >= self.config.full_attention_layers
+                layer.summary_config = self.config if sparse else None
+                layer.prefill_summary = None
 
     # -- generate --------------------------------------------------------
     def _generate(self, original_generate, args, kwargs):
@@ -570,10 +587,26 @@ class RefineKV:
                                         scaling=scaling, **kwargs)
         state = _LayerState(prompt, prompt)
         if index >= self.config.full_attention_layers:
-            state.summary = build_summary(key[0, :, :prompt], value[0, :, :prompt], self.config)
+            state.summary = self._stored_summary(index, prompt)
+            if state.summary is None:
+                state.summary = build_summary(key[0, :, :prompt], value[0, :, :prompt],
+                                              self.config)
             state.anchor_mask = self._anchor_mask(index, state, query, key, prompt)
         self._layers[index] = state
         return output
+
+    def _stored_summary(self, index, prompt):
+        """The summary the visible cache built while writing this layer's
+        prompt, if it did."""
+        layers = getattr(self._cache, "layers", None)
+        if layers is None or index >= len(layers):
+            return None
+        layer = layers[index]
+        summary = getattr(layer, "prefill_summary", None)
+        if summary is None or summary.prompt_length != prompt:
+            return None
+        layer.prefill_summary = None
+        return summary
 
     def _anchor_mask(self, index, state, query, key, prompt):
         """Union of the selections of the last anchor_tokens prompt queries

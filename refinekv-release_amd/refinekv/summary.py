@@ -102,3 +102,35 @@ def build_summary(keys: torch.Tensor, values: torch.Tensor,
     return BlockSummary(keys=key_pages, values=value_pages, counts=counts, key_mean=key_mean,
                         value_mean=value_mean, ellipsoid=ellipsoid, value_norm=value_norm,
                         max_value_norm=max_value_norm, prompt_length=length, block_size=block)
+
+
+def store_and_build_summary(keys: torch.Tensor, values: torch.Tensor, cache_keys: torch.Tensor,
+                            cache_values: torch.Tensor,
+                            config: RefineKVConfig | None = None) -> BlockSummary:
+    """Write (kv_heads, tokens, head_dim) prompt keys/values into the KV cache
+    views cache_keys / cache_values and return build_summary of the written
+    prompt, whose pages view the cache.  With the HIP backend one kernel does
+    both from a single read of keys/values (the reference writes the cache,
+    then build_summary reads it back, integrations/transformers.py:529-536);
+    otherwise a copy, then build_summary."""
+    config = config or RefineKVConfig()
+    if keys.shape != cache_keys.shape or values.shape != cache_values.shape:
+        raise ValueError("cache views must have the keys' and values' shape")
+    if _use_hip(keys, config) and cache_keys.stride(-1) == 1 and cache_values.stride(-1) == 1:
+        from . import _hip
+
+        if keys.ndim != 3 or keys.shape != values.shape or min(keys.shape) <= 0:
+            raise ValueError(
+                "keys and values must have the same nonempty (kv_heads, tokens, dim) shape")
+        block = config.block_size
+        fields = _hip.summary_fields(keys.detach(), values.detach(), block, cache_keys,
+                                     cache_values)
+        counts, key_mean, value_mean, ellipsoid, value_norm, max_value_norm = fields
+        return BlockSummary(keys=_pages(cache_keys, block), values=_pages(cache_values, block),
+                            counts=counts, key_mean=key_mean, value_mean=value_mean,
+                            ellipsoid=ellipsoid, value_norm=value_norm,
+                            max_value_norm=max_value_norm, prompt_length=keys.shape[1],
+                            block_size=block)
+    cache_keys.copy_(keys)
+    cache_values.copy_(values)
+    return build_summary(cache_keys, cache_values, config)

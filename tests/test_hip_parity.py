@@ -176,6 +176,34 @@ def test_summary_of_strided_cache_view(hip, oracle_lib):
     assert s2.keys.data_ptr() == ck.data_ptr()
 
 
+@pytest.mark.parametrize("dtype,dim,block,length", [
+    (torch.bfloat16, 128, 32, 4099), (torch.bfloat16, 64, 16, 300), (torch.float16, 128, 32, 777),
+    (torch.float32, 96, 64, 1000), (torch.bfloat16, 256, 32, 999)])
+def test_summary_written_with_the_cache(hip, dtype, dim, block, length):
+    """store_and_build_summary (one kernel: cache write + summary) equals a
+    cache copy followed by build_summary, bit for bit, and fills the cache."""
+    from refinekv.summary import store_and_build_summary
+
+    gen = torch.Generator(device=DEV).manual_seed(dim + length)
+    # (H, L, D) sources with the projection's layout: token stride H * D
+    keys = torch.randn(length, 3, dim, generator=gen, device=DEV).to(dtype).transpose(0, 1)
+    values = torch.randn(length, 3, dim, generator=gen, device=DEV).to(dtype).transpose(0, 1)
+    cache_k = torch.full((1, 3, length + 40, dim), float("nan"), device=DEV, dtype=dtype)
+    cache_v = torch.full_like(cache_k, float("nan"))
+    cfg = RefineKVConfig(backend="hip", block_size=block)
+    fused = store_and_build_summary(keys, values, cache_k[0, :, :length], cache_v[0, :, :length],
+                                    cfg)
+    torch.cuda.synchronize()
+    assert torch.equal(cache_k[0, :, :length], keys) and torch.equal(cache_v[0, :, :length], values)
+    assert torch.isnan(cache_k[0, :, length:].float()).all()  # nothing written past the prompt
+    ref = build_summary(keys.contiguous(), values.contiguous(), cfg)
+    for name in ("counts", "key_mean", "value_mean", "ellipsoid", "value_norm", "max_value_norm"):
+        a, b = getattr(fused, name), getattr(ref, name)
+        assert torch.equal(a.view(torch.uint8) if a.is_floating_point() else a,
+                           b.view(torch.uint8) if b.is_floating_point() else b), name
+    assert torch.equal(fused.keys, ref.keys) and torch.equal(fused.values, ref.values)
+
+
 # ---------------------------------------------------------------------------
 # Selection statistics and masks
 # ---------------------------------------------------------------------------
