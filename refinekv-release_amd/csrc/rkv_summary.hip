@@ -3,9 +3,13 @@
 //
 // One wave per (KV head, block).  Pass 1 streams the block's tokens once with
 // coalesced row loads (each lane owns 2 or 4 adjacent columns) and keeps the
-// column sums, min and max in registers.  Pass 2 re-reads the block (an
-// L1/L2 hit) with each 8-lane group owning one token, so the per-token
-// head_dim sums are lane-local.  Summation orders (fixed, shared with the CPU
+// column sums, min and max in registers.  Pass 2 re-reads the block (an L2
+// hit: HBM sees each row once) with each 8-lane group owning one token, so the
+// per-token head_dim sums are lane-local.  Every row access is a buffer load
+// from a per-block buffer view (scalar base and token offset, one lane offset,
+// immediate column offsets: no per-load address arithmetic), the block index
+// is wave-uniform, and the min/max use the NaN-propagating v_maximum3 /
+// v_minimum3 forms, which keeps the vector ALU well below the memory time.  Summation orders (fixed, shared with the CPU
 // oracle and equal to torch's CPU kernels the reference runs):
 //   column sums   16-token chunks summed left to right from +0, chunk sums
 //                 added left to right from +0;
@@ -25,7 +29,11 @@ struct InBf16 {
 };
 struct InF16 {
   using T = uint16_t;
-  static __device__ __forceinline__ float cvt(uint16_t h) { return f16_to_f32(h); }
+  // v_cvt_f32_f16: exact for every finite and infinite half (as f16_to_f32);
+  // a signalling NaN comes out quiet
+  static __device__ __forceinline__ float cvt(uint16_t h) {
+    return (float)__builtin_bit_cast(_Float16, h);
+  }
 };
 struct InF32 {
   using T = float;
@@ -41,38 +49,6 @@ struct RawCols {
 };
 
 template <class In, int N>
-__device__ __forceinline__ RawCols<In, N> load_cols(const typename In::T* __restrict__ p) {
-  RawCols<In, N> r;
-  constexpr int W = RawCols<In, N>::W;
-  if constexpr (W == 1) {
-    r.w[0] = *reinterpret_cast<const uint32_t*>(p);
-  } else if constexpr (W == 2) {
-    const uint2 u = *reinterpret_cast<const uint2*>(p);
-    r.w[0] = u.x;
-    r.w[1] = u.y;
-  } else {
-    const uint4 u = *reinterpret_cast<const uint4*>(p);
-    r.w[0] = u.x;
-    r.w[1] = u.y;
-    r.w[2] = u.z;
-    r.w[3] = u.w;
-  }
-  return r;
-}
-
-template <class In, int N>
-__device__ __forceinline__ void store_cols(typename In::T* __restrict__ p, const RawCols<In, N>& r) {
-  constexpr int W = RawCols<In, N>::W;
-  if constexpr (W == 1) {
-    *reinterpret_cast<uint32_t*>(p) = r.w[0];
-  } else if constexpr (W == 2) {
-    *reinterpret_cast<uint2*>(p) = make_uint2(r.w[0], r.w[1]);
-  } else {
-    *reinterpret_cast<uint4*>(p) = make_uint4(r.w[0], r.w[1], r.w[2], r.w[3]);
-  }
-}
-
-template <class In, int N>
 __device__ __forceinline__ void cols_f32(const RawCols<In, N>& r, float (&x)[N]) {
   if constexpr (sizeof(typename In::T) == 2) {
 #pragma unroll
@@ -86,13 +62,66 @@ __device__ __forceinline__ void cols_f32(const RawCols<In, N>& r, float (&x)[N])
   }
 }
 
-template <class In>
-__device__ __forceinline__ float elem_f32(const typename In::T* __restrict__ p) {
-  if constexpr (sizeof(typename In::T) == 2) {
-    return In::cvt(*reinterpret_cast<const uint16_t*>(p));
+// Buffer view of one block's rows: a scalar base and 32-bit byte offsets.
+// Reads at or past `bytes` return 0 and writes there are dropped.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t rows_view(const void* base, int bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, bytes, 0x00020000);
+}
+
+template <class In, int N>
+__device__ __forceinline__ RawCols<In, N> buf_cols(__amdgpu_buffer_rsrc_t r, int voff, int soff) {
+  RawCols<In, N> c;
+  constexpr int W = RawCols<In, N>::W;
+  if constexpr (W == 1) {
+    c.w[0] = __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0);
+  } else if constexpr (W == 2) {
+    const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0);
+    c.w[0] = v[0];
+    c.w[1] = v[1];
   } else {
-    return *p;
+    const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+    c.w[0] = v[0];
+    c.w[1] = v[1];
+    c.w[2] = v[2];
+    c.w[3] = v[3];
   }
+  return c;
+}
+
+template <class In, int N>
+__device__ __forceinline__ void buf_store_cols(__amdgpu_buffer_rsrc_t r, int voff, int soff,
+                                               const RawCols<In, N>& c) {
+  constexpr int W = RawCols<In, N>::W;
+  typedef unsigned int U2 __attribute__((ext_vector_type(2)));
+  typedef unsigned int U4 __attribute__((ext_vector_type(4)));
+  if constexpr (W == 1) {
+    __builtin_amdgcn_raw_buffer_store_b32(c.w[0], r, voff, soff, 0);
+  } else if constexpr (W == 2) {
+    const U2 v = {c.w[0], c.w[1]};
+    __builtin_amdgcn_raw_buffer_store_b64(v, r, voff, soff, 0);
+  } else {
+    const U4 v = {c.w[0], c.w[1], c.w[2], c.w[3]};
+    __builtin_amdgcn_raw_buffer_store_b128(v, r, voff, soff, 0);
+  }
+}
+
+template <class In>
+__device__ __forceinline__ float buf_elem(__amdgpu_buffer_rsrc_t r, int voff) {
+  if constexpr (sizeof(typename In::T) == 2) {
+    return In::cvt(__builtin_amdgcn_raw_buffer_load_b16(r, voff, 0, 0));
+  } else {
+    return bits_f32(__builtin_amdgcn_raw_buffer_load_b32(r, voff, 0, 0));
+  }
+}
+
+// NaN-propagating max/min (v_maximum3_f32 / v_minimum3_f32).  They differ
+// from nanmax/nanmin only in which zero a +0/-0 tie returns, which no output
+// depends on: a zero extreme enters only |extreme - mean|, clamped to 1e-6.
+__device__ __forceinline__ float max3_nan(float a, float b, float c) {
+  return __builtin_elementwise_maximum(a, __builtin_elementwise_maximum(b, c));
+}
+__device__ __forceinline__ float min3_nan(float a, float b, float c) {
+  return __builtin_elementwise_minimum(a, __builtin_elementwise_minimum(b, c));
 }
 
 constexpr int kSummaryWaves = 4;
@@ -109,6 +138,7 @@ struct CacheOut {
   int64_t v_hs, v_ts;
 };
 
+// Byte strides of a block's rows fit 31 bits (checked on the host).
 template <int D, class In, bool kStore>
 __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
@@ -116,24 +146,31 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     int block, int64_t n_blocks, int64_t* __restrict__ counts, uint16_t* __restrict__ key_mean,
     uint16_t* __restrict__ value_mean, uint16_t* __restrict__ ellipsoid,
     float* __restrict__ value_norm, CacheOut<In> out) {
+  constexpr int E = (int)sizeof(typename In::T);
   constexpr int CPL = D <= 128 ? 2 : 4;  // columns per lane in pass 1
   constexpr int LANES1 = D / CPL;
   __shared__ float s_mk[kSummaryWaves][D];
   __shared__ float s_rs[kSummaryWaves][D];
 
-  const int wave = threadIdx.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int lane = threadIdx.x % kWave;
   const int64_t h = blockIdx.y;
   const int64_t b = (int64_t)blockIdx.x * kSummaryWaves + wave;
   const bool valid = b < n_blocks;
   const int64_t bb = valid ? b : n_blocks - 1;  // in-bounds block for addresses
-  const int64_t cnt = !valid ? 0 : (b == n_blocks - 1 ? length - (n_blocks - 1) * block : block);
+  // (64-bit compares run on the vector ALU: readfirstlane keeps the counts
+  // and buffer views in scalar registers)
+  const int cnt = __builtin_amdgcn_readfirstlane(
+      !valid ? 0 : (int)(b == n_blocks - 1 ? length - (n_blocks - 1) * block : block));
+  // the block's rows; a wave past the last block reads nothing (zeros)
+  const int kts = (int)k_ts * E, vts = (int)v_ts * E;
+  auto extent = [&](int ts) { return __builtin_amdgcn_readfirstlane(cnt ? (cnt - 1) * ts + D * E : 0); };
+  const auto kr = rows_view(keys + h * k_hs + bb * block * k_ts, extent(kts));
+  const auto vr = rows_view(values + h * v_hs + bb * block * v_ts, extent(vts));
 
   // ---- pass 1: column sums (TOKSUM order), min, max -------------------
   const bool on1 = valid && lane < LANES1;
   const int col = lane < LANES1 ? lane * CPL : 0;
-  const typename In::T* kb = keys + h * k_hs + (bb * block) * k_ts + col;
-  const typename In::T* vb = values + h * v_hs + (bb * block) * v_ts + col;
   float ksum[CPL], vsum[CPL], kmax[CPL], kmin[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -142,44 +179,72 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     kmax[j] = kNegInf;
     kmin[j] = kPosInf;
   }
+  // the cache rows of this block (kStore): live tokens, lanes on1
+  const int cks = kStore ? (int)out.k_ts * E : 0, cvs = kStore ? (int)out.v_ts * E : 0;
+  const auto ckr =
+      kStore ? rows_view(out.keys + h * out.k_hs + bb * block * out.k_ts, extent(cks)) : kr;
+  const auto cvr =
+      kStore ? rows_view(out.values + h * out.v_hs + bb * block * out.v_ts, extent(cvs)) : vr;
+  // token t's columns added to the chunk sums (t < cnt, wave-uniform)
+  auto take = [&](int t, const RawCols<In, CPL>& rk, const RawCols<In, CPL>& rv,
+                  float (&ak)[CPL], float (&av)[CPL], float (&xk)[CPL]) {
+    if constexpr (kStore) {
+      if (on1) {
+        buf_store_cols<In, CPL>(ckr, col * E, t * cks, rk);
+        buf_store_cols<In, CPL>(cvr, col * E, t * cvs, rv);
+      }
+    }
+    float xv[CPL];
+    cols_f32<In, CPL>(rk, xk);
+    cols_f32<In, CPL>(rv, xv);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      ak[j] = ak[j] + xk[j];
+      av[j] = av[j] + xv[j];
+    }
+  };
   for (int c0 = 0; c0 < block; c0 += 16) {
     float ak[CPL], av[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) ak[j] = av[j] = 0.0f;
+    if (cnt - c0 >= 16) {
 #pragma unroll
-    for (int i0 = 0; i0 < 16; i0 += kTokBatch) {
-      RawCols<In, CPL> rk[kTokBatch], rv[kTokBatch];
+      for (int i0 = 0; i0 < 16; i0 += kTokBatch) {
+        RawCols<In, CPL> rk[kTokBatch], rv[kTokBatch];
 #pragma unroll
-      for (int i = 0; i < kTokBatch; ++i) {
-        const int t = c0 + i0 + i;
-        const int tt = t < cnt ? t : 0;  // rows past the block end read its first row
-        rk[i] = load_cols<In, CPL>(kb + tt * k_ts);
-        rv[i] = load_cols<In, CPL>(vb + tt * v_ts);
-      }
+        for (int i = 0; i < kTokBatch; ++i) {
+          rk[i] = buf_cols<In, CPL>(kr, col * E, (c0 + i0 + i) * kts);
+          rv[i] = buf_cols<In, CPL>(vr, col * E, (c0 + i0 + i) * vts);
+        }
 #pragma unroll
-      for (int i = 0; i < kTokBatch; ++i) {
-        const int t = c0 + i0 + i;
-        const bool live = on1 && t < cnt;
-        if constexpr (kStore) {
-          if (live) {
-            store_cols<In, CPL>(out.keys + h * out.k_hs + (bb * block + t) * out.k_ts + col, rk[i]);
-            store_cols<In, CPL>(out.values + h * out.v_hs + (bb * block + t) * out.v_ts + col,
-                                rv[i]);
+        for (int i = 0; i < kTokBatch; i += 2) {
+          float x0[CPL], x1[CPL];
+          take(c0 + i0 + i, rk[i], rv[i], ak, av, x0);
+          take(c0 + i0 + i + 1, rk[i + 1], rv[i + 1], ak, av, x1);
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            kmax[j] = max3_nan(kmax[j], x0[j], x1[j]);
+            kmin[j] = min3_nan(kmin[j], x0[j], x1[j]);
           }
         }
-        float xk[CPL], xv[CPL];
-        cols_f32<In, CPL>(rk[i], xk);
-        cols_f32<In, CPL>(rv[i], xv);
+      }
+    } else {
+      for (int t = c0; t < cnt; ++t) {
+        float x[CPL];
+        take(t, buf_cols<In, CPL>(kr, col * E, t * kts), buf_cols<In, CPL>(vr, col * E, t * vts),
+             ak, av, x);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
-          // Padded tokens add +0, as the reference's zero-padded pages do.
-          ak[j] = ak[j] + (live ? xk[j] : 0.0f);
-          av[j] = av[j] + (live ? xv[j] : 0.0f);
-          if (live) {
-            kmax[j] = nanmax(kmax[j], xk[j]);
-            kmin[j] = nanmin(kmin[j], xk[j]);
-          }
+          kmax[j] = max3_nan(kmax[j], x[j], x[j]);
+          kmin[j] = min3_nan(kmin[j], x[j], x[j]);
         }
+      }
+      // the chunk's padded tokens each add +0, as the reference's zero-padded
+      // pages do (repeated +0 adds equal one)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        ak[j] = ak[j] + 0.0f;
+        av[j] = av[j] + 0.0f;
       }
     }
 #pragma unroll
@@ -210,19 +275,17 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
   // ---- pass 2: per-token radius (RADSUM) and value norm (NORMSUM) ------
   const int l8 = lane & 7;
   const int g8 = lane >> 3;
-  const int base = lane & ~7;
   float r2max = kNegInf, vnmax = kNegInf;
   for (int t0 = 0; t0 < cnt; t0 += 8) {
     const int t = t0 + g8;
     const bool on = t < cnt;
     const int tt = on ? t : 0;
-    const typename In::T* kr = keys + h * k_hs + (bb * block + tt) * k_ts;
-    const typename In::T* vr = values + h * v_hs + (bb * block + tt) * v_ts;
+    const int ko = tt * kts + l8 * E, vo = tt * vts + l8 * E;
     float kx[D / 8], vx[D / 8];
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
-      kx[m] = elem_f32<In>(kr + 8 * m + l8);
-      vx[m] = elem_f32<In>(vr + 8 * m + l8);
+      kx[m] = buf_elem<In>(kr, ko + 8 * m * E);
+      vx[m] = buf_elem<In>(vr, vo + 8 * m * E);
     }
     float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f, an = 0.0f;
 #pragma unroll
@@ -237,16 +300,17 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
       an = __builtin_fmaf(vx[m], vx[m], an);
     }
     const float P = ((A0 + A1) + A2) + A3;
-    float tot = 0.0f;
-    float vt = shfl(an, base);
+    // the group's lanes added left to right: a DPP scan whose last lane
+    // (l8 == 7) holds ((P0 + P1) + P2) + ... + P7
+    float tot = P, vt = an;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) tot = tot + shfl(P, base + j);
-#pragma unroll
-    for (int j = 1; j < 8; ++j) vt = vt + shfl(an, base + j);
-    if (on) {
-      r2max = nanmax(r2max, tot);
-      vnmax = nanmax(vnmax, sqrtf(vt));
+    for (int j = 1; j < 8; ++j) {
+      tot = row_shr<1>(tot) + P;
+      vt = row_shr<1>(vt) + an;
     }
+    const bool last = on && l8 == 7;
+    r2max = nanmax(r2max, last ? tot : kNegInf);
+    vnmax = nanmax(vnmax, last ? sqrtf(vt) : kNegInf);
   }
   r2max = wave_nanmax(r2max);
   vnmax = wave_nanmax(vnmax);
@@ -366,6 +430,12 @@ int summary_impl(const char* who, const void* keys, int64_t k_head_stride,
   const int64_t n_blocks = (length + block_size - 1) / block_size;
   if ((n_blocks + kSummaryWaves - 1) / kSummaryWaves > 0x7FFFFFFF)
     return set_error(kInvalidArgument, "%s: too many blocks", who);
+  // one block's rows are addressed with 31-bit byte offsets
+  const int64_t row_limit = (int64_t{1} << 31) / (block_size * elem);
+  if (k_token_stride >= row_limit || v_token_stride >= row_limit ||
+      (store && (ck_token_stride >= row_limit || cv_token_stride >= row_limit)))
+    return set_error(kUnsupported, "%s: token stride above %lld elements", who,
+                     (long long)(row_limit - 1));
   switch (dtype) {
     case 0: {
       const CacheOut<InBf16> out{static_cast<uint16_t*>(cache_keys), ck_head_stride,

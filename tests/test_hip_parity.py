@@ -140,6 +140,8 @@ SUMMARY_CASES = [
     (torch.bfloat16, 256, 32, 999), (torch.float16, 128, 32, 777), (torch.float16, 64, 64, 200),
     (torch.float32, 128, 32, 999), (torch.float32, 32, 16, 517), (torch.float32, 96, 64, 1000),
     (torch.float32, 256, 16, 400), (torch.bfloat16, 128, 32, 1), (torch.bfloat16, 64, 64, 63),
+    # the largest blocks (64 KiB and 128 KiB of K plus V)
+    (torch.float32, 256, 64, 300), (torch.float32, 128, 64, 700),
 ]
 
 
@@ -176,9 +178,22 @@ def test_summary_of_strided_cache_view(hip, oracle_lib):
     assert s2.keys.data_ptr() == ck.data_ptr()
 
 
+def test_summary_of_rows_not_16_byte_aligned(hip, oracle_lib):
+    """Rows 4-byte but not 16-byte aligned (a column slice of a wider buffer,
+    token stride not a multiple of the row size)."""
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    wide_k = torch.randn(3, 777, 98, generator=gen, device=DEV).to(torch.bfloat16)
+    wide_v = torch.randn(3, 777, 98, generator=gen, device=DEV).to(torch.bfloat16)
+    k, v = wide_k[:, :, 2:], wide_v[:, :, 2:]
+    summary = build_summary(k, v, RefineKVConfig(backend="hip", block_size=32))
+    ref = oracle_lib.summary(k.float().cpu().numpy(), v.float().cpu().numpy(), 32)
+    torch.cuda.synchronize()
+    assert_summary_equal(summary, ref)
+
+
 @pytest.mark.parametrize("dtype,dim,block,length", [
     (torch.bfloat16, 128, 32, 4099), (torch.bfloat16, 64, 16, 300), (torch.float16, 128, 32, 777),
-    (torch.float32, 96, 64, 1000), (torch.bfloat16, 256, 32, 999)])
+    (torch.float32, 96, 64, 1000), (torch.bfloat16, 256, 32, 999), (torch.float32, 256, 64, 300)])
 def test_summary_written_with_the_cache(hip, dtype, dim, block, length):
     """store_and_build_summary (one kernel: cache write + summary) equals a
     cache copy followed by build_summary, bit for bit, and fills the cache."""
