@@ -113,22 +113,40 @@ inline int64_t rows_per_pass(int64_t group, int64_t dim) {
 // Shared scalar math (reference.py:16-34), identical to the CPU oracle.
 // ---------------------------------------------------------------------------
 // The delta-only terms of a (row, block) pair, computed once by the score
-// kernel: log cosh delta (reference.py:19-22) and the two factors the risk
+// phase: log cosh delta (reference.py:19-22) and the two factors the risk
 // (reference.py:24-34) multiplies in -- A = cosh(delta) - 1 written as
 // 0.5 (t + 1/t) - 1 with t = e^delta (delta <= 10), or log(cosh(delta) - 1)
 // in its large-delta form; th = tanh(delta / 2) in the matching form.
-__device__ __forceinline__ void delta_terms(float delta, float& log_cosh, float& A, float& th) {
+// Every lane computes the small-delta forms (on delta clamped to kDeltaMax);
+// lanes with a larger delta (rare) take the large-delta forms behind a
+// wave-uniform branch, so the common case is branch-free.  The terms come in
+// two parts: log cosh delta, which the LSE partials need, and the risk's
+// factors A and th, which only the decision needs (computed after the
+// partials are out).  t = e^min(delta, kDeltaMax) passes between them.
+__device__ __forceinline__ float delta_log_cosh(float delta, float& t) {
   const float c = clamp_max(delta, kDeltaMax);
-  const float t = expf_(c);
-  if (delta <= kDeltaMax) {
-    log_cosh = logf_((t + expf_(-c)) * 0.5f);
-    A = (0.5f * (t + 1.0f / t)) - 1.0f;
-    th = (t - 1.0f) / (t + 1.0f);
-  } else {
-    log_cosh = delta + logf_((1.0f + expf_(-2.0f * delta)) * 0.5f);
-    const float exp_neg = expf_(-delta);
-    A = (delta + 2.0f * logf_(clamp_min(1.0f - exp_neg, 1e-30f))) - kLn2;
-    th = (1.0f - exp_neg) / (1.0f + exp_neg);
+  t = expf_(c);
+  float log_cosh = logf_((t + expf_(-c)) * 0.5f);
+  const bool large = !(delta <= kDeltaMax);  // NaN takes the large form, as on the host
+  if (__ballot(large) != 0) {
+    const float d = large ? delta : 0.0f;
+    const float lc = d + logf_((1.0f + expf_(-2.0f * d)) * 0.5f);
+    log_cosh = large ? lc : log_cosh;
+  }
+  return log_cosh;
+}
+
+__device__ __forceinline__ void delta_factors(float delta, float t, float& A, float& th) {
+  A = (0.5f * (t + 1.0f / t)) - 1.0f;
+  th = (t - 1.0f) / (t + 1.0f);
+  const bool large = !(delta <= kDeltaMax);
+  if (__ballot(large) != 0) {
+    const float d = large ? delta : 0.0f;
+    const float exp_neg = expf_(-d);
+    const float la = (d + 2.0f * logf_(clamp_min(1.0f - exp_neg, 1e-30f))) - kLn2;
+    const float lt = (1.0f - exp_neg) / (1.0f + exp_neg);
+    A = large ? la : A;
+    th = large ? lt : th;
   }
 }
 
@@ -194,6 +212,7 @@ struct ScoreArgs {
   int group;
   int summary_heads;          // query head h reads the summaries of head h % summary_heads
   float scale;
+  float ln_full, ln_last;     // logf_ of a full block's and of the last block's token count
 };
 
 // q and bf16(q^2) are staged once per workgroup in LDS as fp32, each row as
@@ -363,30 +382,26 @@ __device__ __forceinline__ void score_stats(const ScoreArgs& a, int64_t tile, co
                                             const float* pdot, PutZ put_z, PutLse put_lse) {
   const int G = a.group;
   const int64_t N = a.n_blocks;
-  const int tid = threadIdx.x, lane = tid % kWave, wave = tid / kWave;
-  // ln(count): every block holds block_size tokens except the last.
-  const float ln_full = logf_((float)a.block);
-  const float ln_last = logf_((float)(a.length - (N - 1) * a.block));
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
   for (int g = wave; g < G; g += kWaves) {
+    // Branch-free (lanes past the last block compute on its dot products and
+    // take -inf): the z row's LSE chain interleaves with the delta terms.
     const int64_t b = tile * kTile + lane;
     const bool valid = b < N;
-    float z = kNegInf, zc = kNegInf;
-    float4 zf = make_float4(kNegInf, 0.0f, 0.0f, 0.0f);
-    if (valid) {
-      const float s = sdot[g * kTile + lane] * a.scale;
-      const float dl = (sqrtf(clamp_min(pdot[g * kTile + lane], 0.0f)) * a.scale) * kInflate;
-      z = s + (b == N - 1 ? ln_last : ln_full);
-      float lcosh, ra, rth;
-      delta_terms(dl, lcosh, ra, rth);
-      zc = z + lcosh;
-      zf = make_float4(z, dl, ra, rth);
-    }
-    put_z(g, valid, zf);
+    const float s = sdot[g * kTile + lane] * a.scale;
+    const float z = valid ? s + (b == N - 1 ? a.ln_last : a.ln_full) : kNegInf;
     const float zm = wave_nanmax_u(z);
     const float zl = wave_sum_u(expf_(z - inf_to_zero(zm)));
+    const float dl = (sqrtf(clamp_min(pdot[g * kTile + lane], 0.0f)) * a.scale) * kInflate;
+    float t;
+    const float zc = valid ? z + delta_log_cosh(dl, t) : kNegInf;
     const float cm = wave_nanmax_u(zc);
     const float cl = wave_sum_u(expf_(zc - inf_to_zero(cm)));
     if (lane == 0) put_lse(g, make_float4(zm, zl, cm, cl));
+    float ra, rth;
+    delta_factors(dl, t, ra, rth);
+    put_z(g, valid, valid ? make_float4(z, dl, ra, rth) : make_float4(kNegInf, 0.0f, 0.0f, 0.0f));
   }
 }
 
@@ -486,7 +501,8 @@ template <bool kStats = true>
 __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t h,
                                                     int64_t tile, int64_t rh = -1) {
   if (rh < 0) rh = h;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
   const int64_t b = tile * kTile + lane;
@@ -597,6 +613,22 @@ __device__ __forceinline__ float merge_lse_chunks(const float (&m)[kChunks],
   return logf_(wave_sum_u(acc)) + ms;
 }
 
+// Both merges of one row (z and c): for T <= 64 (one tile per lane) a single
+// branch-free block, so that the two independent chains interleave; the same
+// operations as merge_lse_chunks, whose chunks past the first then hold
+// m = -inf, l = 0 and change nothing.
+__device__ __forceinline__ float2 merge_lse_pair(const RowLse& r, uint32_t T, int lane) {
+  if (T > (uint32_t)kWave)
+    return make_float2(merge_lse_chunks(r.zm, r.zl, T, lane),
+                       merge_lse_chunks(r.cm, r.cl, T, lane));
+  const float sz = inf_to_zero(wave_nanmax_u(r.zm[0]));
+  const float sc = inf_to_zero(wave_nanmax_u(r.cm[0]));
+  const bool live = (uint32_t)lane < T;
+  const float az = live ? r.zl[0] * expf_(r.zm[0] - sz) : 0.0f;
+  const float ac = live ? r.cl[0] * expf_(r.cm[0] - sc) : 0.0f;
+  return make_float2(logf_(wave_sum_u(az)) + sz, logf_(wave_sum_u(ac)) + sc);
+}
+
 template <bool kFused = false>
 __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
                                                   const DecideLoads& in, DecideShared& sh,
@@ -605,7 +637,8 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
                                                   const StepStats* ss = nullptr,
                                                   int64_t rh = -1) {
   if (rh < 0) rh = h;
-  const int tid = threadIdx.x, wave = tid / kWave, lane = tid % kWave;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
   const int G = a.group;
   const int64_t N = a.n_blocks, T = a.n_tiles;
   const int64_t b = tile * kTile + lane;
@@ -640,8 +673,8 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
 #pragma unroll 1
     for (int g = wave; g < G; g += kWaves) {
       const RowLse rl = gather_lse(*ss, (h * G + g) * a.tile_stride, (uint32_t)T, lane);
-      row_tail(g, merge_lse_chunks(rl.zm, rl.zl, (uint32_t)T, lane),
-               merge_lse_chunks(rl.cm, rl.cl, (uint32_t)T, lane), ss->zs[g][lane]);
+      const float2 lzc = merge_lse_pair(rl, (uint32_t)T, lane);
+      row_tail(g, lzc.x, lzc.y, ss->zs[g][lane]);
     }
   } else {
     auto row_stats = [&](int g, float4 part, float4 zf) {
@@ -1074,9 +1107,71 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
 // LDS, the decision waits until every tile of the head has published its
 // LSE partials, the partials are published with coherent stores and the
 // head's last tile merges them.
+//
+// attend_tile's loads that do not depend on the statistics or the decision:
+// the one-launch step issues them before its statistics, so they land while
+// the statistics are computed.
+template <int D, int GBM>
+struct AttendLoads {
+  DecideLoads din;
+  uint32_t S;                            // suffix length
+  RawBf16<D / 16> vraw[kTile / 16];      // value means of the lane group's blocks
+  RawBf16<D / 16> qraw[GBM];             // the pass's query rows
+  RawBf16<D / 16> ksr[1], vsr[1];        // the lane group's first suffix token
+};
+
+template <int D, int GBM, bool kFused>
+__device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a) {
+  constexpr int CH = D / 16;
+  constexpr int NB = kTile / 16;
+  const DecideArgs& da = a.decide;
+  const int64_t h = blockIdx.y;
+  const uint32_t tile = blockIdx.x;
+  const int G = da.group;
+  const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
+  const int tid = threadIdx.x;
+  const int lg = tid >> 4, c = tid & 15;
+  const int g0 = blockIdx.z * GBM;
+  AttendLoads<D, GBM> ld;
+  ld.din = decide_issue<!kFused>(da, h, tile);
+  // The suffix length does not change during a launch: a scalar load from
+  // the constant address space, outside the vector loads' in-order count.
+  uint32_t S = (uint32_t)a.suffix_cap;
+  if (a.suffix_len_dev) {
+    typedef __attribute__((address_space(4))) const int32_t ConstI32;
+    const int32_t sl = *(ConstI32*)(uintptr_t)a.suffix_len_dev;
+    S = sl < 0 ? 0u : ((uint32_t)sl > S ? S : (uint32_t)sl);
+  }
+  ld.S = S;
+  // value means of this lane group's blocks lg + 16 i
+  const uint16_t* vm = a.value_mean + (h * N) * D + c * CH;
+#pragma unroll
+  for (int i = 0; i < NB; ++i) {
+    uint32_t b = tile * kTile + lg + 16 * i;
+    b = b < N ? b : N - 1;
+    ld.vraw[i] = load_raw<CH>(vm + b * D);
+  }
+  const uint16_t* qh = a.query + (h * G) * D + c * CH;
+#pragma unroll
+  for (int g = 0; g < GBM; ++g)
+    ld.qraw[g] = load_raw<CH>(qh + (g0 + g < G ? g0 + g : G - 1) * D);
+  // This tile's slice of the suffix: tokens tile, tile + T, ... (< S); the
+  // first 16 of them, one per lane group, are prefetched here.
+  const uint32_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0u;
+  const uint32_t n_pre = n_suffix < 16u ? n_suffix : 16u;
+  const uint16_t* kbase = a.key_pages + h * a.kp_hs;
+  const uint16_t* vbase = a.value_pages + h * a.vp_hs;
+  const bool has = (uint32_t)lg < n_pre;
+  const uint64_t t = has ? tile + (uint32_t)lg * T : 0u;
+  ld.ksr[0] = load_raw<CH>((has ? a.key_suffix + h * a.ks_hs + t * a.ks_ts : kbase) + c * CH);
+  ld.vsr[0] = load_raw<CH>((has ? a.value_suffix + h * a.vs_hs + t * a.vs_ts : vbase) + c * CH);
+  return ld;
+}
+
 template <int D, int GBM, bool kFused>
 __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& dsh,
-                                            CombineShared<D, GBM>& cmb, const StepCtx* sx) {
+                                            CombineShared<D, GBM>& cmb, const StepCtx* sx,
+                                            const AttendLoads<D, GBM>& ld) {
   constexpr int CH = D / 16;
   constexpr int R = kRowBatch;
   constexpr int NB = kTile / 16;  // representatives per lane group
@@ -1091,25 +1186,18 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   const int lg = tid >> 4, c = tid & 15;
   const int g0 = blockIdx.z * GBM, gn = min(GBM, G - g0);  // this pass's query rows
 
-  // ---- loads independent of the decision ---------------------------------
-  DecideLoads din = decide_issue<!kFused>(da, h, tile);
-  // The suffix length does not change during a launch: a scalar load from
-  // the constant address space, outside the vector loads' in-order count.
-  uint32_t S = (uint32_t)a.suffix_cap;
-  if (a.suffix_len_dev) {
-    typedef __attribute__((address_space(4))) const int32_t ConstI32;
-    const int32_t sl = *(ConstI32*)(uintptr_t)a.suffix_len_dev;
-    S = sl < 0 ? 0u : ((uint32_t)sl > S ? S : (uint32_t)sl);
-  }
-  // value means, z and row maxima of this lane group's blocks lg + 16 i
-  RawBf16<CH> vraw[NB];
+  // ---- what attend_issue loaded; z and the row maxima from the statistics -
+  const DecideLoads& din = ld.din;
+  const uint32_t S = ld.S;
+  const auto& vraw = ld.vraw;
+  const auto& qraw = ld.qraw;
+  const auto& ksr = ld.ksr;
+  const auto& vsr = ld.vsr;
   float zr[GBM][NB], mt[GBM];
-  const uint16_t* vm = a.value_mean + (h * N) * D + c * CH;
 #pragma unroll
   for (int i = 0; i < NB; ++i) {
     uint32_t b = tile * kTile + lg + 16 * i;
     b = b < N ? b : N - 1;
-    vraw[i] = load_raw<CH>(vm + b * D);
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       const int gg = g0 + g < G ? g0 + g : G - 1;
@@ -1123,12 +1211,6 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     if constexpr (kFused) mt[g] = sx->mts[gg];
     else mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
   }
-  RawBf16<CH> qraw[GBM];
-  const uint16_t* qh = a.query + (h * G) * D + c * CH;
-#pragma unroll
-  for (int g = 0; g < GBM; ++g) qraw[g] = load_raw<CH>(qh + (g0 + g < G ? g0 + g : G - 1) * D);
-  // This tile's slice of the suffix: tokens tile, tile + T, ... (< S); the
-  // first 16 of them, one per lane group, are prefetched here.
   const uint32_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0u;
   const uint32_t n_pre = n_suffix < 16u ? n_suffix : 16u;
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
@@ -1136,14 +1218,6 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   const uint16_t* ks = a.key_suffix + h * a.ks_hs;
   const uint16_t* vs = a.value_suffix + h * a.vs_hs;
   const uint32_t kts = (uint32_t)a.ks_ts, vts = (uint32_t)a.vs_ts;
-  RawBf16<CH> ksr[1], vsr[1];
-  {
-    const bool has = (uint32_t)lg < n_pre;
-    const uint64_t t = has ? tile + (uint32_t)lg * T : 0u;
-    ksr[0] = load_raw<CH>((has ? ks + t * kts : kbase) + c * CH);
-    vsr[0] = load_raw<CH>((has ? vs + t * vts : vbase) + c * CH);
-  }
-
 
   // ---- every representative of this lane group, expanded or not ----------
   GroupState<D, GBM> st;
@@ -1231,16 +1305,19 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       }
       return ok;
     };
+    // two batches in flight; no loads for batches past the last (their
+    // loads would only hold up later waits)
     RawBf16<CH> ka[R], va[R], kb[R], vb[R];
     uint32_t oka = issue(0, ka, va);
-    uint32_t okb = issue(1, kb, vb);
+    uint32_t okb = 0;
+    if (16 * R < n_rows) okb = issue(1, kb, vb);
 #pragma unroll 1
     for (uint32_t k = 0; k * 16 * R < n_rows; k += 2) {
       fold_tokens<D, GBM>(st, qraw, ka, va, oka, a.scale, gn);
-      oka = issue(k + 2, ka, va);
+      if ((k + 2) * 16 * R < n_rows) oka = issue(k + 2, ka, va);
       if ((k + 1) * 16 * R >= n_rows) break;
       fold_tokens<D, GBM>(st, qraw, kb, vb, okb, a.scale, gn);
-      okb = issue(k + 3, kb, vb);
+      if ((k + 3) * 16 * R < n_rows) okb = issue(k + 3, kb, vb);
     }
   };
   const uint32_t last = N - 1, last_count = L - last * B;
@@ -1356,7 +1433,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void attend_kernel(AttendArgs a) {
   __shared__ alignas(16) DecideShared dsh;
   __shared__ alignas(16) CombineShared<D, GBM> cmb;
-  attend_tile<D, GBM, false>(a, dsh, cmb, nullptr);
+  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a);
+  attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld);
 }
 
 
@@ -1435,10 +1513,14 @@ void step_kernel(StepArgs s) {
         s.control + ((int64_t)s.heads + 1) * kLine + h * sa.tile_stride + tile, 1ull,
         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   score_dots<D>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+  // (the epoch is read before the loads below are issued: loads complete in
+  // order, so a later read would wait for them too)
   if (tid == 0) {
     sh.base = epoch * (uint64_t)s.attend.decide.n_tiles;
     sh.tag = (uint32_t)epoch + 1u;
   }
+  // the attention's loads that need no statistics land during them
+  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, true>(s.attend);
   __syncthreads();
   score_stats(
       sa, tile, sh.u.score.sdot, sh.u.score.pdot,
@@ -1450,7 +1532,7 @@ void step_kernel(StepArgs s) {
         sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
       });
   __syncthreads();
-  attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx);
+  attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld);
 }
 
 // ---------------------------------------------------------------------------
@@ -1601,6 +1683,9 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
   sa.group = (int)p.group;
   sa.summary_heads = (int)p.heads;
   sa.scale = (float)pow((double)p.dim, -0.5);
+  // the host and device logf_ agree bit for bit
+  sa.ln_full = logf_((float)p.block);
+  sa.ln_last = logf_((float)(p.length - (p.n_blocks - 1) * p.block));
   return sa;
 }
 
