@@ -1,15 +1,18 @@
 // Prefill summarizer: per-block counts, bf16 mean K/V, centred diagonal
 // ellipsoid and value norms (src/refinekv/summary.py:46-113).
 //
-// One wave per (KV head, block).  Pass 1 streams the block's tokens once with
-// coalesced row loads (each lane owns 2 or 4 adjacent columns) and keeps the
-// column sums, min and max in registers.  Pass 2 re-reads the block (an L2
-// hit: HBM sees each row once) with each 8-lane group owning one token, so the
-// per-token head_dim sums are lane-local.  Every row access is a buffer load
-// from a per-block buffer view (scalar base and token offset, one lane offset,
-// immediate column offsets: no per-load address arithmetic), the block index
-// is wave-uniform, and the min/max use the NaN-propagating v_maximum3 /
-// v_minimum3 forms, which keeps the vector ALU well below the memory time.  Summation orders (fixed, shared with the CPU
+// One wave per (KV head, block).  Pass 1 reads the block's rows with each lane
+// owning 2 or 4 adjacent columns and keeps the column sums, min and max in
+// registers.  Pass 2 reads the rows again with each 8-lane group owning one
+// token, so the per-token head_dim sums are lane-local.  Where a block's K
+// and V fit 64 KiB (kStage), the wave first moves the whole block from HBM
+// into LDS with 16-byte buffer-to-LDS loads (all of it in flight at once) and
+// both passes read LDS: HBM sees each row once.  Larger blocks stream pass 1
+// from global memory and re-read the rows there in pass 2.  Row accesses go
+// through per-block buffer views (scalar base and token offset, one lane
+// offset, immediate column offsets: no per-load address arithmetic; rows past
+// the block's end read 0), the block index is wave-uniform, and the min/max
+// use the NaN-propagating v_maximum3 / v_minimum3 forms.  Summation orders (fixed, shared with the CPU
 // oracle and equal to torch's CPU kernels the reference runs):
 //   column sums   16-token chunks summed left to right from +0, chunk sums
 //                 added left to right from +0;
@@ -114,6 +117,22 @@ __device__ __forceinline__ float buf_elem(__amdgpu_buffer_rsrc_t r, int voff) {
   }
 }
 
+// 16 bytes per lane from a buffer view straight into LDS: lane i's bytes land
+// at lds_base + 16 i (lds_base wave-uniform).
+__device__ __forceinline__ void load_to_lds16(__amdgpu_buffer_rsrc_t r, uint4* lds_base, int voff) {
+  typedef __attribute__((address_space(3))) void LdsVoid;
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (LdsVoid*)lds_base, 16, voff, 0, 0, 0);
+}
+
+template <class In>
+__device__ __forceinline__ float lds_elem(const typename In::T* p) {
+  if constexpr (sizeof(typename In::T) == 2) {
+    return In::cvt(*reinterpret_cast<const uint16_t*>(p));
+  } else {
+    return *p;
+  }
+}
+
 // NaN-propagating max/min (v_maximum3_f32 / v_minimum3_f32).  They differ
 // from nanmax/nanmin only in which zero a +0/-0 tie returns, which no output
 // depends on: a zero extreme enters only |extreme - mean|, clamped to 1e-6.
@@ -126,6 +145,36 @@ __device__ __forceinline__ float min3_nan(float a, float b, float c) {
 
 constexpr int kSummaryWaves = 4;
 constexpr int kTokBatch = 8;  // tokens per batch of pass-1 row loads
+constexpr int64_t kStageWaveMax = 64 * 1024;   // LDS of one staged block, at most
+constexpr int64_t kStageGroupMax = 32 * 1024;  // LDS of a staged workgroup, aimed at
+// Staging pays while a block holds at most 4096 elements per tensor: larger
+// blocks leave too few waves per CU (LDS) for their longer passes, and the
+// two-pass form, whose pass 2 re-reads from the L2 and MALL, is faster.
+constexpr int64_t kStageElemsMax = 4096;
+
+// A staged block in LDS (per wave): its K rows, then its V rows, as 16-byte
+// chunks, then D key means and D inverse widths (fp32).  Chunk c of token t
+// sits at slot c ^ swizzle(t) of the row so that the 8 tokens of one pass-2
+// read start on different banks: pass 2 reads 8 consecutive elements of a
+// row, G chunks (one for 2-byte types, two for fp32); the swizzle stays
+// inside aligned groups of SW * G chunks, SW the largest power of two (at
+// most 8) dividing NC / G (4 for head_dim 32, 96, 160 and 224).
+template <class In, int D>
+struct Staging {
+  static constexpr int E = (int)sizeof(typename In::T);
+  static constexpr int NC = D * E / 16;  // chunks per row
+  static constexpr int EPC = 16 / E;     // elements per chunk
+  static constexpr int G = 8 * E / 16;
+  static constexpr int LOW = (NC / G) & -(NC / G);
+  static constexpr int SW = LOW < 8 ? LOW : 8;
+  static __device__ __forceinline__ int slot(int c, int t) { return c ^ ((t & (SW - 1)) * G); }
+};
+
+// LDS bytes of one wave's block (kStage) or of its means and widths alone.
+__host__ __device__ constexpr int64_t summary_wave_lds(bool stage, int64_t dim, int64_t elem,
+                                                       int64_t block) {
+  return (stage ? 2 * block * dim * elem : 0) + 2 * dim * 4;
+}
 
 // Where the keys and values also go when the summary is built while the
 // prompt is written to the cache (kStore): the same element strides as the
@@ -139,23 +188,27 @@ struct CacheOut {
 };
 
 // Byte strides of a block's rows fit 31 bits (checked on the host).
-template <int D, class In, bool kStore>
+// blockDim.x / 64 waves (1, 2 or 4), one block each, and summary_wave_lds
+// bytes of dynamic LDS per wave.  kStage needs 16-byte aligned rows.
+template <int D, class In, bool kStore, bool kStage>
 __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
     const typename In::T* __restrict__ values, int64_t v_hs, int64_t v_ts, int64_t length,
     int block, int64_t n_blocks, int64_t* __restrict__ counts, uint16_t* __restrict__ key_mean,
     uint16_t* __restrict__ value_mean, uint16_t* __restrict__ ellipsoid,
     float* __restrict__ value_norm, CacheOut<In> out) {
-  constexpr int E = (int)sizeof(typename In::T);
+  using T = typename In::T;
+  using St = Staging<In, D>;
+  constexpr int E = (int)sizeof(T);
   constexpr int CPL = D <= 128 ? 2 : 4;  // columns per lane in pass 1
   constexpr int LANES1 = D / CPL;
-  __shared__ float s_mk[kSummaryWaves][D];
-  __shared__ float s_rs[kSummaryWaves][D];
+  extern __shared__ uint4 s_dyn[];
 
+  const int waves = blockDim.x / kWave;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int lane = threadIdx.x % kWave;
   const int64_t h = blockIdx.y;
-  const int64_t b = (int64_t)blockIdx.x * kSummaryWaves + wave;
+  const int64_t b = (int64_t)blockIdx.x * waves + wave;
   const bool valid = b < n_blocks;
   const int64_t bb = valid ? b : n_blocks - 1;  // in-bounds block for addresses
   // (64-bit compares run on the vector ALU: readfirstlane keeps the counts
@@ -167,10 +220,51 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
   auto extent = [&](int ts) { return __builtin_amdgcn_readfirstlane(cnt ? (cnt - 1) * ts + D * E : 0); };
   const auto kr = rows_view(keys + h * k_hs + bb * block * k_ts, extent(kts));
   const auto vr = rows_view(values + h * v_hs + bb * block * v_ts, extent(vts));
+  const int chunks = kStage ? block * St::NC : 0;  // per tensor, a multiple of 64
+  uint4* kst = s_dyn + wave * (2 * chunks + D / 2);
+  uint4* vst = kst + chunks;
+  float* s_mk = reinterpret_cast<float*>(vst + chunks);
+  float* s_rs = s_mk + D;
+  if constexpr (kStage) {
+    // the whole block in flight: LDS chunk p (token p / NC, slot p % NC)
+    // takes chunk slot(p % NC, t) of that token's row
+    for (int p0 = 0; p0 < chunks; p0 += kWave) {
+      const int p = p0 + lane, t = p / St::NC;
+      const int off = St::slot(p % St::NC, t) * 16;
+      load_to_lds16(kr, kst + p0, t * kts + off);
+      load_to_lds16(vr, vst + p0, t * vts + off);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
 
   // ---- pass 1: column sums (TOKSUM order), min, max -------------------
   const bool on1 = valid && lane < LANES1;
   const int col = lane < LANES1 ? lane * CPL : 0;
+  // this lane's columns in a staged row: chunk c1, 4-byte word w1 within it
+  const int c1 = col / St::EPC, w1 = (col % St::EPC) * E / 4;
+  auto row_cols = [&](const __amdgpu_buffer_rsrc_t& r, const uint4* st, int t, int ts) {
+    if constexpr (kStage) {
+      const uint32_t* w = reinterpret_cast<const uint32_t*>(st + t * St::NC + St::slot(c1, t)) + w1;
+      RawCols<In, CPL> x;
+      constexpr int W = RawCols<In, CPL>::W;
+      if constexpr (W == 1) {
+        x.w[0] = w[0];
+      } else if constexpr (W == 2) {
+        const uint2 u = *reinterpret_cast<const uint2*>(w);
+        x.w[0] = u.x;
+        x.w[1] = u.y;
+      } else {
+        const uint4 u = *reinterpret_cast<const uint4*>(w);
+        x.w[0] = u.x;
+        x.w[1] = u.y;
+        x.w[2] = u.z;
+        x.w[3] = u.w;
+      }
+      return x;
+    } else {
+      return buf_cols<In, CPL>(r, col * E, t * ts);
+    }
+  };
   float ksum[CPL], vsum[CPL], kmax[CPL], kmin[CPL];
 #pragma unroll
   for (int j = 0; j < CPL; ++j) {
@@ -213,8 +307,8 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
         RawCols<In, CPL> rk[kTokBatch], rv[kTokBatch];
 #pragma unroll
         for (int i = 0; i < kTokBatch; ++i) {
-          rk[i] = buf_cols<In, CPL>(kr, col * E, (c0 + i0 + i) * kts);
-          rv[i] = buf_cols<In, CPL>(vr, col * E, (c0 + i0 + i) * vts);
+          rk[i] = row_cols(kr, kst, c0 + i0 + i, kts);
+          rv[i] = row_cols(vr, vst, c0 + i0 + i, vts);
         }
 #pragma unroll
         for (int i = 0; i < kTokBatch; i += 2) {
@@ -231,8 +325,7 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     } else {
       for (int t = c0; t < cnt; ++t) {
         float x[CPL];
-        take(t, buf_cols<In, CPL>(kr, col * E, t * kts), buf_cols<In, CPL>(vr, col * E, t * vts),
-             ak, av, x);
+        take(t, row_cols(kr, kst, t, kts), row_cols(vr, vst, t, vts), ak, av, x);
 #pragma unroll
         for (int j = 0; j < CPL; ++j) {
           kmax[j] = max3_nan(kmax[j], x[j], x[j]);
@@ -266,8 +359,8 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
       const float width = nanmax(kmax[j] - mk, mk - kmin[j]);
       const float cw = clamp_min(width, 1e-6f);
       w2[j] = round_bf16(cw * cw);
-      s_mk[wave][col + j] = mk;
-      s_rs[wave][col + j] = 1.0f / sqrtf(w2[j]);
+      s_mk[col + j] = mk;
+      s_rs[col + j] = 1.0f / sqrtf(w2[j]);
     }
   }
   __syncthreads();
@@ -284,14 +377,21 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     float kx[D / 8], vx[D / 8];
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
-      kx[m] = buf_elem<In>(kr, ko + 8 * m * E);
-      vx[m] = buf_elem<In>(vr, vo + 8 * m * E);
+      if constexpr (kStage) {
+        const int e = 8 * m + l8;
+        const int o = tt * St::NC + St::slot(e / St::EPC, tt);
+        kx[m] = lds_elem<In>(reinterpret_cast<const T*>(kst + o) + e % St::EPC);
+        vx[m] = lds_elem<In>(reinterpret_cast<const T*>(vst + o) + e % St::EPC);
+      } else {
+        kx[m] = buf_elem<In>(kr, ko + 8 * m * E);
+        vx[m] = buf_elem<In>(vr, vo + 8 * m * E);
+      }
     }
     float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f, an = 0.0f;
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
       const int e = 8 * m + l8;
-      const float c = (kx[m] - s_mk[wave][e]) * s_rs[wave][e];
+      const float c = (kx[m] - s_mk[e]) * s_rs[e];
       const float c2 = c * c;
       if ((m & 3) == 0) A0 = A0 + c2;
       if ((m & 3) == 1) A1 = A1 + c2;
@@ -353,24 +453,40 @@ int launch_summary(const void* keys, int64_t k_hs, int64_t k_ts, const void* val
                    float* value_norm, float* max_value_norm, const CacheOut<In>& out,
                    hipStream_t stream) {
   const int64_t n_blocks = (length + block - 1) / block;
-  dim3 grid((unsigned)((n_blocks + kSummaryWaves - 1) / kSummaryWaves), (unsigned)heads);
-  dim3 threads(kWave * kSummaryWaves);
+  const int64_t elem = (int64_t)sizeof(typename In::T);
+  auto rows16 = [&](const void* p, int64_t hs, int64_t ts) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && (hs * elem) % 16 == 0 &&
+           (ts * elem) % 16 == 0;
+  };
+  const bool stage = block * dim <= kStageElemsMax &&
+                     summary_wave_lds(true, dim, elem, block) <= kStageWaveMax &&
+                     rows16(keys, k_hs, k_ts) && rows16(values, v_hs, v_ts);
+  const int64_t per_wave = summary_wave_lds(stage, dim, elem, block);
+  int waves = kSummaryWaves;
+  while (stage && waves > 1 && waves * per_wave > kStageGroupMax) waves /= 2;
+  dim3 grid((unsigned)((n_blocks + waves - 1) / waves), (unsigned)heads);
+  dim3 threads(kWave * waves);
+  const size_t lds = (size_t)(waves * per_wave);
   const auto* k = static_cast<const typename In::T*>(keys);
   const auto* v = static_cast<const typename In::T*>(values);
   auto* km = static_cast<uint16_t*>(key_mean);
   auto* vm = static_cast<uint16_t*>(value_mean);
   auto* el = static_cast<uint16_t*>(ellipsoid);
-  if (out.keys) {
-    RKV_DISPATCH_DIM(dim, D,
-                     summary_kernel<D, In, true><<<grid, threads, 0, stream>>>(
-                         k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, km,
-                         vm, el, value_norm, out));
+#define RKV_SUMMARY_LAUNCH(STORE, STAGE)                                                   \
+  RKV_DISPATCH_DIM(dim, D,                                                                 \
+                   summary_kernel<D, In, STORE, STAGE><<<grid, threads, lds, stream>>>(    \
+                       k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, \
+                       km, vm, el, value_norm, out))
+  if (out.keys && stage) {
+    RKV_SUMMARY_LAUNCH(true, true);
+  } else if (out.keys) {
+    RKV_SUMMARY_LAUNCH(true, false);
+  } else if (stage) {
+    RKV_SUMMARY_LAUNCH(false, true);
   } else {
-    RKV_DISPATCH_DIM(dim, D,
-                     summary_kernel<D, In, false><<<grid, threads, 0, stream>>>(
-                         k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, km,
-                         vm, el, value_norm, out));
+    RKV_SUMMARY_LAUNCH(false, false);
   }
+#undef RKV_SUMMARY_LAUNCH
   int rc = check_launch("summary_kernel");
   if (rc) return rc;
   max_norm_kernel<<<dim3((unsigned)heads), dim3(256), 0, stream>>>(value_norm, n_blocks,
@@ -428,7 +544,7 @@ int summary_impl(const char* who, const void* keys, int64_t k_head_stride,
       return set_error(kInvalidArgument, "%s: cache token stride smaller than head_dim", who);
   }
   const int64_t n_blocks = (length + block_size - 1) / block_size;
-  if ((n_blocks + kSummaryWaves - 1) / kSummaryWaves > 0x7FFFFFFF)
+  if (n_blocks > 0x7FFFFFFF)
     return set_error(kInvalidArgument, "%s: too many blocks", who);
   // one block's rows are addressed with 31-bit byte offsets
   const int64_t row_limit = (int64_t{1} << 31) / (block_size * elem);
