@@ -840,16 +840,16 @@ __device__ __forceinline__ float dot2_bf16(uint32_t a, uint32_t b, float c) {
                                          __builtin_bit_cast(Bf16x2, b), c, false);
 }
 
-template <int D, int GBM>
+template <int D, int GBM, int R = kRowBatch>
 __device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st,
                                             const RawBf16<D / 16> (&q)[GBM],
-                                            const RawBf16<D / 16> (&kr)[kRowBatch],
-                                            const RawBf16<D / 16> (&vr)[kRowBatch], uint32_t ok,
+                                            const RawBf16<D / 16> (&kr)[R],
+                                            const RawBf16<D / 16> (&vr)[R], uint32_t ok,
                                             float scale, int gn) {
   constexpr int CH = D / 16;
-  float x[GBM][kRowBatch], v[kRowBatch][CH];
+  float x[GBM][R], v[R][CH];
 #pragma unroll
-  for (int u = 0; u < kRowBatch; ++u) {
+  for (int u = 0; u < R; ++u) {
     const bool live = (ok >> u) & 1u;
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
@@ -863,7 +863,7 @@ __device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st,
 #pragma unroll
     for (int i = 0; i < CH; ++i) v[u][i] = live ? v[u][i] : 0.0f;
   }
-  fold<D, GBM, kRowBatch>(st, x, v, gn);
+  fold<D, GBM, R>(st, x, v, gn);
 }
 
 // Lane-group states are combined through LDS in chunks of rows small enough
@@ -1274,18 +1274,11 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   }
 
   // ---- the prefetched suffix rows (after the subtraction, which assumes
-  // the representatives' scale) ---------------------------------------------
-  {
-    RawBf16<CH> kr[R], vr[R];
-    kr[0] = ksr[0];
-    vr[0] = vsr[0];
-#pragma unroll
-    for (int u = 1; u < R; ++u) {
-      kr[u] = ksr[0];
-      vr[u] = vsr[0];
-    }
-    fold_tokens<D, GBM>(st, qraw, kr, vr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
-  }
+  // the representatives' scale): lane groups lg < n_pre hold one; a wave
+  // whose four lane groups hold none skips the fold, which would leave its
+  // state unchanged (a masked row adds exp(-inf) = 0 times a zeroed value)
+  if (4 * __builtin_amdgcn_readfirstlane(tid / kWave) < (int)n_pre)
+    fold_tokens<D, GBM, 1>(st, qraw, ksr, vsr, (uint32_t)lg < n_pre ? 1u : 0u, a.scale, gn);
 
   // ---- token rows ---------------------------------------------------------
   // Runs n_rows rows through the online softmax, 16 R rows per batch, two
@@ -1311,12 +1304,14 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     uint32_t oka = issue(0, ka, va);
     uint32_t okb = 0;
     if (16 * R < n_rows) okb = issue(1, kb, vb);
+    // (a wave with no live row in a batch skips its fold: it would leave
+    // the state unchanged)
 #pragma unroll 1
     for (uint32_t k = 0; k * 16 * R < n_rows; k += 2) {
-      fold_tokens<D, GBM>(st, qraw, ka, va, oka, a.scale, gn);
+      if (__ballot(oka != 0)) fold_tokens<D, GBM>(st, qraw, ka, va, oka, a.scale, gn);
       if ((k + 2) * 16 * R < n_rows) oka = issue(k + 2, ka, va);
       if ((k + 1) * 16 * R >= n_rows) break;
-      fold_tokens<D, GBM>(st, qraw, kb, vb, okb, a.scale, gn);
+      if (__ballot(okb != 0)) fold_tokens<D, GBM>(st, qraw, kb, vb, okb, a.scale, gn);
       if ((k + 3) * 16 * R < n_rows) okb = issue(k + 3, kb, vb);
     }
   };
