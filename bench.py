@@ -65,6 +65,9 @@ def parse_args():
                     help="rkv_decode path: one launch per step (default) or three kernels")
     ap.add_argument("--graph-only", action="store_true",
                     help="only the graph-replay timing (for profiler runs)")
+    ap.add_argument("--sweep", action="store_true",
+                    help="the isolated-op sweep (BASELINE.json configs[4]): one JSON line per "
+                         "(context, block, eps, spike fraction) point")
     return ap.parse_args()
 
 
@@ -152,6 +155,9 @@ def main():
         sys.exit(2)
     if a.copy_calibration:
         copy_calibration()
+        return
+    if a.sweep:
+        sweep(a)
         return
     from refinekv import RefineKVConfig, build_summary, sparse_attention, _hip
 
@@ -332,6 +338,92 @@ def main():
         "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
     }
     print(json.dumps(result), flush=True)
+
+
+def sweep(a):
+    """The isolated decode-op sweep of BASELINE.json configs[4]: 8 KV / 32
+    query heads, d 128, bf16, GQA "any"; context x block x eps x spike
+    fraction.  Each (context, block, spikes) gets its own layers (own caches
+    and summaries, enough of them that one graph step touches >= ~1.5 GB of
+    summaries where that fits 256 layers, so the Infinity Cache does not hold
+    a step); each eps is timed as graph replays of decode steps over those
+    layers.  Prints one JSON line per point: us per layer-step, the expanded
+    fraction f, algorithmic bytes and HBM GB/s."""
+    from refinekv import RefineKVConfig, build_summary, sparse_attention, _hip
+
+    assert torch.cuda.is_available(), "bench.py needs a GPU"
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _hip.lib()
+    _hip.set_decode_path("step")  # the three kernels past 256 tiles per head
+    warmup, steps = 2, 10
+    capacity = warmup + steps + 1
+    for context in (8192, 32768, 131072, 524288):
+        for block in (16, 32, 64):
+            n = -(-context // block)
+            per_layer = a.heads * n * a.dim * 2 * 3  # key/value means and ellipsoid
+            n_layers = max(4, min(256, -(-1_500_000_000 // per_layer)))
+            for spikes in (0.01, 0.05, 0.2):
+                pa = argparse.Namespace(**{**vars(a), "context": context, "block": block,
+                                          "spikes": spikes})
+                gen = torch.Generator(device=dev).manual_seed(a.seed)
+                layers = []
+                for _ in range(n_layers):
+                    q, k, v = make_layer(gen, pa, capacity, dev)
+                    cfg0 = RefineKVConfig(backend="hip", block_size=block)
+                    layers.append(dict(q=q, k=k, v=v, ws={},
+                                       summary=build_summary(k[:, :context], v[:, :context], cfg0)))
+                torch.cuda.synchronize()
+                suffix_len = torch.zeros((), dtype=torch.int32, device=dev)
+                for eps in (0.001, 0.01, 0.1):
+                    cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps,
+                                         gqa_reduction=a.reduction)
+                    for L in layers:
+                        L["ws"] = {}
+
+                    def step():
+                        suffix_len.add_(1)
+                        for L in layers:
+                            sparse_attention(L["q"], L["summary"], L["k"][:, context:],
+                                             L["v"][:, context:], cfg, workspace=L["ws"],
+                                             suffix_length=suffix_len)
+
+                    suffix_len.fill_(0)
+                    for _ in range(warmup):
+                        step()
+                    torch.cuda.synchronize()
+                    graph = torch.cuda.CUDAGraph()
+                    with torch.cuda.graph(graph):
+                        step()
+                    torch.cuda.synchronize()
+                    e0 = torch.cuda.Event(enable_timing=True)
+                    e1 = torch.cuda.Event(enable_timing=True)
+                    e0.record()
+                    for _ in range(steps):
+                        graph.replay()
+                    e1.record()
+                    torch.cuda.synchronize()
+                    us = e0.elapsed_time(e1) * 1e3 / (steps * n_layers)
+                    del graph
+                    masks = torch.stack([
+                        sparse_attention(L["q"], L["summary"], L["k"][:, context:],
+                                         L["v"][:, context:], cfg, workspace=L["ws"],
+                                         return_selected=True,
+                                         suffix_length=suffix_len).selected.clone()
+                        for L in layers])
+                    f = masks.float().mean().item()
+                    nbytes = algorithmic_bytes(pa, masks, layers[0]["summary"].counts,
+                                               int(suffix_len.item()))["decode"]
+                    gbps = nbytes / (us * 1e-6) / 1e9
+                    tiles = -(-n // 64)
+                    point = dict(context=context, block=block, eps=eps, spikes=spikes,
+                                 layers=n_layers, path="step" if tiles <= 256 else "split",
+                                 us_per_layer_step=round(us, 2), expanded_fraction=round(f, 5),
+                                 algorithmic_bytes=int(nbytes), GBps=round(gbps, 1),
+                                 frac_of_peak=round(gbps / PEAK_HBM_GBPS, 4))
+                    print(json.dumps(point), flush=True)
+                del layers
+                torch.cuda.empty_cache()
 
 
 def measured_traffic(kernel):

@@ -93,10 +93,12 @@ size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_
  * same as tagged 16-byte slots for the one-launch step), part_ml, part_acc
  * (per-tile attention partials: (m, l) and acc), counts (per-tile access
  * counts), xbits (per-tile expanded-block masks, tagged slots), total, then
- * n_tiles and the padded row strides (elements) of zf and of the per-tile
- * arrays -> out12[0..11]. */
+ * n_tiles, the padded row strides (elements) of zf and of the per-tile
+ * arrays, and the one-launch step's workgroups per KV head (n_tiles scoring
+ * tiles, then helpers that only attend token rows; each has a call counter
+ * and a per-tile array entry) -> out13[0..12]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                         int64_t* out12);
+                         int64_t* out13);
 
 /*
  * Expanded-block mask for one query.  Replaces select_blocks_triton

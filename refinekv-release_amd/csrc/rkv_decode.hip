@@ -63,6 +63,7 @@ inline void mark(int i, hipStream_t stream) {
 // ---------------------------------------------------------------------------
 struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
+  int64_t step_workers;  // workgroups per head of the one-launch step
   int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, xbits, total;
 };
 
@@ -73,6 +74,12 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
   L.z_stride = L.n_tiles * kTile;
   L.tile_stride = (L.n_tiles + 63) / 64 * 64;
+  // The one-launch step runs max(n_tiles, 512 / heads) workgroups per head
+  // (at most tile_stride): the n_tiles tiles and, with short prompts, copies
+  // of them that also take a share of the head's suffix and expanded token
+  // rows, so that the token work spreads over the GPU (two workgroups per CU).
+  const int64_t want = 512 / heads;
+  L.step_workers = L.n_tiles > want ? L.n_tiles : (want < L.tile_stride ? want : L.tile_stride);
   const int64_t rows = heads * group;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -788,6 +795,7 @@ struct AttendArgs {
   int64_t kp_hs, vp_hs, ks_hs, ks_ts, vs_hs, vs_ts;
   int64_t suffix_cap;
   int log2_block;  // block_size is 16, 32 or 64
+  int workers;     // workgroups per head (gridDim.x): n_tiles, or the step's step_workers
   float scale;
 };
 
@@ -940,7 +948,7 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
 // (first row, row count).  Integer arithmetic only: every tile sees the same
 // split.
 __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
-                               uint32_t tile, int lb) {
+                               uint32_t W, uint32_t tile, int lb) {
   const int lane = threadIdx.x % kWave;
   const uint32_t tag = *sx.stats.tag;
   uint64_t bm[kChunks];
@@ -978,7 +986,7 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
     total += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
   }
   const uint64_t R = (uint64_t)total << lb;
-  const uint64_t r0 = (uint64_t)tile * R / T, r1 = ((uint64_t)tile + 1) * R / T;
+  const uint64_t r0 = (uint64_t)tile * R / W, r1 = ((uint64_t)tile + 1) * R / W;
   const uint32_t e0 = (uint32_t)(r0 >> lb);
   const uint32_t e1 = (uint32_t)((r1 + (1u << lb) - 1) >> lb);
 #pragma unroll
@@ -1034,7 +1042,8 @@ constexpr int kMergers = 8;
 template <int D>
 __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, int m, int K) {
   const DecideArgs& da = a.decide;
-  const int G = da.group, T = (int)da.n_tiles;
+  // the head's partials: one per workgroup of the launch
+  const int G = da.group, T = a.workers;
   const int64_t ts = da.tile_stride;
   const int tid = threadIdx.x;
   constexpr int Q = D / 4;
@@ -1082,7 +1091,8 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
   // the step's access count: this head's tile counts, added once
   if (sx.accessed && m == 0) {
     unsigned long long c = 0;
-    for (int t = tid; t < T; t += kThreads) c += sx.counts.load_u32((uint32_t)((h * ts + t) * 4));
+    for (int t = tid; t < (int)da.n_tiles; t += kThreads)
+      c += sx.counts.load_u32((uint32_t)((h * ts + t) * 4));
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, kWave);
     if (tid % kWave == 0) sx.wsum[tid / kWave] = c;
@@ -1126,9 +1136,11 @@ __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a)
   constexpr int NB = kTile / 16;
   const DecideArgs& da = a.decide;
   const int64_t h = blockIdx.y;
-  const uint32_t tile = blockIdx.x;
+  // workgroup wk of the head's W scores tile wk % T (copies past the first T)
+  const uint32_t wk = blockIdx.x, tile = wk % (uint32_t)da.n_tiles;
   const int G = da.group;
-  const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
+  const uint32_t N = (uint32_t)da.n_blocks;
+  const uint32_t W = (uint32_t)a.workers;  // the suffix is sliced over the workgroups
   const int tid = threadIdx.x;
   const int lg = tid >> 4, c = tid & 15;
   const int g0 = blockIdx.z * GBM;
@@ -1155,14 +1167,14 @@ __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a)
 #pragma unroll
   for (int g = 0; g < GBM; ++g)
     ld.qraw[g] = load_raw<CH>(qh + (g0 + g < G ? g0 + g : G - 1) * D);
-  // This tile's slice of the suffix: tokens tile, tile + T, ... (< S); the
+  // This workgroup's slice of the suffix: tokens wk, wk + W, ... (< S); the
   // first 16 of them, one per lane group, are prefetched here.
-  const uint32_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0u;
+  const uint32_t n_suffix = S > wk ? (S - wk + W - 1) / W : 0u;
   const uint32_t n_pre = n_suffix < 16u ? n_suffix : 16u;
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
   const uint16_t* vbase = a.value_pages + h * a.vp_hs;
   const bool has = (uint32_t)lg < n_pre;
-  const uint64_t t = has ? tile + (uint32_t)lg * T : 0u;
+  const uint64_t t = has ? wk + (uint32_t)lg * W : 0u;
   ld.ksr[0] = load_raw<CH>((has ? a.key_suffix + h * a.ks_hs + t * a.ks_ts : kbase) + c * CH);
   ld.vsr[0] = load_raw<CH>((has ? a.value_suffix + h * a.vs_hs + t * a.vs_ts : vbase) + c * CH);
   return ld;
@@ -1178,13 +1190,20 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   using Comb = CombineShared<D, GBM>;
   const DecideArgs& da = a.decide;
   const int64_t h = blockIdx.y;
-  const uint32_t tile = blockIdx.x;
   const int G = da.group;
   const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
   const uint32_t L = (uint32_t)da.length, lb = (uint32_t)a.log2_block, B = 1u << lb;
   const int tid = threadIdx.x;
   const int lg = tid >> 4, c = tid & 15;
   const int g0 = blockIdx.z * GBM, gn = min(GBM, G - g0);  // this pass's query rows
+  // The launch's W workgroups per head: workgroup wk scores tile wk % T.
+  // With short prompts the one-launch step runs copies of the T tiles (wk >=
+  // T) so that the suffix and the head's expanded token rows spread over more
+  // workgroups: a copy repeats its tile's scores and decision (publishing the
+  // same slots, bit for bit) but adds no representatives of its own.
+  const uint32_t W = (uint32_t)a.workers;
+  const uint32_t wk = blockIdx.x, tile = wk % T;
+  const bool primary = wk < T;
 
   // ---- what attend_issue loaded; z and the row maxima from the statistics -
   const DecideLoads& din = ld.din;
@@ -1211,7 +1230,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     if constexpr (kFused) mt[g] = sx->mts[gg];
     else mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
   }
-  const uint32_t n_suffix = S > tile ? (S - tile + T - 1) / T : 0u;
+  const uint32_t n_suffix = S > wk ? (S - wk + W - 1) / W : 0u;
   const uint32_t n_pre = n_suffix < 16u ? n_suffix : 16u;
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
   const uint16_t* vbase = a.value_pages + h * a.vp_hs;
@@ -1235,7 +1254,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       for (int e = 0; e < CH; ++e) st.acc[g][e] = 0.0f;
 #pragma unroll
       for (int i = 0; i < NB; ++i) {
-        const bool valid = tile * kTile + lg + 16 * i < N;
+        const bool valid = primary && tile * kTile + lg + 16 * i < N;
         pw[g][i] = valid ? __builtin_amdgcn_exp2f((zr[g][i] - m) * kLog2e) : 0.0f;
         st.l[g] = st.l[g] + pw[g][i];
 #pragma unroll
@@ -1331,7 +1350,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   const uint32_t own_rows = kFused ? 0u : (uint32_t)__popcll(bits) * B;
   run_rows(n_rest + own_rows, [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) {
     if (v < n_rest) {
-      const uint64_t t = tile + (n_pre + v) * T;
+      const uint64_t t = wk + (n_pre + v) * W;
       kp = ks + t * kts;
       vp = vs + t * vts;
       return true;
@@ -1343,7 +1362,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   // ---- then (one-launch step): this tile's share of the head's expanded
   // rows, once every tile of the head has published its mask ---------------
   if constexpr (kFused) {
-    if (tid < kWave) expanded_share(*sx, h, da.tile_stride, T, tile, (int)lb);
+    if (tid < kWave) expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb);
     __syncthreads();
     const int32_t* xl = sx->xl;
     const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
@@ -1387,7 +1406,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
         a1 = __builtin_fmaf(av.y, e, a1);
         l = __builtin_fmaf(cmb.ml[w][j][1], e, l);
       }
-      const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + tile;
+      const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + wk;
       if constexpr (kFused) {
         sx->acc.store2((uint32_t)((at * D + d) * 4), make_float2(a0, a1));
         if (d == 0) sx->ml.store2((uint32_t)(at * 8), make_float2(M, l));
@@ -1398,8 +1417,9 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     }
   }
   if (a.tile_counts && tid == 0 && blockIdx.z == 0) {
-    if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + tile) * 4), count);
-    else a.tile_counts[h * da.tile_stride + tile] = count;
+    // (a copy's count sits past the first T entries, which alone are summed)
+    if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + wk) * 4), count);
+    else a.tile_counts[h * da.tile_stride + wk] = count;
   }
   if constexpr (kFused) {
     // publish and take a ticket; the head's last K tiles wait for the rest
@@ -1414,11 +1434,11 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     }
     __syncthreads();
     const uint32_t ticket = *sx->flag;
-    const uint32_t K = T < (uint32_t)kMergers ? T : (uint32_t)kMergers;
-    if (ticket >= T - K) {
-      if (tid == 0) wait_counter<uint64_t>(merged, *sx->base + T, kSpinLimit, sx->error());
+    const uint32_t K = W < (uint32_t)kMergers ? W : (uint32_t)kMergers;
+    if (ticket >= W - K) {
+      if (tid == 0) wait_counter<uint64_t>(merged, *sx->base + W, kSpinLimit, sx->error());
       __syncthreads();
-      merge_slice<D>(a, *sx, h, (int)(ticket - (T - K)), (int)K);
+      merge_slice<D>(a, *sx, h, (int)(ticket - (W - K)), (int)K);
     }
   }
 }
@@ -1482,7 +1502,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void step_kernel(StepArgs s) {
   __shared__ StepShared<D, GBM> sh;
   const ScoreArgs& sa = s.score;
-  const int64_t h = blockIdx.y, tile = blockIdx.x;
+  // workgroup wk of the head scores tile wk % n_tiles (copies past the first
+  // n_tiles with short prompts, see attend_tile)
+  const int64_t h = blockIdx.y, wk = blockIdx.x;
+  const int64_t tile = wk % (int64_t)s.attend.decide.n_tiles;
   const int G = sa.group, tid = threadIdx.x, lane = tid % kWave;
   const StepCtx sx{StepStats{sh.zs, Coherent(s.lse_slots, s.slots_bytes), &sh.tag,
                              reinterpret_cast<uint32_t*>(s.control + (int64_t)s.heads * kLine)},
@@ -1500,18 +1523,19 @@ void step_kernel(StepArgs s) {
                    sh.xl,
                    sh.xr,
                    s.heads};
-  // this launch's epoch, from the tile's own launch counter: its tag marks
-  // the slots the launch publishes
+  // this launch's epoch, from the workgroup's own launch counter: its tag
+  // marks the slots the launch publishes (read only after the score loads
+  // are issued: a read right after the atomic would wait out its round trip)
   uint64_t epoch = 0;
   if (tid == 0)
     epoch = __hip_atomic_fetch_add(
-        s.control + ((int64_t)s.heads + 1) * kLine + h * sa.tile_stride + tile, 1ull,
+        s.control + ((int64_t)s.heads + 1) * kLine + h * sa.tile_stride + wk, 1ull,
         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   score_dots<D>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
   // (the epoch is read before the loads below are issued: loads complete in
   // order, so a later read would wait for them too)
   if (tid == 0) {
-    sh.base = epoch * (uint64_t)s.attend.decide.n_tiles;
+    sh.base = epoch * (uint64_t)s.attend.workers;
     sh.tag = (uint32_t)epoch + 1u;
   }
   // the attention's loads that need no statistics land during them
@@ -1781,6 +1805,7 @@ AttendArgs attend_args(const SelectParams& p, const Layout& L, const DecodeBuffe
   aa.vs_ts = b.vs_ts;
   aa.suffix_cap = b.suffix_cap;
   aa.log2_block = p.block == 16 ? 4 : (p.block == 32 ? 5 : 6);
+  aa.workers = (int)L.n_tiles;
   aa.scale = (float)pow((double)p.dim, -0.5);
   return aa;
 }
@@ -1868,6 +1893,7 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) 
   StepArgs s;
   s.score = score_args(p, L);
   s.attend = attend_args(p, L, b);
+  s.attend.workers = (int)L.step_workers;
   s.control = at<uint64_t>(p.ws, L.control);
   s.counts = at<uint32_t>(p.ws, L.counts);
   s.attend.tile_counts = p.accessed ? s.counts : nullptr;
@@ -1886,7 +1912,8 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) 
   mark(0, p.stream);
   int rc = kUnsupported;
   RKV_DISPATCH_DIM(p.dim, D,
-                   rc = launch_step_d<D>(s, rows, dim3((unsigned)L.n_tiles, (unsigned)p.heads),
+                   rc = launch_step_d<D>(s, rows,
+                                         dim3((unsigned)L.step_workers, (unsigned)p.heads),
                                          p.stream));
   mark(1, p.stream);
   return rc;
@@ -1931,14 +1958,15 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 // tagged expanded-block masks), total, then n_tiles, the row stride (blocks)
 // of zf and of the per-tile arrays.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
-                                    int64_t* out12) {
+                                    int64_t* out13) {
   clear_error();
-  if (!out12 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+  if (!out13 || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  const int64_t v[12] = {L.control, L.zf,     L.lse,   L.lse_slots, L.part_ml,  L.part_acc,
-                         L.counts,  L.xbits,  L.total, L.n_tiles,   L.z_stride, L.tile_stride};
-  for (int i = 0; i < 12; ++i) out12[i] = v[i];
+  const int64_t v[13] = {L.control,  L.zf,     L.lse,         L.lse_slots, L.part_ml,
+                         L.part_acc, L.counts, L.xbits,       L.total,     L.n_tiles,
+                         L.z_stride, L.tile_stride, L.step_workers};
+  for (int i = 0; i < 13; ++i) out13[i] = v[i];
   return kOk;
 }
 

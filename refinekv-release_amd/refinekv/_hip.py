@@ -160,7 +160,7 @@ def workspace_bytes(heads, group, dim, n_blocks):
 
 
 LAYOUT_NAMES = ("control", "zf", "lse", "lse_slots", "part_ml", "part_acc", "counts", "xbits",
-                "total", "n_tiles", "z_stride", "tile_stride")
+                "total", "n_tiles", "z_stride", "tile_stride", "step_workers")
 # rkv_set_decode_path codes: the one-launch step where it fits, or always the
 # three kernels (score, attend, merge).
 DECODE_PATHS = {"step": 0, "split": 1}

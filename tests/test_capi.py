@@ -73,4 +73,9 @@ def test_workspace_size_covers_layout(lib):
         assert layout["counts"] - layout["part_acc"] >= rows * ts * dim * 4
         assert layout["xbits"] - layout["counts"] >= heads * ts * 4
         assert layout["total"] - layout["xbits"] >= heads * ts * 16
+        # the one-launch step's workgroups per head: every tile, topped up
+        # with helpers to 512 / heads, within the per-tile arrays
+        want = 512 // heads
+        assert layout["step_workers"] == max(tiles, min(want, ts))
+        assert tiles <= layout["step_workers"] <= ts
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0

@@ -40,12 +40,12 @@ def decode_path(hip, request):
 
 
 def assert_control_clean(hip, ws):
-    """After every launch each head's merge counter is n_tiles times the
-    launch count that every tile's own counter holds, and no hand-off wait
-    gave up.  Returns the launch count."""
+    """After every launch each head's merge counter is step_workers times the
+    launch count that every workgroup's own counter holds, and no hand-off
+    wait gave up.  Returns the launch count."""
     heads, group, dim, n = ws["hip_scratch_shape"]
     layout = hip.workspace_layout(heads, group, dim, n)
-    tiles, ts = layout["n_tiles"], layout["tile_stride"]
+    tiles, ts = layout["step_workers"], layout["tile_stride"]
     words = ws["hip_scratch"][:layout["zf"]].view(torch.int64).cpu().numpy()
     lines = words[:(heads + 1) * 8].reshape(heads + 1, 8)
     assert lines[heads, 0] & 0xFFFFFFFF == 0, "a hand-off wait gave up"
