@@ -73,13 +73,14 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   Layout L{};
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
   L.z_stride = L.n_tiles * kTile;
-  L.tile_stride = (L.n_tiles + 63) / 64 * 64;
-  // The one-launch step runs max(n_tiles, 512 / heads) workgroups per head
-  // (at most tile_stride): the n_tiles tiles and, with short prompts, copies
+  // The one-launch step runs max(n_tiles, min(512 / heads, 256)) workgroups
+  // per head: the n_tiles tiles and, with short prompts or few heads, copies
   // of them that also take a share of the head's suffix and expanded token
-  // rows, so that the token work spreads over the GPU (two workgroups per CU).
-  const int64_t want = 512 / heads;
-  L.step_workers = L.n_tiles > want ? L.n_tiles : (want < L.tile_stride ? want : L.tile_stride);
+  // rows, so that the token work spreads over the GPU (two workgroups per
+  // CU).  The per-tile arrays have a slot per workgroup.
+  const int64_t want = 512 / heads < kStepMaxTiles ? 512 / heads : kStepMaxTiles;
+  L.step_workers = L.n_tiles > want ? L.n_tiles : want;
+  L.tile_stride = (L.step_workers + 63) / 64 * 64;
   const int64_t rows = heads * group;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {

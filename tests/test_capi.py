@@ -74,8 +74,8 @@ def test_workspace_size_covers_layout(lib):
         assert layout["xbits"] - layout["counts"] >= heads * ts * 4
         assert layout["total"] - layout["xbits"] >= heads * ts * 16
         # the one-launch step's workgroups per head: every tile, topped up
-        # with helpers to 512 / heads, within the per-tile arrays
-        want = 512 // heads
-        assert layout["step_workers"] == max(tiles, min(want, ts))
+        # with copies to min(512 / heads, 256), each with a per-tile slot
+        want = min(512 // heads, 256)
+        assert layout["step_workers"] == max(tiles, want)
         assert tiles <= layout["step_workers"] <= ts
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0
