@@ -355,7 +355,10 @@ def sweep(a):
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     _hip.lib()
-    _hip.set_decode_path("step")  # the three kernels past 256 tiles per head
+    # the three kernels past 256 tiles per head or a grid larger than the
+    # device holds at once (two step workgroups per CU)
+    _hip.set_decode_path("step")
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     warmup, steps = 2, 10
     capacity = warmup + steps + 1
     for context in (8192, 32768, 131072, 524288):
@@ -416,8 +419,10 @@ def sweep(a):
                                                int(suffix_len.item()))["decode"]
                     gbps = nbytes / (us * 1e-6) / 1e9
                     tiles = -(-n // 64)
+                    workers = max(tiles, min(512 // a.heads, 256))
+                    fits = tiles <= 256 and a.heads * workers <= 2 * cus
                     point = dict(context=context, block=block, eps=eps, spikes=spikes,
-                                 layers=n_layers, path="step" if tiles <= 256 else "split",
+                                 layers=n_layers, path="step" if fits else "split",
                                  us_per_layer_step=round(us, 2), expanded_fraction=round(f, 5),
                                  algorithmic_bytes=int(nbytes), GBps=round(gbps, 1),
                                  frac_of_peak=round(gbps / PEAK_HBM_GBPS, 4))

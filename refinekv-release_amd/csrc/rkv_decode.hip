@@ -29,6 +29,8 @@
 // are deterministic run to run.
 #include <math.h>
 
+#include <atomic>
+
 #include "rkv_common.h"
 #include "rkv_internal.h"
 
@@ -57,6 +59,18 @@ inline void mark(int i, hipStream_t stream) {
   if (g_events) (void)hipEventRecord(g_events[i], stream);
 }
 
+// Query rows one attention pass carries in registers: the next power of two
+// >= group (at least 4), capped so that rows * head_dim / 16 (per-lane
+// accumulators) stays <= 64.
+inline int64_t rows_per_pass(int64_t group, int64_t dim) {
+  const int64_t cap = 64 / (dim / 16);
+  int64_t p = 16;
+  while (p > cap) p >>= 1;
+  int64_t want = 4;
+  while (want < group && want < 16) want <<= 1;
+  return want < p ? want : p;
+}
+
 // ---------------------------------------------------------------------------
 // Workspace layout.  Every per-row region starts on a 256-byte boundary and
 // per-row strides cover whole tiles.
@@ -73,12 +87,15 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   Layout L{};
   L.n_tiles = (n_blocks + kTile - 1) / kTile;
   L.z_stride = L.n_tiles * kTile;
-  // The one-launch step runs max(n_tiles, min(512 / heads, 256)) workgroups
+  // The one-launch step runs max(n_tiles, min(S / heads, 256)) workgroups
   // per head: the n_tiles tiles and, with short prompts or few heads, copies
   // of them that also take a share of the head's suffix and expanded token
-  // rows, so that the token work spreads over the GPU (two workgroups per
-  // CU).  The per-tile arrays have a slot per workgroup.
-  const int64_t want = 512 / heads < kStepMaxTiles ? 512 / heads : kStepMaxTiles;
+  // rows, so that the token work spreads over the GPU (S = 512, two
+  // workgroups per CU on 256 CUs; 256 for the 16-row kernels, which take
+  // more than 256 registers per lane).  The per-tile arrays have a slot per
+  // workgroup.
+  const int64_t slots = rows_per_pass(group, dim) == 16 ? 256 : 512;
+  const int64_t want = slots / heads < kStepMaxTiles ? slots / heads : kStepMaxTiles;
   L.step_workers = L.n_tiles > want ? L.n_tiles : want;
   L.tile_stride = (L.step_workers + 63) / 64 * 64;
   const int64_t rows = heads * group;
@@ -103,18 +120,6 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
 template <typename T>
 T* at(void* ws, int64_t off) {
   return reinterpret_cast<T*>(static_cast<char*>(ws) + off);
-}
-
-// Query rows one attention pass carries in registers: the next power of two
-// >= group (at least 4), capped so that rows * head_dim / 16 (per-lane
-// accumulators) stays <= 64.
-inline int64_t rows_per_pass(int64_t group, int64_t dim) {
-  const int64_t cap = 64 / (dim / 16);
-  int64_t p = 16;
-  while (p > cap) p >>= 1;
-  int64_t want = 4;
-  while (want < group && want < 16) want <<= 1;
-  return want < p ? want : p;
 }
 
 // ---------------------------------------------------------------------------
@@ -904,10 +909,9 @@ struct CombineShared {
 //
 // Progress: a tile waits only for the tiles of its own head, and only after
 // publishing what they wait for from it.  Workgroups are dispatched in
-// blockIdx order (x fastest, so a head's tiles are consecutive); with at
-// least n_tiles workgroups resident at once (the host allows this path only
-// for n_tiles <= kStepMaxTiles, one workgroup per CU), the lowest head still
-// waiting has all of its tiles dispatched, so its wait ends.  A wait that
+// blockIdx order (x fastest, so a head's tiles are consecutive); the host
+// takes this path only when the whole grid fits on the device at once (two
+// workgroups per CU), so every tile a wait depends on is running.  A wait that
 // does not end within kSpinLimit polls records an error instead of hanging.
 
 struct StepCtx {
@@ -1878,15 +1882,53 @@ int launch_step_d(const StepArgs& sa, int64_t rows, dim3 grid, hipStream_t strea
 // the three kernels.
 thread_local int g_decode_path = 0;
 
+// Workgroups of step_kernel<D, GBM> the current device holds at once (its
+// occupancy per CU times the CUs), 0 if unknown.
+template <int D, int GBM>
+int64_t step_resident() {
+  static std::atomic<int> of_dev[64];  // per device; 0 = not asked yet
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = of_dev[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel<D, GBM>, kThreads, 0) !=
+            hipSuccess)
+      return 0;
+    n = cus * per_cu;
+    of_dev[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+// The residency of the step kernel launch_step_d<D> takes for `rows` rows.
+template <int D>
+int64_t step_resident_d(int64_t rows) {
+  constexpr int CH = D / 16;
+  constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
+  if (rows == 4) return step_resident<D, 4>();
+  if constexpr (CAP >= 8)
+    if (rows == 8) return step_resident<D, 8>();
+  if constexpr (CAP >= 16)
+    if (rows == 16) return step_resident<D, 16>();
+  return 0;
+}
+
 // The one-launch step needs every query row in one attention pass, at most
-// kStepMaxTiles tiles per head (so that a head's tiles can all be resident),
-// its coherent regions addressable with 31-bit byte offsets and an 8-byte
-// aligned output (it stores 4 columns at a time).
+// kStepMaxTiles tiles per head, the whole grid resident at once (a tile waits
+// for the other tiles of its head; a grid larger than the device would run
+// in rounds, slower than the three kernels), its coherent regions
+// addressable with 31-bit byte offsets and an 8-byte aligned output (it
+// stores 4 columns at a time).
 bool step_fits(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const int64_t rows = rows_per_pass(p.group, p.dim);
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
   const int64_t limit = int64_t(1) << 31;
-  return p.group <= rows && L.n_tiles <= kStepMaxTiles && hg * ts * 32 < limit &&
+  int64_t resident = 0;
+  RKV_DISPATCH_DIM(p.dim, D, resident = step_resident_d<D>(rows));
+  return p.group <= rows && L.n_tiles <= kStepMaxTiles &&
+         p.heads * L.step_workers <= resident && hg * ts * 32 < limit &&
          hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8);
 }
 

@@ -49,6 +49,18 @@ def test_version_and_error_channel(lib):
     assert b"bad arguments" in lib.rkv_last_error()
 
 
+def rows_per_pass(group, dim):
+    """Query rows one attention pass of the decode kernels carries: the next
+    power of two >= group (at least 4), at most 64 // (dim // 16)."""
+    want = 4
+    while want < group and want < 16:
+        want *= 2
+    cap = 16
+    while cap > 64 // (dim // 16):
+        cap //= 2
+    return min(want, cap)
+
+
 def test_workspace_size_covers_layout(lib):
     from refinekv import _hip
 
@@ -74,8 +86,9 @@ def test_workspace_size_covers_layout(lib):
         assert layout["xbits"] - layout["counts"] >= heads * ts * 4
         assert layout["total"] - layout["xbits"] >= heads * ts * 16
         # the one-launch step's workgroups per head: every tile, topped up
-        # with copies to min(512 / heads, 256), each with a per-tile slot
-        want = min(512 // heads, 256)
+        # with copies to min(S / heads, 256), each with a per-tile slot (S =
+        # 256 for the 16-row kernels, which hold one workgroup per CU)
+        want = min((256 if rows_per_pass(group, dim) == 16 else 512) // heads, 256)
         assert layout["step_workers"] == max(tiles, want)
         assert tiles <= layout["step_workers"] <= ts
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0
