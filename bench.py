@@ -68,6 +68,10 @@ def parse_args():
     ap.add_argument("--sweep", action="store_true",
                     help="the isolated-op sweep (BASELINE.json configs[4]): one JSON line per "
                          "(context, block, eps, spike fraction) point")
+    ap.add_argument("--sweep-contexts", default="8192,32768,131072,524288",
+                    help="--sweep: prompt lengths, comma-separated")
+    ap.add_argument("--sweep-blocks", default="16,32,64",
+                    help="--sweep: block sizes, comma-separated")
     return ap.parse_args()
 
 
@@ -361,8 +365,10 @@ def sweep(a):
     cus = torch.cuda.get_device_properties(dev).multi_processor_count
     warmup, steps = 2, 10
     capacity = warmup + steps + 1
-    for context in (8192, 32768, 131072, 524288):
-        for block in (16, 32, 64):
+    contexts = [int(x) for x in a.sweep_contexts.split(",")]
+    blocks = [int(x) for x in a.sweep_blocks.split(",")]
+    for context in contexts:
+        for block in blocks:
             n = -(-context // block)
             per_layer = a.heads * n * a.dim * 2 * 3  # key/value means and ellipsoid
             n_layers = max(4, min(256, -(-1_500_000_000 // per_layer)))
