@@ -480,6 +480,35 @@ def test_headline_shape_128k(hip, oracle_lib):
     _headline_shape_128k(hip, oracle_lib)
 
 
+def test_long_context_512k(hip, oracle_lib):
+    """The sweep's longest context (H_kv 8, G 4, d 128, 524288 prompt tokens,
+    B 32: 256 tiles per head, 2048 workgroups, more than the device holds at
+    once, so the three kernels run): masks equal the oracle's selection over
+    this summary, outputs within tolerance of the oracle's, and nothing
+    touched the step's counters.  (The
+    summary kernel itself is pinned bit for bit at 131072 tokens.)"""
+    prompt, block, eps = 524288, 32, 0.01
+    inp = _decode_case(8, 4, 128, block, prompt, 0.01, suffix=17, seed=5)
+    cfg = RefineKVConfig(backend="hip", eps=eps, block_size=block)
+    k, v = inp["prompt_keys"], inp["prompt_values"]
+    summary = build_summary(k.to(DEV), v.to(DEV), cfg)
+    summ = oracle_summary_of(summary)
+    qn = inp["query"][:, :, 0].float().numpy()
+    out, mask = oracle_lib.sparse_attention(qn, summ, _pages_bits(k, block),
+                                            _pages_bits(v, block),
+                                            gc.bf16_bits(inp["suffix_keys"]),
+                                            gc.bf16_bits(inp["suffix_values"]), eps, "any")
+    assert 0.005 < mask.mean() < 0.1
+    ws = {}
+    res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                           inp["suffix_values"].to(DEV), cfg, workspace=ws, return_selected=True)
+    torch.cuda.synchronize()
+    assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask)
+    assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
+                        torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+    assert assert_control_clean(hip, ws) == 0
+
+
 def _headline_shape_128k(hip, oracle_lib):
     inp = _decode_case(8, 4, 128, 32, 131072, 0.02, suffix=65, seed=1)
     cfg = RefineKVConfig(backend="hip", eps=0.01)
