@@ -1441,7 +1441,10 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     const uint32_t ticket = *sx->flag;
     const uint32_t K = W < (uint32_t)kMergers ? W : (uint32_t)kMergers;
     if (ticket >= W - K) {
-      if (tid == 0) wait_counter<uint64_t>(merged, *sx->base + W, kSpinLimit, sx->error());
+      // (the last ticket's own bump completed the count: every other tile's
+      // partial landed before its bump did, so it merges without a poll)
+      if (tid == 0 && ticket != W - 1)
+        wait_counter<uint64_t>(merged, *sx->base + W, kSpinLimit, sx->error());
       __syncthreads();
       merge_slice<D>(a, *sx, h, (int)(ticket - (W - K)), (int)K);
     }
