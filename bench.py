@@ -426,7 +426,9 @@ def sweep(a):
                     gbps = nbytes / (us * 1e-6) / 1e9
                     tiles = -(-n // 64)
                     workers = max(tiles, min(512 // a.heads, 256))
-                    fits = tiles <= 256 and a.heads * workers <= 2 * cus
+                    grid, resident = a.heads * workers, 2 * cus
+                    fits = tiles <= 256 and (grid <= resident or (
+                        block >= 64 and workers <= resident and grid <= 2 * resident))
                     point = dict(context=context, block=block, eps=eps, spikes=spikes,
                                  layers=n_layers, path="step" if fits else "split",
                                  us_per_layer_step=round(us, 2), expanded_fraction=round(f, 5),

@@ -1919,19 +1919,24 @@ int64_t step_resident_d(int64_t rows) {
 }
 
 // The one-launch step needs every query row in one attention pass, at most
-// kStepMaxTiles tiles per head, the whole grid resident at once (a tile waits
-// for the other tiles of its head; a grid larger than the device would run
-// in rounds, slower than the three kernels), its coherent regions
-// addressable with 31-bit byte offsets and an 8-byte aligned output (it
-// stores 4 columns at a time).
+// kStepMaxTiles tiles per head, its grid resident at once (a tile waits for
+// the other tiles of its head), its coherent regions addressable with 31-bit
+// byte offsets and an 8-byte aligned output (it stores 4 columns at a time).
+// One exception to residency, measured faster than the three kernels: with
+// blocks of 64 or more tokens a grid of up to two rounds, whole heads per
+// round (workgroups are dispatched in blockIdx order, a head's tiles
+// consecutive, so each head of the second round starts only as the first
+// round's heads end, and all of its tiles are then dispatched).
 bool step_fits(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const int64_t rows = rows_per_pass(p.group, p.dim);
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
   const int64_t limit = int64_t(1) << 31;
   int64_t resident = 0;
   RKV_DISPATCH_DIM(p.dim, D, resident = step_resident_d<D>(rows));
-  return p.group <= rows && L.n_tiles <= kStepMaxTiles &&
-         p.heads * L.step_workers <= resident && hg * ts * 32 < limit &&
+  const int64_t grid = p.heads * L.step_workers;
+  const bool fits = grid <= resident ||
+                    (p.block >= 64 && L.step_workers <= resident && grid <= 2 * resident);
+  return p.group <= rows && L.n_tiles <= kStepMaxTiles && fits && hg * ts * 32 < limit &&
          hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8);
 }
 

@@ -55,15 +55,16 @@ def assert_control_clean(hip, ws):
     return int(launches[0, 0])
 
 
-def step_fits(group, dim, n_blocks, heads):
+def step_fits(group, dim, n_blocks, heads, block):
     """Whether rkv_decode takes the one-launch step for this shape: every
     query row in one attention pass (4, 8 or 16 rows as head_dim allows), at
     most 256 tiles of 64 blocks and the grid (heads x workers, workers =
     max(tiles, min(S // heads, 256))) resident at once: S = 512 and two
     workgroups per CU, or, for the 16-row kernels (more than 256 registers
-    per lane), S = 256 and one.  (Two per CU is the head_dim-128 kernels'
-    occupancy; smaller ones hold more, which matters only past 512
-    workgroups, a case the tests run at head_dim 128.)"""
+    per lane), S = 256 and one; with blocks of 64 or more tokens, up to two
+    rounds of it.  (Two per CU is the head_dim-128 kernels' occupancy;
+    smaller ones hold more, which matters only past 512 workgroups, a case
+    the tests run at head_dim 128.)"""
     cap = 64 // (dim // 16)
     rows = 16
     while rows > cap:
@@ -75,7 +76,9 @@ def step_fits(group, dim, n_blocks, heads):
     tiles = -(-n_blocks // 64)
     workers = max(tiles, min(256 * per_cu // heads, 256))
     resident = per_cu * torch.cuda.get_device_properties(0).multi_processor_count
-    return group <= min(want, rows) and tiles <= 256 and heads * workers <= resident
+    grid = heads * workers
+    fits = grid <= resident or (block >= 64 and workers <= resident and grid <= 2 * resident)
+    return group <= min(want, rows) and tiles <= 256 and fits
 
 
 def bits16(t):
@@ -386,7 +389,7 @@ def test_decode_matches_oracle(hip, oracle_lib, decode_path, heads, group, dim, 
             got = res.output.float().cpu().numpy()[:, :, 0]
             assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
     launches = assert_control_clean(hip, ws)
-    assert launches == (6 if decode_path == "step" and step_fits(group, dim, n, heads) else 0)
+    assert launches == (6 if decode_path == "step" and step_fits(group, dim, n, heads, block) else 0)
 
 
 def test_device_suffix_length_matches_slicing(hip, decode_path):
