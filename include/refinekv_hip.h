@@ -183,6 +183,37 @@ int rkv_set_profile_events(void* events);
  * kernels.  Per thread. */
 int rkv_set_decode_path(int path);
 
+/* Hand-off status of an rkv_decode workspace (no reference counterpart: the
+ * reference's Triton kernels have no cross-workgroup waits).  *status
+ * receives the workspace's sticky status word: bit 0 is set when a wait of
+ * the one-launch step gave up after its poll limit, in which case that
+ * call's output and mask are not to be trusted.  Copies the word to the host
+ * and synchronizes `stream` (a debugging query: not for graph capture).
+ * The shape arguments are those the workspace was sized for. */
+int rkv_workspace_status(const void* workspace, size_t workspace_bytes, int64_t heads,
+                         int64_t group, int64_t dim, int64_t n_blocks, uint32_t* status,
+                         rkv_stream_t stream);
+
+/* Clears the status word (one tiny kernel on `stream`). */
+int rkv_workspace_clear_status(void* workspace, size_t workspace_bytes, int64_t heads,
+                               int64_t group, int64_t dim, int64_t n_blocks,
+                               rkv_stream_t stream);
+
+/* Which path rkv_decode takes for this shape on the current device, for
+ * tests and benchmarks (no reference counterpart): *mode_out = 0 for three
+ * kernels, 1 for one launch with its whole grid resident, 2 for one launch
+ * whose workgroups draw (head, workgroup) tickets in start order (grids of
+ * up to two device-fulls, blocks of 64 tokens). */
+int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
+                    int64_t block_size, int* mode_out);
+
+/* Test hook with no reference counterpart: spin_limit replaces the one-launch
+ * step's poll limit per hand-off wait (0 = the default, 2^20), and a nonzero
+ * skew makes every wait accept no published data, so each wait runs out its
+ * limit, sets the status word and goes on; every kernel still ends.  Per
+ * thread; (0, 0) restores normal operation. */
+int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew);
+
 /* Test hook with no reference counterpart: applies the kernels' device
  * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */
 int rkv_math_probe(int fn, const float* x, float* y, int64_t n, rkv_stream_t stream);

@@ -2,22 +2,27 @@
 // the reference's Triton kernels in src/refinekv/kernels/ follow the same
 // semantics).  No host sync, no allocation: the caller passes a workspace.
 //
-// One decode step is three kernels, each over every (tile, KV head) pair or
-// every query row:
+// A decode step runs as ONE launch where the shape allows it (step_kernel):
+// workgroup (w, h) of the W per KV head h scores tile w mod T (64 blocks),
+// publishes its log-sum-exp partials in tagged slots, reads the head's T
+// tiles' slots, decides its blocks (risk, GQA reduction, anchors), folds its
+// representatives, publishes its expanded-block mask, attends an even share
+// of the head's expanded token rows and its slice of the suffix, publishes
+// an (m, l, acc) partial, and the head's last 8 workgroups by ticket merge
+// the partials into the bf16 output.  Other shapes run three kernels over the
+// same workspace:
 //
 //   score  (tile, h)    one 64-block tile of head h: for every query row the
 //                       selection dot products s = q.k_mean and
 //                       p = q^2.ellipsoid (FMA chains over 8 or 16 lanes per
 //                       block, then an xor butterfly), z = s*scale + ln n,
 //                       delta, and the tile's log-sum-exp partials of z and
-//                       of z + log cosh delta.  Reads the two summary arrays
-//                       once; nothing else.
+//                       of z + log cosh delta.
 //   attend (tile, h)    log Z / log C of each row from the tile partials, the
 //                       risk, the GQA reduction, the non-finite fail-safes and
 //                       the anchor union -> mask and access count; then one
 //                       online softmax per row over the tile's
-//                       representatives (the value means of its unexpanded
-//                       blocks, logit z), the tokens of its expanded blocks
+//                       representatives, the tokens of its expanded blocks
 //                       and a 1/T slice of the generated suffix -> one
 //                       (m, l, acc) partial per row and tile.
 //   merge  (row, cols)  the row's tile partials -> bf16 output columns, and
@@ -42,7 +47,7 @@ constexpr int kWaves = kThreads / kWave;
 constexpr int kRowsPerWave = kMaxGroup / kWaves;  // query rows a wave owns in a tile
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr int kLine = 8;  // u64 counters per 64-byte hand-off line
-constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a hand-off wait gives up
+constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a hand-off wait gives up (default)
 constexpr int64_t kStepMaxTiles = 256;     // tiles per head the one-launch step takes
 
 // Bytes of the one-launch step's hand-off counters: one line per KV head,
@@ -276,8 +281,10 @@ __device__ __forceinline__ void lds_read(const float* p, float (&out)[N]) {
 // The selection dot products of tile `tile` of head h for every query row:
 // sdot[g][b] = q_g . k_mean_b and pdot[g][b] = bf16(q_g^2) . ellipsoid_b
 // (DSUM), b tile-relative; ends with a barrier.  qstage holds
-// score_q_floats(G, D) floats of LDS.
-template <int D>
+// score_q_floats(G, D) floats of LDS.  kMaxG bounds the group (the step
+// kernel's rows per pass), so the four-row loop is compiled only where
+// groups above four can reach it.
+template <int D, int kMaxG = kMaxGroup>
 __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_t tile,
                                            float* sdot, float* pdot, float* qstage) {
   using S = Dots<D>;
@@ -378,7 +385,7 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
       }
     }
   };
-  if (G <= 4) {
+  if (kMaxG <= 4 || G <= 4) {
     four_rows(0);
   } else {
     for (int g0 = 0; g0 < G; g0 += 4) four_rows(g0);
@@ -566,13 +573,15 @@ constexpr int kChunks = (int)(kStepMaxTiles / kWave);  // tiles per lane, at mos
 struct StepStats {
   const float4 (*zs)[kTile];  // [row][block of the tile]
   Coherent slots;             // (H*G, tile_stride, 2) tagged slots
-  const uint32_t* tag;        // LDS: this launch's tag
+  const uint32_t* tag;        // LDS: this launch's tag (what the workgroup publishes)
+  const uint32_t* rtag;       // LDS: the tag its waits accept (the same, unless a test skews it)
   uint32_t* error;
+  uint32_t spin;              // polls before a wait gives up
 };
 
 // One row's LSE partials of the head's T tiles (lane t holds tiles t + 64 k)
 // from the tagged slots, read until every slot carries this launch's tag
-// (at most kSpinLimit rounds, then the error word is set).
+// (at most ss.spin rounds, then the error word is set).
 struct RowLse {
   float zm[kChunks], zl[kChunks], cm[kChunks], cl[kChunks];
 };
@@ -580,7 +589,7 @@ struct RowLse {
 __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, uint32_t T,
                                              int lane) {
   RowLse r;
-  const uint32_t tag = *ss.tag;
+  const uint32_t tag = *ss.rtag;
   for (uint32_t n = 0;; ++n) {
     bool ok = true;
 #pragma unroll
@@ -600,7 +609,7 @@ __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, u
       r.cl[k] = live ? b.y : 0.0f;
     }
     if (__ballot(!ok) == 0) break;
-    if (n + 1 >= kSpinLimit) {
+    if (n + 1 >= ss.spin) {
       if (lane == 0) __hip_atomic_fetch_or(ss.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       break;
     }
@@ -898,21 +907,27 @@ struct CombineShared {
 // Hand-offs between the tiles of a head.  Counters (u64 at the start of
 // the workspace): head h owns the 64-byte line at counter kLine * h, whose
 // [1] counts tiles that have published their attention partials; after the
-// heads' lines, a sticky u32 error word (bit 0: a wait gave up after
-// kSpinLimit polls); then one launch counter per tile.  Nothing is reset:
-// each launch adds one to every tile's counter and n_tiles to each head's,
-// so a tile's own counter (old value) is the launch's epoch e, e + 1 tags
-// the slots it publishes (LSE partials, expanded-block masks: readers poll
-// the slots themselves) and (e + 1) n_tiles is the merge count it waits
-// for.  This needs the workspace zero-filled once when created and used for
-// one shape thereafter.
+// heads' lines, a line holding a sticky u32 error word (bit 0: a wait gave up
+// after its poll limit) and, at [1], the launches' workgroup ticket count;
+// then one launch counter per workgroup.  Nothing is reset: each launch adds
+// one to every workgroup's counter and W (workgroups per head) to each
+// head's, so a workgroup's own counter (old value) is the launch's epoch e,
+// e + 1 tags the slots it publishes (LSE partials, expanded-block masks:
+// readers poll the slots themselves) and (e + 1) W is the merge count it
+// waits for.  This needs the workspace zero-filled once when created and
+// used for one shape thereafter.
 //
-// Progress: a tile waits only for the tiles of its own head, and only after
-// publishing what they wait for from it.  Workgroups are dispatched in
-// blockIdx order (x fastest, so a head's tiles are consecutive); the host
-// takes this path only when the whole grid fits on the device at once (two
-// workgroups per CU), so every tile a wait depends on is running.  A wait that
-// does not end within kSpinLimit polls records an error instead of hanging.
+// Progress: a workgroup waits only for the workgroups of its own head, and
+// only after publishing what they wait for from it.  When the whole grid fits
+// on the device at once, every workgroup a wait depends on is running.  A
+// grid of up to two device-fulls (blocks of 64 tokens) takes its (head,
+// workgroup) from a ticket drawn when it starts instead of from blockIdx:
+// tickets are handed out in start order, so every head whose tickets are all
+// drawn is entirely running, and at most one head (the one holding the
+// latest ticket) is partly running; its workgroups wait for peers that start
+// as the fully drawn heads finish, whatever order the hardware dispatches
+// workgroups in.  A wait that does not end within its poll limit records an
+// error instead of hanging.
 
 struct StepCtx {
   StepStats stats;
@@ -928,6 +943,7 @@ struct StepCtx {
   int32_t* xl;                    // LDS: blocks of this tile's expanded-row share
   uint32_t* xr;                   // LDS: the share's first row and row count
   int heads;
+  uint32_t skew;                  // 0; a test's nonzero value makes every wait run out
   __device__ uint32_t* error() const {
     return reinterpret_cast<uint32_t*>(control + (int64_t)heads * kLine);
   }
@@ -953,12 +969,14 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
 // (first row, row count).  Integer arithmetic only: every tile sees the same
 // split.
 __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
-                               uint32_t W, uint32_t tile, int lb) {
+                               uint32_t W, uint32_t tile, int lb, uint64_t last_bits) {
   const int lane = threadIdx.x % kWave;
-  const uint32_t tag = *sx.stats.tag;
+  const uint32_t tag = *sx.stats.rtag;
   uint64_t bm[kChunks];
   uint32_t cnt[kChunks], first[kChunks];
-  // the head's tagged masks, read until every one has landed
+  // the head's tagged masks, read until every one has landed (a mask is
+  // taken as read even when a wait gives up, so the last tile's bits are
+  // cut to its blocks: every row address below stays inside the pages)
   for (uint32_t n = 0;; ++n) {
     bool ok = true;
 #pragma unroll
@@ -970,11 +988,12 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
         if (t < T) {
           ok = ok && slot_ok(v, tag);
           bm[k] = (uint64_t)f32_bits(v.x) | ((uint64_t)f32_bits(v.y) << 32);
+          if (t == T - 1) bm[k] &= last_bits;
         }
       }
     }
     if (__ballot(!ok) == 0) break;
-    if (n + 1 >= kSpinLimit) {
+    if (n + 1 >= sx.stats.spin) {
       if (lane == 0)
         __hip_atomic_fetch_or(sx.stats.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       break;
@@ -1135,14 +1154,15 @@ struct AttendLoads {
   RawBf16<D / 16> ksr[1], vsr[1];        // the lane group's first suffix token
 };
 
+// Workgroup wk of head h (blockIdx.x and blockIdx.y, or the step's ticket).
 template <int D, int GBM, bool kFused>
-__device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a) {
+__device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a, int64_t h,
+                                                            uint32_t wk) {
   constexpr int CH = D / 16;
   constexpr int NB = kTile / 16;
   const DecideArgs& da = a.decide;
-  const int64_t h = blockIdx.y;
   // workgroup wk of the head's W scores tile wk % T (copies past the first T)
-  const uint32_t wk = blockIdx.x, tile = wk % (uint32_t)da.n_tiles;
+  const uint32_t tile = wk % (uint32_t)da.n_tiles;
   const int G = da.group;
   const uint32_t N = (uint32_t)da.n_blocks;
   const uint32_t W = (uint32_t)a.workers;  // the suffix is sliced over the workgroups
@@ -1188,13 +1208,13 @@ __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a)
 template <int D, int GBM, bool kFused>
 __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& dsh,
                                             CombineShared<D, GBM>& cmb, const StepCtx* sx,
-                                            const AttendLoads<D, GBM>& ld) {
+                                            const AttendLoads<D, GBM>& ld, int64_t h,
+                                            uint32_t wk) {
   constexpr int CH = D / 16;
   constexpr int R = kRowBatch;
   constexpr int NB = kTile / 16;  // representatives per lane group
   using Comb = CombineShared<D, GBM>;
   const DecideArgs& da = a.decide;
-  const int64_t h = blockIdx.y;
   const int G = da.group;
   const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
   const uint32_t L = (uint32_t)da.length, lb = (uint32_t)a.log2_block, B = 1u << lb;
@@ -1207,7 +1227,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   // workgroups: a copy repeats its tile's scores and decision (publishing the
   // same slots, bit for bit) but adds no representatives of its own.
   const uint32_t W = (uint32_t)a.workers;
-  const uint32_t wk = blockIdx.x, tile = wk % T;
+  const uint32_t tile = wk % T;
   const bool primary = wk < T;
 
   // ---- what attend_issue loaded; z and the row maxima from the statistics -
@@ -1367,7 +1387,11 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   // ---- then (one-launch step): this tile's share of the head's expanded
   // rows, once every tile of the head has published its mask ---------------
   if constexpr (kFused) {
-    if (tid < kWave) expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb);
+    if (tid < kWave) {
+      const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
+      const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
+      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits);
+    }
     __syncthreads();
     const int32_t* xl = sx->xl;
     const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
@@ -1444,7 +1468,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       // (the last ticket's own bump completed the count: every other tile's
       // partial landed before its bump did, so it merges without a poll)
       if (tid == 0 && ticket != W - 1)
-        wait_counter<uint64_t>(merged, *sx->base + W, kSpinLimit, sx->error());
+        wait_counter<uint64_t>(merged, *sx->base + W + sx->skew, sx->stats.spin, sx->error());
       __syncthreads();
       merge_slice<D>(a, *sx, h, (int)(ticket - (W - K)), (int)K);
     }
@@ -1456,8 +1480,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void attend_kernel(AttendArgs a) {
   __shared__ alignas(16) DecideShared dsh;
   __shared__ alignas(16) CombineShared<D, GBM> cmb;
-  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a);
-  attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld);
+  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a, blockIdx.y, blockIdx.x);
+  attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld, blockIdx.y, blockIdx.x);
 }
 
 
@@ -1475,6 +1499,8 @@ struct StepArgs {
   float4* xbits;                  // (H, tile_stride) tagged expanded-block masks
   uint32_t slots_bytes, ml_bytes, acc_bytes, counts_bytes, xbits_bytes;
   int heads;
+  uint32_t spin;      // polls before a hand-off wait gives up
+  uint32_t skew;      // 0 (a test hook's nonzero value makes every wait run out)
 };
 
 // Every region starts on a 16-byte boundary: the q staging and the combine
@@ -1487,7 +1513,8 @@ struct StepShared {
   alignas(16) int32_t xl[kTile + 4];
   uint32_t xr[2];
   uint64_t base;
-  uint32_t tag;
+  uint32_t tag, rtag;
+  uint32_t ticket;
   alignas(16) DecideShared dec;
   alignas(16) union {
     struct {
@@ -1505,18 +1532,44 @@ struct StepShared {
 // arrival counter bumped), then attend_tile's decision (after the head's
 // tiles have all arrived), attention and, for the head's last tile, the
 // merge.
-template <int D, int GBM>
+// kTicketed: (head, workgroup) from a start-order ticket instead of blockIdx
+// (grids larger than the device holds at once).
+template <int D, int GBM, bool kTicketed>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void step_kernel(StepArgs s) {
   __shared__ StepShared<D, GBM> sh;
   const ScoreArgs& sa = s.score;
-  // workgroup wk of the head scores tile wk % n_tiles (copies past the first
-  // n_tiles with short prompts, see attend_tile)
-  const int64_t h = blockIdx.y, wk = blockIdx.x;
-  const int64_t tile = wk % (int64_t)s.attend.decide.n_tiles;
   const int G = sa.group, tid = threadIdx.x, lane = tid % kWave;
-  const StepCtx sx{StepStats{sh.zs, Coherent(s.lse_slots, s.slots_bytes), &sh.tag,
-                             reinterpret_cast<uint32_t*>(s.control + (int64_t)s.heads * kLine)},
+  const uint32_t W = (uint32_t)s.attend.workers;
+  // this launch's epoch, from the workgroup's own launch counter: its tag
+  // marks the slots the launch publishes (read only after the score loads
+  // are issued: a read right after the atomic would wait out its round trip)
+  uint64_t epoch = 0;
+  if (tid == 0)
+    epoch = __hip_atomic_fetch_add(
+        s.control + ((int64_t)s.heads + 1) * kLine + (int64_t)blockIdx.y * sa.tile_stride +
+            blockIdx.x,
+        1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // workgroup wk of head h scores tile wk % n_tiles (copies past the first
+  // n_tiles with short prompts, see attend_tile): blockIdx, or with a grid
+  // larger than the device holds at once, the ticket this workgroup draws as
+  // it starts (launch e's tickets are e * grid + 0 .. grid - 1)
+  int64_t h = blockIdx.y, wk = blockIdx.x;
+  if constexpr (kTicketed) {
+    if (tid == 0) {
+      const uint64_t t = __hip_atomic_fetch_add(s.control + (int64_t)s.heads * kLine + 1, 1ull,
+                                                __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      sh.ticket = (uint32_t)(t - epoch * (uint64_t)(W * gridDim.y));
+    }
+    __syncthreads();
+    const uint32_t t = __builtin_amdgcn_readfirstlane(sh.ticket);
+    h = t / W;
+    wk = t % W;
+  }
+  const int64_t tile = wk % (int64_t)s.attend.decide.n_tiles;
+  const StepCtx sx{StepStats{sh.zs, Coherent(s.lse_slots, s.slots_bytes), &sh.tag, &sh.rtag,
+                             reinterpret_cast<uint32_t*>(s.control + (int64_t)s.heads * kLine),
+                             s.spin},
                    sh.mts,
                    Coherent(s.attend.part_ml, s.ml_bytes),
                    Coherent(s.attend.part_acc, s.acc_bytes),
@@ -1530,24 +1583,18 @@ void step_kernel(StepArgs s) {
                    Coherent(s.xbits, s.xbits_bytes),
                    sh.xl,
                    sh.xr,
-                   s.heads};
-  // this launch's epoch, from the workgroup's own launch counter: its tag
-  // marks the slots the launch publishes (read only after the score loads
-  // are issued: a read right after the atomic would wait out its round trip)
-  uint64_t epoch = 0;
-  if (tid == 0)
-    epoch = __hip_atomic_fetch_add(
-        s.control + ((int64_t)s.heads + 1) * kLine + h * sa.tile_stride + wk, 1ull,
-        __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  score_dots<D>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+                   s.heads,
+                   s.skew};
+  score_dots<D, GBM>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
   // (the epoch is read before the loads below are issued: loads complete in
   // order, so a later read would wait for them too)
   if (tid == 0) {
-    sh.base = epoch * (uint64_t)s.attend.workers;
+    sh.base = epoch * (uint64_t)W;
     sh.tag = (uint32_t)epoch + 1u;
+    sh.rtag = sh.tag + s.skew;
   }
   // the attention's loads that need no statistics land during them
-  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, true>(s.attend);
+  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
   __syncthreads();
   score_stats(
       sa, tile, sh.u.score.sdot, sh.u.score.pdot,
@@ -1559,7 +1606,7 @@ void step_kernel(StepArgs s) {
         sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
       });
   __syncthreads();
-  attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld);
+  attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk);
 }
 
 // ---------------------------------------------------------------------------
@@ -1856,26 +1903,33 @@ int launch_attend(const AttendArgs& aa, int64_t rows, dim3 grid, hipStream_t str
   return set_error(kUnsupported, "rkv_decode: no attention kernel for this group");
 }
 
+// The one-launch step is built for head_dim <= kStepMaxDim: larger head
+// dims would spill registers to scratch in it, and take the three kernels.
+constexpr int kStepMaxDim = 160;
+
+template <int D, int GBM>
+int launch_step_g(const StepArgs& sa, bool ticketed, dim3 grid, hipStream_t stream) {
+  if (ticketed) step_kernel<D, GBM, true><<<grid, dim3(kThreads), 0, stream>>>(sa);
+  else step_kernel<D, GBM, false><<<grid, dim3(kThreads), 0, stream>>>(sa);
+  return check_launch("step_kernel");
+}
+
 template <int D>
-int launch_step_d(const StepArgs& sa, int64_t rows, dim3 grid, hipStream_t stream) {
+int launch_step_d(const StepArgs& sa, int64_t rows, bool ticketed, dim3 grid,
+                  hipStream_t stream) {
   constexpr int CH = D / 16;
   constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
-  switch (rows) {
-    case 4:
-      step_kernel<D, 4><<<grid, dim3(kThreads), 0, stream>>>(sa);
-      return check_launch("step_kernel");
-    case 8:
-      if constexpr (CAP >= 8) {
-        step_kernel<D, 8><<<grid, dim3(kThreads), 0, stream>>>(sa);
-        return check_launch("step_kernel");
-      }
-      break;
-    default:
-      if constexpr (CAP >= 16) {
-        step_kernel<D, 16><<<grid, dim3(kThreads), 0, stream>>>(sa);
-        return check_launch("step_kernel");
-      }
-      break;
+  if constexpr (D <= kStepMaxDim) {
+    switch (rows) {
+      case 4:
+        return launch_step_g<D, 4>(sa, ticketed, grid, stream);
+      case 8:
+        if constexpr (CAP >= 8) return launch_step_g<D, 8>(sa, ticketed, grid, stream);
+        break;
+      default:
+        if constexpr (CAP >= 16) return launch_step_g<D, 16>(sa, ticketed, grid, stream);
+        break;
+    }
   }
   return set_error(kUnsupported, "rkv_decode: no step kernel for this group");
 }
@@ -1888,7 +1942,7 @@ thread_local int g_decode_path = 0;
 // Workgroups of step_kernel<D, GBM> the current device holds at once (its
 // occupancy per CU times the CUs), 0 if unknown.
 template <int D, int GBM>
-int64_t step_resident() {
+int64_t step_resident() {  // (the ticketed build's occupancy is the same: same resources)
   static std::atomic<int> of_dev[64];  // per device; 0 = not asked yet
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
@@ -1896,7 +1950,8 @@ int64_t step_resident() {
   if (n == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel<D, GBM>, kThreads, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel<D, GBM, false>,
+                                                     kThreads, 0) !=
             hipSuccess)
       return 0;
     n = cus * per_cu;
@@ -1910,37 +1965,49 @@ template <int D>
 int64_t step_resident_d(int64_t rows) {
   constexpr int CH = D / 16;
   constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
-  if (rows == 4) return step_resident<D, 4>();
-  if constexpr (CAP >= 8)
-    if (rows == 8) return step_resident<D, 8>();
-  if constexpr (CAP >= 16)
-    if (rows == 16) return step_resident<D, 16>();
+  if constexpr (D <= kStepMaxDim) {
+    if (rows == 4) return step_resident<D, 4>();
+    if constexpr (CAP >= 8)
+      if (rows == 8) return step_resident<D, 8>();
+    if constexpr (CAP >= 16)
+      if (rows == 16) return step_resident<D, 16>();
+  }
   return 0;
 }
 
+// How rkv_decode runs a step.
+enum StepMode { kSplit = 0, kResident = 1, kTicketed = 2 };
+
 // The one-launch step needs every query row in one attention pass, at most
-// kStepMaxTiles tiles per head, its grid resident at once (a tile waits for
-// the other tiles of its head), its coherent regions addressable with 31-bit
-// byte offsets and an 8-byte aligned output (it stores 4 columns at a time).
-// One exception to residency, measured faster than the three kernels: with
-// blocks of 64 or more tokens a grid of up to two rounds, whole heads per
-// round (workgroups are dispatched in blockIdx order, a head's tiles
-// consecutive, so each head of the second round starts only as the first
-// round's heads end, and all of its tiles are then dispatched).
-bool step_fits(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+// kStepMaxTiles tiles per head, its coherent regions addressable with 31-bit
+// byte offsets, an 8-byte aligned output (it stores 4 columns at a time) and
+// every workgroup a wait depends on running: the whole grid resident at once
+// (kResident), or, with blocks of 64 tokens (measured faster than the three
+// kernels there), a grid of up to two device-fulls whose workgroups draw
+// their (head, workgroup) from start-order tickets (kTicketed: a head's W
+// workgroups must fit the device at once).
+StepMode step_mode(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
   const int64_t rows = rows_per_pass(p.group, p.dim);
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
   const int64_t limit = int64_t(1) << 31;
+  if (!(p.dim <= kStepMaxDim && p.group <= rows && L.n_tiles <= kStepMaxTiles &&
+        hg * ts * 32 < limit &&
+        hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8)))
+    return kSplit;
   int64_t resident = 0;
   RKV_DISPATCH_DIM(p.dim, D, resident = step_resident_d<D>(rows));
   const int64_t grid = p.heads * L.step_workers;
-  const bool fits = grid <= resident ||
-                    (p.block >= 64 && L.step_workers <= resident && grid <= 2 * resident);
-  return p.group <= rows && L.n_tiles <= kStepMaxTiles && fits && hg * ts * 32 < limit &&
-         hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8);
+  if (grid <= resident) return kResident;
+  if (p.block >= 64 && L.step_workers <= resident && grid <= 2 * resident) return kTicketed;
+  return kSplit;
 }
 
-int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
+// Test hooks (rkv_set_handoff_test, per thread): the step's poll limit per
+// wait (0 = kSpinLimit) and a tag skew that makes every wait run out.
+thread_local uint32_t g_spin_limit = 0;
+thread_local uint32_t g_skew = 0;
+
+int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, bool ticketed) {
   StepArgs s;
   s.score = score_args(p, L);
   s.attend = attend_args(p, L, b);
@@ -1959,11 +2026,13 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) 
   s.xbits = at<float4>(p.ws, L.xbits);
   s.xbits_bytes = (uint32_t)(p.heads * ts * 16);
   s.heads = (int)p.heads;
+  s.spin = g_spin_limit ? g_spin_limit : kSpinLimit;
+  s.skew = g_skew;
   const int64_t rows = rows_per_pass(p.group, p.dim);
   mark(0, p.stream);
   int rc = kUnsupported;
   RKV_DISPATCH_DIM(p.dim, D,
-                   rc = launch_step_d<D>(s, rows,
+                   rc = launch_step_d<D>(s, rows, ticketed,
                                          dim3((unsigned)L.step_workers, (unsigned)p.heads),
                                          p.stream));
   mark(1, p.stream);
@@ -1972,7 +2041,10 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b) 
 
 // One decode step: the one-launch step, or score, decide + attend, merge.
 int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b) {
-  if (g_decode_path == 0 && step_fits(p, L, b)) return launch_step(p, L, b);
+  if (g_decode_path == 0) {
+    const StepMode mode = step_mode(p, L, b);
+    if (mode != kSplit) return launch_step(p, L, b, mode == kTicketed);
+  }
   const AttendArgs aa = attend_args(p, L, b);
   const MergeArgs ma = merge_args(p, L, b);
   const int64_t rows = rows_per_pass(p.group, p.dim);
@@ -2135,4 +2207,78 @@ extern "C" int rkv_set_decode_path(int path) {
   if (path < 0 || path > 1) return set_error(kInvalidArgument, "rkv_set_decode_path: %d", path);
   g_decode_path = path;
   return kOk;
+}
+
+// Test hook: the one-launch step's poll limit per hand-off wait (0 = the
+// default) and, with skew != 0, readers that accept no published slot, so
+// that every wait runs out its limit, sets the error word and goes on (every
+// kernel still ends).  Per thread.
+extern "C" int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew) {
+  clear_error();
+  g_spin_limit = spin_limit;
+  g_skew = skew;
+  return kOk;
+}
+
+// Which path rkv_decode takes for a shape on the current device (with an
+// aligned output): 0 = three kernels, 1 = one launch with the grid resident,
+// 2 = one launch with start-order tickets.
+extern "C" int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
+                               int64_t block_size, int* mode_out) {
+  clear_error();
+  if (!mode_out || heads <= 0 || group <= 0 || n_blocks <= 0 || !supported_dim(dim) ||
+      !supported_block(block_size) || group > kMaxGroup)
+    return set_error(kInvalidArgument, "rkv_decode_plan: bad arguments");
+  SelectParams p{};
+  p.heads = heads;
+  p.group = group;
+  p.dim = dim;
+  p.n_blocks = n_blocks;
+  p.block = block_size;
+  const Layout L = make_layout(heads, group, dim, n_blocks);
+  DecodeBuffers b{};
+  b.output = reinterpret_cast<void*>(uintptr_t(256));
+  *mode_out = g_decode_path == 0 ? (int)step_mode(p, L, b) : 0;
+  return kOk;
+}
+
+namespace {
+__global__ void clear_word_kernel(uint32_t* word) { *word = 0u; }
+}  // namespace
+
+// The hand-off status word of an rkv_decode workspace: bit 0 set when a wait
+// of the one-launch step gave up (its output is then not to be trusted).
+// Copies the word to the host and synchronizes `stream`; not for capture.
+extern "C" int rkv_workspace_status(const void* workspace, size_t workspace_bytes,
+                                    int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
+                                    uint32_t* status, hipStream_t stream) {
+  clear_error();
+  if (!workspace || !status || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+    return set_error(kInvalidArgument, "rkv_workspace_status: bad arguments");
+  const Layout L = make_layout(heads, group, dim, n_blocks);
+  if (workspace_bytes < (size_t)L.total)
+    return set_error(kWorkspaceTooSmall, "rkv_workspace_status: workspace smaller than its shape");
+  const char* word = static_cast<const char*>(workspace) + L.control + heads * kLine * 8;
+  uint32_t host = 0;
+  if (hipMemcpyAsync(&host, word, sizeof(host), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return set_error(kLaunchFailed, "rkv_workspace_status: copy failed");
+  *status = host;
+  return kOk;
+}
+
+// Clears the status word (a one-thread kernel on `stream`, capturable).
+extern "C" int rkv_workspace_clear_status(void* workspace, size_t workspace_bytes, int64_t heads,
+                                          int64_t group, int64_t dim, int64_t n_blocks,
+                                          hipStream_t stream) {
+  clear_error();
+  if (!workspace || heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+    return set_error(kInvalidArgument, "rkv_workspace_clear_status: bad arguments");
+  const Layout L = make_layout(heads, group, dim, n_blocks);
+  if (workspace_bytes < (size_t)L.total)
+    return set_error(kWorkspaceTooSmall,
+                     "rkv_workspace_clear_status: workspace smaller than its shape");
+  clear_word_kernel<<<1, 1, 0, stream>>>(
+      reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + L.control + heads * kLine * 8));
+  return check_launch("clear_word_kernel");
 }

@@ -6,6 +6,12 @@ and never synchronizes, so calls can be captured in a HIP graph.  This module
 owns the per-call plumbing: argument checks the kernels rely on, the
 caller-owned workspace, and mapping C error codes to Python exceptions.
 There is no fallback: if the library is missing, calls raise.
+
+Hand-off checking: the one-launch decode step's waits are bounded; a wait
+that gives up sets a sticky status word in the workspace instead of
+hanging.  ``check_workspace`` reads it and raises; with the environment
+variable ``REFINEKV_HIP_CHECK=1`` every ``decode`` call checks it (a host
+synchronization per call, so not under graph capture).
 """
 
 import ctypes
@@ -23,11 +29,14 @@ MAX_GROUP = 16
 _lib = None
 _load_error = None
 
+CHECK_HANDOFFS = os.environ.get("REFINEKV_HIP_CHECK", "0") not in ("", "0")
+
 _p = ctypes.c_void_p
 _i64 = ctypes.c_int64
 _f32 = ctypes.c_float
 _int = ctypes.c_int
 _size = ctypes.c_size_t
+_u32 = ctypes.c_uint32
 
 
 class HipUnavailable(RuntimeError):
@@ -64,6 +73,14 @@ def _bind(lib):
     lib.rkv_set_profile_events.restype = _int
     lib.rkv_set_decode_path.argtypes = [_int]
     lib.rkv_set_decode_path.restype = _int
+    lib.rkv_workspace_status.argtypes = [_p, _size, _i64, _i64, _i64, _i64, _p, _p]
+    lib.rkv_workspace_status.restype = _int
+    lib.rkv_workspace_clear_status.argtypes = [_p, _size, _i64, _i64, _i64, _i64, _p]
+    lib.rkv_workspace_clear_status.restype = _int
+    lib.rkv_decode_plan.argtypes = [_i64, _i64, _i64, _i64, _i64, _p]
+    lib.rkv_decode_plan.restype = _int
+    lib.rkv_set_handoff_test.argtypes = [_u32, _u32]
+    lib.rkv_set_handoff_test.restype = _int
     return lib
 
 
@@ -290,7 +307,70 @@ def decode(query, summary, key_suffix, value_suffix, config, anchor_mask=None, w
         REDUCTION_CODES[config.gqa_reduction], _ptr(anchor), _ptr(mask), _ptr(output),
         _ptr(accessed), _ptr(scratch), scratch.numel(), _stream(device))
     _check(rc, "rkv_decode")
+    if CHECK_HANDOFFS and not torch.cuda.is_current_stream_capturing():
+        check_workspace(workspace if workspace is not None else {"hip_scratch": scratch,
+                                                                  "hip_scratch_shape": (
+                                                                      heads, group, dim,
+                                                                      n_blocks)})
     return output, mask
+
+
+class HandoffError(RuntimeError):
+    """A wait of the one-launch decode step gave up: the call's output and
+    mask are not to be trusted."""
+
+
+def workspace_status(workspace):
+    """The sticky hand-off status word of a decode workspace (0 = clean); a
+    host synchronization."""
+    scratch = workspace.get("hip_scratch") if workspace else None
+    if scratch is None:
+        return 0
+    heads, group, dim, n_blocks = workspace["hip_scratch_shape"]
+    word = ctypes.c_uint32()
+    _check(lib().rkv_workspace_status(_ptr(scratch), scratch.numel(), heads, group, dim, n_blocks,
+                                      ctypes.byref(word), _stream(scratch.device)),
+           "rkv_workspace_status")
+    return int(word.value)
+
+
+def clear_workspace_status(workspace):
+    scratch = workspace.get("hip_scratch") if workspace else None
+    if scratch is None:
+        return
+    heads, group, dim, n_blocks = workspace["hip_scratch_shape"]
+    _check(lib().rkv_workspace_clear_status(_ptr(scratch), scratch.numel(), heads, group, dim,
+                                            n_blocks, _stream(scratch.device)),
+           "rkv_workspace_clear_status")
+
+
+def check_workspace(workspace):
+    """Raise HandoffError if a decode step on this workspace had a hand-off
+    wait give up since the status was last cleared."""
+    status = workspace_status(workspace)
+    if status & 1:
+        raise HandoffError(
+            "rkv_decode: a hand-off wait of the one-launch step gave up (its workgroups were "
+            "not all running at once); outputs computed with this workspace are invalid")
+
+
+PLAN_NAMES = {0: "split", 1: "step", 2: "step-ticketed"}
+
+
+def decode_plan(heads, group, dim, n_blocks, block):
+    """The path rkv_decode takes for a shape on the current device: "split"
+    (three kernels), "step" (one launch, grid resident) or "step-ticketed"
+    (one launch, workgroups mapped by start-order tickets)."""
+    mode = ctypes.c_int()
+    _check(lib().rkv_decode_plan(heads, group, dim, n_blocks, block, ctypes.byref(mode)),
+           "rkv_decode_plan")
+    return PLAN_NAMES[mode.value]
+
+
+def set_handoff_test(spin_limit=0, skew=0):
+    """Test hook: the step's poll limit per wait (0 = default) and a skew
+    that makes every wait run out (0 = off), for later calls on this thread."""
+    _check(lib().rkv_set_handoff_test(spin_limit, skew), "rkv_set_handoff_test")
 
 
 def set_decode_path(name):

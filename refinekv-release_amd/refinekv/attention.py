@@ -1,18 +1,24 @@
 """Single-token decode attention API (mirror of src/refinekv/attention.py:12-134).
 
 ``select_blocks`` and ``sparse_attention`` keep the reference's signatures,
-validation and error types.  ``backend="hip"`` runs the gfx950 kernels
+validation and error types.  ``backend="hip"`` (or ``"triton"``, the
+reference's name for its accelerated backend) runs the gfx950 kernels
 through the C ABI; ``"auto"`` picks them for ROCm tensors whose shapes they
 support (bf16 query, head_dim 32..256 in steps of 32, GQA group <= 16) and
-the torch restatement for CPU tensors.  On a ROCm device "auto" never falls
-back silently when the library is missing: it raises.
+the torch restatement otherwise.  The decode kernels read bf16 pages and
+suffix rows: with another cache dtype "auto" takes the torch path and an
+explicit kernel request converts them (the reference's Triton kernel
+converts them as it loads, src/refinekv/kernels/attention.py:222-235).  On
+a ROCm device "auto" never falls back silently when the library is missing:
+it raises.
 """
 
+import dataclasses
 from typing import NamedTuple
 
 import torch
 
-from .config import RefineKVConfig
+from .config import KERNEL_BACKENDS, RefineKVConfig
 from .summary import BlockSummary
 
 
@@ -27,18 +33,19 @@ def _backend(query, config):
 
     if config.backend == "torch":
         return "torch"
+    explicit = config.backend in KERNEL_BACKENDS
     on_rocm = _hip.is_rocm_device(query)
-    if config.backend == "hip" and not on_rocm:
+    if explicit and not on_rocm:
         raise RuntimeError("the HIP backend requires a ROCm GPU tensor")
     if not on_rocm:
         return "torch"
     if query.dtype != torch.bfloat16:
-        if config.backend == "hip":
+        if explicit:
             raise TypeError("the HIP backend requires BF16 queries")
         return "torch"
     dim, group = query.shape[-1], query.shape[1]
     if dim < 32 or dim > 256 or dim % 32 or group > _hip.MAX_GROUP:
-        if config.backend == "hip":
+        if explicit:
             raise ValueError("HIP requires head_dim in 32..256 (multiple of 32) and GQA group <= 16")
         return "torch"
     _hip.lib()  # raises when the kernels are not built: no silent fallback on a GPU
@@ -66,8 +73,17 @@ def _validate(query, summary, config, anchor_mask=None):
 
 
 def _check_hip_summary(summary):
-    if summary.key_mean.dtype != torch.bfloat16 or summary.keys.dtype != torch.bfloat16:
-        raise TypeError("the HIP decode kernels need bf16 summaries and a bf16 KV cache")
+    if summary.key_mean.dtype != torch.bfloat16 or summary.ellipsoid.dtype != torch.bfloat16:
+        raise TypeError("the HIP kernels need bf16 summaries (build_summary's format)")
+
+
+def _bf16_pages(summary):
+    """The summary with bf16 page views (a converted copy of the pages when
+    the cache holds another dtype)."""
+    if summary.keys.dtype == torch.bfloat16 and summary.values.dtype == torch.bfloat16:
+        return summary
+    return dataclasses.replace(summary, keys=summary.keys.to(torch.bfloat16),
+                               values=summary.values.to(torch.bfloat16))
 
 
 @torch.no_grad()
@@ -142,6 +158,10 @@ def sparse_attention(
     if key_suffix.device != query.device or value_suffix.device != query.device:
         raise ValueError("suffix K/V must be on the query device")
     backend = _backend(query, config)
+    pages_bf16 = (summary.keys.dtype == torch.bfloat16 and summary.values.dtype == torch.bfloat16
+                  and key_suffix.dtype == torch.bfloat16 and value_suffix.dtype == torch.bfloat16)
+    if backend == "hip" and not pages_bf16 and config.backend not in KERNEL_BACKENDS:
+        backend = "torch"  # "auto": the kernels read bf16 pages
     if suffix_length is not None:
         if (suffix_length.shape != () or suffix_length.device != query.device
                 or suffix_length.dtype != torch.int32):
@@ -152,10 +172,9 @@ def sparse_attention(
         from . import _hip
 
         _check_hip_summary(summary)
-        if key_suffix.dtype != torch.bfloat16 or value_suffix.dtype != torch.bfloat16:
-            raise TypeError("the HIP decode kernels need a bf16 suffix")
-        output, mask = _hip.decode(query, summary, key_suffix, value_suffix, config,
-                                   anchor_mask, workspace, suffix_length)
+        output, mask = _hip.decode(query, _bf16_pages(summary), key_suffix.to(torch.bfloat16),
+                                   value_suffix.to(torch.bfloat16), config, anchor_mask,
+                                   workspace, suffix_length)
         return AttentionResult(output, mask if return_selected else None)
     from .reference import sparse_attention as attention_torch
 

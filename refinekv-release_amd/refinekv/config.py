@@ -1,14 +1,17 @@
 """Validated RefineKV settings (mirror of src/refinekv/config.py:7-38).
 
-The only change from the reference is the backend set: ``"hip"`` replaces
-``"triton"``.  ``"auto"`` picks the HIP kernels for bf16 queries on a ROCm
-device and the torch implementation for CPU tensors.
+The only change from the reference is the backend set: ``"hip"`` joins it,
+and ``"triton"`` (the reference's accelerated backend) is accepted as another
+name for it, so configurations written for the reference keep working.
+``"auto"`` picks the HIP kernels for bf16 queries on a ROCm device and the
+torch implementation for CPU tensors.
 """
 
 from dataclasses import dataclass
 import math
 
-BACKENDS = ("auto", "torch", "hip")
+BACKENDS = ("auto", "torch", "hip", "triton")
+KERNEL_BACKENDS = ("hip", "triton")  # explicit requests for the gfx950 kernels
 REDUCTIONS = ("mean", "max", "any")
 
 
@@ -40,7 +43,7 @@ class RefineKVConfig:
         if self.gqa_reduction not in REDUCTIONS:
             raise ValueError("gqa_reduction must be 'mean', 'max', or 'any'")
         if self.backend not in BACKENDS:
-            raise ValueError("backend must be 'auto', 'torch', or 'hip'")
+            raise ValueError("backend must be 'auto', 'torch', 'hip', or 'triton'")
         for name in ("anchor_tokens", "full_attention_layers"):
             value = getattr(self, name)
             if not isinstance(value, int) or isinstance(value, bool) or value < 0:

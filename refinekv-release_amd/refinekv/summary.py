@@ -11,7 +11,7 @@ from dataclasses import dataclass
 
 import torch
 
-from .config import RefineKVConfig
+from .config import KERNEL_BACKENDS, RefineKVConfig
 
 
 @dataclass
@@ -60,13 +60,14 @@ def _use_hip(keys, config):
 
     if not keys.is_cuda or config.backend == "torch":
         return False
+    explicit = config.backend in KERNEL_BACKENDS
     if not _hip.is_rocm_device(keys):
-        if config.backend == "hip":
+        if explicit:
             raise RuntimeError("the HIP backend requires a ROCm device")
         return False
     supported = keys.dtype in _hip.DTYPE_CODES and keys.shape[-1] in _hip.SUPPORTED_DIMS
     if not supported:
-        if config.backend == "hip":
+        if explicit:
             raise ValueError("the HIP summarizer needs bf16/fp16/fp32 K/V with head_dim in "
                              "32..256 (multiple of 32)")
         return False

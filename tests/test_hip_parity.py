@@ -49,36 +49,19 @@ def assert_control_clean(hip, ws):
     words = ws["hip_scratch"][:layout["zf"]].view(torch.int64).cpu().numpy()
     lines = words[:(heads + 1) * 8].reshape(heads + 1, 8)
     assert lines[heads, 0] & 0xFFFFFFFF == 0, "a hand-off wait gave up"
+    assert hip.workspace_status(ws) == 0
     launches = words[(heads + 1) * 8:(heads + 1) * 8 + heads * ts].reshape(heads, ts)[:, :tiles]
     assert np.all(launches == launches[0, 0]), launches
     assert np.all(lines[:heads, 1] == launches[0, 0] * tiles), lines[:heads, 1]
+    # start-order tickets: none, or one per workgroup of every launch
+    assert lines[heads, 1] in (0, launches[0, 0] * tiles * heads), lines[heads, 1]
     return int(launches[0, 0])
 
 
-def step_fits(group, dim, n_blocks, heads, block):
-    """Whether rkv_decode takes the one-launch step for this shape: every
-    query row in one attention pass (4, 8 or 16 rows as head_dim allows), at
-    most 256 tiles of 64 blocks and the grid (heads x workers, workers =
-    max(tiles, min(S // heads, 256))) resident at once: S = 512 and two
-    workgroups per CU, or, for the 16-row kernels (more than 256 registers
-    per lane), S = 256 and one; with blocks of 64 or more tokens, up to two
-    rounds of it.  (Two per CU is the head_dim-128 kernels' occupancy;
-    smaller ones hold more, which matters only past 512 workgroups, a case
-    the tests run at head_dim 128.)"""
-    cap = 64 // (dim // 16)
-    rows = 16
-    while rows > cap:
-        rows //= 2
-    want = 4
-    while want < group and want < 16:
-        want *= 2
-    per_cu = 1 if min(want, rows) == 16 else 2
-    tiles = -(-n_blocks // 64)
-    workers = max(tiles, min(256 * per_cu // heads, 256))
-    resident = per_cu * torch.cuda.get_device_properties(0).multi_processor_count
-    grid = heads * workers
-    fits = grid <= resident or (block >= 64 and workers <= resident and grid <= 2 * resident)
-    return group <= min(want, rows) and tiles <= 256 and fits
+def one_launch(hip, heads, group, dim, n_blocks, block):
+    """Whether rkv_decode (default path) runs this shape as one launch, as the
+    library itself decides on this device."""
+    return hip.decode_plan(heads, group, dim, n_blocks, block) != "split"
 
 
 def bits16(t):
@@ -206,9 +189,10 @@ def test_summary_of_rows_not_16_byte_aligned(hip, oracle_lib):
 @pytest.mark.parametrize("dtype,dim,block,length", [
     (torch.bfloat16, 128, 32, 4099), (torch.bfloat16, 64, 16, 300), (torch.float16, 128, 32, 777),
     (torch.float32, 96, 64, 1000), (torch.bfloat16, 256, 32, 999), (torch.float32, 256, 64, 300)])
-def test_summary_written_with_the_cache(hip, dtype, dim, block, length):
-    """store_and_build_summary (one kernel: cache write + summary) equals a
-    cache copy followed by build_summary, bit for bit, and fills the cache."""
+def test_summary_written_with_the_cache(hip, oracle_lib, dtype, dim, block, length):
+    """store_and_build_summary (one kernel: cache write + summary) equals the
+    oracle's summary of the same keys/values bit for bit, and a cache copy
+    followed by build_summary, and fills the cache."""
     from refinekv.summary import store_and_build_summary
 
     gen = torch.Generator(device=DEV).manual_seed(dim + length)
@@ -223,6 +207,8 @@ def test_summary_written_with_the_cache(hip, dtype, dim, block, length):
     torch.cuda.synchronize()
     assert torch.equal(cache_k[0, :, :length], keys) and torch.equal(cache_v[0, :, :length], values)
     assert torch.isnan(cache_k[0, :, length:].float()).all()  # nothing written past the prompt
+    assert_summary_equal(fused, oracle_lib.summary(keys.float().cpu().numpy(),
+                                                   values.float().cpu().numpy(), block))
     ref = build_summary(keys.contiguous(), values.contiguous(), cfg)
     for name in ("counts", "key_mean", "value_mean", "ellipsoid", "value_norm", "max_value_norm"):
         a, b = getattr(fused, name), getattr(ref, name)
@@ -324,16 +310,13 @@ def test_anchor_union_matches_per_query_selection(hip, oracle_lib, heads, group,
 # Decode step
 # ---------------------------------------------------------------------------
 
-# This shape faulted the GPU on the first launch of a since-removed persistent
-# decode kernel's head_dim-256 build; the cause was never shown, so the case
-# stays off the GPU.  Other head_dim-256 decode shapes run below.
-FAULTED = (2, 4, 256, 64, 999, "max", 0.01, 0.05)
-
+# (2, 4, 256, 64, 999, "max", ...) faulted the GPU with a since-removed
+# persistent kernel (head_dim-256 build, 556 B/lane of register spills).
+# head_dim above 160 now runs only the three kernels (score, attend, merge:
+# no spills, LDS and index ranges checked on the CPU for this exact shape in
+# tests/test_kernel_resources_cpu.py), and the case runs again.
 DECODE_CASES = [
-    pytest.param(*c, marks=pytest.mark.skip(reason="faulted the GPU with a since-removed "
-                                            "persistent decode kernel; cause not shown"))
-    if c == FAULTED else c
-    for c in SELECT_CASES + [
+    c for c in SELECT_CASES + [
         (8, 4, 128, 32, 4096, "any", 0.0, 0.02),   # every block expanded (dense)
         (8, 4, 128, 32, 4096, "mean", 1e6, 0.02),  # none expanded
         (2, 2, 256, 32, 1500, "any", 0.01, 0.05),
@@ -389,7 +372,8 @@ def test_decode_matches_oracle(hip, oracle_lib, decode_path, heads, group, dim, 
             got = res.output.float().cpu().numpy()[:, :, 0]
             assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
     launches = assert_control_clean(hip, ws)
-    assert launches == (6 if decode_path == "step" and step_fits(group, dim, n, heads, block) else 0)
+    assert launches == (6 if decode_path == "step" and one_launch(hip, heads, group, dim, n, block)
+                        else 0)
 
 
 def test_device_suffix_length_matches_slicing(hip, decode_path):
@@ -551,3 +535,125 @@ def _headline_shape_128k(hip, oracle_lib):
     # The reference's output is in the query dtype: compare bf16 with bf16.
     assert_close_output(dense.output.float().reshape(32, 1, 128).cpu().numpy(),
                         want.to(torch.bfloat16).float().cpu().numpy())
+
+
+# ---------------------------------------------------------------------------
+# The BASELINE configs' attention ops at their full sizes
+# ---------------------------------------------------------------------------
+
+def _op_case(hip, oracle_lib, *, heads, group, block, prompt, reduction, eps, spikes, suffix,
+             anchors, seed, paths=("step", "split"), repeats=1):
+    """One decode step of the op at a config's full size, on each path:
+    prompt-anchor union (when anchors > 0) equal to the OR of the oracle's
+    per-query masks, decode masks equal to the oracle's, outputs within
+    tolerance, control words consistent.  Returns the oracle mask."""
+    inp = testing.decode_inputs(heads=heads, group=group, dim=128, prompt=prompt, suffix=suffix,
+                                block=block, spike_fraction=spikes, anchors=max(anchors, 1),
+                                seed=seed)
+    inp = {k: (v.to(torch.bfloat16) if v.is_floating_point() else v) for k, v in inp.items()}
+    cfg = RefineKVConfig(backend="hip", block_size=block, eps=eps, gqa_reduction=reduction)
+    k, v = inp["prompt_keys"], inp["prompt_values"]
+    summary = build_summary(k.to(DEV), v.to(DEV), cfg)
+    summ = oracle_summary_of(summary)
+    anchor = None
+    if anchors:
+        queries = inp["anchor_queries"]
+        got = select_blocks_union(queries.to(DEV), summary, cfg, workspace={})
+        want = np.zeros((heads, summary.num_blocks), np.uint8)
+        for a in range(anchors):
+            mask, _, _ = oracle_lib.select(queries[:, :, a].float().numpy(), summ, eps, reduction)
+            want |= mask
+        assert np.array_equal(got.cpu().numpy().astype(np.uint8), want), "anchor union"
+        anchor = got
+    qn = inp["query"][:, :, 0].float().numpy()
+    out, mask = oracle_lib.sparse_attention(
+        qn, summ, _pages_bits(k, block), _pages_bits(v, block), gc.bf16_bits(inp["suffix_keys"]),
+        gc.bf16_bits(inp["suffix_values"]), eps, reduction,
+        None if anchor is None else anchor.cpu().numpy())
+    want_out = torch.from_numpy(out).to(torch.bfloat16).float().numpy()
+    one = one_launch(hip, heads, group, 128, summary.num_blocks, block)
+    for path in paths:
+        hip.set_decode_path(path)
+        ws = {}
+        try:
+            for _ in range(repeats):
+                res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                                       inp["suffix_values"].to(DEV), cfg, anchor_mask=anchor,
+                                       workspace=ws, return_selected=True)
+                torch.cuda.synchronize()
+                assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask), path
+                assert_close_output(res.output.float().cpu().numpy()[:, :, 0], want_out)
+        finally:
+            hip.set_decode_path("step")
+        assert assert_control_clean(hip, ws) == (repeats if path == "step" and one else 0)
+    return mask
+
+
+def test_config1_op_llama_32k(hip, oracle_lib):
+    """BASELINE configs[1]'s attention op: 8 KV / 32 query heads, d 128,
+    32768 prompt tokens, block 32, eps 0.01, "any", 32 prompt anchors,
+    suffix 65 (the middle of a 128-token decode)."""
+    mask = _op_case(hip, oracle_lib, heads=8, group=4, block=32, prompt=32768, reduction="any",
+                    eps=0.01, spikes=0.02, suffix=65, anchors=32, seed=21)
+    assert 0.005 < mask.mean() < 0.5
+
+
+def test_config3_op_qwen_64k(hip, oracle_lib):
+    """BASELINE configs[3]'s attention op: 4 KV / 28 query heads (group 7),
+    d 128, 65536 prompt tokens, block 64, eps 0.005, "max", 64 prompt
+    anchors."""
+    _op_case(hip, oracle_lib, heads=4, group=7, block=64, prompt=65536, reduction="max",
+             eps=0.005, spikes=0.02, suffix=65, anchors=64, seed=22)
+
+
+def test_two_device_fulls_step_512k_block64(hip, oracle_lib):
+    """8 KV heads, 524288 prompt tokens, block 64: 128 tiles per head, 1024
+    workgroups, twice what the device holds at once, so the one-launch step
+    maps workgroups to (head, tile) by start-order tickets.  Two launches on
+    one workspace (the tickets and tags of the second follow the first)."""
+    n_blocks = 524288 // 64
+    assert hip.decode_plan(8, 4, 128, n_blocks, 64) == "step-ticketed"
+    _op_case(hip, oracle_lib, heads=8, group=4, block=64, prompt=524288, reduction="any",
+             eps=0.01, spikes=0.02, suffix=17, anchors=0, seed=23, paths=("step",), repeats=2)
+
+
+# ---------------------------------------------------------------------------
+# A hand-off wait that gives up is reported, not silent
+# ---------------------------------------------------------------------------
+
+def test_handoff_give_up_is_reported_and_recoverable(hip, oracle_lib):
+    """With the test hook every wait of the one-launch step accepts no data
+    and gives up after 64 polls: every kernel still ends, the status word is
+    set and check_workspace raises.  After clearing it, the same workspace
+    decodes correctly again."""
+    inp = _decode_case(8, 4, 128, 32, 8192, 0.02, suffix=9, seed=4)
+    cfg = RefineKVConfig(backend="hip", eps=0.01)
+    summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
+    assert one_launch(hip, 8, 4, 128, summary.num_blocks, 32)
+    args = (inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+            inp["suffix_values"].to(DEV), cfg)
+    ws = {}
+    sparse_attention(*args, workspace=ws)
+    torch.cuda.synchronize()
+    assert hip.workspace_status(ws) == 0
+    hip.set_handoff_test(64, 1)
+    try:
+        sparse_attention(*args, workspace=ws)
+        torch.cuda.synchronize()
+    finally:
+        hip.set_handoff_test(0, 0)
+    assert hip.workspace_status(ws) & 1
+    with pytest.raises(hip.HandoffError):
+        hip.check_workspace(ws)
+    hip.clear_workspace_status(ws)
+    res = sparse_attention(*args, workspace=ws, return_selected=True)
+    torch.cuda.synchronize()
+    summ = oracle_summary_of(summary)
+    out, mask = oracle_lib.sparse_attention(
+        inp["query"][:, :, 0].float().numpy(), summ, _pages_bits(inp["prompt_keys"], 32),
+        _pages_bits(inp["prompt_values"], 32), gc.bf16_bits(inp["suffix_keys"]),
+        gc.bf16_bits(inp["suffix_values"]), 0.01, "any")
+    assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask)
+    assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
+                        torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+    assert assert_control_clean(hip, ws) == 3

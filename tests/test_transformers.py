@@ -248,3 +248,122 @@ def test_hip_stats_and_dense_layers():
                                         collect_stats=True)) as s:
         generate(model)
         assert s.stats["equivalent_access_ratio"] == 1
+
+
+# ---------------------------------------------------------------------------
+# GPU: the hook's decode calls against the CPU oracle (eager and graph replay)
+# ---------------------------------------------------------------------------
+
+def _oracle_check(oracle_lib, call):
+    """The oracle's sparse_attention on one recorded decode call: mask equal,
+    output within the north-star tolerance.  Returns the expanded fraction."""
+    import numpy as np
+
+    def bits(t):
+        return t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    s = call["summary"]
+    summ = dict(counts=s.counts.cpu().numpy(), key_mean=bits(s.key_mean),
+                value_mean=bits(s.value_mean), ellipsoid=bits(s.ellipsoid),
+                value_norm=s.value_norm.cpu().numpy(),
+                max_value_norm=s.max_value_norm.cpu().numpy(), prompt_length=s.prompt_length,
+                block_size=s.block_size)
+    n = call["suffix"]
+    anchor = call["anchor"]
+    out, mask = oracle_lib.sparse_attention(
+        call["query"][:, :, 0].float().cpu().numpy(), summ, bits(s.keys), bits(s.values),
+        bits(call["key_suffix"][:, :n]), bits(call["value_suffix"][:, :n]), call["eps"],
+        call["reduction"], None if anchor is None else anchor.cpu().numpy())
+    got_mask = call["selected"].cpu().numpy().astype(np.uint8)
+    assert np.array_equal(got_mask, mask), "hook mask differs from the oracle"
+    want = torch.from_numpy(out).to(torch.bfloat16).float().numpy()
+    got = call["output"][:, :, 0].float().cpu().numpy()
+    err = np.abs(got - want)
+    assert err.max() <= 2e-2 and err.mean() <= 1e-3 * np.abs(want).mean() + 1e-6, err.max()
+    return float(mask.mean())
+
+
+class _Recorder:
+    """Wraps the hook's sparse_attention: eager calls are recorded with
+    copies of their inputs and outputs; a call under graph capture records a
+    device copy of the query into the graph (so every replay refreshes it)
+    and keeps references to the persistent buffers the replays reuse."""
+
+    def __init__(self, real):
+        self.real = real
+        self.eager, self.graph = [], []
+
+    def __call__(self, query, summary, key_suffix, value_suffix, config, *, anchor_mask=None,
+                 workspace=None, return_selected=False, suffix_length=None):
+        from refinekv.attention import AttentionResult
+
+        result = self.real(query, summary, key_suffix, value_suffix, config,
+                           anchor_mask=anchor_mask, workspace=workspace, return_selected=True,
+                           suffix_length=suffix_length)
+        call = dict(summary=summary, anchor=anchor_mask, eps=config.eps,
+                    reduction=config.gqa_reduction, key_suffix=key_suffix,
+                    value_suffix=value_suffix)
+        if torch.cuda.is_current_stream_capturing():
+            call.update(query=query.clone(), output=result.output, selected=result.selected,
+                        suffix_tensor=suffix_length)
+            self.graph.append(call)
+        else:
+            n = key_suffix.shape[1] if suffix_length is None else int(suffix_length.item())
+            call.update(query=query.clone(), output=result.output.clone(),
+                        selected=result.selected.clone(), suffix=n,
+                        key_suffix=key_suffix.clone(), value_suffix=value_suffix.clone())
+            self.eager.append(call)
+        return AttentionResult(result.output, result.selected if return_selected else None)
+
+
+def small_model(family):
+    torch.manual_seed(3)
+    config_cls, model_cls = {
+        "llama": (transformers.LlamaConfig, transformers.LlamaForCausalLM),
+        "qwen2": (transformers.Qwen2Config, transformers.Qwen2ForCausalLM),
+    }[family]
+    config = config_cls(vocab_size=512, hidden_size=512, intermediate_size=1024,
+                        num_hidden_layers=2, num_attention_heads=8, num_key_value_heads=2,
+                        pad_token_id=0, eos_token_id=None)
+    return model_cls(config).eval().to("cuda").to(torch.bfloat16)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("family,reduction,anchors", [("llama", "any", 4), ("qwen2", "max", 0)])
+def test_hip_hook_decode_calls_match_oracle(family, reduction, anchors, monkeypatch, oracle_lib):
+    """Every decode call the hook makes (eager generation: visible cache,
+    suffix slices; then graph replays: device suffix length over the full
+    buffer) has the oracle's mask and output for the query, summary, suffix
+    and anchor mask it was given."""
+    _gpu_or_skip()
+    from refinekv.integrations import transformers as hook
+
+    model = small_model(family)
+    recorder = _Recorder(hook.sparse_attention)
+    monkeypatch.setattr(hook, "sparse_attention", recorder)
+    config = RefineKVConfig(backend="hip", eps=0.01, block_size=16, gqa_reduction=reduction,
+                            anchor_tokens=anchors)
+    gen = torch.Generator().manual_seed(11)
+    ids = torch.randint(3, 500, (1, 700), generator=gen).cuda()
+    options = dict(input_ids=ids, attention_mask=torch.ones_like(ids), max_new_tokens=6,
+                   min_new_tokens=6, eos_token_id=None, forced_eos_token_id=None,
+                   do_sample=False)
+    with RefineKV(model, config):
+        eager_tokens = model.generate(**options)
+    assert len(recorder.eager) == 5 * 2  # 5 decode forwards x 2 layers
+    fractions = [_oracle_check(oracle_lib, call) for call in recorder.eager]
+    assert all(0 < f <= 1 for f in fractions)
+    recorder.eager.clear()
+    with RefineKV(model, config, cuda_graph=True):
+        graph_tokens = model.generate(**options)
+        # (the graph's replays have run: its last replay left its query copy,
+        # mask and output in the recorded buffers)
+        assert len(recorder.graph) == 2
+        for call in recorder.graph:
+            call["suffix"] = int(call["suffix_tensor"].item())
+            assert call["suffix"] == 5
+            _oracle_check(oracle_lib, call)
+    assert torch.equal(graph_tokens, eager_tokens)
+    assert recorder.eager, "the graph path's warm-up steps run eagerly"
+    for call in recorder.eager:
+        _oracle_check(oracle_lib, call)
