@@ -40,6 +40,18 @@ def log(msg):
     print(msg, file=sys.stderr, flush=True)
 
 
+# BASELINE.json configs[1..3] as model stacks (random-init weights of the
+# named architectures; uniform random prompt ids).
+MODEL_CONFIGS = {
+    "llama32k": dict(family="llama", prompt=32768, block=32, eps=0.01, reduction="any",
+                     anchors=32, config_index=1),
+    "llama128k": dict(family="llama", prompt=131072, block=32, eps=0.01, reduction="any",
+                      anchors=0, config_index=2),
+    "qwen64k": dict(family="qwen2", prompt=65536, block=64, eps=0.005, reduction="max",
+                    anchors=64, config_index=3),
+}
+
+
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -56,8 +68,8 @@ def parse_args():
     ap.add_argument("--spikes", type=float, default=0.02)
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--no-dense", action="store_true", help="skip the eps=0 dense baseline")
-    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
-    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true",
+                    help="skip the CPU baseline (the reference's torch CPU backend)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 64 MiB buffer 5 times (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings to bytes)")
@@ -72,6 +84,11 @@ def parse_args():
                     help="--sweep: prompt lengths, comma-separated")
     ap.add_argument("--sweep-blocks", default="16,32,64",
                     help="--sweep: block sizes, comma-separated")
+    ap.add_argument("--model", choices=sorted(MODEL_CONFIGS),
+                    help="run a BASELINE.json model config as a random-init model stack "
+                         "through RefineKV(cuda_graph=True) and report per-layer attention "
+                         "time and expanded fractions")
+    ap.add_argument("--new-tokens", type=int, default=128, help="--model: tokens to generate")
     return ap.parse_args()
 
 
@@ -162,6 +179,9 @@ def main():
         return
     if a.sweep:
         sweep(a)
+        return
+    if a.model:
+        model_bench(a)
         return
     from refinekv import RefineKVConfig, build_summary, sparse_attention, _hip
 
@@ -290,11 +310,16 @@ def main():
         for L in layers:
             L["dws"].clear()
 
-    # ---- CPU baseline: the oracle (C restatement), one thread -----------
+    # ---- blocks within 1e-6 relative of eps ------------------------------
+    near, blocks = near_eps_blocks(a, layers, suffix_now)
+    log(f"[bench] near-eps blocks: {near} of {blocks}")
+
+    # ---- CPU baseline: the reference's torch CPU backend -------------------
     cpu = None
     if not a.no_cpu:
         cpu = cpu_baseline(a, layers[0], suffix_now)
-        log(f"[bench] cpu oracle: {cpu['value']:.0f} us/layer-step ({cpu['sample']})")
+        log(f"[bench] cpu torch backend: {cpu['value']:.0f} us/layer-step on {cpu['cores']} "
+            f"cores, {cpu['one_thread_value']:.0f} on one")
 
     result = {
         "metric": METRIC,
@@ -331,6 +356,8 @@ def main():
         },
         "cpu_baseline": cpu,
         "expanded_fraction": round(frac, 5),
+        "near_eps_blocks": near,
+        "near_eps_of_blocks": blocks,
         "kernel_us": {k: round(v, 3) for k, v in kernel_us.items()},
         "kernel_timing": timing,
         "algorithmic_bytes": {k: int(v) for k, v in nbytes.items()},
@@ -439,6 +466,182 @@ def sweep(a):
                 torch.cuda.empty_cache()
 
 
+def _model(family, max_positions, seed):
+    """Random-init Llama-3.1-8B / Qwen2.5-7B-shaped causal LM, bf16, built on
+    the GPU."""
+    import transformers
+
+    if family == "llama":
+        config = transformers.LlamaConfig(
+            vocab_size=128256, hidden_size=4096, intermediate_size=14336, num_hidden_layers=32,
+            num_attention_heads=32, num_key_value_heads=8, max_position_embeddings=max_positions,
+            rms_norm_eps=1e-5, rope_parameters={"rope_type": "default", "rope_theta": 500000.0},
+            bos_token_id=None, eos_token_id=None, pad_token_id=None)
+        cls = transformers.LlamaForCausalLM
+    else:
+        config = transformers.Qwen2Config(
+            vocab_size=152064, hidden_size=3584, intermediate_size=18944, num_hidden_layers=28,
+            num_attention_heads=28, num_key_value_heads=4, max_position_embeddings=4 * 32768,
+            rms_norm_eps=1e-6, rope_parameters={"rope_type": "yarn", "factor": 4.0,
+                                                "original_max_position_embeddings": 32768,
+                                                "rope_theta": 1000000.0},
+            use_sliding_window=False, bos_token_id=None, eos_token_id=None, pad_token_id=None)
+        cls = transformers.Qwen2ForCausalLM
+    torch.manual_seed(seed)
+    saved = torch.get_default_dtype()
+    torch.set_default_dtype(torch.bfloat16)
+    try:
+        with torch.device("cuda"):
+            model = cls(config)
+    finally:
+        torch.set_default_dtype(saved)
+    return model.eval(), config
+
+
+class _GraphTap:
+    """Wraps the RefineKV hook's sparse_attention.  Every decode call adds
+    its mask to a per-layer count of how often each block expanded (made on
+    the layer's first, eager, call); under graph capture the add and a copy
+    of the layer's query become part of the captured step, so every replay
+    refreshes them.  It keeps the layer's call arguments for the isolated
+    replay afterwards."""
+
+    def __init__(self, real):
+        self.real = real
+        self.layers = []
+        self.expanded = {}  # id(workspace) -> (int32 counts, calls)
+
+    def __call__(self, query, summary, key_suffix, value_suffix, config, *, anchor_mask=None,
+                 workspace=None, return_selected=False, suffix_length=None,
+                 access_counter=None):
+        from refinekv.attention import AttentionResult
+
+        result = self.real(query, summary, key_suffix, value_suffix, config,
+                           anchor_mask=anchor_mask, workspace=workspace, return_selected=True,
+                           suffix_length=suffix_length, access_counter=access_counter)
+        capturing = torch.cuda.is_current_stream_capturing()
+        key = id(workspace)
+        if key not in self.expanded:
+            assert not capturing, "the first decode call of a layer runs eagerly"
+            self.expanded[key] = [torch.zeros(result.selected.shape, dtype=torch.int32,
+                                              device=query.device), 0]
+        counts = self.expanded[key]
+        counts[0].add_(result.selected)
+        counts[1] += 1
+        if capturing:
+            self.layers.append(dict(query=query.clone(), summary=summary, key_suffix=key_suffix,
+                                    value_suffix=value_suffix, config=config,
+                                    anchor=anchor_mask, suffix_length=suffix_length,
+                                    expanded=counts))
+        return AttentionResult(result.output, result.selected if return_selected else None)
+
+
+def model_bench(a):
+    """BASELINE.json configs[1..3] as random-init model stacks: prefill with
+    RefineKV (dense SDPA prefill, summaries, prompt anchors), then
+    --new-tokens greedy tokens as replays of one captured HIP graph per
+    token.  Reports per layer the fraction of blocks expanded over the
+    replays, and the attention op's us per layer-step: its kernels timed in
+    isolation by replaying all layers' decode calls (the last step's query,
+    summary, suffix and anchors) as one graph, 125 times."""
+    import statistics
+
+    from refinekv import RefineKV, RefineKVConfig, sparse_attention
+    from refinekv.integrations import transformers as hook
+
+    spec = MODEL_CONFIGS[a.model]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    new = a.new_tokens
+    t0 = time.perf_counter()
+    model, mconfig = _model(spec["family"], spec["prompt"] + new + 8, a.seed)
+    torch.cuda.synchronize()
+    log(f"[model] {a.model}: {sum(p.numel() for p in model.parameters()) / 1e9:.2f}B parameters "
+        f"initialised in {time.perf_counter() - t0:.1f} s")
+    gen = torch.Generator().manual_seed(a.seed + 1)
+    ids = torch.randint(0, mconfig.vocab_size, (1, spec["prompt"]), generator=gen).to(dev)
+    cfg = RefineKVConfig(backend="hip", block_size=spec["block"], eps=spec["eps"],
+                         gqa_reduction=spec["reduction"], anchor_tokens=spec["anchors"])
+    tap = _GraphTap(hook.sparse_attention)
+    hook.sparse_attention = tap
+    try:
+        with RefineKV(model, cfg, cuda_graph=True) as session:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            out = model.generate(input_ids=ids, attention_mask=torch.ones_like(ids),
+                                 max_new_tokens=new, min_new_tokens=new, eos_token_id=None,
+                                 forced_eos_token_id=None, do_sample=False)
+            torch.cuda.synchronize()
+            wall = time.perf_counter() - t0
+            assert out.shape[1] == spec["prompt"] + new
+            replays = new - 1 - min(2, new - 2)
+            layers = tap.layers
+            # eager warm-up calls, the capture (recorded, not run) and the replays
+            calls = [L["expanded"][1] - 1 + replays for L in layers]
+            fractions = [float(L["expanded"][0].float().mean().item()) / n
+                         for L, n in zip(layers, calls)]
+            # the attention op alone: every layer's decode call of the last step
+            suffix_now = int(layers[0]["suffix_length"].item())
+            steps = 125
+            for L in layers:
+                L["ws"] = {}
+                L["args"] = (L["query"], L["summary"], L["key_suffix"], L["value_suffix"],
+                             L["config"])
+
+            def op_step(config=None):
+                for L in layers:
+                    sparse_attention(*L["args"][:4], config or L["config"],
+                                     anchor_mask=L["anchor"], workspace=L["ws"],
+                                     suffix_length=L["suffix_length"])
+
+            def time_graph(config=None):
+                op_step(config)
+                torch.cuda.synchronize()
+                graph = torch.cuda.CUDAGraph()
+                with torch.cuda.graph(graph):
+                    op_step(config)
+                graph.replay()
+                torch.cuda.synchronize()
+                e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for _ in range(steps):
+                    graph.replay()
+                e1.record()
+                torch.cuda.synchronize()
+                return e0.elapsed_time(e1) * 1e3 / (steps * len(layers))
+
+            us = time_graph()
+            for L in layers:
+                L["ws"] = {}
+            dense_us = time_graph(RefineKVConfig(backend="hip", block_size=spec["block"],
+                                                 eps=0.0, gqa_reduction=spec["reduction"]))
+            check = session.check_handoffs
+            check()
+    finally:
+        hook.sparse_attention = tap.real
+    heads, group, dim = layers[0]["query"].shape[0], layers[0]["query"].shape[1], 128
+    result = {
+        "metric": f"RefineKV decode attention on a random-init model stack, {a.model}",
+        "config_index": spec["config_index"],
+        "model": {"family": spec["family"], "layers": len(layers), "kv_heads": heads,
+                  "q_heads": heads * group, "head_dim": dim, "weights": "random init (seeded)",
+                  "prompt": "uniform random token ids"},
+        "prompt_tokens": spec["prompt"], "new_tokens": new,
+        "refinekv": {"block_size": spec["block"], "eps": spec["eps"],
+                     "gqa_reduction": spec["reduction"], "anchor_tokens": spec["anchors"]},
+        "expanded_fraction_mean": round(statistics.fmean(fractions), 5),
+        "decode_calls_per_layer": calls[0],
+        "expanded_fraction_per_layer": [round(f, 4) for f in fractions],
+        "attention_us_per_layer_step": round(us, 3),
+        "attention_timing": f"the {len(layers)} layers' decode calls at suffix {suffix_now} "
+                            f"(last step's queries), one HIP graph, {steps} replays",
+        "dense_eps0_us_per_layer_step": round(dense_us, 3),
+        "speedup_vs_dense_eps0": round(dense_us / us, 3),
+        "generate_wall_s": round(wall, 2),
+    }
+    print(json.dumps(result), flush=True)
+
+
 def measured_traffic(kernel):
     """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
     summary (FETCH_SIZE and WRITE_SIZE runs scaled by a plain copy's
@@ -464,37 +667,125 @@ def copy_calibration():
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "copies": 5}))
 
 
-def cpu_baseline(a, layer, suffix):
-    """The oracle's select + mixed attention on one layer's tensors, timed on
-    the host for about --cpu-seconds (single thread)."""
-    import numpy as np
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    import oracle
 
-    s = layer["summary"]
-    bits = lambda t: t.detach().cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
-    summ = dict(counts=s.counts.cpu().numpy(), key_mean=bits(s.key_mean),
-                value_mean=bits(s.value_mean), ellipsoid=bits(s.ellipsoid),
-                value_norm=s.value_norm.cpu().numpy(),
-                max_value_norm=s.max_value_norm.cpu().numpy(), prompt_length=s.prompt_length,
-                block_size=s.block_size)
-    kp, vp = bits(s.keys), bits(s.values)
-    ks = bits(layer["k"][:, a.context:a.context + suffix])
-    vs = bits(layer["v"][:, a.context:a.context + suffix])
-    q = layer["q"][:, :, 0].float().cpu().numpy()
-    oracle.sparse_attention(q, summ, kp, vp, ks, vs, a.eps, a.reduction)  # warm
-    n, t0 = 0, time.perf_counter()
-    while True:
-        oracle.sparse_attention(q, summ, kp, vp, ks, vs, a.eps, a.reduction)
-        n += 1
-        el = time.perf_counter() - t0
-        if el >= a.cpu_seconds or n >= 1000:
+def _median_us(fn, reps, warmup=3, budget_s=None):
+    """Median wall time of fn() in us over `reps` runs after `warmup` runs
+    (fewer runs, at least 5, if `budget_s` runs out first)."""
+    for _ in range(warmup):
+        fn()
+    times, t_start = [], time.perf_counter()
+    while len(times) < reps:
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+        if budget_s is not None and len(times) >= 5 and time.perf_counter() - t_start > budget_s:
             break
-    return {"value": round(el / n * 1e6, 1), "unit": "us/step/layer", "cores": 1,
-            "kind": "port",
-            "sample": f"{n} layer-steps of the same workload on one layer's tensors "
-                      f"({a.context} tokens, suffix {suffix}), oracle C restatement "
-                      f"(oracle/rkv_oracle.c), 1 thread, {os.cpu_count()} host CPUs visible"}
+    times.sort()
+    return times[len(times) // 2] * 1e6, len(times)
+
+
+def cpu_baseline(a, layer, suffix):
+    """The reference's PyTorch CPU backend (this package's torch restatement
+    of it, bit-identical to the reference on the golden fixtures) timed on
+    this host: sparse_attention (selection + mixed attention) on one layer of
+    the headline workload, with every usable core and with one thread, median
+    of >= 30 runs after 3 warm-ups; and BASELINE.json configs[0] (fp32, 4096
+    prompt + 16 suffix tokens, 32 anchors): sparse_attention and
+    build_summary, with every usable core and one thread."""
+    from refinekv import RefineKVConfig, build_summary, sparse_attention, testing
+    from refinekv.summary import BlockSummary
+
+    cores = len(os.sched_getaffinity(0))
+    saved = torch.get_num_threads()
+    s = layer["summary"]
+    # the GPU summary equals the torch path's bit for bit (pinned by the tests)
+    cpu_summary = BlockSummary(**{f: (getattr(s, f).cpu() if torch.is_tensor(getattr(s, f))
+                                      else getattr(s, f))
+                                  for f in ("keys", "values", "counts", "key_mean", "value_mean",
+                                            "ellipsoid", "value_norm", "max_value_norm",
+                                            "prompt_length", "block_size")})
+    q = layer["q"].cpu()
+    ks = layer["k"][:, a.context:a.context + suffix].cpu()
+    vs = layer["v"][:, a.context:a.context + suffix].cpu()
+    cfg = RefineKVConfig(backend="torch", block_size=a.block, eps=a.eps,
+                         gqa_reduction=a.reduction)
+    head = lambda: sparse_attention(q, cpu_summary, ks, vs, cfg)
+
+    inp = testing.decode_inputs(heads=8, group=4, dim=128, prompt=4096, suffix=16, block=32,
+                                spike_fraction=0.02, anchors=32, seed=0)
+    cfg1 = RefineKVConfig(backend="torch", block_size=32, eps=0.01, gqa_reduction="any",
+                          anchor_tokens=32)
+    s1 = build_summary(inp["prompt_keys"], inp["prompt_values"], cfg1)
+    from refinekv.attention import select_blocks_union
+    anchor1 = select_blocks_union(inp["anchor_queries"], s1, cfg1)
+    c1_attn = lambda: sparse_attention(inp["query"], s1, inp["suffix_keys"],
+                                       inp["suffix_values"], cfg1, anchor_mask=anchor1)
+    c1_summ = lambda: build_summary(inp["prompt_keys"], inp["prompt_values"], cfg1)
+    out = {}
+    try:
+        for threads in (cores, 1):
+            torch.set_num_threads(threads)
+            key = "all" if threads == cores else "one"
+            out[f"head_{key}"] = _median_us(head, 30, budget_s=20.0)
+            out[f"c1_attn_{key}"] = _median_us(c1_attn, 30)
+            out[f"c1_summ_{key}"] = _median_us(c1_summ, 30)
+    finally:
+        torch.set_num_threads(saved)
+    (v_all, n_all), (v_one, n_one) = out["head_all"], out["head_one"]
+    return {
+        "value": round(v_all, 1), "unit": "us/step/layer", "cores": cores, "kind": "port",
+        "sample": f"reference torch CPU backend (refinekv backend='torch', bit-identical to the "
+                  f"reference's torch path on the golden fixtures): sparse_attention on one "
+                  f"layer of the headline workload ({a.context} tokens, suffix {suffix}, bf16), "
+                  f"median of {n_all} runs after 3 warm-ups with torch.set_num_threads({cores}) "
+                  f"(len(os.sched_getaffinity(0))); CPU {_cpu_model()}, torch {torch.__version__}",
+        "one_thread_value": round(v_one, 1),
+        "one_thread_runs": n_one,
+        "config1_fp32": {
+            "workload": "BASELINE configs[0]: 8 KV / 32 q heads, d128, fp32, 4096 prompt + 16 "
+                        "suffix tokens, block 32, eps 0.01, any, 32 anchors",
+            "sparse_attention_us": {"all_cores": round(out["c1_attn_all"][0], 1),
+                                    "one_thread": round(out["c1_attn_one"][0], 1)},
+            "build_summary_us": {"all_cores": round(out["c1_summ_all"][0], 1),
+                                 "one_thread": round(out["c1_summ_one"][0], 1)},
+            "runs": 30, "warmup": 3,
+        },
+    }
+
+
+def near_eps_blocks(a, layers, suffix_len):
+    """Blocks whose GQA-reduced risk lies within 1e-6 relative of eps (where
+    the north star allows a mask to differ from the reference's fp32 order),
+    over every layer at the current step: (count, blocks)."""
+    from refinekv import _hip
+
+    count = total = 0
+    cfg = _hip_cfg(a)
+    for L in layers:
+        s = L["summary"]
+        risk = torch.empty(a.heads, a.group, s.num_blocks, device=L["q"].device)
+        _hip.select(L["q"], s, cfg, {}, risk_out=risk)
+        reduced = risk.mean(1) if a.reduction == "mean" else risk.amax(1)
+        count += int(((reduced - a.eps).abs() <= 1e-6 * a.eps).sum().item())
+        total += reduced.numel()
+    return count, total
+
+
+def _hip_cfg(a):
+    from refinekv import RefineKVConfig
+
+    return RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps,
+                          gqa_reduction=a.reduction)
 
 
 if __name__ == "__main__":

@@ -138,6 +138,7 @@ def sparse_attention(
     workspace: dict | None = None,
     return_selected: bool = False,
     suffix_length: torch.Tensor | None = None,
+    access_counter: torch.Tensor | None = None,
 ) -> AttentionResult:
     """Attend to representatives, expanded prompt blocks and the exact suffix.
 
@@ -147,6 +148,12 @@ def sparse_attention(
     fixed-capacity suffix buffer, for HIP graph replay.  HIP outputs live in
     the workspace and are overwritten by the next call that reuses it; clone
     them to keep them longer.
+
+    ``access_counter`` (no reference counterpart): an int64 scalar on the
+    query device to which the call adds the block term of the access counter,
+    the sum over (KV head, block) of the block's token count if it expanded
+    and 1 otherwise (src/refinekv/integrations/transformers.py:590-594
+    computes it from the mask); the HIP kernels add it in-kernel.
     """
     config = config or RefineKVConfig(block_size=summary.block_size)
     _validate(query, summary, config, anchor_mask)
@@ -162,6 +169,10 @@ def sparse_attention(
                   and key_suffix.dtype == torch.bfloat16 and value_suffix.dtype == torch.bfloat16)
     if backend == "hip" and not pages_bf16 and config.backend not in KERNEL_BACKENDS:
         backend = "torch"  # "auto": the kernels read bf16 pages
+    if access_counter is not None and (access_counter.shape != ()
+                                       or access_counter.dtype != torch.int64
+                                       or access_counter.device != query.device):
+        raise ValueError("access_counter must be a scalar int64 tensor on the query device")
     if suffix_length is not None:
         if (suffix_length.shape != () or suffix_length.device != query.device
                 or suffix_length.dtype != torch.int32):
@@ -174,10 +185,12 @@ def sparse_attention(
         _check_hip_summary(summary)
         output, mask = _hip.decode(query, _bf16_pages(summary), key_suffix.to(torch.bfloat16),
                                    value_suffix.to(torch.bfloat16), config, anchor_mask,
-                                   workspace, suffix_length)
+                                   workspace, suffix_length, access_counter)
         return AttentionResult(output, mask if return_selected else None)
     from .reference import sparse_attention as attention_torch
 
     output, selected = attention_torch(query, summary, key_suffix, value_suffix, config,
                                        anchor_mask)
+    if access_counter is not None:
+        access_counter += (selected * summary.counts).sum() + (~selected).sum()
     return AttentionResult(output, selected if return_selected else None)

@@ -191,6 +191,8 @@ class RefineKV:
         self._cache = None
         self._active = False
         self._totals = self._zero_totals()
+        self._block_accesses = None  # device int64: the kernels' block term
+        self._group = 1
 
     @staticmethod
     def _zero_totals():
@@ -200,11 +202,27 @@ class RefineKV:
     def stats(self):
         """Decode-only KV access counters (transformers.py:161-176): an
         unexpanded block counts as one representative token.  Reading this
-        synchronizes the device when counters are tensors."""
+        synchronizes the device when counters are tensors, and raises
+        refinekv._hip.HandoffError if a HIP decode step of a live layer had a
+        hand-off wait give up (its outputs were not to be trusted)."""
+        self.check_handoffs()
         totals = {k: (v.item() if torch.is_tensor(v) else v) for k, v in self._totals.items()}
+        blocks = self._block_accesses
+        if blocks is not None:
+            # the kernels' block term counts per KV head; each serves `group` query heads
+            totals["accessed"] += int(blocks.item()) * self._group
         dense = totals["dense"]
         totals["equivalent_access_ratio"] = totals["accessed"] / dense if dense else None
         return totals
+
+    def check_handoffs(self):
+        """Raise HandoffError if any live layer's HIP decode workspace had a
+        hand-off wait give up (a host synchronization per layer)."""
+        from .. import _hip
+
+        for state in self._layers.values():
+            if "hip_scratch" in state.workspace:
+                _hip.check_workspace(state.workspace)
 
     # -- context ---------------------------------------------------------
     def __enter__(self):
@@ -300,6 +318,7 @@ class RefineKV:
         self._layers.clear()
         self._anchor_queries.clear()
         self._totals = self._zero_totals()
+        self._block_accesses = None
         self._cache = cache
         # the visible caches build the sparse layers' summaries as they take
         # the prompt
@@ -561,18 +580,23 @@ class RefineKV:
                 self._record(dense, dense)
             return self._dense_decode(module, query, key, value, mask, scaling, kwargs,
                                       state.visible_length)
+        counter = None
+        if self.config.collect_stats:
+            # expanded blocks count their tokens, the others one representative:
+            # the call adds that block term (per KV head) to one device counter
+            if self._block_accesses is None:
+                self._block_accesses = torch.zeros((), dtype=torch.int64, device=query.device)
+                self._group = groups
+            counter = self._block_accesses
         result = sparse_attention(
             query[0].reshape(heads, groups, 1, dim), state.summary,
             key[0, :, state.prompt_length:state.visible_length],
             value[0, :, state.prompt_length:state.visible_length],
             self.config, anchor_mask=state.anchor_mask, workspace=state.workspace,
-            return_selected=self.config.collect_stats)
+            access_counter=counter)
         if self.config.collect_stats:
-            sel = result.selected
-            # expanded blocks count their tokens, the others one representative
-            per_head = (sel * state.summary.counts).sum() + (~sel).sum()
             suffix = query.shape[1] * (state.visible_length - state.prompt_length)
-            self._record(per_head * groups + suffix, query.shape[1] * state.visible_length)
+            self._record(suffix, query.shape[1] * state.visible_length)
         return self._to_model_layout(result.output, query), None
 
     @staticmethod

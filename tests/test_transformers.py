@@ -294,12 +294,13 @@ class _Recorder:
         self.eager, self.graph = [], []
 
     def __call__(self, query, summary, key_suffix, value_suffix, config, *, anchor_mask=None,
-                 workspace=None, return_selected=False, suffix_length=None):
+                 workspace=None, return_selected=False, suffix_length=None,
+                 access_counter=None):
         from refinekv.attention import AttentionResult
 
         result = self.real(query, summary, key_suffix, value_suffix, config,
                            anchor_mask=anchor_mask, workspace=workspace, return_selected=True,
-                           suffix_length=suffix_length)
+                           suffix_length=suffix_length, access_counter=access_counter)
         call = dict(summary=summary, anchor=anchor_mask, eps=config.eps,
                     reduction=config.gqa_reduction, key_suffix=key_suffix,
                     value_suffix=value_suffix)
