@@ -889,16 +889,284 @@ __device__ __forceinline__ void fold_tokens(GroupState<D, GBM>& st,
   fold<D, GBM, R>(st, x, v, gn);
 }
 
+// ---------------------------------------------------------------------------
+// Page rows on the matrix cores
+// ---------------------------------------------------------------------------
+// A wave attends 16-token chunks of page rows with MFMA.  QK^T:
+// v_mfma_f32_16x16x32_bf16 with A = the chunk's key rows straight from
+// memory (lane l: row l % 16, columns 8 (l / 16) + 32 s .. +7, 16 bytes) and
+// B = the query rows (lane l: row g = l % 16, the same columns; zero past
+// the pass's rows) gives S[t][g] in lane l for t = 4 (l / 16) + i, i = 0..3,
+// g = l % 16.  The online softmax works on those values in place, and PV,
+// v_mfma_f32_16x16x16_bf16, takes them unchanged as its A operand (lane l:
+// P[g = l % 16][t = 4 (l / 16) + j]); its B operand (lane l: V[t = 4 (l /
+// 16) + j][d0 + l % 16]) is one transposing LDS read (ds_read_b64_tr_b16:
+// within each 16 lanes, lane p addresses 4 values of row p / 4 at column
+// 4 (p % 4) and receives column p of the 4 rows) of the chunk's value rows,
+// which buffer-to-LDS loads stage per wave.  The output O[g][d0 + n] sits in
+// lane (g / 4) * 16 + n, register g % 4, one 4-register accumulator per 16
+// columns.  Logits use the same bf16 products as the oracle's fp64 softmax;
+// the sums' order is the matrix core's (tolerance-checked attention); P
+// enters as the sum of two bf16 parts.
+typedef __bf16 Bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 Bf16x2v __attribute__((ext_vector_type(2)));
+typedef short I16x4 __attribute__((ext_vector_type(4)));
+typedef float F32x4 __attribute__((ext_vector_type(4)));
+typedef float F32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t U32x2 __attribute__((ext_vector_type(2)));
+
+constexpr int kMmaStages = 3;     // value-chunk buffers per wave: two chunks in flight
+constexpr int kMmaMaxDim = 160;   // head dims whose page rows run on the matrix cores
+
+template <int D>
+struct MmaShape {
+  static constexpr int kSteps = D / 32;             // QK MFMAs per chunk (32 columns each)
+  static constexpr int kBlocks = D / 16;            // PV MFMAs per chunk (16 columns each)
+  static constexpr int kNC = D / 8;                 // 16-byte pieces per row
+  static constexpr int kChunkBytes = 16 * D * 2;    // one chunk of value rows
+  static constexpr int kLdsLoads = kChunkBytes / 1024;  // wave-wide 16-byte LDS loads per chunk
+  static constexpr int kOps = kSteps + kLdsLoads;   // memory ops one chunk issues
+};
+
+// A wave's staged value chunks: row t of a chunk holds its 16-byte piece c at
+// position (c + 2 t) mod kNC, so the 16 rows a transposing read touches at
+// one column start on different banks.
+template <int D>
+struct MmaStage {
+  alignas(16) char bytes[kMmaStages][MmaShape<D>::kChunkBytes];
+};
+
+// A wave's attention state after its page rows, for the combine.
+template <int D, int GBM>
+struct MmaOut {
+  float acc[GBM][D];
+  float ml[GBM][2];
+};
+
+template <int D>
+struct MmaState {
+  F32x4 o[MmaShape<D>::kBlocks];  // O[4 (l / 16) + i][16 b + l % 16] in o[b][i]
+  float m;                        // running max of row l % 16
+  float lsum;                     // this lane's share of row l % 16's denominator
+};
+
+__device__ __forceinline__ Bf16x8 load_b128(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(Bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0));
+}
+
+// A buffer view of `bytes` bytes at `base`; both must be wave-uniform (they
+// are read from the first lane, so the view lives in scalar registers and the
+// loads through it need no per-lane descriptor loop).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_view(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)a);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(a >> 32));
+  void* p = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, (short)0,
+                                           (int)__builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// Waits until at most N vector-memory operations of this wave are pending
+// (the buffer-to-LDS loads of a chunk are among them; the compiler does not
+// track their LDS results).
+template <int N>
+__device__ __forceinline__ void wait_vm() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Issues one chunk: the K operands of its 16 rows (lane l: row l % 16,
+// columns 8 (l / 16) + 32 s .. +7) and its 16 value rows into the staged
+// layout at dst.  krow(t) / vrow(t): byte offsets of row t in kres / vres.
+template <int D, typename KRow, typename VRow>
+__device__ __forceinline__ void mma_issue_rows(__amdgpu_buffer_rsrc_t kres,
+                                               __amdgpu_buffer_rsrc_t vres, char* dst,
+                                               Bf16x8 (&kop)[MmaShape<D>::kSteps], KRow krow,
+                                               VRow vrow) {
+  using S = MmaShape<D>;
+  constexpr uint32_t NC = S::kNC;
+  typedef __attribute__((address_space(3))) void LdsVoid;
+  const uint32_t lane = threadIdx.x % kWave;
+  const uint32_t k_off = krow(lane & 15u) + (lane >> 4) * 16u;
+#pragma unroll
+  for (int s = 0; s < S::kSteps; ++s) kop[s] = load_b128(kres, k_off + 64u * s);
+#pragma unroll
+  for (int u = 0; u < S::kLdsLoads; ++u) {
+    // staged position p = 64 u + l: row p / NC, position p % NC holds piece
+    // (position - 2 row) mod NC of that row
+    const uint32_t p = 64u * u + lane, t = p / NC;
+    const uint32_t piece = (p % NC + 32u * NC - 2u * t) % NC;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (LdsVoid*)(dst + 1024 * u), 16,
+                                             (int)(vrow(t) + piece * 16u), 0, 0, 0);
+  }
+}
+
+// QK^T of a chunk: S[t = 4 (l / 16) + i][g = l % 16] in lane l, register i.
+template <int D>
+__device__ __forceinline__ F32x4 mma_qk(const Bf16x8 (&kop)[MmaShape<D>::kSteps],
+                                        const Bf16x8 (&qop)[MmaShape<D>::kSteps]) {
+  F32x4 s4 = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+  for (int s = 0; s < MmaShape<D>::kSteps; ++s)
+    s4 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kop[s], qop[s], s4, 0, 0, 0);
+  return s4;
+}
+
+// Folds a chunk into the wave's state: x[i] is the logit of row t = 4 (l /
+// 16) + i for query row l % 16 (-inf for rows that do not count), src the
+// chunk's staged value rows.  Online softmax in place, then PV with P as a
+// sum of two bf16 parts (relative error ~2^-17, where bf16 alone leaves
+// 2^-9) against the same value rows.
+template <int D>
+__device__ __forceinline__ void mma_fold(MmaState<D>& st, const float (&x)[4], const char* src) {
+  using S = MmaShape<D>;
+  constexpr uint32_t NC = S::kNC;
+  const int lane = threadIdx.x % kWave;
+  float mx = fmaxf(fmaxf(x[0], x[1]), fmaxf(x[2], x[3]));
+  float a, b2;
+  xor16_pair(mx, a, b2);
+  mx = fmaxf(a, b2);
+  xor32_pair(mx, a, b2);
+  mx = fmaxf(a, b2);
+  const float mn = fmaxf(st.m, mx);
+  const float ms = mn == kNegInf ? 0.0f : mn;
+  const float alpha = __builtin_amdgcn_exp2f((st.m - ms) * kLog2e);
+  float p[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) p[i] = __builtin_amdgcn_exp2f((x[i] - ms) * kLog2e);
+  st.lsum = __builtin_fmaf(st.lsum, alpha, (p[0] + p[1]) + (p[2] + p[3]));
+  st.m = mn;
+  if (__ballot(alpha != 1.0f) != 0) {
+    // O's rows in this lane: 4 (l / 16) + i; their factors from lanes 0..15
+    float ar[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) ar[i] = __shfl(alpha, 4 * (lane >> 4) + i, kWave);
+#pragma unroll
+    for (int b = 0; b < S::kBlocks; ++b)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) st.o[b][i] *= ar[i];
+  }
+  // (whole bf16 pairs as 32-bit words: extracting single bf16 elements of
+  // the converted pairs miscompiles to a duplicated half)
+  auto pack = [](float x0, float x1) {
+    const F32x2 v = {x0, x1};
+    return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, Bf16x2v));
+  };
+  const uint32_t h01 = pack(p[0], p[1]), h23 = pack(p[2], p[3]);
+  const U32x2 hw = {h01, h23};
+  const U32x2 lw = {pack(p[0] - bits_f32(h01 << 16), p[1] - bits_f32(h01 & 0xFFFF0000u)),
+                    pack(p[2] - bits_f32(h23 << 16), p[3] - bits_f32(h23 & 0xFFFF0000u))};
+  const I16x4 ph = __builtin_bit_cast(I16x4, hw), pl = __builtin_bit_cast(I16x4, lw);
+  // transposing reads: row 4 (l / 16) + (l % 16) / 4, column 16 b + 4 (l % 4)
+  const uint32_t t_row = 4u * (uint32_t)(lane >> 4) + (uint32_t)((lane & 15) >> 2);
+  const uint32_t base = t_row * (uint32_t)(D * 2) + (uint32_t)(lane & 1) * 8u;
+  const uint32_t rot = ((uint32_t)(lane >> 1) & 1u) + 2u * t_row;
+  I16x4 vb[S::kBlocks];
+#pragma unroll
+  for (int b = 0; b < S::kBlocks; ++b) {
+    const uint32_t piece = (2u * b + rot) % NC;
+    vb[b] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) I16x4*)(src + base + piece * 16u));
+    st.o[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb[b], st.o[b], 0, 0, 0);
+  }
+#pragma unroll
+  for (int b = 0; b < S::kBlocks; ++b)
+    st.o[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(pl, vb[b], st.o[b], 0, 0, 0);
+}
+
+// Runs `count` chunks of one wave through three stages, two chunks in
+// flight: issue(j, sidx, kop) issues chunk j (exactly MmaShape<D>::kOps
+// memory operations, or none for a chunk whose loads were issued before the
+// ring started) into stage sidx, compute(j, sidx, kop) folds it.  The stage
+// index is a constant in each unrolled slot.
+template <int D, typename Issue, typename Compute>
+__device__ __forceinline__ void mma_ring(uint32_t count, Issue issue, Compute compute) {
+  using S = MmaShape<D>;
+  if (count == 0) return;
+  Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
+  issue(0u, 0, k0);
+  if (count > 1) issue(1u, 1, k1);
+  // chunk j's loads landed: at most the chunks issued after it are pending
+  // (loads complete in order)
+  auto wait_for = [&](uint32_t j) {
+    const uint32_t ahead = count - 1 - j;
+    if (ahead >= 2) wait_vm<2 * S::kOps>();
+    else if (ahead == 1) wait_vm<S::kOps>();
+    else wait_vm<0>();
+  };
+#pragma unroll 1
+  for (uint32_t j = 0; j < count; j += 3) {
+    if (j + 2 < count) issue(j + 2, 2, k2);
+    wait_for(j);
+    compute(j, 0, k0);
+    if (j + 1 >= count) break;
+    if (j + 3 < count) issue(j + 3, 0, k0);
+    wait_for(j + 1);
+    compute(j + 1, 1, k1);
+    if (j + 2 >= count) break;
+    if (j + 4 < count) issue(j + 4, 1, k1);
+    wait_for(j + 2);
+    compute(j + 2, 2, k2);
+  }
+}
+
+// The pass's query rows g0 .. g0 + 15 (zero past min(GBM, G - g0)) as QK B
+// operands: lane l holds row g0 + l % 16, columns 32 s + 8 (l / 16) .. +7.
+template <int D, int GBM>
+__device__ __forceinline__ void mma_query(Bf16x8 (&qop)[MmaShape<D>::kSteps],
+                                          const uint16_t* q_head, int g0, int G) {
+  const int lane = threadIdx.x % kWave;
+  const int g = lane & 15;
+  const bool live = g < GBM && g0 + g < G;
+  const uint16_t* row = q_head + (live ? g0 + g : 0) * D + 8 * (lane >> 4);
+#pragma unroll
+  for (int s = 0; s < MmaShape<D>::kSteps; ++s) {
+    const uint4 u = *reinterpret_cast<const uint4*>(row + 32 * s);
+    const uint4 z = live ? u : make_uint4(0u, 0u, 0u, 0u);
+    qop[s] = __builtin_bit_cast(Bf16x8, z);
+  }
+}
+
+// A wave's state into its MmaOut: (m, l) of rows g < GBM (l summed over the
+// four lanes of each row) and O's rows g < GBM.
+template <int D, int GBM>
+__device__ __forceinline__ void mma_publish(const MmaState<D>& st, MmaOut<D, GBM>& out) {
+  const int lane = threadIdx.x % kWave;
+  float a, b;
+  xor16_pair(st.lsum, a, b);
+  float l = a + b;
+  xor32_pair(l, a, b);
+  l = a + b;
+  if (lane < GBM) {
+    out.ml[lane][0] = st.m;
+    out.ml[lane][1] = l;
+  }
+  const int q = lane >> 4, n = lane & 15;
+#pragma unroll
+  for (int b2 = 0; b2 < MmaShape<D>::kBlocks; ++b2)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (4 * q + i < GBM) out.acc[4 * q + i][16 * b2 + n] = st.o[b2][i];
+}
+
 // Lane-group states are combined through LDS in chunks of rows small enough
 // that 16 groups' accumulators fit in 32 KiB.  A lane's D/16 columns sit in
 // a slice padded by 4 floats, so the 16-byte stores of a group's lanes fall
-// on distinct banks.
+// on distinct banks.  (Head dims above kMmaMaxDim.)
 template <int D, int GBM>
-struct CombineShared {
+struct LaneCombine {
   static constexpr int kRows = (512 / D) < GBM ? (512 / D) : GBM;
   static constexpr int kSlice = D / 16 + 4;
   float acc[16][kRows][16 * kSlice];
   float ml[16][kRows][2];
+};
+
+// The matrix-core path's LDS: each wave's staged value chunks, then each
+// wave's state for the combine.
+template <int D, int GBM>
+struct MmaCombine {
+  MmaStage<D> stage[kWaves];
+  MmaOut<D, GBM> mma[kWaves];
 };
 
 // ---------------------------------------------------------------------------
@@ -1207,13 +1475,13 @@ __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a,
 
 template <int D, int GBM, bool kFused>
 __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& dsh,
-                                            CombineShared<D, GBM>& cmb, const StepCtx* sx,
+                                            LaneCombine<D, GBM>& cmb, const StepCtx* sx,
                                             const AttendLoads<D, GBM>& ld, int64_t h,
                                             uint32_t wk) {
   constexpr int CH = D / 16;
   constexpr int R = kRowBatch;
   constexpr int NB = kTile / 16;  // representatives per lane group
-  using Comb = CombineShared<D, GBM>;
+  using Comb = LaneCombine<D, GBM>;
   const DecideArgs& da = a.decide;
   const int G = da.group;
   const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
@@ -1475,14 +1743,294 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
   }
 }
 
+// ---------------------------------------------------------------------------
+// The matrix-core attention of one (tile, head): representatives, suffix
+// and expanded page rows as 16-row chunks on the MFMA engine
+// ---------------------------------------------------------------------------
+// What the matrix-core path loads before the statistics: the decision's
+// inputs, the suffix length and the pass's query rows as QK operands.
+template <int D>
+struct MmaLoads {
+  DecideLoads din;
+  uint32_t S;
+  Bf16x8 qop[MmaShape<D>::kSteps];
+};
+
+template <int D, int GBM, bool kFused>
+__device__ __forceinline__ MmaLoads<D> mma_issue(const AttendArgs& a, int64_t h, uint32_t wk) {
+  const DecideArgs& da = a.decide;
+  const uint32_t tile = wk % (uint32_t)da.n_tiles;
+  MmaLoads<D> ld;
+  ld.din = decide_issue<!kFused>(da, h, tile);
+  // the suffix length does not change during a launch: a scalar load
+  uint32_t S = (uint32_t)a.suffix_cap;
+  if (a.suffix_len_dev) {
+    typedef __attribute__((address_space(4))) const int32_t ConstI32;
+    const int32_t sl = *(ConstI32*)(uintptr_t)a.suffix_len_dev;
+    S = sl < 0 ? 0u : ((uint32_t)sl > S ? S : (uint32_t)sl);
+  }
+  ld.S = S;
+  mma_query<D, GBM>(ld.qop, a.query + (h * da.group) * D, (int)blockIdx.z * GBM, da.group);
+  return ld;
+}
+
+// Wave w's representative chunk (the value means of blocks 16 w .. 16 w + 15
+// of the tile, clamped to the last block) into its stage 0: issued before
+// the decision, so it lands during the wait for the head's LSE partials.
+// Copies (wk >= T) attend no representatives.
+template <int D>
+__device__ __forceinline__ void mma_stage_reps(const AttendArgs& a, int64_t h, uint32_t wk,
+                                               MmaStage<D>& stage) {
+  using S = MmaShape<D>;
+  constexpr uint32_t NC = S::kNC;
+  typedef __attribute__((address_space(3))) void LdsVoid;
+  const uint32_t N = (uint32_t)a.decide.n_blocks, T = (uint32_t)a.decide.n_tiles;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const uint32_t first = (wk % T) * kTile + 16u * wave;
+  if (wk >= T || first >= N) return;
+  const uint32_t lane = threadIdx.x % kWave;
+  const auto vres = buffer_view(a.value_mean + h * (int64_t)N * D, N * (uint32_t)(D * 2));
+#pragma unroll
+  for (int u = 0; u < S::kLdsLoads; ++u) {
+    const uint32_t p = 64u * u + lane, t = p / NC;
+    const uint32_t piece = (p % NC + 32u * NC - 2u * t) % NC;
+    const uint32_t row = first + t < N ? first + t : N - 1;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (LdsVoid*)(stage.bytes[0] + 1024 * u), 16,
+                                             (int)(row * (uint32_t)(D * 2) + piece * 16u), 0,
+                                             0, 0);
+  }
+}
+
+// Decision, then attention of wave-sized chunks on the matrix cores: first
+// each wave's representative chunk (staged before the decision; logits z,
+// expanded and missing blocks at -inf) and its share of the suffix, then
+// the page rows (one-launch step: the head's expanded rows split evenly over
+// its workgroups; three kernels: the tile's own expanded blocks); the four
+// waves' states merge through LDS into the tile's partial, and (one-launch
+// step) the head's last workgroups merge the partials.
+template <int D, int GBM, bool kFused>
+__device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShared& dsh,
+                                                MmaCombine<D, GBM>& cmb, const StepCtx* sx,
+                                                const MmaLoads<D>& ld, int64_t h, uint32_t wk) {
+  using S = MmaShape<D>;
+  const DecideArgs& da = a.decide;
+  const int G = da.group;
+  const uint32_t N = (uint32_t)da.n_blocks, T = (uint32_t)da.n_tiles;
+  const uint32_t L = (uint32_t)da.length, lb = (uint32_t)a.log2_block, B = 1u << lb;
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(tid / kWave);
+  const int g0 = blockIdx.z * GBM, gn = min(GBM, G - g0);  // this pass's query rows
+  const uint32_t W = (uint32_t)a.workers;
+  const uint32_t tile = wk % T;
+  const bool primary = wk < T;
+  const uint32_t n_suffix = ld.S > wk ? (ld.S - wk + W - 1) / W : 0u;
+  constexpr uint32_t kRowBytes = D * 2;
+
+  // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
+  const int32_t* list;
+  uint32_t count = 0;
+  const uint64_t bits = decide_finish<kFused>(da, h, tile, ld.din, dsh, nullptr, list, count,
+                                              kFused ? &sx->stats : nullptr);
+  if constexpr (kFused) {
+    // publish the expanded blocks (a tagged slot) for the head's even split
+    // of pooled token rows
+    if (tid == 0)
+      sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
+                       make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
+  }
+
+  MmaState<D> st;
+  st.m = kNegInf;
+  st.lsum = 0.0f;
+#pragma unroll
+  for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  MmaStage<D>& stage = cmb.stage[wave];
+
+  // ---- representatives and suffix -------------------------------------------
+  const bool has_reps = primary && tile * kTile + 16u * wave < N;
+  const uint32_t ns_chunks = (n_suffix + 15u) / 16u;
+  const uint32_t ns_wave = ns_chunks > wave ? (ns_chunks - 1u - wave) / 4u + 1u : 0u;
+  const uint32_t cap = (uint32_t)a.suffix_cap;
+  const uint32_t kts = (uint32_t)a.ks_ts * 2u, vts = (uint32_t)a.vs_ts * 2u;  // bytes
+  const auto kres_s = buffer_view(a.key_suffix + h * a.ks_hs, cap ? (cap - 1u) * kts + kRowBytes : 0u);
+  const auto vres_s = buffer_view(a.value_suffix + h * a.vs_hs, cap ? (cap - 1u) * vts + kRowBytes : 0u);
+  const uint32_t rep_first = tile * kTile + 16u * wave;  // the wave's representative blocks
+  mma_ring<D>(
+      (has_reps ? 1u : 0u) + ns_wave,
+      [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+        if (has_reps && j == 0) return;  // staged before the decision
+        const uint32_t ci = wave + 4u * (j - (has_reps ? 1u : 0u));
+        // suffix row t of the chunk: token wk + (16 ci + t) W (rows past this
+        // workgroup's slice repeat its last token and are masked)
+        auto token = [&](uint32_t t) {
+          const uint32_t r = 16u * ci + t;
+          return wk + (r < n_suffix ? r : n_suffix - 1u) * W;
+        };
+        mma_issue_rows<D>(kres_s, vres_s, stage.bytes[sidx], kop,
+                          [&](uint32_t t) { return token(t) * kts; },
+                          [&](uint32_t t) { return token(t) * vts; });
+      },
+      [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+        float x[4];
+        const int g = lane & 15;
+        if (has_reps && j == 0) {
+          // logit z of block rep_first + 4 (l / 16) + i for query row g
+          const int gg = g < gn ? g : 0;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t tb = 16u * wave + 4u * (uint32_t)(lane >> 4) + i;  // in the tile
+            const uint32_t b = tile * kTile + tb;
+            const bool live = b < N && !((bits >> tb) & 1ull);
+            float z;
+            if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
+            else z = da.zf[(h * G + g0 + gg) * da.z_stride + (b < N ? b : N - 1)].x;
+            x[i] = live ? z : kNegInf;
+          }
+        } else {
+          const uint32_t ci = wave + 4u * (j - (has_reps ? 1u : 0u));
+          const F32x4 s4 = mma_qk<D>(kop, ld.qop);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t r = 16u * ci + 4u * (uint32_t)(lane >> 4) + i;
+            x[i] = r < n_suffix ? s4[i] * a.scale : kNegInf;
+          }
+        }
+        mma_fold<D>(st, x, stage.bytes[sidx]);
+      });
+
+  // ---- page rows ------------------------------------------------------------
+  const uint16_t* kbase = a.key_pages + h * a.kp_hs;
+  const uint16_t* vbase = a.value_pages + h * a.vp_hs;
+  const uint32_t page_bytes = (N << lb) * kRowBytes;
+  const auto kres = buffer_view(kbase, page_bytes), vres = buffer_view(vbase, page_bytes);
+  const uint32_t last = N - 1, last_count = L - last * B;
+  // rows [r_first, r_first + n_rows): row r is token (16 c) mod B + r mod 16 of
+  // block block_of(c), c = r / 16 (B is a multiple of 16, so a chunk never
+  // crosses a block); chunk c goes to wave (c - c0 + rot) mod 4, the waves
+  // with fewer suffix chunks first
+  auto run_pages = [&](uint32_t r_first, uint32_t n_rows, auto block_of) {
+    if (n_rows == 0) return;
+    const uint32_t r_end = r_first + n_rows;
+    const uint32_t c0 = r_first >> 4, c_end = (r_end + 15u) >> 4;
+    const uint32_t lead = (wave + 4u - ns_chunks % 4u) % 4u;  // this wave's first chunk
+    const uint32_t n = c0 + lead < c_end ? (c_end - c0 - lead - 1u) / 4u + 1u : 0u;
+    mma_ring<D>(
+        n,
+        [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+          const uint32_t c = c0 + lead + 4u * j;
+          const uint32_t row0 = ((uint32_t)block_of(c) << lb) + ((c << 4) & (B - 1u));
+          auto row = [&](uint32_t t) { return (row0 + t) * kRowBytes; };
+          mma_issue_rows<D>(kres, vres, stage.bytes[sidx], kop, row, row);
+        },
+        [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+          const uint32_t c = c0 + lead + 4u * j;
+          const uint32_t bb = (uint32_t)block_of(c);
+          const F32x4 s4 = mma_qk<D>(kop, ld.qop);
+          float x[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const uint32_t r = (c << 4) + 4u * (uint32_t)(lane >> 4) + i;
+            const uint32_t tok = r & (B - 1u);
+            const bool live = r >= r_first && r < r_end && (bb != last || tok < last_count);
+            x[i] = live ? s4[i] * a.scale : kNegInf;
+          }
+          mma_fold<D>(st, x, stage.bytes[sidx]);
+        });
+  };
+  if constexpr (kFused) {
+    // this workgroup's share of the head's expanded rows, once every tile of
+    // the head has published its mask
+    if (tid < kWave) {
+      const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
+      const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
+      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits);
+    }
+    __syncthreads();
+    const int32_t* xl = sx->xl;
+    const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
+    run_pages(x_first, sx->xr[1],
+              [&](uint32_t c) { return (uint32_t)xl[((c << 4) >> lb) - e_first]; });
+  } else {
+    run_pages(0u, (uint32_t)__popcll(bits) * B,
+              [&](uint32_t c) { return tile * kTile + (uint32_t)list[(c << 4) >> lb]; });
+  }
+
+  // ---- the four waves -> one partial per query row, through LDS ------------
+  mma_publish<D, GBM>(st, cmb.mma[wave]);
+  __syncthreads();
+  for (int idx = 2 * tid; idx < gn * D; idx += 2 * kThreads) {
+    const int j = idx / D, d = idx % D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, cmb.mma[w].ml[j][0]);
+    float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = cmb.mma[w].ml[j][0];
+      const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
+      const float2 av = *reinterpret_cast<const float2*>(&cmb.mma[w].acc[j][d]);
+      a0 = __builtin_fmaf(av.x, e, a0);
+      a1 = __builtin_fmaf(av.y, e, a1);
+      l = __builtin_fmaf(cmb.mma[w].ml[j][1], e, l);
+    }
+    const int64_t at = (h * G + g0 + j) * da.tile_stride + wk;
+    if constexpr (kFused) {
+      sx->acc.store2((uint32_t)((at * D + d) * 4), make_float2(a0, a1));
+      if (d == 0) sx->ml.store2((uint32_t)(at * 8), make_float2(M, l));
+    } else {
+      *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
+      if (d == 0) a.part_ml[at] = make_float2(M, l);
+    }
+  }
+  if (a.tile_counts && tid == 0 && blockIdx.z == 0) {
+    // (a copy's count sits past the first T entries, which alone are summed)
+    if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + wk) * 4), count);
+    else a.tile_counts[h * da.tile_stride + wk] = count;
+  }
+  if constexpr (kFused) {
+    // publish and take a ticket; the head's last K workgroups wait for the
+    // rest and merge a column slice each
+    wait_memory();
+    __syncthreads();
+    uint64_t* merged = sx->control + h * kLine + 1;
+    if (tid == 0) {
+      const uint64_t old = __hip_atomic_fetch_add(merged, 1ull, __ATOMIC_RELAXED,
+                                                  __HIP_MEMORY_SCOPE_AGENT);
+      *sx->flag = (uint32_t)(old - *sx->base);
+    }
+    __syncthreads();
+    const uint32_t ticket = *sx->flag;
+    const uint32_t K = W < (uint32_t)kMergers ? W : (uint32_t)kMergers;
+    if (ticket >= W - K) {
+      // (the last ticket's own bump completed the count: every other
+      // workgroup's partial landed before its bump did, so it merges without
+      // a poll)
+      if (tid == 0 && ticket != W - 1)
+        wait_counter<uint64_t>(merged, *sx->base + W + sx->skew, sx->stats.spin, sx->error());
+      __syncthreads();
+      merge_slice<D>(a, *sx, h, (int)(ticket - (W - K)), (int)K);
+    }
+  }
+}
+
 template <int D, int GBM>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void attend_kernel(AttendArgs a) {
   __shared__ alignas(16) DecideShared dsh;
-  __shared__ alignas(16) CombineShared<D, GBM> cmb;
-  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a, blockIdx.y, blockIdx.x);
-  attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld, blockIdx.y, blockIdx.x);
+  if constexpr (D <= kMmaMaxDim) {
+    __shared__ alignas(16) MmaCombine<D, GBM> cmb;
+    const int64_t h = blockIdx.y;
+    const uint32_t wk = blockIdx.x;
+    const MmaLoads<D> ld = mma_issue<D, GBM, false>(a, h, wk);
+    mma_stage_reps<D>(a, h, wk, cmb.stage[__builtin_amdgcn_readfirstlane(threadIdx.x / kWave)]);
+    attend_tile_mma<D, GBM, false>(a, dsh, cmb, nullptr, ld, h, wk);
+  } else {
+    __shared__ alignas(16) LaneCombine<D, GBM> cmb;
+    const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a, blockIdx.y, blockIdx.x);
+    attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld, blockIdx.y, blockIdx.x);
+  }
 }
+
 
 
 // ---------------------------------------------------------------------------
@@ -1522,7 +2070,7 @@ struct StepShared {
       alignas(16) float pdot[GBM * kTile];
       alignas(16) float q[score_q_floats_max(GBM, D)];
     } score;
-    alignas(16) CombineShared<D, GBM> cmb;
+    alignas(16) MmaCombine<D, GBM> cmb;
   } u;
   uint32_t flag;
 };
@@ -1594,7 +2142,7 @@ void step_kernel(StepArgs s) {
     sh.rtag = sh.tag + s.skew;
   }
   // the attention's loads that need no statistics land during them
-  const AttendLoads<D, GBM> ld = attend_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
+  const MmaLoads<D> ld = mma_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
   __syncthreads();
   score_stats(
       sa, tile, sh.u.score.sdot, sh.u.score.pdot,
@@ -1606,7 +2154,11 @@ void step_kernel(StepArgs s) {
         sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
       });
   __syncthreads();
-  attend_tile<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk);
+  // (the score arrays are dead: the representative rows stage over them and
+  // land while the decision waits for the head's LSE partials)
+  mma_stage_reps<D>(s.attend, h, (uint32_t)wk,
+                    sh.u.cmb.stage[__builtin_amdgcn_readfirstlane(tid / kWave)]);
+  attend_tile_mma<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk);
 }
 
 // ---------------------------------------------------------------------------
