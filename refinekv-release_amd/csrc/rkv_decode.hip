@@ -1076,16 +1076,21 @@ __device__ __forceinline__ void mma_fold(MmaState<D>& st, const float (&x)[4], c
 
 // Runs `count` chunks of one wave through three stages, two chunks in
 // flight: issue(j, sidx, kop) issues chunk j (exactly MmaShape<D>::kOps
-// memory operations, or none for a chunk whose loads were issued before the
-// ring started) into stage sidx, compute(j, sidx, kop) folds it.  The stage
-// index is a constant in each unrolled slot.
+// memory operations, or none for a chunk whose loads carry no K operands)
+// into stage sidx, compute(j, sidx, kop) folds it.  Chunk j uses stage j % 3
+// and registers kj % 3; the first `pre` chunks (at most 2) were issued by
+// the caller before the ring.  The stage index is a constant in each
+// unrolled slot.
 template <int D, typename Issue, typename Compute>
-__device__ __forceinline__ void mma_ring(uint32_t count, Issue issue, Compute compute) {
+__device__ __forceinline__ void mma_ring(uint32_t count, uint32_t pre,
+                                         Bf16x8 (&k0)[MmaShape<D>::kSteps],
+                                         Bf16x8 (&k1)[MmaShape<D>::kSteps],
+                                         Bf16x8 (&k2)[MmaShape<D>::kSteps], Issue issue,
+                                         Compute compute) {
   using S = MmaShape<D>;
   if (count == 0) return;
-  Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
-  issue(0u, 0, k0);
-  if (count > 1) issue(1u, 1, k1);
+  if (pre < 1) issue(0u, 0, k0);
+  if (count > 1 && pre < 2) issue(1u, 1, k1);
   // chunk j's loads landed: at most the chunks issued after it are pending
   // (loads complete in order)
   auto wait_for = [&](uint32_t j) {
@@ -1281,15 +1286,28 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
   const uint64_t r0 = (uint64_t)tile * R / W, r1 = ((uint64_t)tile + 1) * R / W;
   const uint32_t e0 = (uint32_t)(r0 >> lb);
   const uint32_t e1 = (uint32_t)((r1 + (1u << lb) - 1) >> lb);
+  // every tile whose ordinals meet [e0, e1), one at a time, its 64 blocks
+  // over the 64 lanes: lane i's block, if expanded, has ordinal first +
+  // (expanded blocks of the tile below i)
 #pragma unroll
   for (int k = 0; k < kChunks; ++k) {
     const uint32_t lo = first[k] > e0 ? first[k] : e0;
     const uint32_t end = first[k] + cnt[k];
     const uint32_t hi = end < e1 ? end : e1;
-    const uint32_t t = k * kWave + lane;
-    for (uint32_t e = lo; e < hi; ++e)
-      sx.xl[e - e0] =
-          (int32_t)(t * kTile + (uint32_t)nth_set_bit(bm[k], (int)(e - first[k])));
+    uint64_t meet = __ballot(lo < hi);
+    while (meet != 0) {
+      const int src = __builtin_ctzll(meet);
+      meet &= meet - 1ull;
+      const uint64_t m = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bm[k], src)) |
+                         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(bm[k] >> 32), src)
+                          << 32);
+      const uint32_t f = (uint32_t)__builtin_amdgcn_readlane((int)first[k], src);
+      if ((m >> lane) & 1ull) {
+        const uint32_t e = f + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
+        if (e >= e0 && e < e1)
+          sx.xl[e - e0] = (int32_t)((uint32_t)(k * kWave + src) * kTile + (uint32_t)lane);
+      }
+    }
   }
   if (lane == 0) {
     sx.xr[0] = (uint32_t)r0;
@@ -1826,6 +1844,39 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   const uint32_t n_suffix = ld.S > wk ? (ld.S - wk + W - 1) / W : 0u;
   constexpr uint32_t kRowBytes = D * 2;
 
+  MmaStage<D>& stage = cmb.stage[wave];
+
+  // ---- representatives and suffix: loads issued before the decision -------
+  // (the representative rows into stage 0; the wave's first suffix chunk
+  // into the next stage and K registers), so that they land while it waits
+  const bool has_reps = primary && tile * kTile + 16u * wave < N;
+  const uint32_t ns_chunks = (n_suffix + 15u) / 16u;
+  const uint32_t ns_wave = ns_chunks > wave ? (ns_chunks - 1u - wave) / 4u + 1u : 0u;
+  const uint32_t cap = (uint32_t)a.suffix_cap;
+  const uint32_t kts = (uint32_t)a.ks_ts * 2u, vts = (uint32_t)a.vs_ts * 2u;  // bytes
+  const auto kres_s = buffer_view(a.key_suffix + h * a.ks_hs, cap ? (cap - 1u) * kts + kRowBytes : 0u);
+  const auto vres_s = buffer_view(a.value_suffix + h * a.vs_hs, cap ? (cap - 1u) * vts + kRowBytes : 0u);
+  const uint32_t n_loop1 = (has_reps ? 1u : 0u) + ns_wave;
+  const uint32_t n_pre = (has_reps ? 1u : 0u) + (ns_wave > 0 ? 1u : 0u);
+  Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
+  auto issue_suffix = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+    const uint32_t ci = wave + 4u * (j - (has_reps ? 1u : 0u));
+    // suffix row t of the chunk: token wk + (16 ci + t) W (rows past this
+    // workgroup's slice repeat its last token and are masked)
+    auto token = [&](uint32_t t) {
+      const uint32_t r = 16u * ci + t;
+      return wk + (r < n_suffix ? r : n_suffix - 1u) * W;
+    };
+    mma_issue_rows<D>(kres_s, vres_s, stage.bytes[sidx], kop,
+                      [&](uint32_t t) { return token(t) * kts; },
+                      [&](uint32_t t) { return token(t) * vts; });
+  };
+  mma_stage_reps<D>(a, h, wk, stage);
+  if (ns_wave > 0) {
+    if (has_reps) issue_suffix(1u, 1, k1);
+    else issue_suffix(0u, 0, k0);
+  }
+
   // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
   const int32_t* list;
   uint32_t count = 0;
@@ -1833,8 +1884,10 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
                                               kFused ? &sx->stats : nullptr);
   if constexpr (kFused) {
     // publish the expanded blocks (a tagged slot) for the head's even split
-    // of pooled token rows
-    if (tid == 0)
+    // of pooled token rows: from the last wave, which next polls the head's
+    // masks (loads complete in order, so the first wait after a store also
+    // waits for its write-through; the other waves go on to their chunks)
+    if (tid == kThreads - kWave)
       sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
                        make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
   }
@@ -1844,31 +1897,11 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   st.lsum = 0.0f;
 #pragma unroll
   for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  MmaStage<D>& stage = cmb.stage[wave];
-
-  // ---- representatives and suffix -------------------------------------------
-  const bool has_reps = primary && tile * kTile + 16u * wave < N;
-  const uint32_t ns_chunks = (n_suffix + 15u) / 16u;
-  const uint32_t ns_wave = ns_chunks > wave ? (ns_chunks - 1u - wave) / 4u + 1u : 0u;
-  const uint32_t cap = (uint32_t)a.suffix_cap;
-  const uint32_t kts = (uint32_t)a.ks_ts * 2u, vts = (uint32_t)a.vs_ts * 2u;  // bytes
-  const auto kres_s = buffer_view(a.key_suffix + h * a.ks_hs, cap ? (cap - 1u) * kts + kRowBytes : 0u);
-  const auto vres_s = buffer_view(a.value_suffix + h * a.vs_hs, cap ? (cap - 1u) * vts + kRowBytes : 0u);
-  const uint32_t rep_first = tile * kTile + 16u * wave;  // the wave's representative blocks
   mma_ring<D>(
-      (has_reps ? 1u : 0u) + ns_wave,
+      n_loop1, n_pre, k0, k1, k2,
       [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-        if (has_reps && j == 0) return;  // staged before the decision
-        const uint32_t ci = wave + 4u * (j - (has_reps ? 1u : 0u));
-        // suffix row t of the chunk: token wk + (16 ci + t) W (rows past this
-        // workgroup's slice repeat its last token and are masked)
-        auto token = [&](uint32_t t) {
-          const uint32_t r = 16u * ci + t;
-          return wk + (r < n_suffix ? r : n_suffix - 1u) * W;
-        };
-        mma_issue_rows<D>(kres_s, vres_s, stage.bytes[sidx], kop,
-                          [&](uint32_t t) { return token(t) * kts; },
-                          [&](uint32_t t) { return token(t) * vts; });
+        if (has_reps && j == 0) return;  // no K operands: staged before the decision
+        issue_suffix(j, sidx, kop);
       },
       [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
         float x[4];
@@ -1915,7 +1948,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
     const uint32_t lead = (wave + 4u - ns_chunks % 4u) % 4u;  // this wave's first chunk
     const uint32_t n = c0 + lead < c_end ? (c_end - c0 - lead - 1u) / 4u + 1u : 0u;
     mma_ring<D>(
-        n,
+        n, 0u, k0, k1, k2,
         [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
           const uint32_t c = c0 + lead + 4u * j;
           const uint32_t row0 = ((uint32_t)block_of(c) << lb) + ((c << 4) & (B - 1u));
@@ -1939,8 +1972,9 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   };
   if constexpr (kFused) {
     // this workgroup's share of the head's expanded rows, once every tile of
-    // the head has published its mask
-    if (tid < kWave) {
+    // the head has published its mask (polled by the last wave, which has
+    // suffix rows only when every wave has)
+    if (wave == kWaves - 1) {
       const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
       const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
       expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits);
@@ -2022,7 +2056,6 @@ void attend_kernel(AttendArgs a) {
     const int64_t h = blockIdx.y;
     const uint32_t wk = blockIdx.x;
     const MmaLoads<D> ld = mma_issue<D, GBM, false>(a, h, wk);
-    mma_stage_reps<D>(a, h, wk, cmb.stage[__builtin_amdgcn_readfirstlane(threadIdx.x / kWave)]);
     attend_tile_mma<D, GBM, false>(a, dsh, cmb, nullptr, ld, h, wk);
   } else {
     __shared__ alignas(16) LaneCombine<D, GBM> cmb;
@@ -2154,10 +2187,9 @@ void step_kernel(StepArgs s) {
         sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
       });
   __syncthreads();
-  // (the score arrays are dead: the representative rows stage over them and
-  // land while the decision waits for the head's LSE partials)
-  mma_stage_reps<D>(s.attend, h, (uint32_t)wk,
-                    sh.u.cmb.stage[__builtin_amdgcn_readfirstlane(tid / kWave)]);
+  // (the score arrays are dead: the representative rows and the first suffix
+  // chunks stage over them and land while the decision waits for the head's
+  // LSE partials)
   attend_tile_mma<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk);
 }
 
