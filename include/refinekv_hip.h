@@ -183,6 +183,32 @@ int rkv_set_profile_events(void* events);
  * kernels.  Per thread. */
 int rkv_set_decode_path(int path);
 
+/*
+ * rkv_decode without a caller workspace (no counterpart in the reference):
+ * for callers that cannot allocate device memory -- code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc.  Arguments
+ * and results are rkv_decode's, minus the workspace: the library keeps one
+ * 64 MiB device array per GPU for the call's intermediates (allocated with
+ * the library, held until the process ends) and allocates nothing.  Shapes
+ * whose rkv_workspace_bytes exceed 64 MiB return RKV_WORKSPACE_TOO_SMALL.
+ * Each call first clears the array's hand-off counters and slots with a fill
+ * kernel on `stream`, so calls of different shapes may follow each other on
+ * one stream; calls that overlap on one GPU (other streams or threads) race
+ * on the shared array and must not be issued.
+ */
+int rkv_decode_static(const void* query, const void* key_mean, const void* ellipsoid,
+                      const void* value_mean, const float* value_norm,
+                      const float* max_value_norm, const void* key_pages,
+                      int64_t key_page_head_stride, const void* value_pages,
+                      int64_t value_page_head_stride, const void* key_suffix,
+                      int64_t key_suffix_head_stride, int64_t key_suffix_token_stride,
+                      const void* value_suffix, int64_t value_suffix_head_stride,
+                      int64_t value_suffix_token_stride, int64_t suffix_capacity,
+                      const int32_t* suffix_length, int64_t heads, int64_t group, int64_t dim,
+                      int64_t n_blocks, int64_t block_size, int64_t prompt_length, float eps,
+                      int reduction, const uint8_t* anchor_mask, uint8_t* mask_out,
+                      void* output, unsigned long long* accessed_blocks, rkv_stream_t stream);
+
 /* Hand-off status of an rkv_decode workspace (no reference counterpart: the
  * reference's Triton kernels have no cross-workgroup waits).  *status
  * receives the workspace's sticky status word: bit 0 is set when a wait of

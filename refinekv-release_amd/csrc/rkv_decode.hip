@@ -2866,3 +2866,113 @@ extern "C" int rkv_workspace_clear_status(void* workspace, size_t workspace_byte
       reinterpret_cast<uint32_t*>(static_cast<char*>(workspace) + L.control + heads * kLine * 8));
   return check_launch("clear_word_kernel");
 }
+
+// ---------------------------------------------------------------------------
+// rkv_decode_static: rkv_decode with the library's own device scratch
+// ---------------------------------------------------------------------------
+extern "C" const char* rkv_last_error(void);
+
+namespace rkv {
+
+// The scratch of rkv_decode_static: one array per GPU the library runs on,
+// held until the process ends.  Host code never uses its name as an address:
+// each device's copy is found with hipGetSymbolAddress.
+constexpr size_t kStaticScratchBytes = size_t(64) << 20;
+static __device__ __align__(256) char scratch[kStaticScratchBytes];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<char*> g_scratch_ptr[kMaxDevices];
+
+// This device's scratch address (looked up once per device, with it current).
+int static_scratch(char** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(kLaunchFailed, "rkv_decode_static: no current device (or index >= %d)",
+                     kMaxDevices);
+  char* ptr = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (ptr == nullptr) {
+    void* addr = nullptr;
+    const hipError_t err = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+    if (err != hipSuccess || addr == nullptr)
+      return set_error(kLaunchFailed, "rkv_decode_static: hipGetSymbolAddress: %s",
+                       hipGetErrorString(err));
+    ptr = static_cast<char*>(addr);
+    g_scratch_ptr[dev].store(ptr, std::memory_order_release);
+  }
+  *out = ptr;
+  return kOk;
+}
+
+// Zero-fills [begin, begin + bytes) (16-byte aligned, a multiple of 16).
+__global__ void zero_fill_kernel(uint4* begin, int64_t n16) {
+  for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n16;
+       i += (int64_t)gridDim.x * blockDim.x)
+    begin[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
+int zero_region(char* base, int64_t off, int64_t bytes, hipStream_t stream) {
+  const int64_t n16 = (bytes + 15) / 16;
+  if (n16 == 0) return kOk;
+  const int64_t blocks = (n16 + 255) / 256 < 1024 ? (n16 + 255) / 256 : 1024;
+  zero_fill_kernel<<<dim3((unsigned)blocks), dim3(256), 0, stream>>>(
+      reinterpret_cast<uint4*>(base + off), n16);
+  return check_launch("zero_fill_kernel");
+}
+
+}  // namespace
+}  // namespace rkv
+
+// No counterpart in the reference: rkv_decode for callers that cannot
+// allocate (HIP graph capture, serving loops, harnesses that forbid it).  The
+// workspace is a file-scope device array of kStaticScratchBytes (64 MiB) per
+// GPU; shapes whose rkv_workspace_bytes exceed it are rejected.  Each call
+// first clears the array's hand-off counters and tagged slots (a fill kernel
+// on `stream`), so calls of any shapes may follow each other; calls that
+// overlap on one GPU (other streams, other threads) race on the array.
+extern "C" int rkv_decode_static(const void* query, const void* key_mean, const void* ellipsoid,
+                                 const void* value_mean, const float* value_norm,
+                                 const float* max_value_norm, const void* key_pages,
+                                 int64_t key_page_head_stride, const void* value_pages,
+                                 int64_t value_page_head_stride, const void* key_suffix,
+                                 int64_t key_suffix_head_stride, int64_t key_suffix_token_stride,
+                                 const void* value_suffix, int64_t value_suffix_head_stride,
+                                 int64_t value_suffix_token_stride, int64_t suffix_capacity,
+                                 const int32_t* suffix_length, int64_t heads, int64_t group,
+                                 int64_t dim, int64_t n_blocks, int64_t block_size,
+                                 int64_t prompt_length, float eps, int reduction,
+                                 const uint8_t* anchor_mask, uint8_t* mask_out, void* output,
+                                 unsigned long long* accessed_blocks, hipStream_t stream) {
+  clear_error();
+  if (heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
+    return set_error(kInvalidArgument, "rkv_decode_static: empty shape");
+  const Layout L = make_layout(heads, group, dim, n_blocks);
+  if ((size_t)L.total > kStaticScratchBytes)
+    return set_error(kWorkspaceTooSmall,
+                     "rkv_decode_static: this shape needs %lld bytes of workspace, more than the "
+                     "static scratch's %lld; use rkv_decode with a caller workspace",
+                     (long long)L.total, (long long)kStaticScratchBytes);
+  char* ws = nullptr;
+  int rc = static_scratch(&ws);
+  if (rc) return rc;
+  // the one-launch step's counters and tagged slots start at zero
+  if ((rc = zero_region(ws, L.control, control_bytes(heads, L.tile_stride), stream)) ||
+      (rc = zero_region(ws, L.lse_slots, heads * group * L.tile_stride * 32, stream)) ||
+      (rc = zero_region(ws, L.xbits, heads * L.tile_stride * 16, stream)))
+    return rc;
+  rc = rkv_decode(query, key_mean, ellipsoid, value_mean, value_norm, max_value_norm, key_pages,
+                  key_page_head_stride, value_pages, value_page_head_stride, key_suffix,
+                  key_suffix_head_stride, key_suffix_token_stride, value_suffix,
+                  value_suffix_head_stride, value_suffix_token_stride, suffix_capacity,
+                  suffix_length, heads, group, dim, n_blocks, block_size, prompt_length, eps,
+                  reduction, anchor_mask, mask_out, output, accessed_blocks, ws,
+                  kStaticScratchBytes, stream);
+  if (rc) {
+    // rkv_decode's message names rkv_decode; say which entry point failed
+    char message[512];
+    snprintf(message, sizeof(message), "%s", rkv_last_error());
+    return set_error(rc, "rkv_decode_static: %s", message);
+  }
+  return kOk;
+}

@@ -81,6 +81,8 @@ def _bind(lib):
     lib.rkv_decode_plan.restype = _int
     lib.rkv_set_handoff_test.argtypes = [_u32, _u32]
     lib.rkv_set_handoff_test.restype = _int
+    lib.rkv_decode_static.argtypes = lib.rkv_decode.argtypes[:-3] + [_p]
+    lib.rkv_decode_static.restype = _int
     return lib
 
 
@@ -371,6 +373,30 @@ def set_handoff_test(spin_limit=0, skew=0):
     """Test hook: the step's poll limit per wait (0 = default) and a skew
     that makes every wait run out (0 = off), for later calls on this thread."""
     _check(lib().rkv_set_handoff_test(spin_limit, skew), "rkv_set_handoff_test")
+
+
+def decode_static(query, summary, key_suffix, value_suffix, config, output, mask,
+                  anchor_mask=None, suffix_length=None, accessed=None):
+    """decode() through rkv_decode_static: the library's own device scratch,
+    no workspace, nothing allocated by the call; output (H, G, 1, D) and mask
+    (H, N) bool are the caller's."""
+    heads, group, _, dim = query.shape
+    q = query.reshape(heads * group, dim)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    kp, vp = summary.keys, summary.values
+    capacity = key_suffix.shape[1]
+    rc = lib().rkv_decode_static(
+        _ptr(q), _ptr(summary.key_mean), _ptr(summary.ellipsoid), _ptr(summary.value_mean),
+        _ptr(summary.value_norm), _ptr(summary.max_value_norm), _ptr(kp), kp.stride(0), _ptr(vp),
+        vp.stride(0), _ptr(key_suffix) if capacity else None, key_suffix.stride(0),
+        key_suffix.stride(1), _ptr(value_suffix) if capacity else None, value_suffix.stride(0),
+        value_suffix.stride(1), capacity, _ptr(suffix_length), heads, group, dim,
+        summary.num_blocks, summary.block_size, summary.prompt_length, float(config.eps),
+        REDUCTION_CODES[config.gqa_reduction], _ptr(anchor_mask), _ptr(mask), _ptr(output),
+        _ptr(accessed), _stream(query.device))
+    _check(rc, "rkv_decode_static")
+    return output, mask
 
 
 def set_decode_path(name):
