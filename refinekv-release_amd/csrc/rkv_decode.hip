@@ -35,6 +35,7 @@
 #include <math.h>
 
 #include <atomic>
+#include <type_traits>
 
 #include "rkv_common.h"
 #include "rkv_internal.h"
@@ -1361,6 +1362,13 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
   const int units = G * nq;
   int S = 1;
   while (S * 2 * units <= kThreads && S < 16) S *= 2;
+  // slice 0 also adds the head's access count: its tile counts (at most
+  // kStepMaxTiles <= kThreads) are loaded ahead of the partials, so they
+  // land with them
+  const bool counting = sx.accessed && m == 0;
+  uint32_t tile_count = 0;
+  if (counting && tid < (int)da.n_tiles)
+    tile_count = sx.counts.load_u32((uint32_t)((h * ts + tid) * 4));
   for (int u0 = 0; u0 < units; u0 += kThreads / S) {
     const int u = u0 + tid / S, sl = tid % S;
     const int uc = u < units ? u : units - 1;
@@ -1368,19 +1376,31 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
     const int64_t row = (h * G + g) * ts;
     float mx = kNegInf, den = 0.0f;
     float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    for (int t0 = sl; t0 < T; t0 += S * kMergeBatch) {
-      float2 ml[kMergeBatch];
-      float4 av[kMergeBatch];
+    // partials t0, t0 + S, ... (nb of them), loaded together; lanes past T
+    // load nothing and fold an empty state
+    auto batch = [&](auto nb, int t0) {
+      constexpr int NB = decltype(nb)::value;
+      float2 ml[NB];
+      float4 av[NB];
 #pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) {
+      for (int k = 0; k < NB; ++k) {
         const int t = t0 + k * S;
-        const int tc = t < T ? t : 0;
-        ml[k] = sx.ml.load2((uint32_t)((row + tc) * 8));
-        av[k] = sx.acc.load4((uint32_t)(((row + tc) * D + 4 * q) * 4));
-        if (t >= T) ml[k].y = 0.0f;
+        ml[k] = make_float2(kNegInf, 0.0f);
+        av[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        if (t < T) {
+          ml[k] = sx.ml.load2((uint32_t)((row + t) * 8));
+          av[k] = sx.acc.load4((uint32_t)(((row + t) * D + 4 * q) * 4));
+        }
       }
 #pragma unroll
-      for (int k = 0; k < kMergeBatch; ++k) merge_state4(ml[k].x, ml[k].y, av[k], mx, num, den);
+      for (int k = 0; k < NB; ++k) merge_state4(ml[k].x, ml[k].y, av[k], mx, num, den);
+    };
+    // (the common case, T <= 4 S: one batch of four)
+    if (T <= 4 * S) {
+      batch(std::integral_constant<int, 4>{}, sl);
+    } else {
+      for (int t0 = sl; t0 < T; t0 += S * kMergeBatch)
+        batch(std::integral_constant<int, kMergeBatch>{}, t0);
     }
     auto fold_from = [&](auto shift) {
       const float m2 = shift(mx), d2 = shift(den);
@@ -1399,10 +1419,8 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
     }
   }
   // the step's access count: this head's tile counts, added once
-  if (sx.accessed && m == 0) {
-    unsigned long long c = 0;
-    for (int t = tid; t < (int)da.n_tiles; t += kThreads)
-      c += sx.counts.load_u32((uint32_t)((h * ts + t) * 4));
+  if (counting) {
+    unsigned long long c = tile_count;
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) c += __shfl_xor(c, o, kWave);
     if (tid % kWave == 0) sx.wsum[tid / kWave] = c;
