@@ -167,6 +167,13 @@ def algorithmic_bytes(a, masks, counts, suffix):
     return dict(phases, step=total, decode=total)
 
 
+def dense_bytes(a, suffix):
+    """Algorithmic bytes of one dense decode: every visible key and value
+    row, the query and the output."""
+    H, G, D = a.heads, a.group, a.dim
+    return H * (a.context + suffix) * D * 2 * 2 + 2 * H * G * D * 2
+
+
 def main():
     a = parse_args()
     if a.gpus != 1:
@@ -299,16 +306,51 @@ def main():
         + ", ".join(f"{k} {v:.2f}" for k, v in kernel_us.items())
         + f"; expanded {frac:.4f}")
 
-    # ---- dense baseline on the same GPU: every block expanded -----------
-    dense_us = None
+    # ---- dense baselines on the same GPU ----------------------------------
+    # (1) the dense decode kernel (rkv_dense_decode: every visible token, no
+    # summary reads; the reference's "Full" is SDPA decode over the cache),
+    # (2) RefineKV's own step at eps 0 (every block expanded).  The speedup
+    # is quoted against the faster of the two.
+    dense_us = eps0_us = None
     if not a.no_dense:
         d_steps = min(a.steps, 20)
-        ms_d, graph = timed_graph(dense_cfg, "dws", 1, d_steps)
-        dense_us = ms_d * 1e3 / (d_steps * a.layers)
+        visible = torch.zeros((), dtype=torch.int32, device=dev)
+
+        def dense_step():
+            visible.add_(1)
+            for L in layers:
+                _hip.dense_decode(L["q"][:, :, 0], L["k"], L["v"], length=visible,
+                                  workspace=L["dws"])
+
+        visible.fill_(a.context)
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            dense_step()
+        torch.cuda.current_stream().wait_stream(s)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            dense_step()
+        visible.fill_(a.context + a.warmup)
+        torch.cuda.synchronize()
+        start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        start.record()
+        for _ in range(d_steps):
+            graph.replay()
+        end.record()
+        torch.cuda.synchronize()
+        dense_us = start.elapsed_time(end) * 1e3 / (d_steps * a.layers)
         del graph
-        log(f"[bench] dense (eps=0) graph: {dense_us:.2f} us/layer-step")
+        log(f"[bench] dense decode kernel graph: {dense_us:.2f} us/layer-step")
         for L in layers:
             L["dws"].clear()
+        ms_d, graph = timed_graph(dense_cfg, "dws", 1, d_steps)
+        eps0_us = ms_d * 1e3 / (d_steps * a.layers)
+        del graph
+        log(f"[bench] refinekv eps=0 graph: {eps0_us:.2f} us/layer-step")
+        for L in layers:
+            L["dws"].clear()
+    dense_best = None if dense_us is None else min(dense_us, eps0_us)
 
     # ---- blocks within 1e-6 relative of eps ------------------------------
     near, blocks = near_eps_blocks(a, layers, suffix_now)
@@ -364,7 +406,10 @@ def main():
         "step_GBps": round(total_bytes / (us_layer * 1e-6) / 1e9, 1),
         "step_frac_of_peak": round(total_bytes / (us_layer * 1e-6) / 1e9 / PEAK_HBM_GBPS, 4),
         "dense_us_per_layer_step": None if dense_us is None else round(dense_us, 3),
-        "speedup_vs_dense": None if dense_us is None else round(dense_us / us_layer, 3),
+        "dense_eps0_us_per_layer_step": None if eps0_us is None else round(eps0_us, 3),
+        "dense_GBps": None if dense_us is None else round(
+            dense_bytes(a, suffix_now) / (dense_us * 1e-6) / 1e9, 1),
+        "speedup_vs_dense": None if dense_best is None else round(dense_best / us_layer, 3),
         "summary_us_per_layer_wall": round(t_sum / a.layers * 1e6, 1),
         "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
     }

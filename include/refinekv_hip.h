@@ -168,6 +168,34 @@ int rkv_decode(const void* query, const void* key_mean, const void* ellipsoid,
                unsigned long long* accessed_blocks, void* workspace, size_t workspace_bytes,
                rkv_stream_t stream);
 
+/*
+ * Dense decode: one query token per row attends every cached token of its
+ * head, with no summary.  Replaces the SDPA call of the reference's dense
+ * decode (src/refinekv/integrations/transformers.py:510-520: layers below
+ * full_attention_layers, and the dense baseline of speed/README.md:73):
+ *   out[h, g] = softmax(query[h, g] . keys[h, t] / sqrt(dim)) @ values[h, t]
+ *   over t = 0 .. L - 1.
+ *   query: (heads, group, dim) bf16, contiguous; out: the same shape.
+ *   keys/values: bf16, token t of head h at base + h * head_stride +
+ *     t * token_stride elements (the (1, heads, capacity, dim) cache of a
+ *     Transformers layer: head_stride capacity*dim, token_stride dim).
+ *   length: L, or, when length_dev is given, the capacity the views cover and
+ *     L = *length_dev (device int32) clamped to [0, length] (graph replays).
+ *   workspace: rkv_dense_plan's bytes (per-split partials).
+ * dim 32..160 step 32, group <= 16.  L = 0 gives zeros.
+ */
+int rkv_dense_decode(const void* query, const void* keys, int64_t key_head_stride,
+                     int64_t key_token_stride, const void* values, int64_t value_head_stride,
+                     int64_t value_token_stride, int64_t heads, int64_t group, int64_t dim,
+                     int64_t length, const int32_t* length_dev, void* output, void* workspace,
+                     size_t workspace_bytes, rkv_stream_t stream);
+
+/* rkv_dense_decode's split of each head's tokens on the current device and
+ * the workspace bytes it needs for `length` tokens (no reference
+ * counterpart: SDPA allocates internally). */
+int rkv_dense_plan(int64_t heads, int64_t group, int64_t dim, int64_t length, int64_t* splits,
+                   size_t* workspace_bytes);
+
 /* Profiling hook with no reference counterpart: when `events` points to 4
  * hipEvent_t handles, later rkv_select / rkv_decode calls on this thread
  * record events[0] before their first kernel and events[k] after their k-th

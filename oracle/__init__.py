@@ -56,6 +56,8 @@ def lib():
                                            ctypes.c_float, ctypes.c_int, ctypes.c_void_p, _u8p,
                                            _f32p]
         L.orc_sparse_attention.restype = ctypes.c_int
+        L.orc_dense_attention.argtypes = [_f32p, _u16p, _u16p, _i64, _i64, _i64, _i64, _f32p]
+        L.orc_dense_attention.restype = ctypes.c_int
         for name in ("orc_expf_n", "orc_logf_n"):
             getattr(L, name).argtypes = [_f32p, _f32p, _i64]
         L.orc_bf16_n.argtypes = [_f32p, _u16p, _i64]
@@ -206,6 +208,19 @@ def sparse_attention(query, summ, key_pages, value_pages, key_suffix, value_suff
     if rc:
         raise ValueError("orc_sparse_attention rejected its inputs")
     return out, mask
+
+
+def dense_attention(query, keys, values):
+    """Dense decode (transformers.py:510-520's SDPA over the cache): returns
+    out (H, G, D) fp32.  query (H, G, D); keys/values (H, L, D) bf16 bits."""
+    q = _f32(query)
+    H, G, D = q.shape
+    k, v = _u16(keys), _u16(values)
+    L = k.shape[1]
+    out = np.empty((H, G, D), np.float32)
+    if lib().orc_dense_attention(q, k, v, H, G, D, L, out):
+        raise ValueError("orc_dense_attention rejected its inputs")
+    return out
 
 
 def access_blocks(mask, counts):

@@ -11,6 +11,8 @@
  *   orc_select_stats    src/refinekv/reference.py:10-34  (selection_statistics)
  *   orc_select          src/refinekv/reference.py:37-47  (select_blocks_reference)
  *   orc_sparse_attention src/refinekv/reference.py:50-73 (sparse_attention_reference)
+ *   orc_dense_attention  src/refinekv/integrations/transformers.py:510-520 (dense
+ *                        decode: SDPA over the visible cache)
  *   orc_expf / orc_logf  elementary functions used by all of the above
  *
  * fp32 evaluation order.  torch leaves the order of fp32 sums open; this
@@ -503,6 +505,44 @@ int orc_sparse_attention(const float *q, const uint16_t *key_mean, const uint16_
     }
   }
   free(z); free(risk); free(logit); free(vrow); free(qt); free(prod); free(acc);
+  return 0;
+}
+
+/* Dense decode (the SDPA call of src/refinekv/integrations/transformers.py:
+ * 510-520, softmax(q k^T * D^-0.5) v over the first L cached tokens): the
+ * exact-token half of orc_sparse_attention with every token visible.
+ * q: (H, G, D) fp32 (rounded to bf16 as the attention's query is);
+ * keys/values: (H, L, D) bf16 bits; out: (H, G, D) fp32. */
+int orc_dense_attention(const float *q, const uint16_t *keys, const uint16_t *values,
+                        int64_t H, int64_t G, int64_t D, int64_t L, float *out) {
+  if (H <= 0 || G <= 0 || D <= 0 || D % 16 || L <= 0) return 1;
+  float scale = (float)pow((double)D, -0.5);
+  float *logit = malloc(sizeof(float) * L);
+  float *qt = malloc(sizeof(float) * D), *prod = malloc(sizeof(float) * D);
+  double *acc = malloc(sizeof(double) * D);
+  for (int64_t h = 0; h < H; ++h) {
+    for (int64_t g = 0; g < G; ++g) {
+      int64_t r = h * G + g;
+      for (int64_t d = 0; d < D; ++d) qt[d] = rbf16(q[r * D + d]);
+      float m = -INFINITY;
+      for (int64_t t = 0; t < L; ++t) {
+        const uint16_t *k = keys + (h * L + t) * D;
+        for (int64_t d = 0; d < D; ++d) prod[d] = bf16f(k[d]);
+        logit[t] = dsum(qt, prod, D) * scale;
+        m = nmax(m, logit[t]);
+      }
+      double den = 0.0;
+      for (int64_t d = 0; d < D; ++d) acc[d] = 0.0;
+      for (int64_t t = 0; t < L; ++t) {
+        double p = exp((double)logit[t] - (double)m);
+        const uint16_t *v = values + (h * L + t) * D;
+        den += p;
+        for (int64_t d = 0; d < D; ++d) acc[d] += p * (double)bf16f(v[d]);
+      }
+      for (int64_t d = 0; d < D; ++d) out[r * D + d] = (float)(acc[d] / den);
+    }
+  }
+  free(logit); free(qt); free(prod); free(acc);
   return 0;
 }
 

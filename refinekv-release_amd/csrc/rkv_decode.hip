@@ -1175,6 +1175,30 @@ struct MmaCombine {
   MmaOut<D, GBM> mma[kWaves];
 };
 
+// The four waves' published states -> one (m, l, acc) per query row j < gn,
+// in a fixed order: put(j, d, (acc[d], acc[d + 1]), m, l) for each column
+// pair d of each row (after a barrier that follows every wave's publish).
+template <int D, int GBM, typename Put>
+__device__ __forceinline__ void mma_combine(const MmaCombine<D, GBM>& cmb, int gn, Put put) {
+  for (int idx = 2 * (int)threadIdx.x; idx < gn * D; idx += 2 * kThreads) {
+    const int j = idx / D, d = idx % D;
+    float M = kNegInf;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, cmb.mma[w].ml[j][0]);
+    float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      const float mw = cmb.mma[w].ml[j][0];
+      const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
+      const float2 av = *reinterpret_cast<const float2*>(&cmb.mma[w].acc[j][d]);
+      a0 = __builtin_fmaf(av.x, e, a0);
+      a1 = __builtin_fmaf(av.y, e, a1);
+      l = __builtin_fmaf(cmb.mma[w].ml[j][1], e, l);
+    }
+    put(j, d, make_float2(a0, a1), M, l);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // One-launch step: hand-off counters and the merge of a head by its last tile
 // ---------------------------------------------------------------------------
@@ -2010,30 +2034,16 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   // ---- the four waves -> one partial per query row, through LDS ------------
   mma_publish<D, GBM>(st, cmb.mma[wave]);
   __syncthreads();
-  for (int idx = 2 * tid; idx < gn * D; idx += 2 * kThreads) {
-    const int j = idx / D, d = idx % D;
-    float M = kNegInf;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, cmb.mma[w].ml[j][0]);
-    float a0 = 0.0f, a1 = 0.0f, l = 0.0f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) {
-      const float mw = cmb.mma[w].ml[j][0];
-      const float e = mw == kNegInf ? 0.0f : __builtin_amdgcn_exp2f((mw - M) * kLog2e);
-      const float2 av = *reinterpret_cast<const float2*>(&cmb.mma[w].acc[j][d]);
-      a0 = __builtin_fmaf(av.x, e, a0);
-      a1 = __builtin_fmaf(av.y, e, a1);
-      l = __builtin_fmaf(cmb.mma[w].ml[j][1], e, l);
-    }
+  mma_combine<D, GBM>(cmb, gn, [&](int j, int d, float2 acc, float M, float l) {
     const int64_t at = (h * G + g0 + j) * da.tile_stride + wk;
     if constexpr (kFused) {
-      sx->acc.store2((uint32_t)((at * D + d) * 4), make_float2(a0, a1));
+      sx->acc.store2((uint32_t)((at * D + d) * 4), acc);
       if (d == 0) sx->ml.store2((uint32_t)(at * 8), make_float2(M, l));
     } else {
-      *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
+      *reinterpret_cast<float2*>(a.part_acc + at * D + d) = acc;
       if (d == 0) a.part_ml[at] = make_float2(M, l);
     }
-  }
+  });
   if (a.tile_counts && tid == 0 && blockIdx.z == 0) {
     // (a copy's count sits past the first T entries, which alone are summed)
     if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + wk) * 4), count);
@@ -2080,6 +2090,96 @@ void attend_kernel(AttendArgs a) {
     const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a, blockIdx.y, blockIdx.x);
     attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld, blockIdx.y, blockIdx.x);
   }
+}
+
+// ---------------------------------------------------------------------------
+// Dense decode: every cached token of every head, no summary (the
+// full-attention decode of dense layers and of the dense baseline,
+// transformers.py:510-520's SDPA call)
+// ---------------------------------------------------------------------------
+struct DenseArgs {
+  const uint16_t* query;           // (H, G, D) bf16
+  const uint16_t* keys;            // token t of head h at keys + h * k_hs + t * k_ts
+  const uint16_t* values;          // likewise with v_hs, v_ts
+  int64_t k_hs, v_hs;              // elements
+  uint32_t k_ts, v_ts;             // elements
+  const int32_t* length_dev;       // tokens, read on the device (null: cap)
+  uint32_t cap;                    // tokens the key/value views address
+  int group, splits;
+  float scale;
+  float2* part_ml;                 // (H G, splits): m, l
+  float* part_acc;                 // (H G, splits, D)
+};
+
+// Workgroup (split sp, head h, row pass z): the split's share of the head's
+// 16-token chunks, C sp / splits .. C (sp + 1) / splits (C = ceil(L / 16)),
+// chunk c0 + w + 4 j to wave w, through the same three-stage matrix-core ring
+// as the decode's page rows; the four waves' states combine into one partial
+// per query row, which merge_kernel folds with the other splits'.
+// (two workgroups per CU up to head_dim 128; at 160 the ring's registers take
+// a whole SIMD per wave, one workgroup per CU, rather than spill)
+template <int D, int GBM>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
+void dense_kernel(DenseArgs a) {
+  using S = MmaShape<D>;
+  constexpr uint32_t kRowBytes = D * 2;
+  __shared__ alignas(16) MmaCombine<D, GBM> cmb;
+  const int64_t h = blockIdx.y;
+  const uint32_t sp = blockIdx.x, splits = (uint32_t)a.splits;
+  const int G = a.group, g0 = blockIdx.z * GBM, gn = min(GBM, G - g0);
+  const int lane = threadIdx.x % kWave;
+  const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  uint32_t L = a.cap;
+  if (a.length_dev) {
+    // the length does not change during a launch: a scalar load
+    typedef __attribute__((address_space(4))) const int32_t ConstI32;
+    const int32_t n = *(ConstI32*)(uintptr_t)a.length_dev;
+    L = n < 0 ? 0u : ((uint32_t)n > a.cap ? a.cap : (uint32_t)n);
+  }
+  const uint32_t C = (L + 15u) / 16u;
+  const uint32_t c0 = (uint32_t)((uint64_t)C * sp / splits);
+  const uint32_t c1 = (uint32_t)((uint64_t)C * (sp + 1u) / splits);
+  const uint32_t n = c0 + wave < c1 ? (c1 - c0 - wave - 1u) / 4u + 1u : 0u;
+  const uint32_t kts = a.k_ts * 2u, vts = a.v_ts * 2u;  // bytes
+  const auto kres = buffer_view(a.keys + h * a.k_hs, a.cap ? (a.cap - 1u) * kts + kRowBytes : 0u);
+  const auto vres = buffer_view(a.values + h * a.v_hs, a.cap ? (a.cap - 1u) * vts + kRowBytes : 0u);
+  Bf16x8 qop[S::kSteps];
+  mma_query<D, GBM>(qop, a.query + h * (int64_t)G * D, g0, G);
+  MmaStage<D>& stage = cmb.stage[wave];
+  MmaState<D> st;
+  st.m = kNegInf;
+  st.lsum = 0.0f;
+#pragma unroll
+  for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
+  mma_ring<D>(
+      n, 0u, k0, k1, k2,
+      [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+        const uint32_t c = c0 + wave + 4u * j;
+        // rows past the last token repeat it and are masked
+        auto token = [&](uint32_t t) { return 16u * c + t < L ? 16u * c + t : L - 1u; };
+        mma_issue_rows<D>(kres, vres, stage.bytes[sidx], kop,
+                          [&](uint32_t t) { return token(t) * kts; },
+                          [&](uint32_t t) { return token(t) * vts; });
+      },
+      [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+        const uint32_t c = c0 + wave + 4u * j;
+        const F32x4 s4 = mma_qk<D>(kop, qop);
+        float x[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t r = 16u * c + 4u * (uint32_t)(lane >> 4) + i;
+          x[i] = r < L ? s4[i] * a.scale : kNegInf;
+        }
+        mma_fold<D>(st, x, stage.bytes[sidx]);
+      });
+  mma_publish<D, GBM>(st, cmb.mma[wave]);
+  __syncthreads();
+  mma_combine<D, GBM>(cmb, gn, [&](int j, int d, float2 acc, float M, float l) {
+    const int64_t at = (h * G + g0 + j) * (int64_t)splits + sp;
+    *reinterpret_cast<float2*>(a.part_acc + at * D + d) = acc;
+    if (d == 0) a.part_ml[at] = make_float2(M, l);
+  });
 }
 
 
@@ -2666,6 +2766,158 @@ int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b
   return rc;
 }
 
+// ---- dense decode -----------------------------------------------------------
+// Workgroups of dense_kernel<D, GBM> the current device holds at once, 0 if
+// unknown.
+template <int D, int GBM>
+int64_t dense_resident() {
+  static std::atomic<int> of_dev[64];  // per device; 0 = not asked yet
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  int n = of_dev[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
+    int cus = 0, per_cu = 0;
+    if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, dense_kernel<D, GBM>, kThreads,
+                                                     0) != hipSuccess)
+      return 0;
+    n = cus * per_cu;
+    of_dev[dev].store(n, std::memory_order_relaxed);
+  }
+  return n;
+}
+
+constexpr int64_t kDenseMaxSplits = 1024;
+
+// Query rows per workgroup (the matrix core's 16 columns hold up to 16) and
+// the split of each head's tokens: enough workgroups to fill the device
+// once, each wave with at least one 16-token chunk of the longest length.
+struct DensePlan {
+  int64_t rows = 0, passes = 0, splits = 0;
+  size_t ml_off = 0, acc_off = 0, total = 0;
+};
+
+inline int64_t dense_rows(int64_t group) { return group <= 4 ? 4 : (group <= 8 ? 8 : 16); }
+
+DensePlan dense_plan(int64_t heads, int64_t group, int64_t dim, int64_t cap) {
+  DensePlan P;
+  P.rows = dense_rows(group);
+  P.passes = (group + P.rows - 1) / P.rows;
+  int64_t resident = 0;
+  RKV_DISPATCH_DIM(dim, D, {
+    if constexpr (D <= kMmaMaxDim) {
+      if (P.rows == 4) resident = dense_resident<D, 4>();
+      else if (P.rows == 8) resident = dense_resident<D, 8>();
+      else resident = dense_resident<D, 16>();
+    }
+  });
+  if (resident <= 0) resident = 512;
+  const int64_t chunks = (cap + 15) / 16;
+  int64_t splits = resident / (heads * P.passes);
+  const int64_t most = chunks / kWaves > 1 ? chunks / kWaves : 1;
+  splits = splits < most ? splits : most;
+  splits = splits < kDenseMaxSplits ? splits : kDenseMaxSplits;
+  P.splits = splits > 1 ? splits : 1;
+  auto up = [](size_t x) { return (x + 255) & ~(size_t)255; };
+  const size_t parts = (size_t)(heads * group * P.splits);
+  P.ml_off = 0;
+  P.acc_off = up(parts * 8);
+  P.total = P.acc_off + up(parts * (size_t)dim * 4);
+  return P;
+}
+
+struct DenseParams {
+  const void* query;
+  const void* keys;
+  const void* values;
+  int64_t k_hs, k_ts, v_hs, v_ts;
+  int64_t heads, group, dim, length;
+  const int32_t* length_dev;
+  void* workspace;
+  size_t workspace_bytes;
+  void* out;
+  hipStream_t stream;
+};
+
+template <int D>
+int launch_dense_d(const DenseArgs& da, int64_t rows, dim3 grid, hipStream_t stream) {
+  if constexpr (D <= kMmaMaxDim) {
+    if (rows == 4) dense_kernel<D, 4><<<grid, dim3(kThreads), 0, stream>>>(da);
+    else if (rows == 8) dense_kernel<D, 8><<<grid, dim3(kThreads), 0, stream>>>(da);
+    else dense_kernel<D, 16><<<grid, dim3(kThreads), 0, stream>>>(da);
+    return check_launch("dense_kernel");
+  }
+  return set_error(kUnsupported, "rkv_dense_decode: head_dim %d above %d", D, kMmaMaxDim);
+}
+
+int validate_dense(const DenseParams& p, DensePlan& P) {
+  const char* who = "rkv_dense_decode";
+  if (!p.query || !p.keys || !p.values || !p.out)
+    return set_error(kInvalidArgument, "%s: null pointer argument", who);
+  if (p.heads <= 0 || p.group <= 0 || p.length <= 0 || p.heads > 65535)
+    return set_error(kInvalidArgument, "%s: empty or oversized shape", who);
+  if (p.group > 16) return set_error(kUnsupported, "%s: GQA group %lld exceeds 16", who,
+                                     (long long)p.group);
+  if (p.dim < 32 || p.dim > kMmaMaxDim || p.dim % 32)
+    return set_error(kUnsupported, "%s: head_dim %lld not in 32..%d step 32", who,
+                     (long long)p.dim, kMmaMaxDim);
+  if (p.k_ts < p.dim || p.v_ts < p.dim || p.k_hs < 0 || p.v_hs < 0 || p.k_ts % 8 ||
+      p.v_ts % 8 || p.k_hs % 8 || p.v_hs % 8)
+    return set_error(kInvalidArgument,
+                     "%s: token strides must be >= head_dim and strides multiples of 8", who);
+  if (!aligned(p.query, 16) || !aligned(p.keys, 16) || !aligned(p.values, 16) ||
+      !aligned(p.out, 16))
+    return set_error(kInvalidArgument, "%s: query, keys, values and out must be 16-byte aligned",
+                     who);
+  // a head's keys (values) are addressed with 32-bit byte offsets
+  const int64_t lim = (int64_t(1) << 32) - 1;
+  if ((p.length - 1) * p.k_ts * 2 + p.dim * 2 > lim || (p.length - 1) * p.v_ts * 2 + p.dim * 2 > lim)
+    return set_error(kUnsupported, "%s: a head's keys or values span more than 4 GiB", who);
+  P = dense_plan(p.heads, p.group, p.dim, p.length);
+  if (!p.workspace || p.workspace_bytes < P.total)
+    return set_error(kWorkspaceTooSmall, "%s: workspace of %zu bytes, %zu needed", who,
+                     p.workspace_bytes, P.total);
+  if (!aligned(p.workspace, 16))
+    return set_error(kInvalidArgument, "%s: workspace must be 16-byte aligned", who);
+  return kOk;
+}
+
+int launch_dense(const DenseParams& p, const DensePlan& P) {
+  char* ws = static_cast<char*>(p.workspace);
+  DenseArgs da;
+  da.query = static_cast<const uint16_t*>(p.query);
+  da.keys = static_cast<const uint16_t*>(p.keys);
+  da.values = static_cast<const uint16_t*>(p.values);
+  da.k_hs = p.k_hs;
+  da.v_hs = p.v_hs;
+  da.k_ts = (uint32_t)p.k_ts;
+  da.v_ts = (uint32_t)p.v_ts;
+  da.length_dev = p.length_dev;
+  da.cap = (uint32_t)p.length;
+  da.group = (int)p.group;
+  da.splits = (int)P.splits;
+  da.scale = (float)pow((double)p.dim, -0.5);
+  da.part_ml = reinterpret_cast<float2*>(ws + P.ml_off);
+  da.part_acc = reinterpret_cast<float*>(ws + P.acc_off);
+  const dim3 grid((unsigned)P.splits, (unsigned)p.heads, (unsigned)P.passes);
+  int rc = kUnsupported;
+  RKV_DISPATCH_DIM(p.dim, D, rc = launch_dense_d<D>(da, P.rows, grid, p.stream));
+  if (rc) return rc;
+  MergeArgs ma;
+  ma.part_ml = da.part_ml;
+  ma.part_acc = da.part_acc;
+  ma.out = static_cast<uint16_t*>(p.out);
+  ma.tile_counts = nullptr;
+  ma.accessed = nullptr;
+  ma.tile_stride = P.splits;
+  ma.parts = (int)P.splits;
+  ma.dim = (int)p.dim;
+  ma.heads = (int)p.heads;
+  merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
+                 dim3(kThreads), 0, p.stream>>>(ma);
+  return check_launch("merge_kernel");
+}
+
 }  // namespace
 }  // namespace rkv
 
@@ -2993,4 +3245,38 @@ extern "C" int rkv_decode_static(const void* query, const void* key_mean, const 
     return set_error(rc, "rkv_decode_static: %s", message);
   }
   return kOk;
+}
+
+// Dense decode of one token per query row over every cached token (no
+// summary): out[h, g] = softmax(q[h, g] K_h^T / sqrt(D)) V_h over tokens
+// 0 .. L - 1, L = *length_dev clamped to [0, length] when length_dev is
+// given (graph replays), else length.
+extern "C" int rkv_dense_plan(int64_t heads, int64_t group, int64_t dim, int64_t length,
+                              int64_t* splits, size_t* workspace_bytes) {
+  clear_error();
+  if (heads <= 0 || group <= 0 || length <= 0 || dim <= 0)
+    return set_error(kInvalidArgument, "rkv_dense_plan: empty shape");
+  if (group > 16 || dim < 32 || dim > kMmaMaxDim || dim % 32)
+    return set_error(kUnsupported, "rkv_dense_plan: group %lld / head_dim %lld not supported",
+                     (long long)group, (long long)dim);
+  const DensePlan P = dense_plan(heads, group, dim, length);
+  if (splits) *splits = P.splits;
+  if (workspace_bytes) *workspace_bytes = P.total;
+  return kOk;
+}
+
+extern "C" int rkv_dense_decode(const void* query, const void* keys, int64_t key_head_stride,
+                                int64_t key_token_stride, const void* values,
+                                int64_t value_head_stride, int64_t value_token_stride,
+                                int64_t heads, int64_t group, int64_t dim, int64_t length,
+                                const int32_t* length_dev, void* output, void* workspace,
+                                size_t workspace_bytes, hipStream_t stream) {
+  clear_error();
+  const DenseParams p{query, keys, values, key_head_stride, key_token_stride,
+                      value_head_stride, value_token_stride, heads, group, dim, length,
+                      length_dev, workspace, workspace_bytes, output, stream};
+  DensePlan P;
+  const int rc = validate_dense(p, P);
+  if (rc) return rc;
+  return launch_dense(p, P);
 }

@@ -83,6 +83,11 @@ def _bind(lib):
     lib.rkv_set_handoff_test.restype = _int
     lib.rkv_decode_static.argtypes = lib.rkv_decode.argtypes[:-3] + [_p]
     lib.rkv_decode_static.restype = _int
+    lib.rkv_dense_decode.argtypes = [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64,
+                                     _p, _p, _p, _size, _p]
+    lib.rkv_dense_decode.restype = _int
+    lib.rkv_dense_plan.argtypes = [_i64, _i64, _i64, _i64, _p, _p]
+    lib.rkv_dense_plan.restype = _int
     return lib
 
 
@@ -397,6 +402,61 @@ def decode_static(query, summary, key_suffix, value_suffix, config, output, mask
         _ptr(accessed), _stream(query.device))
     _check(rc, "rkv_decode_static")
     return output, mask
+
+
+# ---------------------------------------------------------------------------
+# Dense decode
+# ---------------------------------------------------------------------------
+
+DENSE_MAX_DIM = 160
+
+
+def dense_plan(heads, group, dim, length):
+    """(splits, workspace bytes) of rkv_dense_decode for this shape on the
+    current device."""
+    splits, nbytes = ctypes.c_int64(), ctypes.c_size_t()
+    _check(lib().rkv_dense_plan(heads, group, dim, length, ctypes.byref(splits),
+                                ctypes.byref(nbytes)), "rkv_dense_plan")
+    return int(splits.value), int(nbytes.value)
+
+
+def dense_decode(query, keys, values, length=None, workspace=None, output=None):
+    """Full attention of one query token per row over every cached token.
+
+    query (H, G, D) or (H, G, 1, D) bf16; keys/values (H, T, D) bf16 views
+    (head_dim dense, e.g. ``cache[0]`` of a (1, H, T, D) Transformers cache).
+    ``length``: None attends all T tokens; an int attends the first `length`;
+    a device int32 scalar attends the first min(max(length, 0), T) tokens as
+    read when the kernel runs (graph replays).  Returns (H, G, D) bf16 (the
+    ``output`` tensor when given), computed by rkv_dense_decode and
+    merge of its per-split partials; the partials live in ``workspace``.
+    """
+    heads, group, dim = query.shape[0], query.shape[1], query.shape[-1]
+    device = query.device
+    if not query.dtype == keys.dtype == values.dtype == torch.bfloat16:
+        raise TypeError("rkv_dense_decode: query, keys and values must be bfloat16")
+    q = query.reshape(heads, group, dim)
+    if not q.is_contiguous():
+        q = q.contiguous()
+    capacity = keys.shape[1]
+    length_dev = None
+    if isinstance(length, torch.Tensor):
+        length_dev, cap = length, capacity
+    else:
+        cap = capacity if length is None else int(length)
+        if not 0 < cap <= capacity:
+            raise ValueError(f"length {length} outside 1..{capacity}")
+    keys, values = _row_aligned(keys, 16), _row_aligned(values, 16)
+    _, nbytes = dense_plan(heads, group, dim, cap)
+    scratch = _buffer(workspace, "hip_dense_scratch", (nbytes,), device, torch.uint8)
+    if output is None:
+        output = torch.empty(heads, group, dim, device=device, dtype=query.dtype)
+    rc = lib().rkv_dense_decode(
+        _ptr(q), _ptr(keys), keys.stride(0), keys.stride(1), _ptr(values), values.stride(0),
+        values.stride(1), heads, group, dim, cap, _ptr(length_dev), _ptr(output), _ptr(scratch),
+        scratch.numel(), _stream(device))
+    _check(rc, "rkv_dense_decode")
+    return output
 
 
 def set_decode_path(name):
