@@ -20,3 +20,21 @@ def oracle_lib():
     if not os.path.exists(oracle.LIB_PATH):
         oracle.build()
     return oracle
+
+
+def pytest_terminal_summary(terminalreporter):
+    """Near-eps exceptions of the golden mask comparisons: blocks whose
+    reduced risk lies within 1e-6 relative of eps (where a reordered fp32 sum
+    may decide either way) and how many of them differed."""
+    near = diff = cases = 0
+    for report in terminalreporter.stats.get("passed", []) + terminalreporter.stats.get(
+            "failed", []):
+        props = dict(getattr(report, "user_properties", []))
+        if "near_eps_blocks" in props and report.when == "call":
+            cases += 1
+            near += props["near_eps_blocks"]
+            diff += props.get("near_eps_mask_differences", 0)
+    if cases:
+        terminalreporter.write_line(
+            f"near-eps blocks over {cases} golden mask cases: {near} within 1e-6 relative of "
+            f"eps; {diff} mask entries differ from the golden masks (only near-eps entries may)")

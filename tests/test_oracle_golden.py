@@ -80,7 +80,7 @@ def _near_eps(risk, reduction, eps, rel=1e-6):
     return (np.abs(risk - eps) <= rel * eps).any(1)
 
 
-def test_masks_and_counters_exact(case, oracle_lib):
+def test_masks_and_counters_exact(case, oracle_lib, record_property):
     g, meta, inp = case
     cfg = meta["config"]
     block, eps, red = cfg["block_size"], cfg["eps"], cfg["gqa_reduction"]
@@ -88,7 +88,10 @@ def test_masks_and_counters_exact(case, oracle_lib):
     q = inp["query"][:, :, 0].float().numpy()
     mask, z, risk = oracle_lib.select(q, summ, eps, red)
     near = _near_eps(g["risk"], red, eps)
-    # The north-star exception: only blocks within 1e-6 relative of eps may differ.
+    # The north-star exception: only blocks within 1e-6 relative of eps may
+    # differ; how many there are, and how many did, is reported.
+    record_property("near_eps_blocks", int(near.sum()))
+    record_property("near_eps_mask_differences", int((mask != g["mask"]).sum()))
     assert ((mask != g["mask"]) & ~near).sum() == 0
     anchor = g.get("anchor")
     kp = gc.padded_pages(inp["keys"], block)
