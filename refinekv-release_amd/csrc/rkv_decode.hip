@@ -28,6 +28,11 @@
 //   merge  (row, cols)  the row's tile partials -> bf16 output columns, and
 //                       the access counter.
 //
+// Token rows (representatives, expanded blocks, suffix) are attended on the
+// matrix cores for head_dim <= 160 (QK^T and PV MFMAs, value rows staged in
+// LDS), on the vector ALUs above.  The dense decode (dense_kernel + merge)
+// attends every cached token with the same matrix-core engine.
+//
 // Selection statistics (z, delta, log Z, log C, risk) follow fixed fp32
 // orders shared with the CPU oracle (oracle/rkv_oracle.c), so masks are
 // reproducible bit for bit; the attention's orders are fixed too, so outputs
