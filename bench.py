@@ -434,7 +434,6 @@ def sweep(a):
     # the three kernels past 256 tiles per head or a grid larger than the
     # device holds at once (two step workgroups per CU)
     _hip.set_decode_path("step")
-    cus = torch.cuda.get_device_properties(dev).multi_processor_count
     warmup, steps = 2, 10
     capacity = warmup + steps + 1
     contexts = [int(x) for x in a.sweep_contexts.split(",")]
@@ -496,13 +495,9 @@ def sweep(a):
                     nbytes = algorithmic_bytes(pa, masks, layers[0]["summary"].counts,
                                                int(suffix_len.item()))["decode"]
                     gbps = nbytes / (us * 1e-6) / 1e9
-                    tiles = -(-n // 64)
-                    workers = max(tiles, min(512 // a.heads, 256))
-                    grid, resident = a.heads * workers, 2 * cus
-                    fits = tiles <= 256 and (grid <= resident or (
-                        block >= 64 and workers <= resident and grid <= 2 * resident))
                     point = dict(context=context, block=block, eps=eps, spikes=spikes,
-                                 layers=n_layers, path="step" if fits else "split",
+                                 layers=n_layers,
+                                 path=_hip.decode_plan(a.heads, a.group, a.dim, n, block),
                                  us_per_layer_step=round(us, 2), expanded_fraction=round(f, 5),
                                  algorithmic_bytes=int(nbytes), GBps=round(gbps, 1),
                                  frac_of_peak=round(gbps / PEAK_HBM_GBPS, 4))

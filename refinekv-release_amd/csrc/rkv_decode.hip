@@ -1209,7 +1209,9 @@ __device__ __forceinline__ void mma_combine(const MmaCombine<D, GBM>& cmb, int g
 // ---------------------------------------------------------------------------
 // Hand-offs between the tiles of a head.  Counters (u64 at the start of
 // the workspace): head h owns the 64-byte line at counter kLine * h, whose
-// [1] counts tiles that have published their attention partials; after the
+// [1] counts tiles that have published their attention partials and whose
+// [2] holds e + 2 when launch e expanded every block of the head (read by
+// launch e + 1, whose workgroups then speculate); after the
 // heads' lines, a line holding a sticky u32 error word (bit 0: a wait gave up
 // after its poll limit) and, at [1], the launches' workgroup ticket count;
 // then one launch counter per workgroup.  Nothing is reset: each launch adds
@@ -1247,6 +1249,7 @@ struct StepCtx {
   uint32_t* xr;                   // LDS: the share's first row and row count
   int heads;
   uint32_t skew;                  // 0; a test's nonzero value makes every wait run out
+  const uint32_t* spec;           // LDS: nonzero when the launch speculates (or null)
   __device__ uint32_t* error() const {
     return reinterpret_cast<uint32_t*>(control + (int64_t)heads * kLine);
   }
@@ -1272,7 +1275,8 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
 // (first row, row count).  Integer arithmetic only: every tile sees the same
 // split.
 __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
-                               uint32_t W, uint32_t tile, int lb, uint64_t last_bits) {
+                               uint32_t W, uint32_t tile, int lb, uint64_t last_bits,
+                               uint32_t N) {
   const int lane = threadIdx.x % kWave;
   const uint32_t tag = *sx.stats.rtag;
   uint64_t bm[kChunks];
@@ -1342,6 +1346,7 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
   if (lane == 0) {
     sx.xr[0] = (uint32_t)r0;
     sx.xr[1] = (uint32_t)(r1 - r0);
+    sx.xr[2] = total == N ? 1u : 0u;  // every block of the head expanded
   }
 }
 
@@ -1723,7 +1728,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     if (tid < kWave) {
       const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
       const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
-      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits);
+      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits, N);
     }
     __syncthreads();
     const int32_t* xl = sx->xl;
@@ -1903,11 +1908,22 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   const uint32_t kts = (uint32_t)a.ks_ts * 2u, vts = (uint32_t)a.vs_ts * 2u;  // bytes
   const auto kres_s = buffer_view(a.key_suffix + h * a.ks_hs, cap ? (cap - 1u) * kts + kRowBytes : 0u);
   const auto vres_s = buffer_view(a.value_suffix + h * a.vs_hs, cap ? (cap - 1u) * vts + kRowBytes : 0u);
-  const uint32_t n_loop1 = (has_reps ? 1u : 0u) + ns_wave;
-  const uint32_t n_pre = (has_reps ? 1u : 0u) + (ns_wave > 0 ? 1u : 0u);
+  // Speculation (one-launch step): when the previous launch on this
+  // workspace expanded every block of the head, the workgroup attends its
+  // suffix chunks and its share of all the head's rows before the decision,
+  // without the representative chunk (with every block expanded that chunk's
+  // logits are all -inf, and its fold leaves the initial state unchanged),
+  // so the result equals the normal order's bit for bit whenever every block
+  // expands again; otherwise the state is dropped and the normal order runs
+  // after the decision.
+  const bool spec = kFused && sx->spec != nullptr && *sx->spec != 0u;
+  bool reps_on = has_reps && !spec;
   Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
+  // loop1's chunk 0 is the representative chunk (a no-op without
+  // representatives: nothing issued, nothing folded), chunk j >= 1 the
+  // wave's suffix chunk j - 1, so every chunk keeps its stage and K registers
   auto issue_suffix = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-    const uint32_t ci = wave + 4u * (j - (has_reps ? 1u : 0u));
+    const uint32_t ci = wave + 4u * (j - 1u);
     // suffix row t of the chunk: token wk + (16 ci + t) W (rows past this
     // workgroup's slice repeat its last token and are masked)
     auto token = [&](uint32_t t) {
@@ -1918,65 +1934,56 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
                       [&](uint32_t t) { return token(t) * kts; },
                       [&](uint32_t t) { return token(t) * vts; });
   };
-  mma_stage_reps<D>(a, h, wk, stage);
-  if (ns_wave > 0) {
-    if (has_reps) issue_suffix(1u, 1, k1);
-    else issue_suffix(0u, 0, k0);
-  }
-
-  // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
-  const int32_t* list;
-  uint32_t count = 0;
-  const uint64_t bits = decide_finish<kFused>(da, h, tile, ld.din, dsh, nullptr, list, count,
-                                              kFused ? &sx->stats : nullptr);
-  if constexpr (kFused) {
-    // publish the expanded blocks (a tagged slot) for the head's even split
-    // of pooled token rows: from the last wave, which next polls the head's
-    // masks (loads complete in order, so the first wait after a store also
-    // waits for its write-through; the other waves go on to their chunks)
-    if (tid == kThreads - kWave)
-      sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
-                       make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
-  }
+  auto pre_issue = [&]() {
+    if (reps_on) mma_stage_reps<D>(a, h, wk, stage);
+    if (ns_wave > 0) issue_suffix(1u, 1, k1);
+  };
 
   MmaState<D> st;
-  st.m = kNegInf;
-  st.lsum = 0.0f;
+  auto init_state = [&]() {
+    st.m = kNegInf;
+    st.lsum = 0.0f;
 #pragma unroll
-  for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  mma_ring<D>(
-      n_loop1, n_pre, k0, k1, k2,
-      [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-        if (has_reps && j == 0) return;  // no K operands: staged before the decision
-        issue_suffix(j, sidx, kop);
-      },
-      [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
-        float x[4];
-        const int g = lane & 15;
-        if (has_reps && j == 0) {
-          // logit z of block rep_first + 4 (l / 16) + i for query row g
-          const int gg = g < gn ? g : 0;
+    for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  };
+  uint64_t bits = 0;
+  // the representative chunk (if reps_on, first) and the wave's suffix chunks
+  auto loop1 = [&]() {
+    mma_ring<D>(
+        1u + ns_wave, ns_wave > 0 ? 2u : 1u, k0, k1, k2,
+        [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+          if (j == 0) return;  // no K operands: staged before the decision
+          issue_suffix(j, sidx, kop);
+        },
+        [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+          if (j == 0 && !reps_on) return;
+          float x[4];
+          const int g = lane & 15;
+          if (j == 0) {
+            // logit z of block rep_first + 4 (l / 16) + i for query row g
+            const int gg = g < gn ? g : 0;
 #pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t tb = 16u * wave + 4u * (uint32_t)(lane >> 4) + i;  // in the tile
-            const uint32_t b = tile * kTile + tb;
-            const bool live = b < N && !((bits >> tb) & 1ull);
-            float z;
-            if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
-            else z = da.zf[(h * G + g0 + gg) * da.z_stride + (b < N ? b : N - 1)].x;
-            x[i] = live ? z : kNegInf;
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t tb = 16u * wave + 4u * (uint32_t)(lane >> 4) + i;  // in the tile
+              const uint32_t b = tile * kTile + tb;
+              const bool live = b < N && !((bits >> tb) & 1ull);
+              float z;
+              if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
+              else z = da.zf[(h * G + g0 + gg) * da.z_stride + (b < N ? b : N - 1)].x;
+              x[i] = live ? z : kNegInf;
+            }
+          } else {
+            const uint32_t ci = wave + 4u * (j - 1u);
+            const F32x4 s4 = mma_qk<D>(kop, ld.qop);
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              const uint32_t r = 16u * ci + 4u * (uint32_t)(lane >> 4) + i;
+              x[i] = r < n_suffix ? s4[i] * a.scale : kNegInf;
+            }
           }
-        } else {
-          const uint32_t ci = wave + 4u * (j - (has_reps ? 1u : 0u));
-          const F32x4 s4 = mma_qk<D>(kop, ld.qop);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t r = 16u * ci + 4u * (uint32_t)(lane >> 4) + i;
-            x[i] = r < n_suffix ? s4[i] * a.scale : kNegInf;
-          }
-        }
-        mma_fold<D>(st, x, stage.bytes[sidx]);
-      });
+          mma_fold<D>(st, x, stage.bytes[sidx]);
+        });
+  };
 
   // ---- page rows ------------------------------------------------------------
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
@@ -2017,20 +2024,67 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
           mma_fold<D>(st, x, stage.bytes[sidx]);
         });
   };
+
+  pre_issue();
+  if (spec) {
+    // every block of the head assumed expanded: this workgroup's share of
+    // the head's N B rows, in block order (what the mask hand-off gives
+    // when every mask is full)
+    init_state();
+    loop1();
+    const uint64_t R = (uint64_t)N << lb;
+    const uint32_t r0 = (uint32_t)((uint64_t)wk * R / W);
+    const uint32_t r1 = (uint32_t)(((uint64_t)wk + 1u) * R / W);
+    run_pages(r0, r1 - r0, [&](uint32_t c) { return (c << 4) >> lb; });
+  }
+
+  // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
+  const int32_t* list;
+  uint32_t count = 0;
+  bits = decide_finish<kFused>(da, h, tile, ld.din, dsh, nullptr, list, count,
+                               kFused ? &sx->stats : nullptr);
+  if constexpr (kFused) {
+    // publish the expanded blocks (a tagged slot) for the head's even split
+    // of pooled token rows: from the last wave, which next polls the head's
+    // masks (loads complete in order, so the first wait after a store also
+    // waits for its write-through; the other waves go on to their chunks)
+    if (tid == kThreads - kWave)
+      sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
+                       make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
+  }
+  if (!spec) {
+    init_state();
+    loop1();
+  }
+
   if constexpr (kFused) {
     // this workgroup's share of the head's expanded rows, once every tile of
     // the head has published its mask (polled by the last wave, which has
-    // suffix rows only when every wave has)
+    // suffix rows only when every wave has); workgroup 0 records for the
+    // next launch whether every block expanded
     if (wave == kWaves - 1) {
       const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
       const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
-      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits);
+      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits, N);
+      if (wk == 0 && lane == 0)
+        __hip_atomic_store(sx->control + h * kLine + 2,
+                           sx->xr[2] ? (uint64_t)*sx->stats.tag + 1u : 0ull, __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
     }
     __syncthreads();
-    const int32_t* xl = sx->xl;
-    const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
-    run_pages(x_first, sx->xr[1],
-              [&](uint32_t c) { return (uint32_t)xl[((c << 4) >> lb) - e_first]; });
+    const bool again = spec && sx->xr[2] == 0u;  // the speculation missed
+    if (again) {
+      reps_on = has_reps;
+      init_state();
+      pre_issue();
+      loop1();
+    }
+    if (!spec || again) {
+      const int32_t* xl = sx->xl;
+      const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
+      run_pages(x_first, sx->xr[1],
+                [&](uint32_t c) { return (uint32_t)xl[((c << 4) >> lb) - e_first]; });
+    }
   } else {
     run_pages(0u, (uint32_t)__popcll(bits) * B,
               [&](uint32_t c) { return tile * kTile + (uint32_t)list[(c << 4) >> lb]; });
@@ -2205,6 +2259,7 @@ struct StepArgs {
   int heads;
   uint32_t spin;      // polls before a hand-off wait gives up
   uint32_t skew;      // 0 (a test hook's nonzero value makes every wait run out)
+  uint32_t speculate; // 1: speculate where the previous launch expanded every block
 };
 
 // Every region starts on a 16-byte boundary: the q staging and the combine
@@ -2215,10 +2270,11 @@ struct StepShared {
   alignas(16) float mts[GBM];         // the tile's max z per row
   alignas(16) unsigned long long wsum[kWaves];
   alignas(16) int32_t xl[kTile + 4];
-  uint32_t xr[2];
+  uint32_t xr[3];
   uint64_t base;
   uint32_t tag, rtag;
   uint32_t ticket;
+  uint32_t spec;
   alignas(16) DecideShared dec;
   alignas(16) union {
     struct {
@@ -2288,7 +2344,14 @@ void step_kernel(StepArgs s) {
                    sh.xl,
                    sh.xr,
                    s.heads,
-                   s.skew};
+                   s.skew,
+                   &sh.spec};
+  // whether the previous launch on the workspace expanded every block of the
+  // head (its workgroup 0 left that launch's tag + 1 here)
+  uint64_t prev_full = 0;
+  if (tid == 0 && s.speculate)
+    prev_full = __hip_atomic_load(s.control + h * kLine + 2, __ATOMIC_RELAXED,
+                                  __HIP_MEMORY_SCOPE_AGENT);
   score_dots<D, GBM>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
   // (the epoch is read before the loads below are issued: loads complete in
   // order, so a later read would wait for them too)
@@ -2296,6 +2359,7 @@ void step_kernel(StepArgs s) {
     sh.base = epoch * (uint64_t)W;
     sh.tag = (uint32_t)epoch + 1u;
     sh.rtag = sh.tag + s.skew;
+    sh.spec = s.speculate && prev_full == epoch + 1u ? 1u : 0u;
   }
   // the attention's loads that need no statistics land during them
   const MmaLoads<D> ld = mma_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
@@ -2713,6 +2777,9 @@ StepMode step_mode(const SelectParams& p, const Layout& L, const DecodeBuffers& 
 // wait (0 = kSpinLimit) and a tag skew that makes every wait run out.
 thread_local uint32_t g_spin_limit = 0;
 thread_local uint32_t g_skew = 0;
+// Test hook (rkv_set_speculation, per thread): 0 turns the step's
+// speculation off.
+thread_local uint32_t g_speculate = 1;
 
 int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, bool ticketed) {
   StepArgs s;
@@ -2735,6 +2802,7 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, 
   s.heads = (int)p.heads;
   s.spin = g_spin_limit ? g_spin_limit : kSpinLimit;
   s.skew = g_skew;
+  s.speculate = g_speculate;
   const int64_t rows = rows_per_pass(p.group, p.dim);
   mark(0, p.stream);
   int rc = kUnsupported;
@@ -3076,6 +3144,16 @@ extern "C" int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew) {
   clear_error();
   g_spin_limit = spin_limit;
   g_skew = skew;
+  return kOk;
+}
+
+// Test hook: 0 turns off the one-launch step's speculation (attending every
+// block's rows before the decision when the previous launch on the workspace
+// expanded every block), 1 (default) turns it on.  Results are the same bit
+// for bit either way.  Per thread.
+extern "C" int rkv_set_speculation(int enable) {
+  clear_error();
+  g_speculate = enable ? 1u : 0u;
   return kOk;
 }
 

@@ -81,6 +81,8 @@ def _bind(lib):
     lib.rkv_decode_plan.restype = _int
     lib.rkv_set_handoff_test.argtypes = [_u32, _u32]
     lib.rkv_set_handoff_test.restype = _int
+    lib.rkv_set_speculation.argtypes = [_int]
+    lib.rkv_set_speculation.restype = _int
     lib.rkv_decode_static.argtypes = lib.rkv_decode.argtypes[:-3] + [_p]
     lib.rkv_decode_static.restype = _int
     lib.rkv_dense_decode.argtypes = [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64,
@@ -378,6 +380,14 @@ def set_handoff_test(spin_limit=0, skew=0):
     """Test hook: the step's poll limit per wait (0 = default) and a skew
     that makes every wait run out (0 = off), for later calls on this thread."""
     _check(lib().rkv_set_handoff_test(spin_limit, skew), "rkv_set_handoff_test")
+
+
+def set_speculation(enable=True):
+    """Test hook: the one-launch step's speculation (attending every block's
+    rows before the decision when the previous launch on the workspace
+    expanded every block) on or off for later calls on this thread; results
+    are the same bit for bit either way."""
+    _check(lib().rkv_set_speculation(1 if enable else 0), "rkv_set_speculation")
 
 
 def decode_static(query, summary, key_suffix, value_suffix, config, output, mask,

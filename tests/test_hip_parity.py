@@ -437,6 +437,50 @@ def test_graph_replays_match_eager(hip, decode_path):
     assert_control_clean(hip, ws)
 
 
+@pytest.mark.parametrize("heads,group,dim,block,prompt", [
+    (8, 4, 128, 32, 8192), (4, 7, 128, 64, 8192), (2, 8, 64, 16, 3000)])
+def test_speculation_matches_the_normal_order_bit_for_bit(hip, heads, group, dim, block,
+                                                          prompt):
+    """After a launch that expanded every block, the step's workgroups attend
+    every row before the decision: when every block expands again the result
+    is the normal order's bit for bit, and when not (a sparse eps on the same
+    workspace) the speculation is dropped and the normal order runs."""
+    inp = _decode_case(heads, group, dim, block, prompt, 0.05, suffix=16, seed=5)
+    full = RefineKVConfig(backend="hip", block_size=block, eps=0.0, gqa_reduction="any")
+    summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), full)
+    q, sk, sv = (inp[k].to(DEV) for k in ("query", "suffix_keys", "suffix_values"))
+    assert hip.decode_plan(heads, group, dim, summary.num_blocks, block) == "step"
+
+    def run(cfg, ws):
+        res = sparse_attention(q, summary, sk, sv, cfg, workspace=ws, return_selected=True)
+        return res.output.clone(), res.selected.clone()
+
+    hip.set_speculation(False)
+    try:
+        want_full = run(full, {})
+        # the smallest of these eps that leaves some block unexpanded
+        for eps in (0.01, 0.05, 0.2, 1.0, 5.0):
+            sparse = RefineKVConfig(backend="hip", block_size=block, eps=eps,
+                                    gqa_reduction="any")
+            want_sparse = run(sparse, {})
+            if not want_sparse[1].all():
+                break
+    finally:
+        hip.set_speculation(True)
+    assert want_full[1].all() and not want_sparse[1].all()
+    ws = {}
+    got = [run(full, ws) for _ in range(3)]  # the first in the normal order, then speculating
+    got.append(run(sparse, ws))              # speculates and misses
+    got.append(run(full, ws))                # the previous launch did not expand every block
+    got.append(run(full, ws))                # speculates again
+    torch.cuda.synchronize()
+    for i, (out, mask) in enumerate(got):
+        want = want_sparse if i == 3 else want_full
+        assert torch.equal(mask, want[1]), i
+        assert torch.equal(out, want[0]), i
+    assert assert_control_clean(hip, ws) == len(got)
+
+
 @pytest.mark.parametrize("path", [p for p in gc.fixture_paths() if "f32" not in p],
                          ids=lambda p: p.split("/")[-1][:-4])
 def test_reference_golden_end_to_end(hip, path):
