@@ -579,7 +579,7 @@ class RefineKV:
                 dense = query.shape[1] * state.visible_length
                 self._record(dense, dense)
             return self._dense_decode(module, query, key, value, mask, scaling, kwargs,
-                                      state.visible_length)
+                                      state.visible_length, state.workspace)
         counter = None
         if self.config.collect_stats:
             # expanded blocks count their tokens, the others one representative:
@@ -648,10 +648,16 @@ class RefineKV:
         q = queries[:, :count].reshape(heads, groups, count, dim)
         return select_blocks_union(q, state.summary, self.config, workspace=state.workspace)
 
-    def _dense_decode(self, module, query, key, value, mask, scaling, kwargs, visible):
+    def _dense_decode(self, module, query, key, value, mask, scaling, kwargs, visible,
+                      workspace=None):
         """Dense layers and the dense baseline: SDPA with an explicit additive
         mask over the visible prefix (transformers.py:510-520; the mask-free
-        GQA path can round differently in bf16)."""
+        GQA path can round differently in bf16).  With a kernel backend on a
+        ROCm device, shapes the dense decode kernel runs go to it instead
+        (the same tokens [0, visible), the same default scaling)."""
+        out = self._hip_dense_decode(query, key, value, scaling, visible, workspace)
+        if out is not None:
+            return out, None
         if mask is None:
             mask = query.new_full((1, 1, 1, key.shape[2]), torch.finfo(query.dtype).min)
             mask[..., :visible] = 0
@@ -659,6 +665,29 @@ class RefineKV:
             mask = query.new_zeros(mask.shape).masked_fill(~mask, torch.finfo(query.dtype).min)
         return sdpa_attention_forward(module, query, key, value, mask, dropout=0,
                                       scaling=scaling, **kwargs)
+
+    def _hip_dense_decode(self, query, key, value, scaling, visible, workspace):
+        """rkv_dense_decode over the visible prefix when the backend allows the
+        kernels and the shape is one it runs (bf16, batch 1, head_dim 32..160
+        in steps of 32, group <= 16, scaling 1/sqrt(head_dim)); else None."""
+        from .. import _hip
+        from ..config import KERNEL_BACKENDS
+
+        if workspace is None or self.config.backend not in KERNEL_BACKENDS + ("auto",):
+            return None
+        if not _hip.is_rocm_device(query):
+            return None
+        heads, dim = key.shape[1], query.shape[-1]
+        group = query.shape[1] // heads
+        if (query.shape[0] != 1 or query.shape[2] != 1 or query.shape[1] != heads * group
+                or not query.dtype == key.dtype == value.dtype == torch.bfloat16
+                or dim % 32 or not 32 <= dim <= _hip.DENSE_MAX_DIM or group > _hip.MAX_GROUP):
+            return None
+        if scaling is not None and not math.isclose(scaling, dim ** -0.5, rel_tol=1e-6):
+            return None
+        out = _hip.dense_decode(query[0, :, 0].reshape(heads, group, dim), key[0], value[0],
+                                length=visible, workspace=workspace)
+        return self._to_model_layout(out.unsqueeze(2), query)
 
     def _record(self, accessed, dense):
         self._totals["accessed"] = self._totals["accessed"] + accessed

@@ -250,6 +250,44 @@ def test_hip_stats_and_dense_layers():
         assert s.stats["equivalent_access_ratio"] == 1
 
 
+@pytest.mark.gpu
+def test_hip_dense_layers_run_the_dense_kernel_and_match_the_oracle(monkeypatch, oracle_lib):
+    """Dense layers (full_attention_layers) decode through rkv_dense_decode
+    over the visible prefix: every call's output against the oracle's dense
+    attention of the same query, keys and values."""
+    import numpy as np
+
+    _gpu_or_skip()
+    from refinekv import _hip
+
+    calls = []
+    real = _hip.dense_decode
+
+    def record(query, keys, values, length=None, workspace=None, output=None):
+        out = real(query, keys, values, length=length, workspace=workspace, output=output)
+        calls.append((query.clone(), keys[:, :length].clone(), values[:, :length].clone(),
+                      out.clone()))
+        return out
+
+    monkeypatch.setattr(_hip, "dense_decode", record)
+    model = tiny_model("llama", "cuda")
+    with RefineKV(model, RefineKVConfig(backend="hip", full_attention_layers=1,
+                                        collect_stats=True)) as session:
+        generate(model)
+        assert session.stats["decode_attention_calls"] == 6
+    assert len(calls) == 3  # layer 0, three decode steps
+
+    def bits(t):
+        return t.cpu().contiguous().view(torch.int16).numpy().view(np.uint16)
+
+    for step, (q, k, v, out) in enumerate(calls):
+        assert k.shape[1] == 40 + step  # the visible prefix: prompt + tokens so far
+        want = oracle_lib.dense_attention(q.float().cpu().numpy(), bits(k), bits(v))
+        want = torch.from_numpy(want).to(torch.bfloat16).float().numpy()
+        err = np.abs(out.float().cpu().numpy() - want)
+        assert err.max() <= 2e-2 and err.mean() <= 1e-3 * np.abs(want).mean() + 1e-6
+
+
 # ---------------------------------------------------------------------------
 # GPU: the hook's decode calls against the CPU oracle (eager and graph replay)
 # ---------------------------------------------------------------------------
