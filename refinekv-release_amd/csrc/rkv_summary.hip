@@ -190,53 +190,26 @@ struct CacheOut {
 // Byte strides of a block's rows fit 31 bits (checked on the host).
 // blockDim.x / 64 waves (1, 2 or 4), one block each, and summary_wave_lds
 // bytes of dynamic LDS per wave.  kStage needs 16-byte aligned rows.
+// Pass 1 (column sums in TOKSUM order, min, max -> means, widths) and pass 2
+// (per-token radius and value norm -> ellipsoid, value_norm) of block b of
+// head h, whose rows are kr / vr (byte strides kts / vts) or, with kStage,
+// staged in LDS at kst / vst; s_mk / s_rs: D floats each of LDS.  One wave;
+// its workgroup holds whole waves only (the __syncthreads between the passes
+// orders the LDS writes of the means before their reads).
 template <int D, class In, bool kStore, bool kStage>
-__global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
-    const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
-    const typename In::T* __restrict__ values, int64_t v_hs, int64_t v_ts, int64_t length,
-    int block, int64_t n_blocks, int64_t* __restrict__ counts, uint16_t* __restrict__ key_mean,
-    uint16_t* __restrict__ value_mean, uint16_t* __restrict__ ellipsoid,
-    float* __restrict__ value_norm, CacheOut<In> out) {
+__device__ __forceinline__ void summary_passes(
+    int64_t h, int64_t b, int64_t bb, bool valid, int cnt, int block, int64_t n_blocks,
+    __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int kts, int vts, const uint4* kst,
+    const uint4* vst, float* s_mk, float* s_rs, int64_t* __restrict__ counts,
+    uint16_t* __restrict__ key_mean, uint16_t* __restrict__ value_mean,
+    uint16_t* __restrict__ ellipsoid, float* __restrict__ value_norm, const CacheOut<In>& out) {
   using T = typename In::T;
   using St = Staging<In, D>;
   constexpr int E = (int)sizeof(T);
   constexpr int CPL = D <= 128 ? 2 : 4;  // columns per lane in pass 1
   constexpr int LANES1 = D / CPL;
-  extern __shared__ uint4 s_dyn[];
-
-  const int waves = blockDim.x / kWave;
-  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
   const int lane = threadIdx.x % kWave;
-  const int64_t h = blockIdx.y;
-  const int64_t b = (int64_t)blockIdx.x * waves + wave;
-  const bool valid = b < n_blocks;
-  const int64_t bb = valid ? b : n_blocks - 1;  // in-bounds block for addresses
-  // (64-bit compares run on the vector ALU: readfirstlane keeps the counts
-  // and buffer views in scalar registers)
-  const int cnt = __builtin_amdgcn_readfirstlane(
-      !valid ? 0 : (int)(b == n_blocks - 1 ? length - (n_blocks - 1) * block : block));
-  // the block's rows; a wave past the last block reads nothing (zeros)
-  const int kts = (int)k_ts * E, vts = (int)v_ts * E;
   auto extent = [&](int ts) { return __builtin_amdgcn_readfirstlane(cnt ? (cnt - 1) * ts + D * E : 0); };
-  const auto kr = rows_view(keys + h * k_hs + bb * block * k_ts, extent(kts));
-  const auto vr = rows_view(values + h * v_hs + bb * block * v_ts, extent(vts));
-  const int chunks = kStage ? block * St::NC : 0;  // per tensor, a multiple of 64
-  uint4* kst = s_dyn + wave * (2 * chunks + D / 2);
-  uint4* vst = kst + chunks;
-  float* s_mk = reinterpret_cast<float*>(vst + chunks);
-  float* s_rs = s_mk + D;
-  if constexpr (kStage) {
-    // the whole block in flight: LDS chunk p (token p / NC, slot p % NC)
-    // takes chunk slot(p % NC, t) of that token's row
-    for (int p0 = 0; p0 < chunks; p0 += kWave) {
-      const int p = p0 + lane, t = p / St::NC;
-      const int off = St::slot(p % St::NC, t) * 16;
-      load_to_lds16(kr, kst + p0, t * kts + off);
-      load_to_lds16(vr, vst + p0, t * vts + off);
-    }
-    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  }
-
   // ---- pass 1: column sums (TOKSUM order), min, max -------------------
   const bool on1 = valid && lane < LANES1;
   const int col = lane < LANES1 ? lane * CPL : 0;
@@ -428,6 +401,146 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
   }
 }
 
+template <int D, class In, bool kStore, bool kStage>
+__global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
+    const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
+    const typename In::T* __restrict__ values, int64_t v_hs, int64_t v_ts, int64_t length,
+    int block, int64_t n_blocks, int64_t* __restrict__ counts, uint16_t* __restrict__ key_mean,
+    uint16_t* __restrict__ value_mean, uint16_t* __restrict__ ellipsoid,
+    float* __restrict__ value_norm, CacheOut<In> out) {
+  using T = typename In::T;
+  using St = Staging<In, D>;
+  constexpr int E = (int)sizeof(T);
+  extern __shared__ uint4 s_dyn[];
+
+  const int waves = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);  // wave-uniform
+  const int lane = threadIdx.x % kWave;
+  const int64_t h = blockIdx.y;
+  const int64_t b = (int64_t)blockIdx.x * waves + wave;
+  const bool valid = b < n_blocks;
+  const int64_t bb = valid ? b : n_blocks - 1;  // in-bounds block for addresses
+  // (64-bit compares run on the vector ALU: readfirstlane keeps the counts
+  // and buffer views in scalar registers)
+  const int cnt = __builtin_amdgcn_readfirstlane(
+      !valid ? 0 : (int)(b == n_blocks - 1 ? length - (n_blocks - 1) * block : block));
+  // the block's rows; a wave past the last block reads nothing (zeros)
+  const int kts = (int)k_ts * E, vts = (int)v_ts * E;
+  auto extent = [&](int ts) { return __builtin_amdgcn_readfirstlane(cnt ? (cnt - 1) * ts + D * E : 0); };
+  const auto kr = rows_view(keys + h * k_hs + bb * block * k_ts, extent(kts));
+  const auto vr = rows_view(values + h * v_hs + bb * block * v_ts, extent(vts));
+  const int chunks = kStage ? block * St::NC : 0;  // per tensor, a multiple of 64
+  uint4* kst = s_dyn + wave * (2 * chunks + D / 2);
+  uint4* vst = kst + chunks;
+  float* s_mk = reinterpret_cast<float*>(vst + chunks);
+  float* s_rs = s_mk + D;
+  if constexpr (kStage) {
+    // the whole block in flight: LDS chunk p (token p / NC, slot p % NC)
+    // takes chunk slot(p % NC, t) of that token's row
+    for (int p0 = 0; p0 < chunks; p0 += kWave) {
+      const int p = p0 + lane, t = p / St::NC;
+      const int off = St::slot(p % St::NC, t) * 16;
+      load_to_lds16(kr, kst + p0, t * kts + off);
+      load_to_lds16(vr, vst + p0, t * vts + off);
+    }
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  }
+
+  summary_passes<D, In, kStore, kStage>(h, b, bb, valid, cnt, block, n_blocks, kr, vr, kts,
+                                        vts, kst, vst, s_mk, s_rs, counts, key_mean,
+                                        value_mean, ellipsoid, value_norm, out);
+}
+
+// The staged summary as a stream (2-byte K/V, head_dim >= 192): one-wave
+// workgroups, each going through the (head, block) pairs f = w, w + nw, ...
+// (w its index, nw the grid).  The next block's rows are loaded into registers (16 bytes per
+// lane per load, at most 8 per tensor) while the current block's passes read
+// LDS, then written into the staged layout: the wave keeps a block's loads
+// in flight all the time, where a wave per block waits for its loads, then
+// computes with none in flight.  The passes are summary_kernel's.
+constexpr int kStreamChunks = 8;  // 16-byte chunks per lane per tensor, at most
+
+template <int D, class In, bool kStore>
+__global__ __launch_bounds__(kWave) void summary_stream_kernel(
+    const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
+    const typename In::T* __restrict__ values, int64_t v_hs, int64_t v_ts, int64_t length,
+    int block, int64_t n_blocks, int64_t heads, int64_t* __restrict__ counts,
+    uint16_t* __restrict__ key_mean, uint16_t* __restrict__ value_mean,
+    uint16_t* __restrict__ ellipsoid, float* __restrict__ value_norm, CacheOut<In> out) {
+  using St = Staging<In, D>;
+  constexpr int E = (int)sizeof(typename In::T);
+  static_assert(E == 2, "the stream holds 2-byte elements");
+  typedef unsigned int U4 __attribute__((ext_vector_type(4)));
+  extern __shared__ uint4 s_dyn[];
+  const int lane = threadIdx.x;
+  const int64_t total = heads * n_blocks;
+  const int64_t nw = gridDim.x;
+  const int chunks = block * St::NC;  // per tensor: 64 .. 64 kStreamChunks
+  const int per_lane = chunks / kWave;
+  uint4* kst = s_dyn;
+  uint4* vst = kst + chunks;
+  float* s_mk = reinterpret_cast<float*>(vst + chunks);
+  float* s_rs = s_mk + D;
+  const int kts = (int)k_ts * E, vts = (int)v_ts * E;
+
+  struct Views {
+    int64_t h, b;
+    int cnt;
+    __amdgpu_buffer_rsrc_t kr, vr;
+  };
+  // (head, block) pair f: its token count and row views, wave-uniform
+  auto views = [&](int64_t f) {
+    Views v;
+    v.h = f / n_blocks;
+    v.b = f - v.h * n_blocks;
+    v.cnt = __builtin_amdgcn_readfirstlane(
+        (int)(v.b == n_blocks - 1 ? length - (n_blocks - 1) * block : block));
+    const int ek = __builtin_amdgcn_readfirstlane((v.cnt - 1) * kts + D * E);
+    const int ev = __builtin_amdgcn_readfirstlane((v.cnt - 1) * vts + D * E);
+    v.kr = rows_view(keys + v.h * k_hs + v.b * block * k_ts, ek);
+    v.vr = rows_view(values + v.h * v_hs + v.b * block * v_ts, ev);
+    return v;
+  };
+  U4 rk[kStreamChunks], rv[kStreamChunks];
+  // chunk p = 64 i + lane of the staged layout: token p / NC, slot p % NC
+  // takes chunk slot(p % NC, t) of that token's row
+  auto issue = [&](const Views& v) {
+#pragma unroll
+    for (int i = 0; i < kStreamChunks; ++i) {
+      if (i < per_lane) {
+        const int p = kWave * i + lane, t = p / St::NC;
+        const int off = St::slot(p % St::NC, t) * 16;
+        rk[i] = __builtin_amdgcn_raw_buffer_load_b128(v.kr, t * kts + off, 0, 0);
+        rv[i] = __builtin_amdgcn_raw_buffer_load_b128(v.vr, t * vts + off, 0, 0);
+      }
+    }
+  };
+  int64_t f = blockIdx.x;
+  if (f >= total) return;
+  issue(views(f));
+  for (;;) {
+    // the block's rows from registers into the staged layout
+#pragma unroll
+    for (int i = 0; i < kStreamChunks; ++i) {
+      if (i < per_lane) {
+        kst[kWave * i + lane] = __builtin_bit_cast(uint4, rk[i]);
+        vst[kWave * i + lane] = __builtin_bit_cast(uint4, rv[i]);
+      }
+    }
+    __syncthreads();
+    // the next block's loads fly while this one is summarized
+    const int64_t fn = f + nw;
+    if (fn < total) issue(views(fn));
+    const Views cur = views(f);
+    summary_passes<D, In, kStore, true>(cur.h, cur.b, cur.b, true, cur.cnt, block, n_blocks,
+                                        cur.kr, cur.vr, kts, vts, kst, vst, s_mk, s_rs, counts,
+                                        key_mean, value_mean, ellipsoid, value_norm, out);
+    __syncthreads();
+    if (fn >= total) break;
+    f = fn;
+  }
+}
+
 // max_value_norm[h] = max over blocks (summary.py:148).
 __global__ __launch_bounds__(256) void max_norm_kernel(const float* __restrict__ value_norm,
                                                        int64_t n_blocks,
@@ -462,6 +575,49 @@ int launch_summary(const void* keys, int64_t k_hs, int64_t k_ts, const void* val
                      summary_wave_lds(true, dim, elem, block) <= kStageWaveMax &&
                      rows16(keys, k_hs, k_ts) && rows16(values, v_hs, v_ts);
   const int64_t per_wave = summary_wave_lds(stage, dim, elem, block);
+  // (head_dim >= 192: 161 -> 142 us at 65536 tokens, d 256, B 16; at d 128 the
+  // passes' vector work bounds the kernel and the stream is no faster, at B 16
+  // slower)
+  if constexpr (sizeof(typename In::T) == 2) {
+  if (stage && dim >= 192 && block * dim * elem / 16 <= kWave * kStreamChunks) {
+    // the stream: one-wave workgroups, as many as the device holds at once
+    int64_t resident = 0;
+    int dev = -1, cus = 0, per_cu = 0;
+    RKV_DISPATCH_DIM(dim, D, {
+      if (hipGetDevice(&dev) == hipSuccess &&
+          hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) ==
+              hipSuccess &&
+          hipOccupancyMaxActiveBlocksPerMultiprocessor(
+              &per_cu, out.keys ? summary_stream_kernel<D, In, true>
+                                : summary_stream_kernel<D, In, false>,
+              kWave, (size_t)per_wave) == hipSuccess)
+        resident = (int64_t)cus * per_cu;
+    });
+    const int64_t total = heads * n_blocks;
+    const int64_t grid = resident > 0 ? (resident < total ? resident : total) : total;
+    const auto* k = static_cast<const typename In::T*>(keys);
+    const auto* v = static_cast<const typename In::T*>(values);
+    RKV_DISPATCH_DIM(dim, D, {
+      if (out.keys)
+        summary_stream_kernel<D, In, true><<<dim3((unsigned)grid), dim3(kWave), per_wave,
+                                              stream>>>(
+            k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, heads, counts,
+            static_cast<uint16_t*>(key_mean), static_cast<uint16_t*>(value_mean),
+            static_cast<uint16_t*>(ellipsoid), value_norm, out);
+      else
+        summary_stream_kernel<D, In, false><<<dim3((unsigned)grid), dim3(kWave), per_wave,
+                                               stream>>>(
+            k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, heads, counts,
+            static_cast<uint16_t*>(key_mean), static_cast<uint16_t*>(value_mean),
+            static_cast<uint16_t*>(ellipsoid), value_norm, out);
+    });
+    int rc = check_launch("summary_stream_kernel");
+    if (rc) return rc;
+    max_norm_kernel<<<dim3((unsigned)heads), dim3(256), 0, stream>>>(value_norm, n_blocks,
+                                                                      max_value_norm);
+    return check_launch("max_norm_kernel");
+  }
+  }
   int waves = kSummaryWaves;
   while (stage && waves > 1 && waves * per_wave > kStageGroupMax) waves /= 2;
   dim3 grid((unsigned)((n_blocks + waves - 1) / waves), (unsigned)heads);

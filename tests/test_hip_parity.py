@@ -135,6 +135,8 @@ SUMMARY_CASES = [
     (torch.bfloat16, 256, 32, 999), (torch.float16, 128, 32, 777), (torch.float16, 64, 64, 200),
     (torch.float32, 128, 32, 999), (torch.float32, 32, 16, 517), (torch.float32, 96, 64, 1000),
     (torch.float32, 256, 16, 400), (torch.bfloat16, 128, 32, 1), (torch.bfloat16, 64, 64, 63),
+    # the streaming form (2-byte, staged, head_dim >= 192)
+    (torch.bfloat16, 256, 16, 777), (torch.float16, 224, 16, 500),
     # the largest blocks (64 KiB and 128 KiB of K plus V)
     (torch.float32, 256, 64, 300), (torch.float32, 128, 64, 700),
 ]
