@@ -1374,8 +1374,8 @@ __device__ __forceinline__ void merge_state4(float m2, float d2, const float4& n
   mx = M;
 }
 
-// The head's last kMergers tiles (by ticket) merge it, each a slice of the
-// columns, once every tile of the head has published.  Slice m: head h's
+// The head's last K workgroups (by ticket; K = mergers(W)) merge it, each a
+// slice of the columns, once every workgroup of the head has published.  Slice m: head h's
 // rows, column quads [m Q / K, (m + 1) Q / K), from every tile's partial ->
 // bf16 output; slice 0 also adds the head's access count.  Each (row, 4
 // columns) unit is merged by S adjacent lanes (S a power of two <= 16, so a
@@ -1383,6 +1383,13 @@ __device__ __forceinline__ void merge_state4(float m2, float d2, const float4& n
 // over the S lanes into the unit's last lane (DPP row shifts): a fixed
 // order, so outputs repeat bit for bit.
 constexpr int kMergers = 8;
+
+// Mergers of a head of W workgroups: W / 8, at least 8 (or W) -- the slices
+// shrink as the partials to fold per slice grow.
+__device__ __forceinline__ uint32_t mergers(uint32_t W) {
+  const uint32_t k = W / 8u > (uint32_t)kMergers ? W / 8u : (uint32_t)kMergers;
+  return W < k ? W : k;
+}
 
 template <int D>
 __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, int m, int K) {
@@ -1801,7 +1808,7 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     }
     __syncthreads();
     const uint32_t ticket = *sx->flag;
-    const uint32_t K = W < (uint32_t)kMergers ? W : (uint32_t)kMergers;
+    const uint32_t K = mergers(W);
     if (ticket >= W - K) {
       // (the last ticket's own bump completed the count: every other tile's
       // partial landed before its bump did, so it merges without a poll)
@@ -2121,7 +2128,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
     }
     __syncthreads();
     const uint32_t ticket = *sx->flag;
-    const uint32_t K = W < (uint32_t)kMergers ? W : (uint32_t)kMergers;
+    const uint32_t K = mergers(W);
     if (ticket >= W - K) {
       // (the last ticket's own bump completed the count: every other
       // workgroup's partial landed before its bump did, so it merges without
