@@ -50,7 +50,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr int kRowsPerWave = kMaxGroup / kWaves;  // query rows a wave owns in a tile
 constexpr float kLog2e = 1.44269504088896341f;
 constexpr int kLine = 8;  // u64 counters per 64-byte hand-off line
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a hand-off wait gives up (default)
@@ -187,11 +186,6 @@ __device__ __forceinline__ float risk_from(float z, float delta, float A, float 
 
 __host__ __device__ __forceinline__ float inf_to_zero(float m) {
   return (m == kPosInf || m == kNegInf) ? 0.0f : m;
-}
-
-__device__ __forceinline__ int64_t block_count(int64_t b, int64_t n, int64_t block,
-                                               int64_t length) {
-  return b == n - 1 ? length - (n - 1) * block : block;
 }
 
 // Sum over each 8-lane group (lanes 0-7 and 8-15 of every 16-lane row) in
@@ -420,7 +414,7 @@ __device__ __forceinline__ void score_stats(const ScoreArgs& a, int64_t tile, co
     const float zm = wave_nanmax_u(z);
     const float zl = wave_sum_u(expf_(z - inf_to_zero(zm)));
     const float dl = (sqrtf(clamp_min(pdot[g * kTile + lane], 0.0f)) * a.scale) * kInflate;
-    float t;
+    float t = 1.0f;  // (set by delta_log_cosh on the lanes of existing blocks)
     const float zc = valid ? z + delta_log_cosh(dl, t) : kNegInf;
     const float cm = wave_nanmax_u(zc);
     const float cl = wave_sum_u(expf_(zc - inf_to_zero(cm)));
@@ -1471,25 +1465,17 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
   }
 }
 
-// Two workgroups per CU (<= 256 registers per lane), so a 512-tile step runs
-// in one round on 256 CUs.
+// The attention of one (tile, head) on the vector ALUs (the three-kernel
+// form's attend kernel above head_dim 160, where the matrix-core engine's
+// staging does not fit): 16 lane groups, two workgroups per CU.
 //
 // Order of work: every load that does not depend on the decision is issued
 // first (the decision's inputs, the value means, z and the tile max of this
 // lane group's representatives, one suffix row per lane group); the full
 // representative sum over the tile is folded while the decision's inputs
-// are in flight; after the decision the
-// expanded blocks' representative terms are taken out again and the
-// expanded blocks' tokens and the suffix rows are attended.
-//
-// kFused: the one-launch step (sx set): the tile's statistics come from
-// LDS, the decision waits until every tile of the head has published its
-// LSE partials, the partials are published with coherent stores and the
-// head's last tile merges them.
-//
-// attend_tile's loads that do not depend on the statistics or the decision:
-// the one-launch step issues them before its statistics, so they land while
-// the statistics are computed.
+// are in flight; after the decision the expanded blocks' representative
+// terms are taken out again and the expanded blocks' tokens and the suffix
+// rows are attended.
 template <int D, int GBM>
 struct AttendLoads {
   DecideLoads din;
@@ -1499,8 +1485,8 @@ struct AttendLoads {
   RawBf16<D / 16> ksr[1], vsr[1];        // the lane group's first suffix token
 };
 
-// Workgroup wk of head h (blockIdx.x and blockIdx.y, or the step's ticket).
-template <int D, int GBM, bool kFused>
+// Workgroup wk of head h (blockIdx.x and blockIdx.y).
+template <int D, int GBM>
 __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a, int64_t h,
                                                             uint32_t wk) {
   constexpr int CH = D / 16;
@@ -1515,7 +1501,7 @@ __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a,
   const int lg = tid >> 4, c = tid & 15;
   const int g0 = blockIdx.z * GBM;
   AttendLoads<D, GBM> ld;
-  ld.din = decide_issue<!kFused>(da, h, tile);
+  ld.din = decide_issue<true>(da, h, tile);
   // The suffix length does not change during a launch: a scalar load from
   // the constant address space, outside the vector loads' in-order count.
   uint32_t S = (uint32_t)a.suffix_cap;
@@ -1550,9 +1536,9 @@ __device__ __forceinline__ AttendLoads<D, GBM> attend_issue(const AttendArgs& a,
   return ld;
 }
 
-template <int D, int GBM, bool kFused>
+template <int D, int GBM>
 __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& dsh,
-                                            LaneCombine<D, GBM>& cmb, const StepCtx* sx,
+                                            LaneCombine<D, GBM>& cmb,
                                             const AttendLoads<D, GBM>& ld, int64_t h,
                                             uint32_t wk) {
   constexpr int CH = D / 16;
@@ -1590,15 +1576,13 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
 #pragma unroll
     for (int g = 0; g < GBM; ++g) {
       const int gg = g0 + g < G ? g0 + g : G - 1;
-      if constexpr (kFused) zr[g][i] = sx->stats.zs[gg][lg + 16 * i].x;
-      else zr[g][i] = da.zf[(h * G + gg) * da.z_stride + b].x;
+      zr[g][i] = da.zf[(h * G + gg) * da.z_stride + b].x;
     }
   }
 #pragma unroll
   for (int g = 0; g < GBM; ++g) {
     const int gg = g0 + g < G ? g0 + g : G - 1;
-    if constexpr (kFused) mt[g] = sx->mts[gg];
-    else mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
+    mt[g] = da.lse[((h * G + gg) * da.tile_stride + tile) * 4];
   }
   const uint32_t n_suffix = S > wk ? (S - wk + W - 1) / W : 0u;
   const uint32_t n_pre = n_suffix < 16u ? n_suffix : 16u;
@@ -1632,18 +1616,10 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
       }
     }
   }
-  // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
+  // ---- the decision --------------------------------------------------------
   const int32_t* list;
   uint32_t count = 0;
-  const uint64_t bits = decide_finish<kFused>(da, h, tile, din, dsh, nullptr, list, count,
-                                              kFused ? &sx->stats : nullptr);
-  if constexpr (kFused) {
-    // publish the expanded blocks (a tagged slot) for the head's even split
-    // of pooled token rows
-    if (tid == 0)
-      sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
-                       make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
-  }
+  const uint64_t bits = decide_finish<false>(da, h, tile, din, dsh, nullptr, list, count);
 
   // take the expanded blocks' representatives out again
   if ((bits >> lg) & 0x0001000100010001ull) {
@@ -1713,11 +1689,9 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     return bb != last || t < last_count;
   };
 
-  // ---- first: the rest of the suffix slice and, with three kernels, this
-  // tile's own expanded blocks (the one-launch step splits the head's
-  // expanded rows evenly over its tiles instead, below).
+  // ---- the rest of the suffix slice and this tile's expanded blocks
   const uint32_t n_rest = n_suffix - n_pre;
-  const uint32_t own_rows = kFused ? 0u : (uint32_t)__popcll(bits) * B;
+  const uint32_t own_rows = (uint32_t)__popcll(bits) * B;
   run_rows(n_rest + own_rows, [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) {
     if (v < n_rest) {
       const uint64_t t = wk + (n_pre + v) * W;
@@ -1729,22 +1703,6 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
     return page_row(tile * kTile + (uint32_t)list[w >> lb], w & (B - 1), kp, vp);
   });
 
-  // ---- then (one-launch step): this tile's share of the head's expanded
-  // rows, once every tile of the head has published its mask ---------------
-  if constexpr (kFused) {
-    if (tid < kWave) {
-      const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
-      const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
-      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits, N);
-    }
-    __syncthreads();
-    const int32_t* xl = sx->xl;
-    const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
-    run_rows(sx->xr[1], [&](uint32_t v, const uint16_t*& kp, const uint16_t*& vp) {
-      const uint32_t r = x_first + v;
-      return page_row((uint32_t)xl[(r >> lb) - e_first], r & (B - 1), kp, vp);
-    });
-  }
 
   // ---- the 16 lane groups -> one partial per query row, through LDS ------
   // (fully unrolled: the state arrays are indexed by constants only)
@@ -1781,43 +1739,11 @@ __device__ __forceinline__ void attend_tile(const AttendArgs& a, DecideShared& d
         l = __builtin_fmaf(cmb.ml[w][j][1], e, l);
       }
       const int64_t at = (h * G + g0 + gc + j) * da.tile_stride + wk;
-      if constexpr (kFused) {
-        sx->acc.store2((uint32_t)((at * D + d) * 4), make_float2(a0, a1));
-        if (d == 0) sx->ml.store2((uint32_t)(at * 8), make_float2(M, l));
-      } else {
-        *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
-        if (d == 0) a.part_ml[at] = make_float2(M, l);
-      }
+      *reinterpret_cast<float2*>(a.part_acc + at * D + d) = make_float2(a0, a1);
+      if (d == 0) a.part_ml[at] = make_float2(M, l);
     }
   }
-  if (a.tile_counts && tid == 0 && blockIdx.z == 0) {
-    // (a copy's count sits past the first T entries, which alone are summed)
-    if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + wk) * 4), count);
-    else a.tile_counts[h * da.tile_stride + wk] = count;
-  }
-  if constexpr (kFused) {
-    // publish and take a ticket; the head's last K tiles wait for the rest
-    // and merge a column slice each
-    wait_memory();
-    __syncthreads();
-    uint64_t* merged = sx->control + h * kLine + 1;
-    if (tid == 0) {
-      const uint64_t old = __hip_atomic_fetch_add(merged, 1ull, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      *sx->flag = (uint32_t)(old - *sx->base);
-    }
-    __syncthreads();
-    const uint32_t ticket = *sx->flag;
-    const uint32_t K = mergers(W);
-    if (ticket >= W - K) {
-      // (the last ticket's own bump completed the count: every other tile's
-      // partial landed before its bump did, so it merges without a poll)
-      if (tid == 0 && ticket != W - 1)
-        wait_counter<uint64_t>(merged, *sx->base + W + sx->skew, sx->stats.spin, sx->error());
-      __syncthreads();
-      merge_slice<D>(a, *sx, h, (int)(ticket - (W - K)), (int)K);
-    }
-  }
+  if (a.tile_counts && tid == 0 && blockIdx.z == 0) a.tile_counts[h * da.tile_stride + wk] = count;
 }
 
 // ---------------------------------------------------------------------------
@@ -2153,8 +2079,8 @@ void attend_kernel(AttendArgs a) {
     attend_tile_mma<D, GBM, false>(a, dsh, cmb, nullptr, ld, h, wk);
   } else {
     __shared__ alignas(16) LaneCombine<D, GBM> cmb;
-    const AttendLoads<D, GBM> ld = attend_issue<D, GBM, false>(a, blockIdx.y, blockIdx.x);
-    attend_tile<D, GBM, false>(a, dsh, cmb, nullptr, ld, blockIdx.y, blockIdx.x);
+    const AttendLoads<D, GBM> ld = attend_issue<D, GBM>(a, blockIdx.y, blockIdx.x);
+    attend_tile<D, GBM>(a, dsh, cmb, ld, blockIdx.y, blockIdx.x);
   }
 }
 
@@ -2182,10 +2108,12 @@ struct DenseArgs {
 // chunk c0 + w + 4 j to wave w, through the same three-stage matrix-core ring
 // as the decode's page rows; the four waves' states combine into one partial
 // per query row, which merge_kernel folds with the other splits'.
-// (two workgroups per CU up to head_dim 128; at 160 the ring's registers take
-// a whole SIMD per wave, one workgroup per CU, rather than spill)
+// (two workgroups per CU up to head_dim 128 and 8 query rows; beyond, the
+// ring's registers take a whole SIMD per wave, one workgroup per CU, rather
+// than spill)
 template <int D, int GBM>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(D <= 128 ? 2 : 1)))
+__global__ __launch_bounds__(kThreads)
+__attribute__((amdgpu_waves_per_eu(D <= 128 && GBM <= 8 ? 2 : 1)))
 void dense_kernel(DenseArgs a) {
   using S = MmaShape<D>;
   constexpr uint32_t kRowBytes = D * 2;
