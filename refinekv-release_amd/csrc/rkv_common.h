@@ -139,17 +139,24 @@ __device__ __forceinline__ float wave_sum_u(float v) {
   return readlane(row16_sum_last(v), 15);
 }
 
-// NaN-propagating wave max, returned uniformly.
+// NaN-propagating wave max, returned uniformly, with the NaN-propagating
+// maximum (v_maximum3_f32, one instruction per step).  A maximum is exact,
+// so the tree's shape does not matter; it differs from nanmax's only in the
+// zero a +0/-0 tie returns (and in a NaN's payload).  Every caller uses the
+// result m as a shift, exp(x - m), added back after a log, log(s) + m:
+// x - (+0) and x - (-0) differ only for x = ±0, where exp gives 1 either way,
+// and log(s) + (±0) are equal for every s (logf_ never returns -0), so no
+// output depends on the tie.
 __device__ __forceinline__ float wave_nanmax_u(float v) {
   float a, b;
   xor32_pair(v, a, b);
-  v = nanmax(a, b);
+  v = __builtin_elementwise_maximum(a, b);
   xor16_pair(v, a, b);
-  v = nanmax(a, b);
-  v = nanmax(v, row_shr<8>(v));
-  v = nanmax(v, row_shr<4>(v));
-  v = nanmax(v, row_shr<2>(v));
-  v = nanmax(v, row_shr<1>(v));
+  v = __builtin_elementwise_maximum(a, b);
+  v = __builtin_elementwise_maximum(v, row_shr<8>(v));
+  v = __builtin_elementwise_maximum(v, row_shr<4>(v));
+  v = __builtin_elementwise_maximum(v, row_shr<2>(v));
+  v = __builtin_elementwise_maximum(v, row_shr<1>(v));
   return readlane(v, 15);
 }
 

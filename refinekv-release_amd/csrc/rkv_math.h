@@ -122,10 +122,11 @@ RKV_HD float expf_(float x) {
   p = __builtin_fmaf(p, r, 1.0f);
 #if defined(__HIP_DEVICE_COMPILE__)
   // v_ldexp_f32 rounds once, exactly as scale_pow2's exact-then-rounded
-  // multiplies do.
-  float y = __builtin_amdgcn_ldexpf(p, (int)k);
-  y = x > 88.8f ? bits_f32(0x7F800000u) : y;
-  y = x < -104.0f ? 0.0f : y;
+  // multiplies do.  The clamped ends need no select of their own: at
+  // xs = 88.8 (k = 128, p > 1) the scale overflows to +inf, and at
+  // xs = -104 (k = -150, p < 0.98) it rounds to +0, the host's results for
+  // x > 88.8 and x < -104.  Only NaN (clamped to -104 by fmaxf) is selected.
+  const float y = __builtin_amdgcn_ldexpf(p, (int)k);
   return is_nan(x) ? x + x : y;
 #else
   return scale_pow2(p, (int)k);
@@ -138,23 +139,20 @@ RKV_HD float expf_(float x) {
 // Taylor series of 2*atanh(s)/s - 2 - ... truncated after s^8 (2/3, 2/5,
 // 2/7, 2/9).  log(1) == +0 exactly; log(0) == -inf; log(x<0) == NaN.
 //
-// The device build, as for expf_, runs the main path in every lane (on 1.0
-// in place of the special inputs) and selects the special results after.
+// The device build runs the main path in every lane and, when any lane of
+// the wave holds a special input (NaN, <= 0, +inf), selects the special
+// results after.  It splits x with v_frexp_mant / v_frexp_exp (x = mant 2^ef,
+// mant in [0.5, 1), subnormals included): m = 2 mant and e = ef - 1 are the
+// host's m in [1, 2) and e, and its halving step (m > sqrt 2) is mant >
+// sqrt(2) / 2 (the same float constant halved, exactly), keeping m = mant and
+// e = ef.
 RKV_HD float logf_(float x) {
 #if defined(__HIP_DEVICE_COMPILE__)
-  const bool special = !(x > 0.0f) || x == bits_f32(0x7F800000u);  // NaN, <= 0, +inf
-  const float xin = x;
-  x = special ? 1.0f : x;
-  uint32_t u = f32_bits(x);
-  const bool sub = u < 0x00800000u;  // subnormal
-  x = sub ? x * 8388608.0f : x;
-  u = f32_bits(x);
-  int e = sub ? -23 : 0;
-  e += (int)(u >> 23) - 127;
-  float m = bits_f32((u & 0x007FFFFFu) | 0x3F800000u);
-  const bool hi = m > 1.41421356237309505f;
-  m = hi ? m * 0.5f : m;
-  e += hi ? 1 : 0;
+  const float mant = __builtin_amdgcn_frexp_mantf(x);
+  const int ef = __builtin_amdgcn_frexp_expf(x);
+  const bool hi = mant > 0.5f * 1.41421356237309505f;
+  const float m = hi ? mant : mant + mant;
+  const int e = hi ? ef : ef - 1;
 #else
   if (is_nan(x)) return x + x;
   if (x < 0.0f) return bits_f32(0x7FC00000u);
@@ -188,10 +186,14 @@ RKV_HD float logf_(float x) {
                   ((hfsq - (s * (hfsq + R) + dk * 1.42860682030941723e-06f)) - f);
 #if defined(__HIP_DEVICE_COMPILE__)
   // the host build's early returns, lowest priority first
-  float r = xin == bits_f32(0x7F800000u) ? xin : y;
-  r = xin == 0.0f ? bits_f32(0xFF800000u) : r;
-  r = xin < 0.0f ? bits_f32(0x7FC00000u) : r;
-  return is_nan(xin) ? xin + xin : r;
+  float r = y;
+  if (__builtin_amdgcn_ballot_w64(!(x > 0.0f) || x == bits_f32(0x7F800000u)) != 0) {
+    r = x == bits_f32(0x7F800000u) ? x : r;
+    r = x == 0.0f ? bits_f32(0xFF800000u) : r;
+    r = x < 0.0f ? bits_f32(0x7FC00000u) : r;
+    r = is_nan(x) ? x + x : r;
+  }
+  return r;
 #else
   return y;
 #endif
