@@ -257,7 +257,10 @@ int rkv_workspace_clear_status(void* workspace, size_t workspace_bytes, int64_t 
  * tests and benchmarks (no reference counterpart): *mode_out = 0 for three
  * kernels, 1 for one launch with its whole grid resident, 2 for one launch
  * whose workgroups draw (head, workgroup) tickets in start order (grids of
- * up to two device-fulls, blocks of 64 tokens). */
+ * up to two device-fulls, blocks of 64 tokens), 3 for one resident launch
+ * whose workgroups score up to 4 tiles of 64 blocks each (heads with more
+ * tiles than the device holds workgroups for them, query groups of at most
+ * 4, head_dim <= 128). */
 int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
                     int64_t block_size, int* mode_out);
 

@@ -54,6 +54,7 @@ constexpr float kLog2e = 1.44269504088896341f;
 constexpr int kLine = 8;  // u64 counters per 64-byte hand-off line
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a hand-off wait gives up (default)
 constexpr int64_t kStepMaxTiles = 256;     // tiles per head the one-launch step takes
+constexpr int kStepTiles = 4;              // tiles a workgroup of the one-launch step scores, at most
 
 // Bytes of the one-launch step's hand-off counters: one line per KV head,
 // one for the launch, then one launch counter per tile.
@@ -88,6 +89,7 @@ inline int64_t rows_per_pass(int64_t group, int64_t dim) {
 struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
   int64_t step_workers;  // workgroups per head of the one-launch step
+  int64_t step_tiles;    // tiles its workgroups score, at most (1: one each)
   int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, xbits, total;
 };
 
@@ -104,10 +106,22 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   // workgroups per CU on 256 CUs; 256 for the 16-row kernels, which take
   // more than 256 registers per lane).  The per-tile arrays have a slot per
   // workgroup.
-  const int64_t slots = rows_per_pass(group, dim) == 16 ? 256 : 512;
+  // With more tiles than that, four-row passes up to head_dim 128 keep
+  // min(S / heads, 256) workgroups per head, each scoring up to kStepTiles
+  // tiles (so 128K tokens at block 16 or 512K at block 32 stay one resident
+  // launch); other shapes take one workgroup per tile.
+  const int64_t pass_rows = rows_per_pass(group, dim);
+  const int64_t slots = pass_rows == 16 ? 256 : 512;
   const int64_t want = slots / heads < kStepMaxTiles ? slots / heads : kStepMaxTiles;
   L.step_workers = L.n_tiles > want ? L.n_tiles : want;
-  L.tile_stride = (L.step_workers + 63) / 64 * 64;
+  L.step_tiles = 1;
+  if (L.n_tiles > want && want > 0 && pass_rows == 4 && dim <= 128 &&
+      (L.n_tiles + want - 1) / want <= kStepTiles) {
+    L.step_workers = want;
+    L.step_tiles = (L.n_tiles + want - 1) / want;
+  }
+  const int64_t per_tile = L.step_workers > L.n_tiles ? L.step_workers : L.n_tiles;
+  L.tile_stride = (per_tile + 63) / 64 * 64;
   const int64_t rows = heads * group;
   int64_t off = 0;
   auto take = [&](int64_t bytes) {
@@ -465,6 +479,7 @@ struct DecideArgs {
 
 struct DecideShared {
   float risk[kMaxGroup][kTile];  // the mean reduction reads every row's risks
+  uint64_t tile_bits[kStepTiles];  // several tiles per workgroup: each tile's expanded blocks
   uint64_t wsel[kWaves];         // per wave: OR over its rows of (risk > eps or not finite)
   uint32_t wbad[kWaves];         // per wave: a row's log Z or log C is not finite
   int32_t list[kWaves][kTile];   // per wave: the expanded blocks (tile-relative), ascending
@@ -651,6 +666,20 @@ __device__ __forceinline__ float2 merge_lse_pair(const RowLse& r, uint32_t T, in
   return make_float2(logf_(wave_sum_u(az)) + sz, logf_(wave_sum_u(ac)) + sc);
 }
 
+// Access count of a tile with expanded blocks `bits` (transformers.py:590-594):
+// the count of an expanded block, 1 for a representative; only the prompt's
+// last block can be short.
+__device__ __forceinline__ uint32_t tile_access_count(const DecideArgs& a, int64_t tile,
+                                                      uint64_t bits) {
+  const int64_t N = a.n_blocks, T = a.n_tiles;
+  const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
+  const int64_t nsel = __popcll(bits);
+  int64_t c = (nvalid - nsel) + nsel * a.block;
+  if (tile == T - 1 && ((bits >> (N - 1 - tile * kTile)) & 1ull))
+    c -= a.block - (a.length - (N - 1) * a.block);
+  return (uint32_t)c;
+}
+
 template <bool kFused = false>
 __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
                                                   const DecideLoads& in, DecideShared& sh,
@@ -748,16 +777,101 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   list = sh.list[wave];
   if (wave == 0) {
     if (valid && owner && a.write_mask) a.mask[h * N + b] = sel ? 1 : 0;
-    // access count (transformers.py:590-594): count of an expanded block,
-    // 1 for a representative; only the prompt's last block can be short
-    const int64_t nvalid = N - tile * kTile < kTile ? N - tile * kTile : kTile;
-    const int64_t nsel = __popcll(bits);
-    int64_t c = (nvalid - nsel) + nsel * a.block;
-    if (tile == T - 1 && ((bits >> (N - 1 - tile * kTile)) & 1ull))
-      c -= a.block - (a.length - (N - 1) * a.block);
-    count = (uint32_t)c;
+    count = tile_access_count(a, tile, bits);
   }
   return bits;
+}
+
+// The tiles a one-launch step workgroup scores when its head has more tiles
+// than workgroups (kTiles > 1, four-row passes: one row per wave): tiles
+// wk + m W for m < n, each with this thread's decision inputs (block lane of
+// the tile), this lane's (z, delta, A, th) of its wave's row, and the
+// tile's z row in LDS (the logits of its representative chunk).
+template <int kTiles, int GBM>
+struct TileSet {
+  uint32_t n;
+  DecideLoads din[kTiles];
+  float4 zown[kTiles];
+  float (*z)[GBM][kTile];  // LDS: [m][row][block]
+};
+
+// The decisions of a workgroup's tiles (one-launch step, kTiles > 1): each
+// wave's row's log Z / log C from the head's tagged slots once, then, tile
+// by tile, decide_finish's risk, reduction, fail-safes, anchors, mask and
+// access count (summed into count, thread 0).  bits[m]: tile m's expanded
+// blocks, uniform over the workgroup.
+template <int kTiles, int GBM>
+__device__ __forceinline__ void decide_tiles(const DecideArgs& a, int64_t h, uint32_t wk,
+                                             uint32_t W, const TileSet<kTiles, GBM>& ts,
+                                             DecideShared& sh, const StepStats& ss,
+                                             uint64_t (&bits)[kTiles], uint32_t& count) {
+  const int tid = threadIdx.x, lane = tid % kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);  // wave-uniform
+  const int G = a.group;
+  const int64_t N = a.n_blocks, T = a.n_tiles;
+  const float vmax = a.max_value_norm[h];
+  float lz = 0.0f, lc = 0.0f;
+  bool bad = false;
+  if (wave < G) {
+    const RowLse rl = gather_lse(ss, (h * G + wave) * a.tile_stride, (uint32_t)T, lane);
+    const float2 lzc = merge_lse_pair(rl, (uint32_t)T, lane);
+    lz = lzc.x;
+    lc = lzc.y;
+    if (a.stats_out && wk == 0 && lane == 0) {
+      a.stats_out[(h * G + wave) * 2] = lz;
+      a.stats_out[(h * G + wave) * 2 + 1] = lc;
+    }
+    bad = !is_finite(lz) || !is_finite(lc);
+  }
+  count = 0;
+#pragma unroll
+  for (int m = 0; m < kTiles; ++m) {
+    bits[m] = 0;
+    if ((uint32_t)m >= ts.n) continue;
+    const int64_t tile = wk + (int64_t)m * W;
+    const int64_t b = tile * kTile + lane;
+    const bool valid = b < N;
+    const DecideLoads& in = ts.din[m];
+    uint64_t wsel = 0;
+    if (wave < G) {
+      float r = 0.0f;
+      if (valid) {
+        const float4 zf = ts.zown[m];
+        r = risk_from(zf.x, zf.y, zf.z, zf.w, lz, lc, vmax, in.vnorm);
+        if (a.risk_out) a.risk_out[(h * G + wave) * N + b] = r;
+      }
+      wsel = __ballot(valid && (r > a.eps || !is_finite(r)));
+      if (a.reduction == kMean) sh.risk[wave][lane] = r;
+    }
+    if (lane == 0) {
+      sh.wsel[wave] = wsel;
+      sh.wbad[wave] = bad ? 1u : 0u;
+    }
+    __syncthreads();
+    bool sel;
+    if (a.reduction == kMean) {
+      float acc = sh.risk[0][lane];
+      bool bad_local = !is_finite(acc);
+      for (int g = 1; g < G; ++g) {
+        const float r = sh.risk[g][lane];
+        acc = acc + r;
+        bad_local |= !is_finite(r);
+      }
+      sel = (acc / (float)G) > a.eps || bad_local;
+    } else {
+      sel = (((sh.wsel[0] | sh.wsel[1]) | (sh.wsel[2] | sh.wsel[3])) >> lane) & 1ull;
+    }
+    const bool bad_global = (sh.wbad[0] | sh.wbad[1] | sh.wbad[2] | sh.wbad[3]) != 0;
+    const bool anchored = valid && a.anchor != nullptr && in.anc != 0;
+    sel = (sel || bad_global || anchored) && valid;
+    bits[m] = __ballot(sel);
+    if (tid == 0) sh.tile_bits[m] = bits[m];
+    if (wave == 0) {
+      if (valid && a.write_mask) a.mask[h * N + b] = sel ? 1 : 0;
+      count += tile_access_count(a, tile, bits[m]);
+    }
+    __syncthreads();  // (sh is written again for the next tile)
+  }
 }
 
 // rkv_select's second kernel: decisions only.
@@ -1230,7 +1344,6 @@ __device__ __forceinline__ void mma_combine(const MmaCombine<D, GBM>& cmb, int g
 
 struct StepCtx {
   StepStats stats;
-  const float* mts;               // [row] the tile's max z (LDS)
   Coherent ml, acc, counts;       // partial (m, l), partial acc, tile counts
   uint64_t* control;
   uint16_t* out;                  // (H, G, D) bf16
@@ -1397,12 +1510,14 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
   const int units = G * nq;
   int S = 1;
   while (S * 2 * units <= kThreads && S < 16) S *= 2;
-  // slice 0 also adds the head's access count: its tile counts (at most
+  // slice 0 also adds the head's access count: the counts of its
+  // min(n_tiles, W) workgroups that score distinct tiles (at most
   // kStepMaxTiles <= kThreads) are loaded ahead of the partials, so they
   // land with them
   const bool counting = sx.accessed && m == 0;
+  const int n_counts = (int)da.n_tiles < T ? (int)da.n_tiles : T;
   uint32_t tile_count = 0;
-  if (counting && tid < (int)da.n_tiles)
+  if (counting && tid < n_counts)
     tile_count = sx.counts.load_u32((uint32_t)((h * ts + tid) * 4));
   for (int u0 = 0; u0 < units; u0 += kThreads / S) {
     const int u = u0 + tid / S, sl = tid % S;
@@ -1778,19 +1893,19 @@ __device__ __forceinline__ MmaLoads<D> mma_issue(const AttendArgs& a, int64_t h,
 }
 
 // Wave w's representative chunk (the value means of blocks 16 w .. 16 w + 15
-// of the tile, clamped to the last block) into its stage 0: issued before
-// the decision, so it lands during the wait for the head's LSE partials.
-// Copies (wk >= T) attend no representatives.
+// of the tile, clamped to the last block) into dst (a stage): the first
+// ones are issued before the decision, so they land during the wait for the
+// head's LSE partials.
 template <int D>
-__device__ __forceinline__ void mma_stage_reps(const AttendArgs& a, int64_t h, uint32_t wk,
-                                               MmaStage<D>& stage) {
+__device__ __forceinline__ void mma_stage_reps(const AttendArgs& a, int64_t h, uint32_t tile,
+                                               char* dst) {
   using S = MmaShape<D>;
   constexpr uint32_t NC = S::kNC;
   typedef __attribute__((address_space(3))) void LdsVoid;
-  const uint32_t N = (uint32_t)a.decide.n_blocks, T = (uint32_t)a.decide.n_tiles;
+  const uint32_t N = (uint32_t)a.decide.n_blocks;
   const uint32_t wave = (uint32_t)__builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
-  const uint32_t first = (wk % T) * kTile + 16u * wave;
-  if (wk >= T || first >= N) return;
+  const uint32_t first = tile * kTile + 16u * wave;
+  if (first >= N) return;
   const uint32_t lane = threadIdx.x % kWave;
   const auto vres = buffer_view(a.value_mean + h * (int64_t)N * D, N * (uint32_t)(D * 2));
 #pragma unroll
@@ -1798,7 +1913,7 @@ __device__ __forceinline__ void mma_stage_reps(const AttendArgs& a, int64_t h, u
     const uint32_t p = 64u * u + lane, t = p / NC;
     const uint32_t piece = (p % NC + 32u * NC - 2u * t) % NC;
     const uint32_t row = first + t < N ? first + t : N - 1;
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (LdsVoid*)(stage.bytes[0] + 1024 * u), 16,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(vres, (LdsVoid*)(dst + 1024 * u), 16,
                                              (int)(row * (uint32_t)(D * 2) + piece * 16u), 0,
                                              0, 0);
   }
@@ -1811,10 +1926,15 @@ __device__ __forceinline__ void mma_stage_reps(const AttendArgs& a, int64_t h, u
 // its workgroups; three kernels: the tile's own expanded blocks); the four
 // waves' states merge through LDS into the tile's partial, and (one-launch
 // step) the head's last workgroups merge the partials.
-template <int D, int GBM, bool kFused>
+// kTiles > 1 (one-launch step): the workgroup's tiles are tset's, one
+// representative chunk per tile ahead of the suffix chunks.
+template <int D, int GBM, bool kFused, int kTiles = 1>
 __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShared& dsh,
                                                 MmaCombine<D, GBM>& cmb, const StepCtx* sx,
-                                                const MmaLoads<D>& ld, int64_t h, uint32_t wk) {
+                                                const MmaLoads<D>& ld, int64_t h, uint32_t wk,
+                                                const TileSet<kTiles, GBM>* tset = nullptr) {
+  constexpr bool kMulti = kTiles > 1;
+  static_assert(!kMulti || (kFused && GBM == 4), "several tiles: one-launch step, 4-row passes");
   using S = MmaShape<D>;
   const DecideArgs& da = a.decide;
   const int G = da.group;
@@ -1835,6 +1955,8 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   // (the representative rows into stage 0; the wave's first suffix chunk
   // into the next stage and K registers), so that they land while it waits
   const bool has_reps = primary && tile * kTile + 16u * wave < N;
+  // representative chunks (one per tile; chunk m < R is tile wk + m W's)
+  const uint32_t R = kMulti ? tset->n : 1u;
   const uint32_t ns_chunks = (n_suffix + 15u) / 16u;
   const uint32_t ns_wave = ns_chunks > wave ? (ns_chunks - 1u - wave) / 4u + 1u : 0u;
   const uint32_t cap = (uint32_t)a.suffix_cap;
@@ -1852,11 +1974,12 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   const bool spec = kFused && sx->spec != nullptr && *sx->spec != 0u;
   bool reps_on = has_reps && !spec;
   Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
-  // loop1's chunk 0 is the representative chunk (a no-op without
-  // representatives: nothing issued, nothing folded), chunk j >= 1 the
-  // wave's suffix chunk j - 1, so every chunk keeps its stage and K registers
+  // loop1's chunks m < R are the representative chunks (a no-op without
+  // representatives: nothing issued, nothing folded), chunk j >= R the
+  // wave's suffix chunk j - R, so every chunk keeps its stage and K registers
+  auto rep_tile = [&](uint32_t m) { return kMulti ? wk + m * W : tile; };
   auto issue_suffix = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-    const uint32_t ci = wave + 4u * (j - 1u);
+    const uint32_t ci = wave + 4u * (j - R);
     // suffix row t of the chunk: token wk + (16 ci + t) W (rows past this
     // workgroup's slice repeat its last token and are masked)
     auto token = [&](uint32_t t) {
@@ -1867,9 +1990,30 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
                       [&](uint32_t t) { return token(t) * kts; },
                       [&](uint32_t t) { return token(t) * vts; });
   };
+  // representative chunk m into dst.  With several tiles every chunk of the
+  // ring issues the same loads (the ring's waits count them): the value
+  // means through mma_issue_rows (an empty view past the last block) and
+  // key operands from an empty view (zeros; a representative chunk has
+  // none).  With one tile chunk 0 is issued before the ring and stages the
+  // value means alone.
+  auto issue_reps = [&](uint32_t m, char* dst, Bf16x8 (&kop)[S::kSteps]) {
+    if constexpr (kMulti) {
+      const uint32_t first = rep_tile(m) * kTile + 16u * wave;
+      const auto vres =
+          buffer_view(a.value_mean + h * (int64_t)N * D, first < N ? N * kRowBytes : 0u);
+      mma_issue_rows<D>(buffer_view(a.value_mean, 0u), vres, dst, kop,
+                        [](uint32_t) { return 0u; },
+                        [&](uint32_t t) { return (first + t < N ? first + t : N - 1u) * kRowBytes; });
+    } else {
+      (void)kop;
+      mma_stage_reps<D>(a, h, rep_tile(m), dst);
+    }
+  };
+  // chunks 0 and 1 are issued before the decision
   auto pre_issue = [&]() {
-    if (reps_on) mma_stage_reps<D>(a, h, wk, stage);
-    if (ns_wave > 0) issue_suffix(1u, 1, k1);
+    if (kMulti || reps_on) issue_reps(0u, stage.bytes[0], k0);
+    if (R > 1) issue_reps(1u, stage.bytes[1], k1);
+    else if (ns_wave > 0) issue_suffix(1u, 1, k1);
   };
 
   MmaState<D> st;
@@ -1879,34 +2023,40 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
 #pragma unroll
     for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
   };
-  uint64_t bits = 0;
-  // the representative chunk (if reps_on, first) and the wave's suffix chunks
+  uint64_t bits[kTiles] = {};
+  // the representative chunks (if reps_on, first) and the wave's suffix chunks
   auto loop1 = [&]() {
+    const uint32_t count = R + ns_wave;
     mma_ring<D>(
-        1u + ns_wave, ns_wave > 0 ? 2u : 1u, k0, k1, k2,
+        count, count > 1 ? 2u : 1u, k0, k1, k2,
         [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-          if (j == 0) return;  // no K operands: staged before the decision
-          issue_suffix(j, sidx, kop);
+          if (j < R) issue_reps(j, stage.bytes[sidx], kop);
+          else issue_suffix(j, sidx, kop);
         },
         [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
-          if (j == 0 && !reps_on) return;
+          if (j < R && !(kMulti ? rep_tile(j) * kTile + 16u * wave < N : reps_on)) return;
           float x[4];
           const int g = lane & 15;
-          if (j == 0) {
+          if (j < R) {
             // logit z of block rep_first + 4 (l / 16) + i for query row g
             const int gg = g < gn ? g : 0;
+            const uint32_t rt = rep_tile(j);
+            // (tile j's bits from LDS: a register array indexed by j would
+            // live in scratch)
+            const uint64_t rbits = kMulti ? dsh.tile_bits[j] : bits[0];
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
               const uint32_t tb = 16u * wave + 4u * (uint32_t)(lane >> 4) + i;  // in the tile
-              const uint32_t b = tile * kTile + tb;
-              const bool live = b < N && !((bits >> tb) & 1ull);
+              const uint32_t b = rt * kTile + tb;
+              const bool live = b < N && !((rbits >> tb) & 1ull);
               float z;
-              if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
+              if constexpr (kMulti) z = tset->z[j < kTiles ? j : 0][gg][tb];
+              else if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
               else z = da.zf[(h * G + g0 + gg) * da.z_stride + (b < N ? b : N - 1)].x;
               x[i] = live ? z : kNegInf;
             }
           } else {
-            const uint32_t ci = wave + 4u * (j - 1u);
+            const uint32_t ci = wave + 4u * (j - R);
             const F32x4 s4 = mma_qk<D>(kop, ld.qop);
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
@@ -1974,16 +2124,27 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
   const int32_t* list;
   uint32_t count = 0;
-  bits = decide_finish<kFused>(da, h, tile, ld.din, dsh, nullptr, list, count,
-                               kFused ? &sx->stats : nullptr);
+  if constexpr (kMulti) {
+    list = nullptr;
+    decide_tiles<kTiles, GBM>(da, h, wk, W, *tset, dsh, sx->stats, bits, count);
+  } else {
+    bits[0] = decide_finish<kFused>(da, h, tile, ld.din, dsh, nullptr, list, count,
+                                    kFused ? &sx->stats : nullptr);
+  }
   if constexpr (kFused) {
-    // publish the expanded blocks (a tagged slot) for the head's even split
-    // of pooled token rows: from the last wave, which next polls the head's
-    // masks (loads complete in order, so the first wait after a store also
-    // waits for its write-through; the other waves go on to their chunks)
-    if (tid == kThreads - kWave)
-      sx->xbits.store4((uint32_t)((h * da.tile_stride + tile) * 16),
-                       make_slot((uint32_t)bits, (uint32_t)(bits >> 32), *sx->stats.tag));
+    // publish the expanded blocks (a tagged slot per tile) for the head's
+    // even split of pooled token rows: from the last wave, which next polls
+    // the head's masks (loads complete in order, so the first wait after a
+    // store also waits for its write-through; the other waves go on to
+    // their chunks)
+    if (tid == kThreads - kWave) {
+#pragma unroll
+      for (int m = 0; m < kTiles; ++m)
+        if ((uint32_t)m < R)
+          sx->xbits.store4((uint32_t)((h * da.tile_stride + rep_tile(m)) * 16),
+                           make_slot((uint32_t)bits[m], (uint32_t)(bits[m] >> 32),
+                                     *sx->stats.tag));
+    }
   }
   if (!spec) {
     init_state();
@@ -2019,7 +2180,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
                 [&](uint32_t c) { return (uint32_t)xl[((c << 4) >> lb) - e_first]; });
     }
   } else {
-    run_pages(0u, (uint32_t)__popcll(bits) * B,
+    run_pages(0u, (uint32_t)__popcll(bits[0]) * B,
               [&](uint32_t c) { return tile * kTile + (uint32_t)list[(c << 4) >> lb]; });
   }
 
@@ -2197,12 +2358,21 @@ struct StepArgs {
   uint32_t speculate; // 1: speculate where the previous launch expanded every block
 };
 
+// z of each (row, block) of a workgroup's tiles when it scores several
+// (kTiles > 1): the logits of their representative chunks.
+template <int kTiles, int GBM>
+struct TileZ {
+  float z[kTiles][GBM][kTile];
+};
+template <int GBM>
+struct TileZ<1, GBM> {};
+
 // Every region starts on a 16-byte boundary: the q staging and the combine
 // buffer are read with 16-byte LDS accesses.
-template <int D, int GBM>
+template <int D, int GBM, int kTiles = 1>
 struct StepShared {
   alignas(16) float4 zs[GBM][kTile];  // z, delta, A, th of the tile's (row, block) pairs
-  alignas(16) float mts[GBM];         // the tile's max z per row
+  alignas(16) TileZ<kTiles, GBM> tz;  // several tiles: each tile's z rows
   alignas(16) unsigned long long wsum[kWaves];
   alignas(16) int32_t xl[kTile + 4];
   uint32_t xr[3];
@@ -2229,10 +2399,14 @@ struct StepShared {
 // merge.
 // kTicketed: (head, workgroup) from a start-order ticket instead of blockIdx
 // (grids larger than the device holds at once).
-template <int D, int GBM, bool kTicketed>
+// kTiles > 1: heads with more tiles than workgroups (W < n_tiles, four-row
+// passes): workgroup wk scores tiles wk, wk + W, ... (at most kTiles), one
+// after another, and attend_tile_mma decides and attends all of them.
+template <int D, int GBM, bool kTicketed, int kTiles = 1>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2)))
 void step_kernel(StepArgs s) {
-  __shared__ StepShared<D, GBM> sh;
+  static_assert(kTiles == 1 || (!kTicketed && GBM == 4), "several tiles: resident 4-row step");
+  __shared__ StepShared<D, GBM, kTiles> sh;
   const ScoreArgs& sa = s.score;
   const int G = sa.group, tid = threadIdx.x, lane = tid % kWave;
   const uint32_t W = (uint32_t)s.attend.workers;
@@ -2265,7 +2439,6 @@ void step_kernel(StepArgs s) {
   const StepCtx sx{StepStats{sh.zs, Coherent(s.lse_slots, s.slots_bytes), &sh.tag, &sh.rtag,
                              reinterpret_cast<uint32_t*>(s.control + (int64_t)s.heads * kLine),
                              s.spin},
-                   sh.mts,
                    Coherent(s.attend.part_ml, s.ml_bytes),
                    Coherent(s.attend.part_acc, s.acc_bytes),
                    Coherent(s.counts, s.counts_bytes),
@@ -2283,8 +2456,9 @@ void step_kernel(StepArgs s) {
                    &sh.spec};
   // whether the previous launch on the workspace expanded every block of the
   // head (its workgroup 0 left that launch's tag + 1 here)
+  // (a workgroup of several tiles does not speculate)
   uint64_t prev_full = 0;
-  if (tid == 0 && s.speculate)
+  if (kTiles == 1 && tid == 0 && s.speculate)
     prev_full = __hip_atomic_load(s.control + h * kLine + 2, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
   score_dots<D, GBM>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
@@ -2296,23 +2470,60 @@ void step_kernel(StepArgs s) {
     sh.rtag = sh.tag + s.skew;
     sh.spec = s.speculate && prev_full == epoch + 1u ? 1u : 0u;
   }
-  // the attention's loads that need no statistics land during them
-  const MmaLoads<D> ld = mma_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
+  // the attention's loads that need no statistics land during them (with
+  // several tiles after the last tile's statistics: the query operands
+  // would stay live through the later tiles' scores)
+  MmaLoads<D> ld;
+  if constexpr (kTiles == 1) ld = mma_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
   __syncthreads();
-  score_stats(
-      sa, tile, sh.u.score.sdot, sh.u.score.pdot,
-      [&](int g, bool, float4 zf) { sh.zs[g][lane] = zf; },
-      [&](int g, float4 part) {
-        sh.mts[g] = part.x;
-        const uint32_t at = (uint32_t)(((h * G + g) * sa.tile_stride + tile) * 2 * 16);
-        sx.stats.slots.store4(at, make_slot(f32_bits(part.x), f32_bits(part.y), sh.tag));
-        sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
-      });
-  __syncthreads();
-  // (the score arrays are dead: the representative rows and the first suffix
-  // chunks stage over them and land while the decision waits for the head's
-  // LSE partials)
-  attend_tile_mma<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk);
+  // a tile's LSE partials out as two tagged slots
+  auto publish = [&](int64_t t, int g, float4 part) {
+    const uint32_t at = (uint32_t)(((h * G + g) * sa.tile_stride + t) * 2 * 16);
+    sx.stats.slots.store4(at, make_slot(f32_bits(part.x), f32_bits(part.y), sh.tag));
+    sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
+  };
+  if constexpr (kTiles == 1) {
+    score_stats(
+        sa, tile, sh.u.score.sdot, sh.u.score.pdot,
+        [&](int g, bool, float4 zf) { sh.zs[g][lane] = zf; },
+        [&](int g, float4 part) { publish(tile, g, part); });
+    __syncthreads();
+    // (the score arrays are dead: the representative rows and the first
+    // suffix chunks stage over them and land while the decision waits for
+    // the head's LSE partials)
+    attend_tile_mma<D, GBM, true>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk);
+  } else {
+    const uint32_t T = (uint32_t)s.attend.decide.n_tiles;
+    const int wave = __builtin_amdgcn_readfirstlane(tid / kWave);
+    TileSet<kTiles, GBM> tset;
+    tset.n = (T - (uint32_t)wk + W - 1u) / W;
+    tset.z = sh.tz.z;
+#pragma unroll
+    for (int m = 0; m < kTiles; ++m) tset.zown[m] = make_float4(kNegInf, 0.0f, 0.0f, 0.0f);
+#pragma unroll
+    for (int m = 0; m < kTiles; ++m) {
+      if ((uint32_t)m >= tset.n) break;
+      const int64_t t = wk + (int64_t)m * W;
+      // (score_dots' first barrier orders the previous tile's reads of the
+      // score arrays before this tile's writes)
+      if (m > 0) score_dots<D, GBM>(sa, h, t, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+      score_stats(
+          sa, t, sh.u.score.sdot, sh.u.score.pdot,
+          [&](int g, bool, float4 zf) {
+            sh.tz.z[m][g][lane] = zf.x;
+            if (g == wave) tset.zown[m] = zf;
+          },
+          [&](int g, float4 part) { publish(t, g, part); });
+    }
+    ld = mma_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
+    tset.din[0] = ld.din;
+#pragma unroll
+    for (int m = 1; m < kTiles; ++m)
+      if ((uint32_t)m < tset.n) tset.din[m] = decide_issue<false>(s.attend.decide, h, wk + (int64_t)m * W);
+    __syncthreads();
+    attend_tile_mma<D, GBM, true, kTiles>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk,
+                                          &tset);
+  }
 }
 
 // ---------------------------------------------------------------------------
@@ -2614,26 +2825,33 @@ int launch_attend(const AttendArgs& aa, int64_t rows, dim3 grid, hipStream_t str
 constexpr int kStepMaxDim = 160;
 
 template <int D, int GBM>
-int launch_step_g(const StepArgs& sa, bool ticketed, dim3 grid, hipStream_t stream) {
+int launch_step_g(const StepArgs& sa, bool ticketed, bool multi, dim3 grid, hipStream_t stream) {
+  if constexpr (GBM == 4 && D <= 128) {
+    if (multi) {
+      step_kernel<D, GBM, false, kStepTiles><<<grid, dim3(kThreads), 0, stream>>>(sa);
+      return check_launch("step_kernel");
+    }
+  }
+  if (multi) return set_error(kUnsupported, "rkv_decode: no several-tile step for this shape");
   if (ticketed) step_kernel<D, GBM, true><<<grid, dim3(kThreads), 0, stream>>>(sa);
   else step_kernel<D, GBM, false><<<grid, dim3(kThreads), 0, stream>>>(sa);
   return check_launch("step_kernel");
 }
 
 template <int D>
-int launch_step_d(const StepArgs& sa, int64_t rows, bool ticketed, dim3 grid,
+int launch_step_d(const StepArgs& sa, int64_t rows, bool ticketed, bool multi, dim3 grid,
                   hipStream_t stream) {
   constexpr int CH = D / 16;
   constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
   if constexpr (D <= kStepMaxDim) {
     switch (rows) {
       case 4:
-        return launch_step_g<D, 4>(sa, ticketed, grid, stream);
+        return launch_step_g<D, 4>(sa, ticketed, multi, grid, stream);
       case 8:
-        if constexpr (CAP >= 8) return launch_step_g<D, 8>(sa, ticketed, grid, stream);
+        if constexpr (CAP >= 8) return launch_step_g<D, 8>(sa, ticketed, multi, grid, stream);
         break;
       default:
-        if constexpr (CAP >= 16) return launch_step_g<D, 16>(sa, ticketed, grid, stream);
+        if constexpr (CAP >= 16) return launch_step_g<D, 16>(sa, ticketed, multi, grid, stream);
         break;
     }
   }
@@ -2647,7 +2865,7 @@ thread_local int g_decode_path = 0;
 
 // Workgroups of step_kernel<D, GBM> the current device holds at once (its
 // occupancy per CU times the CUs), 0 if unknown.
-template <int D, int GBM>
+template <int D, int GBM, int kTiles = 1>
 int64_t step_resident() {  // (the ticketed build's occupancy is the same: same resources)
   static std::atomic<int> of_dev[64];  // per device; 0 = not asked yet
   int dev = -1;
@@ -2656,7 +2874,7 @@ int64_t step_resident() {  // (the ticketed build's occupancy is the same: same 
   if (n == 0) {
     int cus = 0, per_cu = 0;
     if (hipDeviceGetAttribute(&cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel<D, GBM, false>,
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&per_cu, step_kernel<D, GBM, false, kTiles>,
                                                      kThreads, 0) !=
             hipSuccess)
       return 0;
@@ -2666,12 +2884,16 @@ int64_t step_resident() {  // (the ticketed build's occupancy is the same: same 
   return n;
 }
 
-// The residency of the step kernel launch_step_d<D> takes for `rows` rows.
+// The residency of the step kernel launch_step_d<D> takes for `rows` rows
+// (multi: the several-tile build).
 template <int D>
-int64_t step_resident_d(int64_t rows) {
+int64_t step_resident_d(int64_t rows, bool multi) {
   constexpr int CH = D / 16;
   constexpr int CAP = (64 / CH) >= 16 ? 16 : ((64 / CH) >= 8 ? 8 : 4);
   if constexpr (D <= kStepMaxDim) {
+    if constexpr (D <= 128)
+      if (rows == 4 && multi) return step_resident<D, 4, kStepTiles>();
+    if (multi) return 0;
     if (rows == 4) return step_resident<D, 4>();
     if constexpr (CAP >= 8)
       if (rows == 8) return step_resident<D, 8>();
@@ -2701,10 +2923,12 @@ StepMode step_mode(const SelectParams& p, const Layout& L, const DecodeBuffers& 
         hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8)))
     return kSplit;
   int64_t resident = 0;
-  RKV_DISPATCH_DIM(p.dim, D, resident = step_resident_d<D>(rows));
+  const bool multi = L.step_tiles > 1;
+  RKV_DISPATCH_DIM(p.dim, D, resident = step_resident_d<D>(rows, multi));
   const int64_t grid = p.heads * L.step_workers;
   if (grid <= resident) return kResident;
-  if (p.block >= 64 && L.step_workers <= resident && grid <= 2 * resident) return kTicketed;
+  if (!multi && p.block >= 64 && L.step_workers <= resident && grid <= 2 * resident)
+    return kTicketed;
   return kSplit;
 }
 
@@ -2742,7 +2966,7 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, 
   mark(0, p.stream);
   int rc = kUnsupported;
   RKV_DISPATCH_DIM(p.dim, D,
-                   rc = launch_step_d<D>(s, rows, ticketed,
+                   rc = launch_step_d<D>(s, rows, ticketed, L.step_tiles > 1,
                                          dim3((unsigned)L.step_workers, (unsigned)p.heads),
                                          p.stream));
   mark(1, p.stream);
@@ -3094,7 +3318,8 @@ extern "C" int rkv_set_speculation(int enable) {
 
 // Which path rkv_decode takes for a shape on the current device (with an
 // aligned output): 0 = three kernels, 1 = one launch with the grid resident,
-// 2 = one launch with start-order tickets.
+// 2 = one launch with start-order tickets, 3 = one resident launch whose
+// workgroups score several tiles each.
 extern "C" int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
                                int64_t block_size, int* mode_out) {
   clear_error();
@@ -3110,7 +3335,8 @@ extern "C" int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_
   const Layout L = make_layout(heads, group, dim, n_blocks);
   DecodeBuffers b{};
   b.output = reinterpret_cast<void*>(uintptr_t(256));
-  *mode_out = g_decode_path == 0 ? (int)step_mode(p, L, b) : 0;
+  const StepMode mode = g_decode_path == 0 ? step_mode(p, L, b) : kSplit;
+  *mode_out = mode == kResident && L.step_tiles > 1 ? 3 : (int)mode;
   return kOk;
 }
 

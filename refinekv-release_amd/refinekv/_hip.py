@@ -363,13 +363,14 @@ def check_workspace(workspace):
             "not all running at once); outputs computed with this workspace are invalid")
 
 
-PLAN_NAMES = {0: "split", 1: "step", 2: "step-ticketed"}
+PLAN_NAMES = {0: "split", 1: "step", 2: "step-ticketed", 3: "step-tiles"}
 
 
 def decode_plan(heads, group, dim, n_blocks, block):
     """The path rkv_decode takes for a shape on the current device: "split"
-    (three kernels), "step" (one launch, grid resident) or "step-ticketed"
-    (one launch, workgroups mapped by start-order tickets)."""
+    (three kernels), "step" (one launch, grid resident), "step-ticketed"
+    (one launch, workgroups mapped by start-order tickets) or "step-tiles"
+    (one resident launch, each workgroup scoring several tiles)."""
     mode = ctypes.c_int()
     _check(lib().rkv_decode_plan(heads, group, dim, n_blocks, block, ctypes.byref(mode)),
            "rkv_decode_plan")

@@ -65,7 +65,8 @@ def test_workspace_size_covers_layout(lib):
     from refinekv import _hip
 
     for heads, group, dim, n in ((8, 4, 128, 4096), (4, 7, 128, 1024), (2, 16, 64, 3),
-                                 (1, 1, 256, 1)):
+                                 (1, 1, 256, 1), (8, 4, 128, 8192), (8, 4, 128, 16384),
+                                 (3, 4, 128, 11250), (8, 8, 128, 16384), (8, 4, 160, 16384)):
         layout = _hip.workspace_layout(heads, group, dim, n)
         assert _hip.workspace_bytes(heads, group, dim, n) == layout["total"]
         assert layout["n_tiles"] == -(-n // 64)
@@ -87,8 +88,12 @@ def test_workspace_size_covers_layout(lib):
         assert layout["total"] - layout["xbits"] >= heads * ts * 16
         # the one-launch step's workgroups per head: every tile, topped up
         # with copies to min(S / heads, 256), each with a per-tile slot (S =
-        # 256 for the 16-row kernels, which hold one workgroup per CU)
+        # 256 for the 16-row kernels, which hold one workgroup per CU); with
+        # more tiles than that, four-row passes up to head_dim 128 keep
+        # min(S / heads, 256) workgroups scoring up to 4 tiles each
         want = min((256 if rows_per_pass(group, dim) == 16 else 512) // heads, 256)
-        assert layout["step_workers"] == max(tiles, want)
-        assert tiles <= layout["step_workers"] <= ts
+        several = (tiles > want and rows_per_pass(group, dim) == 4 and dim <= 128
+                   and -(-tiles // want) <= 4)
+        assert layout["step_workers"] == (want if several else max(tiles, want))
+        assert tiles <= ts and layout["step_workers"] <= ts
     assert _hip.workspace_bytes(0, 4, 128, 10) == 0

@@ -330,9 +330,12 @@ DECODE_CASES = [
         # hand-offs), and more than the step takes (the three kernels run)
         (1, 4, 128, 16, 140000, "max", 0.01, 0.02),
         (1, 2, 64, 16, 310000, "any", 0.01, 0.01),
-        # at most 256 tiles per head, but 3 x 176 tiles more workgroups than
-        # the device holds at once (the three kernels run)
+        # 176 tiles per head over 170 workgroups per head: the step's first
+        # 6 workgroups score 2 tiles each, the rest one (the last one short)
         (3, 4, 128, 16, 180000, "any", 0.01, 0.02),
+        # several tiles per workgroup, a 2-query group: 88 tiles per head
+        # over 32 workgroups (3, 3, ..., 2 tiles each)
+        (16, 2, 64, 16, 90000, "mean", 0.01, 0.02),
     ]
 ]
 
@@ -515,11 +518,12 @@ def test_headline_shape_128k(hip, oracle_lib):
 
 def test_long_context_512k(hip, oracle_lib):
     """The sweep's longest context (H_kv 8, G 4, d 128, 524288 prompt tokens,
-    B 32: 256 tiles per head, 2048 workgroups, more than the device holds at
-    once, so the three kernels run): masks equal the oracle's selection over
-    this summary, outputs within tolerance of the oracle's, and nothing
-    touched the step's counters.  (The
-    summary kernel itself is pinned bit for bit at 131072 tokens.)"""
+    B 32: 256 tiles per head, four times the workgroups the device holds for
+    a head, so each of the step's 64 workgroups per head scores 4 tiles):
+    masks equal the oracle's selection over this summary and outputs are
+    within tolerance of the oracle's, for the one-launch step and for the
+    three kernels.  (The summary kernel itself is pinned bit for bit at
+    131072 tokens.)"""
     prompt, block, eps = 524288, 32, 0.01
     inp = _decode_case(8, 4, 128, block, prompt, 0.01, suffix=17, seed=5)
     cfg = RefineKVConfig(backend="hip", eps=eps, block_size=block)
@@ -532,14 +536,21 @@ def test_long_context_512k(hip, oracle_lib):
                                             gc.bf16_bits(inp["suffix_keys"]),
                                             gc.bf16_bits(inp["suffix_values"]), eps, "any")
     assert 0.005 < mask.mean() < 0.1
-    ws = {}
-    res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
-                           inp["suffix_values"].to(DEV), cfg, workspace=ws, return_selected=True)
-    torch.cuda.synchronize()
-    assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask)
-    assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
-                        torch.from_numpy(out).to(torch.bfloat16).float().numpy())
-    assert assert_control_clean(hip, ws) == 0
+    assert hip.decode_plan(8, 4, 128, summary.num_blocks, block) == "step-tiles"
+    for path in ("step", "split"):
+        hip.set_decode_path(path)
+        try:
+            ws = {}
+            res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
+                                   inp["suffix_values"].to(DEV), cfg, workspace=ws,
+                                   return_selected=True)
+            torch.cuda.synchronize()
+            assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask), path
+            assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
+                                torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+        finally:
+            hip.set_decode_path("step")
+        assert assert_control_clean(hip, ws) == (1 if path == "step" else 0)
 
 
 def _headline_shape_128k(hip, oracle_lib):
@@ -653,14 +664,26 @@ def test_config3_op_qwen_64k(hip, oracle_lib):
 
 
 def test_two_device_fulls_step_512k_block64(hip, oracle_lib):
-    """8 KV heads, 524288 prompt tokens, block 64: 128 tiles per head, 1024
+    """8 KV heads of 6 query heads (eight-row passes, which score one tile
+    per workgroup), 524288 prompt tokens, block 64: 128 tiles per head, 1024
     workgroups, twice what the device holds at once, so the one-launch step
     maps workgroups to (head, tile) by start-order tickets.  Two launches on
     one workspace (the tickets and tags of the second follow the first)."""
     n_blocks = 524288 // 64
-    assert hip.decode_plan(8, 4, 128, n_blocks, 64) == "step-ticketed"
-    _op_case(hip, oracle_lib, heads=8, group=4, block=64, prompt=524288, reduction="any",
+    assert hip.decode_plan(8, 6, 128, n_blocks, 64) == "step-ticketed"
+    _op_case(hip, oracle_lib, heads=8, group=6, block=64, prompt=524288, reduction="any",
              eps=0.01, spikes=0.02, suffix=17, anchors=0, seed=23, paths=("step",), repeats=2)
+
+
+def test_several_tiles_per_workgroup_128k_block16(hip, oracle_lib):
+    """The headline shape at block 16: 128 tiles per head, twice the 64
+    workgroups per head the device holds, so each workgroup of the one-launch
+    step scores 2 tiles.  Both paths, two launches on one workspace, with
+    prompt anchors."""
+    n_blocks = 131072 // 16
+    assert hip.decode_plan(8, 4, 128, n_blocks, 16) == "step-tiles"
+    _op_case(hip, oracle_lib, heads=8, group=4, block=16, prompt=131072, reduction="any",
+             eps=0.01, spikes=0.02, suffix=33, anchors=16, seed=24, repeats=2)
 
 
 # ---------------------------------------------------------------------------

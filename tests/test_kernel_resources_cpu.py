@@ -95,7 +95,7 @@ def test_no_scratch_in_the_kernels_of_common_shapes(kernels):
     only in the 16-row builds (GQA groups above 8) and the 8-row step at
     head_dim 128, whose two four-row score passes keep both passes' loads
     live; every other decode and summary kernel runs without it."""
-    allowed = {("step_kernel", (128, 8, 0))}
+    allowed = {("step_kernel", (128, 8, 0, 1))}
     for family in ("step_kernel", "attend_kernel", "score_kernel", "summary_kernel"):
         for args, res in _instances(kernels, family):
             rows16 = family in ("step_kernel", "attend_kernel") and args[1] == 16
