@@ -293,68 +293,48 @@ __device__ __forceinline__ void lds_read(const float* p, float (&out)[N]) {
 }
 
 // The selection dot products of tile `tile` of head h for every query row:
-// sdot[g][b] = q_g . k_mean_b and pdot[g][b] = bf16(q_g^2) . ellipsoid_b
-// (DSUM), b tile-relative; ends with a barrier.  qstage holds
-// score_q_floats(G, D) floats of LDS.  kMaxG bounds the group (the step
-// kernel's rows per pass), so the four-row loop is compiled only where
-// groups above four can reach it.
-template <int D, int kMaxG = kMaxGroup>
-__device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_t tile,
-                                           float* sdot, float* pdot, float* qstage) {
+// A tile's summary rows as loaded: this thread's key-mean and ellipsoid
+// slices of its blocks (one per pass).
+template <int D>
+struct ScoreRaw {
+  RawBf16<Dots<D>::kCh> k[Dots<D>::kPasses], e[Dots<D>::kPasses];
+};
+
+// The summary loads of tile `tile` of head h (blocks past the end read block
+// N - 1; their results are discarded).
+template <int D>
+__device__ __forceinline__ void score_load(const ScoreArgs& a, int64_t h, int64_t tile,
+                                           ScoreRaw<D>& raw) {
   using S = Dots<D>;
   constexpr int CH = S::kCh;
-  const int G = a.group;
   const int64_t N = a.n_blocks;
   const int tid = threadIdx.x;
   const int c = tid % S::kLanes, sub = tid / S::kLanes;
-
-  constexpr int QW = CH + kQPad;          // padded slice
-  constexpr int QS = S::kLanes * QW;      // padded row
-  float* qs = qstage;                     // [G][QS] bf16(q)
-  float* q2s = qs + G * QS;               // [G][QS] bf16(q^2)
-  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
   const int64_t hs = h % a.summary_heads;  // the summaries' head
-  const int first = tid, step = kThreads;
-  // The query words first (the staging below waits only for them: loads
-  // complete in order), then every load of the tile.  Blocks past the end
-  // read block N-1 (their results are discarded).
-  uint32_t qw[kQWords];
-#pragma unroll
-  for (int k = 0; k < kQWords; ++k) {
-    const int i = first + k * step;
-    qw[k] = q32[i < G * D / 2 ? i : 0];
-  }
-
-  RawBf16<CH> kraw[S::kPasses], eraw[S::kPasses];
 #pragma unroll
   for (int ps = 0; ps < S::kPasses; ++ps) {
     int64_t b = tile * kTile + ps * S::kPerPass + sub;
     b = b < N ? b : N - 1;
     const int64_t o = (hs * N + b) * D + c * CH;
-    kraw[ps] = load_raw<CH>(a.key_mean + o);
-    eraw[ps] = load_raw<CH>(a.ellipsoid + o);
+    raw.k[ps] = load_raw<CH>(a.key_mean + o);
+    raw.e[ps] = load_raw<CH>(a.ellipsoid + o);
   }
-  // The query words are used here, after the summary loads are issued: a
-  // query load sunk into the staging branch below would be issued after
-  // them and wait for all of them.
-#pragma unroll
-  for (int k = 0; k < kQWords; ++k) asm volatile("" : "+v"(qw[k]));
-  auto stage = [&](int i, uint32_t u) {
-    const float q0 = bits_f32(u << 16), q1 = bits_f32(u & 0xFFFF0000u);
-    const int g = 2 * i / D, e = 2 * i % D;  // element pair e, e + 1 of row g
-    const int at = g * QS + (e / CH) * QW + e % CH;
-    qs[at] = q0;
-    qs[at + 1] = q1;
-    q2s[at] = round_bf16(q0 * q0);
-    q2s[at + 1] = round_bf16(q1 * q1);
-  };
-#pragma unroll
-  for (int k = 0; k < kQWords; ++k) {
-    const int i = first + k * step;
-    if (i < G * D / 2) stage(i, qw[k]);
-  }
-  for (int i = first + kQWords * step; i < G * D / 2; i += step) stage(i, q32[i]);
-  __syncthreads();
+}
+
+// The dot products of a tile from its loaded rows and the staged q (see
+// score_dots); ends with a barrier.
+template <int D, int kMaxG = kMaxGroup>
+__device__ __forceinline__ void score_from(const ScoreArgs& a, const ScoreRaw<D>& raw,
+                                           float* sdot, float* pdot, const float* qstage) {
+  using S = Dots<D>;
+  constexpr int CH = S::kCh;
+  const int G = a.group;
+  const int tid = threadIdx.x;
+  const int c = tid % S::kLanes, sub = tid / S::kLanes;
+  constexpr int QW = CH + kQPad;          // padded slice
+  constexpr int QS = S::kLanes * QW;      // padded row
+  const float* qs = qstage;               // [G][QS] bf16(q)
+  const float* q2s = qs + G * QS;         // [G][QS] bf16(q^2)
 
   // Rows g0 .. g0+3: a lambda so that the common case (G <= 4, one call)
   // waits for each pass's loads just before it, not for both passes first.
@@ -370,8 +350,8 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
 #pragma unroll
     for (int ps = 0; ps < S::kPasses; ++ps) {
       float km[CH], el[CH];
-      unpack(kraw[ps], km);
-      unpack(eraw[ps], el);
+      unpack(raw.k[ps], km);
+      unpack(raw.e[ps], el);
       float sv[4], pv[4];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
@@ -405,6 +385,60 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
     for (int g0 = 0; g0 < G; g0 += 4) four_rows(g0);
   }
   __syncthreads();
+}
+
+// sdot[g][b] = q_g . k_mean_b and pdot[g][b] = bf16(q_g^2) . ellipsoid_b
+// (DSUM), b tile-relative; ends with a barrier.  qstage holds
+// score_q_floats(G, D) floats of LDS (q and bf16(q^2), staged here; they
+// stay for score_from of further tiles).  kMaxG bounds the group (the step
+// kernel's rows per pass), so the four-row loop is compiled only where
+// groups above four can reach it.
+template <int D, int kMaxG = kMaxGroup>
+__device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_t tile,
+                                           float* sdot, float* pdot, float* qstage) {
+  using S = Dots<D>;
+  constexpr int CH = S::kCh;
+  const int G = a.group;
+  const int tid = threadIdx.x;
+
+  constexpr int QW = CH + kQPad;          // padded slice
+  constexpr int QS = S::kLanes * QW;      // padded row
+  float* qs = qstage;                     // [G][QS] bf16(q)
+  float* q2s = qs + G * QS;               // [G][QS] bf16(q^2)
+  const uint32_t* q32 = reinterpret_cast<const uint32_t*>(a.query + h * G * D);
+  const int first = tid, step = kThreads;
+  // The query words first (the staging below waits only for them: loads
+  // complete in order), then every load of the tile.
+  uint32_t qw[kQWords];
+#pragma unroll
+  for (int k = 0; k < kQWords; ++k) {
+    const int i = first + k * step;
+    qw[k] = q32[i < G * D / 2 ? i : 0];
+  }
+  ScoreRaw<D> raw;
+  score_load<D>(a, h, tile, raw);
+  // The query words are used here, after the summary loads are issued: a
+  // query load sunk into the staging branch below would be issued after
+  // them and wait for all of them.
+#pragma unroll
+  for (int k = 0; k < kQWords; ++k) asm volatile("" : "+v"(qw[k]));
+  auto stage = [&](int i, uint32_t u) {
+    const float q0 = bits_f32(u << 16), q1 = bits_f32(u & 0xFFFF0000u);
+    const int g = 2 * i / D, e = 2 * i % D;  // element pair e, e + 1 of row g
+    const int at = g * QS + (e / CH) * QW + e % CH;
+    qs[at] = q0;
+    qs[at + 1] = q1;
+    q2s[at] = round_bf16(q0 * q0);
+    q2s[at + 1] = round_bf16(q1 * q1);
+  };
+#pragma unroll
+  for (int k = 0; k < kQWords; ++k) {
+    const int i = first + k * step;
+    if (i < G * D / 2) stage(i, qw[k]);
+  }
+  for (int i = first + kQWords * step; i < G * D / 2; i += step) stage(i, q32[i]);
+  __syncthreads();
+  score_from<D, kMaxG>(a, raw, sdot, pdot, qstage);
 }
 
 // z, delta, the risk's delta-only factors and the tile's LSE partials from
@@ -2500,13 +2534,17 @@ void step_kernel(StepArgs s) {
     tset.z = sh.tz.z;
 #pragma unroll
     for (int m = 0; m < kTiles; ++m) tset.zown[m] = make_float4(kNegInf, 0.0f, 0.0f, 0.0f);
+    // tile m + 1's summary loads are issued before tile m's statistics (and
+    // land during them); its dot products follow the statistics (a barrier
+    // first: the statistics read the score arrays), from q as staged for
+    // tile 0
+    ScoreRaw<D> next;
 #pragma unroll
     for (int m = 0; m < kTiles; ++m) {
       if ((uint32_t)m >= tset.n) break;
       const int64_t t = wk + (int64_t)m * W;
-      // (score_dots' first barrier orders the previous tile's reads of the
-      // score arrays before this tile's writes)
-      if (m > 0) score_dots<D, GBM>(sa, h, t, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+      const bool more = (uint32_t)m + 1u < tset.n;
+      if (more) score_load<D>(sa, h, t + W, next);
       score_stats(
           sa, t, sh.u.score.sdot, sh.u.score.pdot,
           [&](int g, bool, float4 zf) {
@@ -2514,6 +2552,10 @@ void step_kernel(StepArgs s) {
             if (g == wave) tset.zown[m] = zf;
           },
           [&](int g, float4 part) { publish(t, g, part); });
+      if (more) {
+        __syncthreads();
+        score_from<D, GBM>(sa, next, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+      }
     }
     ld = mma_issue<D, GBM, true>(s.attend, h, (uint32_t)wk);
     tset.din[0] = ld.din;
