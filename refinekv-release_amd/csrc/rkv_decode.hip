@@ -1386,7 +1386,8 @@ struct StepCtx {
   unsigned long long* wsum;       // kWaves LDS words
   uint64_t* base;                 // LDS: epoch * n_tiles (thread 0's copy)
   Coherent xbits;                 // (H, tile_stride) expanded-block masks
-  int32_t* xl;                    // LDS: blocks of this tile's expanded-row share
+  int32_t* xl;                    // LDS: blocks of this workgroup's expanded-row share
+  uint32_t xl_cap;                // xl's entries
   uint32_t* xr;                   // LDS: the share's first row and row count
   int heads;
   uint32_t skew;                  // 0; a test's nonzero value makes every wait run out
@@ -1407,14 +1408,16 @@ __device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
   return v;
 }
 
-// Wave 0 of a step workgroup: this tile's share of its head's expanded
-// token rows.  The head's expanded blocks, in (tile, block) order, give B
-// rows each (R rows in all) and tile w attends rows [w R / T, (w + 1) R / T),
-// so every tile of the head gets the same number of rows (+-1) wherever the
-// expanded blocks sit.  From the T published masks: xl[i] = the block (index
-// in the head) of ordinal e0 + i for the ordinals the share touches, xr =
-// (first row, row count).  Integer arithmetic only: every tile sees the same
-// split.
+// One wave of a step workgroup: this workgroup's share of its head's
+// expanded token rows.  The head's expanded blocks, in (tile, block) order,
+// give B rows each (R rows in all) and workgroup w of the W attends rows
+// [w R / W, (w + 1) R / W), so every workgroup of the head gets the same
+// number of rows (+-1) wherever the expanded blocks sit.  From the T
+// published masks: xl[i] = the block (index in the head) of ordinal e0 + i
+// for the ordinals the share touches, xr = (first row, row count).  Integer
+// arithmetic only: every workgroup sees the same split.  A share touches at
+// most R / (W B) + 2 <= 64 ceil(T / W) + 2 blocks (R <= 64 T B), which
+// sx.xl_cap covers (an entry past it would set the error word instead).
 __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
                                uint32_t W, uint32_t tile, int lb, uint64_t last_bits,
                                uint32_t N) {
@@ -1479,8 +1482,12 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
       const uint32_t f = (uint32_t)__builtin_amdgcn_readlane((int)first[k], src);
       if ((m >> lane) & 1ull) {
         const uint32_t e = f + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-        if (e >= e0 && e < e1)
-          sx.xl[e - e0] = (int32_t)((uint32_t)(k * kWave + src) * kTile + (uint32_t)lane);
+        if (e >= e0 && e < e1) {
+          if (e - e0 < sx.xl_cap)
+            sx.xl[e - e0] = (int32_t)((uint32_t)(k * kWave + src) * kTile + (uint32_t)lane);
+          else
+            __hip_atomic_fetch_or(sx.stats.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
       }
     }
   }
@@ -2209,9 +2216,11 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
     }
     if (!spec || again) {
       const int32_t* xl = sx->xl;
-      const uint32_t x_first = sx->xr[0], e_first = x_first >> lb;
-      run_pages(x_first, sx->xr[1],
-                [&](uint32_t c) { return (uint32_t)xl[((c << 4) >> lb) - e_first]; });
+      const uint32_t x_first = sx->xr[0], e_first = x_first >> lb, last_e = sx->xl_cap - 1u;
+      run_pages(x_first, sx->xr[1], [&](uint32_t c) {
+        const uint32_t e = ((c << 4) >> lb) - e_first;  // < xl_cap (expanded_share)
+        return (uint32_t)xl[e < last_e ? e : last_e];
+      });
     }
   } else {
     run_pages(0u, (uint32_t)__popcll(bits[0]) * B,
@@ -2408,7 +2417,9 @@ struct StepShared {
   alignas(16) float4 zs[GBM][kTile];  // z, delta, A, th of the tile's (row, block) pairs
   alignas(16) TileZ<kTiles, GBM> tz;  // several tiles: each tile's z rows
   alignas(16) unsigned long long wsum[kWaves];
-  alignas(16) int32_t xl[kTile + 4];
+  // a workgroup's expanded-row share: at most 64 ceil(T / W) + 2 blocks,
+  // ceil(T / W) <= kTiles
+  alignas(16) int32_t xl[kTiles * kTile + 4];
   uint32_t xr[3];
   uint64_t base;
   uint32_t tag, rtag;
@@ -2484,6 +2495,7 @@ void step_kernel(StepArgs s) {
                    &sh.base,
                    Coherent(s.xbits, s.xbits_bytes),
                    sh.xl,
+                   (uint32_t)(kTiles * kTile + 4),
                    sh.xr,
                    s.heads,
                    s.skew,

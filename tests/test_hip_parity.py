@@ -336,6 +336,9 @@ DECODE_CASES = [
         # several tiles per workgroup, a 2-query group: 88 tiles per head
         # over 32 workgroups (3, 3, ..., 2 tiles each)
         (16, 2, 64, 16, 90000, "mean", 0.01, 0.02),
+        # the same with every block expanded: a workgroup's share of the
+        # head's expanded rows spans up to 178 blocks (64 ceil(T / W) + 2)
+        (16, 2, 64, 16, 90000, "any", 0.0, 0.02),
     ]
 ]
 
