@@ -590,28 +590,32 @@ __device__ __forceinline__ DecideLoads decide_issue(const DecideArgs& a, int64_t
 }
 
 // Self-validating hand-off slots of the one-launch step: 16 bytes {a, b,
-// tag, check(a, b, tag)} written with one coherent store, tag = the launch's
-// epoch + 1 (a zero-filled slot is never valid).  A reader accepts a slot
-// only when it carries this launch's tag and a matching check, so it needs
-// no counter to know that the data has landed, and a stale or torn read is
-// simply read again.
-__host__ __device__ inline uint32_t slot_check(uint32_t a, uint32_t b, uint32_t tag) {
-  uint32_t x = (a * 0x9E3779B1u) ^ ((b + 0x7F4A7C15u) * 0x85EBCA77u) ^ (tag * 0xC2B2AE3Du);
-  x ^= x >> 15;
-  x *= 0x2C1B3C6Du;
-  x ^= x >> 12;
-  x *= 0x297A2D39u;
-  x ^= x >> 15;
-  return x;
+// tag, check} written with one coherent store, tag = the launch's epoch + 1
+// (a zero-filled slot is never valid) and check = a ^ rotl(b, 13) ^ mix(tag),
+// mix(tag) = tag * an odd constant (a bijection: two launches never share a
+// mix).  A reader accepts a slot only when it carries this launch's tag and
+// a matching check, so it needs no counter to know that the data has landed,
+// and a stale or torn read is simply read again.  A torn read mixes words
+// of this launch's store and of an earlier one: with this launch's tag and
+// check, an older a or b (not both) fails unless it equals the new one;
+// with an older check, the launches' mixes differ and the check fails
+// unless the older words' differences cancel them exactly.  The mix is
+// computed once per launch (the tag is uniform), the check in two
+// operations per slot.
+__host__ __device__ inline uint32_t tag_mix(uint32_t tag) { return tag * 0x9E3779B1u; }
+
+__host__ __device__ inline uint32_t slot_check(uint32_t a, uint32_t b, uint32_t mix) {
+  return a ^ ((b << 13) | (b >> 19)) ^ mix;
 }
 
 __device__ __forceinline__ float4 make_slot(uint32_t a, uint32_t b, uint32_t tag) {
-  return make_float4(bits_f32(a), bits_f32(b), bits_f32(tag), bits_f32(slot_check(a, b, tag)));
+  return make_float4(bits_f32(a), bits_f32(b), bits_f32(tag),
+                     bits_f32(slot_check(a, b, tag_mix(tag))));
 }
 
-__device__ __forceinline__ bool slot_ok(float4 s, uint32_t tag) {
-  const uint32_t t = f32_bits(s.z);
-  return t == tag && f32_bits(s.w) == slot_check(f32_bits(s.x), f32_bits(s.y), t);
+// mix = tag_mix(tag), tag this launch's (uniform)
+__device__ __forceinline__ bool slot_ok(float4 s, uint32_t tag, uint32_t mix) {
+  return f32_bits(s.z) == tag && f32_bits(s.w) == slot_check(f32_bits(s.x), f32_bits(s.y), mix);
 }
 
 constexpr int kChunks = (int)(kStepMaxTiles / kWave);  // tiles per lane, at most
@@ -638,7 +642,7 @@ struct RowLse {
 __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, uint32_t T,
                                              int lane) {
   RowLse r;
-  const uint32_t tag = *ss.rtag;
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(*ss.rtag), mix = tag_mix(tag);
   for (uint32_t n = 0;; ++n) {
     bool ok = true;
 #pragma unroll
@@ -650,7 +654,7 @@ __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, u
         const uint32_t at = (uint32_t)((row + (live ? t : 0u)) * 2);
         a = ss.slots.load4(at * 16);
         b = ss.slots.load4(at * 16 + 16);
-        ok = ok && (!live || (slot_ok(a, tag) && slot_ok(b, tag)));
+        ok = ok && (!live || (slot_ok(a, tag, mix) && slot_ok(b, tag, mix)));
       }
       r.zm[k] = live ? a.x : kNegInf;
       r.zl[k] = live ? a.y : 0.0f;
@@ -1422,7 +1426,7 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
                                uint32_t W, uint32_t tile, int lb, uint64_t last_bits,
                                uint32_t N) {
   const int lane = threadIdx.x % kWave;
-  const uint32_t tag = *sx.stats.rtag;
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(*sx.stats.rtag), mix = tag_mix(tag);
   uint64_t bm[kChunks];
   uint32_t cnt[kChunks], first[kChunks];
   // the head's tagged masks, read until every one has landed (a mask is
@@ -1437,7 +1441,7 @@ __device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_
       if (k * kWave < (int)T) {
         const float4 v = sx.xbits.load4((uint32_t)((h * ts + (t < T ? t : 0u)) * 16));
         if (t < T) {
-          ok = ok && slot_ok(v, tag);
+          ok = ok && slot_ok(v, tag, mix);
           bm[k] = (uint64_t)f32_bits(v.x) | ((uint64_t)f32_bits(v.y) << 32);
           if (t == T - 1) bm[k] &= last_bits;
         }
@@ -2179,12 +2183,12 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
     // store also waits for its write-through; the other waves go on to
     // their chunks)
     if (tid == kThreads - kWave) {
+      const uint32_t tag = __builtin_amdgcn_readfirstlane(*sx->stats.tag);
 #pragma unroll
       for (int m = 0; m < kTiles; ++m)
         if ((uint32_t)m < R)
           sx->xbits.store4((uint32_t)((h * da.tile_stride + rep_tile(m)) * 16),
-                           make_slot((uint32_t)bits[m], (uint32_t)(bits[m] >> 32),
-                                     *sx->stats.tag));
+                           make_slot((uint32_t)bits[m], (uint32_t)(bits[m] >> 32), tag));
     }
   }
   if (!spec) {
@@ -2525,8 +2529,9 @@ void step_kernel(StepArgs s) {
   // a tile's LSE partials out as two tagged slots
   auto publish = [&](int64_t t, int g, float4 part) {
     const uint32_t at = (uint32_t)(((h * G + g) * sa.tile_stride + t) * 2 * 16);
-    sx.stats.slots.store4(at, make_slot(f32_bits(part.x), f32_bits(part.y), sh.tag));
-    sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), sh.tag));
+    const uint32_t tag = __builtin_amdgcn_readfirstlane(sh.tag);
+    sx.stats.slots.store4(at, make_slot(f32_bits(part.x), f32_bits(part.y), tag));
+    sx.stats.slots.store4(at + 16, make_slot(f32_bits(part.z), f32_bits(part.w), tag));
   };
   if constexpr (kTiles == 1) {
     score_stats(
