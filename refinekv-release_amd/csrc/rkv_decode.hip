@@ -41,6 +41,7 @@
 
 #include <atomic>
 #include <type_traits>
+#include <utility>
 
 #include "rkv_common.h"
 #include "rkv_internal.h"
@@ -1169,7 +1170,76 @@ __device__ __forceinline__ F32x4 mma_qk(const Bf16x8 (&kop)[MmaShape<D>::kSteps]
 // chunk's staged value rows.  Online softmax in place, then PV with P as a
 // sum of two bf16 parts (relative error ~2^-17, where bf16 alone leaves
 // 2^-9) against the same value rows.
-template <int D>
+// N transposing 64-bit LDS reads (ds_read_b64_tr_b16) of the staged value
+// rows at LDS byte addresses at[], issued by one asm statement that does not
+// wait for them; lds_ready<N, b>(v[b]) then waits until read b has landed.
+// The compiler does not see these reads, so it adds no wait for the
+// buffer-to-LDS loads still in flight (it cannot tell that they fill other
+// stages, and such a wait would drain the ring's two chunks ahead); the
+// ring's own vmcnt wait before each chunk orders that chunk's LDS writes
+// before these reads.  Each wait names its register as an operand, so no use
+// of v[b] is placed before it.  LDS operations return in issue order, and
+// any other LDS or scalar-memory operation counted by lgkmcnt only makes a
+// count stricter, so lgkmcnt(N - 1 - b) always covers reads 0..b.
+template <int N>
+__device__ __forceinline__ void lds_read_tr(I16x4 (&v)[N], const uint32_t (&at)[N]) {
+  static_assert(N == 2 || N == 4 || N == 6 || N == 8, "2-8 reads");
+  if constexpr (N == 2) {
+    asm volatile("ds_read_b64_tr_b16 %0, %2\n\tds_read_b64_tr_b16 %1, %3"
+                 : "=&v"(v[0]), "=&v"(v[1])
+                 : "v"(at[0]), "v"(at[1])
+                 : "memory");
+  } else if constexpr (N == 4) {
+    asm volatile("ds_read_b64_tr_b16 %0, %4\n\tds_read_b64_tr_b16 %1, %5\n\t"
+                 "ds_read_b64_tr_b16 %2, %6\n\tds_read_b64_tr_b16 %3, %7"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3])
+                 : "v"(at[0]), "v"(at[1]), "v"(at[2]), "v"(at[3])
+                 : "memory");
+  } else if constexpr (N == 6) {
+    asm volatile("ds_read_b64_tr_b16 %0, %6\n\tds_read_b64_tr_b16 %1, %7\n\t"
+                 "ds_read_b64_tr_b16 %2, %8\n\tds_read_b64_tr_b16 %3, %9\n\t"
+                 "ds_read_b64_tr_b16 %4, %10\n\tds_read_b64_tr_b16 %5, %11"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5])
+                 : "v"(at[0]), "v"(at[1]), "v"(at[2]), "v"(at[3]), "v"(at[4]), "v"(at[5])
+                 : "memory");
+  } else {
+    asm volatile("ds_read_b64_tr_b16 %0, %8\n\tds_read_b64_tr_b16 %1, %9\n\t"
+                 "ds_read_b64_tr_b16 %2, %10\n\tds_read_b64_tr_b16 %3, %11\n\t"
+                 "ds_read_b64_tr_b16 %4, %12\n\tds_read_b64_tr_b16 %5, %13\n\t"
+                 "ds_read_b64_tr_b16 %6, %14\n\tds_read_b64_tr_b16 %7, %15"
+                 : "=&v"(v[0]), "=&v"(v[1]), "=&v"(v[2]), "=&v"(v[3]), "=&v"(v[4]), "=&v"(v[5]),
+                   "=&v"(v[6]), "=&v"(v[7])
+                 : "v"(at[0]), "v"(at[1]), "v"(at[2]), "v"(at[3]), "v"(at[4]), "v"(at[5]),
+                   "v"(at[6]), "v"(at[7])
+                 : "memory");
+  }
+}
+
+template <int N, int B>
+__device__ __forceinline__ void lds_ready(I16x4& v) {
+  constexpr int k = N - 1 - B;
+  static_assert(k >= 0 && k <= 7, "count");
+  if constexpr (k == 0) asm volatile("s_waitcnt lgkmcnt(0)" : "+v"(v));
+  else if constexpr (k == 1) asm volatile("s_waitcnt lgkmcnt(1)" : "+v"(v));
+  else if constexpr (k == 2) asm volatile("s_waitcnt lgkmcnt(2)" : "+v"(v));
+  else if constexpr (k == 3) asm volatile("s_waitcnt lgkmcnt(3)" : "+v"(v));
+  else if constexpr (k == 4) asm volatile("s_waitcnt lgkmcnt(4)" : "+v"(v));
+  else if constexpr (k == 5) asm volatile("s_waitcnt lgkmcnt(5)" : "+v"(v));
+  else if constexpr (k == 6) asm volatile("s_waitcnt lgkmcnt(6)" : "+v"(v));
+  else asm volatile("s_waitcnt lgkmcnt(7)" : "+v"(v));
+}
+
+// o[b] += p x v[b] for each b, each product after its read has landed and
+// (the scheduling barrier) before the next read's wait
+template <int N, int... B>
+__device__ __forceinline__ void mfma_as_ready(F32x4 (&o)[N], I16x4 p, I16x4 (&v)[N],
+                                              std::integer_sequence<int, B...>) {
+  ((lds_ready<N, B>(v[B]), o[B] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(p, v[B], o[B], 0, 0, 0),
+    __builtin_amdgcn_sched_barrier(0)),
+   ...);
+}
+
+template <int D, bool kAsmReads = true>
 __device__ __forceinline__ void mma_fold(MmaState<D>& st, const float (&x)[4], const char* src) {
   using S = MmaShape<D>;
   constexpr uint32_t NC = S::kNC;
@@ -1214,12 +1284,25 @@ __device__ __forceinline__ void mma_fold(MmaState<D>& st, const float (&x)[4], c
   const uint32_t base = t_row * (uint32_t)(D * 2) + (uint32_t)(lane & 1) * 8u;
   const uint32_t rot = ((uint32_t)(lane >> 1) & 1u) + 2u * t_row;
   I16x4 vb[S::kBlocks];
+  if constexpr (D <= 128 && kAsmReads) {
+    const uint32_t lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const char*)src;
+    uint32_t at[S::kBlocks];
 #pragma unroll
-  for (int b = 0; b < S::kBlocks; ++b) {
-    const uint32_t piece = (2u * b + rot) % NC;
-    vb[b] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-        (__attribute__((address_space(3))) I16x4*)(src + base + piece * 16u));
-    st.o[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb[b], st.o[b], 0, 0, 0);
+    for (int b = 0; b < S::kBlocks; ++b) at[b] = lds + base + ((2u * b + rot) % NC) * 16u;
+    lds_read_tr<S::kBlocks>(vb, at);
+    mfma_as_ready(st.o, ph, vb, std::make_integer_sequence<int, S::kBlocks>{});
+  } else {
+    // (head_dim 160: the ten addresses and outputs live at once would spill.
+    // The representative and suffix ring takes the compiler's reads too: it
+    // is short, so the compiler's wait for every buffer-to-LDS load costs
+    // little there, and it measured faster than the asm reads.  The
+    // compiler's reads keep that wait.)
+#pragma unroll
+    for (int b = 0; b < S::kBlocks; ++b) {
+      vb[b] = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+          (__attribute__((address_space(3))) I16x4*)(src + base + ((2u * b + rot) % NC) * 16u));
+      st.o[b] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(ph, vb[b], st.o[b], 0, 0, 0);
+    }
   }
 #pragma unroll
   for (int b = 0; b < S::kBlocks; ++b)
@@ -2109,7 +2192,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
               x[i] = r < n_suffix ? s4[i] * a.scale : kNegInf;
             }
           }
-          mma_fold<D>(st, x, stage.bytes[sidx]);
+          mma_fold<D, false>(st, x, stage.bytes[sidx]);
         });
   };
 
