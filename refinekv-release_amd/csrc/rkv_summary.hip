@@ -215,6 +215,42 @@ __device__ __forceinline__ void summary_passes(
   const int col = lane < LANES1 ? lane * CPL : 0;
   // this lane's columns in a staged row: chunk c1, 4-byte word w1 within it
   const int c1 = col / St::EPC, w1 = (col % St::EPC) * E / 4;
+  // a staged row's words at w (this lane's columns)
+  auto lds_cols = [&](const uint32_t* w) {
+    RawCols<In, CPL> x;
+    constexpr int W = RawCols<In, CPL>::W;
+    if constexpr (W == 1) {
+      x.w[0] = w[0];
+    } else if constexpr (W == 2) {
+      const uint2 u = *reinterpret_cast<const uint2*>(w);
+      x.w[0] = u.x;
+      x.w[1] = u.y;
+    } else {
+      const uint4 u = *reinterpret_cast<const uint4*>(w);
+      x.w[0] = u.x;
+      x.w[1] = u.y;
+      x.w[2] = u.z;
+      x.w[3] = u.w;
+    }
+    return x;
+  };
+  // Token t's swizzle depends on t mod SW alone, so this lane's staged words
+  // for each residue sit at fixed addresses kw1[s] / vw1[s] plus the row
+  // offset t NC 16, a constant of the unrolled full-chunk loop below (the
+  // reads' immediate offset): no per-read address arithmetic.
+  // (head_dim 64 .. 128: above it the tables' registers cost the stream form
+  // its second wave per SIMD; below it a staged block's 128 tokens are too
+  // many to unroll)
+  constexpr bool kFixed = kStage && D >= 64 && D <= 128;
+  constexpr int kMaxBlock = kFixed ? (int)(kStageElemsMax / D) / 16 * 16 : 16;
+  const char* kw1[St::SW];
+  const char* vw1[St::SW];
+#pragma unroll
+  for (int sr = 0; sr < St::SW; ++sr) {
+    const int o = St::slot(c1, sr) * 16 + w1 * 4;
+    kw1[sr] = reinterpret_cast<const char*>(kst) + o;
+    vw1[sr] = reinterpret_cast<const char*>(vst) + o;
+  }
   auto row_cols = [&](const __amdgpu_buffer_rsrc_t& r, const uint4* st, int t, int ts) {
     if constexpr (kStage) {
       const uint32_t* w = reinterpret_cast<const uint32_t*>(st + t * St::NC + St::slot(c1, t)) + w1;
@@ -270,7 +306,8 @@ __device__ __forceinline__ void summary_passes(
       av[j] = av[j] + xv[j];
     }
   };
-  for (int c0 = 0; c0 < block; c0 += 16) {
+  // the 16-token chunk at c0 (a multiple of 16)
+  auto chunk = [&](int c0) {
     float ak[CPL], av[CPL];
 #pragma unroll
     for (int j = 0; j < CPL; ++j) ak[j] = av[j] = 0.0f;
@@ -280,8 +317,15 @@ __device__ __forceinline__ void summary_passes(
         RawCols<In, CPL> rk[kTokBatch], rv[kTokBatch];
 #pragma unroll
         for (int i = 0; i < kTokBatch; ++i) {
-          rk[i] = row_cols(kr, kst, c0 + i0 + i, kts);
-          rv[i] = row_cols(vr, vst, c0 + i0 + i, vts);
+          const int t = c0 + i0 + i;  // t mod SW == (i0 + i) mod SW
+          if constexpr (kFixed) {
+            const int row = t * St::NC * 16;
+            rk[i] = lds_cols(reinterpret_cast<const uint32_t*>(kw1[(i0 + i) % St::SW] + row));
+            rv[i] = lds_cols(reinterpret_cast<const uint32_t*>(vw1[(i0 + i) % St::SW] + row));
+          } else {
+            rk[i] = row_cols(kr, kst, t, kts);
+            rv[i] = row_cols(vr, vst, t, vts);
+          }
         }
 #pragma unroll
         for (int i = 0; i < kTokBatch; i += 2) {
@@ -318,16 +362,43 @@ __device__ __forceinline__ void summary_passes(
       ksum[j] = ksum[j] + ak[j];
       vsum[j] = vsum[j] + av[j];
     }
+  };
+  if constexpr (kFixed) {
+    // (a staged block holds at most kMaxBlock tokens)
+#pragma unroll
+    for (int c0 = 0; c0 < kMaxBlock; c0 += 16) {
+      if (c0 >= block) break;
+      chunk(c0);
+    }
+  } else {
+    for (int c0 = 0; c0 < block; c0 += 16) chunk(c0);
   }
   float w2[CPL];
   if (on1) {
     const float fc = (float)cnt;
     const int64_t o = (h * n_blocks + b) * D + col;
+    // x / 2^k and x * 2^-k are the same correctly rounded value of x 2^-k,
+    // so a power-of-two count (every full block) takes a multiply
+    float km[CPL], vm[CPL];
+    if ((cnt & (cnt - 1)) == 0) {
+      const float inv = 1.0f / fc;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        km[j] = ksum[j] * inv;
+        vm[j] = vsum[j] * inv;
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        km[j] = ksum[j] / fc;
+        vm[j] = vsum[j] / fc;
+      }
+    }
 #pragma unroll
     for (int j = 0; j < CPL; ++j) {
-      const uint16_t mkb = bf16_rne(ksum[j] / fc);
+      const uint16_t mkb = bf16_rne(km[j]);
       key_mean[o + j] = mkb;
-      value_mean[o + j] = bf16_rne(vsum[j] / fc);
+      value_mean[o + j] = bf16_rne(vm[j]);
       const float mk = bf16_to_f32(mkb);
       const float width = nanmax(kmax[j] - mk, mk - kmin[j]);
       const float cw = clamp_min(width, 1e-6f);
@@ -341,25 +412,12 @@ __device__ __forceinline__ void summary_passes(
   // ---- pass 2: per-token radius (RADSUM) and value norm (NORMSUM) ------
   const int l8 = lane & 7;
   const int g8 = lane >> 3;
+  // vnmax: the largest squared token norm; its square root is taken once,
+  // after the block (a correctly rounded sqrt is monotone, so the root of the
+  // maximum is the maximum of the roots; a NaN propagates either way)
   float r2max = kNegInf, vnmax = kNegInf;
-  for (int t0 = 0; t0 < cnt; t0 += 8) {
-    const int t = t0 + g8;
-    const bool on = t < cnt;
-    const int tt = on ? t : 0;
-    const int ko = tt * kts + l8 * E, vo = tt * vts + l8 * E;
-    float kx[D / 8], vx[D / 8];
-#pragma unroll
-    for (int m = 0; m < D / 8; ++m) {
-      if constexpr (kStage) {
-        const int e = 8 * m + l8;
-        const int o = tt * St::NC + St::slot(e / St::EPC, tt);
-        kx[m] = lds_elem<In>(reinterpret_cast<const T*>(kst + o) + e % St::EPC);
-        vx[m] = lds_elem<In>(reinterpret_cast<const T*>(vst + o) + e % St::EPC);
-      } else {
-        kx[m] = buf_elem<In>(kr, ko + 8 * m * E);
-        vx[m] = buf_elem<In>(vr, vo + 8 * m * E);
-      }
-    }
+  // the 8 tokens t0 + g8 (t0 a multiple of 8): this lane's elements 8 m + l8
+  auto group = [&](const float (&kx)[D / 8], const float (&vx)[D / 8], bool on) {
     float A0 = 0.0f, A1 = 0.0f, A2 = 0.0f, A3 = 0.0f, an = 0.0f;
 #pragma unroll
     for (int m = 0; m < D / 8; ++m) {
@@ -383,10 +441,57 @@ __device__ __forceinline__ void summary_passes(
     }
     const bool last = on && l8 == 7;
     r2max = nanmax(r2max, last ? tot : kNegInf);
-    vnmax = nanmax(vnmax, last ? sqrtf(vt) : kNegInf);
+    vnmax = nanmax(vnmax, last ? vt : kNegInf);
+  };
+  if constexpr (kFixed) {
+    // element 8 m + l8 of token t0 + g8 sits at ka2[m] / va2[m] plus the row
+    // offset t0 NC 16 (t0 + g8 has the residue g8 mod SW): rows past cnt in
+    // the group read the block's zero-filled tail (t0 + 7 < block), masked
+    const char* ka2[D / 8];
+    const char* va2[D / 8];
+#pragma unroll
+    for (int m = 0; m < D / 8; ++m) {
+      const int e = 8 * m + l8;
+      const int o = (g8 * St::NC + St::slot(e / St::EPC, g8)) * 16 + (e % St::EPC) * E;
+      ka2[m] = reinterpret_cast<const char*>(kst) + o;
+      va2[m] = reinterpret_cast<const char*>(vst) + o;
+    }
+#pragma unroll
+    for (int t0 = 0; t0 < kMaxBlock; t0 += 8) {
+      if (t0 >= cnt) break;
+      const int row = t0 * St::NC * 16;
+      float kx[D / 8], vx[D / 8];
+#pragma unroll
+      for (int m = 0; m < D / 8; ++m) {
+        kx[m] = lds_elem<In>(reinterpret_cast<const T*>(ka2[m] + row));
+        vx[m] = lds_elem<In>(reinterpret_cast<const T*>(va2[m] + row));
+      }
+      group(kx, vx, t0 + g8 < cnt);
+    }
+  } else {
+    for (int t0 = 0; t0 < cnt; t0 += 8) {
+      const int t = t0 + g8;
+      const bool on = t < cnt;
+      const int tt = on ? t : 0;
+      const int ko = tt * kts + l8 * E, vo = tt * vts + l8 * E;
+      float kx[D / 8], vx[D / 8];
+#pragma unroll
+      for (int m = 0; m < D / 8; ++m) {
+        if constexpr (kStage) {
+          const int e = 8 * m + l8;
+          const int o = tt * St::NC + St::slot(e / St::EPC, tt);
+          kx[m] = lds_elem<In>(reinterpret_cast<const T*>(kst + o) + e % St::EPC);
+          vx[m] = lds_elem<In>(reinterpret_cast<const T*>(vst + o) + e % St::EPC);
+        } else {
+          kx[m] = buf_elem<In>(kr, ko + 8 * m * E);
+          vx[m] = buf_elem<In>(vr, vo + 8 * m * E);
+        }
+      }
+      group(kx, vx, on);
+    }
   }
   r2max = wave_nanmax(r2max);
-  vnmax = wave_nanmax(vnmax);
+  vnmax = sqrtf(wave_nanmax(vnmax));
   if (on1) {
     float r2 = clamp_min(r2max, 0.0f);
     r2 = sqrtf(r2);
@@ -547,8 +652,21 @@ __global__ __launch_bounds__(256) void max_norm_kernel(const float* __restrict__
                                                        float* __restrict__ max_value_norm) {
   __shared__ float part[4];
   const int64_t h = blockIdx.x;
+  const float* vn = value_norm + h * n_blocks;
   float m = kNegInf;
-  for (int64_t b = threadIdx.x; b < n_blocks; b += blockDim.x) m = nanmax(m, value_norm[h * n_blocks + b]);
+  // blocks tid, tid + 256, ... in that order, sixteen loads in flight at a
+  // time (one batch for 4096 blocks)
+  constexpr int kBatch = 16;
+  for (int64_t b0 = threadIdx.x; b0 < n_blocks; b0 += (int64_t)blockDim.x * kBatch) {
+    float x[kBatch];
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) {
+      const int64_t b = b0 + (int64_t)k * blockDim.x;
+      x[k] = b < n_blocks ? vn[b] : kNegInf;
+    }
+#pragma unroll
+    for (int k = 0; k < kBatch; ++k) m = nanmax(m, x[k]);
+  }
   m = wave_nanmax(m);
   if (threadIdx.x % kWave == 0) part[threadIdx.x / kWave] = m;
   __syncthreads();
