@@ -7,8 +7,11 @@
 // token, so the per-token head_dim sums are lane-local.  Where a block's K
 // and V fit 64 KiB (kStage), the wave first moves the whole block from HBM
 // into LDS with 16-byte buffer-to-LDS loads (all of it in flight at once) and
-// both passes read LDS: HBM sees each row once.  Larger blocks stream pass 1
-// from global memory and re-read the rows there in pass 2.  Row accesses go
+// both passes read LDS: HBM sees each row once.  Blocks above 4096 elements
+// per tensor go to a workgroup of block / 16 waves, each staging one 16-token
+// chunk, whose chunk sums wave 0 adds in order (the same sums); blocks whose
+// chunks do not fit either stream pass 1 from global memory and re-read the
+// rows there in pass 2.  Row accesses go
 // through per-block buffer views (scalar base and token offset, one lane
 // offset, immediate column offsets: no per-load address arithmetic; rows past
 // the block's end read 0), the block index is wave-uniform, and the min/max
@@ -147,9 +150,10 @@ constexpr int kSummaryWaves = 4;
 constexpr int kTokBatch = 8;  // tokens per batch of pass-1 row loads
 constexpr int64_t kStageWaveMax = 64 * 1024;   // LDS of one staged block, at most
 constexpr int64_t kStageGroupMax = 32 * 1024;  // LDS of a staged workgroup, aimed at
-// Staging pays while a block holds at most 4096 elements per tensor: larger
-// blocks leave too few waves per CU (LDS) for their longer passes, and the
-// two-pass form, whose pass 2 re-reads from the L2 and MALL, is faster.
+// One wave stages a block while it holds at most 4096 elements per tensor:
+// larger blocks in one wave leave too few waves per CU (LDS) for their longer
+// passes; they are split into 16-token chunks over a workgroup's waves
+// (summary_split_kernel) instead.
 constexpr int64_t kStageElemsMax = 4096;
 
 // A staged block in LDS (per wave): its K rows, then its V rows, as 16-byte
@@ -196,13 +200,23 @@ struct CacheOut {
 // staged in LDS at kst / vst; s_mk / s_rs: D floats each of LDS.  One wave;
 // its workgroup holds whole waves only (the __syncthreads between the passes
 // orders the LDS writes of the means before their reads).
-template <int D, class In, bool kStore, bool kStage>
+// A block summarized by several waves of one workgroup (kSplit): wave w
+// holds the block's 16-token chunk w (its own cnt and block are that chunk's
+// live tokens and 16), and the chunks' sums meet in LDS.
+struct SplitPart {
+  int wave, waves;  // this wave's chunk, the block's chunks
+  int cnt;          // the block's tokens
+  float* part;      // LDS: waves x 4 x D floats (chunk sums, max, min), then waves x 2
+};
+
+template <int D, class In, bool kStore, bool kStage, bool kSplit = false>
 __device__ __forceinline__ void summary_passes(
-    int64_t h, int64_t b, int64_t bb, bool valid, int cnt, int block, int64_t n_blocks,
+    int64_t h, int64_t b, int64_t row0, bool valid, int cnt, int block, int64_t n_blocks,
     __amdgpu_buffer_rsrc_t kr, __amdgpu_buffer_rsrc_t vr, int kts, int vts, const uint4* kst,
     const uint4* vst, float* s_mk, float* s_rs, int64_t* __restrict__ counts,
     uint16_t* __restrict__ key_mean, uint16_t* __restrict__ value_mean,
-    uint16_t* __restrict__ ellipsoid, float* __restrict__ value_norm, const CacheOut<In>& out) {
+    uint16_t* __restrict__ ellipsoid, float* __restrict__ value_norm, const CacheOut<In>& out,
+    const SplitPart& sp = SplitPart{0, 1, 0, nullptr}) {
   using T = typename In::T;
   using St = Staging<In, D>;
   constexpr int E = (int)sizeof(T);
@@ -285,9 +299,9 @@ __device__ __forceinline__ void summary_passes(
   // the cache rows of this block (kStore): live tokens, lanes on1
   const int cks = kStore ? (int)out.k_ts * E : 0, cvs = kStore ? (int)out.v_ts * E : 0;
   const auto ckr =
-      kStore ? rows_view(out.keys + h * out.k_hs + bb * block * out.k_ts, extent(cks)) : kr;
+      kStore ? rows_view(out.keys + h * out.k_hs + row0 * out.k_ts, extent(cks)) : kr;
   const auto cvr =
-      kStore ? rows_view(out.values + h * out.v_hs + bb * block * out.v_ts, extent(cvs)) : vr;
+      kStore ? rows_view(out.values + h * out.v_hs + row0 * out.v_ts, extent(cvs)) : vr;
   // token t's columns added to the chunk sums (t < cnt, wave-uniform)
   auto take = [&](int t, const RawCols<In, CPL>& rk, const RawCols<In, CPL>& rv,
                   float (&ak)[CPL], float (&av)[CPL], float (&xk)[CPL]) {
@@ -373,14 +387,49 @@ __device__ __forceinline__ void summary_passes(
   } else {
     for (int c0 = 0; c0 < block; c0 += 16) chunk(c0);
   }
+  if constexpr (kSplit) {
+    // the chunk's sums, max and min out; wave 0 adds the chunks' sums left
+    // to right from +0 (each is its chunk summed from +0, and a running sum
+    // from +0 is never -0, so this is the one-wave TOKSUM order exactly)
+    float* q = sp.part + sp.wave * 4 * D;
+    if (on1) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        q[col + j] = ksum[j];
+        q[D + col + j] = vsum[j];
+        q[2 * D + col + j] = kmax[j];
+        q[3 * D + col + j] = kmin[j];
+      }
+    }
+    __syncthreads();
+    if (sp.wave == 0) {
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        ksum[j] = 0.0f;
+        vsum[j] = 0.0f;
+      }
+      for (int w = 0; w < sp.waves; ++w) {
+        const float* r = sp.part + w * 4 * D;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) {
+          ksum[j] = ksum[j] + r[col + j];
+          vsum[j] = vsum[j] + r[D + col + j];
+          kmax[j] = max3_nan(kmax[j], r[2 * D + col + j], r[2 * D + col + j]);
+          kmin[j] = min3_nan(kmin[j], r[3 * D + col + j], r[3 * D + col + j]);
+        }
+      }
+    }
+  }
+  // the block's token count (the whole block's in split mode)
+  const int bcnt = kSplit ? sp.cnt : cnt;
   float w2[CPL];
-  if (on1) {
-    const float fc = (float)cnt;
+  if (on1 && (!kSplit || sp.wave == 0)) {
+    const float fc = (float)bcnt;
     const int64_t o = (h * n_blocks + b) * D + col;
     // x / 2^k and x * 2^-k are the same correctly rounded value of x 2^-k,
     // so a power-of-two count (every full block) takes a multiply
     float km[CPL], vm[CPL];
-    if ((cnt & (cnt - 1)) == 0) {
+    if ((bcnt & (bcnt - 1)) == 0) {
       const float inv = 1.0f / fc;
 #pragma unroll
       for (int j = 0; j < CPL; ++j) {
@@ -491,7 +540,22 @@ __device__ __forceinline__ void summary_passes(
     }
   }
   r2max = wave_nanmax(r2max);
-  vnmax = sqrtf(wave_nanmax(vnmax));
+  vnmax = wave_nanmax(vnmax);
+  if constexpr (kSplit) {
+    // the chunks' maxima meet in wave 0, which writes the block's outputs
+    float* q = sp.part + sp.waves * 4 * D;
+    if (lane == 0) {
+      q[2 * sp.wave] = r2max;
+      q[2 * sp.wave + 1] = vnmax;
+    }
+    __syncthreads();
+    if (sp.wave != 0) return;
+    for (int w = 0; w < sp.waves; ++w) {
+      r2max = nanmax(r2max, q[2 * w]);
+      vnmax = nanmax(vnmax, q[2 * w + 1]);
+    }
+  }
+  vnmax = sqrtf(vnmax);
   if (on1) {
     float r2 = clamp_min(r2max, 0.0f);
     r2 = sqrtf(r2);
@@ -502,7 +566,7 @@ __device__ __forceinline__ void summary_passes(
   }
   if (valid && lane == 0) {
     value_norm[h * n_blocks + b] = vnmax;
-    if (h == 0) counts[b] = cnt;
+    if (h == 0) counts[b] = bcnt;
   }
 }
 
@@ -551,9 +615,63 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   }
 
-  summary_passes<D, In, kStore, kStage>(h, b, bb, valid, cnt, block, n_blocks, kr, vr, kts,
-                                        vts, kst, vst, s_mk, s_rs, counts, key_mean,
+  summary_passes<D, In, kStore, kStage>(h, b, bb * block, valid, cnt, block, n_blocks, kr, vr,
+                                        kts, vts, kst, vst, s_mk, s_rs, counts, key_mean,
                                         value_mean, ellipsoid, value_norm, out);
+}
+
+// Blocks above kStageElemsMax elements per tensor (B 64 at d 128, B 32 at
+// d 160 and up): one workgroup of block / 16 waves per block; wave w moves
+// the block's 16-token chunk w into LDS (all its loads in flight at once) and
+// runs both passes on it, and wave 0 combines the chunks (summary_passes,
+// kSplit), so HBM sees each row once.  LDS: the waves' chunks (K then V, the
+// staged layout), then D key means, D inverse widths and the chunks'
+// partials.
+template <int D, class In, bool kStore>
+__global__ __launch_bounds__(kWave * 4) void summary_split_kernel(
+    const typename In::T* __restrict__ keys, int64_t k_hs, int64_t k_ts,
+    const typename In::T* __restrict__ values, int64_t v_hs, int64_t v_ts, int64_t length,
+    int block, int64_t n_blocks, int64_t* __restrict__ counts, uint16_t* __restrict__ key_mean,
+    uint16_t* __restrict__ value_mean, uint16_t* __restrict__ ellipsoid,
+    float* __restrict__ value_norm, CacheOut<In> out) {
+  using St = Staging<In, D>;
+  constexpr int E = (int)sizeof(typename In::T);
+  constexpr int chunks = 16 * St::NC;  // 16-byte chunks per tensor and wave, a multiple of 64
+  extern __shared__ uint4 s_dyn[];
+  const int waves = blockDim.x / kWave;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  const int lane = threadIdx.x % kWave;
+  const int64_t h = blockIdx.y, b = blockIdx.x;
+  const int cnt_all = __builtin_amdgcn_readfirstlane(
+      (int)(b == n_blocks - 1 ? length - (n_blocks - 1) * block : block));
+  const int rest = cnt_all - 16 * wave;
+  const int cnt = __builtin_amdgcn_readfirstlane(rest < 0 ? 0 : rest > 16 ? 16 : rest);
+  const int64_t row0 = b * block + 16 * wave;
+  const int kts = (int)k_ts * E, vts = (int)v_ts * E;
+  auto extent = [&](int ts) { return __builtin_amdgcn_readfirstlane(cnt ? (cnt - 1) * ts + D * E : 0); };
+  // the chunk's rows; rows past its live tokens read 0
+  const auto kr = rows_view(keys + h * k_hs + row0 * k_ts, extent(kts));
+  const auto vr = rows_view(values + h * v_hs + row0 * v_ts, extent(vts));
+  uint4* kst = s_dyn + wave * 2 * chunks;
+  uint4* vst = kst + chunks;
+  float* s_mk = reinterpret_cast<float*>(s_dyn + waves * 2 * chunks);
+  float* s_rs = s_mk + D;
+  for (int p0 = 0; p0 < chunks; p0 += kWave) {
+    const int p = p0 + lane, t = p / St::NC;
+    const int off = St::slot(p % St::NC, t) * 16;
+    load_to_lds16(kr, kst + p0, t * kts + off);
+    load_to_lds16(vr, vst + p0, t * vts + off);
+  }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  summary_passes<D, In, kStore, true, true>(h, b, row0, true, cnt, 16, n_blocks, kr, vr, kts, vts,
+                                            kst, vst, s_mk, s_rs, counts, key_mean, value_mean,
+                                            ellipsoid, value_norm, out,
+                                            SplitPart{wave, waves, cnt_all, s_rs + D});
+}
+
+// LDS bytes of a split block's workgroup (summary_split_kernel).
+constexpr int64_t summary_split_lds(int64_t dim, int64_t elem, int64_t block) {
+  return (block / 16) * (2 * 16 * dim * elem + 4 * dim * 4 + 2 * 4) + 2 * dim * 4;
 }
 
 // The staged summary as a stream (2-byte K/V, head_dim >= 192): one-wave
@@ -637,7 +755,7 @@ __global__ __launch_bounds__(kWave) void summary_stream_kernel(
     const int64_t fn = f + nw;
     if (fn < total) issue(views(fn));
     const Views cur = views(f);
-    summary_passes<D, In, kStore, true>(cur.h, cur.b, cur.b, true, cur.cnt, block, n_blocks,
+    summary_passes<D, In, kStore, true>(cur.h, cur.b, cur.b * block, true, cur.cnt, block, n_blocks,
                                         cur.kr, cur.vr, kts, vts, kst, vst, s_mk, s_rs, counts,
                                         key_mean, value_mean, ellipsoid, value_norm, out);
     __syncthreads();
@@ -736,16 +854,40 @@ int launch_summary(const void* keys, int64_t k_hs, int64_t k_ts, const void* val
     return check_launch("max_norm_kernel");
   }
   }
-  int waves = kSummaryWaves;
-  while (stage && waves > 1 && waves * per_wave > kStageGroupMax) waves /= 2;
-  dim3 grid((unsigned)((n_blocks + waves - 1) / waves), (unsigned)heads);
-  dim3 threads(kWave * waves);
-  const size_t lds = (size_t)(waves * per_wave);
   const auto* k = static_cast<const typename In::T*>(keys);
   const auto* v = static_cast<const typename In::T*>(values);
   auto* km = static_cast<uint16_t*>(key_mean);
   auto* vm = static_cast<uint16_t*>(value_mean);
   auto* el = static_cast<uint16_t*>(ellipsoid);
+  // blocks too large to stage in one wave: a workgroup of block / 16 waves
+  // (d 128, B 64, 8 heads of 131072 tokens: 160 -> 124 us, the two-pass
+  // form's re-read of pass 2 gone)
+  const int64_t split_lds = summary_split_lds(dim, elem, block);
+  if (!stage && block >= 32 && 16 * dim <= kStageElemsMax && split_lds <= kStageWaveMax &&
+      rows16(keys, k_hs, k_ts) && rows16(values, v_hs, v_ts)) {
+    const dim3 sgrid((unsigned)n_blocks, (unsigned)heads);
+    const dim3 sthreads((unsigned)(kWave * (block / 16)));
+    RKV_DISPATCH_DIM(dim, D, {
+      if (out.keys)
+        summary_split_kernel<D, In, true><<<sgrid, sthreads, (size_t)split_lds, stream>>>(
+            k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, km, vm, el,
+            value_norm, out);
+      else
+        summary_split_kernel<D, In, false><<<sgrid, sthreads, (size_t)split_lds, stream>>>(
+            k, k_hs, k_ts, v, v_hs, v_ts, length, (int)block, n_blocks, counts, km, vm, el,
+            value_norm, out);
+    });
+    int rc = check_launch("summary_split_kernel");
+    if (rc) return rc;
+    max_norm_kernel<<<dim3((unsigned)heads), dim3(256), 0, stream>>>(value_norm, n_blocks,
+                                                                      max_value_norm);
+    return check_launch("max_norm_kernel");
+  }
+  int waves = kSummaryWaves;
+  while (stage && waves > 1 && waves * per_wave > kStageGroupMax) waves /= 2;
+  dim3 grid((unsigned)((n_blocks + waves - 1) / waves), (unsigned)heads);
+  dim3 threads(kWave * waves);
+  const size_t lds = (size_t)(waves * per_wave);
 #define RKV_SUMMARY_LAUNCH(STORE, STAGE)                                                   \
   RKV_DISPATCH_DIM(dim, D,                                                                 \
                    summary_kernel<D, In, STORE, STAGE><<<grid, threads, lds, stream>>>(    \

@@ -139,6 +139,8 @@ SUMMARY_CASES = [
     (torch.bfloat16, 256, 16, 777), (torch.float16, 224, 16, 500),
     # the largest blocks (64 KiB and 128 KiB of K plus V)
     (torch.float32, 256, 64, 300), (torch.float32, 128, 64, 700),
+    # blocks split over a workgroup's waves (16 tokens each), last block partial
+    (torch.bfloat16, 128, 64, 1000), (torch.float16, 128, 64, 1999), (torch.bfloat16, 192, 32, 1001),
 ]
 
 
@@ -190,7 +192,8 @@ def test_summary_of_rows_not_16_byte_aligned(hip, oracle_lib):
 
 @pytest.mark.parametrize("dtype,dim,block,length", [
     (torch.bfloat16, 128, 32, 4099), (torch.bfloat16, 64, 16, 300), (torch.float16, 128, 32, 777),
-    (torch.float32, 96, 64, 1000), (torch.bfloat16, 256, 32, 999), (torch.float32, 256, 64, 300)])
+    (torch.float32, 96, 64, 1000), (torch.bfloat16, 256, 32, 999), (torch.float32, 256, 64, 300),
+    (torch.bfloat16, 128, 64, 1000)])
 def test_summary_written_with_the_cache(hip, oracle_lib, dtype, dim, block, length):
     """store_and_build_summary (one kernel: cache write + summary) equals the
     oracle's summary of the same keys/values bit for bit, and a cache copy
