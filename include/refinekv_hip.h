@@ -271,13 +271,15 @@ int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
  * thread; (0, 0) restores normal operation. */
 int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew);
 
-/* Test hook with no reference counterpart: 0 turns off the one-launch
- * step's speculation, 1 (default) turns it on.  When the previous launch on
- * a workspace expanded every block of a head, the step's workgroups of that
- * head attend their share of all its token rows before the decision and keep
- * the result if every block expands again (else they attend as usual): the
- * output is the same bit for bit either way.  Per thread. */
-int rkv_set_speculation(int enable);
+/* Test hook with no reference counterpart: the one-launch step's
+ * speculation, 0 off, 1 (default) where a workgroup's share of a head's
+ * token rows is at least 2048, 2 for every shape; other modes return
+ * RKV_INVALID_ARGUMENT.  When the previous launch on a workspace expanded
+ * every block of a head, the step's workgroups of that head attend their
+ * share of all its token rows before the decision and keep the result if
+ * every block expands again (else they attend as usual): the output is the
+ * same bit for bit either way.  Per thread. */
+int rkv_set_speculation(int mode);
 
 /* Test hook with no reference counterpart: applies the kernels' device
  * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */

@@ -3079,8 +3079,15 @@ StepMode step_mode(const SelectParams& p, const Layout& L, const DecodeBuffers& 
 thread_local uint32_t g_spin_limit = 0;
 thread_local uint32_t g_skew = 0;
 // Test hook (rkv_set_speculation, per thread): 0 turns the step's
-// speculation off.
+// speculation off, 1 (default) leaves it on where a workgroup's share of a
+// head's rows is at least kSpecMinRows, 2 turns it on for every shape.
 thread_local uint32_t g_speculate = 1;
+// Speculation pays where the page rows outweigh the decision it moves off
+// their path: measured on at 2048 rows per workgroup (eps 0 at 131072
+// tokens, 8 heads: 109.0 -> 107.0 us), off at 1024 (65536 tokens: 63.2
+// against 63.5 us) and at 512 (32768 tokens: 39.96 against 40.35 us; the
+// Qwen-shaped op at 65536 tokens: 50.4 against 51.2).
+constexpr int64_t kSpecMinRows = 2048;
 
 int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, bool ticketed) {
   StepArgs s;
@@ -3103,7 +3110,8 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, 
   s.heads = (int)p.heads;
   s.spin = g_spin_limit ? g_spin_limit : kSpinLimit;
   s.skew = g_skew;
-  s.speculate = g_speculate;
+  const int64_t share = p.n_blocks * p.block / (L.step_workers > 0 ? L.step_workers : 1);
+  s.speculate = g_speculate == 2 || (g_speculate == 1 && share >= kSpecMinRows) ? 1u : 0u;
   const int64_t rows = rows_per_pass(p.group, p.dim);
   mark(0, p.stream);
   int rc = kUnsupported;
@@ -3448,13 +3456,15 @@ extern "C" int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew) {
   return kOk;
 }
 
-// Test hook: 0 turns off the one-launch step's speculation (attending every
-// block's rows before the decision when the previous launch on the workspace
-// expanded every block), 1 (default) turns it on.  Results are the same bit
-// for bit either way.  Per thread.
-extern "C" int rkv_set_speculation(int enable) {
+// Test hook: the one-launch step's speculation (attending every block's rows
+// before the decision when the previous launch on the workspace expanded
+// every block): 0 off, 1 (default) where a workgroup's share of a head's
+// rows is at least kSpecMinRows, 2 for every shape.  Results are the same
+// bit for bit either way.  Per thread.
+extern "C" int rkv_set_speculation(int mode) {
   clear_error();
-  g_speculate = enable ? 1u : 0u;
+  if (mode < 0 || mode > 2) return set_error(kInvalidArgument, "rkv_set_speculation: mode %d (0, 1 or 2)", mode);
+  g_speculate = (uint32_t)mode;
   return kOk;
 }
 

@@ -383,12 +383,21 @@ def set_handoff_test(spin_limit=0, skew=0):
     _check(lib().rkv_set_handoff_test(spin_limit, skew), "rkv_set_handoff_test")
 
 
-def set_speculation(enable=True):
+SPECULATION_MODES = {"off": 0, "auto": 1, "always": 2}
+
+
+def set_speculation(mode="auto"):
     """Test hook: the one-launch step's speculation (attending every block's
     rows before the decision when the previous launch on the workspace
-    expanded every block) on or off for later calls on this thread; results
-    are the same bit for bit either way."""
-    _check(lib().rkv_set_speculation(1 if enable else 0), "rkv_set_speculation")
+    expanded every block) for later calls on this thread: "off", "auto" (the
+    default: where a workgroup's share of a head's rows is at least 2048) or
+    "always"; True and False mean "auto" and "off".  Results are the same bit
+    for bit either way."""
+    if isinstance(mode, bool):
+        mode = "auto" if mode else "off"
+    if mode not in SPECULATION_MODES:
+        raise ValueError(f"speculation mode {mode!r}: one of {sorted(SPECULATION_MODES)}")
+    _check(lib().rkv_set_speculation(SPECULATION_MODES[mode]), "rkv_set_speculation")
 
 
 def decode_static(query, summary, key_suffix, value_suffix, config, output, mask,

@@ -49,6 +49,22 @@ def test_version_and_error_channel(lib):
     assert b"bad arguments" in lib.rkv_last_error()
 
 
+def test_speculation_modes(lib):
+    """rkv_set_speculation takes 0 (off), 1 (default) and 2 (every shape) and
+    rejects anything else with RKV_INVALID_ARGUMENT (host-side only)."""
+    from refinekv import _hip
+
+    assert lib.rkv_set_speculation(3) == 1
+    assert b"rkv_set_speculation: mode 3" in lib.rkv_last_error()
+    assert lib.rkv_set_speculation(-1) == 1
+    for mode in (0, 2, 1):
+        assert lib.rkv_set_speculation(mode) == 0
+    with pytest.raises(ValueError):
+        _hip.set_speculation("sometimes")
+    _hip.set_speculation(False)
+    _hip.set_speculation("auto")
+
+
 def rows_per_pass(group, dim):
     """Query rows one attention pass of the decode kernels carries: the next
     power of two >= group (at least 4), at most 64 // (dim // 16)."""

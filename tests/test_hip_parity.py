@@ -466,7 +466,7 @@ def test_speculation_matches_the_normal_order_bit_for_bit(hip, heads, group, dim
         res = sparse_attention(q, summary, sk, sv, cfg, workspace=ws, return_selected=True)
         return res.output.clone(), res.selected.clone()
 
-    hip.set_speculation(False)
+    hip.set_speculation("off")
     try:
         want_full = run(full, {})
         # the smallest of these eps that leaves some block unexpanded
@@ -476,15 +476,18 @@ def test_speculation_matches_the_normal_order_bit_for_bit(hip, heads, group, dim
             want_sparse = run(sparse, {})
             if not want_sparse[1].all():
                 break
+        # (these prompts give each workgroup fewer rows than the default mode
+        # speculates on)
+        hip.set_speculation("always")
+        assert want_full[1].all() and not want_sparse[1].all()
+        ws = {}
+        got = [run(full, ws) for _ in range(3)]  # the first in the normal order, then speculating
+        got.append(run(sparse, ws))              # speculates and misses
+        got.append(run(full, ws))                # the previous launch did not expand every block
+        got.append(run(full, ws))                # speculates again
+        torch.cuda.synchronize()
     finally:
-        hip.set_speculation(True)
-    assert want_full[1].all() and not want_sparse[1].all()
-    ws = {}
-    got = [run(full, ws) for _ in range(3)]  # the first in the normal order, then speculating
-    got.append(run(sparse, ws))              # speculates and misses
-    got.append(run(full, ws))                # the previous launch did not expand every block
-    got.append(run(full, ws))                # speculates again
-    torch.cuda.synchronize()
+        hip.set_speculation("auto")
     for i, (out, mask) in enumerate(got):
         want = want_sparse if i == 3 else want_full
         assert torch.equal(mask, want[1]), i
