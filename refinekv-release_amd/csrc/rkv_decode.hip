@@ -8,9 +8,10 @@
 // tiles' slots, decides its blocks (risk, GQA reduction, anchors), folds its
 // representatives, publishes its expanded-block mask, attends an even share
 // of the head's expanded token rows and its slice of the suffix, publishes
-// an (m, l, acc) partial, and the head's last 8 workgroups by ticket merge
-// the partials into the bf16 output.  Other shapes run three kernels over the
-// same workspace:
+// an (m, l, acc) partial, and the head's last W / 8 workgroups (at least 8)
+// by ticket merge the partials into the bf16 output.  Heads with more tiles
+// than workgroups score up to 4 tiles per workgroup in the same launch.
+// Other shapes run three kernels over the same workspace:
 //
 //   score  (tile, h)    one 64-block tile of head h: for every query row the
 //                       selection dot products s = q.k_mean and
