@@ -73,6 +73,9 @@ def parse_args():
     ap.add_argument("--copy-calibration", action="store_true",
                     help="only copy a 64 MiB buffer 5 times (scales rocprofv3 FETCH_SIZE / "
                          "WRITE_SIZE readings to bytes)")
+    ap.add_argument("--summary-only", action="store_true",
+                    help="only build the prefill summary of one layer (--heads, --context, "
+                         "--dim, --block; N(0,1) bf16 K/V) three times (for profiler runs)")
     ap.add_argument("--path", choices=("step", "split"), default="step",
                     help="rkv_decode path: one launch per step (default) or three kernels")
     ap.add_argument("--graph-only", action="store_true",
@@ -183,6 +186,9 @@ def main():
         sys.exit(2)
     if a.copy_calibration:
         copy_calibration()
+        return
+    if a.summary_only:
+        summary_only(a)
         return
     if a.sweep:
         sweep(a)
@@ -727,6 +733,30 @@ def copy_calibration():
         dst.copy_(src)
     torch.cuda.synchronize()
     print(json.dumps({"copy_bytes_read": n, "copy_bytes_written": n, "copies": 5}))
+
+
+def summary_only(a):
+    """build_summary of one layer's prompt, three calls, HIP events around
+    each: the prefill kernels alone, for kernel traces and counters."""
+    from refinekv import RefineKVConfig, build_summary
+
+    gen = torch.Generator(device="cuda").manual_seed(a.seed)
+    shape = (a.heads, a.context, a.dim)
+    k = torch.randn(shape, generator=gen, device="cuda").to(torch.bfloat16)
+    v = torch.randn(shape, generator=gen, device="cuda").to(torch.bfloat16)
+    cfg = RefineKVConfig(backend="hip", block_size=a.block)
+    times = []
+    for _ in range(3):
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        build_summary(k, v, cfg)
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1) * 1e3)
+    print(json.dumps({"summary_us_per_call": [round(t, 1) for t in times],
+                      "bytes_read": 2 * k.numel() * k.element_size(),
+                      "shape": {"heads": a.heads, "tokens": a.context, "dim": a.dim,
+                                "block": a.block}}))
 
 
 def _cpu_model():
