@@ -7,11 +7,11 @@
 // token, so the per-token head_dim sums are lane-local.  Where a block's K
 // and V fit 64 KiB (kStage), the wave first moves the whole block from HBM
 // into LDS with 16-byte buffer-to-LDS loads (all of it in flight at once) and
-// both passes read LDS: HBM sees each row once.  Blocks above 4096 elements
-// per tensor go to a workgroup of block / 16 waves, each staging one 16-token
-// chunk, whose chunk sums wave 0 adds in order (the same sums); blocks whose
-// chunks do not fit either stream pass 1 from global memory and re-read the
-// rows there in pass 2.  Row accesses go
+// both passes read LDS: HBM sees each row once.  Blocks of 32 and 64 tokens
+// go to a workgroup of block / 16 waves instead, each staging one 16-token
+// chunk, whose chunk sums wave 0 adds in order (the same sums); blocks that
+// fit neither stream pass 1 from global memory and re-read the rows there in
+// pass 2.  Row accesses go
 // through per-block buffer views (scalar base and token offset, one lane
 // offset, immediate column offsets: no per-load address arithmetic; rows past
 // the block's end read 0), the block index is wave-uniform, and the min/max
@@ -150,10 +150,10 @@ constexpr int kSummaryWaves = 4;
 constexpr int kTokBatch = 8;  // tokens per batch of pass-1 row loads
 constexpr int64_t kStageWaveMax = 64 * 1024;   // LDS of one staged block, at most
 constexpr int64_t kStageGroupMax = 32 * 1024;  // LDS of a staged workgroup, aimed at
-// One wave stages a block while it holds at most 4096 elements per tensor:
-// larger blocks in one wave leave too few waves per CU (LDS) for their longer
-// passes; they are split into 16-token chunks over a workgroup's waves
-// (summary_split_kernel) instead.
+// One wave stages a block while it holds at most 4096 elements per tensor
+// (larger blocks in one wave leave too few waves per CU for their longer
+// passes); blocks of 32 or more tokens are split into 16-token chunks over a
+// workgroup's waves (summary_split_kernel) whenever that fits.
 constexpr int64_t kStageElemsMax = 4096;
 
 // A staged block in LDS (per wave): its K rows, then its V rows, as 16-byte
@@ -620,8 +620,8 @@ __global__ __launch_bounds__(kWave * kSummaryWaves) void summary_kernel(
                                         value_mean, ellipsoid, value_norm, out);
 }
 
-// Blocks above kStageElemsMax elements per tensor (B 64 at d 128, B 32 at
-// d 160 and up): one workgroup of block / 16 waves per block; wave w moves
+// Blocks of 32 or 64 tokens: one workgroup of block / 16 waves per block
+// (what fits 64 KiB of LDS, with 16 tokens x head_dim <= 4096); wave w moves
 // the block's 16-token chunk w into LDS (all its loads in flight at once) and
 // runs both passes on it, and wave 0 combines the chunks (summary_passes,
 // kSplit), so HBM sees each row once.  LDS: the waves' chunks (K then V, the
@@ -859,11 +859,13 @@ int launch_summary(const void* keys, int64_t k_hs, int64_t k_ts, const void* val
   auto* km = static_cast<uint16_t*>(key_mean);
   auto* vm = static_cast<uint16_t*>(value_mean);
   auto* el = static_cast<uint16_t*>(ellipsoid);
-  // blocks too large to stage in one wave: a workgroup of block / 16 waves
-  // (d 128, B 64, 8 heads of 131072 tokens: 160 -> 124 us, the two-pass
-  // form's re-read of pass 2 gone)
+  // blocks of 32 and 64 tokens: a workgroup of block / 16 waves, a 16-token
+  // chunk each (8 heads of 131072 tokens: d 128, B 64 160 -> 127 us, the
+  // two-pass form's re-read of pass 2 gone; d 128, B 32 118-122 -> 116 us,
+  // d 64, B 64 72 -> 66, d 96, B 32 97 -> 93: half the LDS per wave, twice
+  // the waves per CU); 16-token blocks keep one wave each
   const int64_t split_lds = summary_split_lds(dim, elem, block);
-  if (!stage && block >= 32 && 16 * dim <= kStageElemsMax && split_lds <= kStageWaveMax &&
+  if (block >= 32 && 16 * dim <= kStageElemsMax && split_lds <= kStageWaveMax &&
       rows16(keys, k_hs, k_ts) && rows16(values, v_hs, v_ts)) {
     const dim3 sgrid((unsigned)n_blocks, (unsigned)heads);
     const dim3 sthreads((unsigned)(kWave * (block / 16)));
