@@ -387,6 +387,73 @@ def test_decode_matches_oracle(hip, oracle_lib, decode_path, heads, group, dim, 
                         else 0)
 
 
+def _random_decode_cases(n, seed):
+    """Seeded random decode shapes across what the kernels take: head_dim
+    32..256, groups 1..16, blocks 16/32/64, prompts from a few tokens to a
+    few thousand, eps from 0 to 1e6, every reduction, suffixes 0..39 and
+    optional anchors."""
+    rng = np.random.default_rng(seed)
+    cases = []
+    for _ in range(n):
+        cases.append(dict(
+            dim=int(rng.choice([32, 64, 96, 128, 160, 256])),
+            group=int(rng.choice([1, 2, 3, 4, 5, 7, 8, 12, 16])),
+            heads=int(rng.integers(1, 9)),
+            block=int(rng.choice([16, 32, 64])),
+            prompt=int(rng.choice([rng.integers(1, 200), rng.integers(200, 3000),
+                                   rng.integers(3000, 9000)])),
+            eps=float(rng.choice([0.0, 1e-3, 1e-2, 0.05, 0.3, 1e6])),
+            reduction=str(rng.choice(["mean", "max", "any"])),
+            spikes=float(rng.choice([0.0, 0.02, 0.2])),
+            suffix=int(rng.integers(0, 40)),
+            anchor=bool(rng.integers(0, 2)),
+            seed=int(rng.integers(0, 1 << 30))))
+    return cases
+
+
+def test_random_shapes_match_oracle(hip, oracle_lib, decode_path):
+    """48 seeded random shapes per path: masks equal to the oracle's, outputs
+    within tolerance, hand-off control words clean (two calls per workspace,
+    the second after a launch on it)."""
+    for c in _random_decode_cases(48, 2024):
+        name = str(c)
+        inp = testing.decode_inputs(heads=c["heads"], group=c["group"], dim=c["dim"],
+                                    prompt=c["prompt"], suffix=max(c["suffix"], 1),
+                                    block=c["block"], spike_fraction=c["spikes"], anchors=4,
+                                    seed=c["seed"])
+        inp = {k: (v.to(torch.bfloat16) if v.is_floating_point() else v) for k, v in inp.items()}
+        cfg = RefineKVConfig(backend="hip", block_size=c["block"], eps=c["eps"],
+                             gqa_reduction=c["reduction"])
+        k, v = inp["prompt_keys"], inp["prompt_values"]
+        summary = build_summary(k.to(DEV), v.to(DEV), cfg)
+        n = summary.num_blocks
+        anchor = None
+        if c["anchor"]:
+            g = torch.Generator().manual_seed(c["seed"])
+            anchor = torch.rand(c["heads"], n, generator=g) < 0.1
+        sl = c["suffix"]
+        ws = {}
+        for _ in range(2):
+            res = sparse_attention(inp["query"].to(DEV), summary, inp["suffix_keys"][:, :sl].to(DEV),
+                                   inp["suffix_values"][:, :sl].to(DEV), cfg,
+                                   anchor_mask=anchor.to(DEV) if anchor is not None else None,
+                                   workspace=ws, return_selected=True)
+        torch.cuda.synchronize()
+        out, mask = oracle_lib.sparse_attention(
+            inp["query"][:, :, 0].float().numpy(), oracle_summary_of(summary),
+            _pages_bits(k, c["block"]), _pages_bits(v, c["block"]),
+            gc.bf16_bits(inp["suffix_keys"][:, :sl]), gc.bf16_bits(inp["suffix_values"][:, :sl]),
+            c["eps"], c["reduction"], None if anchor is None else anchor.numpy())
+        assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask), name
+        got = res.output.float().cpu().numpy()[:, :, 0]
+        try:
+            assert_close_output(got, torch.from_numpy(out).to(torch.bfloat16).float().numpy())
+        except AssertionError as err:
+            raise AssertionError(f"{name}: {err}") from None
+        if ws:
+            assert_control_clean(hip, ws)
+
+
 def test_device_suffix_length_matches_slicing(hip, decode_path):
     """tests/test_attention.py:186-204 for the HIP backend: bit-equal outputs."""
     q, keys, values = testing.small_inputs(length=71, dim=128)
