@@ -160,6 +160,30 @@ def test_summary_bit_exact(hip, oracle_lib, dtype, dim, block, length):
     assert_summary_equal(summary, ref)
 
 
+def test_random_summaries_bit_exact(hip, oracle_lib):
+    """30 seeded random (dtype, head_dim, block, length) summaries bit for bit
+    against the oracle: every kernel form (split blocks, one wave per block,
+    the stream for head_dim >= 192, the two-pass form) and partial last
+    blocks."""
+    rng = np.random.default_rng(77)
+    for _ in range(30):
+        dtype = [torch.bfloat16, torch.float16, torch.float32][int(rng.integers(0, 3))]
+        dim = int(rng.choice([32, 64, 96, 128, 160, 192, 224, 256]))
+        block = int(rng.choice([16, 32, 64]))
+        length = int(rng.choice([rng.integers(1, 64), rng.integers(64, 5000)]))
+        heads = int(rng.integers(1, 5))
+        g = torch.Generator().manual_seed(int(rng.integers(0, 1 << 30)))
+        k = (torch.randn(heads, length, dim, generator=g) * 2).to(dtype)
+        v = torch.randn(heads, length, dim, generator=g).to(dtype)
+        ref = oracle_lib.summary(k.float().numpy(), v.float().numpy(), block)
+        summary = build_summary(k.to(DEV), v.to(DEV), RefineKVConfig(backend="hip", block_size=block))
+        torch.cuda.synchronize()
+        try:
+            assert_summary_equal(summary, ref)
+        except AssertionError as err:
+            raise AssertionError(f"{dtype} d{dim} B{block} L{length} H{heads}: {err}") from None
+
+
 def test_summary_of_strided_cache_view(hip, oracle_lib):
     """A prefix view of a larger (1, H, capacity, D) cache, as the hook passes it."""
     _, k, v = testing.small_inputs(length=3000, dim=128, heads=4)
