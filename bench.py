@@ -92,6 +92,9 @@ def parse_args():
                          "through RefineKV(cuda_graph=True) and report per-layer attention "
                          "time and expanded fractions")
     ap.add_argument("--new-tokens", type=int, default=128, help="--model: tokens to generate")
+    ap.add_argument("--phases", action="store_true",
+                    help="phase timeline of the one-launch step (per-workgroup clock stamps from "
+                         "librefinekv_hip_phases.so), then exit")
     return ap.parse_args()
 
 
@@ -189,6 +192,9 @@ def main():
         return
     if a.summary_only:
         summary_only(a)
+        return
+    if a.phases:
+        phase_timeline(a)
         return
     if a.sweep:
         sweep(a)
@@ -420,6 +426,128 @@ def main():
         "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
     }
     print(json.dumps(result), flush=True)
+
+
+# Stamp slots of the phase-stamps build (enum Stamp in csrc/rkv_decode.hip).
+STAMPS = ("entry", "dots", "stats", "gather", "decided", "ring", "pages_wave0", "combine",
+          "published", "merge_start", "merged", "spec", "end", "merge_loaded", "merge_folded",
+          "merge_stored", "merge_counted", "chunk0", "chunk1", "chunk2", "issued2", "fold0_start",
+          "ring_start", "issue2_addr")
+STAMP_ROWS_PER_HEAD = 256
+STAMP_HEADS = 64
+
+
+def phase_timeline(a):
+    """Phase timeline of the one-launch step on the headline workload: the
+    step kernel of librefinekv_hip_phases.so (the same source built with
+    RKV_PHASE_STAMPS) notes a 100 MHz clock in LDS at each phase boundary of
+    every workgroup; after graph replays of one decode step over the layers
+    the last layer's stamps are read back.  Times are microseconds from the
+    launch's first workgroup start."""
+    import numpy as np
+    from refinekv import RefineKVConfig, build_summary, sparse_attention, _hip
+
+    assert torch.cuda.is_available(), "bench.py --phases needs a GPU"
+    _hip.LIB_PATH = os.path.join(os.path.dirname(_hip.LIB_PATH), "librefinekv_hip_phases.so")
+    lib = _hip.lib()
+    lib.rkv_phase_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    layers = min(a.layers, 8)
+    gen = torch.Generator(device=dev).manual_seed(a.seed)
+    cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps, gqa_reduction=a.reduction)
+    stack = []
+    for _ in range(layers):
+        q, k, v = make_layer(gen, a, 128, dev)
+        stack.append((q, k, v, build_summary(k[:, :a.context], v[:, :a.context], cfg), {}))
+    suffix = torch.tensor(a.warmup + a.steps, dtype=torch.int32, device=dev).clamp(max=127)
+
+    def step():
+        r = None
+        for (q, k, v, summ, ws) in stack:
+            r = sparse_attention(q, summ, k[:, a.context:], v[:, a.context:], cfg, workspace=ws,
+                                 suffix_length=suffix, return_selected=True)
+        return r
+
+    step()
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        res = step()
+    for _ in range(20):
+        graph.replay()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    reps = 50
+    start.record()
+    for _ in range(reps):
+        graph.replay()
+    end.record()
+    torch.cuda.synchronize()
+    us = start.elapsed_time(end) * 1e3 / (reps * layers)
+    frac = res.selected.float().mean().item()
+    buf = np.zeros((STAMP_HEADS * STAMP_ROWS_PER_HEAD, len(STAMPS)), np.uint64)
+    assert lib.rkv_phase_stamps_read(buf.ctypes.data, buf.nbytes) == 0
+    lay = (ctypes.c_int64 * 13)()
+    n_blocks = -(-a.context // a.block)
+    _hip._check(lib.rkv_workspace_layout(a.heads, a.group, a.dim, n_blocks, lay),
+                "rkv_workspace_layout")
+    W = int(lay[12])
+    rows = np.concatenate([np.arange(h * STAMP_ROWS_PER_HEAD, h * STAMP_ROWS_PER_HEAD + W)
+                           for h in range(a.heads)])
+    st = buf[rows].astype(np.int64)
+    col = {n: i for i, n in enumerate(STAMPS)}
+    t0 = st[:, col["entry"]].min()
+    t = (st - t0) * 0.01  # 100 MHz clock -> us
+    spec = st[:, col["spec"]] == 1
+    print(f"# step phase timeline: {a.heads} kv heads x {W} workgroups, {a.context} tokens, "
+          f"block {a.block}, eps {a.eps}, {a.spikes:.0%} spikes; graph {us:.2f} us/layer-step "
+          f"(phases build), last layer f {frac:.4f}, speculating workgroups {int(spec.sum())}")
+    print("| phase (thread 0 of each workgroup unless noted) | mean us | p10 | p50 | p90 | max "
+          "| ends mean | ends max |")
+    print("|---|---|---|---|---|---|---|---|")
+    seq = [("entry", "dots", "score: q staging, summary loads, dot products"),
+           ("dots", "stats", "statistics, LSE slots out, decision-independent loads issued"),
+           ("stats", "gather", "wait for the head's LSE slots (wave 0, row 0)"),
+           ("gather", "decided", "LSE merge, risk, GQA reduction, mask"),
+           ("decided", "ring", "representative, suffix and page-row chunks (wave 0)"),
+           ("ring", "pages_wave0", "mask and speculation flag stores"),
+           ("pages_wave0", "combine", "waiting for the other waves' page rows"),
+           ("combine", "published", "combine, partial slots out")]
+    for a0, a1, name in seq:
+        d = t[:, col[a1]] - t[:, col[a0]]
+        e = t[:, col[a1]]
+        qs = np.quantile(d, [0.1, 0.5, 0.9])
+        print(f"| {name} | {d.mean():.2f} | {qs[0]:.2f} | {qs[1]:.2f} | {qs[2]:.2f} | "
+              f"{d.max():.2f} | {e.mean():.2f} | {e.max():.2f} |")
+    for a0, a1, name in (("merge_start", "merge_loaded", "mergers: poll until the head's partials are in, fold own lanes' partials"),
+                         ("merge_loaded", "merge_folded", "mergers: folds across lanes"),
+                         ("merge_folded", "merge_stored", "mergers: give-up check, normalize, bf16 store"),
+                         ("merge_stored", "merge_counted", "mergers: access count (slice 0)"),
+                         ("decided", "ring_start", "ring: set-up after the decision"),
+                         ("ring_start", "issue2_addr", "ring: chunk 2's rows found"),
+                         ("issue2_addr", "issued2", "ring: chunk 2's loads issued"),
+                         ("issued2", "fold0_start", "ring: wait for chunk 0"),
+                         ("fold0_start", "chunk0", "ring: chunk 0 fold"),
+                         ("decided", "chunk0", "ring: wave 0's first chunk folded"),
+                         ("chunk0", "chunk1", "ring: wave 0's second chunk"),
+                         ("chunk1", "chunk2", "ring: wave 0's third chunk")):
+        mm = (st[:, col[a1]] > 0) & (st[:, col[a0]] > 0)
+        d = t[mm][:, col[a1]] - t[mm][:, col[a0]]
+        e = t[mm][:, col[a1]]
+        if len(d):
+            print(f"| {name} ({int(mm.sum())}) | {d.mean():.2f} | | | | {d.max():.2f} | "
+                  f"{e.mean():.2f} | {e.max():.2f} |")
+    ends = t[:, col["end"]]
+    print(f"\nworkgroup starts {t[:, 0].min():.2f}..{t[:, 0].max():.2f} us, ends "
+          f"{ends.min():.2f}..{ends.max():.2f} us")
+    by_head = ends.reshape(a.heads, W).max(1)
+    print("last end per head (us): " + ", ".join(f"{x:.2f}" for x in by_head))
+    dots_by_head = t[:, col["dots"]].reshape(a.heads, W).mean(1)
+    print("score end per head, mean (us): " + ", ".join(f"{x:.2f}" for x in dots_by_head))
+    print(json.dumps(dict(phases_us_per_layer_step=round(us, 3), workgroups=int(len(rows)),
+                          last_end_us=round(float(ends.max()), 2),
+                          expanded_fraction=round(frac, 5))))
 
 
 def sweep(a):

@@ -218,11 +218,14 @@ int rkv_set_decode_path(int path);
  * and results are rkv_decode's, minus the workspace: the library keeps one
  * 64 MiB device array per GPU for the call's intermediates (allocated with
  * the library, held until the process ends) and allocates nothing.  Shapes
- * whose rkv_workspace_bytes exceed 64 MiB return RKV_WORKSPACE_TOO_SMALL.
- * Each call first clears the array's hand-off counters and slots with a fill
- * kernel on `stream`, so calls of different shapes may follow each other on
- * one stream; calls that overlap on one GPU (other streams or threads) race
- * on the shared array and must not be issued.
+ * whose rkv_workspace_bytes exceed 64 MiB - 256 bytes return
+ * RKV_WORKSPACE_TOO_SMALL.  Each call first clears the array's hand-off
+ * counters and slots with fill kernels on `stream`, so calls of different
+ * shapes may follow each other on one stream; calls that overlap on one GPU
+ * (other streams or threads) race on the shared array and must not be
+ * issued.  A hand-off wait that gives up writes NaN output rows and an
+ * all-expanded mask for its head, as rkv_decode does, and sets the array's
+ * own status word (rkv_static_status), which no later call clears.
  */
 int rkv_decode_static(const void* query, const void* key_mean, const void* ellipsoid,
                       const void* value_mean, const float* value_norm,
@@ -237,13 +240,22 @@ int rkv_decode_static(const void* query, const void* key_mean, const void* ellip
                       int reduction, const uint8_t* anchor_mask, uint8_t* mask_out,
                       void* output, unsigned long long* accessed_blocks, rkv_stream_t stream);
 
+/* The status word of rkv_decode_static's array on the current device (part
+ * of that entry point, for the same callers; no reference counterpart):
+ * *status receives it (bit 0: a hand-off wait of a static call gave up since
+ * the word was last cleared), with clear != 0 it is then zeroed.  Copies the
+ * word to the host and synchronizes `stream` (not for graph capture). */
+int rkv_static_status(uint32_t* status, int clear, rkv_stream_t stream);
+
 /* Hand-off status of an rkv_decode workspace (no reference counterpart: the
  * reference's Triton kernels have no cross-workgroup waits).  *status
  * receives the workspace's sticky status word: bit 0 is set when a wait of
- * the one-launch step gave up after its poll limit, in which case that
- * call's output and mask are not to be trusted.  Copies the word to the host
- * and synchronizes `stream` (a debugging query: not for graph capture).
- * The shape arguments are those the workspace was sized for. */
+ * the one-launch step gave up after its poll limit.  The call that gave up
+ * also wrote NaN to the head's output rows and marked all its blocks
+ * expanded, so its result is not a plausible answer either way.  Copies the
+ * word to the host and synchronizes `stream` (a debugging query: not for
+ * graph capture).  The shape arguments are those the workspace was sized
+ * for. */
 int rkv_workspace_status(const void* workspace, size_t workspace_bytes, int64_t heads,
                          int64_t group, int64_t dim, int64_t n_blocks, uint32_t* status,
                          rkv_stream_t stream);
@@ -267,18 +279,18 @@ int rkv_decode_plan(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
 /* Test hook with no reference counterpart: spin_limit replaces the one-launch
  * step's poll limit per hand-off wait (0 = the default, 2^20), and a nonzero
  * skew makes every wait accept no published data, so each wait runs out its
- * limit, sets the status word and goes on; every kernel still ends.  Per
- * thread; (0, 0) restores normal operation. */
+ * limit, sets the status word and goes on (NaN output, all-expanded mask);
+ * every kernel still ends.  Per thread; (0, 0) restores normal operation. */
 int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew);
 
 /* Test hook with no reference counterpart: the one-launch step's
- * speculation, 0 off, 1 (default) where a workgroup's share of a head's
- * token rows is at least 2048, 2 for every shape; other modes return
+ * speculation, 0 off, 1 (default), 2 forced (the same as 1 since it has no
+ * size threshold any more; kept for the tests); other modes return
  * RKV_INVALID_ARGUMENT.  When the previous launch on a workspace expanded
- * every block of a head, the step's workgroups of that head attend their
- * share of all its token rows before the decision and keep the result if
- * every block expands again (else they attend as usual): the output is the
- * same bit for bit either way.  Per thread. */
+ * every block of a workgroup's tile, the workgroup issues the first page
+ * rows of the tile before the decision and continues from them if every
+ * block expands again (else it lets them land and attends as usual): the
+ * output is the same bit for bit either way.  Per thread. */
 int rkv_set_speculation(int mode);
 
 /* Test hook with no reference counterpart: applies the kernels' device

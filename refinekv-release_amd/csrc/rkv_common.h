@@ -291,6 +291,9 @@ struct Coherent {
   __device__ void store_u32(uint32_t off, uint32_t x) const {
     __builtin_amdgcn_raw_buffer_store_b32(x, r, (int)off, 0, kCoherentPolicy);
   }
+  __device__ void store_u8(uint32_t off, uint8_t x) const {
+    __builtin_amdgcn_raw_buffer_store_b8(x, r, (int)off, 0, kCoherentPolicy);
+  }
   __device__ uint64_t load_u64(uint32_t off) const {
     const auto v = __builtin_amdgcn_raw_buffer_load_b64(r, (int)off, 0, kCoherentPolicy);
     return (uint64_t)v[0] | ((uint64_t)v[1] << 32);

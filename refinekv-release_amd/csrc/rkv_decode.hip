@@ -64,6 +64,32 @@ __host__ __device__ constexpr int64_t control_bytes(int64_t heads, int64_t tile_
   return (heads + 1) * kLine * 8 + heads * tile_stride * 8;
 }
 
+// Phase stamps of the one-launch step (the library built with
+// RKV_PHASE_STAMPS only; bench.py --phases loads it): lane 0 of a wave notes
+// the 100 MHz constant clock (s_memrealtime) in LDS at each phase boundary
+// of its workgroup, and the workgroup copies its stamps to rkv_stamps
+// (row h * 256 + workgroup) as it ends.  LDS stores leave the vector-memory
+// counters alone, so the kernel's own waits are unchanged.  The product build
+// compiles every stamp to nothing.
+constexpr int kStamps = 24;
+constexpr int kStampRowsPerHead = 256;
+enum Stamp {
+  kStEntry = 0, kStDots, kStStats, kStGather, kStDecided, kStRing, kStPagesWave0, kStCombine,
+  kStPublished, kStMergeWait, kStMerged, kStSpec, kStEnd, kStMergeLoaded,
+  kStMergeFolded, kStMergeStored, kStMergeCounted, kStChunk0, kStChunk1, kStChunk2,
+  kStIssued2, kStFold0Start, kStRingStart, kStIssue2Addr
+};
+#if defined(RKV_PHASE_STAMPS)
+constexpr int kStampHeads = 64;
+__device__ unsigned long long rkv_stamps[kStampHeads * kStampRowsPerHead][kStamps];
+#define RKV_STAMP(stamps, i, cond)                                                   \
+  do {                                                                               \
+    if ((stamps) != nullptr && (cond)) (stamps)[i] = __builtin_amdgcn_s_memrealtime(); \
+  } while (0)
+#else
+#define RKV_STAMP(stamps, i, cond) ((void)0)
+#endif
+
 // Optional profiling events (rkv_set_profile_events): events[0] is recorded
 // before the first kernel of a call and events[k] after its k-th kernel.
 thread_local hipEvent_t* g_events = nullptr;
@@ -92,7 +118,7 @@ struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
   int64_t step_workers;  // workgroups per head of the one-launch step
   int64_t step_tiles;    // tiles its workgroups score, at most (1: one each)
-  int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, xbits, total;
+  int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, full, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -135,10 +161,14 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.zf = take(rows * L.z_stride * 16);
   L.lse = take(rows * L.tile_stride * 4 * 4);
   L.lse_slots = take(rows * L.tile_stride * 2 * 16);
-  L.part_ml = take(rows * L.tile_stride * 8);
-  L.part_acc = take(rows * L.tile_stride * dim * 4);
-  L.counts = take(heads * L.tile_stride * 4);
-  L.xbits = take(heads * L.tile_stride * 16);
+  // partials and access counts: the one-launch step's tagged 16-byte slots
+  // (one per row for (m, l), one per row and column pair for acc, one per
+  // workgroup for the count); the three kernels use the first half or
+  // quarter of each region as plain (m, l) pairs, floats and u32 counts
+  L.part_ml = take(rows * L.tile_stride * 16);
+  L.part_acc = take(rows * L.tile_stride * dim * 8);
+  L.counts = take(heads * L.tile_stride * 16);
+  L.full = take(heads * L.tile_stride * 8);
   L.total = off;
   return L;
 }
@@ -632,11 +662,24 @@ struct StepStats {
   const uint32_t* rtag;       // LDS: the tag its waits accept (the same, unless a test skews it)
   uint32_t* error;
   uint32_t spin;              // polls before a wait gives up
+  unsigned long long* stamps;  // LDS phase stamps (RKV_PHASE_STAMPS build) or null
+  uint32_t* gave_up;          // LDS: nonzero once a wait of this workgroup gave up
 };
+
+// A wait of the one-launch step gave up: the sticky error bit, and the
+// workgroup's own flag, which makes its attention partial NaN (so the
+// head's merged output is NaN and its mergers mark every block expanded).
+// (lane 0 only; a rare path)
+__device__ __forceinline__ void handoff_gave_up(const StepStats& ss) {
+  __hip_atomic_fetch_or(ss.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (ss.gave_up != nullptr) *ss.gave_up = 1u;
+}
 
 // One row's LSE partials of the head's T tiles (lane t holds tiles t + 64 k)
 // from the tagged slots, read until every slot carries this launch's tag
-// (at most ss.spin rounds, then the error word is set).
+// (at most ss.spin rounds; then the wait is recorded as given up and the
+// partials come back NaN, so log Z and log C are not finite and the
+// decision's fail-safe expands every block).
 struct RowLse {
   float zm[kChunks], zl[kChunks], cm[kChunks], cl[kChunks];
 };
@@ -665,7 +708,10 @@ __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, u
     }
     if (__ballot(!ok) == 0) break;
     if (n + 1 >= ss.spin) {
-      if (lane == 0) __hip_atomic_fetch_or(ss.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+      if (lane == 0) handoff_gave_up(ss);
+      const float nan = bits_f32(0x7FC00000u);
+#pragma unroll
+      for (int k = 0; k < kChunks; ++k) r.zm[k] = r.cm[k] = nan;
       break;
     }
     __builtin_amdgcn_s_sleep(1);
@@ -720,7 +766,9 @@ __device__ __forceinline__ uint32_t tile_access_count(const DecideArgs& a, int64
   return (uint32_t)c;
 }
 
-template <bool kFused = false>
+// kMask = false leaves the mask store to the caller (the attention stores it
+// after its loads are issued).
+template <bool kFused = false, bool kMask = true>
 __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
                                                   const DecideLoads& in, DecideShared& sh,
                                                   float (*zsh)[kTile], const int32_t*& list,
@@ -764,6 +812,7 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
 #pragma unroll 1
     for (int g = wave; g < G; g += kWaves) {
       const RowLse rl = gather_lse(*ss, (h * G + g) * a.tile_stride, (uint32_t)T, lane);
+      RKV_STAMP(ss->stamps, kStGather, g == 0 && lane == 0);
       const float2 lzc = merge_lse_pair(rl, (uint32_t)T, lane);
       row_tail(g, lzc.x, lzc.y, ss->zs[g][lane]);
     }
@@ -816,7 +865,7 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
   }
   list = sh.list[wave];
   if (wave == 0) {
-    if (valid && owner && a.write_mask) a.mask[h * N + b] = sel ? 1 : 0;
+    if (kMask && valid && owner && a.write_mask) a.mask[h * N + b] = sel ? 1 : 0;
     count = tile_access_count(a, tile, bits);
   }
   return bits;
@@ -839,7 +888,7 @@ struct TileSet {
 // wave's row's log Z / log C from the head's tagged slots once, then, tile
 // by tile, decide_finish's risk, reduction, fail-safes, anchors, mask and
 // access count (summed into count, thread 0).  bits[m]: tile m's expanded
-// blocks, uniform over the workgroup.
+// blocks, uniform over the workgroup (the caller stores the masks).
 template <int kTiles, int GBM>
 __device__ __forceinline__ void decide_tiles(const DecideArgs& a, int64_t h, uint32_t wk,
                                              uint32_t W, const TileSet<kTiles, GBM>& ts,
@@ -854,6 +903,7 @@ __device__ __forceinline__ void decide_tiles(const DecideArgs& a, int64_t h, uin
   bool bad = false;
   if (wave < G) {
     const RowLse rl = gather_lse(ss, (h * G + wave) * a.tile_stride, (uint32_t)T, lane);
+    RKV_STAMP(ss.stamps, kStGather, wave == 0 && lane == 0);
     const float2 lzc = merge_lse_pair(rl, (uint32_t)T, lane);
     lz = lzc.x;
     lc = lzc.y;
@@ -906,10 +956,7 @@ __device__ __forceinline__ void decide_tiles(const DecideArgs& a, int64_t h, uin
     sel = (sel || bad_global || anchored) && valid;
     bits[m] = __ballot(sel);
     if (tid == 0) sh.tile_bits[m] = bits[m];
-    if (wave == 0) {
-      if (valid && a.write_mask) a.mask[h * N + b] = sel ? 1 : 0;
-      count += tile_access_count(a, tile, bits[m]);
-    }
+    if (wave == 0) count += tile_access_count(a, tile, bits[m]);
     __syncthreads();  // (sh is written again for the next tile)
   }
 }
@@ -1438,19 +1485,19 @@ __device__ __forceinline__ void mma_combine(const MmaCombine<D, GBM>& cmb, int g
 // One-launch step: hand-off counters and the merge of a head by its last tile
 // ---------------------------------------------------------------------------
 // Hand-offs between the tiles of a head.  Counters (u64 at the start of
-// the workspace): head h owns the 64-byte line at counter kLine * h, whose
-// [1] counts tiles that have published their attention partials and whose
-// [2] holds e + 2 when launch e expanded every block of the head (read by
-// launch e + 1, whose workgroups then speculate); after the
-// heads' lines, a line holding a sticky u32 error word (bit 0: a wait gave up
-// after its poll limit) and, at [1], the launches' workgroup ticket count;
-// then one launch counter per workgroup.  Nothing is reset: each launch adds
-// one to every workgroup's counter and W (workgroups per head) to each
-// head's, so a workgroup's own counter (old value) is the launch's epoch e,
-// e + 1 tags the slots it publishes (LSE partials, expanded-block masks:
-// readers poll the slots themselves) and (e + 1) W is the merge count it
-// waits for.  This needs the workspace zero-filled once when created and
-// used for one shape thereafter.
+// the workspace): a 64-byte line per head (unused); after the heads' lines,
+// a line holding a sticky u32 error
+// word (bit 0: a wait gave up after its poll limit; the static-scratch entry
+// point keeps its own word) and, at [1], the launches' workgroup ticket
+// count; then one launch counter per workgroup.  Nothing is reset: each
+// launch adds one to every workgroup's counter, so a workgroup's own counter
+// (old value) is the launch's epoch e, and e + 1 tags the slots it publishes
+// (LSE partials, attention partials, access counts: readers poll the slots
+// themselves).
+// Each workgroup also leaves e + 2 in its flag of the `full` region when
+// launch e expanded every block of its tile (read by launch e + 1, which
+// then speculates).  This needs the workspace zero-filled once when created
+// and used for one shape thereafter.
 //
 // Progress: a workgroup waits only for the workgroups of its own head, and
 // only after publishing what they wait for from it.  When the whole grid fits
@@ -1466,236 +1513,174 @@ __device__ __forceinline__ void mma_combine(const MmaCombine<D, GBM>& cmb, int g
 
 struct StepCtx {
   StepStats stats;
-  Coherent ml, acc, counts;       // partial (m, l), partial acc, tile counts
-  uint64_t* control;
+  Coherent ml, acc, counts;       // tagged slots: partial (m, l), partial acc, tile counts
+  Coherent mask;                  // (H, N) expanded-block mask (write-through stores)
   uint16_t* out;                  // (H, G, D) bf16
   unsigned long long* accessed;   // or null
-  uint32_t* flag;                 // one LDS word
   unsigned long long* wsum;       // kWaves LDS words
-  uint64_t* base;                 // LDS: epoch * n_tiles (thread 0's copy)
-  Coherent xbits;                 // (H, tile_stride) expanded-block masks
-  int32_t* xl;                    // LDS: blocks of this workgroup's expanded-row share
-  uint32_t xl_cap;                // xl's entries
-  uint32_t* xr;                   // LDS: the share's first row and row count
-  int heads;
-  uint32_t skew;                  // 0; a test's nonzero value makes every wait run out
+  uint64_t* full;                 // this workgroup's flag: the launch whose tile fully expanded
   const uint32_t* spec;           // LDS: nonzero when the launch speculates (or null)
-  __device__ uint32_t* error() const {
-    return reinterpret_cast<uint32_t*>(control + (int64_t)heads * kLine);
-  }
 };
 
-// Inclusive prefix sum over the wave.
-__device__ __forceinline__ uint32_t wave_inclusive_sum(uint32_t v) {
-  const int lane = threadIdx.x % kWave;
-#pragma unroll
-  for (int o = 1; o < kWave; o <<= 1) {
-    const uint32_t u = __shfl_up(v, o, kWave);
-    if (lane >= o) v += u;
-  }
-  return v;
-}
-
-// One wave of a step workgroup: this workgroup's share of its head's
-// expanded token rows.  The head's expanded blocks, in (tile, block) order,
-// give B rows each (R rows in all) and workgroup w of the W attends rows
-// [w R / W, (w + 1) R / W), so every workgroup of the head gets the same
-// number of rows (+-1) wherever the expanded blocks sit.  From the T
-// published masks: xl[i] = the block (index in the head) of ordinal e0 + i
-// for the ordinals the share touches, xr = (first row, row count).  Integer
-// arithmetic only: every workgroup sees the same split.  A share touches at
-// most R / (W B) + 2 <= 64 ceil(T / W) + 2 blocks (R <= 64 T B), which
-// sx.xl_cap covers (an entry past it would set the error word instead).
-__device__ void expanded_share(const StepCtx& sx, int64_t h, int64_t ts, uint32_t T,
-                               uint32_t W, uint32_t tile, int lb, uint64_t last_bits,
-                               uint32_t N) {
-  const int lane = threadIdx.x % kWave;
-  const uint32_t tag = __builtin_amdgcn_readfirstlane(*sx.stats.rtag), mix = tag_mix(tag);
-  uint64_t bm[kChunks];
-  uint32_t cnt[kChunks], first[kChunks];
-  // the head's tagged masks, read until every one has landed (a mask is
-  // taken as read even when a wait gives up, so the last tile's bits are
-  // cut to its blocks: every row address below stays inside the pages)
-  for (uint32_t n = 0;; ++n) {
-    bool ok = true;
-#pragma unroll
-    for (int k = 0; k < kChunks; ++k) {
-      const uint32_t t = k * kWave + lane;
-      bm[k] = 0ull;
-      if (k * kWave < (int)T) {
-        const float4 v = sx.xbits.load4((uint32_t)((h * ts + (t < T ? t : 0u)) * 16));
-        if (t < T) {
-          ok = ok && slot_ok(v, tag, mix);
-          bm[k] = (uint64_t)f32_bits(v.x) | ((uint64_t)f32_bits(v.y) << 32);
-          if (t == T - 1) bm[k] &= last_bits;
-        }
-      }
-    }
-    if (__ballot(!ok) == 0) break;
-    if (n + 1 >= sx.stats.spin) {
-      if (lane == 0)
-        __hip_atomic_fetch_or(sx.stats.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-      break;
-    }
-    __builtin_amdgcn_s_sleep(1);
-  }
-#pragma unroll
-  for (int k = 0; k < kChunks; ++k) cnt[k] = (uint32_t)__popcll(bm[k]);
-  uint32_t total = 0;
-#pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
-    const uint32_t incl = wave_inclusive_sum(cnt[k]);
-    first[k] = total + incl - cnt[k];
-    total += (uint32_t)__builtin_amdgcn_readlane((int)incl, kWave - 1);
-  }
-  const uint64_t R = (uint64_t)total << lb;
-  const uint64_t r0 = (uint64_t)tile * R / W, r1 = ((uint64_t)tile + 1) * R / W;
-  const uint32_t e0 = (uint32_t)(r0 >> lb);
-  const uint32_t e1 = (uint32_t)((r1 + (1u << lb) - 1) >> lb);
-  // every tile whose ordinals meet [e0, e1), one at a time, its 64 blocks
-  // over the 64 lanes: lane i's block, if expanded, has ordinal first +
-  // (expanded blocks of the tile below i)
-#pragma unroll
-  for (int k = 0; k < kChunks; ++k) {
-    const uint32_t lo = first[k] > e0 ? first[k] : e0;
-    const uint32_t end = first[k] + cnt[k];
-    const uint32_t hi = end < e1 ? end : e1;
-    uint64_t meet = __ballot(lo < hi);
-    while (meet != 0) {
-      const int src = __builtin_ctzll(meet);
-      meet &= meet - 1ull;
-      const uint64_t m = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)bm[k], src)) |
-                         ((uint64_t)(uint32_t)__builtin_amdgcn_readlane((int)(bm[k] >> 32), src)
-                          << 32);
-      const uint32_t f = (uint32_t)__builtin_amdgcn_readlane((int)first[k], src);
-      if ((m >> lane) & 1ull) {
-        const uint32_t e = f + (uint32_t)__popcll(m & ((1ull << lane) - 1ull));
-        if (e >= e0 && e < e1) {
-          if (e - e0 < sx.xl_cap)
-            sx.xl[e - e0] = (int32_t)((uint32_t)(k * kWave + src) * kTile + (uint32_t)lane);
-          else
-            __hip_atomic_fetch_or(sx.stats.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-        }
-      }
-    }
-  }
-  if (lane == 0) {
-    sx.xr[0] = (uint32_t)r0;
-    sx.xr[1] = (uint32_t)(r1 - r0);
-    sx.xr[2] = total == N ? 1u : 0u;  // every block of the head expanded
-  }
-}
-
-constexpr int kMergeBatch = 8;  // partials per lane per batch of loads
-
-// Folds state (m2, d2, n2) into (mx, num, den); empty states (den 0) are
-// skipped.
-__device__ __forceinline__ void merge_state4(float m2, float d2, const float4& n2, float& mx,
-                                             float4& num, float& den) {
-  if (!(d2 > 0.0f)) return;
-  if (!(den > 0.0f)) {
-    mx = m2;
-    den = d2;
-    num = n2;
-    return;
-  }
+// Folds state (m2, d2, (n2a, n2b)) into (mx, den, (na, nb)) in one
+// branch-free form: an empty state (m = -inf, d = 0) weighs 0, and from the
+// empty initial state the first fold copies exactly (fma(d2, 1, 0 x 0) =
+// d2), so the result is that of skipping empty states and copying the
+// first.
+__device__ __forceinline__ void merge_state2(float m2, float d2, float n2a, float n2b, float& mx,
+                                             float& den, float& na, float& nb) {
   const float M = fmaxf(mx, m2);
-  const float ea = __builtin_amdgcn_exp2f((mx - M) * kLog2e);
-  const float eb = __builtin_amdgcn_exp2f((m2 - M) * kLog2e);
+  const float ms = M == kNegInf ? 0.0f : M;
+  const float ea = __builtin_amdgcn_exp2f((mx - ms) * kLog2e);
+  const float eb = __builtin_amdgcn_exp2f((m2 - ms) * kLog2e);
   den = __builtin_fmaf(d2, eb, den * ea);
-  num.x = __builtin_fmaf(n2.x, eb, num.x * ea);
-  num.y = __builtin_fmaf(n2.y, eb, num.y * ea);
-  num.z = __builtin_fmaf(n2.z, eb, num.z * ea);
-  num.w = __builtin_fmaf(n2.w, eb, num.w * ea);
+  na = __builtin_fmaf(n2a, eb, na * ea);
+  nb = __builtin_fmaf(n2b, eb, nb * ea);
   mx = M;
 }
 
-// The head's last K workgroups (by ticket; K = mergers(W)) merge it, each a
-// slice of the columns, once every workgroup of the head has published.  Slice m: head h's
-// rows, column quads [m Q / K, (m + 1) Q / K), from every tile's partial ->
-// bf16 output; slice 0 also adds the head's access count.  Each (row, 4
-// columns) unit is merged by S adjacent lanes (S a power of two <= 16, so a
-// unit sits inside a 16-lane row; tiles s, s + S, ... each), then a tree
-// over the S lanes into the unit's last lane (DPP row shifts): a fixed
-// order, so outputs repeat bit for bit.
+// The merge of a head's partials.  Every workgroup publishes its partial as
+// tagged slots (the LSE slots' format and tag): per query row one slot
+// (m, l) and one per column pair (acc[2p], acc[2p + 1]), and one slot with
+// its access count.  The head's last K = mergers(W) workgroups by index each
+// merge a column slice: slice m covers pairs [m P / K, (m + 1) P / K) of
+// every row (P = D / 2).  A merger polls the slots it needs until every one
+// carries this launch's tag, reloading only those still missing, so after
+// the head's slowest workgroup publishes, one round trip brings in what is
+// left.  Each (row, pair) unit is merged by S adjacent lanes (S a power of
+// two <= 16, so a unit sits inside a 16-lane row; partials s, s + S, ... in
+// order, in batches of kMergeHeld per lane), then a tree over the S lanes
+// into the unit's last lane (DPP row shifts): a fixed order, so outputs
+// repeat bit for bit.  Slice 0 also adds the head's access count.
 constexpr int kMergers = 8;
+constexpr int kMergeHeld = 8;  // partials a lane holds per batch
 
 // Mergers of a head of W workgroups: W / 8, at least 8 (or W) -- the slices
 // shrink as the partials to fold per slice grow.
-__device__ __forceinline__ uint32_t mergers(uint32_t W) {
+__host__ __device__ __forceinline__ uint32_t mergers(uint32_t W) {
   const uint32_t k = W / 8u > (uint32_t)kMergers ? W / 8u : (uint32_t)kMergers;
   return W < k ? W : k;
 }
 
+// Byte offsets of a partial's slots: (row r of the head, workgroup t) at
+// ml_slot(r, t) in the ml region and at acc_slot(r, t, p) in the acc region.
+__host__ __device__ __forceinline__ uint32_t ml_slot(int64_t row_ts, uint32_t t) {
+  return (uint32_t)((row_ts + t) * 16);
+}
+template <int D>
+__device__ __forceinline__ uint32_t acc_slot(int64_t row_ts, uint32_t t, uint32_t p) {
+  return (uint32_t)(((row_ts + t) * (D / 2) + p) * 16);
+}
+
+// If a wait of the head gave up (that workgroup's partial carries NaN, which
+// the fold carries into every unit) or this merger's own poll does, the
+// slice is written as NaN and slice 0 marks every block of the head
+// expanded.
 template <int D>
 __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, int m, int K) {
+  unsigned long long* const stamps = sx.stats.stamps;
+  (void)stamps;
   const DecideArgs& da = a.decide;
-  // the head's partials: one per workgroup of the launch
-  const int G = da.group, T = a.workers;
+  const int G = da.group, W = a.workers;  // the head's partials: one per workgroup
   const int64_t ts = da.tile_stride;
   const int tid = threadIdx.x;
-  constexpr int Q = D / 4;
-  const int q0 = m * Q / K, nq = (m + 1) * Q / K - q0;
-  const int units = G * nq;
+  constexpr int P = D / 2;
+  const int p0 = m * P / K, np = (m + 1) * P / K - p0;
+  const int units = G * np;
   int S = 1;
   while (S * 2 * units <= kThreads && S < 16) S *= 2;
-  // slice 0 also adds the head's access count: the counts of its
-  // min(n_tiles, W) workgroups that score distinct tiles (at most
-  // kStepMaxTiles <= kThreads) are loaded ahead of the partials, so they
-  // land with them
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(*sx.stats.rtag), mix = tag_mix(tag);
+  bool gave_up = false, poisoned = false;
+  auto give_up = [&]() {
+    if (!gave_up)
+      __hip_atomic_fetch_or(sx.stats.error, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    gave_up = true;
+  };
+  // slice 0 also sums the access counts of the min(n_tiles, W) workgroups
+  // that decide distinct tiles (at most kStepMaxTiles <= kThreads), one per
+  // thread
   const bool counting = sx.accessed && m == 0;
-  const int n_counts = (int)da.n_tiles < T ? (int)da.n_tiles : T;
+  const int n_counts = (int)da.n_tiles < W ? (int)da.n_tiles : W;
   uint32_t tile_count = 0;
-  if (counting && tid < n_counts)
-    tile_count = sx.counts.load_u32((uint32_t)((h * ts + tid) * 4));
+  if (counting && tid < n_counts) {
+    for (uint32_t n = 0;; ++n) {
+      const float4 c = sx.counts.load4((uint32_t)((h * ts + tid) * 16));
+      if (slot_ok(c, tag, mix)) {
+        tile_count = f32_bits(c.x);
+        break;
+      }
+      if (n + 1 >= sx.stats.spin) {
+        give_up();
+        break;
+      }
+      __builtin_amdgcn_s_sleep(2);
+    }
+  }
   for (int u0 = 0; u0 < units; u0 += kThreads / S) {
     const int u = u0 + tid / S, sl = tid % S;
     const int uc = u < units ? u : units - 1;
-    const int g = uc / nq, q = q0 + uc % nq;
+    const int g = uc / np, pp = p0 + uc % np;
     const int64_t row = (h * G + g) * ts;
-    float mx = kNegInf, den = 0.0f;
-    float4 num = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-    // partials t0, t0 + S, ... (nb of them), loaded together; lanes past T
-    // load nothing and fold an empty state
-    auto batch = [&](auto nb, int t0) {
-      constexpr int NB = decltype(nb)::value;
-      float2 ml[NB];
-      float4 av[NB];
+    float mx = kNegInf, den = 0.0f, na = 0.0f, nb = 0.0f;
+    for (int t0 = sl; t0 < W; t0 += S * kMergeHeld) {
+      float4 ml[kMergeHeld], av[kMergeHeld];
+      uint32_t need = 0;  // bit k: partial t0 + S k exists and has not landed
 #pragma unroll
-      for (int k = 0; k < NB; ++k) {
-        const int t = t0 + k * S;
-        ml[k] = make_float2(kNegInf, 0.0f);
+      for (int k = 0; k < kMergeHeld; ++k) {
+        ml[k] = make_float4(kNegInf, 0.0f, 0.0f, 0.0f);
         av[k] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
-        if (t < T) {
-          ml[k] = sx.ml.load2((uint32_t)((row + t) * 8));
-          av[k] = sx.acc.load4((uint32_t)(((row + t) * D + 4 * q) * 4));
+        if (t0 + S * k < W) need |= 1u << k;
+      }
+      for (uint32_t n = 0;; ++n) {
+#pragma unroll
+        for (int k = 0; k < kMergeHeld; ++k) {
+          if ((need >> k) & 1u) {
+            const uint32_t t = (uint32_t)(t0 + S * k);
+            ml[k] = sx.ml.load4(ml_slot(row, t));
+            av[k] = sx.acc.load4(acc_slot<D>(row, t, (uint32_t)pp));
+          }
         }
+#pragma unroll
+        for (int k = 0; k < kMergeHeld; ++k)
+          if (((need >> k) & 1u) && slot_ok(ml[k], tag, mix) && slot_ok(av[k], tag, mix))
+            need &= ~(1u << k);
+        if (__ballot(need != 0u) == 0) break;
+        if (n + 1 >= sx.stats.spin) {
+          give_up();
+          break;
+        }
+        __builtin_amdgcn_s_sleep(2);
       }
 #pragma unroll
-      for (int k = 0; k < NB; ++k) merge_state4(ml[k].x, ml[k].y, av[k], mx, num, den);
-    };
-    // (the common case, T <= 4 S: one batch of four)
-    if (T <= 4 * S) {
-      batch(std::integral_constant<int, 4>{}, sl);
-    } else {
-      for (int t0 = sl; t0 < T; t0 += S * kMergeBatch)
-        batch(std::integral_constant<int, kMergeBatch>{}, t0);
+      for (int k = 0; k < kMergeHeld; ++k)
+        if (t0 + S * k < W) merge_state2(ml[k].x, ml[k].y, av[k].x, av[k].y, mx, den, na, nb);
     }
+    RKV_STAMP(stamps, kStMergeLoaded, tid == 0);
     auto fold_from = [&](auto shift) {
-      const float m2 = shift(mx), d2 = shift(den);
-      const float4 n2 = make_float4(shift(num.x), shift(num.y), shift(num.z), shift(num.w));
-      merge_state4(m2, d2, n2, mx, num, den);
+      merge_state2(shift(mx), shift(den), shift(na), shift(nb), mx, den, na, nb);
     };
     if (S > 8) fold_from([](float v) { return row_shr<8>(v); });
     if (S > 4) fold_from([](float v) { return row_shr<4>(v); });
     if (S > 2) fold_from([](float v) { return row_shr<2>(v); });
     if (S > 1) fold_from([](float v) { return row_shr<1>(v); });
+    RKV_STAMP(stamps, kStMergeFolded, tid == 0);
+    if (u0 == 0) poisoned = __syncthreads_or(gave_up || !(den == den)) != 0;
     if (sl == S - 1 && u < units) {
       const float dn = fmaxf(den, 1e-30f);
-      const uint32_t lo = (uint32_t)bf16_rne(num.x / dn) | ((uint32_t)bf16_rne(num.y / dn) << 16);
-      const uint32_t hi = (uint32_t)bf16_rne(num.z / dn) | ((uint32_t)bf16_rne(num.w / dn) << 16);
-      *reinterpret_cast<uint2*>(sx.out + (h * G + g) * D + 4 * q) = make_uint2(lo, hi);
+      // a hand-off of the head gave up: its output is NaN, not a plausible
+      // wrong answer
+      const uint32_t v = poisoned || gave_up
+                             ? 0x7FC07FC0u
+                             : (uint32_t)bf16_rne(na / dn) | ((uint32_t)bf16_rne(nb / dn) << 16);
+      *reinterpret_cast<uint32_t*>(sx.out + (h * G + g) * D + 2 * pp) = v;
     }
+  }
+  RKV_STAMP(stamps, kStMergeStored, tid == 0);
+  if (poisoned && m == 0 && da.write_mask) {
+    // (the workgroups' own mask stores wrote through before their partials,
+    // so these come last)
+    const int64_t N = da.n_blocks;
+    for (int64_t b = tid; b < N; b += kThreads) sx.mask.store_u8((uint32_t)(h * N + b), 1u);
   }
   // the step's access count: this head's tile counts, added once
   if (counting) {
@@ -1706,6 +1691,7 @@ __device__ void merge_slice(const AttendArgs& a, const StepCtx& sx, int64_t h, i
     __syncthreads();
     if (tid == 0)
       atomicAdd(sx.accessed, ((sx.wsum[0] + sx.wsum[1]) + sx.wsum[2]) + sx.wsum[3]);
+    RKV_STAMP(stamps, kStMergeCounted, tid == 0);
   }
 }
 
@@ -2048,15 +2034,17 @@ __device__ __forceinline__ void mma_stage_reps(const AttendArgs& a, int64_t h, u
   }
 }
 
-// Decision, then attention of wave-sized chunks on the matrix cores: first
-// each wave's representative chunk (staged before the decision; logits z,
-// expanded and missing blocks at -inf) and its share of the suffix, then
-// the page rows (one-launch step: the head's expanded rows split evenly over
-// its workgroups; three kernels: the tile's own expanded blocks); the four
-// waves' states merge through LDS into the tile's partial, and (one-launch
-// step) the head's last workgroups merge the partials.
-// kTiles > 1 (one-launch step): the workgroup's tiles are tset's, one
-// representative chunk per tile ahead of the suffix chunks.
+// Decision, then attention of wave-sized chunks on the matrix cores, one ring
+// of chunks per wave: its representative chunk (staged before the decision;
+// logits z, expanded and missing blocks at -inf), its share of the suffix,
+// then its share of the page rows of the expanded blocks of the workgroup's
+// own tile (with several tiles per workgroup, of all of them; copies of a
+// tile -- one-launch step with more workgroups than tiles -- each take an
+// even slice of the tile's rows).  The first page rows' loads are issued as
+// the ring starts, right after the decision, so they are in flight while the
+// earlier chunks fold.  The four waves' states merge through LDS into the
+// workgroup's partial, and (one-launch step) the head's last workgroups merge
+// the partials.
 template <int D, int GBM, bool kFused, int kTiles = 1>
 __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShared& dsh,
                                                 MmaCombine<D, GBM>& cmb, const StepCtx* sx,
@@ -2077,8 +2065,16 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   const bool primary = wk < T;
   const uint32_t n_suffix = ld.S > wk ? (ld.S - wk + W - 1) / W : 0u;
   constexpr uint32_t kRowBytes = D * 2;
+  // with more workgroups than tiles, workgroups wk, wk + T, ... decide the
+  // same tile: this one is copy `copy` of `copies` and takes that slice of
+  // the tile's expanded rows
+  const uint32_t copies = kMulti ? 1u : (W - tile + T - 1u) / T;
+  const uint32_t copy = kMulti ? 0u : wk / T;
 
   MmaStage<D>& stage = cmb.stage[wave];
+  unsigned long long* stamps = nullptr;  // (phase stamps build)
+  if constexpr (kFused) stamps = sx->stats.stamps;
+  (void)stamps;
 
   // ---- representatives and suffix: loads issued before the decision -------
   // (the representative rows into stage 0; the wave's first suffix chunk
@@ -2092,23 +2088,34 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   const uint32_t kts = (uint32_t)a.ks_ts * 2u, vts = (uint32_t)a.vs_ts * 2u;  // bytes
   const auto kres_s = buffer_view(a.key_suffix + h * a.ks_hs, cap ? (cap - 1u) * kts + kRowBytes : 0u);
   const auto vres_s = buffer_view(a.value_suffix + h * a.vs_hs, cap ? (cap - 1u) * vts + kRowBytes : 0u);
-  // Speculation (one-launch step): when the previous launch on this
-  // workspace expanded every block of the head, the workgroup attends its
-  // suffix chunks and its share of all the head's rows before the decision,
-  // without the representative chunk (with every block expanded that chunk's
-  // logits are all -inf, and its fold leaves the initial state unchanged),
-  // so the result equals the normal order's bit for bit whenever every block
-  // expands again; otherwise the state is dropped and the normal order runs
-  // after the decision.
-  const bool spec = kFused && sx->spec != nullptr && *sx->spec != 0u;
+  // Speculation (one-launch step, one tile per workgroup): when the previous
+  // launch on this workspace expanded every block of the tile, the wave
+  // issues its first two chunks of the tile's rows before the decision,
+  // assuming every block expands again (so its ring has no representative
+  // chunk: with every block expanded that chunk's logits are all -inf and its
+  // fold would leave the state unchanged); if the decision agrees, the ring
+  // goes on from them and the result is the normal order's bit for bit, else
+  // the wave waits for them to land and runs the normal order.
+  // (head_dim 160 does not speculate: its two rings below would need the
+  // speculative order in both)
+  const bool spec = kFused && D <= 128 && sx->spec != nullptr && *sx->spec != 0u;
   bool reps_on = has_reps && !spec;
+#if defined(RKV_PHASE_STAMPS)
+  if (stamps != nullptr && tid == 0) stamps[kStSpec] = spec ? 1u : 0u;
+#endif
   Bf16x8 k0[S::kSteps], k1[S::kSteps], k2[S::kSteps];
-  // loop1's chunks m < R are the representative chunks (a no-op without
-  // representatives: nothing issued, nothing folded), chunk j >= R the
-  // wave's suffix chunk j - R, so every chunk keeps its stage and K registers
+  // The wave's ring: chunks m < Rr are the representative chunks (a no-op
+  // without representatives: nothing issued, nothing folded; none while
+  // speculating), chunk Rr <= j < n1 the wave's suffix chunk j - Rr, then its
+  // page chunks of this workgroup's rows [pr0, pr1) -- chunk c = rows 16 c
+  // .. 16 c + 15 (inside one block: B is a multiple of 16) goes to wave
+  // (c - c0 + lead) mod 4, the waves with fewer suffix chunks first.
+  uint32_t Rr = spec ? 0u : R;
+  uint32_t pr0 = 0u, pr1 = 0u;
+  const uint32_t lead = (wave + 4u - ns_chunks % 4u) % 4u;  // this wave's first page chunk
   auto rep_tile = [&](uint32_t m) { return kMulti ? wk + m * W : tile; };
   auto issue_suffix = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-    const uint32_t ci = wave + 4u * (j - R);
+    const uint32_t ci = wave + 4u * (j - Rr);
     // suffix row t of the chunk: token wk + (16 ci + t) W (rows past this
     // workgroup's slice repeat its last token and are masked)
     auto token = [&](uint32_t t) {
@@ -2138,223 +2145,282 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
       mma_stage_reps<D>(a, h, rep_tile(m), dst);
     }
   };
-  // chunks 0 and 1 are issued before the decision
-  auto pre_issue = [&]() {
-    if (kMulti || reps_on) issue_reps(0u, stage.bytes[0], k0);
-    if (R > 1) issue_reps(1u, stage.bytes[1], k1);
-    else if (ns_wave > 0) issue_suffix(1u, 1, k1);
-  };
-
-  MmaState<D> st;
-  auto init_state = [&]() {
-    st.m = kNegInf;
-    st.lsum = 0.0f;
-#pragma unroll
-    for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  };
-  uint64_t bits[kTiles] = {};
-  // the representative chunks (if reps_on, first) and the wave's suffix chunks
-  auto loop1 = [&]() {
-    const uint32_t count = R + ns_wave;
-    mma_ring<D>(
-        count, count > 1 ? 2u : 1u, k0, k1, k2,
-        [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-          if (j < R) issue_reps(j, stage.bytes[sidx], kop);
-          else issue_suffix(j, sidx, kop);
-        },
-        [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
-          if (j < R && !(kMulti ? rep_tile(j) * kTile + 16u * wave < N : reps_on)) return;
-          float x[4];
-          const int g = lane & 15;
-          if (j < R) {
-            // logit z of block rep_first + 4 (l / 16) + i for query row g
-            const int gg = g < gn ? g : 0;
-            const uint32_t rt = rep_tile(j);
-            // (tile j's bits from LDS: a register array indexed by j would
-            // live in scratch)
-            const uint64_t rbits = kMulti ? dsh.tile_bits[j] : bits[0];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const uint32_t tb = 16u * wave + 4u * (uint32_t)(lane >> 4) + i;  // in the tile
-              const uint32_t b = rt * kTile + tb;
-              const bool live = b < N && !((rbits >> tb) & 1ull);
-              float z;
-              if constexpr (kMulti) z = tset->z[j < kTiles ? j : 0][gg][tb];
-              else if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
-              else z = da.zf[(h * G + g0 + gg) * da.z_stride + (b < N ? b : N - 1)].x;
-              x[i] = live ? z : kNegInf;
-            }
-          } else {
-            const uint32_t ci = wave + 4u * (j - R);
-            const F32x4 s4 = mma_qk<D>(kop, ld.qop);
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              const uint32_t r = 16u * ci + 4u * (uint32_t)(lane >> 4) + i;
-              x[i] = r < n_suffix ? s4[i] * a.scale : kNegInf;
-            }
-          }
-          mma_fold<D, false>(st, x, stage.bytes[sidx]);
-        });
-  };
 
   // ---- page rows ------------------------------------------------------------
+  // Expanded block ordinal e of the workgroup's tiles, in (tile, block)
+  // order, gives B rows; row r is token r mod B of block block_of(r / B).
+  // bits[m]: tile m's expanded blocks (wave-uniform, so the lookups below are
+  // scalar arithmetic).
+  uint64_t bits[kTiles] = {};
+  // one tile: the decision's list of the tile's expanded blocks (this wave's
+  // copy in LDS, ascending), or before the decision (speculating) every block
+  const int32_t* plist = nullptr;
+  auto block_of = [&](uint32_t e) -> uint32_t {
+    if constexpr (!kMulti) return tile * kTile + (plist != nullptr ? (uint32_t)plist[e] : e);
+    uint32_t t_sel = wk;
+    uint64_t b_sel = bits[0];
+    if constexpr (kMulti) {
+      bool found = e < (uint32_t)__popcll(b_sel);
+#pragma unroll
+      for (int m = 1; m < kTiles; ++m) {
+        if (!found) {
+          e -= (uint32_t)__popcll(b_sel);
+          t_sel = wk + (uint32_t)m * W;
+          b_sel = bits[m];
+          found = e < (uint32_t)__popcll(b_sel);
+        }
+      }
+    }
+    return t_sel * kTile + (uint32_t)nth_set_bit(b_sel, (int)e);
+  };
   const uint16_t* kbase = a.key_pages + h * a.kp_hs;
   const uint16_t* vbase = a.value_pages + h * a.vp_hs;
   const uint32_t page_bytes = (N << lb) * kRowBytes;
   const auto kres = buffer_view(kbase, page_bytes), vres = buffer_view(vbase, page_bytes);
   const uint32_t last = N - 1, last_count = L - last * B;
-  // rows [r_first, r_first + n_rows): row r is token (16 c) mod B + r mod 16 of
-  // block block_of(c), c = r / 16 (B is a multiple of 16, so a chunk never
-  // crosses a block); chunk c goes to wave (c - c0 + rot) mod 4, the waves
-  // with fewer suffix chunks first
-  auto run_pages = [&](uint32_t r_first, uint32_t n_rows, auto block_of) {
-    if (n_rows == 0) return;
-    const uint32_t r_end = r_first + n_rows;
-    const uint32_t c0 = r_first >> 4, c_end = (r_end + 15u) >> 4;
-    const uint32_t lead = (wave + 4u - ns_chunks % 4u) % 4u;  // this wave's first chunk
-    const uint32_t n = c0 + lead < c_end ? (c_end - c0 - lead - 1u) / 4u + 1u : 0u;
-    mma_ring<D>(
-        n, 0u, k0, k1, k2,
-        [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
-          const uint32_t c = c0 + lead + 4u * j;
-          const uint32_t row0 = ((uint32_t)block_of(c) << lb) + ((c << 4) & (B - 1u));
-          auto row = [&](uint32_t t) { return (row0 + t) * kRowBytes; };
-          mma_issue_rows<D>(kres, vres, stage.bytes[sidx], kop, row, row);
-        },
-        [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
-          const uint32_t c = c0 + lead + 4u * j;
-          const uint32_t bb = (uint32_t)block_of(c);
-          const F32x4 s4 = mma_qk<D>(kop, ld.qop);
-          float x[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const uint32_t r = (c << 4) + 4u * (uint32_t)(lane >> 4) + i;
-            const uint32_t tok = r & (B - 1u);
-            const bool live = r >= r_first && r < r_end && (bb != last || tok < last_count);
-            x[i] = live ? s4[i] * a.scale : kNegInf;
-          }
-          mma_fold<D>(st, x, stage.bytes[sidx]);
-        });
+  // the tile's blocks (the last tile may be short): what speculation assumes
+  const uint32_t n_valid = N - tile * kTile < (uint32_t)kTile ? N - tile * kTile : (uint32_t)kTile;
+  const uint64_t valid_bits = n_valid >= 64u ? ~0ull : (1ull << n_valid) - 1ull;
+  // this workgroup's slice of the rows of `blocks` expanded blocks
+  // (32-bit arithmetic: a workgroup's tiles hold at most 4 x 64 x 64 rows,
+  // and copies come only with one tile, at most 256 per head)
+  auto set_rows = [&](uint32_t blocks) {
+    const uint32_t rows = blocks << lb;
+    if (copies == 1u) {
+      pr0 = 0u;
+      pr1 = rows;
+    } else {
+      pr0 = copy * rows / copies;
+      pr1 = (copy + 1u) * rows / copies;
+    }
+  };
+  auto n1 = [&]() { return Rr + ns_wave; };
+  auto n_chunks = [&]() {
+    const uint32_t c0 = pr0 >> 4, c_end = (pr1 + 15u) >> 4;
+    const uint32_t np = pr1 > pr0 && c0 + lead < c_end ? (c_end - c0 - lead - 1u) / 4u + 1u : 0u;
+    return n1() + np;
+  };
+  auto chunk_of = [&](uint32_t j) { return (pr0 >> 4) + lead + 4u * (j - n1()); };
+  auto issue_page = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+    const uint32_t c = chunk_of(j);
+    const uint32_t row0 = (block_of((c << 4) >> lb) << lb) + ((c << 4) & (B - 1u));
+    RKV_STAMP(stamps, kStIssue2Addr, tid == 0 && j == 2u);
+    auto row = [&](uint32_t t) { return (row0 + t) * kRowBytes; };
+    mma_issue_rows<D>(kres, vres, stage.bytes[sidx], kop, row, row);
+  };
+  auto issue = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+    if (j < Rr) issue_reps(j, stage.bytes[sidx], kop);
+    else if (j < n1()) issue_suffix(j, sidx, kop);
+    else issue_page(j, sidx, kop);
+    RKV_STAMP(stamps, kStIssued2, tid == 0 && j == 2u);
+  };
+  // chunks 0 and 1 are issued before the decision (a representative chunk
+  // without representatives issues nothing)
+  auto pre_issue = [&]() {
+    const uint32_t n = n_chunks();
+    if (Rr == 0u || kMulti || reps_on) {
+      if (n > 0) issue(0u, 0, k0);
+    }
+    if (n > 1 && (Rr == 0u || n1() > 1u)) issue(1u, 1, k1);
   };
 
-  pre_issue();
+  MmaState<D> st;
+  st.m = kNegInf;
+  st.lsum = 0.0f;
+#pragma unroll
+  for (int b = 0; b < S::kBlocks; ++b) st.o[b] = F32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
   if (spec) {
-    // every block of the head assumed expanded: this workgroup's share of
-    // the head's N B rows, in block order (what the mask hand-off gives
-    // when every mask is full)
-    init_state();
-    loop1();
-    const uint64_t R = (uint64_t)N << lb;
-    const uint32_t r0 = (uint32_t)((uint64_t)wk * R / W);
-    const uint32_t r1 = (uint32_t)(((uint64_t)wk + 1u) * R / W);
-    run_pages(r0, r1 - r0, [&](uint32_t c) { return (c << 4) >> lb; });
+    bits[0] = valid_bits;
+    set_rows(n_valid);
   }
+  pre_issue();
 
   // ---- the decision (one-launch step: from the head's tagged LSE slots) ----
-  const int32_t* list;
   uint32_t count = 0;
   if constexpr (kMulti) {
-    list = nullptr;
     decide_tiles<kTiles, GBM>(da, h, wk, W, *tset, dsh, sx->stats, bits, count);
   } else {
-    bits[0] = decide_finish<kFused>(da, h, tile, ld.din, dsh, nullptr, list, count,
-                                    kFused ? &sx->stats : nullptr);
+    bits[0] = decide_finish<kFused, false>(da, h, tile, ld.din, dsh, nullptr, plist, count,
+                                           kFused ? &sx->stats : nullptr);
   }
-  if constexpr (kFused) {
-    // publish the expanded blocks (a tagged slot per tile) for the head's
-    // even split of pooled token rows: from the last wave, which next polls
-    // the head's masks (loads complete in order, so the first wait after a
-    // store also waits for its write-through; the other waves go on to
-    // their chunks)
-    if (tid == kThreads - kWave) {
-      const uint32_t tag = __builtin_amdgcn_readfirstlane(*sx->stats.tag);
+  RKV_STAMP(stamps, kStDecided, tid == 0);
+  if (spec && bits[0] != valid_bits) {
+    // the speculation missed: the chunks issued for it land, then the
+    // normal order
+    wait_vm<0>();
+    Rr = R;
+    reps_on = has_reps;
+  }
+  if (!spec || Rr != 0u) {
+    uint32_t blocks = 0;
 #pragma unroll
-      for (int m = 0; m < kTiles; ++m)
-        if ((uint32_t)m < R)
-          sx->xbits.store4((uint32_t)((h * da.tile_stride + rep_tile(m)) * 16),
-                           make_slot((uint32_t)bits[m], (uint32_t)(bits[m] >> 32), tag));
-    }
-  }
-  if (!spec) {
-    init_state();
-    loop1();
+    for (int m = 0; m < kTiles; ++m) blocks += (uint32_t)__popcll(bits[m]);
+    set_rows(blocks);
+    if (spec) pre_issue();
   }
 
-  if constexpr (kFused) {
-    // this workgroup's share of the head's expanded rows, once every tile of
-    // the head has published its mask (polled by the last wave, which has
-    // suffix rows only when every wave has); workgroup 0 records for the
-    // next launch whether every block expanded
-    if (wave == kWaves - 1) {
-      const uint32_t n_last = N - (T - 1) * kTile;  // blocks of the last tile
-      const uint64_t last_bits = n_last >= 64 ? ~0ull : (1ull << n_last) - 1ull;
-      expanded_share(*sx, h, da.tile_stride, T, W, wk, (int)lb, last_bits, N);
-      if (wk == 0 && lane == 0)
-        __hip_atomic_store(sx->control + h * kLine + 2,
-                           sx->xr[2] ? (uint64_t)*sx->stats.tag + 1u : 0ull, __ATOMIC_RELAXED,
-                           __HIP_MEMORY_SCOPE_AGENT);
+  // ---- the ring -------------------------------------------------------------
+  // logits of chunk j: representative, suffix or page chunk
+  auto rep_logits = [&](uint32_t j, float (&x)[4]) {
+    // logit z of block rep_first + 4 (l / 16) + i for query row g
+    const int g = lane & 15, gg = g < gn ? g : 0;
+    const uint32_t rt = rep_tile(j);
+    // (tile j's bits from LDS: a register array indexed by j would live in
+    // scratch)
+    const uint64_t rbits = kMulti ? dsh.tile_bits[j] : bits[0];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t tb = 16u * wave + 4u * (uint32_t)(lane >> 4) + i;  // in the tile
+      const uint32_t b = rt * kTile + tb;
+      const bool live = b < N && !((rbits >> tb) & 1ull);
+      float z;
+      if constexpr (kMulti) z = tset->z[j < kTiles ? j : 0][gg][tb];
+      else if constexpr (kFused) z = sx->stats.zs[gg][tb].x;
+      else z = da.zf[(h * G + g0 + gg) * da.z_stride + (b < N ? b : N - 1)].x;
+      x[i] = live ? z : kNegInf;
     }
-    __syncthreads();
-    const bool again = spec && sx->xr[2] == 0u;  // the speculation missed
-    if (again) {
-      reps_on = has_reps;
-      init_state();
-      pre_issue();
-      loop1();
+  };
+  auto suffix_logits = [&](uint32_t j, const Bf16x8 (&kop)[S::kSteps], float (&x)[4]) {
+    const uint32_t ci = wave + 4u * (j - Rr);
+    const F32x4 s4 = mma_qk<D>(kop, ld.qop);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = 16u * ci + 4u * (uint32_t)(lane >> 4) + i;
+      x[i] = r < n_suffix ? s4[i] * a.scale : kNegInf;
     }
-    if (!spec || again) {
-      const int32_t* xl = sx->xl;
-      const uint32_t x_first = sx->xr[0], e_first = x_first >> lb, last_e = sx->xl_cap - 1u;
-      run_pages(x_first, sx->xr[1], [&](uint32_t c) {
-        const uint32_t e = ((c << 4) >> lb) - e_first;  // < xl_cap (expanded_share)
-        return (uint32_t)xl[e < last_e ? e : last_e];
-      });
+  };
+  auto page_logits = [&](uint32_t j, const Bf16x8 (&kop)[S::kSteps], float (&x)[4]) {
+    const uint32_t c = chunk_of(j);
+    const uint32_t bb = block_of((c << 4) >> lb);
+    const F32x4 s4 = mma_qk<D>(kop, ld.qop);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const uint32_t r = (c << 4) + 4u * (uint32_t)(lane >> 4) + i;
+      const uint32_t tok = r & (B - 1u);
+      const bool live = r >= pr0 && r < pr1 && (bb != last || tok < last_count);
+      x[i] = live ? s4[i] * a.scale : kNegInf;
     }
+  };
+  // a representative chunk without representatives folds nothing
+  auto reps_live = [&](uint32_t j) {
+    return kMulti ? rep_tile(j) * kTile + 16u * wave < N : reps_on;
+  };
+  const uint32_t pre = !spec || Rr != 0u ? (n1() > 1u ? 2u : 1u) : (n_chunks() > 1u ? 2u : 1u);
+  RKV_STAMP(stamps, kStRingStart, tid == 0);
+  if constexpr (D <= 128) {
+    // one ring: the first page rows' loads are issued as it starts
+    mma_ring<D>(n_chunks(), pre, k0, k1, k2, issue,
+                [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+                  float x[4];
+                  RKV_STAMP(stamps, kStFold0Start, tid == 0 && j == 0u);
+                  if (j < Rr) {
+                    if (!reps_live(j)) return;
+                    rep_logits(j, x);
+                  } else if (j < n1()) {
+                    suffix_logits(j, kop, x);
+                  } else {
+                    page_logits(j, kop, x);
+                  }
+                  mma_fold<D>(st, x, stage.bytes[sidx]);
+                  RKV_STAMP(stamps, kStChunk0 + (j < 3u ? j : 2u), tid == 0 && j < 3u);
+                });
   } else {
-    run_pages(0u, (uint32_t)__popcll(bits[0]) * B,
-              [&](uint32_t c) { return tile * kTile + (uint32_t)list[(c << 4) >> lb]; });
+    // (head_dim 160: one ring of every kind holds more registers than the
+    // kernel has) the representative and suffix chunks, then the page rows
+    // in a ring of their own
+    const uint32_t first = n1();
+    mma_ring<D>(first, pre, k0, k1, k2,
+                [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+                  if (j < Rr) issue_reps(j, stage.bytes[sidx], kop);
+                  else issue_suffix(j, sidx, kop);
+                },
+                [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+                  float x[4];
+                  if (j < Rr) {
+                    if (!reps_live(j)) return;
+                    rep_logits(j, x);
+                  } else {
+                    suffix_logits(j, kop, x);
+                  }
+                  mma_fold<D>(st, x, stage.bytes[sidx]);
+                });
+    mma_ring<D>(n_chunks() - first, 0u, k0, k1, k2,
+                [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+                  issue_page(first + j, sidx, kop);
+                },
+                [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
+                  float x[4];
+                  page_logits(first + j, kop, x);
+                  mma_fold<D>(st, x, stage.bytes[sidx]);
+                });
+  }
+  RKV_STAMP(stamps, kStRing, tid == 0);
+
+  // the expanded-block mask, stored after the ring (a store issued ahead of
+  // the ring's loads would hold its first waits), and for the next launch's
+  // speculation whether every block of the tile expanded
+  if (wave == 0 && blockIdx.z == 0 && da.write_mask) {
+#pragma unroll
+    for (int m = 0; m < kTiles; ++m) {
+      const uint32_t b = rep_tile((uint32_t)m) * kTile + (uint32_t)lane;
+      const uint8_t v = (uint8_t)((bits[m] >> lane) & 1ull);
+      if ((uint32_t)m < R && b < N) {
+        // (one-launch step: written through, so that a merger's later
+        // all-expanded mask after a failed hand-off is the last write)
+        if constexpr (kFused) sx->mask.store_u8((uint32_t)(h * (int64_t)N + b), v);
+        else da.mask[h * (int64_t)N + b] = v;
+      }
+    }
+  }
+  if constexpr (kFused && !kMulti) {
+    if (tid == 0 && sx->full != nullptr)
+      __hip_atomic_store(sx->full, bits[0] == valid_bits ? (uint64_t)*sx->stats.tag + 1u : 0ull,
+                         __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   }
 
   // ---- the four waves -> one partial per query row, through LDS ------------
+  RKV_STAMP(stamps, kStPagesWave0, tid == 0);
   mma_publish<D, GBM>(st, cmb.mma[wave]);
   __syncthreads();
+  RKV_STAMP(stamps, kStCombine, tid == 0);
+  uint32_t tag = 0u;
+  bool nan_partial = false;  // a wait of this workgroup gave up
+  if constexpr (kFused) {
+    tag = __builtin_amdgcn_readfirstlane(*sx->stats.tag);
+    nan_partial = *sx->stats.gave_up != 0u;
+  }
   mma_combine<D, GBM>(cmb, gn, [&](int j, int d, float2 acc, float M, float l) {
+    if (nan_partial) l = bits_f32(0x7FC00000u);
     const int64_t at = (h * G + g0 + j) * da.tile_stride + wk;
     if constexpr (kFused) {
-      sx->acc.store2((uint32_t)((at * D + d) * 4), acc);
-      if (d == 0) sx->ml.store2((uint32_t)(at * 8), make_float2(M, l));
+      // the partial as tagged slots (the mergers poll them)
+      const int64_t row = (h * G + g0 + j) * da.tile_stride;
+      sx->acc.store4(acc_slot<D>(row, wk, (uint32_t)d / 2u),
+                     make_slot(f32_bits(acc.x), f32_bits(acc.y), tag));
+      if (d == 0) sx->ml.store4(ml_slot(row, wk), make_slot(f32_bits(M), f32_bits(l), tag));
     } else {
       *reinterpret_cast<float2*>(a.part_acc + at * D + d) = acc;
       if (d == 0) a.part_ml[at] = make_float2(M, l);
     }
   });
-  if (a.tile_counts && tid == 0 && blockIdx.z == 0) {
+  if (tid == 0 && blockIdx.z == 0) {
     // (a copy's count sits past the first T entries, which alone are summed)
-    if constexpr (kFused) sx->counts.store_u32((uint32_t)((h * da.tile_stride + wk) * 4), count);
-    else a.tile_counts[h * da.tile_stride + wk] = count;
-  }
-  if constexpr (kFused) {
-    // publish and take a ticket; the head's last K workgroups wait for the
-    // rest and merge a column slice each
-    wait_memory();
-    __syncthreads();
-    uint64_t* merged = sx->control + h * kLine + 1;
-    if (tid == 0) {
-      const uint64_t old = __hip_atomic_fetch_add(merged, 1ull, __ATOMIC_RELAXED,
-                                                  __HIP_MEMORY_SCOPE_AGENT);
-      *sx->flag = (uint32_t)(old - *sx->base);
+    if constexpr (kFused) {
+      if (sx->accessed)
+        sx->counts.store4((uint32_t)((h * da.tile_stride + wk) * 16), make_slot(count, 0u, tag));
+    } else if (a.tile_counts) {
+      a.tile_counts[h * da.tile_stride + wk] = count;
     }
-    __syncthreads();
-    const uint32_t ticket = *sx->flag;
+  }
+  RKV_STAMP(stamps, kStPublished, tid == 0);
+  if constexpr (kFused) {
+    // the head's last K workgroups each merge a column slice
     const uint32_t K = mergers(W);
-    if (ticket >= W - K) {
-      // (the last ticket's own bump completed the count: every other
-      // workgroup's partial landed before its bump did, so it merges without
-      // a poll)
-      if (tid == 0 && ticket != W - 1)
-        wait_counter<uint64_t>(merged, *sx->base + W + sx->skew, sx->stats.spin, sx->error());
-      __syncthreads();
-      merge_slice<D>(a, *sx, h, (int)(ticket - (W - K)), (int)K);
+    if (wk >= W - K) {
+      RKV_STAMP(stamps, kStMergeWait, tid == 0);
+      merge_slice<D>(a, *sx, h, (int)(wk - (W - K)), (int)K);
+      RKV_STAMP(stamps, kStMerged, tid == 0);
     }
   }
 }
@@ -2481,8 +2547,9 @@ struct StepArgs {
   uint16_t* out;                  // (H, G, D) bf16
   unsigned long long* accessed;   // or null
   float4* lse_slots;              // (H*G, tile_stride, 2) tagged LSE slots
-  float4* xbits;                  // (H, tile_stride) tagged expanded-block masks
-  uint32_t slots_bytes, ml_bytes, acc_bytes, counts_bytes, xbits_bytes;
+  uint64_t* full;                 // (H, tile_stride): tag + 1 of the launch whose tile fully expanded
+  uint32_t* error;                // the sticky status word (bit 0: a wait gave up)
+  uint32_t slots_bytes, ml_bytes, acc_bytes, counts_bytes, mask_bytes;
   int heads;
   uint32_t spin;      // polls before a hand-off wait gives up
   uint32_t skew;      // 0 (a test hook's nonzero value makes every wait run out)
@@ -2505,14 +2572,10 @@ struct StepShared {
   alignas(16) float4 zs[GBM][kTile];  // z, delta, A, th of the tile's (row, block) pairs
   alignas(16) TileZ<kTiles, GBM> tz;  // several tiles: each tile's z rows
   alignas(16) unsigned long long wsum[kWaves];
-  // a workgroup's expanded-row share: at most 64 ceil(T / W) + 2 blocks,
-  // ceil(T / W) <= kTiles
-  alignas(16) int32_t xl[kTiles * kTile + 4];
-  uint32_t xr[3];
-  uint64_t base;
   uint32_t tag, rtag;
   uint32_t ticket;
   uint32_t spec;
+  uint32_t gave_up;  // a wait of this workgroup gave up
   alignas(16) DecideShared dec;
   alignas(16) union {
     struct {
@@ -2522,7 +2585,9 @@ struct StepShared {
     } score;
     alignas(16) MmaCombine<D, GBM> cmb;
   } u;
-  uint32_t flag;
+#if defined(RKV_PHASE_STAMPS)
+  unsigned long long stamps[kStamps];
+#endif
 };
 
 // Workgroup (tile, h): the tile's scores (z, delta and the risk's delta
@@ -2543,6 +2608,13 @@ void step_kernel(StepArgs s) {
   const ScoreArgs& sa = s.score;
   const int G = sa.group, tid = threadIdx.x, lane = tid % kWave;
   const uint32_t W = (uint32_t)s.attend.workers;
+#if defined(RKV_PHASE_STAMPS)
+  unsigned long long* const stamps = sh.stamps;
+  if (tid < kStamps) stamps[tid] = 0ull;
+#else
+  unsigned long long* const stamps = nullptr;
+#endif
+  RKV_STAMP(stamps, kStEntry, tid == 0);
   // this launch's epoch, from the workgroup's own launch counter: its tag
   // marks the slots the launch publishes (read only after the score loads
   // are issued: a read right after the atomic would wait out its round trip)
@@ -2570,36 +2642,29 @@ void step_kernel(StepArgs s) {
   }
   const int64_t tile = wk % (int64_t)s.attend.decide.n_tiles;
   const StepCtx sx{StepStats{sh.zs, Coherent(s.lse_slots, s.slots_bytes), &sh.tag, &sh.rtag,
-                             reinterpret_cast<uint32_t*>(s.control + (int64_t)s.heads * kLine),
-                             s.spin},
+                             s.error, s.spin, stamps, &sh.gave_up},
                    Coherent(s.attend.part_ml, s.ml_bytes),
                    Coherent(s.attend.part_acc, s.acc_bytes),
                    Coherent(s.counts, s.counts_bytes),
-                   s.control,
+                   Coherent(s.attend.decide.mask, s.mask_bytes),
                    s.out,
                    s.accessed,
-                   &sh.flag,
                    sh.wsum,
-                   &sh.base,
-                   Coherent(s.xbits, s.xbits_bytes),
-                   sh.xl,
-                   (uint32_t)(kTiles * kTile + 4),
-                   sh.xr,
-                   s.heads,
-                   s.skew,
+                   kTiles == 1 ? s.full + h * sa.tile_stride + wk : nullptr,
                    &sh.spec};
-  // whether the previous launch on the workspace expanded every block of the
-  // head (its workgroup 0 left that launch's tag + 1 here)
+  // whether the previous launch on the workspace expanded every block of
+  // this workgroup's tile (it left that launch's tag + 1 in its flag)
   // (a workgroup of several tiles does not speculate)
   uint64_t prev_full = 0;
   if (kTiles == 1 && tid == 0 && s.speculate)
-    prev_full = __hip_atomic_load(s.control + h * kLine + 2, __ATOMIC_RELAXED,
+    prev_full = __hip_atomic_load(s.full + h * sa.tile_stride + wk, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
   score_dots<D, GBM>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+  RKV_STAMP(stamps, kStDots, tid == 0);
   // (the epoch is read before the loads below are issued: loads complete in
   // order, so a later read would wait for them too)
   if (tid == 0) {
-    sh.base = epoch * (uint64_t)W;
+    sh.gave_up = 0u;
     sh.tag = (uint32_t)epoch + 1u;
     sh.rtag = sh.tag + s.skew;
     sh.spec = s.speculate && prev_full == epoch + 1u ? 1u : 0u;
@@ -2623,6 +2688,7 @@ void step_kernel(StepArgs s) {
         [&](int g, bool, float4 zf) { sh.zs[g][lane] = zf; },
         [&](int g, float4 part) { publish(tile, g, part); });
     __syncthreads();
+    RKV_STAMP(stamps, kStStats, tid == 0);
     // (the score arrays are dead: the representative rows and the first
     // suffix chunks stage over them and land while the decision waits for
     // the head's LSE partials)
@@ -2664,9 +2730,16 @@ void step_kernel(StepArgs s) {
     for (int m = 1; m < kTiles; ++m)
       if ((uint32_t)m < tset.n) tset.din[m] = decide_issue<false>(s.attend.decide, h, wk + (int64_t)m * W);
     __syncthreads();
+    RKV_STAMP(stamps, kStStats, tid == 0);
     attend_tile_mma<D, GBM, true, kTiles>(s.attend, sh.dec, sh.u.cmb, &sx, ld, h, (uint32_t)wk,
                                           &tset);
   }
+#if defined(RKV_PHASE_STAMPS)
+  RKV_STAMP(stamps, kStEnd, tid == 0);
+  __syncthreads();
+  if (tid < kStamps && h < kStampHeads && wk < kStampRowsPerHead)
+    rkv_stamps[h * kStampRowsPerHead + wk][tid] = stamps[tid];
+#endif
 }
 
 // ---------------------------------------------------------------------------
@@ -2682,6 +2755,7 @@ struct MergeArgs {
   int parts, dim, heads;
 };
 
+constexpr int kMergeBatch = 8;               // partials per lane per batch of loads
 constexpr int kMergeD = 32;                  // output columns per workgroup
 constexpr int kMergeK = kThreads / kMergeD;  // partial stripes
 
@@ -2963,9 +3037,12 @@ int launch_attend(const AttendArgs& aa, int64_t rows, dim3 grid, hipStream_t str
   return set_error(kUnsupported, "rkv_decode: no attention kernel for this group");
 }
 
-// The one-launch step is built for head_dim <= kStepMaxDim: larger head
-// dims would spill registers to scratch in it, and take the three kernels.
-constexpr int kStepMaxDim = 160;
+// The one-launch step is built for head_dim <= kStepMaxDim: at head_dim 160
+// its one resident workgroup per two CUs spills registers (its ring of
+// representative, suffix and page chunks, or both rings, hold more than the
+// 256 a wave has at two waves per SIMD), so 160 and above take the three
+// kernels.
+constexpr int kStepMaxDim = 128;
 
 template <int D, int GBM>
 int launch_step_g(const StepArgs& sa, bool ticketed, bool multi, dim3 grid, hipStream_t stream) {
@@ -3062,8 +3139,8 @@ StepMode step_mode(const SelectParams& p, const Layout& L, const DecodeBuffers& 
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
   const int64_t limit = int64_t(1) << 31;
   if (!(p.dim <= kStepMaxDim && p.group <= rows && L.n_tiles <= kStepMaxTiles &&
-        hg * ts * 32 < limit &&
-        hg * ts * p.dim * 4 < limit && p.heads * ts * 4 < limit && aligned(b.output, 8)))
+        hg * ts * 32 < limit && hg * ts * p.dim * 8 < limit && p.heads * ts * 16 < limit &&
+        p.heads * p.n_blocks < limit && aligned(b.output, 8)))
     return kSplit;
   int64_t resident = 0;
   const bool multi = L.step_tiles > 1;
@@ -3075,20 +3152,19 @@ StepMode step_mode(const SelectParams& p, const Layout& L, const DecodeBuffers& 
   return kSplit;
 }
 
+// The status word the step's waits report to: the workspace's own (null),
+// or the static scratch's fixed word while rkv_decode_static runs.
+thread_local uint32_t* g_error_word = nullptr;
+
 // Test hooks (rkv_set_handoff_test, per thread): the step's poll limit per
 // wait (0 = kSpinLimit) and a tag skew that makes every wait run out.
 thread_local uint32_t g_spin_limit = 0;
 thread_local uint32_t g_skew = 0;
 // Test hook (rkv_set_speculation, per thread): 0 turns the step's
-// speculation off, 1 (default) leaves it on where a workgroup's share of a
-// head's rows is at least kSpecMinRows, 2 turns it on for every shape.
+// speculation off, 1 (default) and 2 leave it on.  (A miss costs a
+// workgroup at most two chunks' loads per wave, and only where the previous
+// launch expanded all of its tile, so it needs no size threshold.)
 thread_local uint32_t g_speculate = 1;
-// Speculation pays where the page rows outweigh the decision it moves off
-// their path: measured on at 2048 rows per workgroup (eps 0 at 131072
-// tokens, 8 heads: 109.0 -> 107.0 us), off at 1024 (65536 tokens: 63.2
-// against 63.5 us) and at 512 (32768 tokens: 39.96 against 40.35 us; the
-// Qwen-shaped op at 65536 tokens: 50.4 against 51.2).
-constexpr int64_t kSpecMinRows = 2048;
 
 int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, bool ticketed) {
   StepArgs s;
@@ -3103,16 +3179,18 @@ int launch_step(const SelectParams& p, const Layout& L, const DecodeBuffers& b, 
   const int64_t hg = p.heads * p.group, ts = L.tile_stride;
   s.lse_slots = at<float4>(p.ws, L.lse_slots);
   s.slots_bytes = (uint32_t)(hg * ts * 32);
-  s.ml_bytes = (uint32_t)(hg * ts * 8);
-  s.acc_bytes = (uint32_t)(hg * ts * p.dim * 4);
-  s.counts_bytes = (uint32_t)(p.heads * ts * 4);
-  s.xbits = at<float4>(p.ws, L.xbits);
-  s.xbits_bytes = (uint32_t)(p.heads * ts * 16);
+  s.ml_bytes = (uint32_t)(hg * ts * 16);
+  s.acc_bytes = (uint32_t)(hg * ts * p.dim * 8);
+  s.counts_bytes = (uint32_t)(p.heads * ts * 16);
+  s.mask_bytes = (uint32_t)(p.heads * p.n_blocks);
+  s.full = at<uint64_t>(p.ws, L.full);
+  s.error = g_error_word != nullptr
+                ? g_error_word
+                : reinterpret_cast<uint32_t*>(s.control + (int64_t)p.heads * kLine);
   s.heads = (int)p.heads;
   s.spin = g_spin_limit ? g_spin_limit : kSpinLimit;
   s.skew = g_skew;
-  const int64_t share = p.n_blocks * p.block / (L.step_workers > 0 ? L.step_workers : 1);
-  s.speculate = g_speculate == 2 || (g_speculate == 1 && share >= kSpecMinRows) ? 1u : 0u;
+  s.speculate = g_speculate != 0 && L.step_tiles == 1 ? 1u : 0u;
   const int64_t rows = rows_per_pass(p.group, p.dim);
   mark(0, p.stream);
   int rc = kUnsupported;
@@ -3314,9 +3392,10 @@ extern "C" size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim,
 
 // Byte offsets of the workspace regions, for tests: control (hand-off
 // counters), zf (z, delta, A, th per row and block), lse, lse_slots (the
-// step's tagged LSE partials), part_ml, part_acc, counts, xbits (the step's
-// tagged expanded-block masks), total, then n_tiles, the row stride (blocks)
-// of zf and of the per-tile arrays.
+// step's tagged LSE partials), part_ml, part_acc, counts, full (the step's
+// per-workgroup speculation flags), total, then n_tiles, the row stride
+// (blocks) of zf and of the per-tile arrays, and the step's workgroups per
+// head.
 extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
                                     int64_t* out13) {
   clear_error();
@@ -3324,7 +3403,7 @@ extern "C" int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, i
     return set_error(kInvalidArgument, "rkv_workspace_layout: bad arguments");
   const Layout L = make_layout(heads, group, dim, n_blocks);
   const int64_t v[13] = {L.control,  L.zf,     L.lse,         L.lse_slots, L.part_ml,
-                         L.part_acc, L.counts, L.xbits,       L.total,     L.n_tiles,
+                         L.part_acc, L.counts, L.full,        L.total,     L.n_tiles,
                          L.z_stride, L.tile_stride, L.step_workers};
   for (int i = 0; i < 13; ++i) out13[i] = v[i];
   return kOk;
@@ -3457,11 +3536,10 @@ extern "C" int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew) {
   return kOk;
 }
 
-// Test hook: the one-launch step's speculation (attending every block's rows
-// before the decision when the previous launch on the workspace expanded
-// every block): 0 off, 1 (default) where a workgroup's share of a head's
-// rows is at least kSpecMinRows, 2 for every shape.  Results are the same
-// bit for bit either way.  Per thread.
+// Test hook: the one-launch step's speculation (issuing the first page rows
+// of a workgroup's tile before the decision when the previous launch on the
+// workspace expanded every block of it): 0 off, 1 (default) and 2 on.
+// Results are the same bit for bit either way.  Per thread.
 extern "C" int rkv_set_speculation(int mode) {
   clear_error();
   if (mode < 0 || mode > 2) return set_error(kInvalidArgument, "rkv_set_speculation: mode %d (0, 1 or 2)", mode);
@@ -3546,6 +3624,10 @@ namespace rkv {
 // each device's copy is found with hipGetSymbolAddress.
 constexpr size_t kStaticScratchBytes = size_t(64) << 20;
 static __device__ __align__(256) char scratch[kStaticScratchBytes];
+// The static path's status word sits in the scratch's last 256 bytes, apart
+// from any shape's workspace (whose layout is cleared on every call), so it
+// keeps a failed wait's report until rkv_static_status clears it.
+constexpr size_t kStaticWorkspaceBytes = kStaticScratchBytes - 256;
 
 namespace {
 
@@ -3615,31 +3697,60 @@ extern "C" int rkv_decode_static(const void* query, const void* key_mean, const 
   if (heads <= 0 || group <= 0 || dim <= 0 || n_blocks <= 0)
     return set_error(kInvalidArgument, "rkv_decode_static: empty shape");
   const Layout L = make_layout(heads, group, dim, n_blocks);
-  if ((size_t)L.total > kStaticScratchBytes)
+  if ((size_t)L.total > kStaticWorkspaceBytes)
     return set_error(kWorkspaceTooSmall,
                      "rkv_decode_static: this shape needs %lld bytes of workspace, more than the "
                      "static scratch's %lld; use rkv_decode with a caller workspace",
-                     (long long)L.total, (long long)kStaticScratchBytes);
+                     (long long)L.total, (long long)kStaticWorkspaceBytes);
   char* ws = nullptr;
   int rc = static_scratch(&ws);
   if (rc) return rc;
-  // the one-launch step's counters and tagged slots start at zero
+  // the one-launch step's counters and tagged slots start at zero (the
+  // launch counters restart, so a slot left by an earlier call must not carry
+  // a tag this call's launches use)
   if ((rc = zero_region(ws, L.control, control_bytes(heads, L.tile_stride), stream)) ||
-      (rc = zero_region(ws, L.lse_slots, heads * group * L.tile_stride * 32, stream)) ||
-      (rc = zero_region(ws, L.xbits, heads * L.tile_stride * 16, stream)))
+      (rc = zero_region(ws, L.lse_slots, L.part_acc + heads * group * L.tile_stride * dim * 8 -
+                                             L.lse_slots, stream)) ||
+      (rc = zero_region(ws, L.counts, L.total - L.counts, stream)))
     return rc;
+  g_error_word = reinterpret_cast<uint32_t*>(ws + kStaticWorkspaceBytes);
   rc = rkv_decode(query, key_mean, ellipsoid, value_mean, value_norm, max_value_norm, key_pages,
                   key_page_head_stride, value_pages, value_page_head_stride, key_suffix,
                   key_suffix_head_stride, key_suffix_token_stride, value_suffix,
                   value_suffix_head_stride, value_suffix_token_stride, suffix_capacity,
                   suffix_length, heads, group, dim, n_blocks, block_size, prompt_length, eps,
                   reduction, anchor_mask, mask_out, output, accessed_blocks, ws,
-                  kStaticScratchBytes, stream);
+                  kStaticWorkspaceBytes, stream);
+  g_error_word = nullptr;
   if (rc) {
     // rkv_decode's message names rkv_decode; say which entry point failed
     char message[512];
     snprintf(message, sizeof(message), "%s", rkv_last_error());
     return set_error(rc, "rkv_decode_static: %s", message);
+  }
+  return kOk;
+}
+
+// The static scratch's status word on the current device (bit 0: a wait of
+// an rkv_decode_static call gave up since the word was last cleared; that
+// call's output rows were written as NaN and its mask as all-expanded).
+// Copies the word to the host and synchronizes `stream`; with clear != 0 it
+// then zeroes the word (a one-thread kernel on `stream`).  Not for capture.
+extern "C" int rkv_static_status(uint32_t* status, int clear, hipStream_t stream) {
+  clear_error();
+  if (!status) return set_error(kInvalidArgument, "rkv_static_status: null status");
+  char* ws = nullptr;
+  int rc = static_scratch(&ws);
+  if (rc) return rc;
+  uint32_t* word = reinterpret_cast<uint32_t*>(ws + kStaticWorkspaceBytes);
+  uint32_t host = 0;
+  if (hipMemcpyAsync(&host, word, sizeof(host), hipMemcpyDeviceToHost, stream) != hipSuccess ||
+      hipStreamSynchronize(stream) != hipSuccess)
+    return set_error(kLaunchFailed, "rkv_static_status: copy failed");
+  *status = host;
+  if (clear) {
+    clear_word_kernel<<<1, 1, 0, stream>>>(word);
+    return check_launch("clear_word_kernel");
   }
   return kOk;
 }
@@ -3677,3 +3788,13 @@ extern "C" int rkv_dense_decode(const void* query, const void* keys, int64_t key
   if (rc) return rc;
   return launch_dense(p, P);
 }
+
+#if defined(RKV_PHASE_STAMPS)
+// The phase-stamps build only: copies the stamps of the last step launch on
+// each (head, workgroup) row to host memory (bytes = 64 * 256 * kStamps * 8).
+extern "C" int rkv_phase_stamps_read(void* host, size_t bytes) {
+  if (!host || bytes < sizeof(rkv::rkv_stamps)) return 1;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(rkv::rkv_stamps), sizeof(rkv::rkv_stamps)) ==
+                 hipSuccess ? 0 : 3;
+}
+#endif

@@ -85,6 +85,8 @@ def _bind(lib):
     lib.rkv_set_speculation.restype = _int
     lib.rkv_decode_static.argtypes = lib.rkv_decode.argtypes[:-3] + [_p]
     lib.rkv_decode_static.restype = _int
+    lib.rkv_static_status.argtypes = [_p, _int, _p]
+    lib.rkv_static_status.restype = _int
     lib.rkv_dense_decode.argtypes = [_p, _p, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64,
                                      _p, _p, _p, _size, _p]
     lib.rkv_dense_decode.restype = _int
@@ -185,7 +187,7 @@ def workspace_bytes(heads, group, dim, n_blocks):
     return int(lib().rkv_workspace_bytes(heads, group, dim, n_blocks))
 
 
-LAYOUT_NAMES = ("control", "zf", "lse", "lse_slots", "part_ml", "part_acc", "counts", "xbits",
+LAYOUT_NAMES = ("control", "zf", "lse", "lse_slots", "part_ml", "part_acc", "counts", "full",
                 "total", "n_tiles", "z_stride", "tile_stride", "step_workers")
 # rkv_set_decode_path codes: the one-launch step where it fits, or always the
 # three kernels (score, attend, merge).
@@ -387,12 +389,11 @@ SPECULATION_MODES = {"off": 0, "auto": 1, "always": 2}
 
 
 def set_speculation(mode="auto"):
-    """Test hook: the one-launch step's speculation (attending every block's
-    rows before the decision when the previous launch on the workspace
-    expanded every block) for later calls on this thread: "off", "auto" (the
-    default: where a workgroup's share of a head's rows is at least 2048) or
-    "always"; True and False mean "auto" and "off".  Results are the same bit
-    for bit either way."""
+    """Test hook: the one-launch step's speculation (issuing the first page
+    rows of a workgroup's tile before the decision when the previous launch
+    on the workspace expanded every block of it) for later calls on this
+    thread: "off", "auto" (the default) or "always"; True and False mean
+    "auto" and "off".  Results are the same bit for bit either way."""
     if isinstance(mode, bool):
         mode = "auto" if mode else "off"
     if mode not in SPECULATION_MODES:
@@ -403,9 +404,23 @@ def set_speculation(mode="auto"):
 def decode_static(query, summary, key_suffix, value_suffix, config, output, mask,
                   anchor_mask=None, suffix_length=None, accessed=None):
     """decode() through rkv_decode_static: the library's own device scratch,
-    no workspace, nothing allocated by the call; output (H, G, 1, D) and mask
-    (H, N) bool are the caller's."""
+    no workspace, nothing allocated by the call; output (H, G, 1, D) in the
+    query's dtype and mask (H, N) bool are the caller's, contiguous and on
+    the query's device (checked before the call: the kernels write them
+    whole)."""
     heads, group, _, dim = query.shape
+    expect = ((output, (heads, group, 1, dim), query.dtype, "output"),
+              (mask, (heads, summary.num_blocks), torch.bool, "mask"))
+    for t, shape, dtype, name in expect:
+        if tuple(t.shape) != shape or t.dtype != dtype:
+            raise ValueError(f"rkv_decode_static: {name} must be {shape} {dtype}, "
+                             f"got {tuple(t.shape)} {t.dtype}")
+        if t.device != query.device or not t.is_contiguous():
+            raise ValueError(f"rkv_decode_static: {name} must be contiguous on {query.device}")
+    if accessed is not None and (accessed.dtype != torch.int64 or accessed.numel() < 1 or
+                                 accessed.device != query.device):
+        raise ValueError("rkv_decode_static: accessed must be an int64 tensor on the query's "
+                         "device")
     q = query.reshape(heads * group, dim)
     if not q.is_contiguous():
         q = q.contiguous()
@@ -422,6 +437,18 @@ def decode_static(query, summary, key_suffix, value_suffix, config, output, mask
         _ptr(accessed), _stream(query.device))
     _check(rc, "rkv_decode_static")
     return output, mask
+
+
+def static_status(clear=False):
+    """The status word of rkv_decode_static's scratch on the current device
+    (bit 0: a hand-off wait of a static call gave up since the last clear;
+    that call wrote NaN output rows and an all-expanded mask); a host
+    synchronization.  clear=True zeroes it after reading."""
+    word = ctypes.c_uint32()
+    device = torch.device("cuda", torch.cuda.current_device())
+    _check(lib().rkv_static_status(ctypes.byref(word), 1 if clear else 0, _stream(device)),
+           "rkv_static_status")
+    return int(word.value)
 
 
 # ---------------------------------------------------------------------------

@@ -100,8 +100,9 @@ def test_workspace_size_covers_layout(lib):
         assert layout["part_ml"] - layout["lse_slots"] >= rows * ts * 32
         assert layout["part_acc"] - layout["part_ml"] >= rows * ts * 8
         assert layout["counts"] - layout["part_acc"] >= rows * ts * dim * 4
-        assert layout["xbits"] - layout["counts"] >= heads * ts * 4
-        assert layout["total"] - layout["xbits"] >= heads * ts * 16
+        assert layout["full"] - layout["counts"] >= heads * ts * 4
+        # the step's per-workgroup speculation flags (u64 each)
+        assert layout["total"] - layout["full"] >= heads * ts * 8
         # the one-launch step's workgroups per head: every tile, topped up
         # with copies to min(S / heads, 256), each with a per-tile slot (S =
         # 256 for the 16-row kernels, which hold one workgroup per CU); with

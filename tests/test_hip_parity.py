@@ -40,9 +40,10 @@ def decode_path(hip, request):
 
 
 def assert_control_clean(hip, ws):
-    """After every launch each head's merge counter is step_workers times the
-    launch count that every workgroup's own counter holds, and no hand-off
-    wait gave up.  Returns the launch count."""
+    """After every launch every workgroup's own launch counter holds the same
+    launch count, no hand-off wait gave up (status word clear) and no head's
+    poison word carries the last launch's tag (launch e tags its slots e + 1,
+    so the last of n launches tags n).  Returns the launch count."""
     heads, group, dim, n = ws["hip_scratch_shape"]
     layout = hip.workspace_layout(heads, group, dim, n)
     tiles, ts = layout["step_workers"], layout["tile_stride"]
@@ -52,7 +53,7 @@ def assert_control_clean(hip, ws):
     assert hip.workspace_status(ws) == 0
     launches = words[(heads + 1) * 8:(heads + 1) * 8 + heads * ts].reshape(heads, ts)[:, :tiles]
     assert np.all(launches == launches[0, 0]), launches
-    assert np.all(lines[:heads, 1] == launches[0, 0] * tiles), lines[:heads, 1]
+    assert launches[0, 0] == 0 or np.all(lines[:heads, 3] != launches[0, 0]), lines[:heads, 3]
     # start-order tickets: none, or one per workgroup of every launch
     assert lines[heads, 1] in (0, launches[0, 0] * tiles * heads), lines[heads, 1]
     return int(launches[0, 0])
@@ -543,10 +544,11 @@ def test_graph_replays_match_eager(hip, decode_path):
     (8, 4, 128, 32, 8192), (4, 7, 128, 64, 8192), (2, 8, 64, 16, 3000)])
 def test_speculation_matches_the_normal_order_bit_for_bit(hip, heads, group, dim, block,
                                                           prompt):
-    """After a launch that expanded every block, the step's workgroups attend
-    every row before the decision: when every block expands again the result
-    is the normal order's bit for bit, and when not (a sparse eps on the same
-    workspace) the speculation is dropped and the normal order runs."""
+    """After a launch that expanded every block of its tile, a step workgroup
+    issues its tile's first page rows before the decision: when every block
+    expands again the ring goes on from them and the result is the normal
+    order's bit for bit, and when not (a sparse eps on the same workspace)
+    the speculation is dropped and the normal order runs."""
     inp = _decode_case(heads, group, dim, block, prompt, 0.05, suffix=16, seed=5)
     full = RefineKVConfig(backend="hip", block_size=block, eps=0.0, gqa_reduction="any")
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), full)
@@ -567,8 +569,6 @@ def test_speculation_matches_the_normal_order_bit_for_bit(hip, heads, group, dim
             want_sparse = run(sparse, {})
             if not want_sparse[1].all():
                 break
-        # (these prompts give each workgroup fewer rows than the default mode
-        # speculates on)
         hip.set_speculation("always")
         assert want_full[1].all() and not want_sparse[1].all()
         ws = {}
@@ -793,8 +793,10 @@ def test_several_tiles_per_workgroup_128k_block16(hip, oracle_lib):
 def test_handoff_give_up_is_reported_and_recoverable(hip, oracle_lib):
     """With the test hook every wait of the one-launch step accepts no data
     and gives up after 64 polls: every kernel still ends, the status word is
-    set and check_workspace raises.  After clearing it, the same workspace
-    decodes correctly again."""
+    set and check_workspace raises, and the call's result says so in-band:
+    every output row is NaN and every block is marked expanded (a plain call
+    or a graph replay cannot return a plausible wrong answer).  After
+    clearing the word, the same workspace decodes correctly again."""
     inp = _decode_case(8, 4, 128, 32, 8192, 0.02, suffix=9, seed=4)
     cfg = RefineKVConfig(backend="hip", eps=0.01)
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
@@ -807,11 +809,13 @@ def test_handoff_give_up_is_reported_and_recoverable(hip, oracle_lib):
     assert hip.workspace_status(ws) == 0
     hip.set_handoff_test(64, 1)
     try:
-        sparse_attention(*args, workspace=ws)
+        bad = sparse_attention(*args, workspace=ws, return_selected=True)
         torch.cuda.synchronize()
     finally:
         hip.set_handoff_test(0, 0)
     assert hip.workspace_status(ws) & 1
+    assert torch.isnan(bad.output.float()).all()
+    assert bad.selected.all()
     with pytest.raises(hip.HandoffError):
         hip.check_workspace(ws)
     hip.clear_workspace_status(ws)

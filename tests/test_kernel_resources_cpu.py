@@ -84,18 +84,20 @@ def _instances(kernels, family):
 
 
 @needs_tools
-def test_step_kernel_exists_only_up_to_head_dim_160(kernels):
+def test_step_kernel_exists_only_up_to_head_dim_128(kernels):
     dims = {args[0] for args, _ in _instances(kernels, "step_kernel")}
-    assert dims == {32, 64, 96, 128, 160}, dims
+    assert dims == {32, 64, 96, 128}, dims
 
 
 @needs_tools
 def test_no_scratch_in_the_kernels_of_common_shapes(kernels):
     """Scratch (register spills or dynamically indexed arrays) is allowed
-    only in the 16-row builds (GQA groups above 8) and the 8-row step at
+    only in the 16-row builds (GQA groups above 8), the 8-row step at
     head_dim 128, whose two four-row score passes keep both passes' loads
-    live; every other decode and summary kernel runs without it."""
-    allowed = {("step_kernel", (128, 8, 0, 1))}
+    live, and the head_dim-160 attend kernel (its two rings of
+    five-operand chunks spill 9 registers); every other decode and summary
+    kernel runs without it."""
+    allowed = {("step_kernel", (128, 8, 0, 1)), ("attend_kernel", (160, 4))}
     for family in ("step_kernel", "attend_kernel", "score_kernel", "summary_kernel"):
         for args, res in _instances(kernels, family):
             rows16 = family in ("step_kernel", "attend_kernel") and args[1] == 16

@@ -3,7 +3,9 @@ rkv_decode on the same inputs: bit-identical outputs, masks and access
 counts, for two calls in a row on one stream, the second with a smaller
 shape (different layout of the shared scratch), and again in the reverse
 order; a shape whose workspace exceeds the scratch is refused before any
-launch."""
+launch; a static call whose hand-off waits give up (forced from the host,
+every kernel still ends) reports it in its own status word, which the next
+call does not clear, and in-band: NaN output rows, every block expanded."""
 
 import numpy as np
 import pytest
@@ -80,3 +82,48 @@ def test_static_scratch_rejects_oversized_shapes(hip):
         torch.cuda.current_stream().cuda_stream)
     assert rc == 4
     assert b"rkv_decode_static" in hip.lib().rkv_last_error()
+
+
+def test_static_scratch_give_up_is_reported(hip):
+    """rkv_set_handoff_test(64, 1): every wait of the static call's one-launch
+    step accepts no data and gives up after 64 polls.  The static status
+    word reports it (and keeps it across the next call, whose fill kernels
+    clear only the shape's counters and slots), the output rows are NaN and
+    the mask is all-expanded; after clearing, a call matches rkv_decode."""
+    shape = SHAPES[0]
+    assert hip.decode_plan(8, 4, 128, 16384 // 32, 32) == "step"
+    inp, cfg, summary, anchor = _case(shape, seed=50)
+    args = (inp["query"], summary, inp["suffix_keys"], inp["suffix_values"], cfg)
+    hip.static_status(clear=True)
+    assert hip.static_status() == 0
+    out = torch.empty(8, 4, 1, 128, dtype=torch.bfloat16, device=DEV)
+    mask = torch.empty(8, summary.num_blocks, dtype=torch.bool, device=DEV)
+    hip.set_handoff_test(64, 1)
+    try:
+        hip.decode_static(*args, out, mask, anchor)
+        torch.cuda.synchronize()
+    finally:
+        hip.set_handoff_test(0, 0)
+    assert torch.isnan(out.float()).all()
+    assert mask.all()
+    assert hip.static_status() & 1
+    # a clean call afterwards: correct again, and the word still reports the
+    # earlier give-up until it is cleared
+    _both(hip, shape, seed=51)
+    assert hip.static_status(clear=True) & 1
+    assert hip.static_status() == 0
+    _both(hip, shape, seed=52)
+    assert hip.static_status() == 0
+
+
+def test_static_scratch_checks_caller_buffers(hip):
+    inp, cfg, summary, anchor = _case(SHAPES[1], seed=53)
+    args = (inp["query"], summary, inp["suffix_keys"], inp["suffix_values"], cfg)
+    good_out = torch.empty(2, 7, 1, 64, dtype=torch.bfloat16, device=DEV)
+    good_mask = torch.empty(2, summary.num_blocks, dtype=torch.bool, device=DEV)
+    for out, mask in ((good_out[:1], good_mask), (good_out, good_mask[:, :-1]),
+                      (good_out.float(), good_mask), (good_out, good_mask.to(torch.uint8)),
+                      (torch.empty(2, 7, 1, 128, dtype=torch.bfloat16, device=DEV)[..., ::2],
+                       good_mask)):
+        with pytest.raises(ValueError, match="rkv_decode_static"):
+            hip.decode_static(*args, out, mask, anchor)
