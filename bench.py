@@ -92,6 +92,13 @@ def parse_args():
                          "through RefineKV(cuda_graph=True) and report per-layer attention "
                          "time and expanded fractions")
     ap.add_argument("--new-tokens", type=int, default=128, help="--model: tokens to generate")
+    ap.add_argument("--flip-query", action="store_true",
+                    help="negate every layer's query at each decode step (inside the graph), so "
+                         "consecutive steps expand different blocks")
+    ap.add_argument("--speculation", choices=("auto", "off"), default="auto",
+                    help="the one-launch step's speculation: a tile whose every block the "
+                         "previous launch expanded issues its page rows before the decision "
+                         "(off: always after it)")
     ap.add_argument("--phases", action="store_true",
                     help="phase timeline of the one-launch step (per-workgroup clock stamps from "
                          "librefinekv_hip_phases.so), then exit")
@@ -209,6 +216,7 @@ def main():
     torch.cuda.set_device(dev)
     lib = _hip.lib()
     _hip.set_decode_path(a.path)
+    _hip.set_speculation(a.speculation)
     kernels = KERNELS[a.path]
     capacity = a.warmup + a.steps + 1
     cfg = RefineKVConfig(backend="hip", block_size=a.block, eps=a.eps,
@@ -235,6 +243,8 @@ def main():
     def step(config, key):
         suffix_len.add_(1)
         for L in layers:
+            if a.flip_query:
+                L["q"].neg_()
             sparse_attention(L["q"], L["summary"], L["k"][:, a.context:], L["v"][:, a.context:],
                              config, workspace=L[key], suffix_length=suffix_len)
 
@@ -451,6 +461,7 @@ def phase_timeline(a):
     _hip.LIB_PATH = os.path.join(os.path.dirname(_hip.LIB_PATH), "librefinekv_hip_phases.so")
     lib = _hip.lib()
     lib.rkv_phase_stamps_read.argtypes = [ctypes.c_void_p, ctypes.c_size_t]
+    _hip.set_speculation(a.speculation)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     layers = min(a.layers, 8)

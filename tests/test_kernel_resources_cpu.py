@@ -67,9 +67,21 @@ def kernels(tmp_path_factory):
             name = re.search(r"\.name:\s+(\S+)", block).group(1)
             table[name] = dict(lds=field("group_segment_fixed_size"),
                                scratch=field("private_segment_fixed_size"),
-                               vgpr=field("vgpr_count"), spill=field("vgpr_spill_count"))
+                               vgpr=field("vgpr_count"), spill=field("vgpr_spill_count"),
+                               obj=str(obj))
     assert table, "no kernels found in the library"
     return table
+
+
+def _scratch_instructions(res, name):
+    """Scratch accesses in a kernel's own disassembly (its frame may hold
+    dead SGPR-spill slots the backend reserves after placing every spill in
+    VGPR lanes: a private segment no instruction touches)."""
+    text = subprocess.run([os.path.join(LLVM, "llvm-objdump"), "-d",
+                           f"--disassemble-symbols={name}", res["obj"]],
+                          check=True, capture_output=True, text=True).stdout
+    assert name in text, name
+    return [l for l in text.splitlines() if re.search(r"\bscratch_(load|store)", l)]
 
 
 def _instances(kernels, family):
@@ -81,6 +93,14 @@ def _instances(kernels, family):
         if m:
             out.append((tuple(int(x) for x in re.findall(r"L[ib](\d+)E", m.group(1))), res))
     return out
+
+
+def _name_of(kernels, family, args):
+    for name in kernels:
+        m = re.search(family + r"I((?:L[ib]\d+E)+)E", name)
+        if m and tuple(int(x) for x in re.findall(r"L[ib](\d+)E", m.group(1))) == args:
+            return name
+    raise KeyError((family, args))
 
 
 @needs_tools
@@ -103,7 +123,10 @@ def test_no_scratch_in_the_kernels_of_common_shapes(kernels):
             rows16 = family in ("step_kernel", "attend_kernel") and args[1] == 16
             if rows16 or (family, args) in allowed:
                 continue
-            assert res["scratch"] == 0 and res["spill"] == 0, (family, args, res)
+            assert res["spill"] == 0, (family, args, res)
+            if res["scratch"]:
+                assert not _scratch_instructions(res, _name_of(kernels, family, args)), (
+                    family, args, res)
     for name, res in kernels.items():
         if any(k in name for k in ("merge_kernel", "decide_kernel", "anchor_decide_kernel")):
             assert res["scratch"] == 0, (name, res)
