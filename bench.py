@@ -237,7 +237,11 @@ def main():
         t_sum += time.perf_counter() - t0
         layers.append(dict(q=q, k=k, v=v, summary=summary, ws={}, dws={}))
     log(f"[bench] {a.layers} layers ready, summary build {t_sum / a.layers * 1e6:.1f} us/layer "
-        "(wall, includes launch)")
+        "(wall, first calls: includes setup)")
+    summary_us = summary_event_us(layers[0]["k"][:, :a.context], layers[0]["v"][:, :a.context],
+                                  cfg)
+    log(f"[bench] summary kernel: {summary_us:.1f} us/layer (HIP events, 5 back-to-back calls "
+        "after a warm one)")
     suffix_len = torch.zeros((), dtype=torch.int32, device=dev)
 
     def step(config, key):
@@ -416,7 +420,8 @@ def main():
             "peak": PEAK_HBM_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / PEAK_HBM_GBPS, 4),
-            "traffic": traffic,
+            "traffic": None if traffic is None else traffic["traffic_bytes"],
+            "traffic_source": None if traffic is None else traffic["source"],
         },
         "cpu_baseline": cpu,
         "expanded_fraction": round(frac, 5),
@@ -432,7 +437,9 @@ def main():
         "dense_GBps": None if dense_us is None else round(
             dense_bytes(a, suffix_now) / (dense_us * 1e-6) / 1e9, 1),
         "speedup_vs_dense": None if dense_best is None else round(dense_best / us_layer, 3),
-        "summary_us_per_layer_wall": round(t_sum / a.layers * 1e6, 1),
+        "summary_us_per_layer": round(summary_us, 1),
+        "summary_timing": "HIP events around 5 back-to-back build_summary calls of one layer's "
+                          "prompt after a warm call (the queue stays ahead of the host)",
         "attention_tokens_per_s": round(1e6 / (us_layer * a.layers), 1),
     }
     print(json.dumps(result), flush=True)
@@ -850,16 +857,40 @@ def model_bench(a):
 
 
 def measured_traffic(kernel):
-    """HBM bytes per launch of `kernel` from the committed rocprofv3 PMC
-    summary (FETCH_SIZE and WRITE_SIZE runs scaled by a plain copy's
-    readings), or None when it has none."""
+    """HBM bytes per launch of `kernel` as profiled, not measured in this run:
+    the committed rocprofv3 PMC summary profiles/traffic.json (FETCH_SIZE and
+    WRITE_SIZE runs scaled by a plain copy's readings) with the commit and
+    date of the kernel it was taken on, or None when it has none."""
     path = os.path.join(ROOT, "profiles", "traffic.json")
     try:
         with open(path) as f:
-            entry = json.load(f)["kernels"].get(kernel)
+            doc = json.load(f)
+        entry = doc["kernels"].get(kernel)
     except (OSError, ValueError, KeyError):
         return None
-    return None if entry is None else entry["traffic_bytes"]
+    if entry is None:
+        return None
+    return {"traffic_bytes": entry["traffic_bytes"],
+            "source": f"profiles/traffic.json (rocprofv3 --pmc FETCH_SIZE/WRITE_SIZE, "
+                      f"kernel of commit {doc.get('kernel_commit', 'unrecorded')}, "
+                      f"{doc.get('measured', 'undated')}), not measured in this run"}
+
+
+def summary_event_us(k, v, cfg):
+    """build_summary of one layer's prompt: a warm call, then HIP events around
+    5 back-to-back calls (each call's host work overlaps the previous call's
+    kernels), per call."""
+    from refinekv import build_summary
+
+    build_summary(k, v, cfg)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(5):
+        build_summary(k, v, cfg)
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) * 1e3 / 5
 
 
 def copy_calibration():

@@ -688,25 +688,32 @@ __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, u
                                              int lane) {
   RowLse r;
   const uint32_t tag = __builtin_amdgcn_readfirstlane(*ss.rtag), mix = tag_mix(tag);
+  // bit k: tile k * 64 + lane exists and its slots have not landed yet (a
+  // poll reloads only those: the slots read past the caches)
+  uint32_t need = 0;
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    r.zm[k] = r.cm[k] = kNegInf;
+    r.zl[k] = r.cl[k] = 0.0f;
+    if ((uint32_t)(k * kWave + lane) < T) need |= 1u << k;
+  }
   for (uint32_t n = 0;; ++n) {
-    bool ok = true;
 #pragma unroll
     for (int k = 0; k < kChunks; ++k) {
-      const uint32_t t = k * kWave + lane;
-      const bool live = t < T;
-      float4 a = make_float4(kNegInf, 0.0f, 0.0f, 0.0f), b = a;
-      if (k * kWave < (int)T) {
-        const uint32_t at = (uint32_t)((row + (live ? t : 0u)) * 2);
-        a = ss.slots.load4(at * 16);
-        b = ss.slots.load4(at * 16 + 16);
-        ok = ok && (!live || (slot_ok(a, tag, mix) && slot_ok(b, tag, mix)));
+      if (k * kWave < (int)T && ((need >> k) & 1u)) {
+        const uint32_t at = (uint32_t)((row + (uint32_t)(k * kWave + lane)) * 2);
+        const float4 a = ss.slots.load4(at * 16);
+        const float4 b = ss.slots.load4(at * 16 + 16);
+        if (slot_ok(a, tag, mix) && slot_ok(b, tag, mix)) {
+          need &= ~(1u << k);
+          r.zm[k] = a.x;
+          r.zl[k] = a.y;
+          r.cm[k] = b.x;
+          r.cl[k] = b.y;
+        }
       }
-      r.zm[k] = live ? a.x : kNegInf;
-      r.zl[k] = live ? a.y : 0.0f;
-      r.cm[k] = live ? b.x : kNegInf;
-      r.cl[k] = live ? b.y : 0.0f;
     }
-    if (__ballot(!ok) == 0) break;
+    if (__ballot(need != 0u) == 0) break;
     if (n + 1 >= ss.spin) {
       if (lane == 0) handoff_gave_up(ss);
       const float nan = bits_f32(0x7FC00000u);

@@ -77,13 +77,29 @@ def _check_hip_summary(summary):
         raise TypeError("the HIP kernels need bf16 summaries (build_summary's format)")
 
 
-def _bf16_pages(summary):
-    """The summary with bf16 page views (a converted copy of the pages when
-    the cache holds another dtype)."""
+def _page_identity(t):
+    return (t.data_ptr(), t._version, t.dtype, tuple(t.shape), tuple(t.stride()))
+
+
+def _bf16_pages(summary, workspace=None):
+    """The summary with bf16 page views: the pages themselves, or a converted
+    copy when the cache holds another dtype.  With a workspace the copy is
+    made once and kept there, keyed by the page tensors' storage, version
+    and layout (a write to the cache bumps the version and converts again),
+    so a decode step does not move the whole prompt's K/V through a
+    conversion (the reference converts only the pages it loads,
+    kernels/attention.py:222-235)."""
     if summary.keys.dtype == torch.bfloat16 and summary.values.dtype == torch.bfloat16:
         return summary
-    return dataclasses.replace(summary, keys=summary.keys.to(torch.bfloat16),
-                               values=summary.values.to(torch.bfloat16))
+    key = (_page_identity(summary.keys), _page_identity(summary.values))
+    cached = workspace.get("hip_bf16_pages") if workspace is not None else None
+    if cached is not None and cached[0] == key:
+        keys, values = cached[1]
+    else:
+        keys, values = summary.keys.to(torch.bfloat16), summary.values.to(torch.bfloat16)
+        if workspace is not None:
+            workspace["hip_bf16_pages"] = (key, (keys, values))
+    return dataclasses.replace(summary, keys=keys, values=values)
 
 
 @torch.no_grad()
@@ -183,7 +199,8 @@ def sparse_attention(
         from . import _hip
 
         _check_hip_summary(summary)
-        output, mask = _hip.decode(query, _bf16_pages(summary), key_suffix.to(torch.bfloat16),
+        output, mask = _hip.decode(query, _bf16_pages(summary, workspace),
+                                   key_suffix.to(torch.bfloat16),
                                    value_suffix.to(torch.bfloat16), config, anchor_mask,
                                    workspace, suffix_length, access_counter)
         return AttentionResult(output, mask if return_selected else None)

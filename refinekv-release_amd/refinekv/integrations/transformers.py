@@ -140,6 +140,31 @@ class _LayerState:
     workspace: dict = field(default_factory=dict)
 
 
+def mask_is_visible_prefix(mask, visible, length):
+    """Whether a decode query's attention mask (None, boolean with True =
+    attend, or additive with 0 = attend and the dtype's minimum or -inf =
+    masked; any broadcastable shape ending in the key length) lets every
+    query head see exactly the tokens [0, visible) of a cache of `length`
+    tokens: what the dense decode kernel attends.  A padded or otherwise
+    masked token inside the prefix, a visible token past it, or any other
+    additive bias gives False (the SDPA path then applies the mask, as
+    transformers.py:510-520 does).  Reads the mask on the host."""
+    if mask is None:
+        return True
+    if mask.shape[-1] != length:
+        return False
+    if mask.dtype == torch.bool:
+        allowed = mask
+    else:
+        zero = mask == 0
+        blocked = mask <= torch.finfo(mask.dtype).min / 2
+        if not bool((zero | blocked).all()):
+            return False
+        allowed = zero
+    want = torch.arange(length, device=mask.device) < visible
+    return bool((allowed == want).all())
+
+
 def _refinekv_attention(module, query, key, value, attention_mask, dropout=0.0, scaling=None,
                         **kwargs):
     """The registered "refinekv" attention function (transformers.py:117-123)."""
@@ -654,8 +679,11 @@ class RefineKV:
         mask over the visible prefix (transformers.py:510-520; the mask-free
         GQA path can round differently in bf16).  With a kernel backend on a
         ROCm device, shapes the dense decode kernel runs go to it instead
-        (the same tokens [0, visible), the same default scaling)."""
-        out = self._hip_dense_decode(query, key, value, scaling, visible, workspace)
+        (the same tokens [0, visible), the same default scaling) when the
+        model's mask lets the query see exactly those tokens."""
+        out = None
+        if mask_is_visible_prefix(mask, visible, key.shape[2]):
+            out = self._hip_dense_decode(query, key, value, scaling, visible, workspace)
         if out is not None:
             return out, None
         if mask is None:

@@ -225,6 +225,29 @@ def test_device_suffix_length_requires_hip():
                          suffix_length=torch.tensor(2, dtype=torch.int32))
 
 
+def test_bf16_page_copy_is_made_once_per_cache_version():
+    """An fp32 cache under the kernel backend: the bf16 copy of the pages is
+    converted once and kept in the workspace; a write to the cache (a new
+    tensor version) converts again, and no workspace means a fresh copy."""
+    from refinekv.attention import _bf16_pages
+
+    keys, values = _cache(2, 71, 64, seed=43, dtype=torch.float32)
+    summary = build_summary(keys, values)
+    ws = {}
+    a = _bf16_pages(summary, ws)
+    b = _bf16_pages(summary, ws)
+    assert a.keys.dtype == a.values.dtype == torch.bfloat16
+    assert a.keys is b.keys and a.values is b.values
+    assert torch.equal(a.keys, summary.keys.to(torch.bfloat16))
+    summary.keys[0, 1, 3] += 1.0  # the cache is written: the copy follows it
+    c = _bf16_pages(summary, ws)
+    assert c.keys is not a.keys and torch.equal(c.keys, summary.keys.to(torch.bfloat16))
+    assert c.values is not a.values or summary.values._version == 0
+    assert _bf16_pages(summary).keys is not c.keys
+    bf = build_summary(keys.to(torch.bfloat16), values.to(torch.bfloat16))
+    assert _bf16_pages(bf, ws) is bf
+
+
 @pytest.fixture
 def one_thread():
     # The fixtures were written single-threaded; MKL's matmul order depends on

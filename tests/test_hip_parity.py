@@ -775,6 +775,37 @@ def test_two_device_fulls_step_512k_block64(hip, oracle_lib):
              eps=0.01, spikes=0.02, suffix=17, anchors=0, seed=23, paths=("step",), repeats=2)
 
 
+def test_sweep_512k_block16_three_kernels(hip, oracle_lib):
+    """The op sweep's 524288-token point at block 16 (8 KV heads, G 4, d 128):
+    32768 blocks, 512 tiles per head, more than the one-launch step holds,
+    so rkv_decode runs the three kernels; masks equal the oracle's, outputs
+    within tolerance."""
+    n_blocks = 524288 // 16
+    assert hip.decode_plan(8, 4, 128, n_blocks, 16) == "split"
+    mask = _op_case(hip, oracle_lib, heads=8, group=4, block=16, prompt=524288,
+                    reduction="any", eps=0.01, spikes=0.02, suffix=17, anchors=0, seed=25,
+                    paths=("step",))
+    assert 0.005 < mask.mean() < 0.1
+
+
+@pytest.mark.parametrize("eps,spikes", [(0.01, 0.02), (0.0, 0.02)], ids=["eps0.01", "eps0"])
+def test_sweep_512k_block64_several_tiles(hip, oracle_lib, eps, spikes):
+    """The op sweep's 524288-token point at block 64 with G 4: 8192 blocks,
+    128 tiles per head, so each of the one-launch step's 64 workgroups per
+    head scores two tiles of 64-token blocks; at eps 0 every block of every
+    head expands (each workgroup's share of the head's 524288 rows).  Both
+    paths, two launches on one workspace."""
+    n_blocks = 524288 // 64
+    assert hip.decode_plan(8, 4, 128, n_blocks, 64) == "step-tiles"
+    mask = _op_case(hip, oracle_lib, heads=8, group=4, block=64, prompt=524288,
+                    reduction="any", eps=eps, spikes=spikes, suffix=33, anchors=0, seed=26,
+                    repeats=2)
+    if eps == 0.0:
+        assert mask.all()
+    else:
+        assert 0.005 < mask.mean() < 0.1
+
+
 def test_several_tiles_per_workgroup_128k_block16(hip, oracle_lib):
     """The headline shape at block 16: 128 tiles per head, twice the 64
     workgroups per head the device holds, so each workgroup of the one-launch

@@ -1,7 +1,8 @@
 """BASELINE.json model configs through the Transformers hook on the GPU.
 
 configs[1] (Llama-3.1-8B shape, 32768-token prompt, block 32, eps 0.01,
-"any", 32 prompt anchors) and configs[3] (Qwen2.5-7B shape, group 7, RoPE
+"any", 32 prompt anchors), configs[2] (the same shape at 131072 prompt
+tokens, no anchors) and configs[3] (Qwen2.5-7B shape, group 7, RoPE
 theta 1e6 with static YaRN factor 4, 65536-token prompt, block 64, eps
 0.005, "max", 64 anchors), random-init weights and uniform random prompt ids:
 a few greedy decode steps with RefineKV(backend="hip", collect_stats=True).
@@ -23,6 +24,8 @@ pytestmark = pytest.mark.gpu
 CONFIGS = {
     "llama32k": dict(family="llama", prompt=32768, block=32, eps=0.01, reduction="any",
                      anchors=32),
+    "llama128k": dict(family="llama", prompt=131072, block=32, eps=0.01, reduction="any",
+                      anchors=0),
     "qwen64k": dict(family="qwen2", prompt=65536, block=64, eps=0.005, reduction="max",
                     anchors=64),
 }
@@ -82,7 +85,10 @@ def test_model_config_decode_calls_match_oracle(name, monkeypatch, oracle_lib):
         layers = mconfig.num_hidden_layers
         assert len(recorder.eager) == DECODE_STEPS * layers
         anchors = [recorder.eager[i]["anchor"] for i in range(layers)]
-        assert all(a is not None and a.any() for a in anchors)
+        if spec["anchors"]:
+            assert all(a is not None and a.any() for a in anchors)
+        else:
+            assert all(a is None for a in anchors)
     group = mconfig.num_attention_heads // mconfig.num_key_value_heads
     # the in-kernel access counter equals the closed form over every call's mask
     blocks = sum(oracle_lib.access_blocks(c["selected"].cpu().numpy(),

@@ -70,6 +70,39 @@ def test_selection_statistics_close(case, oracle_lib):
         assert (np.abs(st[key] - g[key]) <= 1e-4 * scale).all(), key
 
 
+def test_risk_within_propagated_rounding(case, oracle_lib, record_property):
+    """The reference's risk (reference.py risk_bound) against the oracle's.
+    The oracle's z, log Z, log C and delta come from fp32 sums in another
+    order, and every term of the risk is an exponential of them, so the
+    difference is bounded by their differences carried through the exponent:
+    |d risk| <= |risk| (exp(E) - 1) with E = 2 |dz| + |d log Z| + |d log C|
+    + 3 delta D u (delta's relative error after a reordered sum of D
+    non-negative products, u = 2^-24, doubled through its square root and the
+    bound's cosh and log terms) + 16 u (the risk's own roundings).  Wherever
+    delta < 100 (every block of the fixtures of the reference's recipe) E
+    stays below 2e-3, so a dropped or mis-signed term (an O(1) change) fails
+    there; the large-delta and wide-magnitude fixtures hold deltas in the
+    hundreds to thousands and only bound the error."""
+    g, meta, inp = case
+    block = meta["config"]["block_size"]
+    summ = _summary_from_golden(g, inp, block)
+    q = inp["query"][:, :, 0].float().numpy()
+    st = oracle_lib.select_stats(q, summ)
+    u, D = 2.0 ** -24, q.shape[-1]
+    assert np.array_equal(np.isfinite(st["risk"]), np.isfinite(g["risk"]))
+    dl = (np.abs(st["log_z"] - g["log_z"]) + np.abs(st["log_c"] - g["log_c"]))[..., None]
+    E = (2 * np.abs(st["z"] - g["z"]) + dl + 3 * st["delta"].astype(np.float64) * D * u
+         + 16 * u)
+    err = np.abs(st["risk"].astype(np.float64) - g["risk"])
+    allowed = np.abs(g["risk"].astype(np.float64)) * np.expm1(E)
+    record_property("risk_worst_error_over_bound", float((err / np.maximum(allowed, 1e-300)).max()))
+    assert (err <= allowed).all()
+    moderate = st["delta"] < 100
+    assert not moderate.any() or E[moderate].max() < 2e-3, E[moderate].max()
+    if meta["recipe"]["kind"] == "decode_inputs":
+        assert moderate.all()
+
+
 def _near_eps(risk, reduction, eps, rel=1e-6):
     if reduction == "mean":
         stat = risk.mean(1)

@@ -174,6 +174,57 @@ def test_anchor_queries_come_from_the_tail_projection(family, monkeypatch):
         assert all(not st.anchor_mask.any() for st in s._layers.values())
 
 
+def test_visible_prefix_mask_decides_the_dense_kernel():
+    """The dense decode kernel attends tokens [0, visible) and takes no mask,
+    so the hook uses it only when the model's mask says exactly that; a
+    masked (padded) prompt token, a visible token past the prefix or an
+    additive bias sends the call to SDPA with the mask applied."""
+    from refinekv.integrations.transformers import RefineKV as Hook, mask_is_visible_prefix
+
+    L, visible = 12, 9
+    lo = torch.finfo(torch.bfloat16).min
+    prefix = torch.arange(L) < visible
+    additive = torch.zeros(1, 1, 1, L, dtype=torch.bfloat16).masked_fill(~prefix, lo)
+    assert mask_is_visible_prefix(None, visible, L)
+    assert mask_is_visible_prefix(prefix.view(1, 1, 1, L), visible, L)
+    assert mask_is_visible_prefix(additive, visible, L)
+    assert mask_is_visible_prefix(additive.float().masked_fill(~prefix, float("-inf")), visible, L)
+    padded = additive.clone()
+    padded[..., 2] = lo
+    assert not mask_is_visible_prefix(padded, visible, L)
+    assert not mask_is_visible_prefix(prefix.view(1, 1, 1, L) & (torch.arange(L) != 0), visible, L)
+    assert not mask_is_visible_prefix(additive.masked_fill(torch.arange(L) == visible, 0), visible,
+                                      L)
+    assert not mask_is_visible_prefix(additive.masked_fill(torch.arange(L) == 1, -0.5), visible,
+                                      L)
+    assert not mask_is_visible_prefix(additive[..., :L - 1], visible, L)
+
+    # _dense_decode with a padded prompt token: the kernel is not asked, and
+    # SDPA's output ignores the masked token
+    model = tiny_model()
+    attn = model.model.layers[0].self_attn
+    calls = []
+
+    class Self:
+        def _hip_dense_decode(self, *args):
+            calls.append(args)
+            return None
+
+    gen = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 4, 1, 32, generator=gen)
+    k = torch.randn(1, 2, L, 32, generator=gen)
+    v = torch.randn(1, 2, L, 32, generator=gen)
+    out, _ = Hook._dense_decode(Self(), attn, q, k, v, padded.float(), 32 ** -0.5, {}, visible, {})
+    assert not calls
+    v2 = v.clone()
+    v2[:, :, 2] += 100.0  # the masked token's value does not reach the output
+    out2, _ = Hook._dense_decode(Self(), attn, q, k, v2, padded.float(), 32 ** -0.5, {}, visible,
+                                 {})
+    assert torch.equal(out, out2)
+    Hook._dense_decode(Self(), attn, q, k, v, additive.float(), 32 ** -0.5, {}, visible, {})
+    assert len(calls) == 1
+
+
 def test_graph_mode_preconditions_on_cpu():
     model = tiny_model()
     ids = torch.tensor([[3, 4, 5]])
