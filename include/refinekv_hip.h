@@ -85,18 +85,21 @@ int rkv_summary_store(const void* keys, int64_t k_head_stride, int64_t k_token_s
 size_t rkv_workspace_bytes(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks);
 
 /* Byte offsets inside the workspace (for tests): control (hand-off
- * counters: one 64-byte line per KV head -- u64 tiles merged, summed over
- * calls -- then a line starting with a sticky u32 error word, bit 0 set if a
- * hand-off wait gave up, then a u64 call count per tile), zf (float4 z, delta, A, th
- * per query row and block: the selection statistics and the delta-only
- * factors of the risk), lse (per-tile log-sum-exp partials), lse_slots (the
- * same as tagged 16-byte slots for the one-launch step), part_ml, part_acc
- * (per-tile attention partials: (m, l) and acc), counts (per-tile access
- * counts), xbits (per-tile expanded-block masks, tagged slots), total, then
- * n_tiles, the padded row strides (elements) of zf and of the per-tile
+ * counters: one 64-byte line per KV head, then a line starting with a
+ * sticky u32 error word, bit 0 set if a hand-off wait gave up, and the
+ * start-order ticket count, then a u64 launch count per one-launch step
+ * workgroup), zf (float4 z, delta, A, th per query row and block: the
+ * selection statistics and the delta-only factors of the risk), lse
+ * (per-tile log-sum-exp partials), lse_slots (the same as tagged 16-byte
+ * slots for the one-launch step), part_ml, part_acc (per-workgroup attention
+ * partials: (m, l) and acc; tagged 16-byte slots in the one-launch step),
+ * counts (per-workgroup access counts), full (per step workgroup: the tag
+ * + 1 of the last launch that expanded every block of its tile), total,
+ * then n_tiles, the padded row strides (elements) of zf and of the per-tile
  * arrays, and the one-launch step's workgroups per KV head (n_tiles scoring
- * tiles, then helpers that only attend token rows; each has a call counter
- * and a per-tile array entry) -> out13[0..12]. */
+ * tiles, then copies that repeat a tile's decision and take a share of its
+ * token rows; each has a launch counter and a per-tile array entry) ->
+ * out13[0..12]. */
 int rkv_workspace_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks,
                          int64_t* out13);
 
