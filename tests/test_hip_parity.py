@@ -541,14 +541,16 @@ def test_graph_replays_match_eager(hip, decode_path):
 
 
 @pytest.mark.parametrize("heads,group,dim,block,prompt", [
-    (8, 4, 128, 32, 8192), (4, 7, 128, 64, 8192), (2, 8, 64, 16, 3000)])
+    (8, 4, 128, 32, 8192), (4, 7, 128, 64, 8192), (2, 8, 64, 16, 3000),
+    (8, 4, 128, 32, 65536)])
 def test_speculation_matches_the_normal_order_bit_for_bit(hip, heads, group, dim, block,
                                                           prompt):
     """After a launch that expanded every block of its tile, a step workgroup
     issues its tile's first page rows before the decision: when every block
     expands again the ring goes on from them and the result is the normal
     order's bit for bit, and when not (a sparse eps on the same workspace)
-    the speculation is dropped and the normal order runs."""
+    the speculation is dropped and the normal order runs.  (At 65536 tokens
+    a wave has 16 chunks of page rows, most of them after the decision.)"""
     inp = _decode_case(heads, group, dim, block, prompt, 0.05, suffix=16, seed=5)
     full = RefineKVConfig(backend="hip", block_size=block, eps=0.0, gqa_reduction="any")
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), full)
