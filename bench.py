@@ -191,8 +191,8 @@ def main():
     a = parse_args()
     if a.gpus != 1:
         print(f"bench.py measures one GPU; --gpus {a.gpus} is not supported in this build "
-              "(the path would shard by KV head with no exchange; see DESIGN.md)",
-              file=sys.stderr)
+              "(the path would shard by KV head: each GPU would run the op on its heads "
+              "with no exchange inside it)", file=sys.stderr)
         sys.exit(2)
     if a.copy_calibration:
         copy_calibration()
