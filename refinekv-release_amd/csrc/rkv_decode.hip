@@ -6,10 +6,11 @@
 // workgroup (w, h) of the W per KV head h scores tile w mod T (64 blocks),
 // publishes its log-sum-exp partials in tagged slots, reads the head's T
 // tiles' slots, decides its blocks (risk, GQA reduction, anchors), folds its
-// representatives, publishes its expanded-block mask, attends an even share
-// of the head's expanded token rows and its slice of the suffix, publishes
-// an (m, l, acc) partial, and the head's last W / 8 workgroups (at least 8)
-// by ticket merge the partials into the bf16 output.  Heads with more tiles
+// representatives, its slice of the suffix and the token rows of its own
+// tile's expanded blocks (a copy of a tile, with more workgroups than
+// tiles, an even slice of them), publishes an (m, l, acc) partial in tagged
+// slots, and the head's last max(8, W / 8) workgroups by index each merge a
+// column slice of the partials into the bf16 output.  Heads with more tiles
 // than workgroups score up to 4 tiles per workgroup in the same launch.
 // Other shapes run three kernels over the same workspace:
 //
