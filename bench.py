@@ -449,7 +449,8 @@ def main():
 STAMPS = ("entry", "dots", "stats", "gather", "decided", "ring", "pages_wave0", "combine",
           "published", "merge_start", "merged", "spec", "end", "merge_loaded", "merge_folded",
           "merge_stored", "merge_counted", "chunk0", "chunk1", "chunk2", "issued2", "fold0_start",
-          "ring_start", "issue2_addr")
+          "ring_start", "issue2_addr") + tuple(f"fold_start{j}" for j in range(6)) + tuple(
+              f"fold_end{j}" for j in range(6)) + tuple(f"issue_start{j}" for j in range(2, 8))
 STAMP_ROWS_PER_HEAD = 256
 STAMP_HEADS = 64
 

@@ -72,13 +72,14 @@ __host__ __device__ constexpr int64_t control_bytes(int64_t heads, int64_t tile_
 // (row h * 256 + workgroup) as it ends.  LDS stores leave the vector-memory
 // counters alone, so the kernel's own waits are unchanged.  The product build
 // compiles every stamp to nothing.
-constexpr int kStamps = 24;
+constexpr int kStamps = 42;
 constexpr int kStampRowsPerHead = 256;
 enum Stamp {
   kStEntry = 0, kStDots, kStStats, kStGather, kStDecided, kStRing, kStPagesWave0, kStCombine,
   kStPublished, kStMergeWait, kStMerged, kStSpec, kStEnd, kStMergeLoaded,
   kStMergeFolded, kStMergeStored, kStMergeCounted, kStChunk0, kStChunk1, kStChunk2,
-  kStIssued2, kStFold0Start, kStRingStart, kStIssue2Addr
+  kStIssued2, kStFold0Start, kStRingStart, kStIssue2Addr,
+  kStFoldStart0, kStFoldEnd0 = kStFoldStart0 + 6, kStIssueStart2 = kStFoldEnd0 + 6
 };
 #if defined(RKV_PHASE_STAMPS)
 constexpr int kStampHeads = 64;
@@ -680,7 +681,11 @@ __device__ __forceinline__ void handoff_gave_up(const StepStats& ss) {
 // from the tagged slots, read until every slot carries this launch's tag
 // (at most ss.spin rounds; then the wait is recorded as given up and the
 // partials come back NaN, so log Z and log C are not finite and the
-// decision's fail-safe expands every block).
+// decision's fail-safe expands every block).  With one tile per lane (T <=
+// 64) the polls after the first keep two reads of the missing slots in
+// flight: a poll that returns incomplete is reissued at once while the
+// other is still out, so a slot that lands is seen sooner than with one
+// round trip at a time.
 struct RowLse {
   float zm[kChunks], zl[kChunks], cm[kChunks], cl[kChunks];
 };
@@ -697,6 +702,55 @@ __device__ __forceinline__ RowLse gather_lse(const StepStats& ss, int64_t row, u
     r.zm[k] = r.cm[k] = kNegInf;
     r.zl[k] = r.cl[k] = 0.0f;
     if ((uint32_t)(k * kWave + lane) < T) need |= 1u << k;
+  }
+  if (T <= (uint32_t)kWave) {
+    const uint32_t at = (uint32_t)((row + (uint32_t)lane) * 2) * 16u;
+    bool miss = need != 0u;
+    auto take = [&](float4 a, float4 b) {
+      if (miss && slot_ok(a, tag, mix) && slot_ok(b, tag, mix)) {
+        miss = false;
+        r.zm[0] = a.x;
+        r.zl[0] = a.y;
+        r.cm[0] = b.x;
+        r.cl[0] = b.y;
+      }
+    };
+    float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b0 = a0, a1 = a0, b1 = a0;
+    if (miss) {
+      a0 = ss.slots.load4(at);
+      b0 = ss.slots.load4(at + 16u);
+    }
+    take(a0, b0);
+    if (__ballot(miss) == 0) return r;
+    if (miss) {
+      a0 = ss.slots.load4(at);
+      b0 = ss.slots.load4(at + 16u);
+    }
+    __builtin_amdgcn_s_sleep(8);
+    if (miss) {
+      a1 = ss.slots.load4(at);
+      b1 = ss.slots.load4(at + 16u);
+    }
+    for (uint32_t n = 3;; n += 2) {
+      take(a0, b0);
+      if (__ballot(miss) == 0) break;
+      if (n >= ss.spin) {
+        if (lane == 0) handoff_gave_up(ss);
+        r.zm[0] = r.cm[0] = bits_f32(0x7FC00000u);
+        break;
+      }
+      if (miss) {
+        a0 = ss.slots.load4(at);
+        b0 = ss.slots.load4(at + 16u);
+      }
+      take(a1, b1);
+      if (__ballot(miss) == 0) break;
+      if (miss) {
+        a1 = ss.slots.load4(at);
+        b1 = ss.slots.load4(at + 16u);
+      }
+    }
+    return r;
   }
   for (uint32_t n = 0;; ++n) {
 #pragma unroll
@@ -2217,6 +2271,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
     mma_issue_rows<D>(kres, vres, stage.bytes[sidx], kop, row, row);
   };
   auto issue = [&](uint32_t j, int sidx, Bf16x8 (&kop)[S::kSteps]) {
+    RKV_STAMP(stamps, kStIssueStart2 + (j - 2u), tid == 0 && j >= 2u && j < 8u);
     if (j < Rr) issue_reps(j, stage.bytes[sidx], kop);
     else if (j < n1()) issue_suffix(j, sidx, kop);
     else issue_page(j, sidx, kop);
@@ -2322,6 +2377,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
                 [&](uint32_t j, int sidx, const Bf16x8 (&kop)[S::kSteps]) {
                   float x[4];
                   RKV_STAMP(stamps, kStFold0Start, tid == 0 && j == 0u);
+                  RKV_STAMP(stamps, kStFoldStart0 + j, tid == 0 && j < 6u);
                   if (j < Rr) {
                     if (!reps_live(j)) return;
                     rep_logits(j, x);
@@ -2332,6 +2388,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
                   }
                   mma_fold<D>(st, x, stage.bytes[sidx]);
                   RKV_STAMP(stamps, kStChunk0 + (j < 3u ? j : 2u), tid == 0 && j < 3u);
+                  RKV_STAMP(stamps, kStFoldEnd0 + j, tid == 0 && j < 6u);
                 });
   } else {
     // (head_dim 160: one ring of every kind holds more registers than the

@@ -227,3 +227,72 @@ def test_head_dim_256_block_64_index_ranges():
     d = np.arange(0, D)[None, :]
     assert ((r * tile_stride + T - 1) * D + d).max() < H * G * tile_stride * D
     assert (r * D + d).max() < H * G * D
+
+
+# Instructions that count in lgkmcnt (LDS, scalar memory, messages).
+_LGKM = re.compile(r"^(ds_|s_load|s_buffer_load|s_memrealtime|s_memtime|s_sendmsg|s_dcache)")
+
+
+def _vregs(operand):
+    operand = operand.strip()
+    m = re.match(r"v\[(\d+):(\d+)\]$", operand)
+    if m:
+        return set(range(int(m.group(1)), int(m.group(2)) + 1))
+    m = re.match(r"v(\d+)$", operand)
+    return {int(m.group(1))} if m else set()
+
+
+def _unwaited_transposed_reads(lines):
+    """Transposing LDS reads (ds_read_b64_tr_b16) whose destination registers
+    are read or overwritten, or whose block is left, before an s_waitcnt
+    lgkmcnt(k) that covers them (k at most the lgkmcnt operations issued
+    after the read).  The fold issues these reads from inline asm, which the
+    compiler does not see as loads: a copy it placed between a read and its
+    wait would take the registers before the data lands."""
+    ins = []
+    for line in lines:
+        m = re.match(r"\s+([a-z_0-9]+)\s*(.*?)\s*(//.*)?$", line)
+        if m:
+            ins.append((m.group(1), m.group(2)))
+        elif line.strip().endswith(":"):
+            ins.append(("<label>", ""))
+    bad = []
+    for i, (op, args) in enumerate(ins):
+        if op != "ds_read_b64_tr_b16":
+            continue
+        dst, after = _vregs(args.split(",")[0]), 0
+        for op2, args2 in ins[i + 1:]:
+            if op2 in ("<label>", "s_branch", "s_setpc_b64") or op2.startswith("s_cbranch"):
+                bad.append((i, op2))
+                break
+            if op2 == "s_waitcnt":
+                m = re.search(r"lgkmcnt\((\d+)\)", args2)
+                if m and int(m.group(1)) <= after:
+                    break
+            ops = args2.split(",")
+            writes = not op2.startswith(("s_", "buffer_store", "global_store", "ds_write"))
+            srcs = set().union(*(_vregs(o) for o in (ops[1:] if writes else ops)))
+            if srcs & dst or (writes and _vregs(ops[0]) & dst):
+                bad.append((i, f"{op2} {args2}"))
+                break
+            if _LGKM.match(op2):
+                after += 1
+    return bad
+
+
+@needs_tools
+def test_transposed_reads_are_waited_for_before_use(kernels):
+    """Every asm-issued transposing LDS read of the step, attend and dense
+    kernels is covered by its lgkmcnt wait before anything touches its
+    registers (checked on this repository's own gfx950 disassembly)."""
+    checked = 0
+    for obj in sorted({res["obj"] for res in kernels.values()}):
+        text = subprocess.run([os.path.join(LLVM, "llvm-objdump"), "-d", obj],
+                              check=True, capture_output=True, text=True).stdout
+        for block in re.split(r"\n(?=[0-9a-f]{16} <)", text):
+            m = re.match(r"[0-9a-f]{16} <([^>]+)>:", block)
+            if not m or "ds_read_b64_tr_b16" not in block:
+                continue
+            assert not _unwaited_transposed_reads(block.splitlines()[1:]), m.group(1)
+            checked += block.count("ds_read_b64_tr_b16")
+    assert checked > 0
