@@ -9,8 +9,9 @@
 // representatives, its slice of the suffix and the token rows of its own
 // tile's expanded blocks (a copy of a tile, with more workgroups than
 // tiles, an even slice of them), publishes an (m, l, acc) partial in tagged
-// slots, and the head's last max(8, W / 8) workgroups by index each merge a
-// column slice of the partials into the bf16 output.  Heads with more tiles
+// slots, and the head's last max(8, W / 4) workgroups by index (at most
+// head_dim / 2) each merge a column slice of the partials into the bf16
+// output.  Heads with more tiles
 // than workgroups score up to 4 tiles per workgroup in the same launch.
 // Other shapes run three kernels over the same workspace:
 //
@@ -1604,7 +1605,7 @@ __device__ __forceinline__ void merge_state2(float m2, float d2, float n2a, floa
 // The merge of a head's partials.  Every workgroup publishes its partial as
 // tagged slots (the LSE slots' format and tag): per query row one slot
 // (m, l) and one per column pair (acc[2p], acc[2p + 1]), and one slot with
-// its access count.  The head's last K = mergers(W) workgroups by index each
+// its access count.  The head's last K = mergers(W, D) workgroups by index each
 // merge a column slice: slice m covers pairs [m P / K, (m + 1) P / K) of
 // every row (P = D / 2).  A merger polls the slots it needs until every one
 // carries this launch's tag, reloading only those still missing, so after
@@ -1617,10 +1618,16 @@ __device__ __forceinline__ void merge_state2(float m2, float d2, float n2a, floa
 constexpr int kMergers = 8;
 constexpr int kMergeHeld = 8;  // partials a lane holds per batch
 
-// Mergers of a head of W workgroups: W / 8, at least 8 (or W) -- the slices
-// shrink as the partials to fold per slice grow.
-__host__ __device__ __forceinline__ uint32_t mergers(uint32_t W) {
-  const uint32_t k = W / 8u > (uint32_t)kMergers ? W / 8u : (uint32_t)kMergers;
+// Mergers of a head of W workgroups at head_dim D: W / 4, at least 8, at
+// most W and D / 2 (every slice keeps at least one column pair, so slice 0,
+// which also counts and marks a failed hand-off, always has units).  Slices
+// shrink as the partials to fold per slice grow: each merger's poll reloads
+// fewer slots per round (at 64 workgroups per head 16 mergers measured
+// 0.6 us faster per layer-step than 8, and 32 slower again; at 128, 32
+// beat 16 and 64).
+__host__ __device__ __forceinline__ uint32_t mergers(uint32_t W, uint32_t D) {
+  uint32_t k = W / 4u > (uint32_t)kMergers ? W / 4u : (uint32_t)kMergers;
+  if (k > D / 2u) k = D / 2u;
   return W < k ? W : k;
 }
 
@@ -2481,7 +2488,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   RKV_STAMP(stamps, kStPublished, tid == 0);
   if constexpr (kFused) {
     // the head's last K workgroups each merge a column slice
-    const uint32_t K = mergers(W);
+    const uint32_t K = mergers(W, (uint32_t)D);
     if (wk >= W - K) {
       RKV_STAMP(stamps, kStMergeWait, tid == 0);
       merge_slice<D>(a, *sx, h, (int)(wk - (W - K)), (int)K);
