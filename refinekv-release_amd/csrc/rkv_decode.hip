@@ -121,7 +121,7 @@ struct Layout {
   int64_t n_tiles, z_stride, tile_stride;
   int64_t step_workers;  // workgroups per head of the one-launch step
   int64_t step_tiles;    // tiles its workgroups score, at most (1: one each)
-  int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, full, total;
+  int64_t control, zf, lse, lse_slots, part_ml, part_acc, counts, full, row_lse, total;
 };
 
 __host__ __device__ inline int64_t align256(int64_t x) { return (x + 255) & ~int64_t(255); }
@@ -172,6 +172,8 @@ Layout make_layout(int64_t heads, int64_t group, int64_t dim, int64_t n_blocks) 
   L.part_acc = take(rows * L.tile_stride * dim * 8);
   L.counts = take(heads * L.tile_stride * 16);
   L.full = take(heads * L.tile_stride * 8);
+  // per row log Z, log C merged once (three-kernel path, more than 64 tiles)
+  L.row_lse = take(rows * 2 * 4);
   L.total = off;
   return L;
 }
@@ -540,6 +542,7 @@ struct DecideArgs {
   bool write_mask;              // false: mask only stands in for a null anchor
   float* risk_out;              // (H, G, N) or null
   float* stats_out;             // (H, G, 2) or null: log Z, log C
+  const float* row_lse;         // (H, G, 2) log Z, log C merged once per row, or null
   int64_t n_blocks, n_tiles, block, length;
   int64_t z_stride, tile_stride;
   int group, reduction;
@@ -881,6 +884,11 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
     }
   } else {
     auto row_stats = [&](int g, float4 part, float4 zf) {
+      if (a.row_lse != nullptr) {
+        // (merged once per row by lse_merge_kernel, in this same order)
+        row_tail(g, a.row_lse[(rh * G + g) * 2], a.row_lse[(rh * G + g) * 2 + 1], zf);
+        return;
+      }
       const float* prow = a.lse + (rh * G + g) * a.tile_stride * 4;
       if (lane >= T) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
       auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
@@ -1033,6 +1041,31 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a,
   const DecideLoads in = decide_issue(a, blockIdx.y, blockIdx.x);
   decide_finish(a, blockIdx.y, blockIdx.x, in, sh, nullptr, list, count);
   if (accessed && threadIdx.x == 0) atomicAdd(accessed, (unsigned long long)count);
+}
+
+// log Z and log C of every row from its tiles' partials, once per row, in
+// decide_finish's order (merge_lse over the lane partials), for heads of more
+// than 64 tiles: each tile's decision then reads two floats instead of
+// merging every tile's partials again.  Wave w of workgroup b takes row
+// 4 b + w.
+__global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* lse, float* row_lse,
+                                                             int64_t rows, int64_t n_tiles,
+                                                             int64_t tile_stride) {
+  const int lane = threadIdx.x % kWave;
+  const int64_t r = (int64_t)blockIdx.x * kWaves + __builtin_amdgcn_readfirstlane(threadIdx.x / kWave);
+  if (r >= rows) return;
+  const float* prow = lse + r * tile_stride * 4;
+  const int tl = lane < n_tiles ? lane : 0;
+  float4 part = *reinterpret_cast<const float4*>(prow + tl * 4);
+  if (lane >= n_tiles) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
+  auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
+  auto pc = [&](int64_t t) { return make_float2(prow[t * 4 + 2], prow[t * 4 + 3]); };
+  const float lz = merge_lse(part.x, part.y, pz, n_tiles, lane);
+  const float lc = merge_lse(part.z, part.w, pc, n_tiles, lane);
+  if (lane == 0) {
+    row_lse[r * 2] = lz;
+    row_lse[r * 2 + 1] = lc;
+  }
 }
 
 // Batched anchor selection: the union over `anchors` queries of their
@@ -2980,6 +3013,7 @@ DecideArgs decide_args(const SelectParams& p, const Layout& L) {
   da.write_mask = true;
   da.risk_out = p.risk_out;
   da.stats_out = p.stats_out;
+  da.row_lse = nullptr;
   da.n_blocks = p.n_blocks;
   da.n_tiles = L.n_tiles;
   da.block = p.block;
@@ -3001,13 +3035,27 @@ int launch_score(const SelectParams& p, const Layout& L, int64_t queries = 1) {
   return check_launch("score_kernel");
 }
 
+// With more than 64 tiles per head the rows' log Z / log C are merged once
+// (lse_merge_kernel) and every tile's decision reads them: da.row_lse.
+int launch_lse_merge(const SelectParams& p, const Layout& L, int64_t queries, DecideArgs& da) {
+  if (L.n_tiles <= kWave) return kOk;
+  const int64_t rows = p.heads * queries * p.group;
+  float* row_lse = at<float>(p.ws, L.row_lse);
+  lse_merge_kernel<<<dim3((unsigned)((rows + kWaves - 1) / kWaves)), dim3(kThreads), 0,
+                     p.stream>>>(at<float>(p.ws, L.lse), row_lse, rows, L.n_tiles, L.tile_stride);
+  const int rc = check_launch("lse_merge_kernel");
+  if (rc == kOk) da.row_lse = row_lse;
+  return rc;
+}
+
 // Selection only (rkv_select): score and decide kernels.
 int launch_select(const SelectParams& p, const Layout& L) {
   mark(0, p.stream);
   int rc = launch_score(p, L);
   if (rc) return rc;
   mark(1, p.stream);
-  const DecideArgs da = decide_args(p, L);
+  DecideArgs da = decide_args(p, L);
+  if ((rc = launch_lse_merge(p, L, 1, da))) return rc;
   decide_kernel<<<dim3((unsigned)L.n_tiles, (unsigned)p.heads), dim3(kThreads), 0, p.stream>>>(
       da, p.accessed);
   rc = check_launch("decide_kernel");
@@ -3024,6 +3072,7 @@ int launch_select_anchors(const SelectParams& p, int64_t anchors) {
   if (rc) return rc;
   DecideArgs da = decide_args(p, L);
   da.write_mask = false;  // the mask only stands in for the (absent) anchor input
+  if ((rc = launch_lse_merge(p, L, anchors, da))) return rc;
   anchor_decide_kernel<<<dim3((unsigned)L.n_tiles, (unsigned)p.heads), dim3(kThreads), 0,
                          p.stream>>>(da, (int)anchors, (int)p.heads, p.mask);
   return check_launch("anchor_decide_kernel");
@@ -3280,7 +3329,7 @@ int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b
     const StepMode mode = step_mode(p, L, b);
     if (mode != kSplit) return launch_step(p, L, b, mode == kTicketed);
   }
-  const AttendArgs aa = attend_args(p, L, b);
+  AttendArgs aa = attend_args(p, L, b);
   const MergeArgs ma = merge_args(p, L, b);
   const int64_t rows = rows_per_pass(p.group, p.dim);
   const dim3 tiles((unsigned)L.n_tiles, (unsigned)p.heads, (unsigned)((p.group + rows - 1) / rows));
@@ -3288,6 +3337,7 @@ int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b
   int rc = launch_score(p, L);
   if (rc) return rc;
   mark(1, p.stream);
+  if ((rc = launch_lse_merge(p, L, 1, aa.decide))) return rc;
   rc = kUnsupported;
   RKV_DISPATCH_DIM(p.dim, D, rc = launch_attend<D>(aa, rows, tiles, p.stream));
   if (rc) return rc;

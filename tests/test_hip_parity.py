@@ -261,6 +261,9 @@ SELECT_CASES = [
     (2, 4, 256, 64, 999, "max", 0.01, 0.05),
     (2, 2, 160, 32, 2050, "any", 0.001, 0.01),
     (1, 4, 128, 32, 20000, "any", 0.01, 0.01),
+    # 69 tiles: the rows' log Z / log C merged once (lse_merge_kernel) before
+    # the decisions
+    (1, 4, 128, 16, 70000, "any", 0.01, 0.01),
 ]
 
 
