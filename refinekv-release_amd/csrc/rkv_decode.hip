@@ -1048,6 +1048,8 @@ __global__ __launch_bounds__(kThreads) void decide_kernel(DecideArgs a,
 // than 64 tiles: each tile's decision then reads two floats instead of
 // merging every tile's partials again.  Wave w of workgroup b takes row
 // 4 b + w.
+constexpr int kLseBatch = 8;  // partials per lane beyond its first loaded at once
+
 __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* lse, float* row_lse,
                                                              int64_t rows, int64_t n_tiles,
                                                              int64_t tile_stride) {
@@ -1058,10 +1060,43 @@ __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* lse, f
   const int tl = lane < n_tiles ? lane : 0;
   float4 part = *reinterpret_cast<const float4*>(prow + tl * 4);
   if (lane >= n_tiles) part = make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
-  auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
-  auto pc = [&](int64_t t) { return make_float2(prow[t * 4 + 2], prow[t * 4 + 3]); };
-  const float lz = merge_lse(part.x, part.y, pz, n_tiles, lane);
-  const float lc = merge_lse(part.z, part.w, pc, n_tiles, lane);
+  float lz, lc;
+  if (n_tiles <= kWave * (1 + kLseBatch)) {
+    // every partial of this lane loaded at once (one round trip), then
+    // merge_lse's operations in its order, the z and c chains side by side
+    float4 pv[kLseBatch];
+#pragma unroll
+    for (int k = 0; k < kLseBatch; ++k) {
+      const int64_t t = lane + (int64_t)kWave * (k + 1);
+      pv[k] = t < n_tiles ? *reinterpret_cast<const float4*>(prow + t * 4)
+                          : make_float4(kNegInf, 0.0f, kNegInf, 0.0f);
+    }
+    float mz = lane < n_tiles ? part.x : kNegInf, mc = lane < n_tiles ? part.z : kNegInf;
+#pragma unroll
+    for (int k = 0; k < kLseBatch; ++k) {
+      if (lane + (int64_t)kWave * (k + 1) < n_tiles) {
+        mz = nanmax(mz, pv[k].x);
+        mc = nanmax(mc, pv[k].z);
+      }
+    }
+    const float sz = inf_to_zero(wave_nanmax_u(mz)), sc = inf_to_zero(wave_nanmax_u(mc));
+    float az = lane < n_tiles ? part.y * expf_(part.x - sz) : 0.0f;
+    float ac = lane < n_tiles ? part.w * expf_(part.z - sc) : 0.0f;
+#pragma unroll
+    for (int k = 0; k < kLseBatch; ++k) {
+      if (lane + (int64_t)kWave * (k + 1) < n_tiles) {
+        az = az + pv[k].y * expf_(pv[k].x - sz);
+        ac = ac + pv[k].w * expf_(pv[k].z - sc);
+      }
+    }
+    lz = logf_(wave_sum_u(az)) + sz;
+    lc = logf_(wave_sum_u(ac)) + sc;
+  } else {
+    auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
+    auto pc = [&](int64_t t) { return make_float2(prow[t * 4 + 2], prow[t * 4 + 3]); };
+    lz = merge_lse(part.x, part.y, pz, n_tiles, lane);
+    lc = merge_lse(part.z, part.w, pc, n_tiles, lane);
+  }
   if (lane == 0) {
     row_lse[r * 2] = lz;
     row_lse[r * 2 + 1] = lc;
@@ -2860,8 +2895,8 @@ struct MergeArgs {
   int parts, dim, heads;
 };
 
-constexpr int kMergeBatch = 8;               // partials per lane per batch of loads
-constexpr int kMergeD = 32;                  // output columns per workgroup
+constexpr int kMergeBatch = 16;              // partials per lane per batch of loads
+constexpr int kMergeD = 8;                   // output columns per workgroup
 constexpr int kMergeK = kThreads / kMergeD;  // partial stripes
 
 // Online merge of one partial into (mx, num, den); skips empty partials.
@@ -2919,9 +2954,19 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
   }
   // the step's access count: sum of the tile counts, added once
   if (a.accessed && blockIdx.x == 0 && blockIdx.y == 0) {
+    // (the loads of a batch are issued together: one round trip per batch)
     unsigned long long s = 0;
-    for (int64_t i = tid; i < (int64_t)a.heads * a.tile_stride; i += kThreads)
-      s += a.tile_counts[i];
+    const int64_t n = (int64_t)a.heads * a.tile_stride;
+    for (int64_t i0 = tid; i0 < n; i0 += kThreads * kMergeBatch) {
+      uint32_t c[kMergeBatch];
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) {
+        const int64_t i = i0 + (int64_t)u * kThreads;
+        c[u] = i < n ? a.tile_counts[i] : 0u;
+      }
+#pragma unroll
+      for (int u = 0; u < kMergeBatch; ++u) s += c[u];
+    }
 #pragma unroll
     for (int o = 32; o >= 1; o >>= 1) s += __shfl_xor(s, o, kWave);
     if (tid % kWave == 0) wsum[tid / kWave] = s;
