@@ -2895,9 +2895,12 @@ struct MergeArgs {
   int parts, dim, heads;
 };
 
-constexpr int kMergeBatch = 16;              // partials per lane per batch of loads
-constexpr int kMergeD = 8;                   // output columns per workgroup
-constexpr int kMergeK = kThreads / kMergeD;  // partial stripes
+// merge_kernel<MD, MB>: MD output columns per workgroup, kThreads / MD
+// partial stripes, MB partials per lane per batch of loads.  Few partials
+// (the dense decode's splits, a head of up to 128 tiles): 32 columns, 8
+// stripes of batches of 8; many (more tiles): 8 columns, so that the
+// workgroups fill the device and each stripe takes one or two batches of 16.
+constexpr int kMergeFewParts = 128;
 
 // Online merge of one partial into (mx, num, den); skips empty partials.
 __device__ __forceinline__ void merge_one(float m, float l, float acc, float& mx, float& num,
@@ -2915,7 +2918,9 @@ __device__ __forceinline__ void merge_one(float m, float l, float acc, float& mx
   }
 }
 
+template <int kMergeD, int kMergeBatch>
 __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
+  constexpr int kMergeK = kThreads / kMergeD;  // partial stripes
   __shared__ float sm[kMergeK], sd[kMergeK], sn[kMergeK][kMergeD];
   __shared__ unsigned long long wsum[kWaves];
   const int64_t r = blockIdx.x;
@@ -2978,6 +2983,16 @@ __global__ __launch_bounds__(kThreads) void merge_kernel(MergeArgs a) {
 // ---------------------------------------------------------------------------
 // Host launchers
 // ---------------------------------------------------------------------------
+int launch_merge(const MergeArgs& ma, int64_t rows, int64_t dim, hipStream_t stream) {
+  if (ma.parts <= kMergeFewParts)
+    merge_kernel<32, 8><<<dim3((unsigned)rows, (unsigned)((dim + 31) / 32)), dim3(kThreads), 0,
+                          stream>>>(ma);
+  else
+    merge_kernel<8, 16><<<dim3((unsigned)rows, (unsigned)((dim + 7) / 8)), dim3(kThreads), 0,
+                          stream>>>(ma);
+  return check_launch("merge_kernel");
+}
+
 struct SelectParams {
   const void* query;
   const void* key_mean;
@@ -3387,9 +3402,7 @@ int launch_decode(const SelectParams& p, const Layout& L, const DecodeBuffers& b
   RKV_DISPATCH_DIM(p.dim, D, rc = launch_attend<D>(aa, rows, tiles, p.stream));
   if (rc) return rc;
   mark(2, p.stream);
-  merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
-                 dim3(kThreads), 0, p.stream>>>(ma);
-  rc = check_launch("merge_kernel");
+  rc = launch_merge(ma, p.heads * p.group, p.dim, p.stream);
   mark(3, p.stream);
   return rc;
 }
@@ -3541,9 +3554,7 @@ int launch_dense(const DenseParams& p, const DensePlan& P) {
   ma.parts = (int)P.splits;
   ma.dim = (int)p.dim;
   ma.heads = (int)p.heads;
-  merge_kernel<<<dim3((unsigned)(p.heads * p.group), (unsigned)((p.dim + kMergeD - 1) / kMergeD)),
-                 dim3(kThreads), 0, p.stream>>>(ma);
-  return check_launch("merge_kernel");
+  return launch_merge(ma, p.heads * p.group, p.dim, p.stream);
 }
 
 }  // namespace
