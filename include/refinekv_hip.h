@@ -296,8 +296,11 @@ int rkv_set_handoff_test(uint32_t spin_limit, uint32_t skew);
  * output is the same bit for bit either way.  Per thread. */
 int rkv_set_speculation(int mode);
 
-/* Test hook with no reference counterpart: applies the kernels' device
- * scalar function fn (0 exp, 1 log, 2 bf16 round trip, 3 sqrt) to n floats. */
+/* Test hook with no reference counterpart: applies a device scalar function
+ * fn to n floats: 0 exp and 1 log as the oracle computes them (expf_,
+ * logf_), 2 bf16 round trip, 3 sqrt, 4 exp and 5 log as the selection
+ * kernels compute them (the hardware's transcendental unit); other fn
+ * return RKV_INVALID_ARGUMENT. */
 int rkv_math_probe(int fn, const float* x, float* y, int64_t n, rkv_stream_t stream);
 
 #ifdef __cplusplus

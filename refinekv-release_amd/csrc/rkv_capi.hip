@@ -33,7 +33,9 @@ __global__ void math_probe_kernel(int fn, const float* __restrict__ x, float* __
     case 0: r = expf_(v); break;
     case 1: r = logf_(v); break;
     case 2: r = round_bf16(v); break;
-    default: r = sqrtf(v); break;
+    case 3: r = sqrtf(v); break;
+    case 4: r = exp_hw(v); break;
+    default: r = log_hw(v); break;
   }
   y[i] = r;
 }
@@ -47,11 +49,12 @@ extern "C" const char* rkv_last_error(void) { return g_error; }
 
 extern "C" int rkv_version(void) { return 2; }
 
-// Applies a device scalar function elementwise: fn 0 = exp, 1 = log,
-// 2 = bfloat16 round trip, 3 = sqrt.  x and y are device arrays of n floats.
+// Applies a device scalar function elementwise: fn 0 = exp (expf_), 1 = log
+// (logf_), 2 = bfloat16 round trip, 3 = sqrt, 4 = exp_hw, 5 = log_hw.  x and
+// y are device arrays of n floats.
 extern "C" int rkv_math_probe(int fn, const float* x, float* y, int64_t n, hipStream_t stream) {
   clear_error();
-  if (!x || !y || n < 0 || fn < 0 || fn > 3)
+  if (!x || !y || n < 0 || fn < 0 || fn > 5)
     return set_error(kInvalidArgument, "rkv_math_probe: bad arguments");
   if (n == 0) return kOk;
   const int64_t blocks = (n + 255) / 256;

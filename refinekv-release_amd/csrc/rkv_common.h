@@ -14,8 +14,18 @@ constexpr int kMaxGroup = 16;         // query heads per KV head
 constexpr float kDeltaMax = 10.0f;    // reference.py:20 switch between risk branches
 constexpr float kInflate = 1.00390625f;  // 1 + 2^-8 (reference.py:16, summary.py:96)
 constexpr float kLn2 = 0.693147182464599609375f;  // fp32(math.log(2))
+constexpr float kLog2e = 1.44269504088896341f;    // fp32(1 / math.log(2))
 constexpr float kNegInf = -__builtin_inff();
 constexpr float kPosInf = __builtin_inff();
+
+// e^x and log x on the hardware's transcendental unit: v_exp_f32 (2^x) and
+// v_log_f32 (log2 x), about an ulp each, scaled by fp32 log2(e) and ln(2).
+// Against exact e^x the rounding of x log2(e) adds about |x| 2^-24
+// relative; log x is off by a few 2^-24 absolute plus an ulp.  Special
+// values as expf_ / logf_: e^-inf = 0, e^+inf = +inf, log 0 = -inf, log of a
+// negative = NaN, NaN in, NaN out.
+__device__ __forceinline__ float exp_hw(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+__device__ __forceinline__ float log_hw(float x) { return __builtin_amdgcn_logf(x) * kLn2; }
 
 // Reduction codes of runtime.py:23.
 enum Reduction { kMean = 0, kMax = 1, kAny = 2 };

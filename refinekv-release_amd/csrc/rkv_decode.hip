@@ -37,9 +37,12 @@
 // attends every cached token with the same matrix-core engine.
 //
 // Selection statistics (z, delta, log Z, log C, risk) follow fixed fp32
-// orders shared with the CPU oracle (oracle/rkv_oracle.c), so masks are
-// reproducible bit for bit; the attention's orders are fixed too, so outputs
-// are deterministic run to run.
+// orders shared with the CPU oracle (oracle/rkv_oracle.c): z and delta equal
+// the oracle's bit for bit; e^x and log x run on the hardware's
+// transcendental unit (exp_hw / log_hw below), so log Z, log C and the risks
+// are within a few ulp of the oracle's and a block's mask can differ from
+// the oracle's only where a row's risk lies within that distance of eps.
+// Every order is fixed, so masks and outputs are deterministic run to run.
 #include <math.h>
 
 #include <atomic>
@@ -54,7 +57,6 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
-constexpr float kLog2e = 1.44269504088896341f;
 constexpr int kLine = 8;  // u64 counters per 64-byte hand-off line
 constexpr uint32_t kSpinLimit = 1u << 20;  // polls before a hand-off wait gives up (default)
 constexpr int64_t kStepMaxTiles = 256;     // tiles per head the one-launch step takes
@@ -184,8 +186,16 @@ T* at(void* ws, int64_t off) {
 }
 
 // ---------------------------------------------------------------------------
-// Shared scalar math (reference.py:16-34), identical to the CPU oracle.
+// Selection math (reference.py:16-34): the oracle's operations in its order,
+// with its exponentials and logarithms on the hardware's transcendental unit.
 // ---------------------------------------------------------------------------
+// e^x and log x of the selection statistics, decisions and LSE merges are
+// exp_hw / log_hw (rkv_common.h): the hardware's transcendental unit in
+// place of the oracle's expf_ / logf_, which the device runs bit for bit but
+// at 3-4 times the instructions.  z and delta do not use them and stay
+// bit-exact; log Z, log C and the risks are within a few ulp of the
+// oracle's, and the masks equal its masks wherever no row's risk is within
+// that distance of eps.
 // The delta-only terms of a (row, block) pair, computed once by the score
 // phase: log cosh delta (reference.py:19-22) and the two factors the risk
 // (reference.py:24-34) multiplies in -- A = cosh(delta) - 1 written as
@@ -199,12 +209,12 @@ T* at(void* ws, int64_t off) {
 // partials are out).  t = e^min(delta, kDeltaMax) passes between them.
 __device__ __forceinline__ float delta_log_cosh(float delta, float& t) {
   const float c = clamp_max(delta, kDeltaMax);
-  t = expf_(c);
-  float log_cosh = logf_((t + expf_(-c)) * 0.5f);
+  t = exp_hw(c);
+  float log_cosh = log_hw((t + exp_hw(-c)) * 0.5f);
   const bool large = !(delta <= kDeltaMax);  // NaN takes the large form, as on the host
   if (__ballot(large) != 0) {
     const float d = large ? delta : 0.0f;
-    const float lc = d + logf_((1.0f + expf_(-2.0f * d)) * 0.5f);
+    const float lc = d + log_hw((1.0f + exp_hw(-2.0f * d)) * 0.5f);
     log_cosh = large ? lc : log_cosh;
   }
   return log_cosh;
@@ -216,8 +226,8 @@ __device__ __forceinline__ void delta_factors(float delta, float t, float& A, fl
   const bool large = !(delta <= kDeltaMax);
   if (__ballot(large) != 0) {
     const float d = large ? delta : 0.0f;
-    const float exp_neg = expf_(-d);
-    const float la = (d + 2.0f * logf_(clamp_min(1.0f - exp_neg, 1e-30f))) - kLn2;
+    const float exp_neg = exp_hw(-d);
+    const float la = (d + 2.0f * log_hw(clamp_min(1.0f - exp_neg, 1e-30f))) - kLn2;
     const float lt = (1.0f - exp_neg) / (1.0f + exp_neg);
     A = large ? la : A;
     th = large ? lt : th;
@@ -229,9 +239,9 @@ __device__ __forceinline__ void delta_factors(float delta, float t, float& A, fl
 __device__ __forceinline__ float risk_from(float z, float delta, float A, float th, float log_z,
                                            float log_c, float vmax, float vnorm) {
   float mass;
-  if (delta <= kDeltaMax) mass = ((2.0f * vmax) * expf_(z - log_c)) * A;
-  else mass = (2.0f * vmax) * expf_((z - log_c) + A);
-  const float value = ((2.0f * vnorm) * expf_(z - log_z)) * th;
+  if (delta <= kDeltaMax) mass = ((2.0f * vmax) * exp_hw(z - log_c)) * A;
+  else mass = (2.0f * vmax) * exp_hw((z - log_c) + A);
+  const float value = ((2.0f * vnorm) * exp_hw(z - log_z)) * th;
   return mass + value;
 }
 
@@ -497,12 +507,12 @@ __device__ __forceinline__ void score_stats(const ScoreArgs& a, int64_t tile, co
     const float s = sdot[g * kTile + lane] * a.scale;
     const float z = valid ? s + (b == N - 1 ? a.ln_last : a.ln_full) : kNegInf;
     const float zm = wave_nanmax_u(z);
-    const float zl = wave_sum_u(expf_(z - inf_to_zero(zm)));
+    const float zl = wave_sum_u(exp_hw(z - inf_to_zero(zm)));
     const float dl = (sqrtf(clamp_min(pdot[g * kTile + lane], 0.0f)) * a.scale) * kInflate;
     float t = 1.0f;  // (set by delta_log_cosh on the lanes of existing blocks)
     const float zc = valid ? z + delta_log_cosh(dl, t) : kNegInf;
     const float cm = wave_nanmax_u(zc);
-    const float cl = wave_sum_u(expf_(zc - inf_to_zero(cm)));
+    const float cl = wave_sum_u(exp_hw(zc - inf_to_zero(cm)));
     if (lane == 0) put_lse(g, make_float4(zm, zl, cm, cl));
     float ra, rth;
     delta_factors(dl, t, ra, rth);
@@ -568,12 +578,12 @@ __device__ __forceinline__ float merge_lse(float m0, float l0, Part part, int64_
   for (int64_t t = lane + kWave; t < n_tiles; t += kWave) mx = nanmax(mx, part(t).x);
   mx = wave_nanmax_u(mx);
   const float ms = inf_to_zero(mx);
-  float acc = lane < n_tiles ? l0 * expf_(m0 - ms) : 0.0f;
+  float acc = lane < n_tiles ? l0 * exp_hw(m0 - ms) : 0.0f;
   for (int64_t t = lane + kWave; t < n_tiles; t += kWave) {
     const float2 p = part(t);
-    acc = acc + p.y * expf_(p.x - ms);
+    acc = acc + p.y * exp_hw(p.x - ms);
   }
-  return logf_(wave_sum_u(acc)) + ms;
+  return log_hw(wave_sum_u(acc)) + ms;
 }
 
 // Decides tile `tile` of head h (select_blocks_reference plus the anchor
@@ -795,11 +805,11 @@ __device__ __forceinline__ float merge_lse_chunks(const float (&m)[kChunks],
   for (int k = 1; k < kChunks; ++k) mx = nanmax(mx, m[k]);
   mx = wave_nanmax_u(mx);
   const float ms = inf_to_zero(mx);
-  float acc = (uint32_t)lane < T ? l[0] * expf_(m[0] - ms) : 0.0f;
+  float acc = (uint32_t)lane < T ? l[0] * exp_hw(m[0] - ms) : 0.0f;
 #pragma unroll
   for (int k = 1; k < kChunks; ++k)
-    if ((uint32_t)(k * kWave + lane) < T) acc = acc + l[k] * expf_(m[k] - ms);
-  return logf_(wave_sum_u(acc)) + ms;
+    if ((uint32_t)(k * kWave + lane) < T) acc = acc + l[k] * exp_hw(m[k] - ms);
+  return log_hw(wave_sum_u(acc)) + ms;
 }
 
 // Both merges of one row (z and c): for T <= 64 (one tile per lane) a single
@@ -813,9 +823,9 @@ __device__ __forceinline__ float2 merge_lse_pair(const RowLse& r, uint32_t T, in
   const float sz = inf_to_zero(wave_nanmax_u(r.zm[0]));
   const float sc = inf_to_zero(wave_nanmax_u(r.cm[0]));
   const bool live = (uint32_t)lane < T;
-  const float az = live ? r.zl[0] * expf_(r.zm[0] - sz) : 0.0f;
-  const float ac = live ? r.cl[0] * expf_(r.cm[0] - sc) : 0.0f;
-  return make_float2(logf_(wave_sum_u(az)) + sz, logf_(wave_sum_u(ac)) + sc);
+  const float az = live ? r.zl[0] * exp_hw(r.zm[0] - sz) : 0.0f;
+  const float ac = live ? r.cl[0] * exp_hw(r.cm[0] - sc) : 0.0f;
+  return make_float2(log_hw(wave_sum_u(az)) + sz, log_hw(wave_sum_u(ac)) + sc);
 }
 
 // Access count of a tile with expanded blocks `bits` (transformers.py:590-594):
@@ -1080,17 +1090,17 @@ __global__ __launch_bounds__(kThreads) void lse_merge_kernel(const float* lse, f
       }
     }
     const float sz = inf_to_zero(wave_nanmax_u(mz)), sc = inf_to_zero(wave_nanmax_u(mc));
-    float az = lane < n_tiles ? part.y * expf_(part.x - sz) : 0.0f;
-    float ac = lane < n_tiles ? part.w * expf_(part.z - sc) : 0.0f;
+    float az = lane < n_tiles ? part.y * exp_hw(part.x - sz) : 0.0f;
+    float ac = lane < n_tiles ? part.w * exp_hw(part.z - sc) : 0.0f;
 #pragma unroll
     for (int k = 0; k < kLseBatch; ++k) {
       if (lane + (int64_t)kWave * (k + 1) < n_tiles) {
-        az = az + pv[k].y * expf_(pv[k].x - sz);
-        ac = ac + pv[k].w * expf_(pv[k].z - sc);
+        az = az + pv[k].y * exp_hw(pv[k].x - sz);
+        ac = ac + pv[k].w * exp_hw(pv[k].z - sc);
       }
     }
-    lz = logf_(wave_sum_u(az)) + sz;
-    lc = logf_(wave_sum_u(ac)) + sc;
+    lz = log_hw(wave_sum_u(az)) + sz;
+    lc = log_hw(wave_sum_u(ac)) + sc;
   } else {
     auto pz = [&](int64_t t) { return make_float2(prow[t * 4], prow[t * 4 + 1]); };
     auto pc = [&](int64_t t) { return make_float2(prow[t * 4 + 2], prow[t * 4 + 3]); };
@@ -3056,7 +3066,7 @@ ScoreArgs score_args(const SelectParams& p, const Layout& L) {
   sa.group = (int)p.group;
   sa.summary_heads = (int)p.heads;
   sa.scale = (float)pow((double)p.dim, -0.5);
-  // the host and device logf_ agree bit for bit
+  // (the oracle's logf_, on the host: z stays bit-exact)
   sa.ln_full = logf_((float)p.block);
   sa.ln_last = logf_((float)(p.length - (p.n_blocks - 1) * p.block));
   return sa;

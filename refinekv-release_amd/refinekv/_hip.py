@@ -513,8 +513,9 @@ def set_decode_path(name):
 
 
 def math_probe(fn, x):
-    """Device scalar functions for tests: fn in {'exp', 'log', 'bf16', 'sqrt'}."""
-    code = {"exp": 0, "log": 1, "bf16": 2, "sqrt": 3}[fn]
+    """Device scalar functions for tests: fn in {'exp', 'log', 'bf16', 'sqrt'}
+    (the oracle's forms) and {'exp_hw', 'log_hw'} (the selection kernels')."""
+    code = {"exp": 0, "log": 1, "bf16": 2, "sqrt": 3, "exp_hw": 4, "log_hw": 5}[fn]
     x = x.contiguous().float()
     y = torch.empty_like(x)
     _check(lib().rkv_math_probe(code, _ptr(x), _ptr(y), x.numel(), _stream(x.device)),
