@@ -369,8 +369,11 @@ __device__ __forceinline__ void score_load(const ScoreArgs& a, int64_t h, int64_
 }
 
 // The dot products of a tile from its loaded rows and the staged q (see
-// score_dots); ends with a barrier.
-template <int D, int kMaxG = kMaxGroup>
+// score_dots); ends with a barrier.  kLowReg (the score kernel, four
+// workgroups per CU): one query row's slice of q at a time, read from LDS
+// for each pass, instead of four rows' held across both passes -- the same
+// dot products in the same order, in half the registers.
+template <int D, int kMaxG = kMaxGroup, bool kLowReg = false>
 __device__ __forceinline__ void score_from(const ScoreArgs& a, const ScoreRaw<D>& raw,
                                            float* sdot, float* pdot, const float* qstage) {
   using S = Dots<D>;
@@ -382,6 +385,36 @@ __device__ __forceinline__ void score_from(const ScoreArgs& a, const ScoreRaw<D>
   constexpr int QS = S::kLanes * QW;      // padded row
   const float* qs = qstage;               // [G][QS] bf16(q)
   const float* q2s = qs + G * QS;         // [G][QS] bf16(q^2)
+  if constexpr (kLowReg) {
+#pragma unroll
+    for (int ps = 0; ps < S::kPasses; ++ps) {
+      float km[CH], el[CH];
+      unpack(raw.k[ps], km);
+      unpack(raw.e[ps], el);
+      const int bl = ps * S::kPerPass + sub;
+#pragma unroll 1
+      for (int g = 0; g < G; ++g) {
+        float qv[CH], q2v[CH];
+        lds_read<CH>(qs + g * QS + c * QW, qv);
+        lds_read<CH>(q2s + g * QS + c * QW, q2v);
+        float s = qv[0] * km[0];
+        float p = q2v[0] * el[0];
+#pragma unroll
+        for (int i = 1; i < CH; ++i) {
+          s = __builtin_fmaf(qv[i], km[i], s);
+          p = __builtin_fmaf(q2v[i], el[i], p);
+        }
+        s = lanes_sum_last<S::kLanes>(s);
+        p = lanes_sum_last<S::kLanes>(p);
+        if (c == S::kLanes - 1) {
+          sdot[g * kTile + bl] = s;
+          pdot[g * kTile + bl] = p;
+        }
+      }
+    }
+    __syncthreads();
+    return;
+  }
 
   // Rows g0 .. g0+3: a lambda so that the common case (G <= 4, one call)
   // waits for each pass's loads just before it, not for both passes first.
@@ -440,7 +473,7 @@ __device__ __forceinline__ void score_from(const ScoreArgs& a, const ScoreRaw<D>
 // stay for score_from of further tiles).  kMaxG bounds the group (the step
 // kernel's rows per pass), so the four-row loop is compiled only where
 // groups above four can reach it.
-template <int D, int kMaxG = kMaxGroup>
+template <int D, int kMaxG = kMaxGroup, bool kLowReg = false>
 __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_t tile,
                                            float* sdot, float* pdot, float* qstage) {
   using S = Dots<D>;
@@ -485,7 +518,7 @@ __device__ __forceinline__ void score_dots(const ScoreArgs& a, int64_t h, int64_
   }
   for (int i = first + kQWords * step; i < G * D / 2; i += step) stage(i, q32[i]);
   __syncthreads();
-  score_from<D, kMaxG>(a, raw, sdot, pdot, qstage);
+  score_from<D, kMaxG, kLowReg>(a, raw, sdot, pdot, qstage);
 }
 
 // z, delta, the risk's delta-only factors and the tile's LSE partials from
@@ -521,14 +554,17 @@ __device__ __forceinline__ void score_stats(const ScoreArgs& a, int64_t tile, co
 }
 
 template <int D>
-__global__ __launch_bounds__(kThreads) void score_kernel(ScoreArgs a) {
+// (81 registers at head_dim 128 with score_from's low-register order: up to
+// six workgroups per CU, which the 512-tile heads' 4096 workgroups need to
+// overlap their loads with the dot products)
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(4))) void score_kernel(ScoreArgs a) {
   extern __shared__ float score_lds[];
   const int G = a.group;
   float* sdot = score_lds;          // [G][64]
   float* pdot = sdot + G * kTile;   // [G][64]
   const int64_t h = blockIdx.y, tile = blockIdx.x;
   const int lane = threadIdx.x % kWave;
-  score_dots<D>(a, h, tile, sdot, pdot, pdot + G * kTile);
+  score_dots<D, kMaxGroup, true>(a, h, tile, sdot, pdot, pdot + G * kTile);
   score_stats(
       a, tile, sdot, pdot,
       [&](int g, bool valid, float4 zf) {
