@@ -1538,7 +1538,7 @@ __device__ __forceinline__ void mma_fold(MmaState<D>& st, const float (&x)[4], c
 // flight: issue(j, sidx, kop) issues chunk j (exactly MmaShape<D>::kOps
 // memory operations, or none for a chunk whose loads carry no K operands)
 // into stage sidx, compute(j, sidx, kop) folds it.  Chunk j uses stage j % 3
-// and registers kj % 3; the first `pre` chunks (at most 2) were issued by
+// and registers kj % 3; the first `pre` chunks (at most 3) were issued by
 // the caller before the ring.  The stage index is a constant in each
 // unrolled slot.
 template <int D, typename Issue, typename Compute>
@@ -1561,7 +1561,7 @@ __device__ __forceinline__ void mma_ring(uint32_t count, uint32_t pre,
   };
 #pragma unroll 1
   for (uint32_t j = 0; j < count; j += 3) {
-    if (j + 2 < count) issue(j + 2, 2, k2);
+    if (j + 2 < count && (j > 0 || pre < 3)) issue(j + 2, 2, k2);
     wait_for(j);
     compute(j, 0, k0);
     if (j + 1 >= count) break;
@@ -2273,7 +2273,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   const auto vres_s = buffer_view(a.value_suffix + h * a.vs_hs, cap ? (cap - 1u) * vts + kRowBytes : 0u);
   // Speculation (one-launch step, one tile per workgroup): when the previous
   // launch on this workspace expanded every block of the tile, the wave
-  // issues its first two chunks of the tile's rows before the decision,
+  // issues its first three chunks (every stage of its ring) before the decision,
   // assuming every block expands again (so its ring has no representative
   // chunk: with every block expanded that chunk's logits are all -inf and its
   // fold would leave the state unchanged); if the decision agrees, the ring
@@ -2406,6 +2406,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
       if (n > 0) issue(0u, 0, k0);
     }
     if (n > 1 && (Rr == 0u || n1() > 1u)) issue(1u, 1, k1);
+    if (spec && Rr == 0u && n > 2) issue(2u, 2, k2);  // (speculating: all three stages)
   };
 
   MmaState<D> st;
@@ -2490,7 +2491,8 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   auto reps_live = [&](uint32_t j) {
     return kMulti ? rep_tile(j) * kTile + 16u * wave < N : reps_on;
   };
-  const uint32_t pre = !spec || Rr != 0u ? (n1() > 1u ? 2u : 1u) : (n_chunks() > 1u ? 2u : 1u);
+  const uint32_t pre = !spec || Rr != 0u ? (n1() > 1u ? 2u : 1u)
+                                         : (n_chunks() > 2u ? 3u : n_chunks() > 1u ? 2u : 1u);
   RKV_STAMP(stamps, kStRingStart, tid == 0);
   if constexpr (D <= 128) {
     // one ring: the first page rows' loads are issued as it starts
@@ -3389,7 +3391,7 @@ thread_local uint32_t g_spin_limit = 0;
 thread_local uint32_t g_skew = 0;
 // Test hook (rkv_set_speculation, per thread): 0 turns the step's
 // speculation off, 1 (default) and 2 leave it on.  (A miss costs a
-// workgroup at most two chunks' loads per wave, and only where the previous
+// workgroup at most three chunks' loads per wave, and only where the previous
 // launch expanded all of its tile, so it needs no size threshold.)
 thread_local uint32_t g_speculate = 1;
 
