@@ -335,6 +335,45 @@ def risk_tolerance(z, delta, log_z, log_c, risk):
     return rel * np.abs(risk.astype(np.float64)) + 1e-37
 
 
+@pytest.mark.parametrize("reduction", ["any", "max", "mean"])
+def test_masks_with_eps_next_to_a_risk(hip, oracle_lib, reduction):
+    """eps placed at sampled blocks' reduced risks: ten times the hardware
+    e^x / log x error bound above and below, every mask equals the oracle's;
+    at the risk itself, a mask may differ from the oracle's only for a
+    block whose reduced risk lies within that bound of eps."""
+    heads, group, dim, block = 2, 4, 128, 32
+    inp = _decode_case(heads, group, dim, block, 4096, 0.05)
+    cfg0 = RefineKVConfig(backend="hip", block_size=block, eps=0.01, gqa_reduction=reduction)
+    summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg0)
+    qn = inp["query"][:, :, 0].float().numpy()
+    summ = oracle_summary_of(summary)
+    st = oracle_lib.select_stats(qn, summ)
+    tol = risk_tolerance(st["z"], st["delta"], st["log_z"], st["log_c"], st["risk"])
+    risk = st["risk"].astype(np.float64)
+    # the reduced risk of each (head, block) and its bound
+    if reduction == "mean":
+        red, bound = risk.mean(axis=1), tol.mean(axis=1)
+    else:
+        red, bound = risk.max(axis=1), tol.max(axis=1)
+    rng = np.random.default_rng(5)
+    picks = [tuple(x) for x in rng.choice(np.argwhere(np.isfinite(red) & (red > 1e-30)), 6)]
+    for h, b in picks:
+        r, tb = float(red[h, b]), float(bound[h, b])
+        for eps, exact in ((r + 10 * tb, True), (r - 10 * tb, True), (r, False)):
+            if eps <= 0.0:
+                continue
+            cfg = RefineKVConfig(backend="hip", block_size=block, eps=float(np.float32(eps)),
+                                 gqa_reduction=reduction)
+            got = hip.select(inp["query"].to(DEV), summary, cfg, {}).cpu().numpy().astype(np.uint8)
+            want, _, _ = oracle_lib.select(qn, summ, cfg.eps, reduction)
+            diff = got != want
+            if exact:
+                assert not diff.any(), (h, b, eps, int(diff.sum()))
+            else:
+                near = np.abs(red - cfg.eps) <= bound
+                assert not (diff & ~near).any(), (h, b, eps, int((diff & ~near).sum()))
+
+
 @pytest.mark.parametrize("heads,group,dim,block,prompt,reduction,eps,spikes", SELECT_CASES)
 def test_selection_statistics(hip, oracle_lib, heads, group, dim, block, prompt, reduction, eps,
                               spikes):
