@@ -2847,7 +2847,9 @@ void step_kernel(StepArgs s) {
   if (kTiles == 1 && tid == 0 && s.speculate)
     prev_full = __hip_atomic_load(s.full + h * sa.tile_stride + wk, __ATOMIC_RELAXED,
                                   __HIP_MEMORY_SCOPE_AGENT);
-  score_dots<D, GBM>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
+  // (8-row passes: one query row's slice of q at a time, as the score kernel
+  // does; holding four rows' across both passes spilled)
+  score_dots<D, GBM, (GBM > 4)>(sa, h, tile, sh.u.score.sdot, sh.u.score.pdot, sh.u.score.q);
   RKV_STAMP(stamps, kStDots, tid == 0);
   // (the epoch is read before the loads below are issued: loads complete in
   // order, so a later read would wait for them too)

@@ -112,12 +112,12 @@ def test_step_kernel_exists_only_up_to_head_dim_128(kernels):
 @needs_tools
 def test_no_scratch_in_the_kernels_of_common_shapes(kernels):
     """Scratch (register spills or dynamically indexed arrays) is allowed
-    only in the 16-row builds (GQA groups above 8), the 8-row step at
-    head_dim 128, whose two four-row score passes keep both passes' loads
-    live, and the head_dim-160 attend kernel (its two rings of
-    five-operand chunks spill 9 registers); every other decode and summary
-    kernel runs without it."""
-    allowed = {("step_kernel", (128, 8, 0, 1)), ("attend_kernel", (160, 4))}
+    only in the 16-row builds (GQA groups above 8) and the head_dim-160
+    attend kernel (its two rings of five-operand chunks spill 9 registers);
+    every other decode and summary kernel runs without it (the 8-row steps
+    score one query row's slice of q at a time: holding four rows' across
+    both passes spilled at head_dim 128)."""
+    allowed = {("attend_kernel", (160, 4))}
     for family in ("step_kernel", "attend_kernel", "score_kernel", "summary_kernel"):
         for args, res in _instances(kernels, family):
             rows16 = family in ("step_kernel", "attend_kernel") and args[1] == 16
