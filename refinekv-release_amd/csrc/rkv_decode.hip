@@ -864,6 +864,58 @@ __device__ __forceinline__ float2 merge_lse_pair(const RowLse& r, uint32_t T, in
   return make_float2(log_hw(wave_sum_u(az)) + sz, log_hw(wave_sum_u(ac)) + sc);
 }
 
+// Two rows' LSE partials (row1 only when has1) of a head with T <= 64
+// tiles, polled together until every slot carries this launch's tag, so a
+// wave that owns two rows waits one round trip, not two; each row as
+// gather_lse returns it (at most ss.spin rounds, then recorded as given up
+// with NaN partials).
+__device__ __forceinline__ void gather_lse2(const StepStats& ss, int64_t row0, int64_t row1,
+                                            bool has1, uint32_t T, int lane, RowLse& r0,
+                                            RowLse& r1) {
+  const uint32_t tag = __builtin_amdgcn_readfirstlane(*ss.rtag), mix = tag_mix(tag);
+#pragma unroll
+  for (int k = 0; k < kChunks; ++k) {
+    r0.zm[k] = r0.cm[k] = r1.zm[k] = r1.cm[k] = kNegInf;
+    r0.zl[k] = r0.cl[k] = r1.zl[k] = r1.cl[k] = 0.0f;
+  }
+  uint32_t miss = (uint32_t)lane < T ? (has1 ? 3u : 1u) : 0u;
+  const uint32_t at0 = (uint32_t)((row0 + (uint32_t)lane) * 2) * 16u;
+  const uint32_t at1 = (uint32_t)((row1 + (uint32_t)lane) * 2) * 16u;
+  float4 a0 = make_float4(0.0f, 0.0f, 0.0f, 0.0f), b0 = a0, a1 = a0, b1 = a0;
+#pragma unroll 1
+  for (uint32_t n = 0;; ++n) {
+    if (miss & 1u) {
+      a0 = ss.slots.load4(at0);
+      b0 = ss.slots.load4(at0 + 16u);
+    }
+    if (miss & 2u) {
+      a1 = ss.slots.load4(at1);
+      b1 = ss.slots.load4(at1 + 16u);
+    }
+    if ((miss & 1u) && slot_ok(a0, tag, mix) && slot_ok(b0, tag, mix)) {
+      miss &= ~1u;
+      r0.zm[0] = a0.x;
+      r0.zl[0] = a0.y;
+      r0.cm[0] = b0.x;
+      r0.cl[0] = b0.y;
+    }
+    if ((miss & 2u) && slot_ok(a1, tag, mix) && slot_ok(b1, tag, mix)) {
+      miss &= ~2u;
+      r1.zm[0] = a1.x;
+      r1.zl[0] = a1.y;
+      r1.cm[0] = b1.x;
+      r1.cl[0] = b1.y;
+    }
+    if (__ballot(miss != 0u) == 0) break;
+    if (n + 1 >= ss.spin) {
+      if (lane == 0) handoff_gave_up(ss);
+      r0.zm[0] = r0.cm[0] = r1.zm[0] = r1.cm[0] = bits_f32(0x7FC00000u);
+      break;
+    }
+    __builtin_amdgcn_s_sleep(1);
+  }
+}
+
 // Access count of a tile with expanded blocks `bits` (transformers.py:590-594):
 // the count of an expanded block, 1 for a representative; only the prompt's
 // last block can be short.
@@ -880,7 +932,9 @@ __device__ __forceinline__ uint32_t tile_access_count(const DecideArgs& a, int64
 
 // kMask = false leaves the mask store to the caller (the attention stores it
 // after its loads are issued).
-template <bool kFused = false, bool kMask = true>
+// kMaxG: the most query rows the caller's group can have (above four, a
+// wave owns more than one row).
+template <bool kFused = false, bool kMask = true, int kMaxG = kMaxGroup>
 __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h, int64_t tile,
                                                   const DecideLoads& in, DecideShared& sh,
                                                   float (*zsh)[kTile], const int32_t*& list,
@@ -920,9 +974,25 @@ __device__ __forceinline__ uint64_t decide_finish(const DecideArgs& a, int64_t h
     if (zsh) zsh[g][lane] = valid ? zf.x : kNegInf;
   };
   if constexpr (kFused) {
-    // every row from the head's tagged slots (read until all have landed)
+    // every row from the head's tagged slots (read until all have landed);
+    // a wave owning two rows (groups of 5 to 8, T <= 64) polls both at once
+    bool two = false;
+    if constexpr (kMaxG > kWaves) two = G > kWaves && G <= 2 * kWaves && T <= kWave;
+    if (two) {
+      const bool has1 = wave + kWaves < G;
+      RowLse r0, r1;
+      gather_lse2(*ss, (h * G + wave) * a.tile_stride, (h * G + wave + kWaves) * a.tile_stride,
+                  has1, (uint32_t)T, lane, r0, r1);
+      RKV_STAMP(ss->stamps, kStGather, wave == 0 && lane == 0);
+      const float2 l0 = merge_lse_pair(r0, (uint32_t)T, lane);
+      row_tail(wave, l0.x, l0.y, ss->zs[wave][lane]);
+      if (has1) {
+        const float2 l1 = merge_lse_pair(r1, (uint32_t)T, lane);
+        row_tail(wave + kWaves, l1.x, l1.y, ss->zs[wave + kWaves][lane]);
+      }
+    }
 #pragma unroll 1
-    for (int g = wave; g < G; g += kWaves) {
+    for (int g = wave; g < G && !two; g += kWaves) {
       const RowLse rl = gather_lse(*ss, (h * G + g) * a.tile_stride, (uint32_t)T, lane);
       RKV_STAMP(ss->stamps, kStGather, g == 0 && lane == 0);
       const float2 lzc = merge_lse_pair(rl, (uint32_t)T, lane);
@@ -2426,7 +2496,7 @@ __device__ __forceinline__ void attend_tile_mma(const AttendArgs& a, DecideShare
   if constexpr (kMulti) {
     decide_tiles<kTiles, GBM>(da, h, wk, W, *tset, dsh, sx->stats, bits, count);
   } else {
-    bits[0] = decide_finish<kFused, false>(da, h, tile, ld.din, dsh, nullptr, plist, count,
+    bits[0] = decide_finish<kFused, false, GBM>(da, h, tile, ld.din, dsh, nullptr, plist, count,
                                            kFused ? &sx->stats : nullptr);
   }
   RKV_STAMP(stamps, kStDecided, tid == 0);
