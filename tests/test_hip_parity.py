@@ -935,17 +935,19 @@ def test_several_tiles_per_workgroup_128k_block16(hip, oracle_lib):
 # A hand-off wait that gives up is reported, not silent
 # ---------------------------------------------------------------------------
 
-def test_handoff_give_up_is_reported_and_recoverable(hip, oracle_lib):
+@pytest.mark.parametrize("heads,group,block,prompt", [(8, 4, 32, 8192), (4, 7, 64, 16384)])
+def test_handoff_give_up_is_reported_and_recoverable(hip, oracle_lib, heads, group, block, prompt):
     """With the test hook every wait of the one-launch step accepts no data
     and gives up after 64 polls: every kernel still ends, the status word is
     set and check_workspace raises, and the call's result says so in-band:
     every output row is NaN and every block is marked expanded (a plain call
     or a graph replay cannot return a plausible wrong answer).  After
-    clearing the word, the same workspace decodes correctly again."""
-    inp = _decode_case(8, 4, 128, 32, 8192, 0.02, suffix=9, seed=4)
-    cfg = RefineKVConfig(backend="hip", eps=0.01)
+    clearing the word, the same workspace decodes correctly again.  (Group
+    7 runs the 8-row step, whose waves poll two rows' LSE slots at once.)"""
+    inp = _decode_case(heads, group, 128, block, prompt, 0.02, suffix=9, seed=4)
+    cfg = RefineKVConfig(backend="hip", eps=0.01, block_size=block)
     summary = build_summary(inp["prompt_keys"].to(DEV), inp["prompt_values"].to(DEV), cfg)
-    assert one_launch(hip, 8, 4, 128, summary.num_blocks, 32)
+    assert one_launch(hip, heads, group, 128, summary.num_blocks, block)
     args = (inp["query"].to(DEV), summary, inp["suffix_keys"].to(DEV),
             inp["suffix_values"].to(DEV), cfg)
     ws = {}
@@ -968,8 +970,8 @@ def test_handoff_give_up_is_reported_and_recoverable(hip, oracle_lib):
     torch.cuda.synchronize()
     summ = oracle_summary_of(summary)
     out, mask = oracle_lib.sparse_attention(
-        inp["query"][:, :, 0].float().numpy(), summ, _pages_bits(inp["prompt_keys"], 32),
-        _pages_bits(inp["prompt_values"], 32), gc.bf16_bits(inp["suffix_keys"]),
+        inp["query"][:, :, 0].float().numpy(), summ, _pages_bits(inp["prompt_keys"], block),
+        _pages_bits(inp["prompt_values"], block), gc.bf16_bits(inp["suffix_keys"]),
         gc.bf16_bits(inp["suffix_values"]), 0.01, "any")
     assert np.array_equal(res.selected.cpu().numpy().astype(np.uint8), mask)
     assert_close_output(res.output.float().cpu().numpy()[:, :, 0],
